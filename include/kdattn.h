@@ -1,0 +1,138 @@
+/*
+ * kdattn.h -- C ABI of the MI355X (gfx950) hierarchical-mask flash attention.
+ *
+ * Drop-in device boundary for KernelDev's attention hot path.  The Python
+ * package kerneldev_amd binds these entry points with ctypes behind the same
+ * flash_attention() signature as the reference (original_kernel.py:2096-2112).
+ *
+ * Conventions
+ *   - Every function returns an int status: KD_OK (0) or a negative KD_ERR_*;
+ *     kd_last_error_string() describes the last failure on the calling thread.
+ *     No C++ exception crosses this boundary.
+ *   - The caller owns all device memory: inputs, outputs and workspaces are
+ *     plain device pointers.  The library never allocates or frees device
+ *     memory and keeps no state between calls apart from its code objects.
+ *   - Work is enqueued asynchronously on `stream` (a hipStream_t passed as
+ *     void*; NULL is the default stream).  No call synchronises the host.
+ *   - Tensors [B, H, T, D] are given by a base pointer and element strides for
+ *     (b, h, t); the d stride must be 1, base pointers 16-byte aligned and the
+ *     (b, h, t) strides multiples of 8 elements.
+ *   - LSE is stored in log2 units (LSE2 = log2 sum_j exp2(S_ij * sm_scale *
+ *     log2 e)), as the reference stores it (original_kernel.py:603-604).
+ *     Fully masked rows get O = 0, LSE = -inf and zero gradients.
+ */
+#ifndef KDATTN_H
+#define KDATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KD_OK 0
+#define KD_ERR_INVALID -1     /* bad argument: shape, stride, pointer, alignment */
+#define KD_ERR_UNSUPPORTED -2 /* head dim / dtype / mode not built */
+#define KD_ERR_LAUNCH -3      /* HIP launch error */
+
+/* element dtypes */
+#define KD_BF16 0
+#define KD_F16 1
+/* span_id index dtypes */
+#define KD_I64 0
+#define KD_I32 1
+/* mask modes -- which branch of original_kernel.py:401, :478-517 applies */
+#define KD_MODE_FORMULA 0 /* any metadata given, or attention_mask given */
+#define KD_MODE_CAUSAL 1  /* no metadata, causal=True:  i >= j  (:512-513) */
+#define KD_MODE_ALL 2     /* no metadata, causal=False: all True (:514-515) */
+
+/* Mask metadata, as the reference's forward adapter receives it
+ * (original_kernel.py:1697-1715: lens, in_span, span_id, is_prefix). */
+typedef struct kd_meta_args {
+  const uint8_t *in_span;   /* bool [B, T] or NULL */
+  int64_t in_span_strides[2];
+  const void *span_id;      /* int64 or int32 [B, T] or NULL */
+  int64_t span_id_strides[2];
+  int32_t span_id_dtype;    /* KD_I64 / KD_I32 */
+  int32_t mode;             /* KD_MODE_* */
+  const uint8_t *is_prefix; /* bool [B, T] or NULL */
+  int64_t is_prefix_strides[2];
+  const int32_t *lens;      /* int32 [B] or NULL */
+  int64_t lens_stride;
+  int32_t B, T, D;
+  int32_t pad_;
+} kd_meta_args;
+
+/* Attention operands (forward and backward share one struct). */
+typedef struct kd_attn_args {
+  const void *q, *k, *v;        /* [B, H, T, D] */
+  int64_t q_strides[3], k_strides[3], v_strides[3];
+  void *o;                      /* [B, H, T, D] output (fwd) / input (bwd) */
+  int64_t o_strides[3];
+  float *lse;                   /* [B, H, T] fp32, contiguous */
+  const void *dout;             /* [B, H, T, D] (bwd) */
+  int64_t do_strides[3];
+  void *dq, *dk, *dv;           /* [B, H, T, D] (bwd) */
+  int64_t dq_strides[3], dk_strides[3], dv_strides[3];
+  float *delta;                 /* [B, H, T] fp32 workspace (bwd) */
+  int32_t B, H, T, D;
+  int32_t dtype;                /* KD_BF16 / KD_F16 */
+  float sm_scale;
+} kd_attn_args;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int kd_version(void);
+
+/* Message for the last non-zero status returned on this thread. */
+const char *kd_last_error_string(void);
+
+/* sizeof(kd_meta_args), sizeof(kd_attn_args): lets bindings check layouts. */
+void kd_struct_sizes(size_t *meta, size_t *attn);
+
+/* Workspace ("plan") bytes for B sequences of length T at head dim D, and
+ * the byte offsets of its sections (codes, class map, per-tile allowed
+ * counts, and the forward / dQ / dK-dV work lists).  offsets[] receives 17
+ * int64: codes, rep, cls, nnz, fwd_list, fwd_count, dq_list, dq_count,
+ * dkdv_list, dkdv_count, nT, fwd_group, dq_group, dkdv_group,
+ * n_fwd_blocks, n_dq_blocks, n_dkdv_blocks.  Replaces the per-tile mask evaluation of
+ * original_kernel.py:457-517 (the reference has no tile map). */
+int64_t kd_plan_bytes(int32_t B, int32_t T, int32_t D);
+int kd_plan_layout(int32_t B, int32_t T, int32_t D, int64_t *offsets);
+
+/* Build the plan: token codes, 64x64 tile class map (0 empty / 1 partial /
+ * 2 full, bit-exact against the dense mask), allowed-entry counts and the
+ * per-block work lists.  Mask rules: original_kernel.py:478-517, with lens
+ * (:299-303, :517) and the no-metadata fallbacks (:512-515). */
+int kd_plan_build(const kd_meta_args *meta, void *plan, void *stream);
+
+/* Forward: O and LSE.  Replaces attention_forward_adapter's launch of
+ * _flash_attn_fwd (original_kernel.py:1697-1778, kernel :279-626). */
+int kd_attn_fwd(const kd_attn_args *a, const void *plan, void *stream);
+
+/* Delta = rowsum(O * dO) in fp32 into a->delta.  Replaces
+ * _flash_attn_bwd_precompute (original_kernel.py:649-710, launch :1829-1846). */
+int kd_attn_bwd_delta(const kd_attn_args *a, void *stream);
+
+/* dQ from the saved LSE and Delta.  Replaces the dQ workers of
+ * _flash_attn_bwd (original_kernel.py:1173-1336). */
+int kd_attn_bwd_dq(const kd_attn_args *a, const void *plan, void *stream);
+
+/* dK and dV.  Replaces the dK/dV workers of _flash_attn_bwd
+ * (original_kernel.py:1339-1525). */
+int kd_attn_bwd_dkdv(const kd_attn_args *a, const void *plan, void *stream);
+
+/* Whole backward: Delta, then dQ and dK/dV.  Replaces
+ * attention_backward_adapter (original_kernel.py:1806-1898). */
+int kd_attn_bwd(const kd_attn_args *a, const void *plan, void *stream);
+
+/* Dense bool mask [B, H, T, T] (element strides b, h, q, k) from the plan's
+ * codes.  Replaces the RETURN_ATTENTION_MASK store of _flash_attn_fwd
+ * (original_kernel.py:519-545). */
+int kd_mask_dense(const void *plan, int32_t B, int32_t H, int32_t T, int32_t D, uint8_t *out,
+                  const int64_t *strides, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KDATTN_H */

@@ -1,0 +1,312 @@
+"""``flash_attention()`` -- the drop-in boundary (original_kernel.py:2096-2168).
+
+Keeps the reference's signature, defaults and return forms, and adds three
+optional keyword arguments for the incoherent-processing path.  The work goes
+through two torch custom ops in the ``kdattn`` namespace (the reference uses
+``flash_attention::forward`` / ``::backward``, :1697, :1806), each a thin
+shim over the C ABI of ``libkdattn.so``:
+
+* ``kdattn::fwd``  -> plan (codes, tile map, work lists) + forward kernel,
+  returns ``(O, LSE2, plan)``; the plan is saved for the backward.
+* ``kdattn::bwd``  -> Delta, dQ and dK/dV kernels from the saved plan.
+
+There is no CPU or PyTorch fallback: a missing library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+from ._lib import AttnArgs, MetaArgs
+
+SUPPORTED_HEAD_DIMS = (64, 128)
+REFERENCE_HEAD_DIMS = (16, 32, 64, 128, 256)  # original_kernel.py:1720
+
+
+def _stream(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _strides3(t):
+    s = t.stride()
+    return (ctypes.c_int64 * 3)(s[0], s[1], s[2])
+
+
+def _kernel_ready(x: torch.Tensor) -> torch.Tensor:
+    """Unit d-stride, 16-byte aligned base and 8-element-multiple strides."""
+    s = x.stride()
+    if (s[3] != 1 or x.data_ptr() % 16 != 0 or any(st % 8 for st in s[:3])):
+        x = x.contiguous()
+    return x
+
+
+def _dtype_code(dt) -> int:
+    if dt == torch.bfloat16:
+        return _lib.KD_BF16
+    if dt == torch.float16:
+        return _lib.KD_F16
+    raise ValueError(f"kernel dtype must be bf16 or fp16, got {dt}")
+
+
+def _mode(in_span, span_id, is_prefix, has_attention_mask, causal) -> int:
+    # original_kernel.py:401 FAST_PATH_NO_RULES; :512-515 fallbacks
+    if in_span is None and span_id is None and is_prefix is None and not has_attention_mask:
+        return _lib.KD_MODE_CAUSAL if causal else _lib.KD_MODE_ALL
+    return _lib.KD_MODE_FORMULA
+
+
+def build_plan(B, T, D, device, mode, in_span=None, span_id=None, is_prefix=None, lens=None):
+    """Run ``kd_plan_build`` and return the plan as a uint8 device tensor."""
+    lib = _lib.load()
+    plan = torch.empty(_lib.plan_bytes(B, T, D), dtype=torch.uint8, device=device)
+    m = MetaArgs()
+    m.B, m.T, m.D, m.mode = B, T, D, mode
+    if in_span is not None:
+        m.in_span = in_span.data_ptr()
+        m.in_span_strides[0], m.in_span_strides[1] = in_span.stride()
+    if is_prefix is not None:
+        m.is_prefix = is_prefix.data_ptr()
+        m.is_prefix_strides[0], m.is_prefix_strides[1] = is_prefix.stride()
+    if span_id is not None:
+        m.span_id = span_id.data_ptr()
+        m.span_id_strides[0], m.span_id_strides[1] = span_id.stride()
+        m.span_id_dtype = _lib.KD_I64 if span_id.dtype == torch.int64 else _lib.KD_I32
+    if lens is not None:
+        m.lens = lens.data_ptr()
+        m.lens_stride = lens.stride(0)
+    _lib.check(lib.kd_plan_build(ctypes.byref(m), _ptr(plan), _stream(device)), "kd_plan_build")
+    return plan
+
+
+def _attn_args(q, k, v, sm_scale) -> AttnArgs:
+    a = AttnArgs()
+    B, H, T, D = q.shape
+    a.B, a.H, a.T, a.D = B, H, T, D
+    a.dtype = _dtype_code(q.dtype)
+    a.sm_scale = float(sm_scale)
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    a.q_strides, a.k_strides, a.v_strides = _strides3(q), _strides3(k), _strides3(v)
+    return a
+
+
+# ----------------------------------------------------------------- custom ops
+@torch.library.custom_op("kdattn::fwd", mutates_args=(), device_types=("cuda",))
+def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tensor | None,
+            in_span: torch.Tensor | None, span_id: torch.Tensor | None,
+            is_prefix: torch.Tensor | None, sm_scale: float, mode: int
+            ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    B, H, T, D = q.shape
+    plan = build_plan(B, T, D, q.device, mode, in_span, span_id, is_prefix, lens)
+    o = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
+    lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+    a = _attn_args(q, k, v, sm_scale)
+    a.o, a.o_strides = o.data_ptr(), _strides3(o)
+    a.lse = lse.data_ptr()
+    _lib.check(_lib.load().kd_attn_fwd(ctypes.byref(a), _ptr(plan), _stream(q.device)), "kd_attn_fwd")
+    return o, lse, plan
+
+
+@_fwd_op.register_fake
+def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode):
+    B, H, T, D = q.shape
+    return (torch.empty((B, H, T, D), dtype=q.dtype, device=q.device),
+            torch.empty((B, H, T), dtype=torch.float32, device=q.device),
+            torch.empty(_lib.plan_bytes(B, T, D), dtype=torch.uint8, device=q.device))
+
+
+@torch.library.custom_op("kdattn::bwd", mutates_args=(), device_types=("cuda",))
+def _bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, lse: torch.Tensor,
+            do: torch.Tensor, plan: torch.Tensor, sm_scale: float
+            ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    B, H, T, D = q.shape
+    do = _kernel_ready(do)
+    dq = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
+    dk = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
+    dv = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
+    delta = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+    a = _attn_args(q, k, v, sm_scale)
+    a.o, a.o_strides = o.data_ptr(), _strides3(o)
+    a.lse = lse.data_ptr()
+    a.dout, a.do_strides = do.data_ptr(), _strides3(do)
+    a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+    a.dq_strides, a.dk_strides, a.dv_strides = _strides3(dq), _strides3(dk), _strides3(dv)
+    a.delta = delta.data_ptr()
+    _lib.check(_lib.load().kd_attn_bwd(ctypes.byref(a), _ptr(plan), _stream(q.device)), "kd_attn_bwd")
+    return dq, dk, dv
+
+
+@_bwd_op.register_fake
+def _bwd_fake(q, k, v, o, lse, do, plan, sm_scale):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def _setup_context(ctx, inputs, output):
+    q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode = inputs
+    o, lse, plan = output
+    ctx.save_for_backward(q, k, v, o, lse, plan)
+    ctx.sm_scale = sm_scale
+
+
+def _backward(ctx, do, dlse, dplan):
+    # dlse is ignored, as in original_kernel.py:1965-1992
+    q, k, v, o, lse, plan = ctx.saved_tensors
+    dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, ctx.sm_scale)
+    return dq, dk, dv, None, None, None, None, None, None
+
+
+_fwd_op.register_autograd(_backward, setup_context=_setup_context)
+
+
+# -------------------------------------------------------------- public entry
+def _check_meta(name, t, B, T, device, dtypes):
+    if t is None:
+        return None
+    if t.shape != (B, T):
+        raise ValueError(f"{name} must have shape [B, T] = [{B}, {T}], got {tuple(t.shape)}")
+    if t.dtype not in dtypes:
+        raise ValueError(f"{name} dtype must be one of {dtypes}, got {t.dtype}")
+    if t.device != device:
+        raise ValueError(f"{name} must be on {device}")
+    return t
+
+
+def flash_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    lens: torch.Tensor | None = None,
+    sm_scale: float | None = None,
+    causal: bool = True,
+    autotune=False,
+    return_lse=False,
+    prescale_qk=False,
+    precision="tf32",
+    attention_mask: torch.Tensor | None = None,
+    in_span: torch.Tensor | None = None,
+    span_id: torch.Tensor | None = None,
+    is_prefix: torch.Tensor | None = None,
+    return_attention_mask: bool = False,
+    *,
+    hadamard: bool = False,
+    hadamard_seed: int | None = None,
+    qk_dtype: str = "bf16",
+):
+    """Hierarchical-mask flash attention on MI355X (same contract as the reference).
+
+    Args mirror ``original_kernel.py:2096-2112``.  ``autotune`` and
+    ``prescale_qk`` are accepted and ignored (tile shapes are compile-time
+    constants here and the scale is always applied in fp32); ``precision``
+    must be ``"ieee"`` or ``"tf32"``.  ``attention_mask``'s contents are not
+    read, exactly as in the reference: when it is given without metadata the
+    mask formula runs with default metadata, i.e. ``i >= j``.
+
+    Extra keyword-only arguments: ``hadamard`` rotates Q and K by
+    ``diag(s) H_d / sqrt(d)`` with signs ``generate_hadamard_signs(d,
+    hadamard_seed)`` before the product (exact in real arithmetic);
+    ``qk_dtype="fp8_e4m3"`` additionally runs Q K^T on fp8 with per-(b, h)
+    absmax scales.
+
+    Returns ``O``, ``(O, LSE)``, ``(O, mask)`` or ``((O, LSE), mask)`` as at
+    ``:2083-2089``; LSE is fp32 ``[B, H, T]`` in log2 units, mask is bool
+    ``[B, H, T, T]``.
+    """
+    if q.dim() != 4:
+        raise ValueError("q must be [batch, heads, time, head_dim]")
+    B, H, T, D = q.shape
+    if D not in REFERENCE_HEAD_DIMS:
+        raise ValueError(f"head_dim must be one of {REFERENCE_HEAD_DIMS}, got {D}")
+    if D not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head_dim {D} is not built for gfx950 (supported: {SUPPORTED_HEAD_DIMS})")
+    if k.shape[-1] != D or v.shape[-1] != D:
+        raise ValueError("q, k and v must share head_dim")
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("q, k and v must have the same [B, H, T, d] shape")
+    if precision not in ("ieee", "tf32"):
+        raise ValueError(f"precision must be 'ieee' or 'tf32', got {precision!r}")
+    if lens is not None and (lens.dtype != torch.int32 or lens.dim() != 1 or lens.shape[0] != B):
+        raise ValueError("lens must be an int32 tensor of shape [batch]")
+    if qk_dtype not in ("bf16", "fp8_e4m3"):
+        raise ValueError(f"qk_dtype must be 'bf16' or 'fp8_e4m3', got {qk_dtype!r}")
+    if not q.is_cuda:
+        raise ValueError("flash_attention runs on the GPU only (no CPU fallback)")
+    if k.device != q.device or v.device != q.device:
+        raise ValueError("q, k and v must be on the same device")
+    if qk_dtype != "bf16":
+        raise NotImplementedError("fp8 QK^T path is not built yet")
+    if hadamard:
+        raise NotImplementedError("Hadamard path is not built yet")
+
+    if sm_scale is None:
+        sm_scale = D ** -0.5  # original_kernel.py:2145-2147
+    device = q.device
+    in_span = _check_meta("in_span", in_span, B, T, device, (torch.bool, torch.uint8))
+    is_prefix = _check_meta("is_prefix", is_prefix, B, T, device, (torch.bool, torch.uint8))
+    span_id = _check_meta("span_id", span_id, B, T, device, (torch.int64, torch.int32))
+    if lens is not None and lens.device != device:
+        raise ValueError("lens must be on the same device as q")
+    mode = _mode(in_span, span_id, is_prefix, attention_mask is not None, causal)
+
+    in_dtype = q.dtype
+    if in_dtype == torch.float32:
+        # CDNA4 has no tf32 MFMA: fp32 inputs are computed on bf16 MFMA with
+        # fp32 accumulation and the results cast back to fp32.
+        q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+    elif in_dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"unsupported dtype {in_dtype}")
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+
+    o, lse, plan = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode))
+    if in_dtype == torch.float32:
+        o = o.to(torch.float32)
+
+    mask = None
+    if return_attention_mask:
+        mask = torch.empty((B, H, T, T), dtype=torch.bool, device=device)
+        st = (ctypes.c_int64 * 4)(*mask.stride())
+        _lib.check(_lib.load().kd_mask_dense(_ptr(plan), B, H, T, D, _ptr(mask), st, _stream(device)),
+                   "kd_mask_dense")
+    if return_attention_mask:
+        if return_lse:
+            return (o, lse), mask
+        return o, mask
+    if return_lse:
+        return o, lse
+    return o
+
+
+def plan_views(plan: torch.Tensor, B: int, T: int, D: int) -> dict:
+    """Typed views of a plan tensor's sections (codes, class map, lists)."""
+    L = _lib.plan_layout(B, T, D)
+    nT = L["nT"]
+
+    def view(off, n, dtype):
+        nbytes = n * torch.tensor([], dtype=dtype).element_size()
+        return plan[off: off + nbytes].view(dtype)
+
+    nf, nq, nk = L["n_fwd_blocks"], L["n_dq_blocks"], L["n_dkdv_blocks"]
+    return {
+        "codes": view(L["codes"], B * T, torch.int32).view(B, T),
+        "cls": view(L["cls"], B * nT * nT, torch.uint8).view(B, nT, nT),
+        "nnz": view(L["nnz"], B * nT * nT, torch.int32).view(B, nT, nT),
+        "fwd_list": view(L["fwd_list"], B * nf * nT, torch.int32).view(B, nf, nT),
+        "fwd_count": view(L["fwd_count"], B * nf, torch.int32).view(B, nf),
+        "dq_list": view(L["dq_list"], B * nq * nT, torch.int32).view(B, nq, nT),
+        "dq_count": view(L["dq_count"], B * nq, torch.int32).view(B, nq),
+        "dkdv_list": view(L["dkdv_list"], B * nk * nT, torch.int32).view(B, nk, nT),
+        "dkdv_count": view(L["dkdv_count"], B * nk, torch.int32).view(B, nk),
+        "layout": L,
+    }
+
+
+def mask_mode(in_span=None, span_id=None, is_prefix=None, attention_mask=None, causal=True) -> int:
+    return _mode(in_span, span_id, is_prefix, attention_mask is not None, causal)
+
+
+LOG2E = math.log2(math.e)

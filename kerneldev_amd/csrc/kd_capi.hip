@@ -1,0 +1,174 @@
+// extern "C" entry points of libkdattn.so: argument checks, then launches.
+// Every check that fails returns a status instead of launching, so a bad
+// shape or stride never reaches a kernel.
+#include <cmath>
+#include <cstdio>
+#include <string>
+
+#include "kd_internal.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* msg) {
+  g_err = msg;
+  return code;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool strides_ok(const int64_t* s) {
+  for (int i = 0; i < 3; ++i)
+    if (s[i] < 0 || (s[i] & 7) != 0) return false;
+  return true;
+}
+
+// Largest element offset reachable by a [B, H, T, D] view (for int32 safety
+// of the in-kernel index math the offsets are int64; this only rejects
+// negative / overlapping-by-construction layouts).
+int check_tensor(const void* p, const int64_t* s, const char* name) {
+  if (p == nullptr) {
+    g_err = std::string(name) + " is NULL";
+    return KD_ERR_INVALID;
+  }
+  if (!aligned16(p)) {
+    g_err = std::string(name) + " must be 16-byte aligned";
+    return KD_ERR_INVALID;
+  }
+  if (!strides_ok(s)) {
+    g_err = std::string(name) + " strides (b, h, t) must be non-negative multiples of 8 elements";
+    return KD_ERR_INVALID;
+  }
+  return KD_OK;
+}
+
+int check_common(const kd_attn_args* a) {
+  if (a == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
+  if (a->B < 1 || a->H < 1 || a->T < 1) return fail(KD_ERR_INVALID, "B, H and T must be >= 1");
+  if (a->T > (1 << 24) - 2) return fail(KD_ERR_UNSUPPORTED, "T must be < 2^24 - 1");
+  if (int64_t(a->B) * a->H * ((a->T + 63) / 64) > (int64_t(1) << 31) - 1)
+    return fail(KD_ERR_UNSUPPORTED, "B * H * ceil(T / 64) exceeds the grid limit");
+  if (a->D != 64 && a->D != 128) return fail(KD_ERR_UNSUPPORTED, "head dim must be 64 or 128");
+  if (a->dtype != KD_BF16 && a->dtype != KD_F16) return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16 or fp16");
+  if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale))
+    return fail(KD_ERR_INVALID, "sm_scale must be finite and > 0");
+  return KD_OK;
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+int kd_version(void) { return 100; }
+
+const char* kd_last_error_string(void) { return g_err.c_str(); }
+
+void kd_struct_sizes(size_t* meta, size_t* attn) {
+  if (meta) *meta = sizeof(kd_meta_args);
+  if (attn) *attn = sizeof(kd_attn_args);
+}
+
+int64_t kd_plan_bytes(int32_t B, int32_t T, int32_t D) {
+  if (B < 1 || T < 1) return -1;
+  return int64_t(kd::plan_layout(B, T, D).total);
+}
+
+int kd_plan_layout(int32_t B, int32_t T, int32_t D, int64_t* off) {
+  if (off == nullptr || B < 1 || T < 1) return fail(KD_ERR_INVALID, "bad plan_layout arguments");
+  const kd::PlanLayout L = kd::plan_layout(B, T, D);
+  const int64_t v[17] = {int64_t(L.codes),     int64_t(L.rep),        int64_t(L.cls),     int64_t(L.nnz),
+                         int64_t(L.fwd_list),  int64_t(L.fwd_count),  int64_t(L.dq_list), int64_t(L.dq_count),
+                         int64_t(L.dkdv_list), int64_t(L.dkdv_count), L.nT,               L.fwd_group,
+                         L.dq_group,           L.dkdv_group,          L.n_fwd_blocks,     L.n_dq_blocks,
+                         L.n_dkdv_blocks};
+  for (int i = 0; i < 17; ++i) off[i] = v[i];
+  return KD_OK;
+}
+
+int kd_plan_build(const kd_meta_args* m, void* plan, void* stream) {
+  if (m == nullptr || plan == nullptr) return fail(KD_ERR_INVALID, "meta or plan is NULL");
+  if (!aligned16(plan)) return fail(KD_ERR_INVALID, "plan must be 16-byte aligned");
+  if (m->B < 1 || m->T < 1) return fail(KD_ERR_INVALID, "B and T must be >= 1");
+  if (m->T > (1 << 24) - 2) return fail(KD_ERR_UNSUPPORTED, "T must be < 2^24 - 1");
+  if (m->mode != KD_MODE_FORMULA && m->mode != KD_MODE_CAUSAL && m->mode != KD_MODE_ALL)
+    return fail(KD_ERR_INVALID, "unknown mask mode");
+  if (m->span_id != nullptr && m->span_id_dtype != KD_I64 && m->span_id_dtype != KD_I32)
+    return fail(KD_ERR_INVALID, "span_id dtype must be int64 or int32");
+  const int64_t* ss[3] = {m->in_span_strides, m->span_id_strides, m->is_prefix_strides};
+  for (int i = 0; i < 3; ++i)
+    if (ss[i][0] < 0 || ss[i][1] < 0) return fail(KD_ERR_INVALID, "metadata strides must be non-negative");
+  return kd::launch_plan(*m, static_cast<uint8_t*>(plan), as_stream(stream));
+}
+
+int kd_attn_fwd(const kd_attn_args* a, const void* plan, void* stream) {
+  int r = check_common(a);
+  if (r) return r;
+  if (plan == nullptr) return fail(KD_ERR_INVALID, "plan is NULL");
+  if ((r = check_tensor(a->q, a->q_strides, "q")) || (r = check_tensor(a->k, a->k_strides, "k")) ||
+      (r = check_tensor(a->v, a->v_strides, "v")) || (r = check_tensor(a->o, a->o_strides, "o")))
+    return r;
+  r = kd::launch_fwd(*a, static_cast<const uint8_t*>(plan), as_stream(stream));
+  return r ? fail(r, "kernel launch failed (forward)") : KD_OK;
+}
+
+int kd_attn_bwd_delta(const kd_attn_args* a, void* stream) {
+  int r = check_common(a);
+  if (r) return r;
+  if ((r = check_tensor(a->o, a->o_strides, "o")) || (r = check_tensor(a->dout, a->do_strides, "dout")))
+    return r;
+  if (a->delta == nullptr) return fail(KD_ERR_INVALID, "delta is NULL");
+  r = kd::launch_delta(*a, as_stream(stream));
+  return r ? fail(r, "kernel launch failed (delta)") : KD_OK;
+}
+
+static int check_bwd(const kd_attn_args* a, const void* plan) {
+  int r = check_common(a);
+  if (r) return r;
+  if (plan == nullptr) return fail(KD_ERR_INVALID, "plan is NULL");
+  if (a->lse == nullptr || a->delta == nullptr) return fail(KD_ERR_INVALID, "lse and delta are required");
+  if ((r = check_tensor(a->q, a->q_strides, "q")) || (r = check_tensor(a->k, a->k_strides, "k")) ||
+      (r = check_tensor(a->v, a->v_strides, "v")) || (r = check_tensor(a->dout, a->do_strides, "dout")))
+    return r;
+  return KD_OK;
+}
+
+int kd_attn_bwd_dq(const kd_attn_args* a, const void* plan, void* stream) {
+  int r = check_bwd(a, plan);
+  if (r) return r;
+  if ((r = check_tensor(a->dq, a->dq_strides, "dq"))) return r;
+  r = kd::launch_dq(*a, static_cast<const uint8_t*>(plan), as_stream(stream));
+  return r ? fail(r, "kernel launch failed (dq)") : KD_OK;
+}
+
+int kd_attn_bwd_dkdv(const kd_attn_args* a, const void* plan, void* stream) {
+  int r = check_bwd(a, plan);
+  if (r) return r;
+  if ((r = check_tensor(a->dk, a->dk_strides, "dk")) || (r = check_tensor(a->dv, a->dv_strides, "dv"))) return r;
+  r = kd::launch_dkdv(*a, static_cast<const uint8_t*>(plan), as_stream(stream));
+  return r ? fail(r, "kernel launch failed (dkdv)") : KD_OK;
+}
+
+int kd_attn_bwd(const kd_attn_args* a, const void* plan, void* stream) {
+  int r = kd_attn_bwd_delta(a, stream);
+  if (r) return r;
+  r = kd_attn_bwd_dq(a, plan, stream);
+  if (r) return r;
+  return kd_attn_bwd_dkdv(a, plan, stream);
+}
+
+int kd_mask_dense(const void* plan, int32_t B, int32_t H, int32_t T, int32_t D, uint8_t* out,
+                  const int64_t* strides, void* stream) {
+  if (plan == nullptr || out == nullptr || strides == nullptr) return fail(KD_ERR_INVALID, "NULL argument");
+  if (B < 1 || H < 1 || T < 1) return fail(KD_ERR_INVALID, "B, H and T must be >= 1");
+  for (int i = 0; i < 4; ++i)
+    if (strides[i] < 0) return fail(KD_ERR_INVALID, "mask strides must be non-negative");
+  const kd::PlanLayout L = kd::plan_layout(B, T, D);
+  const uint32_t* codes = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(plan) + L.codes);
+  const int r = kd::launch_mask_dense(codes, B, H, T, out, strides, as_stream(stream));
+  return r ? fail(r, "kernel launch failed (mask)") : KD_OK;
+}
+
+}  // extern "C"

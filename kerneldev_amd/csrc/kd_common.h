@@ -1,0 +1,100 @@
+// Shared device helpers for the gfx950 attention kernels.
+//
+// Token mask codes (one uint32 per token, built by kd_mask.hip):
+//   bit 0  P  is_prefix
+//   bit 1  S  in_span
+//   bit 2  M  MASKQ (span_id == -1, only when span_id is given)
+//   bit 3  C  context  (= !P & !S & !M)
+//   bits 4-7  A  accept mask: which key flag bits this token, as a QUERY, sees
+//             unconditionally:  P|C -> {P},  S -> {C},  M -> {S, P}
+//   bits 8-31 R  span group: 0, or 1 + first position of this token's span id
+//             (only for tokens with S and span_id > 0)
+// Tokens at or beyond seq_len = min(lens[b], T) get code 0 (see nothing, seen
+// by nothing).  With these codes the 7-term rule of original_kernel.py:478-517
+// becomes
+//   allow(i, j) = (A_i & flags_j) | (C_i & C_j & i >= j) | (R_i != 0 & R_i == R_j)
+// because prefix_to_prefix | context_to_prefix | maskq_to_cls are "key is P",
+// span_to_context is "key is C", maskq_to_spans is "key is S", context_causal
+// is the C&C&i>=j term and same_span is the R equality.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define KD_DEV __device__ __forceinline__
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+namespace kd {
+
+enum : uint32_t { FLAG_P = 1u, FLAG_S = 2u, FLAG_M = 4u, FLAG_C = 8u };
+
+KD_DEV bool allow(uint32_t qc, uint32_t kc, int i, int j) {
+  return (((qc >> 4) & kc & 0xFu) != 0u) | (((qc & kc & FLAG_C) != 0u) & (i >= j)) |
+         (((qc >> 8) != 0u) & ((qc >> 8) == (kc >> 8)));
+}
+
+// Host-and-device version for the classifier (same expression).
+__host__ __device__ inline bool allow_hd(uint32_t qc, uint32_t kc, int i, int j) {
+  return (((qc >> 4) & kc & 0xFu) != 0u) || (((qc & kc & FLAG_C) != 0u) && (i >= j)) ||
+         (((qc >> 8) != 0u) && ((qc >> 8) == (kc >> 8)));
+}
+
+// Element types -----------------------------------------------------------
+struct BF16 {};
+struct F16 {};
+
+template <class E> KD_DEV f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c);
+template <> KD_DEV f32x16 mfma32x32x16<BF16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <> KD_DEV f32x16 mfma32x32x16<F16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Two fp32 -> packed pair of 16-bit values (round to nearest even).
+template <class E> KD_DEV uint32_t pack2(float lo, float hi);
+template <> KD_DEV uint32_t pack2<BF16>(float lo, float hi) {
+  f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+template <> KD_DEV uint32_t pack2<F16>(float lo, float hi) {
+  f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
+template <class E> KD_DEV float to_f32(uint16_t bits);
+template <> KD_DEV float to_f32<BF16>(uint16_t bits) { return __uint_as_float(uint32_t(bits) << 16); }
+template <> KD_DEV float to_f32<F16>(uint16_t bits) {
+  return float(__builtin_bit_cast(_Float16, bits));
+}
+
+// Lo/hi 16-bit halves of two dwords packed into one dword (v_perm_b32).
+KD_DEV uint32_t pack_lo(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x05040100u); }
+KD_DEV uint32_t pack_hi(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x07060302u); }
+
+// Row permutation used for the A operand of 32x32 MFMAs whose output feeds the
+// next MFMA's B operand straight from registers.  The 32x32 f32 accumulator
+// gives lane (h = lane/32, c = lane%32) the rows 8g + 4h + i (g, i in 0..3).
+// Loading MFMA row rho from logical row sigma(rho) = rho with bits 2 and 3
+// swapped makes accumulator register r hold logical row 16*(r/8) + 8h + r%8,
+// i.e. registers 8t..8t+7 are exactly the 8 consecutive k-slots lane half h
+// must supply for k-step t of the following 32x32x16 MFMA.
+KD_DEV int sigma(int rho) { return (rho & ~12) | ((rho & 4) << 1) | ((rho & 8) >> 1); }
+
+KD_DEV float wave_max32(float v) { return fmaxf(v, __shfl_xor(v, 32)); }
+KD_DEV float wave_sum32(float v) { return v + __shfl_xor(v, 32); }
+
+KD_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+KD_DEV float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+}  // namespace kd

@@ -1,0 +1,50 @@
+// Internal declarations shared by the kernel translation units and the C ABI.
+#pragma once
+#include <algorithm>
+
+#include "../../include/kdattn.h"
+#include "kd_common.h"
+
+namespace kd {
+
+typedef kd_meta_args MetaArgs;
+typedef kd_attn_args AttnArgs;
+
+enum : uint8_t { TILE_EMPTY = 0, TILE_PARTIAL = 1, TILE_FULL = 2 };
+
+// Block shapes of the attention kernels (rows per workgroup).  The plan's
+// work lists group the 64x64 class map by these.
+inline int fwd_rows_per_block(int /*D*/) { return 128; }
+inline int dq_rows_per_block(int /*D*/) { return 128; }
+inline int dkdv_keys_per_block(int /*D*/) { return 128; }
+
+struct PlanLayout {
+  size_t codes, rep, cls, nnz, fwd_list, fwd_count, dq_list, dq_count, dkdv_list, dkdv_count, total;
+  int nT, fwd_group, dq_group, dkdv_group, n_fwd_blocks, n_dq_blocks, n_dkdv_blocks;
+};
+
+PlanLayout plan_layout(int B, int T, int D);
+int launch_plan(const MetaArgs& m, uint8_t* plan, hipStream_t st);
+int launch_mask_dense(const uint32_t* codes, int B, int H, int T, uint8_t* out, const int64_t* strides,
+                      hipStream_t st);
+int launch_fwd(const AttnArgs& a, const uint8_t* plan, hipStream_t st);
+int launch_delta(const AttnArgs& a, hipStream_t st);
+int launch_dq(const AttnArgs& a, const uint8_t* plan, hipStream_t st);
+int launch_dkdv(const AttnArgs& a, const uint8_t* plan, hipStream_t st);
+
+// Linear workgroup id -> work index so that each XCD (workgroups are dealt
+// round-robin over the 8 XCDs) receives one contiguous range of work items,
+// i.e. the q- or k-blocks of the same (b, h) share that XCD's L2.
+KD_DEV int xcd_remap(int wg, int n) {
+  constexpr int NX = 8;
+  const int per = n / NX;
+  const int rem = n % NX;
+  const int x = wg % NX, slot = wg / NX;
+  // the first `rem` XCDs take per+1 items each
+  const int base = x * per + min(x, rem);
+  const int cap = per + (x < rem ? 1 : 0);
+  if (slot < cap) return base + slot;
+  return wg;  // unreachable when gridDim.x == n
+}
+
+}  // namespace kd

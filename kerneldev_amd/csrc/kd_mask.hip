@@ -1,0 +1,230 @@
+// Mask metadata -> per-token codes -> 64x64 tile class map -> work lists.
+//
+// Replaces the per-element, per-tile re-evaluation of the cocktail-party mask
+// in every reference kernel (original_kernel.py:457-517, :1249-1328,
+// :1435-1514) with one classification pass whose output all attention
+// kernels share:
+//   codes   u32 [B, T]            token code (layout in kd_common.h)
+//   cls     u8  [B, nT, nT]       0 EMPTY / 1 PARTIAL / 2 FULL per 64x64 tile
+//   nnz     i32 [B, nT, nT]       allowed entries per tile
+//   lists   u32 [B, nRB, nT]      per row block: (tile << 1) | full, ascending
+//   counts  i32 [B, nRB]
+#include "kd_internal.h"
+
+namespace kd {
+
+// ---- span-group representative -------------------------------------------
+// rep[b][j] = min { t : S_t & sid_t > 0 & sid_t == sid_j } for eligible j
+// (S_j & sid_j > 0).  Brute force over the lower triangle of 256x256 chunk
+// pairs with an atomic min; exact for any int64 span ids.
+
+__global__ void k_fill_u32(uint32_t* p, int64_t n, uint32_t v) {
+  int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+KD_DEV int64_t load_sid(const MetaArgs& m, int b, int t) {
+  if (m.span_id == nullptr) return 0;
+  int64_t off = int64_t(b) * m.span_id_strides[0] + int64_t(t) * m.span_id_strides[1];
+  return m.span_id_dtype == KD_I64 ? static_cast<const int64_t*>(m.span_id)[off]
+                                   : int64_t(static_cast<const int32_t*>(m.span_id)[off]);
+}
+KD_DEV bool load_flag(const uint8_t* p, const int64_t* st, int b, int t) {
+  return p != nullptr && p[int64_t(b) * st[0] + int64_t(t) * st[1]] != 0;
+}
+KD_DEV bool eligible(const MetaArgs& m, int b, int t, int64_t* sid) {
+  *sid = load_sid(m, b, t);
+  return m.span_id != nullptr && load_flag(m.in_span, m.in_span_strides, b, t) && *sid > 0;
+}
+
+__global__ __launch_bounds__(256) void k_span_rep(MetaArgs m, uint32_t* rep) {
+  const int jc = blockIdx.x, tc = blockIdx.y, b = blockIdx.z;
+  if (tc > jc) return;
+  __shared__ int64_t s_sid[256];
+  __shared__ int s_ok[256];
+  const int t = tc * 256 + threadIdx.x;
+  int64_t sid_t = 0;
+  s_ok[threadIdx.x] = (t < m.T) && eligible(m, b, t, &sid_t);
+  s_sid[threadIdx.x] = sid_t;
+  __syncthreads();
+  const int j = jc * 256 + threadIdx.x;
+  if (j >= m.T) return;
+  int64_t sid_j;
+  if (!eligible(m, b, j, &sid_j)) return;
+  for (int x = 0; x < 256; ++x) {
+    if (s_ok[x] && s_sid[x] == sid_j) {
+      atomicMin(&rep[int64_t(b) * m.T + j], uint32_t(tc * 256 + x));
+      return;
+    }
+  }
+}
+
+// ---- token codes -------------------------------------------------------
+__global__ void k_codes(MetaArgs m, const uint32_t* rep, uint32_t* codes) {
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= int64_t(m.B) * m.T) return;
+  const int b = int(idx / m.T), t = int(idx % m.T);
+  int seq_len = m.T;
+  if (m.lens != nullptr) seq_len = min(m.lens[int64_t(b) * m.lens_stride], m.T);
+  uint32_t code = 0;
+  if (t < seq_len) {
+    if (m.mode == KD_MODE_CAUSAL) {
+      code = FLAG_C;  // every token context: C & C & i >= j  (:512-513)
+    } else if (m.mode == KD_MODE_ALL) {
+      code = FLAG_P | (FLAG_P << 4);  // P sees P: every pair (:514-515)
+    } else {
+      const bool P = load_flag(m.is_prefix, m.is_prefix_strides, b, t);
+      const bool S = load_flag(m.in_span, m.in_span_strides, b, t);
+      const int64_t sid = load_sid(m, b, t);
+      const bool M = m.span_id != nullptr && sid == -1;
+      const bool C = !S && !P && !M;
+      uint32_t acc = 0;
+      if (P || C) acc |= FLAG_P;          // prefix_to_prefix, context_to_prefix
+      if (S) acc |= FLAG_C;               // span_to_context
+      if (M) acc |= FLAG_S | FLAG_P;      // maskq_to_spans, maskq_to_cls
+      code = (P ? FLAG_P : 0u) | (S ? FLAG_S : 0u) | (M ? FLAG_M : 0u) | (C ? FLAG_C : 0u) | (acc << 4);
+      if (m.span_id != nullptr && S && sid > 0) code |= (rep[idx] + 1u) << 8;  // same_span
+    }
+  }
+  codes[idx] = code;
+}
+
+// ---- 64x64 tile classifier ---------------------------------------------
+// One wave per tile: lane = query row, loop over the tile's 64 keys.
+__global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, int nT, uint8_t* cls,
+                                                 int32_t* nnz) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int qt = blockIdx.y, b = blockIdx.z;
+  const int kt0 = blockIdx.x * 4;
+  __shared__ uint32_t s_k[256];
+  {
+    const int j = kt0 * 64 + threadIdx.x;
+    s_k[threadIdx.x] = (j < T) ? codes[int64_t(b) * T + j] : 0u;
+  }
+  __syncthreads();
+  const int kt = kt0 + wave;
+  if (kt >= nT) return;
+  const int i = qt * 64 + lane;
+  const uint32_t qc = (i < T) ? codes[int64_t(b) * T + i] : 0u;
+  int cnt = 0;
+  for (int x = 0; x < 64; ++x) cnt += allow(qc, s_k[wave * 64 + x], i, kt * 64 + x) ? 1 : 0;
+  for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off);
+  if (lane == 0) {
+    const int64_t o = (int64_t(b) * nT + qt) * nT + kt;
+    cls[o] = cnt == 0 ? TILE_EMPTY : (cnt == 64 * 64 ? TILE_FULL : TILE_PARTIAL);
+    if (nnz != nullptr) nnz[o] = cnt;
+  }
+}
+
+// ---- per-row-block work lists ------------------------------------------
+// by_key = 0: row blocks group `group` q-tiles, entries are k-tiles.
+// by_key = 1: row blocks group `group` k-tiles, entries are q-tiles.
+__global__ void k_lists(const uint8_t* cls, int B, int nT, int group, int by_key, uint32_t* entries,
+                        int32_t* counts) {
+  const int nRB = (nT + group - 1) / group;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= B * nRB) return;
+  const int b = idx / nRB, rb = idx % nRB;
+  const uint8_t* base = cls + int64_t(b) * nT * nT;
+  uint32_t* out = entries + int64_t(idx) * nT;
+  int n = 0;
+  for (int c = 0; c < nT; ++c) {
+    bool any_ne = false, all_full = true;
+    for (int r = 0; r < group; ++r) {
+      const int row = rb * group + r;
+      uint8_t k = TILE_EMPTY;
+      if (row < nT) k = by_key ? base[int64_t(c) * nT + row] : base[int64_t(row) * nT + c];
+      any_ne |= (k != TILE_EMPTY);
+      all_full &= (k == TILE_FULL);
+    }
+    if (any_ne) out[n++] = (uint32_t(c) << 1) | (all_full ? 1u : 0u);
+  }
+  for (int c = n; c < nT; ++c) out[c] = 0;
+  counts[idx] = n;
+}
+
+// ---- dense mask output (return_attention_mask) -------------------------
+__global__ void k_mask_dense(const uint32_t* codes, int B, int H, int T, uint8_t* out, int64_t sb,
+                             int64_t sh, int64_t sq, int64_t sk) {
+  const int64_t n = int64_t(B) * H * T * T;
+  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < n;
+       idx += int64_t(gridDim.x) * blockDim.x) {
+    const int j = int(idx % T);
+    const int i = int((idx / T) % T);
+    const int h = int((idx / (int64_t(T) * T)) % H);
+    const int b = int(idx / (int64_t(T) * T * H));
+    const bool a = allow(codes[int64_t(b) * T + i], codes[int64_t(b) * T + j], i, j);
+    out[b * sb + h * sh + i * sq + j * sk] = a ? 1 : 0;
+  }
+}
+
+// ---- host launchers ----------------------------------------------------
+PlanLayout plan_layout(int B, int T, int D) {
+  PlanLayout L{};
+  const int nT = (T + 63) / 64;
+  L.nT = nT;
+  L.fwd_group = fwd_rows_per_block(D) / 64;
+  L.dq_group = dq_rows_per_block(D) / 64;
+  L.dkdv_group = dkdv_keys_per_block(D) / 64;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = off;
+    off += (bytes + 255) & ~size_t(255);
+    return o;
+  };
+  const size_t BT = size_t(B) * T, BTT = size_t(B) * nT * nT;
+  L.codes = take(BT * 4);
+  L.rep = take(BT * 4);
+  L.cls = take(BTT);
+  L.nnz = take(BTT * 4);
+  const int nf = (nT + L.fwd_group - 1) / L.fwd_group;
+  const int nq = (nT + L.dq_group - 1) / L.dq_group;
+  const int nk = (nT + L.dkdv_group - 1) / L.dkdv_group;
+  L.n_fwd_blocks = nf;
+  L.n_dq_blocks = nq;
+  L.n_dkdv_blocks = nk;
+  L.fwd_list = take(size_t(B) * nf * nT * 4);
+  L.fwd_count = take(size_t(B) * nf * 4);
+  L.dq_list = take(size_t(B) * nq * nT * 4);
+  L.dq_count = take(size_t(B) * nq * 4);
+  L.dkdv_list = take(size_t(B) * nk * nT * 4);
+  L.dkdv_count = take(size_t(B) * nk * 4);
+  L.total = off;
+  return L;
+}
+
+int launch_plan(const MetaArgs& m, uint8_t* plan, hipStream_t st) {
+  const PlanLayout L = plan_layout(m.B, m.T, m.D);
+  uint32_t* codes = reinterpret_cast<uint32_t*>(plan + L.codes);
+  uint32_t* rep = reinterpret_cast<uint32_t*>(plan + L.rep);
+  uint8_t* cls = plan + L.cls;
+  int32_t* nnz = reinterpret_cast<int32_t*>(plan + L.nnz);
+  const int64_t BT = int64_t(m.B) * m.T;
+  const int nchunk = (m.T + 255) / 256;
+  if (m.mode == KD_MODE_FORMULA && m.span_id != nullptr && m.in_span != nullptr) {
+    hipLaunchKernelGGL(k_fill_u32, dim3(unsigned((BT + 255) / 256)), dim3(256), 0, st, rep, BT, 0xFFFFFFFFu);
+    hipLaunchKernelGGL(k_span_rep, dim3(nchunk, nchunk, m.B), dim3(256), 0, st, m, rep);
+  }
+  hipLaunchKernelGGL(k_codes, dim3(unsigned((BT + 255) / 256)), dim3(256), 0, st, m, rep, codes);
+  hipLaunchKernelGGL(k_tilemap, dim3((L.nT + 3) / 4, L.nT, m.B), dim3(256), 0, st, codes, m.T, L.nT, cls, nnz);
+  auto lists = [&](int group, int by_key, size_t lo, size_t co, int nrb) {
+    const int n = m.B * nrb;
+    hipLaunchKernelGGL(k_lists, dim3((n + 63) / 64), dim3(64), 0, st, cls, m.B, L.nT, group, by_key,
+                       reinterpret_cast<uint32_t*>(plan + lo), reinterpret_cast<int32_t*>(plan + co));
+  };
+  lists(L.fwd_group, 0, L.fwd_list, L.fwd_count, L.n_fwd_blocks);
+  lists(L.dq_group, 0, L.dq_list, L.dq_count, L.n_dq_blocks);
+  lists(L.dkdv_group, 1, L.dkdv_list, L.dkdv_count, L.n_dkdv_blocks);
+  return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
+}
+
+int launch_mask_dense(const uint32_t* codes, int B, int H, int T, uint8_t* out, const int64_t* s,
+                      hipStream_t st) {
+  const int64_t n = int64_t(B) * H * T * T;
+  const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
+  hipLaunchKernelGGL(k_mask_dense, dim3(unsigned(blocks)), dim3(256), 0, st, codes, B, H, T, out, s[0], s[1],
+                     s[2], s[3]);
+  return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
+}
+
+}  // namespace kd

@@ -1,0 +1,138 @@
+"""GPU parity of the forward and backward kernels against the fp64 oracle.
+
+Tolerance: O, dQ, dK, dV within max-abs 2e-2 and
+rel-RMS 1e-2 for bf16 against the dense-masked reference; LSE (log2 units)
+within the same bounds.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close, oracle_fwd_bwd, oracle_mask, select_heads
+from kerneldev_amd import flash_attention
+from kerneldev_amd.synth import CONFIG3_LAYOUT, cocktail_batch, config_inputs, qkvdo
+
+pytestmark = pytest.mark.gpu
+
+
+def run_gpu(inp, dev, lens=None, attention_mask=None, dtype=None):
+    q, k, v, do = (inp[x].to(dev) for x in ("q", "k", "v", "do"))
+    if dtype is not None:
+        q, k, v, do = (x.to(dtype) for x in (q, k, v, do))
+    q, k, v = (x.detach().requires_grad_(True) for x in (q, k, v))
+    meta = {n: (inp[n].to(dev) if inp.get(n) is not None else None) for n in ("in_span", "span_id", "is_prefix")}
+    o, lse = flash_attention(q, k, v, lens=None if lens is None else lens.to(dev), causal=inp.get("causal", True),
+                             return_lse=True, attention_mask=attention_mask, **meta)
+    o.backward(do)
+    torch.cuda.synchronize()
+    return {"o": o.detach(), "lse": lse.detach(), "dq": q.grad, "dk": k.grad, "dv": v.grad}
+
+
+def compare(got, ref, heads=None, lse_finite_only=True):
+    res = {}
+    for key in ("o", "dq", "dk", "dv"):
+        g = got[key] if heads is None else select_heads(got[key], heads)
+        res[key] = assert_close(key, g, ref[key])
+    g = got["lse"] if heads is None else torch.cat([got["lse"][b:b + 1, h:h + 1] for b, h in heads], 0)
+    g, r = g.double().cpu(), ref["lse"].double().cpu()
+    assert torch.equal(torch.isinf(g), torch.isinf(r)), "LSE -inf pattern differs"
+    fin = torch.isfinite(r)
+    res["lse"] = assert_close("lse", g[fin], r[fin])
+    return res
+
+
+def _case(inp, dev, heads=None, **kw):
+    print(f"attention case {inp.get('name', '?')} heads={heads}", flush=True)
+    got = run_gpu(inp, dev, **kw)
+    T = inp["q"].shape[2]
+    mask = oracle_mask(inp, T, lens=kw.get("lens"), attention_mask_given=kw.get("attention_mask") is not None)
+    q, k, v, do = (inp[x] for x in ("q", "k", "v", "do"))
+    dt = kw.get("dtype")
+    if dt is not None:  # the oracle sees exactly the rounded inputs the GPU sees
+        q, k, v, do = (x.to(dt) for x in (q, k, v, do))
+    ref = oracle_fwd_bwd(q, k, v, do, mask, q.shape[-1] ** -0.5, heads=heads)
+    return compare(got, ref, heads)
+
+
+def test_config1_causal_fp32_inputs(dev):
+    _case(config_inputs(1, seed=0), dev)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_small_no_metadata(dev, D, causal):
+    q, k, v, do = qkvdo(2, 3, 200, D, seed=1)
+    _case(dict(name=f"small D{D} causal={causal}", q=q, k=k, v=v, do=do, causal=causal), dev)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_cocktail_small(dev, D):
+    tokens, in_span, span_id, is_prefix = cocktail_batch(3, 1024, CONFIG3_LAYOUT, seed=4)
+    q, k, v, do = qkvdo(3, 2, 1024, D, seed=5)
+    _case(dict(name=f"cocktail D{D}", q=q, k=k, v=v, do=do, in_span=in_span, span_id=span_id,
+               is_prefix=is_prefix), dev)
+
+
+def test_fp16(dev):
+    tokens, in_span, span_id, is_prefix = cocktail_batch(2, 512, CONFIG3_LAYOUT, seed=6)
+    q, k, v, do = qkvdo(2, 2, 512, 64, seed=7, dtype=torch.float16)
+    _case(dict(name="fp16", q=q, k=k, v=v, do=do, in_span=in_span, span_id=span_id, is_prefix=is_prefix), dev)
+
+
+def test_lens_and_fully_masked_rows(dev):
+    q, k, v, do = qkvdo(3, 2, 300, 64, seed=8)
+    lens = torch.tensor([300, 129, 0], dtype=torch.int32)
+    res = _case(dict(name="lens", q=q, k=k, v=v, do=do, causal=True), dev, lens=lens)
+    got = run_gpu(dict(q=q, k=k, v=v, do=do, causal=True), dev, lens=lens)
+    assert (got["o"][1, :, 129:] == 0).all() and (got["o"][2] == 0).all()
+    assert torch.isinf(got["lse"][2]).all() and (got["lse"][2] < 0).all()
+    assert (got["dq"][2] == 0).all() and (got["dk"][2] == 0).all() and (got["dv"][2] == 0).all()
+
+
+def test_attention_mask_without_metadata_is_causal(dev):
+    q, k, v, do = qkvdo(1, 2, 192, 64, seed=9)
+    am = torch.ones(1, 192, 192, dtype=torch.bool, device=dev)
+    _case(dict(name="attn_mask", q=q, k=k, v=v, do=do, causal=False), dev, attention_mask=am)
+
+
+def test_model_layout_strided_inputs(dev):
+    """q/k/v as [B, L, H, d] memory viewed [B, H, L, d] (model.py:76-78)."""
+    B, L, H, D = 2, 256, 4, 64
+    g = torch.Generator("cpu").manual_seed(10)
+    base = [torch.randn(B, L, H, D, generator=g).to(torch.bfloat16) for _ in range(4)]
+    tokens, in_span, span_id, is_prefix = cocktail_batch(B, 1024, CONFIG3_LAYOUT, seed=11)
+    in_span, span_id, is_prefix = in_span[:, :L], span_id[:, :L], is_prefix[:, :L]
+    views = [x.to(dev).transpose(1, 2) for x in base]
+    q, k, v = (x.detach().requires_grad_(True) for x in views[:3])
+    o = flash_attention(q, k, v, in_span=in_span.to(dev), span_id=span_id.to(dev), is_prefix=is_prefix.to(dev))
+    o.backward(views[3])
+    cpu = [x.transpose(1, 2) for x in base]
+    mask = oracle_mask(dict(q=cpu[0], in_span=in_span, span_id=span_id, is_prefix=is_prefix), L)
+    ref = oracle_fwd_bwd(*cpu, mask, D ** -0.5)
+    assert_close("o", o, ref["o"])
+    assert_close("dq", q.grad, ref["dq"])
+    assert_close("dk", k.grad, ref["dk"])
+    assert_close("dv", v.grad, ref["dv"])
+
+
+def test_config2_causal(dev):
+    inp = config_inputs(2, seed=0)
+    _case(inp, dev, heads=[(0, 0), (3, 7), (7, 15)])
+
+
+def test_config3_cocktail(dev):
+    inp = config_inputs(3, seed=0)
+    _case(inp, dev, heads=[(0, 0), (5, 3), (15, 11)])
+
+
+def test_config4_cocktail_bf16(dev):
+    inp = config_inputs(4, seed=0)
+    _case(inp, dev, heads=[(0, 0), (1, 31)])
+
+
+def test_deterministic(dev):
+    inp = config_inputs(3, seed=1)
+    a = run_gpu(inp, dev)
+    b = run_gpu(inp, dev)
+    for key in a:
+        assert torch.equal(a[key], b[key]), key

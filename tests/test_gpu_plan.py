@@ -1,0 +1,122 @@
+"""GPU: the tile classifier, work lists and dense mask are bit-exact.
+
+Compares the device plan (``kd_plan_build``) and ``return_attention_mask``
+output against the oracle's dense mask (``original_kernel.py:478-517``) and
+its exhaustive tile reduction, on the benchmark configurations and on
+ragged / fuzzed metadata.
+"""
+import numpy as np
+import pytest
+import torch
+
+from kerneldev_amd import build_plan, flash_attention, plan_views
+from kerneldev_amd.attention import mask_mode
+from kerneldev_amd.synth import CONFIG3_LAYOUT, CONFIG4_LAYOUT, cocktail_batch
+from oracle import tilemap
+from oracle.mask import dense_mask
+
+pytestmark = pytest.mark.gpu
+
+
+def _device_plan(dev, B, T, D, in_span=None, span_id=None, is_prefix=None, lens=None, causal=True,
+                 attention_mask_given=False):
+    to = lambda t: None if t is None else t.to(dev)
+    mode = mask_mode(in_span, span_id, is_prefix, True if attention_mask_given else None, causal)
+    plan = build_plan(B, T, D, dev, mode, to(in_span), to(span_id), to(is_prefix), to(lens))
+    torch.cuda.synchronize()
+    return {k: (v.cpu().numpy() if torch.is_tensor(v) else v) for k, v in plan_views(plan, B, T, D).items()}
+
+
+def _check_plan(p, mask):
+    B, T, _ = mask.shape
+    L = p["layout"]
+    cls = tilemap.classify(mask, 64)
+    np.testing.assert_array_equal(p["cls"], cls)
+    n = L["nT"]
+    pad = np.zeros((B, n * 64, n * 64), bool)
+    pad[:, :T, :T] = mask
+    cnt = pad.reshape(B, n, 64, n, 64).sum(axis=(2, 4))
+    np.testing.assert_array_equal(p["nnz"], cnt)
+    for name, group, fn in (("fwd", L["fwd_group"], tilemap.q_lists), ("dq", L["dq_group"], tilemap.q_lists),
+                            ("dkdv", L["dkdv_group"], tilemap.k_lists)):
+        ent, counts = fn(cls, group)
+        np.testing.assert_array_equal(p[f"{name}_count"], counts, err_msg=name)
+        np.testing.assert_array_equal(p[f"{name}_list"].view(np.uint32), ent, err_msg=name)
+
+
+@pytest.mark.parametrize("T,causal", [(256, True), (2048, True), (200, False), (1, True), (77, True)])
+def test_plan_no_metadata(dev, T, causal):
+    B = 2
+    print(f"plan no-metadata T={T} causal={causal}", flush=True)
+    p = _device_plan(dev, B, T, 64, causal=causal)
+    _check_plan(p, dense_mask(T, B=B, causal=causal))
+
+
+def test_plan_attention_mask_defaults_to_tril(dev):
+    T = 300
+    p = _device_plan(dev, 1, T, 128, causal=False, attention_mask_given=True)
+    _check_plan(p, dense_mask(T, B=1, causal=False, attention_mask_given=True))
+
+
+def test_plan_config3(dev):
+    tokens, in_span, span_id, is_prefix = cocktail_batch(16, 1024, CONFIG3_LAYOUT, seed=0)
+    print("plan config3", flush=True)
+    p = _device_plan(dev, 16, 1024, 64, in_span, span_id, is_prefix)
+    m = dense_mask(1024, in_span=in_span.numpy(), span_id=span_id.numpy(), is_prefix=is_prefix.numpy())
+    _check_plan(p, m)
+
+
+def test_plan_config4(dev):
+    tokens, in_span, span_id, is_prefix = cocktail_batch(2, 8192, CONFIG4_LAYOUT, seed=0)
+    print("plan config4", flush=True)
+    p = _device_plan(dev, 2, 8192, 128, in_span, span_id, is_prefix)
+    m = dense_mask(8192, in_span=in_span.numpy(), span_id=span_id.numpy(), is_prefix=is_prefix.numpy())
+    _check_plan(p, m)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_plan_fuzzed_metadata(dev, seed):
+    rng = np.random.default_rng(seed)
+    B = 3
+    T = int(rng.integers(1, 400))
+    in_span = torch.from_numpy(rng.random((B, T)) < 0.4)
+    is_prefix = torch.from_numpy(rng.random((B, T)) < 0.2)
+    # large, repeated and negative span ids; non-contiguous spans sharing an id
+    pool = np.array([-1, 0, 1, 2, 7, 2 ** 40 + 3, 2 ** 40 + 3 + 2 ** 32, -5], np.int64)
+    span_id = torch.from_numpy(pool[rng.integers(0, len(pool), (B, T))])
+    lens = torch.from_numpy(rng.integers(0, T + 3, (B,)).astype(np.int32))
+    which = seed % 3
+    if which == 1:
+        span_id = span_id.to(torch.int32).clamp(-5, 7)  # int32 path
+    kw = dict(in_span=in_span, span_id=span_id, is_prefix=is_prefix)
+    if which == 2:
+        kw["is_prefix"] = None
+    print(f"plan fuzz seed={seed} T={T}", flush=True)
+    p = _device_plan(dev, B, T, 64, lens=lens, **kw)
+    m = dense_mask(T, B=B, lens=lens.numpy(), **{k: (None if v is None else v.numpy()) for k, v in kw.items()})
+    _check_plan(p, m)
+
+
+def test_plan_strided_metadata(dev):
+    rng = np.random.default_rng(11)
+    T = 333
+    base_span = torch.from_numpy(rng.random((2, 2 * T)) < 0.5)
+    base_sid = torch.from_numpy(rng.integers(-1, 4, (2, 2 * T)))
+    base_pre = torch.from_numpy(rng.random((2, 2 * T)) < 0.3)
+    kw = dict(in_span=base_span[:, ::2], span_id=base_sid[:, ::2], is_prefix=base_pre[:, ::2])
+    p = _device_plan(dev, 2, T, 64, **kw)
+    m = dense_mask(T, B=2, **{k: v.numpy() for k, v in kw.items()})
+    _check_plan(p, m)
+
+
+@pytest.mark.parametrize("T", [64, 130])
+def test_return_attention_mask_bit_exact(dev, T):
+    tokens, in_span, span_id, is_prefix = cocktail_batch(2, 512, CONFIG3_LAYOUT, seed=7)
+    in_span, span_id, is_prefix = in_span[:, :T], span_id[:, :T], is_prefix[:, :T]
+    q = torch.randn(2, 3, T, 64, device=dev, dtype=torch.bfloat16)
+    _, mask = flash_attention(q, q, q, in_span=in_span.to(dev), span_id=span_id.to(dev),
+                              is_prefix=is_prefix.to(dev), return_attention_mask=True)
+    ref = dense_mask(T, in_span=in_span.numpy(), span_id=span_id.numpy(), is_prefix=is_prefix.numpy())
+    got = mask.cpu().numpy()
+    for h in range(3):
+        np.testing.assert_array_equal(got[:, h], ref)
