@@ -1,0 +1,272 @@
+#!/usr/bin/env python3
+"""Hierarchical-mask flash attention fwd+bwd on one MI355X: useful TFLOP/s.
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 4]``
+
+A *step* is one pass of the attention hot path over one synthetic batch with
+every input already resident in HBM: tile classifier (plan), forward, Delta,
+dQ and dK/dV -- the same five launches ``flash_attention()`` followed by
+``backward()`` issues, called through the C ABI on preallocated buffers.
+The timed region is bracketed by ``torch.cuda.synchronize()``; HIP events on
+the launch stream sit between the five kernels of every timed step, so each
+kernel's average duration is measured live.
+
+Useful FLOPs count allowed (unmasked) score entries only: 4*d per entry for
+the forward and 10*d for the backward (``nnz`` is popcounted from the device
+tile map, whose bit-exactness the GPU tests check).  The roofline object
+reports the dominant kernel against MI355X's dense bf16 MFMA peak, and the
+CPU baseline is the eager dense-masked SDPA of the oracle, timed on a bounded
+sample of the same workload on this host's cores.
+
+Prints ONE JSON line (rank 0).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "hier-masked flash-attn fwd+bwd useful TFLOP/s & % bf16 MFMA peak, 1 GPU"
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 2.4 GHz)
+PEAK_HBM_GBS = 8000.0
+
+# algorithmic FLOPs per allowed score entry and head-dim unit, per kernel
+KERNEL_FLOPS_PER_ENTRY = {
+    "fwd": 4,   # S = Q K^T, O += P V
+    "dq": 6,    # S recompute, dP = dO V^T, dQ += dS K
+    "dkdv": 8,  # S recompute, dP recompute, dV += P^T dO, dK += dS^T Q
+}
+USEFUL_FWD, USEFUL_BWD = 4, 10
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=4, choices=(2, 3, 4),
+                    help="BASELINE config to time (default 4, the metric's workload)")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true",
+                    help="skip the CPU baseline leg (profiling runs)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target CPU time of the baseline sample")
+    return ap.parse_args()
+
+
+def cpu_threads() -> int:
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit():
+        n = min(n, int(env))
+    return max(1, n)
+
+
+class Step:
+    """Preallocated buffers and the five launches of one fwd+bwd pass."""
+
+    def __init__(self, inp, dev):
+        import torch
+
+        from kerneldev_amd import _lib
+        from kerneldev_amd.attention import _attn_args, _dtype_code, _strides3, mask_mode
+
+        self.torch, self.lib, self.dev = torch, _lib.load(), dev
+        self._check = _lib.check
+        q, k, v, do = (inp[x].to(dev) for x in ("q", "k", "v", "do"))
+        B, H, T, D = q.shape
+        self.shape = (B, H, T, D)
+        self.meta = {n: (inp[n].to(dev) if inp.get(n) is not None else None)
+                     for n in ("in_span", "span_id", "is_prefix")}
+        self.mode = mask_mode(**self.meta, causal=inp.get("causal", True))
+        self.plan = torch.empty(_lib.plan_bytes(B, T, D), dtype=torch.uint8, device=dev)
+        self.o = torch.empty_like(q)
+        self.lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+        self.delta = torch.empty_like(self.lse)
+        self.dq, self.dk, self.dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        self.inputs = (q, k, v, do)
+        a = _attn_args(q, k, v, D ** -0.5)
+        a.dtype = _dtype_code(q.dtype)
+        a.o, a.o_strides = self.o.data_ptr(), _strides3(self.o)
+        a.lse = self.lse.data_ptr()
+        a.dout, a.do_strides = do.data_ptr(), _strides3(do)
+        a.dq, a.dk, a.dv = self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr()
+        a.dq_strides, a.dk_strides, a.dv_strides = _strides3(self.dq), _strides3(self.dk), _strides3(self.dv)
+        a.delta = self.delta.data_ptr()
+        self.args = a
+        m = _lib.MetaArgs()
+        m.B, m.T, m.D, m.mode = B, T, D, self.mode
+        if self.meta["in_span"] is not None:
+            t = self.meta["in_span"]
+            m.in_span = t.data_ptr()
+            m.in_span_strides[0], m.in_span_strides[1] = t.stride()
+        if self.meta["is_prefix"] is not None:
+            t = self.meta["is_prefix"]
+            m.is_prefix = t.data_ptr()
+            m.is_prefix_strides[0], m.is_prefix_strides[1] = t.stride()
+        if self.meta["span_id"] is not None:
+            t = self.meta["span_id"]
+            m.span_id = t.data_ptr()
+            m.span_id_strides[0], m.span_id_strides[1] = t.stride()
+            m.span_id_dtype = _lib.KD_I64 if t.dtype == torch.int64 else _lib.KD_I32
+        self.margs = m
+        self.stream = torch.cuda.current_stream(dev)
+        self.sptr = ctypes.c_void_p(self.stream.cuda_stream)
+        self.pptr = ctypes.c_void_p(self.plan.data_ptr())
+
+    def launches(self):
+        L, a, ck = self.lib, ctypes.byref(self.args), self._check
+        return (
+            ("plan", lambda: ck(L.kd_plan_build(ctypes.byref(self.margs), self.pptr, self.sptr), "plan")),
+            ("fwd", lambda: ck(L.kd_attn_fwd(a, self.pptr, self.sptr), "fwd")),
+            ("delta", lambda: ck(L.kd_attn_bwd_delta(a, self.sptr), "delta")),
+            ("dq", lambda: ck(L.kd_attn_bwd_dq(a, self.pptr, self.sptr), "dq")),
+            ("dkdv", lambda: ck(L.kd_attn_bwd_dkdv(a, self.pptr, self.sptr), "dkdv")),
+        )
+
+    def run(self, events=None):
+        for idx, (_, fn) in enumerate(self.launches()):
+            if events is not None:
+                events[idx].record(self.stream)
+            fn()
+        if events is not None:
+            events[-1].record(self.stream)
+
+    def nnz_total(self) -> int:
+        """Allowed entries summed over b (per head), from the device tile map."""
+        from kerneldev_amd import plan_views
+
+        B, H, T, D = self.shape
+        return int(plan_views(self.plan, B, T, D)["nnz"].to(self.torch.int64).sum().item())
+
+
+def cpu_baseline(inp, budget_s: float):
+    """Eager fp32 dense-masked SDPA fwd+bwd (the oracle) on a head sample."""
+    import torch
+
+    from oracle.attention import sdpa_baseline
+    from oracle.mask import dense_mask
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    q, k, v, do = inp["q"], inp["k"], inp["v"], inp["do"]
+    B, H, T, D = q.shape
+    def np_or_none(t):
+        return None if t is None else t.numpy()
+    mask = torch.from_numpy(dense_mask(T, B=B, in_span=np_or_none(inp.get("in_span")),
+                                       span_id=np_or_none(inp.get("span_id")),
+                                       is_prefix=np_or_none(inp.get("is_prefix")),
+                                       causal=inp.get("causal", True)))
+    heads = [(b, h) for h in range(H) for b in range(B)]
+    done, flops, elapsed = [], 0.0, 0.0
+    for b, h in heads:
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        t0 = time.perf_counter()
+        sdpa_baseline(q[sl], k[sl], v[sl], do[sl], mask[b:b + 1], D ** -0.5)
+        elapsed += time.perf_counter() - t0
+        flops += (USEFUL_FWD + USEFUL_BWD) * D * float(mask[b].sum().item())
+        done.append((b, h))
+        if elapsed >= budget_s:
+            break
+    return {
+        "value": flops / elapsed / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{len(done)} of {B * H} (b, h) heads of the same inputs, fp32 eager "
+                   f"torch SDPA with the dense hierarchical bool mask, fwd+bwd via autograd, "
+                   f"{elapsed:.1f} s"),
+        "ms_per_head": 1e3 * elapsed / len(done),
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the attention path has no "
+                                   "cross-GPU component here (see the sharding note in DESIGN.md); "
+                                   "run with --gpus 1"}))
+        sys.exit(2)
+
+    import torch
+
+    from kerneldev_amd.synth import config_inputs
+
+    dev = torch.device("cuda:0")
+    inp = config_inputs(args.config, seed=args.seed)
+    B, H, T, D = inp["q"].shape
+    st = Step(inp, dev)
+    for _ in range(max(0, args.warmup)):
+        st.run()
+    torch.cuda.synchronize()
+    nnz = st.nnz_total()
+
+    names = [n for n, _ in st.launches()]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        st.run(evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = 1e3 * wall / args.steps
+    per_kernel = {n: statistics.mean(evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(args.steps))
+                  for j, n in enumerate(names)}
+    event_ms = statistics.mean(evs[i][0].elapsed_time(evs[i][-1]) for i in range(args.steps))
+
+    useful = (USEFUL_FWD + USEFUL_BWD) * D * H * nnz
+    value = useful / (ms_step * 1e-3) / 1e12
+
+    dom = max(("fwd", "dq", "dkdv"), key=lambda n: per_kernel[n])
+    dom_flops = KERNEL_FLOPS_PER_ENTRY[dom] * D * H * nnz
+    achieved = dom_flops / (per_kernel[dom] * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "traffic": None, "avg_launch_ms": round(per_kernel[dom], 4)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(inp, args.cpu_seconds)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if inp["q"].dtype == torch.bfloat16 else str(inp["q"].dtype).replace("torch.", ""),
+        "data": "synthetic (seeded cocktail-party token layout and N(0,1) Q/K/V/dO)",
+        "config": {
+            "workload": inp["name"] + " fwd+bwd",
+            "baseline_config": args.config,
+            "B": B, "H": H, "L": T, "d": D,
+            "mask_density": round(nnz / (B * T * T), 4),
+            "useful_tflop_per_step": round(useful / 1e12, 4),
+            "frac_of_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
+            "kernel_ms": {n: round(x, 4) for n, x in per_kernel.items()},
+            "event_ms_per_step": round(event_ms, 4),
+            "hadamard": False,
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

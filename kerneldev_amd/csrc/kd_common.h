@@ -72,6 +72,16 @@ template <> KD_DEV uint32_t pack2<F16>(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
 }
 
+// Sum of the two 16-bit values packed in one dword, in fp32 (exact).
+template <class E> KD_DEV float sum2(uint32_t w);
+template <> KD_DEV float sum2<BF16>(uint32_t w) {
+  return __uint_as_float(w << 16) + __uint_as_float(w & 0xFFFF0000u);
+}
+template <> KD_DEV float sum2<F16>(uint32_t w) {
+  const f16x2 h = __builtin_bit_cast(f16x2, w);
+  return float(h[0]) + float(h[1]);
+}
+
 template <class E> KD_DEV float to_f32(uint16_t bits);
 template <> KD_DEV float to_f32<BF16>(uint16_t bits) { return __uint_as_float(uint32_t(bits) << 16); }
 template <> KD_DEV float to_f32<F16>(uint16_t bits) {

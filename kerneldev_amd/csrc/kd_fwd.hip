@@ -175,14 +175,16 @@ __global__ __launch_bounds__(256) void k_fwd(AttnArgs a, const uint32_t* __restr
     for (int kb = 0; kb < 2; ++kb) {
       float p[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        p[r] = fast_exp2(__builtin_fmaf(s[kb][r], sl2, -ms));
-        lsum += p[r];
-      }
+      for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(s[kb][r], sl2, -ms));
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t) {
         pk[kb][t] = u32x4{pack2<E>(p[8 * t + 0], p[8 * t + 1]), pack2<E>(p[8 * t + 2], p[8 * t + 3]),
                           pack2<E>(p[8 * t + 4], p[8 * t + 5]), pack2<E>(p[8 * t + 6], p[8 * t + 7])};
+        // the row sum uses the ROUNDED P that enters P V, so O = sum(P V) / sum(P)
+        // is a convex combination of V rows even when one key dominates
+#pragma unroll
+        for (int w = 0; w < 4; ++w) lsum += sum2<E>(pk[kb][t][w]);
+      }
     }
     l_i = l_i * alpha + lsum;
 #pragma unroll

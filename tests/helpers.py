@@ -12,7 +12,7 @@ MAX_ABS = 2e-2
 REL_RMS = 1e-2
 
 
-MANTISSA_BITS = {torch.bfloat16: 7, torch.float16: 10, torch.float32: 23}
+MANTISSA_BITS = {torch.bfloat16: 7, torch.float16: 10, torch.float32: 23, torch.float64: 52}
 
 
 def ulp(ref: torch.Tensor, dtype) -> torch.Tensor:
@@ -36,7 +36,7 @@ def errors(x: torch.Tensor, ref: torch.Tensor, out_dtype=None):
     return max_abs, rel, excess
 
 
-def assert_close(name, x, ref, max_abs=MAX_ABS, rel_rms=REL_RMS):
+def assert_close(name, x, ref, max_abs=MAX_ABS, rel_rms=REL_RMS, out_dtype=None):
     """north_star bar: max-abs <= 2e-2 and rel-RMS <= 1e-2.
 
     The max-abs part is measured beyond one ulp of the output dtype at each
@@ -46,7 +46,7 @@ def assert_close(name, x, ref, max_abs=MAX_ABS, rel_rms=REL_RMS):
     plain 2e-2 there.  Below magnitude 2 the ulp term is <= 2^-7 and the bar
     is the plain one.
     """
-    ma, rr, ex = errors(x, ref)
+    ma, rr, ex = errors(x, ref, out_dtype)
     assert np.isfinite(ma), f"{name}: non-finite values"
     assert ex <= max_abs and rr <= rel_rms, (
         f"{name}: max_abs={ma:.3e} (beyond 1 ulp: {ex:.3e}) rel_rms={rr:.3e} max|ref|={ref.abs().max().item():.3e}")

@@ -29,15 +29,23 @@ def run_gpu(inp, dev, lens=None, attention_mask=None, dtype=None):
 
 
 def compare(got, ref, heads=None, lse_finite_only=True):
-    res = {}
+    """Check O, dQ, dK, dV and LSE; report every failure, not just the first."""
+    res, failures = {}, []
     for key in ("o", "dq", "dk", "dv"):
         g = got[key] if heads is None else select_heads(got[key], heads)
-        res[key] = assert_close(key, g, ref[key])
+        try:
+            res[key] = assert_close(key, g, ref[key])
+        except AssertionError as exc:
+            failures.append(str(exc))
     g = got["lse"] if heads is None else torch.cat([got["lse"][b:b + 1, h:h + 1] for b, h in heads], 0)
     g, r = g.double().cpu(), ref["lse"].double().cpu()
     assert torch.equal(torch.isinf(g), torch.isinf(r)), "LSE -inf pattern differs"
     fin = torch.isfinite(r)
-    res["lse"] = assert_close("lse", g[fin], r[fin])
+    try:
+        res["lse"] = assert_close("lse", g[fin], r[fin], out_dtype=torch.float32)
+    except AssertionError as exc:
+        failures.append(str(exc))
+    assert not failures, "; ".join(failures)
     return res
 
 
