@@ -60,6 +60,9 @@ def parse():
                     help="skip the CPU baseline leg (profiling runs)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the baseline sample")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="run one device-to-device copy of this many MiB before timing, as the "
+                         "known-size reference for HBM traffic counters")
     return ap.parse_args()
 
 
@@ -206,6 +209,14 @@ def main():
     inp = config_inputs(args.config, seed=args.seed)
     B, H, T, D = inp["q"].shape
     st = Step(inp, dev)
+    if args.calibrate_copy_mib > 0:
+        n = args.calibrate_copy_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     for _ in range(max(0, args.warmup)):
         st.run()
     torch.cuda.synchronize()

@@ -5,41 +5,40 @@
 // with c = sm_scale * log2(e) kept in fp32 (the reference rounds it to the
 // input dtype at :415; deliberately not reproduced).
 //
-// Layout per workgroup: 4 waves x 32 query rows = 128 rows (one q-block of
-// the plan's forward list), 64 keys per step.  Each wave computes
+// One workgroup = 4 waves x 32 query rows = one 128-row q-block of the plan's
+// forward list; 64 keys per step.  Each wave computes
 //   S^T[64 keys x 32 q]  = K Q^T      (A = K rows from LDS, B = Q in registers)
-//   O^T[D x 32 q]       += V^T P^T    (A = V^T from LDS,   B = P in registers)
-// so a lane owns one query column: the softmax row statistics are per-lane
-// scalars (one cross-half max per step), and P never leaves registers thanks
-// to the sigma() row permutation of the K operand.  K and V^T tiles are
-// double buffered in LDS; the next tile's global loads are in flight while
-// the current one is computed.  Only non-empty key tiles are visited (plan
-// list); FULL tiles skip the mask, PARTIAL tiles evaluate it per element.
-#include "kd_internal.h"
+//   O^T[D x 32 q]       += V^T P^T    (A = V^T read transposed from LDS,
+//                                      B = P straight from the S^T registers)
+// so a lane owns one query column: the softmax statistics are per-lane
+// scalars plus one permlane32 exchange, and P never leaves registers thanks to
+// the sigma() row permutation of the K operand.  K and V tiles are copied
+// global -> LDS by buffer_load ... lds (double buffered: the next tile's copy
+// runs under the current tile's math) and V is transposed by
+// ds_read_b64_tr_b16 on the way into the MFMA.  Only non-empty key tiles are
+// visited (plan list); FULL tiles skip the mask, PARTIAL tiles evaluate it.
+//
+// The running max is rescaled lazily: the accumulators are only rescaled
+// when a row's max grows by more than 2^8 (P is then <= 256, harmless in
+// fp32/bf16), which removes the per-step O *= alpha of the textbook loop.
+// The row sum l adds up the ROUNDED P that enters P V, so O is an exact
+// convex combination of V rows up to the final rounding even when one key
+// dominates the row.
+#include "kd_tile.h"
 
 namespace kd {
 
-template <int D>
-struct FwdCfg {
-  static constexpr int BN = 64;              // keys per step
-  static constexpr int KST = D + 8;          // K row stride (elements) in LDS
-  static constexpr int VST = BN + 8;         // V^T row stride (elements) in LDS
-  static constexpr int DS = D / 16;          // 16-wide k-steps over d
-  static constexpr int DB = D / 32;          // 32-row blocks of O^T
-  static constexpr int KCH = BN * D / 8 / 256;  // 16-byte K chunks per thread
-  static constexpr int VBLK = (BN / 4) * (D / 8);  // 4-key x 8-d V blocks
-  static constexpr int K_ELEMS = BN * KST;
-  static constexpr int V_ELEMS = D * VST;
-};
-
 template <class E, int D>
-__global__ __launch_bounds__(256) void k_fwd(AttnArgs a, const uint32_t* __restrict__ codes,
-                                             const uint32_t* __restrict__ list,
-                                             const int32_t* __restrict__ count, int nT, int nQB) {
-  using C = FwdCfg<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t s_k[2][C::K_ELEMS];
-  __shared__ __attribute__((aligned(16))) uint16_t s_vt[2][C::V_ELEMS];
-  __shared__ __attribute__((aligned(16))) uint32_t s_code[2][C::BN];
+__global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __restrict__ codes,
+                                                const uint32_t* __restrict__ list,
+                                                const int32_t* __restrict__ count, int nT, int nQB) {
+  using TL = Tile<D>;
+  constexpr int DS = D / 16;  // 16-wide k-steps of S^T over d
+  constexpr int DB = D / 32;  // 32-row blocks of O^T
+  constexpr int NL = TL::LOADS_PER_WAVE;
+  __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][TL::BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][TL::BYTES];
+  __shared__ __attribute__((aligned(256))) uint32_t s_code[2][64];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
   const int T = a.T, H = a.H;
@@ -51,98 +50,87 @@ __global__ __launch_bounds__(256) void k_fwd(AttnArgs a, const uint32_t* __restr
   const uint16_t* qg = static_cast<const uint16_t*>(a.q) + b * a.q_strides[0] + h * a.q_strides[1];
   const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_strides[0] + h * a.k_strides[1];
   const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_strides[0] + h * a.v_strides[1];
-  const int64_t kst = a.k_strides[2], vst = a.v_strides[2];
-  const uint32_t* codes_b = codes + int64_t(b) * T;
+  const uint32_t qrb = uint32_t(a.q_strides[2]) * 2u, krb = uint32_t(a.k_strides[2]) * 2u,
+                 vrb = uint32_t(a.v_strides[2]) * 2u;
+  const auto rs_q = make_rsrc(qg, uint32_t(T) * qrb);
+  const auto rs_k = make_rsrc(kg, uint32_t(T) * krb);
+  const auto rs_v = make_rsrc(vg, uint32_t(T) * vrb);
+  const auto rs_c = make_rsrc(codes + int64_t(b) * T, uint32_t(T) * 4u);
 
-  // ---- per-lane query row ----
+  // ---- per-lane query row (B operand of S^T, kept in registers) ----
   const int qrow = qblock * 128 + wave * 32 + c;
   const bool qvalid = qrow < T;
-  u32x4 qf[C::DS];
+  u32x4 qf[DS];
 #pragma unroll
-  for (int st = 0; st < C::DS; ++st) {
-    qf[st] = qvalid ? *reinterpret_cast<const u32x4*>(qg + qrow * a.q_strides[2] + 16 * st + 8 * hf)
-                    : u32x4{0, 0, 0, 0};
-  }
-  const uint32_t qcode = qvalid ? codes_b[qrow] : 0u;
+  for (int st = 0; st < DS; ++st) qf[st] = buf_load16(rs_q, uint32_t(qrow) * qrb + (16 * st + 8 * hf) * 2);
+  const uint32_t qcode = qvalid ? codes[int64_t(b) * T + qrow] : 0u;
 
   const int lbase = b * nQB + qblock;
   const int n = count[lbase];
   const uint32_t* ent = list + int64_t(lbase) * nT;
 
-  // ---- tile loader: global -> registers -> LDS ----
-  u32x4 rk[C::KCH];
-  u32x4 rv[4];
-  uint32_t rcode = 0;
-  auto load_tile = [&](int kt) {
-    const int k0 = kt * C::BN;
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int ch = tid + 256 * i, row = ch / (D / 8), col = ch % (D / 8);
-      const int key = k0 + row;
-      rk[i] = key < T ? *reinterpret_cast<const u32x4*>(kg + key * kst + col * 8) : u32x4{0, 0, 0, 0};
-    }
-    if (tid < C::VBLK) {
-      const int kgp = tid / (D / 8), dc = tid % (D / 8);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = k0 + 4 * kgp + r;
-        rv[r] = key < T ? *reinterpret_cast<const u32x4*>(vg + key * vst + dc * 8) : u32x4{0, 0, 0, 0};
-      }
-    }
-    if (tid < C::BN) rcode = (k0 + tid < T) ? codes_b[k0 + tid] : 0u;
+  uint32_t koff[NL], voff[NL];
+  TL::load_offsets(wave, lane, krb, koff);
+  TL::load_offsets(wave, lane, vrb, voff);
+  auto load_tile = [&](int kt, int buf) {
+    const uint32_t k0 = uint32_t(kt) * 64u;
+    TL::load(rs_k, k0 * krb, koff, s_k[buf], wave);
+    TL::load(rs_v, k0 * vrb, voff, s_v[buf], wave);
+    if (wave == 0)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_t*)&s_code[buf][0], 4, (k0 + lane) * 4u, 0, 0, 0);
   };
-  auto store_tile = [&](int buf) {
+
+  // ---- LDS read addresses (bytes within a tile) ----
+  // K operand: row 32 kb + sigma(c), chunk 2 st + hf
+  const int srow = sigma(c);
+  int kaddr[DS];
 #pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int ch = tid + 256 * i, row = ch / (D / 8), col = ch % (D / 8);
-      *reinterpret_cast<u32x4*>(&s_k[buf][row * C::KST + col * 8]) = rk[i];
-    }
-    if (tid < C::VBLK) {
-      const int kgp = tid / (D / 8), dc = tid % (D / 8);
+  for (int st = 0; st < DS; ++st) kaddr[st] = TL::at(srow, 2 * st + hf);
+  // V^T operand via transposed reads: group g = lane / 16 covers d columns
+  // 32 db + 16 (g & 1) .. +15 and key rows 16 t4 + 8 (g >> 1) + 4 half .. +3
+  int vaddr[DB][2];
+  {
+    const int i = lane & 15, g = lane >> 4;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        u32x2 lo = {pack_lo(rv[0][w], rv[1][w]), pack_lo(rv[2][w], rv[3][w])};
-        u32x2 hi = {pack_hi(rv[0][w], rv[1][w]), pack_hi(rv[2][w], rv[3][w])};
-        *reinterpret_cast<u32x2*>(&s_vt[buf][(8 * dc + 2 * w) * C::VST + 4 * kgp]) = lo;
-        *reinterpret_cast<u32x2*>(&s_vt[buf][(8 * dc + 2 * w + 1) * C::VST + 4 * kgp]) = hi;
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int r = 8 * (g >> 1) + 4 * half + (i >> 2);
+        const int chunk = 4 * db + 2 * (g & 1) + ((i & 3) >> 1);
+        vaddr[db][half] = TL::at(r, chunk) + 8 * (i & 1);
       }
-    }
-    if (tid < C::BN) s_code[buf][tid] = rcode;
-  };
+  }
 
   const float sl2 = a.sm_scale * 1.4426950408889634f;
   const float NEG_INF = -__builtin_inff();
-  float m_i = NEG_INF, l_i = 0.f;
-  f32x16 o[C::DB];
+  float m_ref = NEG_INF, l0 = 0.f, l1 = 0.f;
+  f32x16 o[DB];
 #pragma unroll
-  for (int db = 0; db < C::DB; ++db) o[db] = f32x16{};
+  for (int db = 0; db < DB; ++db) o[db] = f32x16{};
 
-  const int srow = sigma(c);
-  if (n > 0) {
-    load_tile(int(ent[0] >> 1));
-    store_tile(0);
-  }
-  __syncthreads();
+  if (n > 0) load_tile(int(ent[0] >> 1), 0);
 
   for (int e = 0; e < n; ++e) {
     const int buf = e & 1;
     const uint32_t cur = ent[e];
-    const bool has_next = e + 1 < n;
-    if (has_next) load_tile(int(ent[e + 1] >> 1));
+    wait_vmem();
+    __syncthreads();  // tile e landed for every wave; buffer buf^1 free again
+    if (e + 1 < n) load_tile(int(ent[e + 1] >> 1), buf ^ 1);
+    const uint8_t* kt = s_k[buf];
+    const uint8_t* vt = s_v[buf];
 
     // S^T = K Q^T for two 32-key blocks
-    f32x16 s[2];
+    f32x16 s[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      s[kb] = f32x16{};
+    for (int st = 0; st < DS; ++st) {
 #pragma unroll
-      for (int st = 0; st < C::DS; ++st) {
-        const u32x4 ak = *reinterpret_cast<const u32x4*>(&s_k[buf][(32 * kb + srow) * C::KST + 16 * st + 8 * hf]);
+      for (int kb = 0; kb < 2; ++kb) {  // two independent accumulation chains
+        const u32x4 ak = *reinterpret_cast<const u32x4*>(kt + kaddr[st] + kb * 32 * TL::ROWB);
         s[kb] = mfma32x32x16<E>(ak, qf[st], s[kb]);
       }
     }
     if (!(cur & 1u)) {  // PARTIAL tile: evaluate the mask per element
-      const int k0 = int(cur >> 1) * C::BN;
+      const int k0 = int(cur >> 1) * 64;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -158,19 +146,25 @@ __global__ __launch_bounds__(256) void k_fwd(AttnArgs a, const uint32_t* __restr
         }
       }
     }
-    // online softmax (base 2); statistics are per query = per lane column
+    // tile row max (rows = this lane's query)
     float mx = NEG_INF;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-    mx = wave_max32(mx);
-    const float m_new = fmaxf(m_i, mx);
-    const float ms = (m_new == NEG_INF) ? 0.f : m_new * sl2;
-    const float alpha = fast_exp2(m_i * sl2 - ms);
-    m_i = m_new;
+    mx = xhalf_max(mx);
+    const float m_new = fmaxf(m_ref, mx);
+    const bool grow = (m_new - m_ref) * sl2 > 8.f;  // false for -inf - -inf (NaN)
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float alpha = (m_ref == NEG_INF) ? 0.f : fast_exp2((m_ref - m_new) * sl2);
+      m_ref = m_new;
+      l0 *= alpha;
+      l1 *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o[db] *= alpha;
+    }
+    const float ms = (m_ref == NEG_INF) ? 0.f : m_ref * sl2;
     u32x4 pk[2][2];
-    float lsum = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       float p[16];
@@ -180,35 +174,32 @@ __global__ __launch_bounds__(256) void k_fwd(AttnArgs a, const uint32_t* __restr
       for (int t = 0; t < 2; ++t) {
         pk[kb][t] = u32x4{pack2<E>(p[8 * t + 0], p[8 * t + 1]), pack2<E>(p[8 * t + 2], p[8 * t + 3]),
                           pack2<E>(p[8 * t + 4], p[8 * t + 5]), pack2<E>(p[8 * t + 6], p[8 * t + 7])};
-        // the row sum uses the ROUNDED P that enters P V, so O = sum(P V) / sum(P)
-        // is a convex combination of V rows even when one key dominates
-#pragma unroll
-        for (int w = 0; w < 4; ++w) lsum += sum2<E>(pk[kb][t][w]);
+        l0 = acc_pair<E>(pk[kb][t][0], l0);
+        l1 = acc_pair<E>(pk[kb][t][1], l1);
+        l0 = acc_pair<E>(pk[kb][t][2], l0);
+        l1 = acc_pair<E>(pk[kb][t][3], l1);
       }
     }
-    l_i = l_i * alpha + lsum;
-#pragma unroll
-    for (int db = 0; db < C::DB; ++db) o[db] *= alpha;
     // O^T += V^T P^T
 #pragma unroll
-    for (int db = 0; db < C::DB; ++db) {
+    for (int t4 = 0; t4 < 4; ++t4) {
 #pragma unroll
-      for (int t4 = 0; t4 < 4; ++t4) {
-        const u32x4 av = *reinterpret_cast<const u32x4*>(&s_vt[buf][(32 * db + c) * C::VST + 16 * t4 + 8 * hf]);
+      for (int db = 0; db < DB; ++db) {
+        const u32x2 lo = ds_read_tr16(vt + vaddr[db][0] + t4 * 16 * TL::ROWB);
+        const u32x2 hi = ds_read_tr16(vt + vaddr[db][1] + t4 * 16 * TL::ROWB);
+        const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
         o[db] = mfma32x32x16<E>(av, pk[t4 >> 1][t4 & 1], o[db]);
       }
     }
-    if (has_next) store_tile(buf ^ 1);
-    __syncthreads();
   }
 
   // ---- epilogue: normalise, store O and LSE ----
-  const float l_tot = wave_sum32(l_i);
+  const float l_tot = xhalf_sum(l0 + l1);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (qvalid) {
     uint16_t* og = static_cast<uint16_t*>(a.o) + b * a.o_strides[0] + h * a.o_strides[1] + qrow * a.o_strides[2];
 #pragma unroll
-    for (int db = 0; db < C::DB; ++db) {
+    for (int db = 0; db < DB; ++db) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d0 = 32 * db + 8 * g + 4 * hf;
@@ -218,7 +209,7 @@ __global__ __launch_bounds__(256) void k_fwd(AttnArgs a, const uint32_t* __restr
       }
     }
     if (a.lse != nullptr && hf == 0)
-      a.lse[int64_t(bh) * T + qrow] = l_tot > 0.f ? m_i * sl2 + fast_log2(l_tot) : NEG_INF;
+      a.lse[int64_t(bh) * T + qrow] = l_tot > 0.f ? m_ref * sl2 + fast_log2(l_tot) : NEG_INF;
   }
 }
 

@@ -1,0 +1,103 @@
+// LDS tile primitives for the gfx950 attention kernels.
+//
+// A "tile" is 64 rows (keys or queries) x D columns of 16-bit elements,
+// stored row-major in LDS (D * 2 bytes per row) and filled straight from
+// global memory with buffer_load ... lds (no VGPR staging, no VALU).  Rows
+// at or beyond T read as zero: every global access goes through a buffer
+// resource whose size ends at row T, so there are no per-lane branches.
+//
+// Bank-conflict-free layout: the 16-byte chunk c of row r is stored at chunk
+// position c ^ swz(r).  swz is chosen so that both read patterns the kernels
+// use are conflict free:
+//   (a) ds_read_b128 of one chunk from 16 different rows (an MFMA A operand
+//       taken row-wise: 16 lanes, 16 rows r0..r0+15 in any order);
+//   (b) ds_read_b64_tr_b16 of a 4-row x 32-column block by 32 lanes (an MFMA
+//       A operand taken column-wise, i.e. the tile transposed on the fly).
+// For D = 128 (16 chunks per 256-byte row) swz(r) = 4 (r & 3) + ((r >> 2) & 3);
+// for D = 64 (8 chunks per 128-byte row, two rows per bank sweep)
+// swz(r) = 4 ((r >> 1) & 1) + ((r >> 2) & 3).
+#pragma once
+#include "kd_internal.h"
+
+namespace kd {
+
+typedef __attribute__((address_space(3))) void lds_t;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource over [base, base + bytes); word 3 as for every gfx9 part.
+KD_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
+}
+
+KD_DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+template <int D>
+struct Tile {
+  static constexpr int ROWS = 64;
+  static constexpr int ROWB = D * 2;            // bytes per row
+  static constexpr int CPR = D / 8;             // 16-byte chunks per row
+  static constexpr int BYTES = ROWS * ROWB;     // 16 KiB (D = 128) or 8 KiB (D = 64)
+  static constexpr int LOADS = BYTES / 1024;    // 1 KiB per wave-wide buffer_load_dwordx4
+  static constexpr int LOADS_PER_WAVE = LOADS / 4;
+
+  KD_DEV static int swz(int r) {
+    if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+    else return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  }
+  // byte offset of (row, 16-byte chunk) inside the tile
+  KD_DEV static int at(int r, int chunk) { return r * ROWB + ((chunk ^ swz(r)) << 4); }
+
+  // Per-lane global byte offsets (relative to the tile's first row) of the
+  // chunks this lane moves in each of its LOADS_PER_WAVE wave-wide loads.
+  KD_DEV static void load_offsets(int wave, int lane, uint32_t row_bytes, uint32_t (&off)[LOADS_PER_WAVE]) {
+#pragma unroll
+    for (int j = 0; j < LOADS_PER_WAVE; ++j) {
+      const int u = (wave * LOADS_PER_WAVE + j) * 64 + lane;  // LDS chunk index, row-major
+      const int r = u / CPR, pos = u % CPR;
+      const int chunk = pos ^ swz(r);
+      off[j] = uint32_t(r) * row_bytes + uint32_t(chunk) * 16u;
+    }
+  }
+  // Issue this wave's share of the tile load (asynchronous; vmcnt tracks it).
+  KD_DEV static void load(__amdgpu_buffer_rsrc_t rs, uint32_t tile_off, const uint32_t (&off)[LOADS_PER_WAVE],
+                          uint8_t* lds_tile, int wave) {
+#pragma unroll
+    for (int j = 0; j < LOADS_PER_WAVE; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (lds_t*)(lds_tile + (wave * LOADS_PER_WAVE + j) * 1024), 16, off[j] + tile_off, 0, 0, 0);
+  }
+};
+
+// 32 lanes of one half-wave exchange with the other half: returns op(x, x of lane ^ 32).
+KD_DEV float xhalf_max(float x) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+KD_DEV float xhalf_sum(float x) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+// Transposed 4x16 read: lane i of each 16-lane group gets column (i) of the
+// 4 rows addressed by the group (see Tile layout); 4 x 16-bit per lane.
+KD_DEV u32x2 ds_read_tr16(const uint8_t* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4 __attribute__((address_space(3)))*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+KD_DEV void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Sum of a packed pair of 16-bit floats into an fp32 accumulator (v_dot2).
+template <class E> KD_DEV float acc_pair(uint32_t w, float acc);
+template <> KD_DEV float acc_pair<BF16>(uint32_t w, float acc) {
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
+}
+template <> KD_DEV float acc_pair<F16>(uint32_t w, float acc) {
+  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
+}
+
+}  // namespace kd
