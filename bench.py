@@ -94,7 +94,7 @@ class Step:
         self.plan = torch.empty(_lib.plan_bytes(B, T, D), dtype=torch.uint8, device=dev)
         self.o = torch.empty_like(q)
         self.lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
-        self.delta = torch.empty_like(self.lse)
+        self.delta = torch.empty((2, B, H, T), dtype=torch.float32, device=dev)
         self.dq, self.dk, self.dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
         self.inputs = (q, k, v, do)
         a = _attn_args(q, k, v, D ** -0.5)

@@ -15,8 +15,9 @@
  *   - Work is enqueued asynchronously on `stream` (a hipStream_t passed as
  *     void*; NULL is the default stream).  No call synchronises the host.
  *   - Tensors [B, H, T, D] are given by a base pointer and element strides for
- *     (b, h, t); the d stride must be 1, base pointers 16-byte aligned and the
- *     (b, h, t) strides multiples of 8 elements.
+ *     (b, h, t); the d stride must be 1, base pointers 16-byte aligned, the
+ *     (b, h, t) strides multiples of 8 elements, the t stride >= D and
+ *     T * t_stride * 2 < 2^31 bytes.
  *   - LSE is stored in log2 units (LSE2 = log2 sum_j exp2(S_ij * sm_scale *
  *     log2 e)), as the reference stores it (original_kernel.py:603-604).
  *     Fully masked rows get O = 0, LSE = -inf and zero gradients.
@@ -75,7 +76,8 @@ typedef struct kd_attn_args {
   int64_t do_strides[3];
   void *dq, *dk, *dv;           /* [B, H, T, D] (bwd) */
   int64_t dq_strides[3], dk_strides[3], dv_strides[3];
-  float *delta;                 /* [B, H, T] fp32 workspace (bwd) */
+  float *delta;                 /* fp32 workspace of 2 * B*H*T (bwd): Delta [B, H, T],
+                                   then LSE with -inf replaced by +inf [B, H, T] */
   int32_t B, H, T, D;
   int32_t dtype;                /* KD_BF16 / KD_F16 */
   float sm_scale;
@@ -110,8 +112,10 @@ int kd_plan_build(const kd_meta_args *meta, void *plan, void *stream);
  * _flash_attn_fwd (original_kernel.py:1697-1778, kernel :279-626). */
 int kd_attn_fwd(const kd_attn_args *a, const void *plan, void *stream);
 
-/* Delta = rowsum(O * dO) in fp32 into a->delta.  Replaces
- * _flash_attn_bwd_precompute (original_kernel.py:649-710, launch :1829-1846). */
+/* Delta = rowsum(O * dO) in fp32 into a->delta[0 : B*H*T], and the backward's
+ * copy of a->lse (fully masked rows: +inf) into a->delta[B*H*T : 2*B*H*T].
+ * Replaces _flash_attn_bwd_precompute (original_kernel.py:649-710, launch
+ * :1829-1846).  kd_attn_bwd_dq / _dkdv read both halves. */
 int kd_attn_bwd_delta(const kd_attn_args *a, void *stream);
 
 /* dQ from the saved LSE and Delta.  Replaces the dQ workers of

@@ -40,9 +40,10 @@ def _strides3(t):
 
 
 def _kernel_ready(x: torch.Tensor) -> torch.Tensor:
-    """Unit d-stride, 16-byte aligned base and 8-element-multiple strides."""
+    """Unit d-stride, 16-byte aligned base, 8-element-multiple strides, rows that do not overlap."""
     s = x.stride()
-    if (s[3] != 1 or x.data_ptr() % 16 != 0 or any(st % 8 for st in s[:3])):
+    if (s[3] != 1 or x.data_ptr() % 16 != 0 or any(st % 8 for st in s[:3]) or s[2] < x.shape[3]
+            or x.shape[2] * s[2] * 2 >= 2 ** 31):
         x = x.contiguous()
     return x
 
@@ -130,7 +131,7 @@ def _bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, 
     dq = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
     dk = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
     dv = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
-    delta = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+    delta = torch.empty((2, B, H, T), dtype=torch.float32, device=q.device)  # Delta, LSE for bwd
     a = _attn_args(q, k, v, sm_scale)
     a.o, a.o_strides = o.data_ptr(), _strides3(o)
     a.lse = lse.data_ptr()

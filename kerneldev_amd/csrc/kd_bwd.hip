@@ -6,16 +6,22 @@
 // (:1199-1207, :1366-1375) the loops visit EVERY non-empty tile, so the
 // gradient is the true gradient of the forward's mask.
 //
+// Workspace: a->delta holds 2 * B*H*T floats, Delta followed by LSEb, a copy
+// of the LSE with -inf (fully masked rows) replaced by +inf so that
+// exp2(S c - LSEb) is 0 on such rows without a per-element test.
+//
 // dQ kernel: 4 waves x 32 query rows per workgroup, 64 keys per step:
 //   S^T  = K Q^T,  dP^T = V dO^T          (A = K, V rows from LDS; B = Q, dO regs)
 //   dS^T = P^T * (dP^T - Delta)            (per-lane Delta, LSE)
-//   dQ^T += K^T dS^T                       (A = K^T from LDS; B = dS regs)
+//   dQ^T += K^T dS^T                       (A = K^T read transposed from LDS)
 // dK/dV kernel: 4 waves x 32 keys per workgroup, 64 queries per step:
 //   S = Q K^T,  dP = dO V^T                (A = Q, dO rows from LDS; B = K, V regs)
-//   dV^T += dO^T P,  dK^T += Q^T dS        (A = dO^T, Q^T from LDS; B = P, dS regs)
+//   dV^T += dO^T P,  dK^T += Q^T dS        (A = dO^T, Q^T read transposed)
 // Both keep the accumulated gradient transposed in registers so the MFMA
-// output of one product is the register-resident B operand of the next.
-#include "kd_internal.h"
+// output of one product is the register-resident B operand of the next, and
+// both stream their tiles global -> LDS with buffer_load ... lds into the
+// swizzled layout of kd_tile.h, double buffered.
+#include "kd_tile.h"
 
 namespace kd {
 
@@ -46,47 +52,10 @@ __global__ __launch_bounds__(256) void k_delta(AttnArgs a) {
   }
 #pragma unroll
   for (int off = TPR / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-  if (row < nrows && seg == 0) a.delta[row] = sum;
-}
-
-// ------------------------------------------------------------ shared cfg ----
-template <int D>
-struct BwdCfg {
-  static constexpr int BN = 64;              // keys (dQ) or queries (dK/dV) per step
-  static constexpr int RST = D + 8;          // row-major tile stride (elements)
-  static constexpr int TST = BN + 8;         // transposed tile stride (elements)
-  static constexpr int DS = D / 16;
-  static constexpr int DB = D / 32;
-  static constexpr int BLK = (BN / 4) * (D / 8);   // 4-row x 8-col blocks per tile
-  static constexpr int R_ELEMS = BN * RST;
-  static constexpr int T_ELEMS = D * TST;
-};
-
-// Load one 4-row x 8-col block of a [BN, D] tile (rows r0.., 16-byte loads).
-template <int D>
-KD_DEV void load_block(const uint16_t* base, int64_t rstride, int row0, int T, int blk, u32x4 (&r)[4]) {
-  const int rg = blk / (D / 8), dc = blk % (D / 8);
-#pragma unroll
-  for (int x = 0; x < 4; ++x) {
-    const int row = row0 + 4 * rg + x;
-    r[x] = row < T ? *reinterpret_cast<const u32x4*>(base + row * rstride + dc * 8) : u32x4{0, 0, 0, 0};
-  }
-}
-// Store it row-major ([BN][RST]) and transposed ([D][TST]).
-template <int D>
-KD_DEV void store_block(uint16_t* rm, uint16_t* tr, int blk, const u32x4 (&r)[4]) {
-  using C = BwdCfg<D>;
-  const int rg = blk / (D / 8), dc = blk % (D / 8);
-  if (rm != nullptr) {
-#pragma unroll
-    for (int x = 0; x < 4; ++x) *reinterpret_cast<u32x4*>(&rm[(4 * rg + x) * C::RST + dc * 8]) = r[x];
-  }
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    u32x2 lo = {pack_lo(r[0][w], r[1][w]), pack_lo(r[2][w], r[3][w])};
-    u32x2 hi = {pack_hi(r[0][w], r[1][w]), pack_hi(r[2][w], r[3][w])};
-    *reinterpret_cast<u32x2*>(&tr[(8 * dc + 2 * w) * C::TST + 4 * rg]) = lo;
-    *reinterpret_cast<u32x2*>(&tr[(8 * dc + 2 * w + 1) * C::TST + 4 * rg]) = hi;
+  if (row < nrows && seg == 0) {
+    a.delta[row] = sum;
+    const float l = a.lse[row];
+    a.delta[nrows + row] = (l == -__builtin_inff()) ? __builtin_inff() : l;
   }
 }
 
@@ -104,16 +73,32 @@ KD_DEV void store_rows_T(uint16_t* g, const f32x16 (&acc)[D / 32], float scale, 
   }
 }
 
+// Byte offsets of the transposed A-operand reads (tile^T, 32 columns x 16 rows
+// per MFMA k-step) for this lane: [db][half], k-step ks adds ks * 16 rows.
+template <int D>
+KD_DEV void tr_addrs(int lane, int (&addr)[D / 32][2]) {
+  using TL = Tile<D>;
+  const int i = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int r = 8 * (g >> 1) + 4 * half + (i >> 2);
+      const int chunk = 4 * db + 2 * (g & 1) + ((i & 3) >> 1);
+      addr[db][half] = TL::at(r, chunk) + 8 * (i & 1);
+    }
+}
+
 // ------------------------------------------------------------------- dQ ----
 template <class E, int D>
-__global__ __launch_bounds__(256) void k_dq(AttnArgs a, const uint32_t* __restrict__ codes,
-                                            const uint32_t* __restrict__ list,
-                                            const int32_t* __restrict__ count, int nT, int nQB) {
-  using C = BwdCfg<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t s_k[2][C::R_ELEMS];
-  __shared__ __attribute__((aligned(16))) uint16_t s_v[2][C::R_ELEMS];
-  __shared__ __attribute__((aligned(16))) uint16_t s_kt[2][C::T_ELEMS];
-  __shared__ __attribute__((aligned(16))) uint32_t s_code[2][C::BN];
+__global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __restrict__ codes,
+                                               const uint32_t* __restrict__ list,
+                                               const int32_t* __restrict__ count, int nT, int nQB) {
+  using TL = Tile<D>;
+  constexpr int DS = D / 16, DB = D / 32, NL = TL::LOADS_PER_WAVE;
+  __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][TL::BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][TL::BYTES];
+  __shared__ __attribute__((aligned(256))) uint32_t s_code[2][64];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
   const int T = a.T, H = a.H;
@@ -126,84 +111,81 @@ __global__ __launch_bounds__(256) void k_dq(AttnArgs a, const uint32_t* __restri
   const uint16_t* dog = static_cast<const uint16_t*>(a.dout) + b * a.do_strides[0] + h * a.do_strides[1];
   const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_strides[0] + h * a.k_strides[1];
   const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_strides[0] + h * a.v_strides[1];
-  const uint32_t* codes_b = codes + int64_t(b) * T;
+  const uint32_t qrb = uint32_t(a.q_strides[2]) * 2u, dorb = uint32_t(a.do_strides[2]) * 2u,
+                 krb = uint32_t(a.k_strides[2]) * 2u, vrb = uint32_t(a.v_strides[2]) * 2u;
+  const auto rs_q = make_rsrc(qg, uint32_t(T) * qrb);
+  const auto rs_do = make_rsrc(dog, uint32_t(T) * dorb);
+  const auto rs_k = make_rsrc(kg, uint32_t(T) * krb);
+  const auto rs_v = make_rsrc(vg, uint32_t(T) * vrb);
+  const auto rs_c = make_rsrc(codes + int64_t(b) * T, uint32_t(T) * 4u);
+  const int64_t BHT = int64_t(a.B) * H * T;
 
   const int qrow = qblock * 128 + wave * 32 + c;
   const bool qvalid = qrow < T;
-  u32x4 qf[C::DS], dof[C::DS];
+  u32x4 qf[DS], dof[DS];
 #pragma unroll
-  for (int st = 0; st < C::DS; ++st) {
-    qf[st] = qvalid ? *reinterpret_cast<const u32x4*>(qg + qrow * a.q_strides[2] + 16 * st + 8 * hf)
-                    : u32x4{0, 0, 0, 0};
-    dof[st] = qvalid ? *reinterpret_cast<const u32x4*>(dog + qrow * a.do_strides[2] + 16 * st + 8 * hf)
-                     : u32x4{0, 0, 0, 0};
+  for (int st = 0; st < DS; ++st) {
+    qf[st] = buf_load16(rs_q, uint32_t(qrow) * qrb + (16 * st + 8 * hf) * 2);
+    dof[st] = buf_load16(rs_do, uint32_t(qrow) * dorb + (16 * st + 8 * hf) * 2);
   }
   const float INF = __builtin_inff();
-  float lse = qvalid ? a.lse[int64_t(bh) * T + qrow] : -INF;
-  lse = (lse == -INF) ? INF : lse;  // fully masked row: every p becomes 0
+  const float lse = qvalid ? a.delta[BHT + int64_t(bh) * T + qrow] : INF;
   const float delta = qvalid ? a.delta[int64_t(bh) * T + qrow] : 0.f;
-  const uint32_t qcode = qvalid ? codes_b[qrow] : 0u;
+  const uint32_t qcode = qvalid ? codes[int64_t(b) * T + qrow] : 0u;
 
   const int lbase = b * nQB + qblock;
   const int n = count[lbase];
   const uint32_t* ent = list + int64_t(lbase) * nT;
 
-  // K via 4x8 blocks (row-major + transposed), V via the same blocks (row-major)
-  u32x4 rk[4], rv[4];
-  uint32_t rcode = 0;
-  auto load_tile = [&](int kt) {
-    const int k0 = kt * C::BN;
-    if (tid < C::BLK) {
-      load_block<D>(kg, a.k_strides[2], k0, T, tid, rk);
-      load_block<D>(vg, a.v_strides[2], k0, T, tid, rv);
-    }
-    if (tid < C::BN) rcode = (k0 + tid < T) ? codes_b[k0 + tid] : 0u;
+  uint32_t koff[NL], voff[NL];
+  TL::load_offsets(wave, lane, krb, koff);
+  TL::load_offsets(wave, lane, vrb, voff);
+  auto load_tile = [&](int kt, int buf) {
+    const uint32_t k0 = uint32_t(kt) * 64u;
+    TL::load(rs_k, k0 * krb, koff, s_k[buf], wave);
+    TL::load(rs_v, k0 * vrb, voff, s_v[buf], wave);
+    if (wave == 0)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_t*)&s_code[buf][0], 4, (k0 + lane) * 4u, 0, 0, 0);
   };
-  auto store_tile = [&](int buf) {
-    if (tid < C::BLK) {
-      store_block<D>(s_k[buf], s_kt[buf], tid, rk);
-      const int rg = tid / (D / 8), dc = tid % (D / 8);
+
+  const int srow = sigma(c);
+  int raddr[DS];
 #pragma unroll
-      for (int x = 0; x < 4; ++x) *reinterpret_cast<u32x4*>(&s_v[buf][(4 * rg + x) * C::RST + dc * 8]) = rv[x];
-    }
-    if (tid < C::BN) s_code[buf][tid] = rcode;
-  };
+  for (int st = 0; st < DS; ++st) raddr[st] = TL::at(srow, 2 * st + hf);
+  int taddr[DB][2];
+  tr_addrs<D>(lane, taddr);
 
   const float sl2 = a.sm_scale * 1.4426950408889634f;
   const float NEG_INF = -INF;
-  f32x16 acc[C::DB];
+  f32x16 acc[DB];
 #pragma unroll
-  for (int db = 0; db < C::DB; ++db) acc[db] = f32x16{};
-  const int srow = sigma(c);
+  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
 
-  if (n > 0) {
-    load_tile(int(ent[0] >> 1));
-    store_tile(0);
-  }
-  __syncthreads();
+  if (n > 0) load_tile(int(ent[0] >> 1), 0);
 
   for (int e = 0; e < n; ++e) {
     const int buf = e & 1;
     const uint32_t cur = ent[e];
-    const bool has_next = e + 1 < n;
-    if (has_next) load_tile(int(ent[e + 1] >> 1));
+    wait_vmem();
+    __syncthreads();
+    if (e + 1 < n) load_tile(int(ent[e + 1] >> 1), buf ^ 1);
+    const uint8_t* kt = s_k[buf];
+    const uint8_t* vt = s_v[buf];
 
-    f32x16 s[2], dp[2];
+    f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      s[kb] = f32x16{};
-      dp[kb] = f32x16{};
+    for (int st = 0; st < DS; ++st) {
 #pragma unroll
-      for (int st = 0; st < C::DS; ++st) {
-        const int off = (32 * kb + srow) * C::RST + 16 * st + 8 * hf;
-        const u32x4 ak = *reinterpret_cast<const u32x4*>(&s_k[buf][off]);
-        const u32x4 av = *reinterpret_cast<const u32x4*>(&s_v[buf][off]);
+      for (int kb = 0; kb < 2; ++kb) {
+        const int off = raddr[st] + kb * 32 * TL::ROWB;
+        const u32x4 ak = *reinterpret_cast<const u32x4*>(kt + off);
+        const u32x4 av = *reinterpret_cast<const u32x4*>(vt + off);
         s[kb] = mfma32x32x16<E>(ak, qf[st], s[kb]);
         dp[kb] = mfma32x32x16<E>(av, dof[st], dp[kb]);
       }
     }
     if (!(cur & 1u)) {
-      const int k0 = int(cur >> 1) * C::BN;
+      const int k0 = int(cur >> 1) * 64;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -233,16 +215,17 @@ __global__ __launch_bounds__(256) void k_dq(AttnArgs a, const uint32_t* __restri
         dsb[kb][t] = u32x4{pack2<E>(ds[8 * t + 0], ds[8 * t + 1]), pack2<E>(ds[8 * t + 2], ds[8 * t + 3]),
                            pack2<E>(ds[8 * t + 4], ds[8 * t + 5]), pack2<E>(ds[8 * t + 6], ds[8 * t + 7])};
     }
+    // dQ^T += K^T dS^T
 #pragma unroll
-    for (int db = 0; db < C::DB; ++db) {
+    for (int t4 = 0; t4 < 4; ++t4) {
 #pragma unroll
-      for (int t4 = 0; t4 < 4; ++t4) {
-        const u32x4 ak = *reinterpret_cast<const u32x4*>(&s_kt[buf][(32 * db + c) * C::TST + 16 * t4 + 8 * hf]);
+      for (int db = 0; db < DB; ++db) {
+        const u32x2 lo = ds_read_tr16(kt + taddr[db][0] + t4 * 16 * TL::ROWB);
+        const u32x2 hi = ds_read_tr16(kt + taddr[db][1] + t4 * 16 * TL::ROWB);
+        const u32x4 ak = {lo[0], lo[1], hi[0], hi[1]};
         acc[db] = mfma32x32x16<E>(ak, dsb[t4 >> 1][t4 & 1], acc[db]);
       }
     }
-    if (has_next) store_tile(buf ^ 1);
-    __syncthreads();
   }
 
   if (qvalid) {
@@ -253,17 +236,16 @@ __global__ __launch_bounds__(256) void k_dq(AttnArgs a, const uint32_t* __restri
 
 // ---------------------------------------------------------------- dK/dV ----
 template <class E, int D>
-__global__ __launch_bounds__(256) void k_dkdv(AttnArgs a, const uint32_t* __restrict__ codes,
-                                              const uint32_t* __restrict__ list,
-                                              const int32_t* __restrict__ count, int nT, int nKB) {
-  using C = BwdCfg<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t s_q[2][C::R_ELEMS];
-  __shared__ __attribute__((aligned(16))) uint16_t s_do[2][C::R_ELEMS];
-  __shared__ __attribute__((aligned(16))) uint16_t s_qt[2][C::T_ELEMS];
-  __shared__ __attribute__((aligned(16))) uint16_t s_dot[2][C::T_ELEMS];
-  __shared__ __attribute__((aligned(16))) float s_lse[2][C::BN];
-  __shared__ __attribute__((aligned(16))) float s_delta[2][C::BN];
-  __shared__ __attribute__((aligned(16))) uint32_t s_code[2][C::BN];
+__global__ __launch_bounds__(256, D == 128 ? 1 : 2) void k_dkdv(AttnArgs a, const uint32_t* __restrict__ codes,
+                                                 const uint32_t* __restrict__ list,
+                                                 const int32_t* __restrict__ count, int nT, int nKB) {
+  using TL = Tile<D>;
+  constexpr int DS = D / 16, DB = D / 32, NL = TL::LOADS_PER_WAVE;
+  __shared__ __attribute__((aligned(1024))) uint8_t s_q[2][TL::BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_do[2][TL::BYTES];
+  __shared__ __attribute__((aligned(256))) float s_lse[2][64];
+  __shared__ __attribute__((aligned(256))) float s_delta[2][64];
+  __shared__ __attribute__((aligned(256))) uint32_t s_code[2][64];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
   const int T = a.T, H = a.H;
@@ -276,92 +258,87 @@ __global__ __launch_bounds__(256) void k_dkdv(AttnArgs a, const uint32_t* __rest
   const uint16_t* dog = static_cast<const uint16_t*>(a.dout) + b * a.do_strides[0] + h * a.do_strides[1];
   const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_strides[0] + h * a.k_strides[1];
   const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_strides[0] + h * a.v_strides[1];
-  const uint32_t* codes_b = codes + int64_t(b) * T;
-  const float* lse_bh = a.lse + int64_t(bh) * T;
-  const float* delta_bh = a.delta + int64_t(bh) * T;
+  const uint32_t qrb = uint32_t(a.q_strides[2]) * 2u, dorb = uint32_t(a.do_strides[2]) * 2u,
+                 krb = uint32_t(a.k_strides[2]) * 2u, vrb = uint32_t(a.v_strides[2]) * 2u;
+  const auto rs_q = make_rsrc(qg, uint32_t(T) * qrb);
+  const auto rs_do = make_rsrc(dog, uint32_t(T) * dorb);
+  const auto rs_k = make_rsrc(kg, uint32_t(T) * krb);
+  const auto rs_v = make_rsrc(vg, uint32_t(T) * vrb);
+  const int64_t BHT = int64_t(a.B) * H * T;
+  const auto rs_lse = make_rsrc(a.delta + BHT + int64_t(bh) * T, uint32_t(T) * 4u);
+  const auto rs_dl = make_rsrc(a.delta + int64_t(bh) * T, uint32_t(T) * 4u);
+  const auto rs_c = make_rsrc(codes + int64_t(b) * T, uint32_t(T) * 4u);
 
   const int krow = kblock * 128 + wave * 32 + c;
   const bool kvalid = krow < T;
-  u32x4 kf[C::DS], vf[C::DS];
+  u32x4 kf[DS], vf[DS];
 #pragma unroll
-  for (int st = 0; st < C::DS; ++st) {
-    kf[st] = kvalid ? *reinterpret_cast<const u32x4*>(kg + krow * a.k_strides[2] + 16 * st + 8 * hf)
-                    : u32x4{0, 0, 0, 0};
-    vf[st] = kvalid ? *reinterpret_cast<const u32x4*>(vg + krow * a.v_strides[2] + 16 * st + 8 * hf)
-                    : u32x4{0, 0, 0, 0};
+  for (int st = 0; st < DS; ++st) {
+    kf[st] = buf_load16(rs_k, uint32_t(krow) * krb + (16 * st + 8 * hf) * 2);
+    vf[st] = buf_load16(rs_v, uint32_t(krow) * vrb + (16 * st + 8 * hf) * 2);
   }
-  const uint32_t kcode = kvalid ? codes_b[krow] : 0u;
+  const uint32_t kcode = kvalid ? codes[int64_t(b) * T + krow] : 0u;
 
   const int lbase = b * nKB + kblock;
   const int n = count[lbase];
   const uint32_t* ent = list + int64_t(lbase) * nT;
 
-  const float INF = __builtin_inff();
-  u32x4 rq[4], rdo[4];
-  float rsmall = 0.f;
-  uint32_t rcode = 0;
-  auto load_tile = [&](int qt) {
-    const int q0 = qt * C::BN;
-    if (tid < C::BLK) {
-      load_block<D>(qg, a.q_strides[2], q0, T, tid, rq);
-      load_block<D>(dog, a.do_strides[2], q0, T, tid, rdo);
-    }
-    const int x = tid & 63, qi = q0 + x;
-    if (tid < 64) {
-      float l = qi < T ? lse_bh[qi] : -INF;
-      rsmall = (l == -INF) ? INF : l;
-    } else if (tid < 128) {
-      rsmall = qi < T ? delta_bh[qi] : 0.f;
-    } else if (tid < 192) {
-      rcode = qi < T ? codes_b[qi] : 0u;
-    }
-  };
-  auto store_tile = [&](int buf) {
-    if (tid < C::BLK) {
-      store_block<D>(s_q[buf], s_qt[buf], tid, rq);
-      store_block<D>(s_do[buf], s_dot[buf], tid, rdo);
-    }
-    const int x = tid & 63;
-    if (tid < 64) s_lse[buf][x] = rsmall;
-    else if (tid < 128) s_delta[buf][x] = rsmall;
-    else if (tid < 192) s_code[buf][x] = rcode;
+  uint32_t qoff[NL], dooff[NL];
+  TL::load_offsets(wave, lane, qrb, qoff);
+  TL::load_offsets(wave, lane, dorb, dooff);
+  auto load_tile = [&](int qt, int buf) {
+    const uint32_t q0 = uint32_t(qt) * 64u;
+    TL::load(rs_q, q0 * qrb, qoff, s_q[buf], wave);
+    TL::load(rs_do, q0 * dorb, dooff, s_do[buf], wave);
+    if (wave == 0)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, (lds_t*)&s_lse[buf][0], 4, (q0 + lane) * 4u, 0, 0, 0);
+    else if (wave == 1)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_dl, (lds_t*)&s_delta[buf][0], 4, (q0 + lane) * 4u, 0, 0, 0);
+    else if (wave == 2)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_t*)&s_code[buf][0], 4, (q0 + lane) * 4u, 0, 0, 0);
   };
 
-  const float sl2 = a.sm_scale * 1.4426950408889634f;
-  const float NEG_INF = -INF;
-  f32x16 dk[C::DB], dv[C::DB];
+  const int srow = sigma(c);
+  int raddr[DS];
 #pragma unroll
-  for (int db = 0; db < C::DB; ++db) {
+  for (int st = 0; st < DS; ++st) raddr[st] = TL::at(srow, 2 * st + hf);
+  int taddr[DB][2];
+  tr_addrs<D>(lane, taddr);
+
+  const float sl2 = a.sm_scale * 1.4426950408889634f;
+  const float NEG_INF = -__builtin_inff();
+  f32x16 dk[DB], dv[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
     dk[db] = f32x16{};
     dv[db] = f32x16{};
   }
-  const int srow = sigma(c);
 
-  if (n > 0) {
-    load_tile(int(ent[0] >> 1));
-    store_tile(0);
-  }
-  __syncthreads();
+  if (n > 0) load_tile(int(ent[0] >> 1), 0);
 
   for (int e = 0; e < n; ++e) {
     const int buf = e & 1;
     const uint32_t cur = ent[e];
-    const bool has_next = e + 1 < n;
-    if (has_next) load_tile(int(ent[e + 1] >> 1));
-    const int q0 = int(cur >> 1) * C::BN;
+    wait_vmem();
+    __syncthreads();
+    if (e + 1 < n) load_tile(int(ent[e + 1] >> 1), buf ^ 1);
+    const uint8_t* qt = s_q[buf];
+    const uint8_t* dot = s_do[buf];
+    const int q0 = int(cur >> 1) * 64;
+    const bool partial = !(cur & 1u);
 
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
-      for (int st = 0; st < C::DS; ++st) {
-        const int off = (32 * qb + srow) * C::RST + 16 * st + 8 * hf;
-        const u32x4 aq = *reinterpret_cast<const u32x4*>(&s_q[buf][off]);
-        const u32x4 ao = *reinterpret_cast<const u32x4*>(&s_do[buf][off]);
+      for (int st = 0; st < DS; ++st) {
+        const int off = raddr[st] + qb * 32 * TL::ROWB;
+        const u32x4 aq = *reinterpret_cast<const u32x4*>(qt + off);
+        const u32x4 ao = *reinterpret_cast<const u32x4*>(dot + off);
         s = mfma32x32x16<E>(aq, kf[st], s);
         dp = mfma32x32x16<E>(ao, vf[st], dp);
       }
-      // register r of s holds query 32*qb + 16*(r/8) + 8*hf + r%8, key = this lane's key
+      // register r holds query 32 qb + 16 (r / 8) + 8 hf + r % 8 of this lane's key
       u32x4 pb[2], dsb[2];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -371,7 +348,6 @@ __global__ __launch_bounds__(256) void k_dkdv(AttnArgs a, const uint32_t* __rest
         const f32x4 d0 = *reinterpret_cast<const f32x4*>(&s_delta[buf][ql]);
         const f32x4 d1 = *reinterpret_cast<const f32x4*>(&s_delta[buf][ql + 4]);
         u32x4 c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
-        const bool partial = !(cur & 1u);
         if (partial) {
           c0 = *reinterpret_cast<const u32x4*>(&s_code[buf][ql]);
           c1 = *reinterpret_cast<const u32x4*>(&s_code[buf][ql + 4]);
@@ -393,20 +369,21 @@ __global__ __launch_bounds__(256) void k_dkdv(AttnArgs a, const uint32_t* __rest
         dsb[t] = u32x4{pack2<E>(ds[0], ds[1]), pack2<E>(ds[2], ds[3]), pack2<E>(ds[4], ds[5]),
                        pack2<E>(ds[6], ds[7])};
       }
+      // dV^T += dO^T P,  dK^T += Q^T dS   (k-steps 2 qb + t over the 64 queries)
 #pragma unroll
-      for (int db = 0; db < C::DB; ++db) {
+      for (int t = 0; t < 2; ++t) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int off = (32 * db + c) * C::TST + 16 * (2 * qb + t) + 8 * hf;
-          const u32x4 ao = *reinterpret_cast<const u32x4*>(&s_dot[buf][off]);
-          const u32x4 aq = *reinterpret_cast<const u32x4*>(&s_qt[buf][off]);
-          dv[db] = mfma32x32x16<E>(ao, pb[t], dv[db]);
-          dk[db] = mfma32x32x16<E>(aq, dsb[t], dk[db]);
+        for (int db = 0; db < DB; ++db) {
+          const int off = (2 * qb + t) * 16 * TL::ROWB;
+          const u32x2 olo = ds_read_tr16(dot + taddr[db][0] + off);
+          const u32x2 ohi = ds_read_tr16(dot + taddr[db][1] + off);
+          const u32x2 qlo = ds_read_tr16(qt + taddr[db][0] + off);
+          const u32x2 qhi = ds_read_tr16(qt + taddr[db][1] + off);
+          dv[db] = mfma32x32x16<E>(u32x4{olo[0], olo[1], ohi[0], ohi[1]}, pb[t], dv[db]);
+          dk[db] = mfma32x32x16<E>(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]}, dsb[t], dk[db]);
         }
       }
     }
-    if (has_next) store_tile(buf ^ 1);
-    __syncthreads();
   }
 
   if (kvalid) {

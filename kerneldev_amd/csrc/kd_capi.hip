@@ -27,7 +27,7 @@ bool strides_ok(const int64_t* s) {
 // Largest element offset reachable by a [B, H, T, D] view (for int32 safety
 // of the in-kernel index math the offsets are int64; this only rejects
 // negative / overlapping-by-construction layouts).
-int check_tensor(const void* p, const int64_t* s, const char* name) {
+int check_tensor(const void* p, const int64_t* s, const char* name, int T = 1, int D = 0) {
   if (p == nullptr) {
     g_err = std::string(name) + " is NULL";
     return KD_ERR_INVALID;
@@ -39,6 +39,15 @@ int check_tensor(const void* p, const int64_t* s, const char* name) {
   if (!strides_ok(s)) {
     g_err = std::string(name) + " strides (b, h, t) must be non-negative multiples of 8 elements";
     return KD_ERR_INVALID;
+  }
+  if (s[2] < D) {
+    g_err = std::string(name) + " rows overlap: the t stride must be >= head_dim";
+    return KD_ERR_INVALID;
+  }
+  // kernels address one (b, h) slice through a buffer resource of 32-bit size
+  if (int64_t(T) * s[2] * 2 >= (int64_t(1) << 31)) {
+    g_err = std::string(name) + ": T * t_stride * 2 bytes must be < 2^31 per (b, h) slice";
+    return KD_ERR_UNSUPPORTED;
   }
   return KD_OK;
 }
@@ -107,8 +116,8 @@ int kd_attn_fwd(const kd_attn_args* a, const void* plan, void* stream) {
   int r = check_common(a);
   if (r) return r;
   if (plan == nullptr) return fail(KD_ERR_INVALID, "plan is NULL");
-  if ((r = check_tensor(a->q, a->q_strides, "q")) || (r = check_tensor(a->k, a->k_strides, "k")) ||
-      (r = check_tensor(a->v, a->v_strides, "v")) || (r = check_tensor(a->o, a->o_strides, "o")))
+  if ((r = check_tensor(a->q, a->q_strides, "q", a->T, a->D)) || (r = check_tensor(a->k, a->k_strides, "k", a->T, a->D)) ||
+      (r = check_tensor(a->v, a->v_strides, "v", a->T, a->D)) || (r = check_tensor(a->o, a->o_strides, "o", a->T, a->D)))
     return r;
   r = kd::launch_fwd(*a, static_cast<const uint8_t*>(plan), as_stream(stream));
   return r ? fail(r, "kernel launch failed (forward)") : KD_OK;
@@ -117,9 +126,9 @@ int kd_attn_fwd(const kd_attn_args* a, const void* plan, void* stream) {
 int kd_attn_bwd_delta(const kd_attn_args* a, void* stream) {
   int r = check_common(a);
   if (r) return r;
-  if ((r = check_tensor(a->o, a->o_strides, "o")) || (r = check_tensor(a->dout, a->do_strides, "dout")))
+  if ((r = check_tensor(a->o, a->o_strides, "o", a->T, a->D)) || (r = check_tensor(a->dout, a->do_strides, "dout", a->T, a->D)))
     return r;
-  if (a->delta == nullptr) return fail(KD_ERR_INVALID, "delta is NULL");
+  if (a->delta == nullptr || a->lse == nullptr) return fail(KD_ERR_INVALID, "delta and lse are required");
   r = kd::launch_delta(*a, as_stream(stream));
   return r ? fail(r, "kernel launch failed (delta)") : KD_OK;
 }
@@ -129,8 +138,8 @@ static int check_bwd(const kd_attn_args* a, const void* plan) {
   if (r) return r;
   if (plan == nullptr) return fail(KD_ERR_INVALID, "plan is NULL");
   if (a->lse == nullptr || a->delta == nullptr) return fail(KD_ERR_INVALID, "lse and delta are required");
-  if ((r = check_tensor(a->q, a->q_strides, "q")) || (r = check_tensor(a->k, a->k_strides, "k")) ||
-      (r = check_tensor(a->v, a->v_strides, "v")) || (r = check_tensor(a->dout, a->do_strides, "dout")))
+  if ((r = check_tensor(a->q, a->q_strides, "q", a->T, a->D)) || (r = check_tensor(a->k, a->k_strides, "k", a->T, a->D)) ||
+      (r = check_tensor(a->v, a->v_strides, "v", a->T, a->D)) || (r = check_tensor(a->dout, a->do_strides, "dout", a->T, a->D)))
     return r;
   return KD_OK;
 }
@@ -138,7 +147,7 @@ static int check_bwd(const kd_attn_args* a, const void* plan) {
 int kd_attn_bwd_dq(const kd_attn_args* a, const void* plan, void* stream) {
   int r = check_bwd(a, plan);
   if (r) return r;
-  if ((r = check_tensor(a->dq, a->dq_strides, "dq"))) return r;
+  if ((r = check_tensor(a->dq, a->dq_strides, "dq", a->T, a->D))) return r;
   r = kd::launch_dq(*a, static_cast<const uint8_t*>(plan), as_stream(stream));
   return r ? fail(r, "kernel launch failed (dq)") : KD_OK;
 }
@@ -146,7 +155,7 @@ int kd_attn_bwd_dq(const kd_attn_args* a, const void* plan, void* stream) {
 int kd_attn_bwd_dkdv(const kd_attn_args* a, const void* plan, void* stream) {
   int r = check_bwd(a, plan);
   if (r) return r;
-  if ((r = check_tensor(a->dk, a->dk_strides, "dk")) || (r = check_tensor(a->dv, a->dv_strides, "dv"))) return r;
+  if ((r = check_tensor(a->dk, a->dk_strides, "dk", a->T, a->D)) || (r = check_tensor(a->dv, a->dv_strides, "dv", a->T, a->D))) return r;
   r = kd::launch_dkdv(*a, static_cast<const uint8_t*>(plan), as_stream(stream));
   return r ? fail(r, "kernel launch failed (dkdv)") : KD_OK;
 }
