@@ -339,6 +339,19 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void k_dkdv(AttnArgs a, cons
         dp = mfma32x32x16<E>(ao, vf[st], dp);
       }
       // register r holds query 32 qb + 16 (r / 8) + 8 hf + r % 8 of this lane's key
+      if (partial) {  // wave-uniform: evaluate the mask on this 32 x 32 block
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int ql = 32 * qb + 16 * t + 8 * hf;
+          const u32x4 c0 = *reinterpret_cast<const u32x4*>(&s_code[buf][ql]);
+          const u32x4 c1 = *reinterpret_cast<const u32x4*>(&s_code[buf][ql + 4]);
+#pragma unroll
+          for (int x = 0; x < 8; ++x) {
+            const uint32_t qc = x < 4 ? c0[x] : c1[x - 4];
+            if (!allow(qc, kcode, q0 + ql + x, krow)) s[8 * t + x] = NEG_INF;
+          }
+        }
+      }
       u32x4 pb[2], dsb[2];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -347,22 +360,12 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void k_dkdv(AttnArgs a, cons
         const f32x4 l1 = *reinterpret_cast<const f32x4*>(&s_lse[buf][ql + 4]);
         const f32x4 d0 = *reinterpret_cast<const f32x4*>(&s_delta[buf][ql]);
         const f32x4 d1 = *reinterpret_cast<const f32x4*>(&s_delta[buf][ql + 4]);
-        u32x4 c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
-        if (partial) {
-          c0 = *reinterpret_cast<const u32x4*>(&s_code[buf][ql]);
-          c1 = *reinterpret_cast<const u32x4*>(&s_code[buf][ql + 4]);
-        }
         float p[8], ds[8];
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
           const float lx = x < 4 ? l0[x] : l1[x - 4];
           const float dx = x < 4 ? d0[x] : d1[x - 4];
-          float sv = s[8 * t + x];
-          if (partial) {
-            const uint32_t qc = x < 4 ? c0[x] : c1[x - 4];
-            if (!allow(qc, kcode, q0 + ql + x, krow)) sv = NEG_INF;
-          }
-          p[x] = fast_exp2(__builtin_fmaf(sv, sl2, -lx));
+          p[x] = fast_exp2(__builtin_fmaf(s[8 * t + x], sl2, -lx));
           ds[x] = p[x] * (dp[8 * t + x] - dx);
         }
         pb[t] = u32x4{pack2<E>(p[0], p[1]), pack2<E>(p[2], p[3]), pack2<E>(p[4], p[5]), pack2<E>(p[6], p[7])};
