@@ -14,9 +14,10 @@
 //   S^T  = K Q^T,  dP^T = V dO^T          (A = K, V rows from LDS; B = Q, dO regs)
 //   dS^T = P^T * (dP^T - Delta)            (per-lane Delta, LSE)
 //   dQ^T += K^T dS^T                       (A = K^T read transposed from LDS)
-// dK/dV kernel: 4 waves x 32 keys per workgroup, 64 queries per step:
+// dK/dV kernel: 4 wave pairs x 32 keys per workgroup, 64 queries per step:
 //   S = Q K^T,  dP = dO V^T                (A = Q, dO rows from LDS; B = K, V regs)
 //   dV^T += dO^T P,  dK^T += Q^T dS        (A = dO^T, Q^T read transposed)
+// with S/P/dV on one wave of a pair and dP/dS/dK on the other.
 // Both keep the accumulated gradient transposed in registers so the MFMA
 // output of one product is the register-resident B operand of the next, and
 // both stream their tiles global -> LDS with buffer_load ... lds into the
@@ -235,19 +236,32 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
 }
 
 // ---------------------------------------------------------------- dK/dV ----
+// 8 waves per workgroup = 4 pairs, one pair per 32 keys (128 keys in all).
+// The two waves of a pair split the work of their keys by role:
+//   role 0 ("P wave"):  S = Q K^T, P = exp2(S c - LSE)   -> dV^T += dO^T P
+//   role 1 ("dS wave"): dP = dO V^T, dS = P (dP - Delta) -> dK^T += Q^T dS
+// P goes from the P wave to the dS wave through LDS, lane to lane (both
+// waves hold the same MFMA output layout).  Each wave keeps one B operand
+// (K or V) and one accumulator (dV^T or dK^T) in registers, so a pair needs
+// about half the registers of one wave doing all four products, and the
+// pair shares a SIMD (waves w and w + 4), so one wave's VALU softmax runs
+// under the other's MFMAs.
 template <class E, int D>
-__global__ __launch_bounds__(256, D == 128 ? 1 : 2) void k_dkdv(AttnArgs a, const uint32_t* __restrict__ codes,
+__global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __restrict__ codes,
                                                  const uint32_t* __restrict__ list,
                                                  const int32_t* __restrict__ count, int nT, int nKB) {
-  using TL = Tile<D>;
+  constexpr int NW = 8;
+  using TL = Tile<D, NW>;
   constexpr int DS = D / 16, DB = D / 32, NL = TL::LOADS_PER_WAVE;
   __shared__ __attribute__((aligned(1024))) uint8_t s_q[2][TL::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_do[2][TL::BYTES];
+  __shared__ __attribute__((aligned(1024))) float s_p[4][2 * 16][64];  // [pair][register][lane]
   __shared__ __attribute__((aligned(256))) float s_lse[2][64];
   __shared__ __attribute__((aligned(256))) float s_delta[2][64];
   __shared__ __attribute__((aligned(256))) uint32_t s_code[2][64];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
+  const int pair = wave & 3, role = wave >> 2;
   const int T = a.T, H = a.H;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = work / nKB;
@@ -262,20 +276,20 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void k_dkdv(AttnArgs a, cons
                  krb = uint32_t(a.k_strides[2]) * 2u, vrb = uint32_t(a.v_strides[2]) * 2u;
   const auto rs_q = make_rsrc(qg, uint32_t(T) * qrb);
   const auto rs_do = make_rsrc(dog, uint32_t(T) * dorb);
-  const auto rs_k = make_rsrc(kg, uint32_t(T) * krb);
-  const auto rs_v = make_rsrc(vg, uint32_t(T) * vrb);
   const int64_t BHT = int64_t(a.B) * H * T;
   const auto rs_lse = make_rsrc(a.delta + BHT + int64_t(bh) * T, uint32_t(T) * 4u);
   const auto rs_dl = make_rsrc(a.delta + int64_t(bh) * T, uint32_t(T) * 4u);
   const auto rs_c = make_rsrc(codes + int64_t(b) * T, uint32_t(T) * 4u);
 
-  const int krow = kblock * 128 + wave * 32 + c;
+  // this lane's key and its B operand: K for the P wave, V for the dS wave
+  const int krow = kblock * 128 + pair * 32 + c;
   const bool kvalid = krow < T;
-  u32x4 kf[DS], vf[DS];
+  u32x4 bf[DS];
+  {
+    const auto rs_b = role == 0 ? make_rsrc(kg, uint32_t(T) * krb) : make_rsrc(vg, uint32_t(T) * vrb);
+    const uint32_t brb = role == 0 ? krb : vrb;
 #pragma unroll
-  for (int st = 0; st < DS; ++st) {
-    kf[st] = buf_load16(rs_k, uint32_t(krow) * krb + (16 * st + 8 * hf) * 2);
-    vf[st] = buf_load16(rs_v, uint32_t(krow) * vrb + (16 * st + 8 * hf) * 2);
+    for (int st = 0; st < DS; ++st) bf[st] = buf_load16(rs_b, uint32_t(krow) * brb + (16 * st + 8 * hf) * 2);
   }
   const uint32_t kcode = kvalid ? codes[int64_t(b) * T + krow] : 0u;
 
@@ -307,12 +321,10 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void k_dkdv(AttnArgs a, cons
 
   const float sl2 = a.sm_scale * 1.4426950408889634f;
   const float NEG_INF = -__builtin_inff();
-  f32x16 dk[DB], dv[DB];
+  f32x16 acc[DB];  // dV^T (role 0) or dK^T (role 1)
 #pragma unroll
-  for (int db = 0; db < DB; ++db) {
-    dk[db] = f32x16{};
-    dv[db] = f32x16{};
-  }
+  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
+  float* xp = &s_p[pair][0][lane];
 
   if (n > 0) load_tile(int(ent[0] >> 1), 0);
 
@@ -320,80 +332,98 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void k_dkdv(AttnArgs a, cons
     const int buf = e & 1;
     const uint32_t cur = ent[e];
     wait_vmem();
-    __syncthreads();
+    __syncthreads();  // tile e landed; every wave is done with tile e-1 and its P
     if (e + 1 < n) load_tile(int(ent[e + 1] >> 1), buf ^ 1);
     const uint8_t* qt = s_q[buf];
     const uint8_t* dot = s_do[buf];
+    // A operands: rows of Q (role 0) or dO (role 1); transposed dO (role 0) or Q (role 1)
+    const uint8_t* arow = role == 0 ? qt : dot;
+    const uint8_t* atr = role == 0 ? dot : qt;
     const int q0 = int(cur >> 1) * 64;
-    const bool partial = !(cur & 1u);
 
+    // S (role 0) or dP (role 1) for the two 32-query halves; register r of
+    // x[qb] holds query 32 qb + 16 (r / 8) + 8 hf + r % 8 of this lane's key
+    f32x16 x[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      f32x16 s = f32x16{}, dp = f32x16{};
+    for (int st = 0; st < DS; ++st) {
 #pragma unroll
-      for (int st = 0; st < DS; ++st) {
-        const int off = raddr[st] + qb * 32 * TL::ROWB;
-        const u32x4 aq = *reinterpret_cast<const u32x4*>(qt + off);
-        const u32x4 ao = *reinterpret_cast<const u32x4*>(dot + off);
-        s = mfma32x32x16<E>(aq, kf[st], s);
-        dp = mfma32x32x16<E>(ao, vf[st], dp);
+      for (int qb = 0; qb < 2; ++qb) {
+        const u32x4 ar = *reinterpret_cast<const u32x4*>(arow + raddr[st] + qb * 32 * TL::ROWB);
+        x[qb] = mfma32x32x16<E>(ar, bf[st], x[qb]);
       }
-      // register r holds query 32 qb + 16 (r / 8) + 8 hf + r % 8 of this lane's key
-      if (partial) {  // wave-uniform: evaluate the mask on this 32 x 32 block
+    }
+    u32x4 bop[2][2];  // packed P (role 0) or dS (role 1): B operand of k-step 2 qb + t
+    if (role == 0) {
+      if (!(cur & 1u)) {  // PARTIAL tile
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int ql = 32 * qb + 16 * t + 8 * hf;
+            const u32x4 c0 = *reinterpret_cast<const u32x4*>(&s_code[buf][ql]);
+            const u32x4 c1 = *reinterpret_cast<const u32x4*>(&s_code[buf][ql + 4]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const uint32_t qc = j < 4 ? c0[j] : c1[j - 4];
+              if (!allow(qc, kcode, q0 + ql + j, krow)) x[qb][8 * t + j] = NEG_INF;
+            }
+          }
+      }
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const int ql = 32 * qb + 16 * t + 8 * hf;
-          const u32x4 c0 = *reinterpret_cast<const u32x4*>(&s_code[buf][ql]);
-          const u32x4 c1 = *reinterpret_cast<const u32x4*>(&s_code[buf][ql + 4]);
+          const f32x4 l0 = *reinterpret_cast<const f32x4*>(&s_lse[buf][ql]);
+          const f32x4 l1 = *reinterpret_cast<const f32x4*>(&s_lse[buf][ql + 4]);
+          float p[8];
 #pragma unroll
-          for (int x = 0; x < 8; ++x) {
-            const uint32_t qc = x < 4 ? c0[x] : c1[x - 4];
-            if (!allow(qc, kcode, q0 + ql + x, krow)) s[8 * t + x] = NEG_INF;
+          for (int j = 0; j < 8; ++j) {
+            p[j] = fast_exp2(__builtin_fmaf(x[qb][8 * t + j], sl2, -(j < 4 ? l0[j] : l1[j - 4])));
+            xp[(16 * qb + 8 * t + j) * 64] = p[j];
           }
+          bop[qb][t] = u32x4{pack2<E>(p[0], p[1]), pack2<E>(p[2], p[3]), pack2<E>(p[4], p[5]),
+                             pack2<E>(p[6], p[7])};
         }
-      }
-      u32x4 pb[2], dsb[2];
+    }
+    __syncthreads();  // P of this tile visible to the dS waves
+    if (role == 1) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int ql = 32 * qb + 16 * t + 8 * hf;
-        const f32x4 l0 = *reinterpret_cast<const f32x4*>(&s_lse[buf][ql]);
-        const f32x4 l1 = *reinterpret_cast<const f32x4*>(&s_lse[buf][ql + 4]);
-        const f32x4 d0 = *reinterpret_cast<const f32x4*>(&s_delta[buf][ql]);
-        const f32x4 d1 = *reinterpret_cast<const f32x4*>(&s_delta[buf][ql + 4]);
-        float p[8], ds[8];
+      for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-        for (int x = 0; x < 8; ++x) {
-          const float lx = x < 4 ? l0[x] : l1[x - 4];
-          const float dx = x < 4 ? d0[x] : d1[x - 4];
-          p[x] = fast_exp2(__builtin_fmaf(s[8 * t + x], sl2, -lx));
-          ds[x] = p[x] * (dp[8 * t + x] - dx);
+        for (int t = 0; t < 2; ++t) {
+          const int ql = 32 * qb + 16 * t + 8 * hf;
+          const f32x4 d0 = *reinterpret_cast<const f32x4*>(&s_delta[buf][ql]);
+          const f32x4 d1 = *reinterpret_cast<const f32x4*>(&s_delta[buf][ql + 4]);
+          float ds[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float p = xp[(16 * qb + 8 * t + j) * 64];
+            ds[j] = p * (x[qb][8 * t + j] - (j < 4 ? d0[j] : d1[j - 4]));
+          }
+          bop[qb][t] = u32x4{pack2<E>(ds[0], ds[1]), pack2<E>(ds[2], ds[3]), pack2<E>(ds[4], ds[5]),
+                             pack2<E>(ds[6], ds[7])};
         }
-        pb[t] = u32x4{pack2<E>(p[0], p[1]), pack2<E>(p[2], p[3]), pack2<E>(p[4], p[5]), pack2<E>(p[6], p[7])};
-        dsb[t] = u32x4{pack2<E>(ds[0], ds[1]), pack2<E>(ds[2], ds[3]), pack2<E>(ds[4], ds[5]),
-                       pack2<E>(ds[6], ds[7])};
-      }
-      // dV^T += dO^T P,  dK^T += Q^T dS   (k-steps 2 qb + t over the 64 queries)
+    }
+    // acc^T += A^T bop over the 64 queries (k-steps 2 qb + t)
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
           const int off = (2 * qb + t) * 16 * TL::ROWB;
-          const u32x2 olo = ds_read_tr16(dot + taddr[db][0] + off);
-          const u32x2 ohi = ds_read_tr16(dot + taddr[db][1] + off);
-          const u32x2 qlo = ds_read_tr16(qt + taddr[db][0] + off);
-          const u32x2 qhi = ds_read_tr16(qt + taddr[db][1] + off);
-          dv[db] = mfma32x32x16<E>(u32x4{olo[0], olo[1], ohi[0], ohi[1]}, pb[t], dv[db]);
-          dk[db] = mfma32x32x16<E>(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]}, dsb[t], dk[db]);
+          const u32x2 lo = ds_read_tr16(atr + taddr[db][0] + off);
+          const u32x2 hi = ds_read_tr16(atr + taddr[db][1] + off);
+          acc[db] = mfma32x32x16<E>(u32x4{lo[0], lo[1], hi[0], hi[1]}, bop[qb][t], acc[db]);
         }
-      }
-    }
   }
 
   if (kvalid) {
-    uint16_t* gk = static_cast<uint16_t*>(a.dk) + b * a.dk_strides[0] + h * a.dk_strides[1] + krow * a.dk_strides[2];
-    uint16_t* gv = static_cast<uint16_t*>(a.dv) + b * a.dv_strides[0] + h * a.dv_strides[1] + krow * a.dv_strides[2];
-    store_rows_T<E, D>(gk, dk, a.sm_scale, hf);
-    store_rows_T<E, D>(gv, dv, 1.f, hf);
+    uint16_t* g = role == 0
+        ? static_cast<uint16_t*>(a.dv) + b * a.dv_strides[0] + h * a.dv_strides[1] + krow * a.dv_strides[2]
+        : static_cast<uint16_t*>(a.dk) + b * a.dk_strides[0] + h * a.dk_strides[1] + krow * a.dk_strides[2];
+    store_rows_T<E, D>(g, acc, role == 0 ? 1.f : a.sm_scale, hf);
   }
 }
 
@@ -416,7 +446,7 @@ template <class E, int D>
 static void launch_dkdv_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dkdv_blocks;
-  hipLaunchKernelGGL((k_dkdv<E, D>), dim3(grid), dim3(256), 0, st, a,
+  hipLaunchKernelGGL((k_dkdv<E, D>), dim3(grid), dim3(512), 0, st, a,
                      reinterpret_cast<const uint32_t*>(plan + L.codes),
                      reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
                      reinterpret_cast<const int32_t*>(plan + L.dkdv_count), L.nT, L.n_dkdv_blocks);

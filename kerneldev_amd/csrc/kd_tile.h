@@ -33,14 +33,15 @@ KD_DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
-template <int D>
+template <int D, int NW = 4>  // NW: waves that share the copy of one tile
 struct Tile {
   static constexpr int ROWS = 64;
   static constexpr int ROWB = D * 2;            // bytes per row
   static constexpr int CPR = D / 8;             // 16-byte chunks per row
   static constexpr int BYTES = ROWS * ROWB;     // 16 KiB (D = 128) or 8 KiB (D = 64)
   static constexpr int LOADS = BYTES / 1024;    // 1 KiB per wave-wide buffer_load_dwordx4
-  static constexpr int LOADS_PER_WAVE = LOADS / 4;
+  static constexpr int LOADS_PER_WAVE = LOADS / NW;
+  static_assert(LOADS % NW == 0, "tile copy must split evenly over the waves");
 
   KD_DEV static int swz(int r) {
     if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
