@@ -104,9 +104,9 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
   const int T = a.T, H = a.H;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = work / nQB;
+  const int hb = work / nQB;  // head-major: each XCD's range holds every batch row of its heads
   const int qblock = nQB - 1 - (work % nQB);
-  const int b = bh / H, h = bh % H;
+  const int b = hb % a.B, h = hb / a.B, bh = b * H + h;
 
   const uint16_t* qg = static_cast<const uint16_t*>(a.q) + b * a.q_strides[0] + h * a.q_strides[1];
   const uint16_t* dog = static_cast<const uint16_t*>(a.dout) + b * a.do_strides[0] + h * a.do_strides[1];
@@ -264,9 +264,9 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   const int pair = wave & 3, role = wave >> 2;
   const int T = a.T, H = a.H;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = work / nKB;
+  const int hb = work / nKB;  // head-major: each XCD's range holds every batch row of its heads
   const int kblock = work % nKB;
-  const int b = bh / H, h = bh % H;
+  const int b = hb % a.B, h = hb / a.B, bh = b * H + h;
 
   const uint16_t* qg = static_cast<const uint16_t*>(a.q) + b * a.q_strides[0] + h * a.q_strides[1];
   const uint16_t* dog = static_cast<const uint16_t*>(a.dout) + b * a.do_strides[0] + h * a.do_strides[1];

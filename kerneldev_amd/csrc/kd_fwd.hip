@@ -13,14 +13,17 @@
 // so a lane owns one query column: the softmax statistics are per-lane
 // scalars plus one permlane32 exchange, and P never leaves registers thanks to
 // the sigma() row permutation of the K operand.  K and V tiles are copied
-// global -> LDS by buffer_load ... lds (double buffered: the next tile's copy
-// runs under the current tile's math) and V is transposed by
-// ds_read_b64_tr_b16 on the way into the MFMA.  Only non-empty key tiles are
+// global -> LDS by buffer_load ... lds and V is transposed by ds_read_b64_tr_b16
+// on the way into the MFMA.  The loop is software pipelined: while the
+// softmax of tile e runs on the VALU, the MFMAs already compute S of tile
+// e+1 (K tiles are loaded one step ahead of V tiles, both double buffered).  Only non-empty key tiles are
 // visited (plan list); FULL tiles skip the mask, PARTIAL tiles evaluate it.
 //
-// The running max is rescaled lazily: the accumulators are only rescaled
-// when a row's max grows by more than 2^8 (P is then <= 256, harmless in
-// fp32/bf16), which removes the per-step O *= alpha of the textbook loop.
+// The running max is rescaled lazily, per lane: the accumulators are only
+// rescaled when a row's max grows by more than 2^8 (P is then <= 256,
+// harmless in fp32/bf16), which removes the per-step O *= alpha of the
+// textbook loop.  PARTIAL tiles are masked with the table form of the rule
+// (kd_common.h: qmask / mask_score), a handful of VALU ops per score.
 // The row sum l adds up the ROUNDED P that enters P V, so O is an exact
 // convex combination of V rows up to the final rounding even when one key
 // dominates the row.
@@ -43,9 +46,9 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
   const int T = a.T, H = a.H;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = work / nQB;
+  const int hb = work / nQB;  // head-major: each XCD's range holds every batch row of its heads
   const int qblock = nQB - 1 - (work % nQB);  // heaviest (latest) q-blocks first
-  const int b = bh / H, h = bh % H;
+  const int b = hb % a.B, h = hb / a.B, bh = b * H + h;
 
   const uint16_t* qg = static_cast<const uint16_t*>(a.q) + b * a.q_strides[0] + h * a.q_strides[1];
   const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_strides[0] + h * a.k_strides[1];
@@ -72,12 +75,18 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
   uint32_t koff[NL], voff[NL];
   TL::load_offsets(wave, lane, krb, koff);
   TL::load_offsets(wave, lane, vrb, voff);
-  auto load_tile = [&](int kt, int buf) {
-    const uint32_t k0 = uint32_t(kt) * 64u;
-    TL::load(rs_k, k0 * krb, koff, s_k[buf], wave);
-    TL::load(rs_v, k0 * vrb, voff, s_v[buf], wave);
+  // K tiles run one step ahead of V tiles (S of tile e+1 is computed while
+  // tile e is softmaxed), so they are loaded separately; the key codes of a
+  // tile travel with its V tile.
+  auto load_k = [&](int e) {
+    const uint32_t k0 = uint32_t(ent[e] >> 1) * 64u;
+    TL::load(rs_k, k0 * krb, koff, s_k[e & 1], wave);
+  };
+  auto load_v = [&](int e) {
+    const uint32_t k0 = uint32_t(ent[e] >> 1) * 64u;
+    TL::load(rs_v, k0 * vrb, voff, s_v[e & 1], wave);
     if (wave == 0)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_t*)&s_code[buf][0], 4, (k0 + lane) * 4u, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_t*)&s_code[e & 1][0], 4, (k0 + lane) * 4u, 0, 0, 0);
   };
 
   // ---- LDS read addresses (bytes within a tile) ----
@@ -100,6 +109,18 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
         vaddr[db][half] = TL::at(r, chunk) + 8 * (i & 1);
       }
   }
+  // S^T = K Q^T for one tile (two 32-key halves, independent chains)
+  auto scores = [&](const uint8_t* kt, f32x16 (&s)[2]) {
+    s[0] = f32x16{};
+    s[1] = f32x16{};
+#pragma unroll
+    for (int st = 0; st < DS; ++st)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const u32x4 ak = *reinterpret_cast<const u32x4*>(kt + kaddr[st] + kb * 32 * TL::ROWB);
+        s[kb] = mfma32x32x16<E>(ak, qf[st], s[kb]);
+      }
+  };
 
   const float sl2 = a.sm_scale * 1.4426950408889634f;
   const float NEG_INF = -__builtin_inff();
@@ -107,32 +128,33 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
   f32x16 o[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) o[db] = f32x16{};
+  const MaskTab mt = qmask(qcode);
+  const int i_lo = qblock * 128 + wave * 32;  // this wave's query rows: i_lo .. i_lo + 31
 
-  if (n > 0) load_tile(int(ent[0] >> 1), 0);
+  f32x16 s[2] = {f32x16{}, f32x16{}};
+  if (n > 0) {
+    load_k(0);
+    load_v(0);
+    if (n > 1) load_k(1);
+    wait_vmem();
+    __syncthreads();
+    scores(s_k[0], s);
+  }
 
   for (int e = 0; e < n; ++e) {
     const int buf = e & 1;
     const uint32_t cur = ent[e];
     wait_vmem();
-    __syncthreads();  // tile e landed for every wave; buffer buf^1 free again
-    if (e + 1 < n) load_tile(int(ent[e + 1] >> 1), buf ^ 1);
-    const uint8_t* kt = s_k[buf];
-    const uint8_t* vt = s_v[buf];
+    __syncthreads();  // V(e) and K(e+1) landed; every wave is done with K(e) and V(e-1)
+    if (e + 1 < n) load_v(e + 1);
+    if (e + 2 < n) load_k(e + 2);
+    const int k0 = int(cur >> 1) * 64;
 
-    // S^T = K Q^T for two 32-key blocks
-    f32x16 s[2] = {f32x16{}, f32x16{}};
-#pragma unroll
-    for (int st = 0; st < DS; ++st) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {  // two independent accumulation chains
-        const u32x4 ak = *reinterpret_cast<const u32x4*>(kt + kaddr[st] + kb * 32 * TL::ROWB);
-        s[kb] = mfma32x32x16<E>(ak, qf[st], s[kb]);
-      }
-    }
-    if (!(cur & 1u)) {  // PARTIAL tile: evaluate the mask per element
-      const int k0 = int(cur >> 1) * 64;
+    if (!(cur & 1u)) {  // PARTIAL tile: register r of s[kb] holds key k0 + 32 kb + 16 (r / 8) + 8 hf + r % 8
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
+        const int j0 = k0 + 32 * kb;
+        const bool below = j0 + 31 <= i_lo, above = j0 > i_lo + 31;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const int jl = 32 * kb + 16 * t + 8 * hf;
@@ -141,12 +163,14 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
 #pragma unroll
           for (int x = 0; x < 8; ++x) {
             const uint32_t kc = x < 4 ? c0[x] : c1[x - 4];
-            if (!allow(qcode, kc, qrow, k0 + jl + x)) s[kb][8 * t + x] = NEG_INF;
+            uint32_t tbl = below ? mt.hi : mt.lo;
+            if (!below && !above) tbl = (k0 + jl + x <= qrow) ? mt.hi : mt.lo;
+            s[kb][8 * t + x] = mask_score(s[kb][8 * t + x], tbl, kc, kc, mt.rsh);
           }
         }
       }
     }
-    // tile row max (rows = this lane's query)
+    // running max of this lane's row; rescale only when it grows by > 2^8
     float mx = NEG_INF;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -154,8 +178,7 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
     mx = xhalf_max(mx);
     const float m_new = fmaxf(m_ref, mx);
-    const bool grow = (m_new - m_ref) * sl2 > 8.f;  // false for -inf - -inf (NaN)
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+    if ((m_new - m_ref) * sl2 > 8.f) {  // false for -inf - -inf (NaN); per lane
       const float alpha = (m_ref == NEG_INF) ? 0.f : fast_exp2((m_ref - m_new) * sl2);
       m_ref = m_new;
       l0 *= alpha;
@@ -164,6 +187,9 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
       for (int db = 0; db < DB; ++db) o[db] *= alpha;
     }
     const float ms = (m_ref == NEG_INF) ? 0.f : m_ref * sl2;
+
+    // softmax of tile e (VALU) alongside S of tile e+1 (MFMA; computed from
+    // the other K buffer even past the last tile, where it is simply unused)
     u32x4 pk[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -180,15 +206,16 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
         l1 = acc_pair<E>(pk[kb][t][3], l1);
       }
     }
-    // O^T += V^T P^T
+    scores(s_k[buf ^ 1], s);
+    // O^T += V^T P^T for tile e
+    const uint8_t* vt = s_v[buf];
 #pragma unroll
     for (int t4 = 0; t4 < 4; ++t4) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         const u32x2 lo = ds_read_tr16(vt + vaddr[db][0] + t4 * 16 * TL::ROWB);
         const u32x2 hi = ds_read_tr16(vt + vaddr[db][1] + t4 * 16 * TL::ROWB);
-        const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
-        o[db] = mfma32x32x16<E>(av, pk[t4 >> 1][t4 & 1], o[db]);
+        o[db] = mfma32x32x16<E>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[t4 >> 1][t4 & 1], o[db]);
       }
     }
   }

@@ -34,7 +34,10 @@ int launch_dkdv(const AttnArgs& a, const uint8_t* plan, hipStream_t st);
 
 // Linear workgroup id -> work index so that each XCD (workgroups are dealt
 // round-robin over the 8 XCDs) receives one contiguous range of work items,
-// i.e. the q- or k-blocks of the same (b, h) share that XCD's L2.
+// i.e. the q- or k-blocks of the same (b, h) share that XCD's L2.  The
+// kernels order work head-major (h, then b, then block), so that with H a
+// multiple of 8 every XCD gets the same mix of batch rows (whose masks, and
+// so whose amounts of work, differ).
 KD_DEV int xcd_remap(int wg, int n) {
   constexpr int NX = 8;
   const int per = n / NX;
