@@ -5,8 +5,10 @@
 
 A *step* is one pass of the attention hot path over one synthetic batch with
 every input already resident in HBM: tile classifier (plan), forward, Delta,
-dQ and dK/dV -- the same five launches ``flash_attention()`` followed by
-``backward()`` issues, called through the C ABI on preallocated buffers.
+dQ and dK/dV -- the launches ``flash_attention()`` followed by ``backward()``
+issues, called through the C ABI on preallocated buffers.  Config 4 (the
+metric's workload) includes its Hadamard incoherent processing: Q and K are
+rotated before the forward and dQ, dK rotated back after the backward.
 The timed region is bracketed by ``torch.cuda.synchronize()``; HIP events on
 the launch stream sit between the five kernels of every timed step, so each
 kernel's average duration is measured live.
@@ -56,6 +58,8 @@ def parse():
     ap.add_argument("--config", type=int, default=4, choices=(2, 3, 4),
                     help="BASELINE config to time (default 4, the metric's workload)")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-hadamard", action="store_true",
+                    help="config 4 without the Hadamard rotation of Q and K")
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU baseline leg (profiling runs)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -77,16 +81,25 @@ def cpu_threads() -> int:
 class Step:
     """Preallocated buffers and the five launches of one fwd+bwd pass."""
 
-    def __init__(self, inp, dev):
+    def __init__(self, inp, dev, hadamard=False):
         import torch
 
-        from kerneldev_amd import _lib
+        from kerneldev_amd import _lib, generate_hadamard_signs
         from kerneldev_amd.attention import _attn_args, _dtype_code, _strides3, mask_mode
 
         self.torch, self.lib, self.dev = torch, _lib.load(), dev
         self._check = _lib.check
         q, k, v, do = (inp[x].to(dev) for x in ("q", "k", "v", "do"))
         B, H, T, D = q.shape
+        self.hadamard = hadamard
+        if hadamard:
+            # Q' = Q R, K' = K R before attention; dQ = dQ' R^T, dK = dK' R^T after
+            self.signs = generate_hadamard_signs(D, 0, device=dev)
+            self.q_in, self.k_in = q, k
+            q, k = torch.empty_like(q), torch.empty_like(k)
+            self.dq_in, self.dk_in = torch.empty_like(q), torch.empty_like(k)
+            self.rot = [self._rot_args(_lib, _dtype_code, _strides3, src, dst, inverse)
+                        for src, dst, inverse in ((self.q_in, q, 0), (self.k_in, k, 0))]
         self.shape = (B, H, T, D)
         self.meta = {n: (inp[n].to(dev) if inp.get(n) is not None else None)
                      for n in ("in_span", "span_id", "is_prefix")}
@@ -95,6 +108,7 @@ class Step:
         self.o = torch.empty_like(q)
         self.lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
         self.delta = torch.empty((2, B, H, T), dtype=torch.float32, device=dev)
+        self.o_lo = torch.empty_like(q)  # O's rounding residual, kept for Delta (training step)
         self.dq, self.dk, self.dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
         self.inputs = (q, k, v, do)
         a = _attn_args(q, k, v, D ** -0.5)
@@ -105,6 +119,7 @@ class Step:
         a.dq, a.dk, a.dv = self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr()
         a.dq_strides, a.dk_strides, a.dv_strides = _strides3(self.dq), _strides3(self.dk), _strides3(self.dv)
         a.delta = self.delta.data_ptr()
+        a.o_lo = self.o_lo.data_ptr()
         self.args = a
         m = _lib.MetaArgs()
         m.B, m.T, m.D, m.mode = B, T, D, self.mode
@@ -122,19 +137,36 @@ class Step:
             m.span_id_strides[0], m.span_id_strides[1] = t.stride()
             m.span_id_dtype = _lib.KD_I64 if t.dtype == torch.int64 else _lib.KD_I32
         self.margs = m
+        if hadamard:
+            self.unrot = [self._rot_args(_lib, _dtype_code, _strides3, src, dst, 1)
+                          for src, dst in ((self.dq, self.dq_in), (self.dk, self.dk_in))]
         self.stream = torch.cuda.current_stream(dev)
         self.sptr = ctypes.c_void_p(self.stream.cuda_stream)
         self.pptr = ctypes.c_void_p(self.plan.data_ptr())
 
+    def _rot_args(self, _lib, _dtype_code, _strides3, src, dst, inverse):
+        r = _lib.RotArgs()
+        r.x, r.x_strides, r.y, r.y_strides = src.data_ptr(), _strides3(src), dst.data_ptr(), _strides3(dst)
+        r.signs = self.signs.data_ptr()
+        r.B, r.H, r.T, r.D = src.shape
+        r.dtype, r.inverse = _dtype_code(src.dtype), inverse
+        return r
+
     def launches(self):
         L, a, ck = self.lib, ctypes.byref(self.args), self._check
-        return (
-            ("plan", lambda: ck(L.kd_plan_build(ctypes.byref(self.margs), self.pptr, self.sptr), "plan")),
+        out = [("plan", lambda: ck(L.kd_plan_build(ctypes.byref(self.margs), self.pptr, self.sptr), "plan"))]
+        if self.hadamard:
+            out.append(("rot_qk", lambda: [ck(L.kd_hadamard(ctypes.byref(r), self.sptr), "rot") for r in self.rot]))
+        out += [
             ("fwd", lambda: ck(L.kd_attn_fwd(a, self.pptr, self.sptr), "fwd")),
             ("delta", lambda: ck(L.kd_attn_bwd_delta(a, self.sptr), "delta")),
             ("dq", lambda: ck(L.kd_attn_bwd_dq(a, self.pptr, self.sptr), "dq")),
             ("dkdv", lambda: ck(L.kd_attn_bwd_dkdv(a, self.pptr, self.sptr), "dkdv")),
-        )
+        ]
+        if self.hadamard:
+            out.append(("unrot_dqdk",
+                        lambda: [ck(L.kd_hadamard(ctypes.byref(r), self.sptr), "unrot") for r in self.unrot]))
+        return tuple(out)
 
     def run(self, events=None):
         for idx, (_, fn) in enumerate(self.launches()):
@@ -208,7 +240,8 @@ def main():
     dev = torch.device("cuda:0")
     inp = config_inputs(args.config, seed=args.seed)
     B, H, T, D = inp["q"].shape
-    st = Step(inp, dev)
+    hadamard = args.config == 4 and not args.no_hadamard
+    st = Step(inp, dev, hadamard=hadamard)
     if args.calibrate_copy_mib > 0:
         n = args.calibrate_copy_mib << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -271,7 +304,7 @@ def main():
             "frac_of_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
             "kernel_ms": {n: round(x, 4) for n, x in per_kernel.items()},
             "event_ms_per_step": round(event_ms, 4),
-            "hadamard": False,
+            "hadamard": hadamard,
         },
         "roofline": roofline,
         "cpu_baseline": cpu,

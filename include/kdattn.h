@@ -78,10 +78,26 @@ typedef struct kd_attn_args {
   int64_t dq_strides[3], dk_strides[3], dv_strides[3];
   float *delta;                 /* fp32 workspace of 2 * B*H*T (bwd): Delta [B, H, T],
                                    then LSE with -inf replaced by +inf [B, H, T] */
+  void *o_lo;                   /* optional contiguous [B, H, T, D], dtype of o: the
+                                   forward writes O_fp32 - O there, the backward's Delta
+                                   reads it; NULL to skip */
   int32_t B, H, T, D;
   int32_t dtype;                /* KD_BF16 / KD_F16 */
   float sm_scale;
 } kd_attn_args;
+
+/* Walsh-Hadamard rotation of [B, H, T, D] rows (incoherent processing). */
+typedef struct kd_rot_args {
+  const void *x;                /* [B, H, T, D] input */
+  int64_t x_strides[3];
+  void *y;                      /* [B, H, T, D] output (may not alias x) */
+  int64_t y_strides[3];
+  const float *signs;           /* [D] of +1 / -1 */
+  float *amax;                  /* optional [B, H]: max |y| is atomically max-ed in; zero it first */
+  int32_t B, H, T, D;
+  int32_t dtype;                /* KD_BF16 / KD_F16 */
+  int32_t inverse;              /* 0: y = x R;  1: y = x R^T */
+} kd_rot_args;
 
 /* Library version (major*10000 + minor*100 + patch). */
 int kd_version(void);
@@ -91,6 +107,7 @@ const char *kd_last_error_string(void);
 
 /* sizeof(kd_meta_args), sizeof(kd_attn_args): lets bindings check layouts. */
 void kd_struct_sizes(size_t *meta, size_t *attn);
+void kd_struct_sizes2(size_t *rot);
 
 /* Workspace ("plan") bytes for B sequences of length T at head dim D, and
  * the byte offsets of its sections (codes, class map, per-tile allowed
@@ -135,6 +152,12 @@ int kd_attn_bwd(const kd_attn_args *a, const void *plan, void *stream);
  * (original_kernel.py:519-545). */
 int kd_mask_dense(const void *plan, int32_t B, int32_t H, int32_t T, int32_t D, uint8_t *out,
                   const int64_t *strides, void *stream);
+
+/* y = x R with R = diag(signs) H_D / sqrt(D) (or x R^T when inverse), per
+ * row, in a fixed fp32 evaluation order (bit-reproducible); optionally
+ * max |y| per (b, h) into amax.  The reference only names this operation
+ * (README.md:68-71, :77: generate_hadamard_signs / hadamard_transform). */
+int kd_hadamard(const kd_rot_args *a, void *stream);
 
 #ifdef __cplusplus
 }

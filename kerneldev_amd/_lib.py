@@ -49,9 +49,21 @@ class AttnArgs(ctypes.Structure):
         ("dout", c_void_p), ("do_strides", I64x3),
         ("dq", c_void_p), ("dk", c_void_p), ("dv", c_void_p),
         ("dq_strides", I64x3), ("dk_strides", I64x3), ("dv_strides", I64x3),
-        ("delta", c_void_p),
+        ("delta", c_void_p), ("o_lo", c_void_p),
         ("B", c_int32), ("H", c_int32), ("T", c_int32), ("D", c_int32),
         ("dtype", c_int32), ("sm_scale", c_float),
+    ]
+
+
+class RotArgs(ctypes.Structure):
+    """Mirror of ``kd_rot_args``."""
+
+    _fields_ = [
+        ("x", c_void_p), ("x_strides", I64x3),
+        ("y", c_void_p), ("y_strides", I64x3),
+        ("signs", c_void_p), ("amax", c_void_p),
+        ("B", c_int32), ("H", c_int32), ("T", c_int32), ("D", c_int32),
+        ("dtype", c_int32), ("inverse", c_int32),
     ]
 
 
@@ -60,6 +72,8 @@ SIGNATURES = {
     "kd_version": (c_int, []),
     "kd_last_error_string": (c_char_p, []),
     "kd_struct_sizes": (None, [POINTER(c_size_t), POINTER(c_size_t)]),
+    "kd_struct_sizes2": (None, [POINTER(c_size_t)]),
+    "kd_hadamard": (c_int, [POINTER(RotArgs), c_void_p]),
     "kd_plan_bytes": (c_int64, [c_int32, c_int32, c_int32]),
     "kd_plan_layout": (c_int, [c_int32, c_int32, c_int32, POINTER(c_int64)]),
     "kd_plan_build": (c_int, [POINTER(MetaArgs), c_void_p, c_void_p]),
@@ -95,10 +109,14 @@ def load():
         fn.argtypes = args
     ms, as_ = c_size_t(), c_size_t()
     lib.kd_struct_sizes(ctypes.byref(ms), ctypes.byref(as_))
-    if ms.value != ctypes.sizeof(MetaArgs) or as_.value != ctypes.sizeof(AttnArgs):
+    rs = c_size_t()
+    lib.kd_struct_sizes2(ctypes.byref(rs))
+    if (ms.value != ctypes.sizeof(MetaArgs) or as_.value != ctypes.sizeof(AttnArgs)
+            or rs.value != ctypes.sizeof(RotArgs)):
         raise ImportError(
-            f"struct layout mismatch: C meta={ms.value} attn={as_.value}, "
-            f"ctypes meta={ctypes.sizeof(MetaArgs)} attn={ctypes.sizeof(AttnArgs)}")
+            f"struct layout mismatch: C meta={ms.value} attn={as_.value} rot={rs.value}, "
+            f"ctypes meta={ctypes.sizeof(MetaArgs)} attn={ctypes.sizeof(AttnArgs)} "
+            f"rot={ctypes.sizeof(RotArgs)}")
     _lib = lib
     return lib
 

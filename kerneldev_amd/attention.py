@@ -101,30 +101,34 @@ def _attn_args(q, k, v, sm_scale) -> AttnArgs:
 @torch.library.custom_op("kdattn::fwd", mutates_args=(), device_types=("cuda",))
 def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tensor | None,
             in_span: torch.Tensor | None, span_id: torch.Tensor | None,
-            is_prefix: torch.Tensor | None, sm_scale: float, mode: int
-            ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+            is_prefix: torch.Tensor | None, sm_scale: float, mode: int, need_lo: bool
+            ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     B, H, T, D = q.shape
     plan = build_plan(B, T, D, q.device, mode, in_span, span_id, is_prefix, lens)
     o = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+    # rounding residual of O, kept for the backward's Delta (see kd_bwd.hip)
+    o_lo = torch.empty((B, H, T, D) if need_lo else (0,), dtype=q.dtype, device=q.device)
     a = _attn_args(q, k, v, sm_scale)
     a.o, a.o_strides = o.data_ptr(), _strides3(o)
     a.lse = lse.data_ptr()
+    a.o_lo = o_lo.data_ptr() if need_lo else None
     _lib.check(_lib.load().kd_attn_fwd(ctypes.byref(a), _ptr(plan), _stream(q.device)), "kd_attn_fwd")
-    return o, lse, plan
+    return o, lse, plan, o_lo
 
 
 @_fwd_op.register_fake
-def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode):
+def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo):
     B, H, T, D = q.shape
     return (torch.empty((B, H, T, D), dtype=q.dtype, device=q.device),
             torch.empty((B, H, T), dtype=torch.float32, device=q.device),
-            torch.empty(_lib.plan_bytes(B, T, D), dtype=torch.uint8, device=q.device))
+            torch.empty(_lib.plan_bytes(B, T, D), dtype=torch.uint8, device=q.device),
+            torch.empty((B, H, T, D) if need_lo else (0,), dtype=q.dtype, device=q.device))
 
 
 @torch.library.custom_op("kdattn::bwd", mutates_args=(), device_types=("cuda",))
 def _bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, lse: torch.Tensor,
-            do: torch.Tensor, plan: torch.Tensor, sm_scale: float
+            do: torch.Tensor, plan: torch.Tensor, sm_scale: float, o_lo: torch.Tensor
             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     B, H, T, D = q.shape
     do = _kernel_ready(do)
@@ -139,27 +143,28 @@ def _bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, 
     a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
     a.dq_strides, a.dk_strides, a.dv_strides = _strides3(dq), _strides3(dk), _strides3(dv)
     a.delta = delta.data_ptr()
+    a.o_lo = o_lo.data_ptr() if o_lo.numel() > 0 else None
     _lib.check(_lib.load().kd_attn_bwd(ctypes.byref(a), _ptr(plan), _stream(q.device)), "kd_attn_bwd")
     return dq, dk, dv
 
 
 @_bwd_op.register_fake
-def _bwd_fake(q, k, v, o, lse, do, plan, sm_scale):
+def _bwd_fake(q, k, v, o, lse, do, plan, sm_scale, o_lo):
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
 def _setup_context(ctx, inputs, output):
-    q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode = inputs
-    o, lse, plan = output
-    ctx.save_for_backward(q, k, v, o, lse, plan)
+    q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo = inputs
+    o, lse, plan, o_lo = output
+    ctx.save_for_backward(q, k, v, o, lse, plan, o_lo)
     ctx.sm_scale = sm_scale
 
 
-def _backward(ctx, do, dlse, dplan):
+def _backward(ctx, do, dlse, dplan, do_lo):
     # dlse is ignored, as in original_kernel.py:1965-1992
-    q, k, v, o, lse, plan = ctx.saved_tensors
-    dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, ctx.sm_scale)
-    return dq, dk, dv, None, None, None, None, None, None
+    q, k, v, o, lse, plan, o_lo = ctx.saved_tensors
+    dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, ctx.sm_scale, o_lo)
+    return dq, dk, dv, None, None, None, None, None, None, None
 
 
 _fwd_op.register_autograd(_backward, setup_context=_setup_context)
@@ -241,8 +246,6 @@ def flash_attention(
         raise ValueError("q, k and v must be on the same device")
     if qk_dtype != "bf16":
         raise NotImplementedError("fp8 QK^T path is not built yet")
-    if hadamard:
-        raise NotImplementedError("Hadamard path is not built yet")
 
     if sm_scale is None:
         sm_scale = D ** -0.5  # original_kernel.py:2145-2147
@@ -261,9 +264,17 @@ def flash_attention(
         q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
     elif in_dtype not in (torch.bfloat16, torch.float16):
         raise ValueError(f"unsupported dtype {in_dtype}")
+    if hadamard:
+        # (Q R)(K R)^T = Q K^T with R = diag(s) H_d / sqrt(d); autograd maps
+        # dQ' and dK' back through R^T (hadamard.py)
+        from .hadamard import generate_hadamard_signs, hadamard_transform
+
+        signs = generate_hadamard_signs(D, hadamard_seed, device=device)
+        q, k = hadamard_transform(q, signs), hadamard_transform(k, signs)
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
 
-    o, lse, plan = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode))
+    need_lo = torch.is_grad_enabled() and any(x.requires_grad for x in (q, k, v))
+    o, lse, plan, _ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode), need_lo)
     if in_dtype == torch.float32:
         o = o.to(torch.float32)
 

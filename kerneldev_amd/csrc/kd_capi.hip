@@ -80,6 +80,24 @@ void kd_struct_sizes(size_t* meta, size_t* attn) {
   if (attn) *attn = sizeof(kd_attn_args);
 }
 
+void kd_struct_sizes2(size_t* rot) {
+  if (rot) *rot = sizeof(kd_rot_args);
+}
+
+int kd_hadamard(const kd_rot_args* a, void* stream) {
+  if (a == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
+  if (a->B < 1 || a->H < 1 || a->T < 1) return fail(KD_ERR_INVALID, "B, H and T must be >= 1");
+  if (a->D != 64 && a->D != 128) return fail(KD_ERR_UNSUPPORTED, "head dim must be 64 or 128");
+  if (a->dtype != KD_BF16 && a->dtype != KD_F16) return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16 or fp16");
+  if (a->signs == nullptr) return fail(KD_ERR_INVALID, "signs is NULL");
+  int r;
+  if ((r = check_tensor(a->x, a->x_strides, "x", a->T, a->D)) || (r = check_tensor(a->y, a->y_strides, "y", a->T, a->D)))
+    return r;
+  if (a->x == a->y) return fail(KD_ERR_INVALID, "x and y must not alias");
+  r = kd::launch_hadamard(*a, as_stream(stream));
+  return r ? fail(r, "kernel launch failed (hadamard)") : KD_OK;
+}
+
 int64_t kd_plan_bytes(int32_t B, int32_t T, int32_t D) {
   if (B < 1 || T < 1) return -1;
   return int64_t(kd::plan_layout(B, T, D).total);
@@ -119,6 +137,7 @@ int kd_attn_fwd(const kd_attn_args* a, const void* plan, void* stream) {
   if ((r = check_tensor(a->q, a->q_strides, "q", a->T, a->D)) || (r = check_tensor(a->k, a->k_strides, "k", a->T, a->D)) ||
       (r = check_tensor(a->v, a->v_strides, "v", a->T, a->D)) || (r = check_tensor(a->o, a->o_strides, "o", a->T, a->D)))
     return r;
+  if (a->o_lo != nullptr && !aligned16(a->o_lo)) return fail(KD_ERR_INVALID, "o_lo must be 16-byte aligned");
   r = kd::launch_fwd(*a, static_cast<const uint8_t*>(plan), as_stream(stream));
   return r ? fail(r, "kernel launch failed (forward)") : KD_OK;
 }
@@ -129,6 +148,7 @@ int kd_attn_bwd_delta(const kd_attn_args* a, void* stream) {
   if ((r = check_tensor(a->o, a->o_strides, "o", a->T, a->D)) || (r = check_tensor(a->dout, a->do_strides, "dout", a->T, a->D)))
     return r;
   if (a->delta == nullptr || a->lse == nullptr) return fail(KD_ERR_INVALID, "delta and lse are required");
+  if (a->o_lo != nullptr && !aligned16(a->o_lo)) return fail(KD_ERR_INVALID, "o_lo must be 16-byte aligned");
   r = kd::launch_delta(*a, as_stream(stream));
   return r ? fail(r, "kernel launch failed (delta)") : KD_OK;
 }

@@ -24,9 +24,9 @@
 // harmless in fp32/bf16), which removes the per-step O *= alpha of the
 // textbook loop.  PARTIAL tiles are masked with the table form of the rule
 // (kd_common.h: qmask / mask_score), a handful of VALU ops per score.
-// The row sum l adds up the ROUNDED P that enters P V, so O is an exact
-// convex combination of V rows up to the final rounding even when one key
-// dominates the row.
+// O is normalised by the sum of the ROUNDED P that enters P V, so it is an
+// exact convex combination of V rows up to the final rounding even when one
+// key dominates the row; LSE uses the exact fp32 sum.
 #include "kd_tile.h"
 
 namespace kd {
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
 
   const float sl2 = a.sm_scale * 1.4426950408889634f;
   const float NEG_INF = -__builtin_inff();
-  float m_ref = NEG_INF, l0 = 0.f, l1 = 0.f;
+  float m_ref = NEG_INF, l0 = 0.f, l1 = 0.f, le0 = 0.f, le1 = 0.f;
   f32x16 o[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) o[db] = f32x16{};
@@ -183,6 +183,8 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
       m_ref = m_new;
       l0 *= alpha;
       l1 *= alpha;
+      le0 *= alpha;
+      le1 *= alpha;
 #pragma unroll
       for (int db = 0; db < DB; ++db) o[db] *= alpha;
     }
@@ -196,6 +198,11 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
       float p[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(s[kb][r], sl2, -ms));
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        le0 += p[r];
+        le1 += p[r + 1];
+      }
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         pk[kb][t] = u32x4{pack2<E>(p[8 * t + 0], p[8 * t + 1]), pack2<E>(p[8 * t + 2], p[8 * t + 3]),
@@ -221,22 +228,37 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
   }
 
   // ---- epilogue: normalise, store O and LSE ----
+  // O is normalised by the sum of the ROUNDED P that entered P V (exact
+  // convex weights); LSE by the exact fp32 sum, which is what the backward's
+  // recomputed P = exp2(S c - LSE) must sum to
   const float l_tot = xhalf_sum(l0 + l1);
+  const float l_exact = xhalf_sum(le0 + le1);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (qvalid) {
     uint16_t* og = static_cast<uint16_t*>(a.o) + b * a.o_strides[0] + h * a.o_strides[1] + qrow * a.o_strides[2];
+    // optional rounding residual O - bf16(O), so the backward's Delta can be
+    // formed from O to ~16 significant bits (contiguous [B, H, T, D])
+    uint16_t* lg = a.o_lo == nullptr ? nullptr
+                                     : static_cast<uint16_t*>(a.o_lo) + (int64_t(bh) * T + qrow) * D;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d0 = 32 * db + 8 * g + 4 * hf;
-        u32x2 w = {pack2<E>(o[db][4 * g] * inv, o[db][4 * g + 1] * inv),
-                   pack2<E>(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv)};
+        float f[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f[i] = o[db][4 * g + i] * inv;
+        const u32x2 w = {pack2<E>(f[0], f[1]), pack2<E>(f[2], f[3])};
         *reinterpret_cast<u32x2*>(og + d0) = w;
+        if (lg != nullptr) {
+          const u32x2 r = {pack2<E>(f[0] - to_f32<E>(uint16_t(w[0] & 0xFFFFu)), f[1] - to_f32<E>(uint16_t(w[0] >> 16))),
+                           pack2<E>(f[2] - to_f32<E>(uint16_t(w[1] & 0xFFFFu)), f[3] - to_f32<E>(uint16_t(w[1] >> 16)))};
+          *reinterpret_cast<u32x2*>(lg + d0) = r;
+        }
       }
     }
     if (a.lse != nullptr && hf == 0)
-      a.lse[int64_t(bh) * T + qrow] = l_tot > 0.f ? m_ref * sl2 + fast_log2(l_tot) : NEG_INF;
+      a.lse[int64_t(bh) * T + qrow] = l_exact > 0.f ? m_ref * sl2 + fast_log2(l_exact) : NEG_INF;
   }
 }
 

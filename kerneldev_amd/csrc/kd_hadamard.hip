@@ -1,0 +1,119 @@
+// Walsh-Hadamard incoherent processing of Q / K rows on gfx950.
+//
+// The reference names generate_hadamard_signs() / hadamard_transform()
+// (README.md:68-71, :77) without code; the transform is defined here as
+//   x R,  R = diag(s) H_d / sqrt(d),  H_d the Sylvester matrix, s in {+1,-1}^d
+// and its inverse (used for gradients) g R^T = ((g H_d) / sqrt(d)) * s.
+// Q R (K R)^T = Q K^T exactly in real arithmetic.
+//
+// Evaluation order is fixed so the result is bit-identical to the CPU
+// restatement: signs (exact), butterflies h = 1, 2, ..., d/2 each rounded to
+// fp32 ((a, b) -> (a + b, a - b)), one multiply by fp32(1/sqrt(d)), one
+// rounding to the output dtype.  D/8 lanes hold one row, 8 elements each:
+// strides 1, 2, 4 stay inside a lane, strides 8 .. d/2 pair lane t with
+// lane t ^ (h / 8).  Optionally the kernel also records max |y| per (b, h)
+// (the absmax the fp8 path scales by).
+#include "kd_internal.h"
+
+namespace kd {
+
+template <class E, int D, bool INV>
+__global__ __launch_bounds__(256) void k_hadamard(kd_rot_args a) {
+  constexpr int TPR = D / 8;         // lanes per row
+  constexpr int RPB = 256 / TPR;     // rows per block
+  const int tid = threadIdx.x, seg = tid % TPR;
+  const int64_t row = int64_t(blockIdx.x) * RPB + tid / TPR;
+  const int64_t nrows = int64_t(a.B) * a.H * a.T;
+  const bool valid = row < nrows;
+  const int64_t r = valid ? row : nrows - 1;  // idle lanes still join the shuffles
+  const int t = int(r % a.T);
+  const int bh = int(r / a.T);
+  const int b = bh / a.H, h = bh % a.H;
+  const uint16_t* xp = static_cast<const uint16_t*>(a.x) + b * a.x_strides[0] + h * a.x_strides[1] +
+                       t * a.x_strides[2] + seg * 8;
+  const u32x4 xv = *reinterpret_cast<const u32x4*>(xp);
+  float y[8];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    y[2 * w] = to_f32<E>(uint16_t(xv[w] & 0xFFFFu));
+    y[2 * w + 1] = to_f32<E>(uint16_t(xv[w] >> 16));
+  }
+  float sg[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sg[j] = a.signs[seg * 8 + j];
+  if (!INV) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] *= sg[j];
+  }
+  // in-lane butterflies, strides 1, 2, 4
+#pragma unroll
+  for (int hs = 1; hs < 8; hs <<= 1) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j & hs) continue;
+      const float u = y[j], v = y[j + hs];
+      y[j] = u + v;
+      y[j + hs] = u - v;
+    }
+  }
+  // cross-lane butterflies, strides 8 .. D/2
+#pragma unroll
+  for (int m = 1; m < TPR; m <<= 1) {
+    const bool upper = (seg & m) != 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float other = __shfl_xor(y[j], m, TPR);
+      y[j] = upper ? other - y[j] : y[j] + other;
+    }
+  }
+  // fp32(1 / sqrt(D)), correctly rounded
+  constexpr float scale = D == 64 ? 0x1p-3f : 0x1.6a09e6p-4f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] *= scale;
+  if (INV) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] *= sg[j];
+  }
+  u32x4 out;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) out[w] = pack2<E>(y[2 * w], y[2 * w + 1]);
+  if (valid) {
+    uint16_t* yp = static_cast<uint16_t*>(a.y) + b * a.y_strides[0] + h * a.y_strides[1] + t * a.y_strides[2] +
+                   seg * 8;
+    *reinterpret_cast<u32x4*>(yp) = out;
+  }
+  if (a.amax != nullptr) {
+    // |y| of the ROUNDED output, reduced over the row's lanes, one atomic per row
+    float m = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      m = fmaxf(m, fabsf(to_f32<E>(uint16_t(out[w] & 0xFFFFu))));
+      m = fmaxf(m, fabsf(to_f32<E>(uint16_t(out[w] >> 16))));
+    }
+#pragma unroll
+    for (int off = TPR / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, TPR));
+    if (valid && seg == 0) atomicMax(reinterpret_cast<unsigned int*>(a.amax) + bh, __float_as_uint(m));
+  }
+}
+
+template <class E, int D, bool INV>
+static void launch_rot_t(const kd_rot_args& a, hipStream_t st) {
+  constexpr int RPB = 256 / (D / 8);
+  const int64_t rows = int64_t(a.B) * a.H * a.T;
+  hipLaunchKernelGGL((k_hadamard<E, D, INV>), dim3(unsigned((rows + RPB - 1) / RPB)), dim3(256), 0, st, a);
+}
+
+int launch_hadamard(const kd_rot_args& a, hipStream_t st) {
+#define KD_ROT(E_, D_)                                          \
+  if (a.inverse) launch_rot_t<E_, D_, true>(a, st);             \
+  else launch_rot_t<E_, D_, false>(a, st);
+  if (a.dtype == KD_BF16) {
+    if (a.D == 64) { KD_ROT(BF16, 64) } else { KD_ROT(BF16, 128) }
+  } else {
+    if (a.D == 64) { KD_ROT(F16, 64) } else { KD_ROT(F16, 128) }
+  }
+#undef KD_ROT
+  return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
+}
+
+}  // namespace kd

@@ -1,0 +1,105 @@
+"""Walsh-Hadamard incoherent processing of Q and K.
+
+The reference's README names ``generate_hadamard_signs()`` and
+``hadamard_transform()`` (README.md:68-71, :77) but ships no code for them.
+Here they are defined as the rotation ``R = diag(s) H_d / sqrt(d)`` (Sylvester
+``H_d``, seeded signs ``s``), applied to the last dimension of a
+``[B, H, T, d]`` tensor by the gfx950 kernel ``kd_hadamard``.  Because ``R``
+is orthogonal, ``(Q R)(K R)^T = Q K^T``: rotating both operands leaves the
+attention scores unchanged in exact arithmetic while spreading outlier
+channels over all ``d`` lanes (which is what makes per-head fp8 scaling
+usable).  The autograd rule of ``y = x R`` is ``dx = dy R^T``, the same kernel
+with ``inverse=1``.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import RotArgs
+
+
+def generate_hadamard_signs(d: int, seed: int | None = None, device=None) -> torch.Tensor:
+    """Seeded random signs ``s in {+1, -1}^d`` as float32 (seed ``None`` -> 0)."""
+    if d <= 0 or d & (d - 1):
+        raise ValueError(f"d must be a power of two, got {d}")
+    g = torch.Generator("cpu").manual_seed(0 if seed is None else int(seed))
+    s = torch.randint(0, 2, (d,), generator=g, dtype=torch.int64).to(torch.float32) * 2 - 1
+    return s if device is None else s.to(device)
+
+
+def _strides3(t):
+    st = t.stride()
+    return (ctypes.c_int64 * 3)(st[0], st[1], st[2])
+
+
+def _launch(x: torch.Tensor, signs: torch.Tensor, inverse: bool, amax: torch.Tensor | None = None):
+    from .attention import _dtype_code, _kernel_ready
+
+    x = _kernel_ready(x)
+    B, H, T, D = x.shape
+    y = torch.empty((B, H, T, D), dtype=x.dtype, device=x.device)
+    a = RotArgs()
+    a.x, a.x_strides = x.data_ptr(), _strides3(x)
+    a.y, a.y_strides = y.data_ptr(), _strides3(y)
+    a.signs = signs.data_ptr()
+    a.amax = amax.data_ptr() if amax is not None else None
+    a.B, a.H, a.T, a.D = B, H, T, D
+    a.dtype = _dtype_code(x.dtype)
+    a.inverse = 1 if inverse else 0
+    stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+    _lib.check(_lib.load().kd_hadamard(ctypes.byref(a), stream), "kd_hadamard")
+    return y
+
+
+@torch.library.custom_op("kdattn::rot", mutates_args=(), device_types=("cuda",))
+def _rot_op(x: torch.Tensor, signs: torch.Tensor, inverse: bool) -> torch.Tensor:
+    return _launch(x, signs, inverse)
+
+
+@_rot_op.register_fake
+def _rot_fake(x, signs, inverse):
+    return torch.empty(x.shape, dtype=x.dtype, device=x.device)
+
+
+def _rot_setup(ctx, inputs, output):
+    _, signs, inverse = inputs
+    ctx.save_for_backward(signs)
+    ctx.inverse = inverse
+
+
+def _rot_backward(ctx, gy):
+    (signs,) = ctx.saved_tensors
+    return _rot_op(gy.contiguous(), signs, not ctx.inverse), None, None
+
+
+_rot_op.register_autograd(_rot_backward, setup_context=_rot_setup)
+
+
+def _check(x: torch.Tensor, signs: torch.Tensor):
+    if x.dim() != 4:
+        raise ValueError("x must be [batch, heads, time, head_dim]")
+    if x.shape[-1] not in (64, 128):
+        raise ValueError(f"head_dim must be 64 or 128 for the gfx950 transform, got {x.shape[-1]}")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"x must be bf16 or fp16, got {x.dtype}")
+    if not x.is_cuda:
+        raise ValueError("hadamard_transform runs on the GPU only (no CPU fallback)")
+    if signs.shape != (x.shape[-1],) or signs.dtype != torch.float32 or signs.device != x.device:
+        raise ValueError("signs must be float32 [head_dim] on x's device")
+
+
+def hadamard_transform(x: torch.Tensor, signs: torch.Tensor, inverse: bool = False) -> torch.Tensor:
+    """``x R`` (or ``x R^T`` with ``inverse``), differentiable, on the last dim."""
+    _check(x, signs)
+    return _rot_op(x, signs, bool(inverse))
+
+
+def hadamard_absmax(x: torch.Tensor, signs: torch.Tensor):
+    """``(x R, amax)`` with ``amax[b, h] = max |x R|`` over (t, d) of the rounded output."""
+    _check(x, signs)
+    amax = torch.zeros(x.shape[:2], dtype=torch.float32, device=x.device)
+    y = _launch(x, signs, False, amax)
+    return y, amax

@@ -8,33 +8,35 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_close, oracle_fwd_bwd, oracle_mask, select_heads
-from kerneldev_amd import flash_attention
+from helpers import assert_close, assert_close_scaled, oracle_fwd_bwd, oracle_mask, select_heads
+from kerneldev_amd import flash_attention, generate_hadamard_signs
+from oracle import hadamard as ref_h
 from kerneldev_amd.synth import CONFIG3_LAYOUT, cocktail_batch, config_inputs, qkvdo
 
 pytestmark = pytest.mark.gpu
 
 
-def run_gpu(inp, dev, lens=None, attention_mask=None, dtype=None):
+def run_gpu(inp, dev, lens=None, attention_mask=None, dtype=None, **extra):
     q, k, v, do = (inp[x].to(dev) for x in ("q", "k", "v", "do"))
     if dtype is not None:
         q, k, v, do = (x.to(dtype) for x in (q, k, v, do))
     q, k, v = (x.detach().requires_grad_(True) for x in (q, k, v))
     meta = {n: (inp[n].to(dev) if inp.get(n) is not None else None) for n in ("in_span", "span_id", "is_prefix")}
     o, lse = flash_attention(q, k, v, lens=None if lens is None else lens.to(dev), causal=inp.get("causal", True),
-                             return_lse=True, attention_mask=attention_mask, **meta)
+                             return_lse=True, attention_mask=attention_mask, **meta, **extra)
     o.backward(do)
     torch.cuda.synchronize()
     return {"o": o.detach(), "lse": lse.detach(), "dq": q.grad, "dk": k.grad, "dv": v.grad}
 
 
-def compare(got, ref, heads=None, lse_finite_only=True):
+def compare(got, ref, heads=None, scaled=False):
     """Check O, dQ, dK, dV and LSE; report every failure, not just the first."""
     res, failures = {}, []
+    check = assert_close_scaled if scaled else assert_close
     for key in ("o", "dq", "dk", "dv"):
         g = got[key] if heads is None else select_heads(got[key], heads)
         try:
-            res[key] = assert_close(key, g, ref[key])
+            res[key] = check(key, g, ref[key])
         except AssertionError as exc:
             failures.append(str(exc))
     g = got["lse"] if heads is None else torch.cat([got["lse"][b:b + 1, h:h + 1] for b, h in heads], 0)
@@ -42,14 +44,15 @@ def compare(got, ref, heads=None, lse_finite_only=True):
     assert torch.equal(torch.isinf(g), torch.isinf(r)), "LSE -inf pattern differs"
     fin = torch.isfinite(r)
     try:
-        res["lse"] = assert_close("lse", g[fin], r[fin], out_dtype=torch.float32)
+        res["lse"] = (assert_close_scaled("lse", g[fin], r[fin]) if scaled
+                      else assert_close("lse", g[fin], r[fin], out_dtype=torch.float32))
     except AssertionError as exc:
         failures.append(str(exc))
     assert not failures, "; ".join(failures)
     return res
 
 
-def _case(inp, dev, heads=None, **kw):
+def _case(inp, dev, heads=None, scaled=False, **kw):
     print(f"attention case {inp.get('name', '?')} heads={heads}", flush=True)
     got = run_gpu(inp, dev, **kw)
     T = inp["q"].shape[2]
@@ -58,8 +61,20 @@ def _case(inp, dev, heads=None, **kw):
     dt = kw.get("dtype")
     if dt is not None:  # the oracle sees exactly the rounded inputs the GPU sees
         q, k, v, do = (x.to(dt) for x in (q, k, v, do))
+    rot = None
+    if kw.get("hadamard"):
+        # the rotation is bit-exact (tests/test_gpu_hadamard.py); the attention
+        # under test sees Q' = bf16(Q R) and K' = bf16(K R), and the reference
+        # maps dQ', dK' back through R^T in fp64
+        signs = generate_hadamard_signs(q.shape[-1], kw.get("hadamard_seed")).numpy()
+        rot = torch.from_numpy(ref_h.rotation_matrix(signs))
+        q = torch.from_numpy(ref_h.rotate_fp32(q.float().numpy(), signs)).to(q.dtype)
+        k = torch.from_numpy(ref_h.rotate_fp32(k.float().numpy(), signs)).to(k.dtype)
     ref = oracle_fwd_bwd(q, k, v, do, mask, q.shape[-1] ** -0.5, heads=heads)
-    return compare(got, ref, heads)
+    if rot is not None:
+        ref["dq"] = ref["dq"] @ rot.T
+        ref["dk"] = ref["dk"] @ rot.T
+    return compare(got, ref, heads, scaled=scaled)
 
 
 def test_config1_causal_fp32_inputs(dev):
@@ -134,8 +149,15 @@ def test_config3_cocktail(dev):
 
 
 def test_config4_cocktail_bf16(dev):
+    """20-sigma outlier data: max-abs bar relative to each tensor's magnitude."""
     inp = config_inputs(4, seed=0)
-    _case(inp, dev, heads=[(0, 0), (1, 31)])
+    _case(inp, dev, heads=[(0, 0), (1, 31)], scaled=True)
+
+
+def test_config4_cocktail_hadamard_bf16(dev):
+    """Config 4 as specified: Q and K rotated by the seeded d=128 Hadamard."""
+    inp = config_inputs(4, seed=0)
+    _case(inp, dev, heads=[(0, 3), (1, 17)], scaled=True, hadamard=True, hadamard_seed=0)
 
 
 def test_deterministic(dev):

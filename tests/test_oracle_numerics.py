@@ -1,0 +1,227 @@
+"""CPU pinning of the oracle's Hadamard, fp8, metadata, tile-map and attention code.
+
+The reference ships no tests or golden vectors for this path, so each oracle
+function is checked against something it does not restate: a library routine
+(scipy's Hadamard matrix, torch's float8 cast, torch autograd / SDPA), a closed
+form or invariant of the mathematics, or brute force on tiny inputs.  Each
+check is chosen so that a plausible slip (a dropped term, a swapped sign or
+index, a transposed operand) fails it.
+"""
+import math
+
+import numpy as np
+import pytest
+import scipy.linalg
+import torch
+
+from oracle import attention as ref
+from oracle import fp8, hadamard, metadata, tilemap
+from oracle.mask import dense_mask
+
+PAD, CLS, MASK, SPAN, ES, MASKQ = 0, 1, 2, 3, 4, 5
+
+
+# ------------------------------------------------------------------ Hadamard
+@pytest.mark.parametrize("d", [2, 8, 64, 128])
+def test_sylvester_equals_scipy(d):
+    np.testing.assert_array_equal(hadamard.sylvester(d), scipy.linalg.hadamard(d))
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_rotation_orthogonal_and_matches_dense(d):
+    rng = np.random.default_rng(d)
+    s = rng.choice([-1.0, 1.0], size=d)
+    R = hadamard.rotation_matrix(s)
+    np.testing.assert_allclose(R @ R.T, np.eye(d), atol=1e-12)
+    x = rng.standard_normal((5, d)).astype(np.float32)
+    y = hadamard.rotate_fp32(x, s)
+    np.testing.assert_allclose(y, x.astype(np.float64) @ R, rtol=0, atol=1e-5)
+    g = rng.standard_normal((5, d)).astype(np.float32)
+    np.testing.assert_allclose(hadamard.unrotate_fp32(g, s), g.astype(np.float64) @ R.T, rtol=0, atol=1e-5)
+    # un-rotating the rotation gives the input back; scores are preserved
+    np.testing.assert_allclose(hadamard.unrotate_fp32(y, s), x, atol=1e-5)
+    k = rng.standard_normal((7, d)).astype(np.float32)
+    np.testing.assert_allclose(y @ hadamard.rotate_fp32(k, s).T, x @ k.T, atol=1e-4)
+
+
+def test_butterflies_twice_is_d_times_identity():
+    d = 128
+    x = np.arange(d, dtype=np.float32)[None] - 40.0  # small integers: every op exact
+    np.testing.assert_array_equal(hadamard._butterflies(hadamard._butterflies(x)), d * x)
+
+
+def test_rotation_sign_order_matters():
+    # signs are applied BEFORE the butterflies in x R and AFTER them in g R^T
+    d = 8
+    s = np.array([1, -1, 1, 1, -1, 1, 1, 1], np.float64)
+    e0 = np.eye(d, dtype=np.float32)[1:2]
+    y = hadamard.rotate_fp32(e0, s)  # row 1 of R = s_1 * H[1] / sqrt(d)
+    np.testing.assert_allclose(y[0], s[1] * scipy.linalg.hadamard(d)[1] / math.sqrt(d), atol=1e-7)
+
+
+# ----------------------------------------------------------------------- fp8
+def _torch_e4m3_bits(x):
+    return torch.from_numpy(np.asarray(x, np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def test_e4m3_encode_matches_torch_on_grid_and_ties():
+    # every representable magnitude, midpoints between neighbours (ties), and a random cloud
+    mags = np.sort(np.unique(np.abs(fp8.e4m3_decode(np.arange(256, dtype=np.uint8)))))
+    mags = mags[np.isfinite(mags)]
+    mids = (mags[1:] + mags[:-1]) / 2
+    rng = np.random.default_rng(0)
+    cloud = rng.standard_normal(20000).astype(np.float32) * np.exp2(rng.integers(-12, 9, 20000)).astype(np.float32)
+    x = np.concatenate([mags, -mags, mids, -mids, cloud, np.array([447.9, 448.0, 460.0, -1e9, 2.0 ** -10], np.float32)])
+    x = np.clip(x.astype(np.float32), -448, 448)
+    np.testing.assert_array_equal(fp8.e4m3_encode(x), _torch_e4m3_bits(x))
+
+
+def test_e4m3_decode_is_inverse_on_codes():
+    codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], np.uint8)  # skip NaN codes
+    vals = fp8.e4m3_decode(codes)
+    ref_vals = torch.from_numpy(codes).view(torch.float8_e4m3fn).to(torch.float32).numpy()
+    np.testing.assert_array_equal(vals, ref_vals)
+    back = fp8.e4m3_encode(vals)
+    same = (back == codes) | ((codes == 0x80) & (back == 0x00))  # -0 may encode as +0
+    assert same.all()
+
+
+def test_quantize_per_head_scale_and_error_bound():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((2, 3, 16, 64)).astype(np.float32)
+    x[0, 1] *= 100.0
+    q, sigma = fp8.quantize_per_head(x)
+    deq = fp8.e4m3_decode(q) * sigma[:, :, None, None]
+    amax = np.abs(x).max(axis=(2, 3))
+    np.testing.assert_allclose(sigma * 448.0, amax, rtol=1e-6)
+    # e4m3 has 3 mantissa bits: relative error <= 2^-4 for normals, absolute <= 2^-10 sigma below
+    err = np.abs(deq - x)
+    bound = np.maximum(np.abs(x) * 2.0 ** -4, sigma[:, :, None, None] * 2.0 ** -10)
+    assert (err <= bound * 1.0001).all()
+    assert np.abs(fp8.e4m3_decode(q)).max() <= 448.0
+
+
+# ------------------------------------------------------------------ metadata
+def test_collate_metadata_vs_product_derivation_on_cocktail_batches():
+    from kerneldev_amd.metadata import derive_metadata
+    from kerneldev_amd.synth import CONFIG3_LAYOUT, cocktail_batch
+
+    tokens, in_span, span_id, is_prefix = cocktail_batch(6, 1024, CONFIG3_LAYOUT, seed=5)
+    o_in, o_sid, o_pre = metadata.collate_metadata(tokens.numpy())
+    np.testing.assert_array_equal(in_span.numpy(), o_in)
+    np.testing.assert_array_equal(span_id.numpy(), o_sid)
+    np.testing.assert_array_equal(is_prefix.numpy(), o_pre)
+    f_in, f_sid, f_pre = metadata.fallback_metadata(tokens.numpy())
+    d_in, d_sid, d_pre = derive_metadata(tokens, rule="fallback")
+    np.testing.assert_array_equal(d_in.numpy(), f_in)
+    np.testing.assert_array_equal(d_sid.numpy(), f_sid)
+    np.testing.assert_array_equal(d_pre.numpy(), f_pre)
+    # the two rules differ exactly at the [ES] tokens (F7)
+    es = tokens.numpy() == ES
+    np.testing.assert_array_equal(o_in & ~f_in, es)
+
+
+def test_metadata_edge_cases():
+    toks = np.array([[6, 7, 8, 9],                 # no [CLS]: no prefix
+                     [CLS, SPAN, 7, ES],           # span right after [CLS]
+                     [6, CLS, MASKQ, MASKQ]])      # two [MASKQ]: only the first is -1 (collate)
+    i1, s1, p1 = metadata.collate_metadata(toks)
+    assert not p1[0].any() and p1[1].tolist() == [1, 0, 0, 0]
+    assert i1[1].tolist() == [0, 1, 1, 1] and s1[1].tolist() == [0, 1, 1, 1]
+    assert s1[2].tolist() == [0, 0, -1, 0]
+    _, s2, _ = metadata.fallback_metadata(toks)
+    assert s2[2].tolist() == [0, 0, -1, -1]
+
+
+# ------------------------------------------------------------------ tile map
+def test_classify_and_lists_bruteforce():
+    rng = np.random.default_rng(2)
+    for T in (1, 63, 64, 130, 200):
+        m = rng.random((2, T, T)) < rng.choice([0.0, 0.3, 1.0])
+        m[:, : T // 3, : T // 3] = True
+        cls = tilemap.classify(m, 64)
+        n = -(-T // 64)
+        for b in range(2):
+            for qi in range(n):
+                for ki in range(n):
+                    blk = np.zeros((64, 64), bool)
+                    sub = m[b, qi * 64:(qi + 1) * 64, ki * 64:(ki + 1) * 64]
+                    blk[: sub.shape[0], : sub.shape[1]] = sub
+                    want = 0 if not blk.any() else (2 if blk.all() else 1)
+                    assert cls[b, qi, ki] == want
+        for rq in (1, 2):
+            ent, cnt = tilemap.q_lists(cls, rq)
+            kent, kcnt = tilemap.k_lists(cls, rq)
+            for b in range(2):
+                for blk in range(cnt.shape[1]):
+                    rows = [r for r in range(blk * rq, blk * rq + rq) if r < n]
+                    want = [(c << 1) | int(all(cls[b, r, c] == 2 for r in rows) and len(rows) == rq)
+                            for c in range(n) if any(cls[b, r, c] != 0 for r in rows)]
+                    assert ent[b, blk, : cnt[b, blk]].tolist() == want
+                for blk in range(kcnt.shape[1]):
+                    cols = [r for r in range(blk * rq, blk * rq + rq) if r < n]
+                    want = [(r << 1) | int(all(cls[b, r, c] == 2 for c in cols) and len(cols) == rq)
+                            for r in range(n) if any(cls[b, r, c] != 0 for c in cols)]
+                    assert kent[b, blk, : kcnt[b, blk]].tolist() == want
+
+
+# ----------------------------------------------------------------- attention
+def _case(seed=0, T=48, D=16, B=2, H=2):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v, do = (torch.randn(B, H, T, D, generator=g, dtype=torch.float64) for _ in range(4))
+    toks = np.full((B, T), PAD)
+    toks[:, :6] = 9
+    toks[:, 6] = CLS
+    toks[:, 7:20] = 9
+    toks[:, 12] = MASK
+    toks[:, 20], toks[:, 21:26], toks[:, 26] = SPAN, 9, ES
+    toks[:, 27], toks[:, 28:31], toks[:, 31] = SPAN, 9, ES
+    toks[:, 32] = MASKQ
+    in_span, span_id, is_prefix = metadata.collate_metadata(toks)
+    lens = np.array([T, T - 5], np.int32)
+    mask = torch.from_numpy(dense_mask(T, B=B, in_span=in_span, span_id=span_id, is_prefix=is_prefix, lens=lens))
+    return q, k, v, do, mask
+
+
+def test_forward_backward_match_autograd():
+    q, k, v, do, mask = _case()
+    sc = 0.37
+    o, lse2 = ref.forward(q, k, v, mask, sc)
+    dq, dk, dv, delta = ref.backward(q, k, v, o, do, mask, sc)
+    o2, dq2, dk2, dv2 = ref.autograd_reference(q, k, v, do, mask, sc)
+    for a, b in ((o, o2), (dq, dq2), (dk, dk2), (dv, dv2)):
+        torch.testing.assert_close(a, b, rtol=1e-10, atol=1e-10)
+    # fully masked rows (t >= lens) give O = 0, LSE = -inf and no gradient
+    assert (o[1, :, -5:] == 0).all() and torch.isinf(lse2[1, :, -5:]).all()
+    assert (dq[1, :, -5:] == 0).all() and (dk[1, :, -5:] == 0).all() and (dv[1, :, -5:] == 0).all()
+    np.testing.assert_allclose(delta.numpy(), (o * do).sum(-1).numpy())
+
+
+def test_lse_is_base2_logsumexp_and_ds_rows_sum_to_zero():
+    q, k, v, do, mask = _case(seed=1)
+    sc = 0.25
+    o, lse2 = ref.forward(q, k, v, mask, sc)
+    s = (q @ k.transpose(-1, -2)) * sc
+    s = s.masked_fill(~mask[:, None], float("-inf"))
+    lse_e = torch.logsumexp(s, dim=-1)
+    fin = torch.isfinite(lse_e)
+    torch.testing.assert_close(lse2[fin], lse_e[fin] * math.log2(math.e), rtol=1e-12, atol=1e-12)
+    p = ref.probabilities(q, k, mask, sc)
+    dp = do @ v.transpose(-1, -2)
+    ds = p * (dp - (o * do).sum(-1, keepdim=True))
+    assert ds.sum(-1).abs().max().item() < 1e-12
+
+
+def test_sdpa_baseline_matches_oracle():
+    q, k, v, do, mask = _case(seed=2)
+    sc = 0.3
+    # the eager SDPA baseline cannot express fully masked rows (it returns NaN
+    # there), so compare on the unpadded sequence only
+    T = q.shape[2] - 5
+    sl = (slice(None), slice(None), slice(0, T))
+    qs, ks, vs, dos = (x[sl].contiguous() for x in (q, k, v, do))
+    m = mask[:, :T, :T]
+    o, dq, dk, dv = ref.sdpa_baseline(qs, ks, vs, dos, m, sc)
+    o2, dq2, dk2, dv2 = ref.autograd_reference(qs, ks, vs, dos, m, sc)
+    for a, b in ((o, o2), (dq, dq2), (dk, dk2), (dv, dv2)):
+        torch.testing.assert_close(a.double(), b, rtol=1e-4, atol=1e-4)
