@@ -49,6 +49,11 @@ KERNEL_FLOPS_PER_ENTRY = {
 }
 USEFUL_FWD, USEFUL_BWD = 4, 10
 
+# HBM bytes per launch of the attention kernels on config 4 (Hadamard on), from
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs scaled by a 1 GiB copy's counts
+# (profiles/attn_config4_hbm_traffic.md); re-measured whenever the kernels change.
+CONFIG4_TRAFFIC_BYTES = {"fwd": 966.8e6, "dq": 952.7e6, "dkdv": 1231.7e6}
+
 
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
@@ -274,9 +279,13 @@ def main():
     dom = max(("fwd", "dq", "dkdv"), key=lambda n: per_kernel[n])
     dom_flops = KERNEL_FLOPS_PER_ENTRY[dom] * D * H * nnz
     achieved = dom_flops / (per_kernel[dom] * 1e-3) / 1e12
+    traffic = CONFIG4_TRAFFIC_BYTES.get(dom) if (args.config == 4 and hadamard) else None
     roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                "traffic": None, "avg_launch_ms": round(per_kernel[dom], 4)}
+                "traffic": traffic, "avg_launch_ms": round(per_kernel[dom], 4),
+                "algorithmic_tflop_per_launch": round(dom_flops / 1e12, 4)}
+    kernel_tflops = {n: round(KERNEL_FLOPS_PER_ENTRY[n] * D * H * nnz / (per_kernel[n] * 1e-3) / 1e12, 1)
+                     for n in ("fwd", "dq", "dkdv")}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -303,6 +312,7 @@ def main():
             "useful_tflop_per_step": round(useful / 1e12, 4),
             "frac_of_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
             "kernel_ms": {n: round(x, 4) for n, x in per_kernel.items()},
+            "kernel_algorithmic_tflops": kernel_tflops,
             "event_ms_per_step": round(event_ms, 4),
             "hadamard": hadamard,
         },

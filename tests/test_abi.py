@@ -1,0 +1,93 @@
+"""CPU: the C-ABI library loads, exports every symbol include/kdattn.h declares,
+and rejects bad arguments with a status before touching the GPU; the Python
+boundary validates like the reference's adapter (original_kernel.py:1720-1726)
+but raises ValueError.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from kerneldev_amd import _lib, flash_attention
+from kerneldev_amd.attention import REFERENCE_HEAD_DIMS
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "kdattn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?(?:int|int64_t|void|char)\s*\*?\s*(kd_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 13, names
+    for n in names:
+        assert hasattr(lib, n), f"{n} missing from {_lib.LIB_PATH}"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_struct_layouts_and_version():
+    lib = _lib.load()  # load() itself checks the three struct sizes
+    assert lib.kd_version() >= 100
+    assert ctypes.sizeof(_lib.AttnArgs) % 8 == 0
+
+
+def test_plan_sizes_and_layout_offsets():
+    lib = _lib.load()
+    assert lib.kd_plan_bytes(0, 10, 64) < 0
+    L = _lib.plan_layout(2, 8192, 128)
+    assert L["nT"] == 128 and L["n_fwd_blocks"] == 64 and L["fwd_group"] == 2
+    offs = [L[k] for k in _lib.PLAN_FIELDS[:10]]
+    assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
+    assert _lib.plan_bytes(2, 8192, 128) > L["dkdv_count"]
+
+
+def test_bad_arguments_return_status_without_gpu():
+    lib = _lib.load()
+    null = ctypes.c_void_p(0)
+    assert lib.kd_attn_fwd(None, null, null) == _lib.KD_ERR_INVALID
+    assert "NULL" in lib.kd_last_error_string().decode()
+    a = _lib.AttnArgs()
+    a.B, a.H, a.T, a.D, a.dtype, a.sm_scale = 1, 1, 16, 96, _lib.KD_BF16, 0.1
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_UNSUPPORTED
+    a.D = 64
+    a.sm_scale = float("nan")
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_INVALID
+    a.sm_scale = 0.125
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_INVALID  # q is NULL
+    a.q = a.k = a.v = a.o = 32
+    a.q_strides[:] = [1024, 1024, 8]  # t stride < head dim: rows overlap
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_INVALID
+    assert "overlap" in lib.kd_last_error_string().decode()
+    r = _lib.RotArgs()
+    r.B, r.H, r.T, r.D, r.dtype = 1, 1, 4, 32, _lib.KD_BF16
+    assert lib.kd_hadamard(ctypes.byref(r), null) == _lib.KD_ERR_UNSUPPORTED
+    m = _lib.MetaArgs()
+    m.B, m.T, m.mode = 1, 8, 7
+    assert lib.kd_plan_build(ctypes.byref(m), ctypes.c_void_p(256), null) == _lib.KD_ERR_INVALID
+
+
+def test_python_boundary_validation():
+    q = torch.zeros(1, 2, 16, 64)
+    with pytest.raises(ValueError, match="GPU only"):
+        flash_attention(q, q, q)
+    with pytest.raises(ValueError, match="head_dim"):
+        z = torch.zeros(1, 2, 16, 48)
+        flash_attention(z, z, z)
+    with pytest.raises(ValueError, match="not built"):
+        z = torch.zeros(1, 2, 16, 32)  # allowed by the reference, not built for gfx950
+        flash_attention(z, z, z)
+    with pytest.raises(ValueError, match="precision"):
+        flash_attention(q, q, q, precision="fp16")
+    with pytest.raises(ValueError, match="lens"):
+        flash_attention(q, q, q, lens=torch.zeros(1, dtype=torch.int64))
+    with pytest.raises(ValueError, match="qk_dtype"):
+        flash_attention(q, q, q, qk_dtype="int8")
+    assert 32 in REFERENCE_HEAD_DIMS and 256 in REFERENCE_HEAD_DIMS

@@ -166,3 +166,15 @@ def test_deterministic(dev):
     b = run_gpu(inp, dev)
     for key in a:
         assert torch.equal(a[key], b[key]), key
+
+
+def test_config1_against_golden_fixture(dev):
+    """Config 1 head (0, 0) against the committed fp64 golden vectors."""
+    import os
+
+    fx = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config1_b0h0.npz"))
+    inp = config_inputs(1, seed=0)
+    got = run_gpu(inp, dev)
+    for key in ("o", "dq", "dk", "dv"):
+        assert_close(key, got[key][0, 0], torch.from_numpy(fx[key]))
+    assert_close("lse", got["lse"][0, 0], torch.from_numpy(fx["lse"]), out_dtype=torch.float32)

@@ -225,3 +225,19 @@ def test_sdpa_baseline_matches_oracle():
     o2, dq2, dk2, dv2 = ref.autograd_reference(qs, ks, vs, dos, m, sc)
     for a, b in ((o, o2), (dq, dq2), (dk, dk2), (dv, dv2)):
         torch.testing.assert_close(a.double(), b, rtol=1e-4, atol=1e-4)
+
+
+# -------------------------------------------------------------- golden fixture
+def test_config1_golden_fixture_reproduces():
+    import importlib.util
+    import os
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    spec = importlib.util.spec_from_file_location("make_golden", os.path.join(here, "golden", "make_golden.py"))
+    mg = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mg)
+    fx = np.load(os.path.join(here, "golden", "config1_b0h0.npz"))
+    inp, g = mg.golden()
+    assert str(fx["digest"]) == mg.input_digest(inp), "seeded config-1 inputs changed"
+    for key in ("o", "lse", "dq", "dk", "dv"):
+        np.testing.assert_allclose(g[key], fx[key], rtol=0, atol=1e-12, err_msg=key)
