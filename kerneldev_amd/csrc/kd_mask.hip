@@ -117,30 +117,48 @@ __global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, i
 }
 
 // ---- per-row-block work lists ------------------------------------------
-// by_key = 0: row blocks group `group` q-tiles, entries are k-tiles.
-// by_key = 1: row blocks group `group` k-tiles, entries are q-tiles.
-__global__ void k_lists(const uint8_t* cls, int B, int nT, int group, int by_key, uint32_t* entries,
-                        int32_t* counts) {
-  const int nRB = (nT + group - 1) / group;
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= B * nRB) return;
-  const int b = idx / nRB, rb = idx % nRB;
+// One wave per row block: lanes test 64 columns at a time and compact the
+// non-empty ones in ascending order with a ballot + prefix popcount; the
+// tail of the list is zero-filled.  All three lists build in one launch
+// (blockIdx.y picks the list).
+struct ListSpec {
+  uint32_t* entries;
+  int32_t* counts;
+  int group, by_key, nrb;
+};
+struct ListSpecs {
+  ListSpec l[3];
+};
+
+__global__ __launch_bounds__(64) void k_lists(const uint8_t* __restrict__ cls, int B, int nT, ListSpecs specs) {
+  const ListSpec sp = specs.l[blockIdx.y];
+  const int idx = blockIdx.x;  // b * nrb + rb
+  if (idx >= B * sp.nrb) return;
+  const int b = idx / sp.nrb, rb = idx % sp.nrb, lane = threadIdx.x;
   const uint8_t* base = cls + int64_t(b) * nT * nT;
-  uint32_t* out = entries + int64_t(idx) * nT;
+  uint32_t* out = sp.entries + int64_t(idx) * nT;
   int n = 0;
-  for (int c = 0; c < nT; ++c) {
+  for (int c0 = 0; c0 < nT; c0 += 64) {
+    const int c = c0 + lane;
     bool any_ne = false, all_full = true;
-    for (int r = 0; r < group; ++r) {
-      const int row = rb * group + r;
-      uint8_t k = TILE_EMPTY;
-      if (row < nT) k = by_key ? base[int64_t(c) * nT + row] : base[int64_t(row) * nT + c];
-      any_ne |= (k != TILE_EMPTY);
-      all_full &= (k == TILE_FULL);
+    if (c < nT) {
+      for (int r = 0; r < sp.group; ++r) {
+        const int row = rb * sp.group + r;
+        uint8_t k = TILE_EMPTY;
+        if (row < nT) k = sp.by_key ? base[int64_t(c) * nT + row] : base[int64_t(row) * nT + c];
+        any_ne |= (k != TILE_EMPTY);
+        all_full &= (k == TILE_FULL);
+      }
+    } else {
+      all_full = false;
     }
-    if (any_ne) out[n++] = (uint32_t(c) << 1) | (all_full ? 1u : 0u);
+    const uint64_t m = __builtin_amdgcn_ballot_w64(any_ne);
+    const int pos = n + __builtin_popcountll(m & ((uint64_t(1) << lane) - 1));
+    if (any_ne) out[pos] = (uint32_t(c) << 1) | (all_full ? 1u : 0u);
+    n += __builtin_popcountll(m);
   }
-  for (int c = n; c < nT; ++c) out[c] = 0;
-  counts[idx] = n;
+  for (int c = n + lane; c < nT; c += 64) out[c] = 0;
+  if (lane == 0) sp.counts[idx] = n;
 }
 
 // ---- dense mask output (return_attention_mask) -------------------------
@@ -207,14 +225,15 @@ int launch_plan(const MetaArgs& m, uint8_t* plan, hipStream_t st) {
   }
   hipLaunchKernelGGL(k_codes, dim3(unsigned((BT + 255) / 256)), dim3(256), 0, st, m, rep, codes);
   hipLaunchKernelGGL(k_tilemap, dim3((L.nT + 3) / 4, L.nT, m.B), dim3(256), 0, st, codes, m.T, L.nT, cls, nnz);
-  auto lists = [&](int group, int by_key, size_t lo, size_t co, int nrb) {
-    const int n = m.B * nrb;
-    hipLaunchKernelGGL(k_lists, dim3((n + 63) / 64), dim3(64), 0, st, cls, m.B, L.nT, group, by_key,
-                       reinterpret_cast<uint32_t*>(plan + lo), reinterpret_cast<int32_t*>(plan + co));
-  };
-  lists(L.fwd_group, 0, L.fwd_list, L.fwd_count, L.n_fwd_blocks);
-  lists(L.dq_group, 0, L.dq_list, L.dq_count, L.n_dq_blocks);
-  lists(L.dkdv_group, 1, L.dkdv_list, L.dkdv_count, L.n_dkdv_blocks);
+  ListSpecs specs;
+  specs.l[0] = {reinterpret_cast<uint32_t*>(plan + L.fwd_list), reinterpret_cast<int32_t*>(plan + L.fwd_count),
+                L.fwd_group, 0, L.n_fwd_blocks};
+  specs.l[1] = {reinterpret_cast<uint32_t*>(plan + L.dq_list), reinterpret_cast<int32_t*>(plan + L.dq_count),
+                L.dq_group, 0, L.n_dq_blocks};
+  specs.l[2] = {reinterpret_cast<uint32_t*>(plan + L.dkdv_list), reinterpret_cast<int32_t*>(plan + L.dkdv_count),
+                L.dkdv_group, 1, L.n_dkdv_blocks};
+  const int max_rb = std::max(L.n_fwd_blocks, std::max(L.n_dq_blocks, L.n_dkdv_blocks));
+  hipLaunchKernelGGL(k_lists, dim3(unsigned(m.B * max_rb), 3), dim3(64), 0, st, cls, m.B, L.nT, specs);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 
