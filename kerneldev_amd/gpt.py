@@ -1,0 +1,167 @@
+"""GPT training-step harness through the MI355X attention.
+
+A restatement of KernelDev's ``GPTModel`` (``model.py:31-117`` blocks,
+``:127-314`` model), the hot path's only caller: token + position embeddings,
+pre-norm blocks of weightless RMSNorm -> ``MultiHeadAttention`` -> residual and
+RMSNorm -> SwiGLU -> residual, a final RMSNorm, a head tied to the token
+embedding, N(0, 0.02) init (``:174-178``).  Attention goes through
+``flash_attention`` with the mask metadata, exactly as ``model.py:73-96``
+calls it; the q/k/v projections are handed over as strided ``[B, H, L, d]``
+views of ``[B, L, H, d]``, without copies.
+
+The cocktail-party head (``model.py:243-295``) scores the hidden state at the
+first ``[MASK]`` against the mean hidden state of each span's interior
+(``[SPAN] x.. [ES]`` minus the markers) and takes the cross entropy against
+``correct_idx``; spans a row does not have score 0, as the reference's
+zero-padded ``h_spans`` do.  Here the span means are one ``index_add_`` instead
+of the reference's Python double loop, and the scores are formed in fp32.
+
+``attention`` is injectable so a test can run the same weights through a
+dense fp32 reference attention.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .attention import flash_attention
+from .metadata import CLS, ES, MASK, MASKQ, SPAN, derive_metadata
+
+VOCAB = 256 + 6  # byte tokens + [PAD] [CLS] [MASK] [SPAN] [ES] [MASKQ] (data_builder.py:44-52)
+
+
+class RMSNorm(nn.Module):
+    """x / rms(x), no weight (model.py:31-39)."""
+
+    def __init__(self, eps: float = 1e-6):
+        super().__init__()
+        self.eps = eps
+
+    def forward(self, x):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps)
+
+
+class SwiGLU(nn.Module):
+    """w2(silu(w1 x) * w3 x) (model.py:42-52)."""
+
+    def __init__(self, dim: int, hidden: int):
+        super().__init__()
+        self.w1 = nn.Linear(dim, hidden, bias=False)
+        self.w2 = nn.Linear(hidden, dim, bias=False)
+        self.w3 = nn.Linear(dim, hidden, bias=False)
+
+    def forward(self, x):
+        return self.w2(F.silu(self.w1(x)) * self.w3(x))
+
+
+class MultiHeadAttention(nn.Module):
+    """q/k/v projections -> flash_attention -> o_proj (model.py:58-96)."""
+
+    def __init__(self, dim: int, n_heads: int, causal: bool = True, attention=None):
+        super().__init__()
+        self.n_heads, self.head_dim, self.causal = n_heads, dim // n_heads, causal
+        self.q_proj = nn.Linear(dim, dim, bias=False)
+        self.k_proj = nn.Linear(dim, dim, bias=False)
+        self.v_proj = nn.Linear(dim, dim, bias=False)
+        self.o_proj = nn.Linear(dim, dim, bias=False)
+        self.attention = attention or flash_attention
+
+    def forward(self, x, in_span, span_id, is_prefix):
+        B, L, _ = x.shape
+        shape = (B, L, self.n_heads, self.head_dim)
+        q = self.q_proj(x).view(shape).transpose(1, 2)
+        k = self.k_proj(x).view(shape).transpose(1, 2)
+        v = self.v_proj(x).view(shape).transpose(1, 2)
+        out = self.attention(q, k, v, lens=None, causal=self.causal, attention_mask=None,
+                             in_span=in_span, span_id=span_id, is_prefix=is_prefix)
+        return self.o_proj(out.transpose(1, 2).reshape(B, L, -1))
+
+
+class Block(nn.Module):
+    def __init__(self, dim, n_heads, hidden, causal=True, attention=None):
+        super().__init__()
+        self.norm1, self.norm2 = RMSNorm(), RMSNorm()
+        self.attn = MultiHeadAttention(dim, n_heads, causal, attention)
+        self.mlp = SwiGLU(dim, hidden)
+
+    def forward(self, x, in_span, span_id, is_prefix):
+        x = x + self.attn(self.norm1(x), in_span, span_id, is_prefix)
+        return x + self.mlp(self.norm2(x))
+
+
+class GPTModel(nn.Module):
+    """Config 5: d_model 768, 12 layers, 12 heads of 64, SwiGLU 2048, vocab 262."""
+
+    def __init__(self, vocab_size=VOCAB, dim=768, n_layers=12, n_heads=12, max_seq_len=2048, mlp_hidden=2048,
+                 causal=True, attention=None):
+        super().__init__()
+        self.token_emb = nn.Embedding(vocab_size, dim)
+        self.pos_emb = nn.Embedding(max_seq_len, dim)
+        self.blocks = nn.ModuleList(Block(dim, n_heads, mlp_hidden, causal, attention) for _ in range(n_layers))
+        self.norm_out = RMSNorm()
+        self.head = nn.Linear(dim, vocab_size, bias=False)
+        self.head.weight = self.token_emb.weight  # tied (model.py:170)
+        for m in self.modules():
+            if isinstance(m, (nn.Linear, nn.Embedding)):
+                nn.init.normal_(m.weight, mean=0.0, std=0.02)
+
+    def hidden(self, tokens, in_span, span_id, is_prefix):
+        pos = torch.arange(tokens.shape[1], device=tokens.device)
+        h = self.token_emb(tokens) + self.pos_emb(pos)[None]
+        for blk in self.blocks:
+            h = blk(h, in_span, span_id, is_prefix)
+        return self.norm_out(h)
+
+    def forward(self, tokens, correct_idx=None, in_span=None, span_id=None, is_prefix=None, targets=None):
+        """Cocktail-party scores and loss, or LM logits and loss (model.py:180-314)."""
+        if in_span is None or span_id is None or is_prefix is None:
+            in_span, span_id, is_prefix = derive_metadata(tokens, rule="fallback")
+        h = self.hidden(tokens, in_span, span_id, is_prefix)
+        if (tokens == MASK).any() and (tokens == SPAN).any() and (tokens == ES).any():
+            scores = span_scores(tokens, h)
+            loss = F.cross_entropy(scores, correct_idx) if correct_idx is not None else None
+            return scores, loss
+        logits = self.head(h)
+        loss = None
+        if targets is not None:
+            loss = F.cross_entropy(logits.view(-1, logits.size(-1)), targets.view(-1), ignore_index=0)
+        return logits, loss
+
+
+def span_scores(tokens: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
+    """``<h at first [MASK], mean h over each span's interior>`` per row and span."""
+    B, T, D = h.shape
+    is_mask = tokens == MASK
+    first = is_mask & (torch.cumsum(is_mask.to(torch.int32), dim=1) == 1)
+    h_ctx = (h * first[..., None].to(h.dtype)).sum(dim=1)  # zero row if no [MASK]
+    starts = (tokens == SPAN).to(torch.int64)
+    sid = torch.cumsum(starts, dim=1)  # span j (1-based) from its [SPAN] on
+    ends = torch.cumsum((tokens == ES).to(torch.int64), dim=1)
+    inside = (sid > ends) & (tokens != SPAN)  # strictly between [SPAN] and its [ES]
+    n_spans = int(starts.sum(dim=1).max().item())
+    slot = torch.where(inside, torch.arange(B, device=h.device)[:, None] * n_spans + sid - 1,
+                       torch.full_like(sid, B * n_spans))
+    acc = torch.zeros(B * n_spans + 1, D, dtype=torch.float32, device=h.device)
+    acc.index_add_(0, slot.view(-1), h.reshape(-1, D).float())
+    cnt = torch.zeros(B * n_spans + 1, dtype=torch.float32, device=h.device)
+    cnt.index_add_(0, slot.view(-1), torch.ones(B * T, dtype=torch.float32, device=h.device))
+    h_spans = (acc[:-1] / cnt[:-1].clamp_min(1.0)[:, None]).view(B, n_spans, D)
+    # scores in fp32: at random init they are O(500) and nearly equal, so a
+    # bf16 product (spacing 2 there) would decide the loss by its rounding;
+    # [B, n, D] @ [B, D, 1] with a contiguous right operand
+    return torch.bmm(h_spans, h_ctx.float().unsqueeze(-1).contiguous()).squeeze(-1)
+
+
+def config5_batch(B=8, L=2048, seed=0):
+    """Config-3-generator sequences at L, collate metadata, seeded correct_idx."""
+    from .synth import CONFIG3_LAYOUT, cocktail_batch
+
+    tokens, in_span, span_id, is_prefix = cocktail_batch(B, L, CONFIG3_LAYOUT, seed)
+    n_spans = (tokens == SPAN).sum(dim=1)
+    g = torch.Generator("cpu").manual_seed(seed + 7)
+    correct = (torch.rand(B, generator=g) * n_spans.to(torch.float32)).to(torch.int64)
+    return tokens, in_span, span_id, is_prefix, correct
+
+
+__all__ = ["GPTModel", "span_scores", "config5_batch", "VOCAB", "CLS", "MASKQ"]
