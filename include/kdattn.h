@@ -81,6 +81,10 @@ typedef struct kd_attn_args {
   void *o_lo;                   /* optional contiguous [B, H, T, D], dtype of o: the
                                    forward writes O_fp32 - O there, the backward's Delta
                                    reads it; NULL to skip */
+  const uint8_t *q8, *k8;       /* optional fp8 e4m3 copies of q and k, contiguous
+                                   [B, H, T, D] (kd_quant_fp8): when both are given, S = Q K^T
+                                   is computed from them on fp8 MFMA, times q_scale * k_scale */
+  const float *q_scale, *k_scale; /* [B, H] dequantisation scales of q8 / k8 */
   int32_t B, H, T, D;
   int32_t dtype;                /* KD_BF16 / KD_F16 */
   float sm_scale;
@@ -99,6 +103,19 @@ typedef struct kd_rot_args {
   int32_t inverse;              /* 0: y = x R;  1: y = x R^T */
 } kd_rot_args;
 
+/* Per-(b, h) fp8 e4m3 quantisation: y = e4m3(clamp(x * fp32(448 / amax), +-448)),
+ * round to nearest even, scale = amax / 448 (amax == 0: both factors 1). */
+typedef struct kd_quant_args {
+  const void *x;                /* [B, H, T, D] bf16 / fp16 */
+  int64_t x_strides[3];
+  uint8_t *y;                   /* contiguous [B, H, T, D] e4m3 bytes */
+  const float *amax;            /* [B, H] max |x| (kd_hadamard can produce it) */
+  float *scale;                 /* [B, H] output: amax / 448 */
+  int32_t B, H, T, D;
+  int32_t dtype;
+  int32_t pad_;
+} kd_quant_args;
+
 /* Library version (major*10000 + minor*100 + patch). */
 int kd_version(void);
 
@@ -107,7 +124,7 @@ const char *kd_last_error_string(void);
 
 /* sizeof(kd_meta_args), sizeof(kd_attn_args): lets bindings check layouts. */
 void kd_struct_sizes(size_t *meta, size_t *attn);
-void kd_struct_sizes2(size_t *rot);
+void kd_struct_sizes2(size_t *rot, size_t *quant);
 
 /* Workspace ("plan") bytes for B sequences of length T at head dim D, and
  * the byte offsets of its sections (codes, class map, per-tile allowed
@@ -158,6 +175,11 @@ int kd_mask_dense(const void *plan, int32_t B, int32_t H, int32_t T, int32_t D, 
  * max |y| per (b, h) into amax.  The reference only names this operation
  * (README.md:68-71, :77: generate_hadamard_signs / hadamard_transform). */
 int kd_hadamard(const kd_rot_args *a, void *stream);
+
+/* fp8 e4m3 copy of a rotated Q or K for the fp8 QK^T variant of the
+ * attention kernels (kd_attn_args.q8 / k8).  No counterpart in the reference,
+ * which has no fp8 path; the operation is specified by the build. */
+int kd_quant_fp8(const kd_quant_args *a, void *stream);
 
 #ifdef __cplusplus
 }

@@ -50,6 +50,7 @@ class AttnArgs(ctypes.Structure):
         ("dq", c_void_p), ("dk", c_void_p), ("dv", c_void_p),
         ("dq_strides", I64x3), ("dk_strides", I64x3), ("dv_strides", I64x3),
         ("delta", c_void_p), ("o_lo", c_void_p),
+        ("q8", c_void_p), ("k8", c_void_p), ("q_scale", c_void_p), ("k_scale", c_void_p),
         ("B", c_int32), ("H", c_int32), ("T", c_int32), ("D", c_int32),
         ("dtype", c_int32), ("sm_scale", c_float),
     ]
@@ -67,13 +68,25 @@ class RotArgs(ctypes.Structure):
     ]
 
 
+class QuantArgs(ctypes.Structure):
+    """Mirror of ``kd_quant_args``."""
+
+    _fields_ = [
+        ("x", c_void_p), ("x_strides", I64x3),
+        ("y", c_void_p), ("amax", c_void_p), ("scale", c_void_p),
+        ("B", c_int32), ("H", c_int32), ("T", c_int32), ("D", c_int32),
+        ("dtype", c_int32), ("pad_", c_int32),
+    ]
+
+
 # name -> (restype, argtypes); every symbol include/kdattn.h declares
 SIGNATURES = {
     "kd_version": (c_int, []),
     "kd_last_error_string": (c_char_p, []),
     "kd_struct_sizes": (None, [POINTER(c_size_t), POINTER(c_size_t)]),
-    "kd_struct_sizes2": (None, [POINTER(c_size_t)]),
+    "kd_struct_sizes2": (None, [POINTER(c_size_t), POINTER(c_size_t)]),
     "kd_hadamard": (c_int, [POINTER(RotArgs), c_void_p]),
+    "kd_quant_fp8": (c_int, [POINTER(QuantArgs), c_void_p]),
     "kd_plan_bytes": (c_int64, [c_int32, c_int32, c_int32]),
     "kd_plan_layout": (c_int, [c_int32, c_int32, c_int32, POINTER(c_int64)]),
     "kd_plan_build": (c_int, [POINTER(MetaArgs), c_void_p, c_void_p]),
@@ -109,14 +122,14 @@ def load():
         fn.argtypes = args
     ms, as_ = c_size_t(), c_size_t()
     lib.kd_struct_sizes(ctypes.byref(ms), ctypes.byref(as_))
-    rs = c_size_t()
-    lib.kd_struct_sizes2(ctypes.byref(rs))
+    rs, qs = c_size_t(), c_size_t()
+    lib.kd_struct_sizes2(ctypes.byref(rs), ctypes.byref(qs))
     if (ms.value != ctypes.sizeof(MetaArgs) or as_.value != ctypes.sizeof(AttnArgs)
-            or rs.value != ctypes.sizeof(RotArgs)):
+            or rs.value != ctypes.sizeof(RotArgs) or qs.value != ctypes.sizeof(QuantArgs)):
         raise ImportError(
-            f"struct layout mismatch: C meta={ms.value} attn={as_.value} rot={rs.value}, "
+            f"struct layout mismatch: C meta={ms.value} attn={as_.value} rot={rs.value} quant={qs.value}, "
             f"ctypes meta={ctypes.sizeof(MetaArgs)} attn={ctypes.sizeof(AttnArgs)} "
-            f"rot={ctypes.sizeof(RotArgs)}")
+            f"rot={ctypes.sizeof(RotArgs)} quant={ctypes.sizeof(QuantArgs)}")
     _lib = lib
     return lib
 

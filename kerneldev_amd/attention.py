@@ -98,10 +98,30 @@ def _attn_args(q, k, v, sm_scale) -> AttnArgs:
 
 
 # ----------------------------------------------------------------- custom ops
+def _set_fp8(a: AttnArgs, fp8):
+    """Point the kernels at the fp8 copies ``(q8, k8, q_scale, k_scale)``, or not."""
+    if fp8 is None:
+        return
+    q8, k8, qs, ks = fp8
+    a.q8, a.k8 = q8.data_ptr(), k8.data_ptr()
+    a.q_scale, a.k_scale = qs.data_ptr(), ks.data_ptr()
+
+
+def _fp8_tuple(q8, k8, q_scale, k_scale):
+    parts = (q8, k8, q_scale, k_scale)
+    if all(x is None for x in parts):
+        return None
+    if any(x is None for x in parts):
+        raise ValueError("q8, k8, q_scale and k_scale go together")
+    return parts
+
+
 @torch.library.custom_op("kdattn::fwd", mutates_args=(), device_types=("cuda",))
 def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tensor | None,
             in_span: torch.Tensor | None, span_id: torch.Tensor | None,
-            is_prefix: torch.Tensor | None, sm_scale: float, mode: int, need_lo: bool
+            is_prefix: torch.Tensor | None, sm_scale: float, mode: int, need_lo: bool,
+            q8: torch.Tensor | None = None, k8: torch.Tensor | None = None,
+            q_scale: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     B, H, T, D = q.shape
     plan = build_plan(B, T, D, q.device, mode, in_span, span_id, is_prefix, lens)
@@ -110,6 +130,7 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
     # rounding residual of O, kept for the backward's Delta (see kd_bwd.hip)
     o_lo = torch.empty((B, H, T, D) if need_lo else (0,), dtype=q.dtype, device=q.device)
     a = _attn_args(q, k, v, sm_scale)
+    _set_fp8(a, _fp8_tuple(q8, k8, q_scale, k_scale))
     a.o, a.o_strides = o.data_ptr(), _strides3(o)
     a.lse = lse.data_ptr()
     a.o_lo = o_lo.data_ptr() if need_lo else None
@@ -118,7 +139,8 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
 
 
 @_fwd_op.register_fake
-def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo):
+def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8=None, k8=None,
+              q_scale=None, k_scale=None):
     B, H, T, D = q.shape
     return (torch.empty((B, H, T, D), dtype=q.dtype, device=q.device),
             torch.empty((B, H, T), dtype=torch.float32, device=q.device),
@@ -128,7 +150,9 @@ def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_l
 
 @torch.library.custom_op("kdattn::bwd", mutates_args=(), device_types=("cuda",))
 def _bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, lse: torch.Tensor,
-            do: torch.Tensor, plan: torch.Tensor, sm_scale: float, o_lo: torch.Tensor
+            do: torch.Tensor, plan: torch.Tensor, sm_scale: float, o_lo: torch.Tensor,
+            q8: torch.Tensor | None = None, k8: torch.Tensor | None = None,
+            q_scale: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     B, H, T, D = q.shape
     do = _kernel_ready(do)
@@ -144,27 +168,32 @@ def _bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, 
     a.dq_strides, a.dk_strides, a.dv_strides = _strides3(dq), _strides3(dk), _strides3(dv)
     a.delta = delta.data_ptr()
     a.o_lo = o_lo.data_ptr() if o_lo.numel() > 0 else None
+    _set_fp8(a, _fp8_tuple(q8, k8, q_scale, k_scale))
     _lib.check(_lib.load().kd_attn_bwd(ctypes.byref(a), _ptr(plan), _stream(q.device)), "kd_attn_bwd")
     return dq, dk, dv
 
 
 @_bwd_op.register_fake
-def _bwd_fake(q, k, v, o, lse, do, plan, sm_scale, o_lo):
+def _bwd_fake(q, k, v, o, lse, do, plan, sm_scale, o_lo, q8=None, k8=None, q_scale=None, k_scale=None):
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
 def _setup_context(ctx, inputs, output):
-    q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo = inputs
+    q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8, k8, q_scale, k_scale = inputs
     o, lse, plan, o_lo = output
-    ctx.save_for_backward(q, k, v, o, lse, plan, o_lo)
+    ctx.fp8 = q8 is not None
+    extra = (q8, k8, q_scale, k_scale) if ctx.fp8 else ()
+    ctx.save_for_backward(q, k, v, o, lse, plan, o_lo, *extra)
     ctx.sm_scale = sm_scale
 
 
 def _backward(ctx, do, dlse, dplan, do_lo):
-    # dlse is ignored, as in original_kernel.py:1965-1992
-    q, k, v, o, lse, plan, o_lo = ctx.saved_tensors
-    dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, ctx.sm_scale, o_lo)
-    return dq, dk, dv, None, None, None, None, None, None, None
+    # dlse is ignored, as in original_kernel.py:1965-1992.  With fp8 scores the
+    # backward recomputes P from the same fp8 Q8 K8^T and forms dQ = dS K,
+    # dK = dS^T Q from the 16-bit operands: the straight-through estimator.
+    q, k, v, o, lse, plan, o_lo, *extra = ctx.saved_tensors
+    dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, ctx.sm_scale, o_lo, *extra)
+    return dq, dk, dv, None, None, None, None, None, None, None, None, None, None, None
 
 
 _fwd_op.register_autograd(_backward, setup_context=_setup_context)
@@ -244,8 +273,8 @@ def flash_attention(
         raise ValueError("flash_attention runs on the GPU only (no CPU fallback)")
     if k.device != q.device or v.device != q.device:
         raise ValueError("q, k and v must be on the same device")
-    if qk_dtype != "bf16":
-        raise NotImplementedError("fp8 QK^T path is not built yet")
+    if qk_dtype == "fp8_e4m3" and (D != 128 or q.dtype not in (torch.bfloat16, torch.float32)):
+        raise ValueError("the fp8 QK^T path is built for head_dim 128 with bf16 (or fp32) inputs")
 
     if sm_scale is None:
         sm_scale = D ** -0.5  # original_kernel.py:2145-2147
@@ -264,17 +293,27 @@ def flash_attention(
         q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
     elif in_dtype not in (torch.bfloat16, torch.float16):
         raise ValueError(f"unsupported dtype {in_dtype}")
+    from .hadamard import generate_hadamard_signs, hadamard_absmax, hadamard_transform, quantize_fp8
+
+    amax_q = amax_k = None
     if hadamard:
         # (Q R)(K R)^T = Q K^T with R = diag(s) H_d / sqrt(d); autograd maps
-        # dQ' and dK' back through R^T (hadamard.py)
-        from .hadamard import generate_hadamard_signs, hadamard_transform
-
+        # dQ' and dK' back through R^T (hadamard.py).  For fp8 the rotation
+        # pass also yields the per-(b, h) absmax the scales need.
         signs = generate_hadamard_signs(D, hadamard_seed, device=device)
-        q, k = hadamard_transform(q, signs), hadamard_transform(k, signs)
+        if qk_dtype == "fp8_e4m3":
+            (q, amax_q), (k, amax_k) = hadamard_absmax(q, signs), hadamard_absmax(k, signs)
+        else:
+            q, k = hadamard_transform(q, signs), hadamard_transform(k, signs)
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    fp8 = ()
+    if qk_dtype == "fp8_e4m3":
+        (q8, q_scale), (k8, k_scale) = quantize_fp8(q, amax_q), quantize_fp8(k, amax_k)
+        fp8 = (q8, k8, q_scale, k_scale)
 
     need_lo = torch.is_grad_enabled() and any(x.requires_grad for x in (q, k, v))
-    o, lse, plan, _ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode), need_lo)
+    o, lse, plan, _ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode), need_lo,
+                              *fp8)
     if in_dtype == torch.float32:
         o = o.to(torch.float32)
 

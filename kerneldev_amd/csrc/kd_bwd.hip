@@ -99,14 +99,17 @@ KD_DEV void tr_addrs(int lane, int (&addr)[D / 32][2]) {
 }
 
 // ------------------------------------------------------------------- dQ ----
-template <class E, int D>
+template <class E, int D, bool Q8>
 __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __restrict__ codes,
                                                const uint32_t* __restrict__ list,
                                                const int32_t* __restrict__ count, int nT, int nQB) {
   using TL = Tile<D>;
-  constexpr int DS = D / 16, DB = D / 32, NL = TL::LOADS_PER_WAVE;
+  using SO = ScoreOp<E, D, Q8>;  // S^T = K Q^T (16-bit, or fp8 from the K8 tile)
+  using TK8 = typename ScoreOp<E, D, true>::TL;
+  constexpr int DS = D / 16, DB = D / 32, NL = TL::LOADS_PER_WAVE, NL8 = TK8::LOADS_PER_WAVE;
   __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][TL::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][TL::BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_k8[Q8 ? 2 : 1][Q8 ? TK8::BYTES : 16];
   __shared__ __attribute__((aligned(256))) uint32_t s_code[2][64];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
@@ -131,12 +134,12 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
 
   const int qrow = qblock * 128 + wave * 32 + c;
   const bool qvalid = qrow < T;
-  u32x4 qf[DS], dof[DS];
+  SO so;  // B operand: this lane's query row (Q, or its fp8 copy)
+  if constexpr (Q8) so.load_b(make_rsrc(a.q8 + int64_t(bh) * T * D, uint32_t(T) * D), uint32_t(qrow) * D, hf);
+  else so.load_b(rs_q, uint32_t(qrow) * qrb, hf);
+  u32x4 dof[DS];
 #pragma unroll
-  for (int st = 0; st < DS; ++st) {
-    qf[st] = buf_load16(rs_q, uint32_t(qrow) * qrb + (16 * st + 8 * hf) * 2);
-    dof[st] = buf_load16(rs_do, uint32_t(qrow) * dorb + (16 * st + 8 * hf) * 2);
-  }
+  for (int st = 0; st < DS; ++st) dof[st] = buf_load16(rs_do, uint32_t(qrow) * dorb + (16 * st + 8 * hf) * 2);
   const float INF = __builtin_inff();
   const float lse = qvalid ? a.delta[BHT + int64_t(bh) * T + qrow] : INF;
   const float delta = qvalid ? a.delta[int64_t(bh) * T + qrow] : 0.f;
@@ -146,25 +149,32 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
   const int n = count[lbase];
   const uint32_t* ent = list + int64_t(lbase) * nT;
 
-  uint32_t koff[NL], voff[NL];
+  uint32_t koff[NL], voff[NL], k8off[NL8];
   TL::load_offsets(wave, lane, krb, koff);
   TL::load_offsets(wave, lane, vrb, voff);
+  TK8::load_offsets(wave, lane, uint32_t(D), k8off);
+  const auto rs_k8 = make_rsrc(Q8 ? a.k8 + int64_t(bh) * T * D : nullptr, Q8 ? uint32_t(T) * D : 0u);
   auto load_tile = [&](int kt, int buf) {
     const uint32_t k0 = uint32_t(kt) * 64u;
     TL::load(rs_k, k0 * krb, koff, s_k[buf], wave);
     TL::load(rs_v, k0 * vrb, voff, s_v[buf], wave);
+    if constexpr (Q8) TK8::load(rs_k8, k0 * uint32_t(D), k8off, s_k8[buf], wave);
     if (wave == 0)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_t*)&s_code[buf][0], 4, (k0 + lane) * 4u, 0, 0, 0);
   };
 
   const int srow = sigma(c);
+  so.init(srow, hf);
   int raddr[DS];
 #pragma unroll
   for (int st = 0; st < DS; ++st) raddr[st] = TL::at(srow, 2 * st + hf);
   int taddr[DB][2];
   tr_addrs<D>(lane, taddr);
+  const MaskTab mt = qmask(qcode);
+  const int i_lo = qblock * 128 + wave * 32;
 
-  const float sl2 = a.sm_scale * 1.4426950408889634f;
+  // the fp8 product carries the dequantisation scales of Q and K
+  const float sl2 = a.sm_scale * 1.4426950408889634f * (Q8 ? a.q_scale[bh] * a.k_scale[bh] : 1.f);
   const float NEG_INF = -INF;
   f32x16 acc[DB];
 #pragma unroll
@@ -182,21 +192,22 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
     const uint8_t* vt = s_v[buf];
 
     f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
+    so.mma(Q8 ? s_k8[buf & (Q8 ? 1 : 0)] : kt, 0, s[0]);
+    so.mma(Q8 ? s_k8[buf & (Q8 ? 1 : 0)] : kt, 1, s[1]);
 #pragma unroll
     for (int st = 0; st < DS; ++st) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const int off = raddr[st] + kb * 32 * TL::ROWB;
-        const u32x4 ak = *reinterpret_cast<const u32x4*>(kt + off);
-        const u32x4 av = *reinterpret_cast<const u32x4*>(vt + off);
-        s[kb] = mfma32x32x16<E>(ak, qf[st], s[kb]);
+        const u32x4 av = *reinterpret_cast<const u32x4*>(vt + raddr[st] + kb * 32 * TL::ROWB);
         dp[kb] = mfma32x32x16<E>(av, dof[st], dp[kb]);
       }
     }
-    if (!(cur & 1u)) {
+    if (!(cur & 1u)) {  // PARTIAL tile: register r of s[kb] holds key k0 + 32 kb + 16 (r / 8) + 8 hf + r % 8
       const int k0 = int(cur >> 1) * 64;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
+        const int j0 = k0 + 32 * kb;
+        const bool below = j0 + 31 <= i_lo, above = j0 > i_lo + 31;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const int jl = 32 * kb + 16 * t + 8 * hf;
@@ -205,7 +216,9 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
 #pragma unroll
           for (int x = 0; x < 8; ++x) {
             const uint32_t kc = x < 4 ? c0[x] : c1[x - 4];
-            if (!allow(qcode, kc, qrow, k0 + jl + x)) s[kb][8 * t + x] = NEG_INF;
+            uint32_t tbl = below ? mt.hi : mt.lo;
+            if (!below && !above) tbl = (k0 + jl + x <= qrow) ? mt.hi : mt.lo;
+            s[kb][8 * t + x] = mask_score(s[kb][8 * t + x], tbl, kc, kc, mt.rsh);
           }
         }
       }
@@ -254,14 +267,17 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
 // about half the registers of one wave doing all four products, and the
 // pair shares a SIMD (waves w and w + 4), so one wave's VALU softmax runs
 // under the other's MFMAs.
-template <class E, int D>
+template <class E, int D, bool Q8>
 __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __restrict__ codes,
                                                  const uint32_t* __restrict__ list,
                                                  const int32_t* __restrict__ count, int nT, int nKB) {
   constexpr int NW = 8;
   using TL = Tile<D, NW>;
-  constexpr int DS = D / 16, DB = D / 32, NL = TL::LOADS_PER_WAVE;
+  using SO8 = ScoreOp<E, D, true>;  // fp8 S = Q8 K8^T of the P waves
+  using TQ8 = Tile<Q8 ? D / 2 : D, NW>;  // only instantiated at D = 128 for fp8
+  constexpr int DS = D / 16, DB = D / 32, NL = TL::LOADS_PER_WAVE, NL8 = TQ8::LOADS_PER_WAVE;
   __shared__ __attribute__((aligned(1024))) uint8_t s_q[2][TL::BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_q8[Q8 ? 2 : 1][Q8 ? TQ8::BYTES : 16];
   __shared__ __attribute__((aligned(1024))) uint8_t s_do[2][TL::BYTES];
   __shared__ __attribute__((aligned(1024))) float s_p[4][2 * 16][64];  // [pair][register][lane]
   __shared__ __attribute__((aligned(256))) float s_lse[2][64];
@@ -293,25 +309,33 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   const int krow = kblock * 128 + pair * 32 + c;
   const bool kvalid = krow < T;
   u32x4 bf[DS];
-  {
+  SO8 so8;  // fp8: the P waves' B operand is this lane's row of K8 instead
+  if (Q8 && role == 0) {
+    so8.load_b(make_rsrc(a.k8 + int64_t(bh) * T * D, uint32_t(T) * D), uint32_t(krow) * D, hf);
+  } else {
     const auto rs_b = role == 0 ? make_rsrc(kg, uint32_t(T) * krb) : make_rsrc(vg, uint32_t(T) * vrb);
     const uint32_t brb = role == 0 ? krb : vrb;
 #pragma unroll
     for (int st = 0; st < DS; ++st) bf[st] = buf_load16(rs_b, uint32_t(krow) * brb + (16 * st + 8 * hf) * 2);
   }
   const uint32_t kcode = kvalid ? codes[int64_t(b) * T + krow] : 0u;
+  const MaskTab mt = kmask(kcode);
+  const int j_lo = kblock * 128 + pair * 32;
 
   const int lbase = b * nKB + kblock;
   const int n = count[lbase];
   const uint32_t* ent = list + int64_t(lbase) * nT;
 
-  uint32_t qoff[NL], dooff[NL];
+  uint32_t qoff[NL], dooff[NL], q8off[NL8];
   TL::load_offsets(wave, lane, qrb, qoff);
   TL::load_offsets(wave, lane, dorb, dooff);
+  TQ8::load_offsets(wave, lane, uint32_t(D), q8off);
+  const auto rs_q8 = make_rsrc(Q8 ? a.q8 + int64_t(bh) * T * D : nullptr, Q8 ? uint32_t(T) * D : 0u);
   auto load_tile = [&](int qt, int buf) {
     const uint32_t q0 = uint32_t(qt) * 64u;
     TL::load(rs_q, q0 * qrb, qoff, s_q[buf], wave);
     TL::load(rs_do, q0 * dorb, dooff, s_do[buf], wave);
+    if constexpr (Q8) TQ8::load(rs_q8, q0 * uint32_t(D), q8off, s_q8[buf], wave);
     if (wave == 0)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, (lds_t*)&s_lse[buf][0], 4, (q0 + lane) * 4u, 0, 0, 0);
     else if (wave == 1)
@@ -321,14 +345,15 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   };
 
   const int srow = sigma(c);
+  if constexpr (Q8) so8.init(srow, hf);
   int raddr[DS];
 #pragma unroll
   for (int st = 0; st < DS; ++st) raddr[st] = TL::at(srow, 2 * st + hf);
   int taddr[DB][2];
   tr_addrs<D>(lane, taddr);
 
-  const float sl2 = a.sm_scale * 1.4426950408889634f;
-  const float NEG_INF = -__builtin_inff();
+  // the fp8 product carries the dequantisation scales of Q and K
+  const float sl2 = a.sm_scale * 1.4426950408889634f * (Q8 ? a.q_scale[bh] * a.k_scale[bh] : 1.f);
   f32x16 acc[DB];  // dV^T (role 0) or dK^T (role 1)
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
@@ -352,19 +377,26 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
     // S (role 0) or dP (role 1) for the two 32-query halves; register r of
     // x[qb] holds query 32 qb + 16 (r / 8) + 8 hf + r % 8 of this lane's key
     f32x16 x[2] = {f32x16{}, f32x16{}};
+    if (Q8 && role == 0) {
+      so8.mma(s_q8[buf & (Q8 ? 1 : 0)], 0, x[0]);
+      so8.mma(s_q8[buf & (Q8 ? 1 : 0)], 1, x[1]);
+    } else {
 #pragma unroll
-    for (int st = 0; st < DS; ++st) {
+      for (int st = 0; st < DS; ++st) {
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        const u32x4 ar = *reinterpret_cast<const u32x4*>(arow + raddr[st] + qb * 32 * TL::ROWB);
-        x[qb] = mfma32x32x16<E>(ar, bf[st], x[qb]);
+        for (int qb = 0; qb < 2; ++qb) {
+          const u32x4 ar = *reinterpret_cast<const u32x4*>(arow + raddr[st] + qb * 32 * TL::ROWB);
+          x[qb] = mfma32x32x16<E>(ar, bf[st], x[qb]);
+        }
       }
     }
     u32x4 bop[2][2];  // packed P (role 0) or dS (role 1): B operand of k-step 2 qb + t
     if (role == 0) {
-      if (!(cur & 1u)) {  // PARTIAL tile
+      if (!(cur & 1u)) {  // PARTIAL tile: queries i = q0 + ql + j against this lane's key
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < 2; ++qb) {
+          const int i0 = q0 + 32 * qb;
+          const bool after = i0 >= j_lo + 31, before = i0 + 31 < j_lo;
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
             const int ql = 32 * qb + 16 * t + 8 * hf;
@@ -373,9 +405,12 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
               const uint32_t qc = j < 4 ? c0[j] : c1[j - 4];
-              if (!allow(qc, kcode, q0 + ql + j, krow)) x[qb][8 * t + j] = NEG_INF;
+              uint32_t tbl = after ? mt.hi : mt.lo;
+              if (!after && !before) tbl = (q0 + ql + j >= krow) ? mt.hi : mt.lo;
+              x[qb][8 * t + j] = mask_score(x[qb][8 * t + j], tbl, qc >> 3, qc, mt.rsh);
             }
           }
+        }
       }
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb)
@@ -442,19 +477,19 @@ static void launch_delta_t(const AttnArgs& a, hipStream_t st) {
   const int64_t rows = int64_t(a.B) * a.H * a.T;
   hipLaunchKernelGGL((k_delta<E, D>), dim3(unsigned((rows + RPB - 1) / RPB)), dim3(256), 0, st, a);
 }
-template <class E, int D>
+template <class E, int D, bool Q8 = false>
 static void launch_dq_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dq_blocks;
-  hipLaunchKernelGGL((k_dq<E, D>), dim3(grid), dim3(256), 0, st, a, reinterpret_cast<const uint32_t*>(plan + L.codes),
+  hipLaunchKernelGGL((k_dq<E, D, Q8>), dim3(grid), dim3(256), 0, st, a, reinterpret_cast<const uint32_t*>(plan + L.codes),
                      reinterpret_cast<const uint32_t*>(plan + L.dq_list),
                      reinterpret_cast<const int32_t*>(plan + L.dq_count), L.nT, L.n_dq_blocks);
 }
-template <class E, int D>
+template <class E, int D, bool Q8 = false>
 static void launch_dkdv_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dkdv_blocks;
-  hipLaunchKernelGGL((k_dkdv<E, D>), dim3(grid), dim3(512), 0, st, a,
+  hipLaunchKernelGGL((k_dkdv<E, D, Q8>), dim3(grid), dim3(512), 0, st, a,
                      reinterpret_cast<const uint32_t*>(plan + L.codes),
                      reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
                      reinterpret_cast<const int32_t*>(plan + L.dkdv_count), L.nT, L.n_dkdv_blocks);
@@ -476,11 +511,13 @@ int launch_delta(const AttnArgs& a, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 int launch_dq(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
-  KD_DISPATCH(launch_dq_t, a, plan, st);
+  if (a.q8 != nullptr) launch_dq_t<BF16, 128, true>(a, plan, st);  // fp8 QK^T (checked by the C ABI)
+  else KD_DISPATCH(launch_dq_t, a, plan, st);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 int launch_dkdv(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
-  KD_DISPATCH(launch_dkdv_t, a, plan, st);
+  if (a.q8 != nullptr) launch_dkdv_t<BF16, 128, true>(a, plan, st);  // fp8 QK^T (checked by the C ABI)
+  else KD_DISPATCH(launch_dkdv_t, a, plan, st);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 

@@ -80,8 +80,23 @@ void kd_struct_sizes(size_t* meta, size_t* attn) {
   if (attn) *attn = sizeof(kd_attn_args);
 }
 
-void kd_struct_sizes2(size_t* rot) {
+void kd_struct_sizes2(size_t* rot, size_t* quant) {
   if (rot) *rot = sizeof(kd_rot_args);
+  if (quant) *quant = sizeof(kd_quant_args);
+}
+
+int kd_quant_fp8(const kd_quant_args* a, void* stream) {
+  if (a == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
+  if (a->B < 1 || a->H < 1 || a->T < 1) return fail(KD_ERR_INVALID, "B, H and T must be >= 1");
+  if (a->D != 64 && a->D != 128) return fail(KD_ERR_UNSUPPORTED, "head dim must be 64 or 128");
+  if (a->dtype != KD_BF16 && a->dtype != KD_F16) return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16 or fp16");
+  if (a->amax == nullptr || a->scale == nullptr || a->y == nullptr)
+    return fail(KD_ERR_INVALID, "amax, scale and y are required");
+  if (!aligned16(a->y)) return fail(KD_ERR_INVALID, "y must be 16-byte aligned");
+  int r;
+  if ((r = check_tensor(a->x, a->x_strides, "x", a->T, a->D))) return r;
+  r = kd::launch_quant(*a, as_stream(stream));
+  return r ? fail(r, "kernel launch failed (quant)") : KD_OK;
 }
 
 int kd_hadamard(const kd_rot_args* a, void* stream) {
@@ -130,9 +145,20 @@ int kd_plan_build(const kd_meta_args* m, void* plan, void* stream) {
   return kd::launch_plan(*m, static_cast<uint8_t*>(plan), as_stream(stream));
 }
 
+static int check_fp8(const kd_attn_args* a) {
+  if ((a->q8 == nullptr) != (a->k8 == nullptr)) return fail(KD_ERR_INVALID, "q8 and k8 go together");
+  if (a->q8 == nullptr) return KD_OK;
+  if (a->D != 128) return fail(KD_ERR_UNSUPPORTED, "the fp8 QK^T path is built for head dim 128");
+  if (a->dtype != KD_BF16) return fail(KD_ERR_UNSUPPORTED, "the fp8 QK^T path is built for bf16");
+  if (!aligned16(a->q8) || !aligned16(a->k8)) return fail(KD_ERR_INVALID, "q8 and k8 must be 16-byte aligned");
+  if (a->q_scale == nullptr || a->k_scale == nullptr) return fail(KD_ERR_INVALID, "q_scale and k_scale are required");
+  return KD_OK;
+}
+
 int kd_attn_fwd(const kd_attn_args* a, const void* plan, void* stream) {
   int r = check_common(a);
   if (r) return r;
+  if ((r = check_fp8(a))) return r;
   if (plan == nullptr) return fail(KD_ERR_INVALID, "plan is NULL");
   if ((r = check_tensor(a->q, a->q_strides, "q", a->T, a->D)) || (r = check_tensor(a->k, a->k_strides, "k", a->T, a->D)) ||
       (r = check_tensor(a->v, a->v_strides, "v", a->T, a->D)) || (r = check_tensor(a->o, a->o_strides, "o", a->T, a->D)))
@@ -156,6 +182,7 @@ int kd_attn_bwd_delta(const kd_attn_args* a, void* stream) {
 static int check_bwd(const kd_attn_args* a, const void* plan) {
   int r = check_common(a);
   if (r) return r;
+  if ((r = check_fp8(a))) return r;
   if (plan == nullptr) return fail(KD_ERR_INVALID, "plan is NULL");
   if (a->lse == nullptr || a->delta == nullptr) return fail(KD_ERR_INVALID, "lse and delta are required");
   if ((r = check_tensor(a->q, a->q_strides, "q", a->T, a->D)) || (r = check_tensor(a->k, a->k_strides, "k", a->T, a->D)) ||

@@ -31,15 +31,17 @@
 
 namespace kd {
 
-template <class E, int D>
+template <class E, int D, bool Q8>
 __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __restrict__ codes,
                                                 const uint32_t* __restrict__ list,
                                                 const int32_t* __restrict__ count, int nT, int nQB) {
-  using TL = Tile<D>;
-  constexpr int DS = D / 16;  // 16-wide k-steps of S^T over d
+  using TL = Tile<D>;           // V tiles (and K tiles on the 16-bit path)
+  using SO = ScoreOp<E, D, Q8>;  // S^T = K Q^T, 16-bit or fp8
+  using TK = typename SO::TL;   // K tiles
   constexpr int DB = D / 32;  // 32-row blocks of O^T
   constexpr int NL = TL::LOADS_PER_WAVE;
-  __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][TL::BYTES];
+  constexpr int NLK = TK::LOADS_PER_WAVE;
+  __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][TK::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][TL::BYTES];
   __shared__ __attribute__((aligned(256))) uint32_t s_code[2][64];
 
@@ -50,37 +52,43 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
   const int qblock = nQB - 1 - (work % nQB);  // heaviest (latest) q-blocks first
   const int b = hb % a.B, h = hb / a.B, bh = b * H + h;
 
-  const uint16_t* qg = static_cast<const uint16_t*>(a.q) + b * a.q_strides[0] + h * a.q_strides[1];
-  const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_strides[0] + h * a.k_strides[1];
+  // Q and K as the score product sees them: the 16-bit inputs, or their
+  // contiguous fp8 copies (kd_quant_fp8)
+  const void* qs_base = Q8 ? static_cast<const void*>(a.q8 + int64_t(bh) * T * D)
+                           : static_cast<const void*>(static_cast<const uint16_t*>(a.q) + b * a.q_strides[0] +
+                                                      h * a.q_strides[1]);
+  const void* ks_base = Q8 ? static_cast<const void*>(a.k8 + int64_t(bh) * T * D)
+                           : static_cast<const void*>(static_cast<const uint16_t*>(a.k) + b * a.k_strides[0] +
+                                                      h * a.k_strides[1]);
+  const uint32_t qrb = Q8 ? uint32_t(D) : uint32_t(a.q_strides[2]) * 2u;
+  const uint32_t krb = Q8 ? uint32_t(D) : uint32_t(a.k_strides[2]) * 2u;
   const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_strides[0] + h * a.v_strides[1];
-  const uint32_t qrb = uint32_t(a.q_strides[2]) * 2u, krb = uint32_t(a.k_strides[2]) * 2u,
-                 vrb = uint32_t(a.v_strides[2]) * 2u;
-  const auto rs_q = make_rsrc(qg, uint32_t(T) * qrb);
-  const auto rs_k = make_rsrc(kg, uint32_t(T) * krb);
+  const uint32_t vrb = uint32_t(a.v_strides[2]) * 2u;
+  const auto rs_q = make_rsrc(qs_base, uint32_t(T) * qrb);
+  const auto rs_k = make_rsrc(ks_base, uint32_t(T) * krb);
   const auto rs_v = make_rsrc(vg, uint32_t(T) * vrb);
   const auto rs_c = make_rsrc(codes + int64_t(b) * T, uint32_t(T) * 4u);
 
   // ---- per-lane query row (B operand of S^T, kept in registers) ----
   const int qrow = qblock * 128 + wave * 32 + c;
   const bool qvalid = qrow < T;
-  u32x4 qf[DS];
-#pragma unroll
-  for (int st = 0; st < DS; ++st) qf[st] = buf_load16(rs_q, uint32_t(qrow) * qrb + (16 * st + 8 * hf) * 2);
+  SO so;
+  so.load_b(rs_q, uint32_t(qrow) * qrb, hf);
   const uint32_t qcode = qvalid ? codes[int64_t(b) * T + qrow] : 0u;
 
   const int lbase = b * nQB + qblock;
   const int n = count[lbase];
   const uint32_t* ent = list + int64_t(lbase) * nT;
 
-  uint32_t koff[NL], voff[NL];
-  TL::load_offsets(wave, lane, krb, koff);
+  uint32_t koff[NLK], voff[NL];
+  TK::load_offsets(wave, lane, krb, koff);
   TL::load_offsets(wave, lane, vrb, voff);
   // K tiles run one step ahead of V tiles (S of tile e+1 is computed while
   // tile e is softmaxed), so they are loaded separately; the key codes of a
   // tile travel with its V tile.
   auto load_k = [&](int e) {
     const uint32_t k0 = uint32_t(ent[e] >> 1) * 64u;
-    TL::load(rs_k, k0 * krb, koff, s_k[e & 1], wave);
+    TK::load(rs_k, k0 * krb, koff, s_k[e & 1], wave);
   };
   auto load_v = [&](int e) {
     const uint32_t k0 = uint32_t(ent[e] >> 1) * 64u;
@@ -90,11 +98,9 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
   };
 
   // ---- LDS read addresses (bytes within a tile) ----
-  // K operand: row 32 kb + sigma(c), chunk 2 st + hf
+  // K operand: row 32 kb + sigma(c), this lane's k-slots of each k-step
   const int srow = sigma(c);
-  int kaddr[DS];
-#pragma unroll
-  for (int st = 0; st < DS; ++st) kaddr[st] = TL::at(srow, 2 * st + hf);
+  so.init(srow, hf);
   // V^T operand via transposed reads: group g = lane / 16 covers d columns
   // 32 db + 16 (g & 1) .. +15 and key rows 16 t4 + 8 (g >> 1) + 4 half .. +3
   int vaddr[DB][2];
@@ -113,16 +119,12 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
   auto scores = [&](const uint8_t* kt, f32x16 (&s)[2]) {
     s[0] = f32x16{};
     s[1] = f32x16{};
-#pragma unroll
-    for (int st = 0; st < DS; ++st)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const u32x4 ak = *reinterpret_cast<const u32x4*>(kt + kaddr[st] + kb * 32 * TL::ROWB);
-        s[kb] = mfma32x32x16<E>(ak, qf[st], s[kb]);
-      }
+    so.mma(kt, 0, s[0]);
+    so.mma(kt, 1, s[1]);
   };
 
-  const float sl2 = a.sm_scale * 1.4426950408889634f;
+  // the fp8 product carries the dequantisation scales of Q and K
+  const float sl2 = a.sm_scale * 1.4426950408889634f * (Q8 ? a.q_scale[bh] * a.k_scale[bh] : 1.f);
   const float NEG_INF = -__builtin_inff();
   float m_ref = NEG_INF, l0 = 0.f, l1 = 0.f, le0 = 0.f, le1 = 0.f;
   f32x16 o[DB];
@@ -262,19 +264,21 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
   }
 }
 
-template <class E, int D>
+template <class E, int D, bool Q8 = false>
 static void launch_fwd_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const int nQB = L.n_fwd_blocks;
   const unsigned grid = unsigned(a.B) * a.H * nQB;
-  hipLaunchKernelGGL((k_fwd<E, D>), dim3(grid), dim3(256), 0, st, a,
+  hipLaunchKernelGGL((k_fwd<E, D, Q8>), dim3(grid), dim3(256), 0, st, a,
                      reinterpret_cast<const uint32_t*>(plan + L.codes),
                      reinterpret_cast<const uint32_t*>(plan + L.fwd_list),
                      reinterpret_cast<const int32_t*>(plan + L.fwd_count), L.nT, nQB);
 }
 
 int launch_fwd(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
-  if (a.dtype == KD_BF16) {
+  if (a.q8 != nullptr) {  // fp8 QK^T: bf16, head dim 128 (checked by the C ABI)
+    launch_fwd_t<BF16, 128, true>(a, plan, st);
+  } else if (a.dtype == KD_BF16) {
     if (a.D == 64) launch_fwd_t<BF16, 64>(a, plan, st);
     else launch_fwd_t<BF16, 128>(a, plan, st);
   } else {

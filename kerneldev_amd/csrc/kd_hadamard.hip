@@ -96,6 +96,63 @@ __global__ __launch_bounds__(256) void k_hadamard(kd_rot_args a) {
   }
 }
 
+// ---- fp8 e4m3 quantisation per (b, h) -----------------------------------
+// y = e4m3(clamp(fp32(x * inv), -448, 448)) with inv = fp32(448 / amax), round
+// to nearest even (v_cvt_pk_fp8_f32 is OCP e4m3 on gfx950); scale = amax / 448.
+template <class E, int D>
+__global__ __launch_bounds__(256) void k_quant8(kd_quant_args a) {
+  constexpr int TPR = D / 8;
+  constexpr int RPB = 256 / TPR;
+  const int tid = threadIdx.x, seg = tid % TPR;
+  const int64_t row = int64_t(blockIdx.x) * RPB + tid / TPR;
+  const int64_t nrows = int64_t(a.B) * a.H * a.T;
+  if (row >= nrows) return;
+  const int t = int(row % a.T);
+  const int bh = int(row / a.T);
+  const int b = bh / a.H, h = bh % a.H;
+  const float am = a.amax[bh];
+  const float safe = am > 0.f ? am : 448.f;
+  const float inv = 448.f / safe;  // IEEE division (no fast-math)
+  if (t == 0 && seg == 0) a.scale[bh] = safe / 448.f;
+  const uint16_t* xp = static_cast<const uint16_t*>(a.x) + b * a.x_strides[0] + h * a.x_strides[1] +
+                       t * a.x_strides[2] + seg * 8;
+  const u32x4 xv = *reinterpret_cast<const u32x4*>(xp);
+  uint32_t w[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    float f[4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      f[2 * j] = to_f32<E>(uint16_t(xv[2 * k + j] & 0xFFFFu)) * inv;
+      f[2 * j + 1] = to_f32<E>(uint16_t(xv[2 * k + j] >> 16)) * inv;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f[j] = fminf(fmaxf(f[j], -448.f), 448.f);
+    int lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], 0, false);
+    w[k] = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], lo, true));
+  }
+  uint8_t* yp = a.y + row * D + seg * 8;
+  *reinterpret_cast<u32x2*>(yp) = u32x2{w[0], w[1]};
+}
+
+template <class E, int D>
+static void launch_quant_t(const kd_quant_args& a, hipStream_t st) {
+  constexpr int RPB = 256 / (D / 8);
+  const int64_t rows = int64_t(a.B) * a.H * a.T;
+  hipLaunchKernelGGL((k_quant8<E, D>), dim3(unsigned((rows + RPB - 1) / RPB)), dim3(256), 0, st, a);
+}
+
+int launch_quant(const kd_quant_args& a, hipStream_t st) {
+  if (a.dtype == KD_BF16) {
+    if (a.D == 64) launch_quant_t<BF16, 64>(a, st);
+    else launch_quant_t<BF16, 128>(a, st);
+  } else {
+    if (a.D == 64) launch_quant_t<F16, 64>(a, st);
+    else launch_quant_t<F16, 128>(a, st);
+  }
+  return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
+}
+
 template <class E, int D, bool INV>
 static void launch_rot_t(const kd_rot_args& a, hipStream_t st) {
   constexpr int RPB = 256 / (D / 8);

@@ -32,6 +32,7 @@ int launch_delta(const AttnArgs& a, hipStream_t st);
 int launch_dq(const AttnArgs& a, const uint8_t* plan, hipStream_t st);
 int launch_dkdv(const AttnArgs& a, const uint8_t* plan, hipStream_t st);
 int launch_hadamard(const kd_rot_args& a, hipStream_t st);
+int launch_quant(const kd_quant_args& a, hipStream_t st);
 
 // Linear workgroup id -> work index so that each XCD (workgroups are dealt
 // round-robin over the 8 XCDs) receives one contiguous range of work items,

@@ -90,6 +90,76 @@ KD_DEV u32x2 ds_read_tr16(const uint8_t* p) {
 
 KD_DEV void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// The score product S = X Y^T of one 64-row LDS tile (A operand, rows = the
+// tile's tokens, taken sigma-permuted so the 32x32 output feeds the next MFMA
+// as its B operand) against one register-resident row per lane (B operand).
+//   Q8 = false: 16-bit X and Y, v_mfma_f32_32x32x16, D / 16 k-steps.
+//   Q8 = true:  fp8 e4m3 X and Y (D bytes per row), v_mfma_scale_f32_32x32x64
+//               f8f6f4 with unit block scales, D / 64 k-steps; the caller
+//               applies the per-(b, h) dequantisation scales.
+// In both, lane (c, hf) of an operand holds row c and the k-slots of half hf
+// of each k-step, so the register row and the LDS row are read alike.
+template <class E, int D, bool Q8>
+struct ScoreOp;
+
+template <class E, int D>
+struct ScoreOp<E, D, false> {
+  using TL = Tile<D>;
+  static constexpr int ROW_BYTES = D * 2;
+  static constexpr int NK = D / 16;
+  u32x4 b[NK];
+  int addr[NK];
+  KD_DEV void load_b(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, int hf) {
+#pragma unroll
+    for (int st = 0; st < NK; ++st) b[st] = buf_load16(rs, row_off + (16 * st + 8 * hf) * 2);
+  }
+  KD_DEV void init(int srow, int hf) {
+#pragma unroll
+    for (int st = 0; st < NK; ++st) addr[st] = TL::at(srow, 2 * st + hf);
+  }
+  // s += X[32 kb + rows] Y^T
+  KD_DEV void mma(const uint8_t* tile, int kb, f32x16& s) const {
+#pragma unroll
+    for (int st = 0; st < NK; ++st)
+      s = mfma32x32x16<E>(*reinterpret_cast<const u32x4*>(tile + addr[st] + kb * 32 * TL::ROWB), b[st], s);
+  }
+};
+
+template <class E, int D>
+struct ScoreOp<E, D, true> {
+  using TL = Tile<D / 2>;  // D bytes per row, laid out as D/2 16-bit columns
+  static constexpr int ROW_BYTES = D;
+  static constexpr int NK = D / 64;
+  i32x8 b[NK];
+  int addr[NK][2];
+  KD_DEV void load_b(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, int hf) {
+#pragma unroll
+    for (int st = 0; st < NK; ++st) {
+      const u32x4 lo = buf_load16(rs, row_off + 64 * st + 32 * hf);
+      const u32x4 hi = buf_load16(rs, row_off + 64 * st + 32 * hf + 16);
+      b[st] = i32x8{int(lo[0]), int(lo[1]), int(lo[2]), int(lo[3]), int(hi[0]), int(hi[1]), int(hi[2]), int(hi[3])};
+    }
+  }
+  KD_DEV void init(int srow, int hf) {
+#pragma unroll
+    for (int st = 0; st < NK; ++st) {
+      addr[st][0] = TL::at(srow, 4 * st + 2 * hf);
+      addr[st][1] = TL::at(srow, 4 * st + 2 * hf + 1);
+    }
+  }
+  KD_DEV void mma(const uint8_t* tile, int kb, f32x16& s) const {
+#pragma unroll
+    for (int st = 0; st < NK; ++st) {
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(tile + addr[st][0] + kb * 32 * TL::ROWB);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(tile + addr[st][1] + kb * 32 * TL::ROWB);
+      const i32x8 av = {int(lo[0]), int(lo[1]), int(lo[2]), int(lo[3]), int(hi[0]), int(hi[1]), int(hi[2]), int(hi[3])};
+      s = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, b[st], s, 0, 0, 0, 127, 0, 127);
+    }
+  }
+};
+
 // Sum of a packed pair of 16-bit floats into an fp32 accumulator (v_dot2).
 template <class E> KD_DEV float acc_pair(uint32_t w, float acc);
 template <> KD_DEV float acc_pair<BF16>(uint32_t w, float acc) {

@@ -18,7 +18,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import RotArgs
+from ._lib import QuantArgs, RotArgs
 
 
 def generate_hadamard_signs(d: int, seed: int | None = None, device=None) -> torch.Tensor:
@@ -78,6 +78,57 @@ def _rot_backward(ctx, gy):
 _rot_op.register_autograd(_rot_backward, setup_context=_rot_setup)
 
 
+@torch.library.custom_op("kdattn::rot_amax", mutates_args=(), device_types=("cuda",))
+def _rot_amax_op(x: torch.Tensor, signs: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    amax = torch.zeros(x.shape[:2], dtype=torch.float32, device=x.device)
+    return _launch(x, signs, False, amax), amax
+
+
+@_rot_amax_op.register_fake
+def _rot_amax_fake(x, signs):
+    return (torch.empty(x.shape, dtype=x.dtype, device=x.device),
+            torch.empty(x.shape[:2], dtype=torch.float32, device=x.device))
+
+
+def _rot_amax_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[1])
+    ctx.inverse = False
+
+
+def _rot_amax_backward(ctx, gy, gamax):
+    # amax only feeds the fp8 scales, which are not differentiated
+    (signs,) = ctx.saved_tensors
+    return _rot_op(gy.contiguous(), signs, True), None
+
+
+_rot_amax_op.register_autograd(_rot_amax_backward, setup_context=_rot_amax_setup)
+
+
+@torch.library.custom_op("kdattn::quant", mutates_args=(), device_types=("cuda",))
+def _quant_op(x: torch.Tensor, amax: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    from .attention import _dtype_code, _kernel_ready
+
+    x = _kernel_ready(x)
+    B, H, T, D = x.shape
+    y = torch.empty((B, H, T, D), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((B, H), dtype=torch.float32, device=x.device)
+    amax = amax.contiguous()
+    a = QuantArgs()
+    a.x, a.x_strides = x.data_ptr(), _strides3(x)
+    a.y, a.amax, a.scale = y.data_ptr(), amax.data_ptr(), scale.data_ptr()
+    a.B, a.H, a.T, a.D = B, H, T, D
+    a.dtype = _dtype_code(x.dtype)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+    _lib.check(_lib.load().kd_quant_fp8(ctypes.byref(a), stream), "kd_quant_fp8")
+    return y, scale
+
+
+@_quant_op.register_fake
+def _quant_fake(x, amax):
+    return (torch.empty(x.shape, dtype=torch.uint8, device=x.device),
+            torch.empty(x.shape[:2], dtype=torch.float32, device=x.device))
+
+
 def _check(x: torch.Tensor, signs: torch.Tensor):
     if x.dim() != 4:
         raise ValueError("x must be [batch, heads, time, head_dim]")
@@ -98,8 +149,26 @@ def hadamard_transform(x: torch.Tensor, signs: torch.Tensor, inverse: bool = Fal
 
 
 def hadamard_absmax(x: torch.Tensor, signs: torch.Tensor):
-    """``(x R, amax)`` with ``amax[b, h] = max |x R|`` over (t, d) of the rounded output."""
+    """``(x R, amax)`` with ``amax[b, h] = max |x R|`` over (t, d) of the rounded
+    output, from the same pass; differentiable in ``x R`` (amax is not)."""
     _check(x, signs)
-    amax = torch.zeros(x.shape[:2], dtype=torch.float32, device=x.device)
-    y = _launch(x, signs, False, amax)
-    return y, amax
+    return _rot_amax_op(x, signs)
+
+
+def quantize_fp8(x: torch.Tensor, amax: torch.Tensor | None = None):
+    """Per-(b, h) OCP e4m3 quantisation of a bf16 / fp16 ``[B, H, T, d]`` tensor.
+
+    ``x8 = e4m3(clamp(x * fp32(448 / amax), -448, 448))`` with round to nearest
+    even, ``scale = amax / 448`` (``amax == 0``: both factors are 1), so that
+    ``x ~= scale * x8``.  ``amax`` defaults to ``max |x|`` per (b, h).  Returns
+    ``(x8 as uint8 bytes [B, H, T, d], scale fp32 [B, H])``; not differentiable.
+    """
+    if x.dim() != 4 or x.dtype not in (torch.bfloat16, torch.float16) or not x.is_cuda:
+        raise ValueError("x must be a bf16 / fp16 [batch, heads, time, head_dim] GPU tensor")
+    if x.shape[-1] not in (64, 128):
+        raise ValueError(f"head_dim must be 64 or 128, got {x.shape[-1]}")
+    if amax is None:
+        amax = x.detach().abs().amax(dim=(2, 3)).float()
+    if amax.shape != x.shape[:2] or amax.dtype != torch.float32 or amax.device != x.device:
+        raise ValueError("amax must be float32 [batch, heads] on x's device")
+    return _quant_op(x.detach(), amax.detach())

@@ -58,15 +58,25 @@ def probabilities(q, k, mask, sm_scale, dtype=torch.float64):
     return p / torch.where(l > 0, l, torch.ones_like(l))
 
 
-def backward(q, k, v, o, do, mask, sm_scale, dtype=torch.float64):
+def backward(q, k, v, o, do, mask, sm_scale, dtype=torch.float64, score_q=None, score_k=None):
     """Closed-form gradients ``(dQ, dK, dV, Delta)`` of :func:`forward`.
 
     ``Delta = rowsum(O * dO)`` (``original_kernel.py:695``),
     ``dS = P * (dP - Delta)`` (``:1332``), ``dQ = scale * dS K`` (``:1333-1335``),
     ``dK = scale * dS^T Q`` (``:1523-1524``), ``dV = P^T dO`` (``:1517``).
+
+    ``score_q`` / ``score_k`` (the fp8 QK^T variant, which the reference does
+    not have): P is formed from them -- the dequantised fp8 copies
+    ``scale * e4m3`` whose product gave the forward's O and LSE -- while dQ and
+    dK use ``k`` and ``q``: the straight-through estimator applied to the
+    score product (its value is the fp8 product, its gradient that of
+    ``q k^T``).
     """
     q, k, v, o, do = (x.to(dtype) for x in (q, k, v, o, do))
-    p = probabilities(q, k, mask, sm_scale, dtype)
+    if score_q is None:
+        p = probabilities(q, k, mask, sm_scale, dtype)
+    else:
+        p = probabilities(score_q.to(dtype), score_k.to(dtype), mask, sm_scale, dtype)
     delta = (o * do).sum(-1)
     dp = torch.matmul(do, v.transpose(-1, -2))
     ds = p * (dp - delta[..., None])
@@ -76,12 +86,21 @@ def backward(q, k, v, o, do, mask, sm_scale, dtype=torch.float64):
     return dq, dk, dv, delta
 
 
-def autograd_reference(q, k, v, do, mask, sm_scale, dtype=torch.float64):
-    """Independent route: torch autograd through a naive masked softmax."""
+def autograd_reference(q, k, v, do, mask, sm_scale, dtype=torch.float64, score_q=None, score_k=None):
+    """Independent route: torch autograd through a naive masked softmax.
+
+    With ``score_q`` / ``score_k`` the scores are ``q k^T + (score_q score_k^T -
+    q k^T).detach()``: the value of the score operands' product, the gradient
+    of ``q k^T`` (straight through the quantised product).
+    """
     B, H, T, D = q.shape
     m = _mask_t(mask, B, H, T)
     q, k, v = (x.detach().to(dtype).requires_grad_(True) for x in (q, k, v))
-    s = torch.matmul(q, k.transpose(-1, -2)) * sm_scale
+    s = torch.matmul(q, k.transpose(-1, -2))
+    if score_q is not None:
+        s8 = torch.matmul(score_q.to(dtype), score_k.to(dtype).transpose(-1, -2))
+        s = s + (s8 - s).detach()
+    s = s * sm_scale
     s = s.masked_fill(~m, float("-inf"))
     row_any = m.any(-1, keepdim=True)
     s = torch.where(row_any, s, torch.zeros_like(s))

@@ -87,19 +87,27 @@ def oracle_mask(inp, T, lens=None, attention_mask_given=False):
                       causal=inp.get("causal", True), attention_mask_given=attention_mask_given)
 
 
-def oracle_fwd_bwd(q, k, v, do, mask, sm_scale, heads=None):
-    """fp64 dense reference for all (or the listed (b, h)) heads."""
+def oracle_fwd_bwd(q, k, v, do, mask, sm_scale, heads=None, score_q=None, score_k=None):
+    """fp64 dense reference for all (or the listed (b, h)) heads.
+
+    ``score_q`` / ``score_k``: operands of the scores when they differ from
+    q / k (the fp8 variant's dequantised copies; straight-through gradients).
+    """
     if heads is not None:
         out = {"o": [], "lse": [], "dq": [], "dk": [], "dv": []}
         for b, h in heads:
             sl = (slice(b, b + 1), slice(h, h + 1))
-            r = oracle_fwd_bwd(q[sl], k[sl], v[sl], do[sl], mask[b:b + 1], sm_scale)
+            sq = None if score_q is None else score_q[sl]
+            sk = None if score_k is None else score_k[sl]
+            r = oracle_fwd_bwd(q[sl], k[sl], v[sl], do[sl], mask[b:b + 1], sm_scale, score_q=sq, score_k=sk)
             for key in out:
                 out[key].append(r[key])
         return {key: torch.cat(val, 0) for key, val in out.items()}
     m = torch.as_tensor(mask)
-    o, lse = ref_attn.forward(q, k, v, m, sm_scale)
-    dq, dk, dv, _ = ref_attn.backward(q, k, v, o, do, m, sm_scale)
+    sq = q if score_q is None else score_q
+    sk = k if score_k is None else score_k
+    o, lse = ref_attn.forward(sq, sk, v, m, sm_scale)
+    dq, dk, dv, _ = ref_attn.backward(q, k, v, o, do, m, sm_scale, score_q=score_q, score_k=score_k)
     return {"o": o, "lse": lse, "dq": dq, "dk": dk, "dv": dv}
 
 

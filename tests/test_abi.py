@@ -66,9 +66,24 @@ def test_bad_arguments_return_status_without_gpu():
     a.q_strides[:] = [1024, 1024, 8]  # t stride < head dim: rows overlap
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_INVALID
     assert "overlap" in lib.kd_last_error_string().decode()
+    a.q_strides[:] = [1024, 1024, 64]
+    a.q8 = 64  # fp8 operands: q8 without k8, then head dim 64
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_INVALID
+    assert "q8 and k8" in lib.kd_last_error_string().decode()
+    a.k8 = 64
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_UNSUPPORTED
+    a.D = 128
+    a.q_strides[:] = [1024, 1024, 128]
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_INVALID  # no scales
+    assert "scale" in lib.kd_last_error_string().decode()
     r = _lib.RotArgs()
     r.B, r.H, r.T, r.D, r.dtype = 1, 1, 4, 32, _lib.KD_BF16
     assert lib.kd_hadamard(ctypes.byref(r), null) == _lib.KD_ERR_UNSUPPORTED
+    qa = _lib.QuantArgs()
+    qa.B, qa.H, qa.T, qa.D, qa.dtype = 1, 1, 4, 128, _lib.KD_BF16
+    assert lib.kd_quant_fp8(ctypes.byref(qa), null) == _lib.KD_ERR_INVALID  # amax / scale / y missing
+    qa.D = 96
+    assert lib.kd_quant_fp8(ctypes.byref(qa), null) == _lib.KD_ERR_UNSUPPORTED
     m = _lib.MetaArgs()
     m.B, m.T, m.mode = 1, 8, 7
     assert lib.kd_plan_build(ctypes.byref(m), ctypes.c_void_p(256), null) == _lib.KD_ERR_INVALID

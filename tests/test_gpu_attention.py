@@ -10,6 +10,7 @@ import torch
 
 from helpers import assert_close, assert_close_scaled, oracle_fwd_bwd, oracle_mask, select_heads
 from kerneldev_amd import flash_attention, generate_hadamard_signs
+from oracle import fp8 as ref_fp8
 from oracle import hadamard as ref_h
 from kerneldev_amd.synth import CONFIG3_LAYOUT, cocktail_batch, config_inputs, qkvdo
 
@@ -52,12 +53,22 @@ def compare(got, ref, heads=None, scaled=False):
     return res
 
 
+def fp8_scores(x: torch.Tensor) -> torch.Tensor:
+    """Dequantised per-(b, h) e4m3 copy ``scale * x8`` of a bf16 tensor (oracle/fp8.py)."""
+    x8, sigma = ref_fp8.quantize_per_head(x.float().numpy())
+    return torch.from_numpy(ref_fp8.e4m3_decode(x8) * sigma[:, :, None, None]).double()
+
+
 def _case(inp, dev, heads=None, scaled=False, **kw):
-    print(f"attention case {inp.get('name', '?')} heads={heads}", flush=True)
+    print(f"attention case {inp.get('name', '?')} heads={heads} "
+          f"{kw.get('qk_dtype', 'bf16')} hadamard={kw.get('hadamard', False)}", flush=True)
     got = run_gpu(inp, dev, **kw)
     T = inp["q"].shape[2]
     mask = oracle_mask(inp, T, lens=kw.get("lens"), attention_mask_given=kw.get("attention_mask") is not None)
     q, k, v, do = (inp[x] for x in ("q", "k", "v", "do"))
+    if heads is not None:  # the oracle works on the listed (b, h) only
+        q, k, v, do = (select_heads(x, heads) for x in (q, k, v, do))
+        mask = np.stack([mask[b] for b, _ in heads])
     dt = kw.get("dtype")
     if dt is not None:  # the oracle sees exactly the rounded inputs the GPU sees
         q, k, v, do = (x.to(dt) for x in (q, k, v, do))
@@ -70,7 +81,12 @@ def _case(inp, dev, heads=None, scaled=False, **kw):
         rot = torch.from_numpy(ref_h.rotation_matrix(signs))
         q = torch.from_numpy(ref_h.rotate_fp32(q.float().numpy(), signs)).to(q.dtype)
         k = torch.from_numpy(ref_h.rotate_fp32(k.float().numpy(), signs)).to(k.dtype)
-    ref = oracle_fwd_bwd(q, k, v, do, mask, q.shape[-1] ** -0.5, heads=heads)
+    sq = sk = None
+    if kw.get("qk_dtype") == "fp8_e4m3":
+        # scores from the e4m3 copies (bit-exact quantiser: tests/test_gpu_fp8.py),
+        # gradients straight through to the 16-bit Q', K'
+        sq, sk = fp8_scores(q), fp8_scores(k)
+    ref = oracle_fwd_bwd(q, k, v, do, mask, q.shape[-1] ** -0.5, score_q=sq, score_k=sk)
     if rot is not None:
         ref["dq"] = ref["dq"] @ rot.T
         ref["dk"] = ref["dk"] @ rot.T
@@ -158,6 +174,32 @@ def test_config4_cocktail_hadamard_bf16(dev):
     """Config 4 as specified: Q and K rotated by the seeded d=128 Hadamard."""
     inp = config_inputs(4, seed=0)
     _case(inp, dev, heads=[(0, 3), (1, 17)], scaled=True, hadamard=True, hadamard_seed=0)
+
+
+@pytest.mark.parametrize("hadamard", [False, True])
+def test_fp8_cocktail_small(dev, hadamard):
+    """fp8 e4m3 Q K^T against the oracle fed the same e4m3 operands.
+
+    Bar: the north_star bf16 bar, unchanged -- the quantisation itself is in
+    the oracle, so what remains is accumulation order and the bf16 rounding of
+    P, dS and the outputs.
+    """
+    tokens, in_span, span_id, is_prefix = cocktail_batch(2, 1024, CONFIG3_LAYOUT, seed=12)
+    q, k, v, do = qkvdo(2, 2, 1024, 128, seed=13)
+    _case(dict(name="fp8 cocktail", q=q, k=k, v=v, do=do, in_span=in_span, span_id=span_id, is_prefix=is_prefix),
+          dev, qk_dtype="fp8_e4m3", hadamard=hadamard, hadamard_seed=3)
+
+
+def test_fp8_causal_ragged(dev):
+    q, k, v, do = qkvdo(2, 3, 333, 128, seed=14)
+    _case(dict(name="fp8 causal ragged", q=q, k=k, v=v, do=do, causal=True), dev, qk_dtype="fp8_e4m3",
+          lens=torch.tensor([333, 200], dtype=torch.int32))
+
+
+def test_config4_cocktail_hadamard_fp8(dev):
+    """Config 4's second run: Hadamard, then fp8 e4m3 Q K^T with per-(b, h) scales."""
+    inp = config_inputs(4, seed=0)
+    _case(inp, dev, heads=[(0, 5), (1, 30)], scaled=True, hadamard=True, hadamard_seed=0, qk_dtype="fp8_e4m3")
 
 
 def test_deterministic(dev):

@@ -197,6 +197,29 @@ def test_forward_backward_match_autograd():
     np.testing.assert_allclose(delta.numpy(), (o * do).sum(-1).numpy())
 
 
+def test_straight_through_backward_matches_autograd():
+    """fp8 variant: P from the dequantised copies, dQ/dK straight through.
+
+    The closed form is checked against autograd through ``q + (q8 - q).detach()``
+    through ``q k^T + (Qs Ks^T - q k^T).detach()`` (an independent route), and must
+    differ from the plain backward (so a
+    version that ignored the score operands would fail).
+    """
+    q, k, v, do, mask = _case(seed=2)
+    q8, sq = fp8.quantize_per_head(q.float().numpy())
+    k8, sk = fp8.quantize_per_head(k.float().numpy())
+    qs = torch.from_numpy(fp8.e4m3_decode(q8) * sq[:, :, None, None]).double()
+    ks = torch.from_numpy(fp8.e4m3_decode(k8) * sk[:, :, None, None]).double()
+    sc = 0.3
+    o, _ = ref.forward(qs, ks, v, mask, sc)
+    dq, dk, dv, _ = ref.backward(q, k, v, o, do, mask, sc, score_q=qs, score_k=ks)
+    o2, dq2, dk2, dv2 = ref.autograd_reference(q, k, v, do, mask, sc, score_q=qs, score_k=ks)
+    for a, b in ((o, o2), (dq, dq2), (dk, dk2), (dv, dv2)):
+        torch.testing.assert_close(a, b, rtol=1e-10, atol=1e-10)
+    dq0, dk0, _, _ = ref.backward(q, k, v, o, do, mask, sc)
+    assert (dq - dq0).abs().max().item() > 1e-4 and (dk - dk0).abs().max().item() > 1e-4
+
+
 def test_lse_is_base2_logsumexp_and_ds_rows_sum_to_zero():
     q, k, v, do, mask = _case(seed=1)
     sc = 0.25
