@@ -128,10 +128,12 @@ void kd_struct_sizes2(size_t *rot, size_t *quant);
 
 /* Workspace ("plan") bytes for B sequences of length T at head dim D, and
  * the byte offsets of its sections (codes, class map, per-tile allowed
- * counts, and the forward / dQ / dK-dV work lists).  offsets[] receives 17
- * int64: codes, rep, cls, nnz, fwd_list, fwd_count, dq_list, dq_count,
- * dkdv_list, dkdv_count, nT, fwd_group, dq_group, dkdv_group,
- * n_fwd_blocks, n_dq_blocks, n_dkdv_blocks.  Replaces the per-tile mask evaluation of
+ * counts, the forward / dQ / dK-dV work lists, and the 64-bit row / column
+ * masks of PARTIAL tiles).  offsets[] receives 19 int64: codes, rep, cls,
+ * nnz, fwd_list, fwd_count, dq_list, dq_count, dkdv_list, dkdv_count, nT,
+ * fwd_group, dq_group, dkdv_group, n_fwd_blocks, n_dq_blocks, n_dkdv_blocks,
+ * qbits, kbits.  A list entry is (tile << 8) | the class of group member r in
+ * bits 2r..2r+1.  Replaces the per-tile mask evaluation of
  * original_kernel.py:457-517 (the reference has no tile map). */
 int64_t kd_plan_bytes(int32_t B, int32_t T, int32_t D);
 int kd_plan_layout(int32_t B, int32_t T, int32_t D, int64_t *offsets);

@@ -151,10 +151,10 @@ def plan_bytes(B: int, T: int, D: int) -> int:
 
 PLAN_FIELDS = ("codes", "rep", "cls", "nnz", "fwd_list", "fwd_count", "dq_list", "dq_count",
                "dkdv_list", "dkdv_count", "nT", "fwd_group", "dq_group", "dkdv_group",
-               "n_fwd_blocks", "n_dq_blocks", "n_dkdv_blocks")
+               "n_fwd_blocks", "n_dq_blocks", "n_dkdv_blocks", "qbits", "kbits")
 
 
 def plan_layout(B: int, T: int, D: int) -> dict:
-    off = (c_int64 * 17)()
+    off = (c_int64 * len(PLAN_FIELDS))()
     check(load().kd_plan_layout(B, T, D, off), "kd_plan_layout")
     return dict(zip(PLAN_FIELDS, [int(x) for x in off]))

@@ -333,7 +333,7 @@ def flash_attention(
 
 
 def plan_views(plan: torch.Tensor, B: int, T: int, D: int) -> dict:
-    """Typed views of a plan tensor's sections (codes, class map, lists)."""
+    """Typed views of a plan tensor's sections (codes, class map, lists, tile bit masks)."""
     L = _lib.plan_layout(B, T, D)
     nT = L["nT"]
 
@@ -352,6 +352,9 @@ def plan_views(plan: torch.Tensor, B: int, T: int, D: int) -> dict:
         "dq_count": view(L["dq_count"], B * nq, torch.int32).view(B, nq),
         "dkdv_list": view(L["dkdv_list"], B * nk * nT, torch.int32).view(B, nk, nT),
         "dkdv_count": view(L["dkdv_count"], B * nk, torch.int32).view(B, nk),
+        # row / column bit masks, meaningful for PARTIAL tiles only
+        "qbits": view(L["qbits"], B * nT * nT * 64, torch.int64).view(B, nT, nT, 64),
+        "kbits": view(L["kbits"], B * nT * nT * 64, torch.int64).view(B, nT, nT, 64),
         "layout": L,
     }
 

@@ -100,7 +100,7 @@ KD_DEV void tr_addrs(int lane, int (&addr)[D / 32][2]) {
 
 // ------------------------------------------------------------------- dQ ----
 template <class E, int D, bool Q8>
-__global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __restrict__ codes,
+__global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __restrict__ qbits,
                                                const uint32_t* __restrict__ list,
                                                const int32_t* __restrict__ count, int nT, int nQB) {
   using TL = Tile<D>;
@@ -110,7 +110,6 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
   __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][TL::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][TL::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_k8[Q8 ? 2 : 1][Q8 ? TK8::BYTES : 16];
-  __shared__ __attribute__((aligned(256))) uint32_t s_code[2][64];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
   const int T = a.T, H = a.H;
@@ -129,7 +128,6 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
   const auto rs_do = make_rsrc(dog, uint32_t(T) * dorb);
   const auto rs_k = make_rsrc(kg, uint32_t(T) * krb);
   const auto rs_v = make_rsrc(vg, uint32_t(T) * vrb);
-  const auto rs_c = make_rsrc(codes + int64_t(b) * T, uint32_t(T) * 4u);
   const int64_t BHT = int64_t(a.B) * H * T;
 
   const int qrow = qblock * 128 + wave * 32 + c;
@@ -143,7 +141,9 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
   const float INF = __builtin_inff();
   const float lse = qvalid ? a.delta[BHT + int64_t(bh) * T + qrow] : INF;
   const float delta = qvalid ? a.delta[int64_t(bh) * T + qrow] : 0.f;
-  const uint32_t qcode = qvalid ? codes[int64_t(b) * T + qrow] : 0u;
+  // this wave's rows lie in q-tile 2 qblock + member; its row masks per key tile
+  const int member = wave >> 1;
+  const uint64_t* qbits_row = qbits + (int64_t(b) * nT + 2 * qblock + member) * nT * 64 + 32 * (wave & 1) + c;
 
   const int lbase = b * nQB + qblock;
   const int n = count[lbase];
@@ -159,8 +159,10 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
     TL::load(rs_k, k0 * krb, koff, s_k[buf], wave);
     TL::load(rs_v, k0 * vrb, voff, s_v[buf], wave);
     if constexpr (Q8) TK8::load(rs_k8, k0 * uint32_t(D), k8off, s_k8[buf], wave);
-    if (wave == 0)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_t*)&s_code[buf][0], 4, (k0 + lane) * 4u, 0, 0, 0);
+  };
+  // a PARTIAL tile's row mask, fetched one step ahead of its use
+  auto load_bits = [&](int e, uint64_t& bits) {
+    if (entry_class(ent[e], member) == TILE_PARTIAL) bits = qbits_row[int64_t(entry_tile(ent[e])) * 64];
   };
 
   const int srow = sigma(c);
@@ -170,24 +172,28 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
   for (int st = 0; st < DS; ++st) raddr[st] = TL::at(srow, 2 * st + hf);
   int taddr[DB][2];
   tr_addrs<D>(lane, taddr);
-  const MaskTab mt = qmask(qcode);
-  const int i_lo = qblock * 128 + wave * 32;
 
   // the fp8 product carries the dequantisation scales of Q and K
   const float sl2 = a.sm_scale * 1.4426950408889634f * (Q8 ? a.q_scale[bh] * a.k_scale[bh] : 1.f);
-  const float NEG_INF = -INF;
   f32x16 acc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
 
-  if (n > 0) load_tile(int(ent[0] >> 1), 0);
+  uint64_t bits = 0, bits_next = 0;
+  if (n > 0) {
+    load_tile(int(entry_tile(ent[0])), 0);
+    load_bits(0, bits);
+  }
 
   for (int e = 0; e < n; ++e) {
     const int buf = e & 1;
     const uint32_t cur = ent[e];
     wait_vmem();
     __syncthreads();
-    if (e + 1 < n) load_tile(int(ent[e + 1] >> 1), buf ^ 1);
+    if (e + 1 < n) {
+      load_tile(int(entry_tile(ent[e + 1])), buf ^ 1);
+      load_bits(e + 1, bits_next);
+    }
     const uint8_t* kt = s_k[buf];
     const uint8_t* vt = s_v[buf];
 
@@ -202,25 +208,14 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
         dp[kb] = mfma32x32x16<E>(av, dof[st], dp[kb]);
       }
     }
-    if (!(cur & 1u)) {  // PARTIAL tile: register r of s[kb] holds key k0 + 32 kb + 16 (r / 8) + 8 hf + r % 8
-      const int k0 = int(cur >> 1) * 64;
+    const uint32_t mcls = entry_class(cur, member);
+    if (mcls != TILE_FULL) {  // wave-uniform.  Register r of s[kb] holds key 32 kb + 16 (r / 8) + 8 hf + r % 8
+      const uint64_t rowbits = mcls == TILE_PARTIAL ? bits : 0u;  // EMPTY: nothing allowed
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const int j0 = k0 + 32 * kb;
-        const bool below = j0 + 31 <= i_lo, above = j0 > i_lo + 31;
+        const uint32_t w = uint32_t(rowbits >> (32 * kb)) >> (8 * hf);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int jl = 32 * kb + 16 * t + 8 * hf;
-          const u32x4 c0 = *reinterpret_cast<const u32x4*>(&s_code[buf][jl]);
-          const u32x4 c1 = *reinterpret_cast<const u32x4*>(&s_code[buf][jl + 4]);
-#pragma unroll
-          for (int x = 0; x < 8; ++x) {
-            const uint32_t kc = x < 4 ? c0[x] : c1[x - 4];
-            uint32_t tbl = below ? mt.hi : mt.lo;
-            if (!below && !above) tbl = (k0 + jl + x <= qrow) ? mt.hi : mt.lo;
-            s[kb][8 * t + x] = mask_score(s[kb][8 * t + x], tbl, kc, kc, mt.rsh);
-          }
-        }
+        for (int r = 0; r < 16; ++r) s[kb][r] = mask_bit(s[kb][r], w, 16 * (r >> 3) + (r & 7));
       }
     }
     u32x4 dsb[2][2];
@@ -248,6 +243,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
         acc[db] = mfma32x32x16<E>(ak, dsb[t4 >> 1][t4 & 1], acc[db]);
       }
     }
+    bits = bits_next;
   }
 
   if (qvalid) {
@@ -268,7 +264,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
 // pair shares a SIMD (waves w and w + 4), so one wave's VALU softmax runs
 // under the other's MFMAs.
 template <class E, int D, bool Q8>
-__global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __restrict__ codes,
+__global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __restrict__ kbits,
                                                  const uint32_t* __restrict__ list,
                                                  const int32_t* __restrict__ count, int nT, int nKB) {
   constexpr int NW = 8;
@@ -282,7 +278,6 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   __shared__ __attribute__((aligned(1024))) float s_p[4][2 * 16][64];  // [pair][register][lane]
   __shared__ __attribute__((aligned(256))) float s_lse[2][64];
   __shared__ __attribute__((aligned(256))) float s_delta[2][64];
-  __shared__ __attribute__((aligned(256))) uint32_t s_code[2][64];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
   const int pair = wave & 3, role = wave >> 2;
@@ -303,7 +298,6 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   const int64_t BHT = int64_t(a.B) * H * T;
   const auto rs_lse = make_rsrc(a.delta + BHT + int64_t(bh) * T, uint32_t(T) * 4u);
   const auto rs_dl = make_rsrc(a.delta + int64_t(bh) * T, uint32_t(T) * 4u);
-  const auto rs_c = make_rsrc(codes + int64_t(b) * T, uint32_t(T) * 4u);
 
   // this lane's key and its B operand: K for the P wave, V for the dS wave
   const int krow = kblock * 128 + pair * 32 + c;
@@ -318,9 +312,10 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
 #pragma unroll
     for (int st = 0; st < DS; ++st) bf[st] = buf_load16(rs_b, uint32_t(krow) * brb + (16 * st + 8 * hf) * 2);
   }
-  const uint32_t kcode = kvalid ? codes[int64_t(b) * T + krow] : 0u;
-  const MaskTab mt = kmask(kcode);
-  const int j_lo = kblock * 128 + pair * 32;
+  // this pair's keys lie in k-tile 2 kblock + member; the column masks of its
+  // PARTIAL tiles give, per key, the allowed queries of a q-tile
+  const int member = pair >> 1;
+  const uint64_t* kbits_col = kbits + (int64_t(b) * nT * nT + 2 * kblock + member) * 64 + 32 * (pair & 1) + c;
 
   const int lbase = b * nKB + kblock;
   const int n = count[lbase];
@@ -340,8 +335,11 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, (lds_t*)&s_lse[buf][0], 4, (q0 + lane) * 4u, 0, 0, 0);
     else if (wave == 1)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_dl, (lds_t*)&s_delta[buf][0], 4, (q0 + lane) * 4u, 0, 0, 0);
-    else if (wave == 2)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_t*)&s_code[buf][0], 4, (q0 + lane) * 4u, 0, 0, 0);
+  };
+  // a PARTIAL tile's column mask (P waves only), fetched one step ahead of its use
+  auto load_bits = [&](int e, uint64_t& bits) {
+    if (role == 0 && entry_class(ent[e], member) == TILE_PARTIAL)
+      bits = kbits_col[int64_t(entry_tile(ent[e])) * nT * 64];
   };
 
   const int srow = sigma(c);
@@ -359,20 +357,26 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
   float* xp = &s_p[pair][0][lane];
 
-  if (n > 0) load_tile(int(ent[0] >> 1), 0);
+  uint64_t bits = 0, bits_next = 0;
+  if (n > 0) {
+    load_tile(int(entry_tile(ent[0])), 0);
+    load_bits(0, bits);
+  }
 
   for (int e = 0; e < n; ++e) {
     const int buf = e & 1;
     const uint32_t cur = ent[e];
     wait_vmem();
     __syncthreads();  // tile e landed; every wave is done with tile e-1 and its P
-    if (e + 1 < n) load_tile(int(ent[e + 1] >> 1), buf ^ 1);
+    if (e + 1 < n) {
+      load_tile(int(entry_tile(ent[e + 1])), buf ^ 1);
+      load_bits(e + 1, bits_next);
+    }
     const uint8_t* qt = s_q[buf];
     const uint8_t* dot = s_do[buf];
     // A operands: rows of Q (role 0) or dO (role 1); transposed dO (role 0) or Q (role 1)
     const uint8_t* arow = role == 0 ? qt : dot;
     const uint8_t* atr = role == 0 ? dot : qt;
-    const int q0 = int(cur >> 1) * 64;
 
     // S (role 0) or dP (role 1) for the two 32-query halves; register r of
     // x[qb] holds query 32 qb + 16 (r / 8) + 8 hf + r % 8 of this lane's key
@@ -392,24 +396,14 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
     }
     u32x4 bop[2][2];  // packed P (role 0) or dS (role 1): B operand of k-step 2 qb + t
     if (role == 0) {
-      if (!(cur & 1u)) {  // PARTIAL tile: queries i = q0 + ql + j against this lane's key
+      const uint32_t mcls = entry_class(cur, member);
+      if (mcls != TILE_FULL) {  // wave-uniform.  Register r of x[qb] holds query 32 qb + 16 (r / 8) + 8 hf + r % 8
+        const uint64_t colbits = mcls == TILE_PARTIAL ? bits : 0u;  // EMPTY: nothing allowed
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
-          const int i0 = q0 + 32 * qb;
-          const bool after = i0 >= j_lo + 31, before = i0 + 31 < j_lo;
+          const uint32_t w = uint32_t(colbits >> (32 * qb)) >> (8 * hf);
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const int ql = 32 * qb + 16 * t + 8 * hf;
-            const u32x4 c0 = *reinterpret_cast<const u32x4*>(&s_code[buf][ql]);
-            const u32x4 c1 = *reinterpret_cast<const u32x4*>(&s_code[buf][ql + 4]);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const uint32_t qc = j < 4 ? c0[j] : c1[j - 4];
-              uint32_t tbl = after ? mt.hi : mt.lo;
-              if (!after && !before) tbl = (q0 + ql + j >= krow) ? mt.hi : mt.lo;
-              x[qb][8 * t + j] = mask_score(x[qb][8 * t + j], tbl, qc >> 3, qc, mt.rsh);
-            }
-          }
+          for (int r = 0; r < 16; ++r) x[qb][r] = mask_bit(x[qb][r], w, 16 * (r >> 3) + (r & 7));
         }
       }
 #pragma unroll
@@ -460,6 +454,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
           const u32x2 hi = ds_read_tr16(atr + taddr[db][1] + off);
           acc[db] = mfma32x32x16<E>(u32x4{lo[0], lo[1], hi[0], hi[1]}, bop[qb][t], acc[db]);
         }
+    bits = bits_next;
   }
 
   if (kvalid) {
@@ -481,7 +476,7 @@ template <class E, int D, bool Q8 = false>
 static void launch_dq_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dq_blocks;
-  hipLaunchKernelGGL((k_dq<E, D, Q8>), dim3(grid), dim3(256), 0, st, a, reinterpret_cast<const uint32_t*>(plan + L.codes),
+  hipLaunchKernelGGL((k_dq<E, D, Q8>), dim3(grid), dim3(256), 0, st, a, reinterpret_cast<const uint64_t*>(plan + L.qbits),
                      reinterpret_cast<const uint32_t*>(plan + L.dq_list),
                      reinterpret_cast<const int32_t*>(plan + L.dq_count), L.nT, L.n_dq_blocks);
 }
@@ -490,7 +485,7 @@ static void launch_dkdv_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dkdv_blocks;
   hipLaunchKernelGGL((k_dkdv<E, D, Q8>), dim3(grid), dim3(512), 0, st, a,
-                     reinterpret_cast<const uint32_t*>(plan + L.codes),
+                     reinterpret_cast<const uint64_t*>(plan + L.kbits),
                      reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
                      reinterpret_cast<const int32_t*>(plan + L.dkdv_count), L.nT, L.n_dkdv_blocks);
 }

@@ -47,44 +47,10 @@ __host__ __device__ inline bool allow_hd(uint32_t qc, uint32_t kc, int i, int j)
          (((qc >> 8) != 0u) && ((qc >> 8) == (kc >> 8)));
 }
 
-// Table-driven form of allow() for the attention kernels' PARTIAL tiles.
-// A lane fixes one side of the pair (its query, or its key); a 32-bit table
-// answers the flag terms for any code on the other side with one v_bfe_i32,
-// and the same-span term is one xor + compare:
-//   QMask (lane = query i, elements = keys j): bit (kc & 31) of the table
-//     (the 16-entry table over the key's flags, stored twice) is
-//     (A_i & F_j) != 0, plus C_i & C_j in the "causal" table used where j <= i.
-//   KMask (lane = key j, elements = queries i): bit ((qc >> 3) & 31) -- that is
-//     C_i | A_i << 1 -- of the table is (A_i & F_j) != 0, plus C_i & C_j in the
-//     causal table used where i >= j.
-// rsh = R << 8 for span tokens, else a value no code matches, so that
-// ((code ^ rsh) < 256) is exactly "same span".
-struct MaskTab {
-  uint32_t lo, hi, rsh;
-};
-KD_DEV uint32_t span_key(uint32_t code) {
-  const uint32_t R = code >> 8;
-  return R ? (R << 8) : 0xFFFFFF00u;
-}
-KD_DEV MaskTab qmask(uint32_t qcode) {
-  const uint32_t A = (qcode >> 4) & 15u;
-  const uint32_t t = ((A & FLAG_P) ? 0xAAAAu : 0u) | ((A & FLAG_S) ? 0xCCCCu : 0u) |
-                     ((A & FLAG_M) ? 0xF0F0u : 0u) | ((A & FLAG_C) ? 0xFF00u : 0u);
-  const uint32_t th = t | ((qcode & FLAG_C) ? 0xFF00u : 0u);
-  return MaskTab{t * 0x10001u, th * 0x10001u, span_key(qcode)};
-}
-KD_DEV MaskTab kmask(uint32_t kcode) {
-  const uint32_t F = kcode & 15u;
-  const uint32_t t = ((F & FLAG_P) ? 0xCCCCCCCCu : 0u) | ((F & FLAG_S) ? 0xF0F0F0F0u : 0u) |
-                     ((F & FLAG_M) ? 0xFF00FF00u : 0u) | ((F & FLAG_C) ? 0xFFFF0000u : 0u);
-  const uint32_t th = t | ((kcode & FLAG_C) ? 0xAAAAAAAAu : 0u);
-  return MaskTab{t, th, span_key(kcode)};
-}
-// s if (tbl bit `idx` | same span), else -inf.  idx uses its low 5 bits.
-KD_DEV float mask_score(float s, uint32_t tbl, uint32_t idx, uint32_t other_code, uint32_t rsh) {
-  const uint32_t m = uint32_t(__builtin_amdgcn_sbfe(int(tbl), idx, 1u));  // 0 or ~0
-  const uint32_t v = (__float_as_uint(s) & m) | (0xFF800000u & ~m);
-  return ((other_code ^ rsh) < 256u) ? s : __uint_as_float(v);
+// s if bit `pos` of w is set, else -inf (v_bfe_i32 + v_bfi_b32).
+KD_DEV float mask_bit(float s, uint32_t w, int pos) {
+  const uint32_t m = uint32_t(__builtin_amdgcn_sbfe(int(w), pos, 1u));
+  return __uint_as_float((__float_as_uint(s) & m) | (0xFF800000u & ~m));
 }
 
 // Element types -----------------------------------------------------------

@@ -22,8 +22,10 @@
 // The running max is rescaled lazily, per lane: the accumulators are only
 // rescaled when a row's max grows by more than 2^8 (P is then <= 256,
 // harmless in fp32/bf16), which removes the per-step O *= alpha of the
-// textbook loop.  PARTIAL tiles are masked with the table form of the rule
-// (kd_common.h: qmask / mask_score), a handful of VALU ops per score.
+// textbook loop.  Each wave masks by the class of its own 64-row q-tile
+// against the key tile (from the list entry): FULL tiles skip the mask,
+// PARTIAL ones apply the plan's 64-bit row masks (two VALU ops per score,
+// fetched one step ahead), EMPTY ones mask everything.
 // O is normalised by the sum of the ROUNDED P that enters P V, so it is an
 // exact convex combination of V rows up to the final rounding even when one
 // key dominates the row; LSE uses the exact fp32 sum.
@@ -31,19 +33,29 @@
 
 namespace kd {
 
-template <class E, int D, bool Q8>
-__global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __restrict__ codes,
-                                                const uint32_t* __restrict__ list,
-                                                const int32_t* __restrict__ count, int nT, int nQB) {
-  using TL = Tile<D>;           // V tiles (and K tiles on the 16-bit path)
-  using SO = ScoreOp<E, D, Q8>;  // S^T = K Q^T, 16-bit or fp8
-  using TK = typename SO::TL;   // K tiles
+#ifndef FWD_QB
+#define FWD_QB 1
+#endif
+#ifndef FWD_PF
+#define FWD_PF 4
+#endif
+#ifndef FWD_PFV
+#define FWD_PFV 4
+#endif
+
+template <class E, int D, bool Q8, int QB>
+__global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, const uint64_t* __restrict__ qbits,
+                                                                const uint32_t* __restrict__ list,
+                                                                const int32_t* __restrict__ count, int nT, int nQB) {
+  constexpr int NW = 4 / QB;        // waves per 128-row q-block; each owns 32 QB rows
+  using TL = Tile<D, NW>;           // V tiles (and K tiles on the 16-bit path)
+  using SO = ScoreOp<E, D, Q8>;     // S^T = K Q^T, 16-bit or fp8
+  using TK = Tile<Q8 ? D / 2 : D, NW>;  // K tiles (fp8: D bytes a row); same layout as SO::TL
   constexpr int DB = D / 32;  // 32-row blocks of O^T
   constexpr int NL = TL::LOADS_PER_WAVE;
   constexpr int NLK = TK::LOADS_PER_WAVE;
   __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][TK::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][TL::BYTES];
-  __shared__ __attribute__((aligned(256))) uint32_t s_code[2][64];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
   const int T = a.T, H = a.H;
@@ -67,14 +79,23 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
   const auto rs_q = make_rsrc(qs_base, uint32_t(T) * qrb);
   const auto rs_k = make_rsrc(ks_base, uint32_t(T) * krb);
   const auto rs_v = make_rsrc(vg, uint32_t(T) * vrb);
-  const auto rs_c = make_rsrc(codes + int64_t(b) * T, uint32_t(T) * 4u);
 
-  // ---- per-lane query row (B operand of S^T, kept in registers) ----
-  const int qrow = qblock * 128 + wave * 32 + c;
-  const bool qvalid = qrow < T;
-  SO so;
-  so.load_b(rs_q, uint32_t(qrow) * qrb, hf);
-  const uint32_t qcode = qvalid ? codes[int64_t(b) * T + qrow] : 0u;
+  // ---- this lane's query rows, one per 32-row block qb (B operands of S^T,
+  // kept in registers): i_lo[qb] + c ----
+  const int srow = sigma(c);
+  int qrow[QB];
+  bool qvalid[QB];
+  SO so[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    qrow[qb] = qblock * 128 + (wave * QB + qb) * 32 + c;
+    qvalid[qb] = qrow[qb] < T;
+    so[qb].load_b(rs_q, uint32_t(qrow[qb]) * qrb, hf);
+    so[qb].init(srow, hf);
+  }
+  // this wave's rows lie in q-tile 2 qblock + member of the block (group of 2)
+  const int member = (wave * QB) >> 1;
+  const uint64_t* qbits_row = qbits + (int64_t(b) * nT + 2 * qblock + member) * nT * 64 + 32 * ((wave * QB) & 1) + c;
 
   const int lbase = b * nQB + qblock;
   const int n = count[lbase];
@@ -84,23 +105,26 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
   TK::load_offsets(wave, lane, krb, koff);
   TL::load_offsets(wave, lane, vrb, voff);
   // K tiles run one step ahead of V tiles (S of tile e+1 is computed while
-  // tile e is softmaxed), so they are loaded separately; the key codes of a
-  // tile travel with its V tile.
+  // tile e is softmaxed), so they are loaded separately.
   auto load_k = [&](int e) {
-    const uint32_t k0 = uint32_t(ent[e] >> 1) * 64u;
+    const uint32_t k0 = entry_tile(ent[e]) * 64u;
     TK::load(rs_k, k0 * krb, koff, s_k[e & 1], wave);
   };
   auto load_v = [&](int e) {
-    const uint32_t k0 = uint32_t(ent[e] >> 1) * 64u;
+    const uint32_t k0 = entry_tile(ent[e]) * 64u;
     TL::load(rs_v, k0 * vrb, voff, s_v[e & 1], wave);
-    if (wave == 0)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_t*)&s_code[e & 1][0], 4, (k0 + lane) * 4u, 0, 0, 0);
+  };
+  // the row masks of a PARTIAL tile for this lane's rows (q-block rows 32 qb
+  // apart), fetched one step ahead of their use
+  auto load_bits = [&](int e, uint64_t (&bits)[QB]) {
+    const uint32_t en = ent[e];
+    if (entry_class(en, member) == TILE_PARTIAL) {  // wave-uniform
+      const uint64_t* p = qbits_row + int64_t(entry_tile(en)) * 64;
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) bits[qb] = p[32 * qb];
+    }
   };
 
-  // ---- LDS read addresses (bytes within a tile) ----
-  // K operand: row 32 kb + sigma(c), this lane's k-slots of each k-step
-  const int srow = sigma(c);
-  so.init(srow, hf);
   // V^T operand via transposed reads: group g = lane / 16 covers d columns
   // 32 db + 16 (g & 1) .. +15 and key rows 16 t4 + 8 (g >> 1) + 4 half .. +3
   int vaddr[DB][2];
@@ -115,29 +139,49 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
         vaddr[db][half] = TL::at(r, chunk) + 8 * (i & 1);
       }
   }
-  // S^T = K Q^T for one tile (two 32-key halves, independent chains)
-  auto scores = [&](const uint8_t* kt, f32x16 (&s)[2]) {
-    s[0] = f32x16{};
-    s[1] = f32x16{};
-    so.mma(kt, 0, s[0]);
-    so.mma(kt, 1, s[1]);
+  // S^T = K Q^T for one tile: two 32-key halves x QB query blocks, each K
+  // operand read from LDS once for the QB independent chains
+  // The K operand of k-step i is read FWD_PF steps before its MFMA; the
+  // sched_barriers keep LDS reads and MFMAs in this order (VALU, SALU and
+  // transcendental work may move across them, to fill the MFMA shadow).
+  auto scores = [&](const uint8_t* kt, f32x16 (&s)[2][QB]) {
+    constexpr int NS = 2 * SO::NK, PF = FWD_PF < NS ? FWD_PF : NS;  // steps: kb = i & 1, st = i >> 1
+    typename SO::A av[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) av[i] = so[0].read_a(kt, i & 1, i >> 1);
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const int kb = i & 1, st = i >> 1;
+      __builtin_amdgcn_sched_barrier(0x406);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) s[kb][qb] = so[qb].mma_a(av[i % PF], st, st == 0 ? f32x16{} : s[kb][qb]);
+      if (i + PF < NS) av[i % PF] = so[0].read_a(kt, (i + PF) & 1, (i + PF) >> 1);
+    }
+    __builtin_amdgcn_sched_barrier(0x406);
   };
 
   // the fp8 product carries the dequantisation scales of Q and K
   const float sl2 = a.sm_scale * 1.4426950408889634f * (Q8 ? a.q_scale[bh] * a.k_scale[bh] : 1.f);
   const float NEG_INF = -__builtin_inff();
-  float m_ref = NEG_INF, l0 = 0.f, l1 = 0.f, le0 = 0.f, le1 = 0.f;
-  f32x16 o[DB];
+  float m_ref[QB], l0[QB], l1[QB], le0[QB], le1[QB];
+  f32x16 o[QB][DB];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) o[db] = f32x16{};
-  const MaskTab mt = qmask(qcode);
-  const int i_lo = qblock * 128 + wave * 32;  // this wave's query rows: i_lo .. i_lo + 31
+  for (int qb = 0; qb < QB; ++qb) {
+    m_ref[qb] = NEG_INF;
+    l0[qb] = l1[qb] = le0[qb] = le1[qb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[qb][db] = f32x16{};
+  }
 
-  f32x16 s[2] = {f32x16{}, f32x16{}};
+  f32x16 s[2][QB];
+  uint64_t bits[QB], bits_next[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) bits[qb] = bits_next[qb] = 0;
   if (n > 0) {
     load_k(0);
     load_v(0);
     if (n > 1) load_k(1);
+    load_bits(0, bits);
     wait_vmem();
     __syncthreads();
     scores(s_k[0], s);
@@ -148,129 +192,152 @@ __global__ __launch_bounds__(256, 2) void k_fwd(AttnArgs a, const uint32_t* __re
     const uint32_t cur = ent[e];
     wait_vmem();
     __syncthreads();  // V(e) and K(e+1) landed; every wave is done with K(e) and V(e-1)
-    if (e + 1 < n) load_v(e + 1);
+    if (e + 1 < n) {
+      load_v(e + 1);
+      load_bits(e + 1, bits_next);
+    }
     if (e + 2 < n) load_k(e + 2);
-    const int k0 = int(cur >> 1) * 64;
 
-    if (!(cur & 1u)) {  // PARTIAL tile: register r of s[kb] holds key k0 + 32 kb + 16 (r / 8) + 8 hf + r % 8
+    const uint32_t mcls = entry_class(cur, member);
+    if (mcls != TILE_FULL) {  // wave-uniform.  Register r of s[kb][qb] holds key 32 kb + 16 (r / 8) + 8 hf + r % 8
+      // of the tile: bit 16 (r / 8) + r % 8 of word kb of the row mask shifted by 8 hf
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int j0 = k0 + 32 * kb;
-        const bool below = j0 + 31 <= i_lo, above = j0 > i_lo + 31;
+      for (int qb = 0; qb < QB; ++qb) {
+        const uint64_t rowbits = mcls == TILE_PARTIAL ? bits[qb] : 0u;  // EMPTY: nothing allowed
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int jl = 32 * kb + 16 * t + 8 * hf;
-          const u32x4 c0 = *reinterpret_cast<const u32x4*>(&s_code[buf][jl]);
-          const u32x4 c1 = *reinterpret_cast<const u32x4*>(&s_code[buf][jl + 4]);
+        for (int kb = 0; kb < 2; ++kb) {
+          const uint32_t w = uint32_t(rowbits >> (32 * kb)) >> (8 * hf);
 #pragma unroll
-          for (int x = 0; x < 8; ++x) {
-            const uint32_t kc = x < 4 ? c0[x] : c1[x - 4];
-            uint32_t tbl = below ? mt.hi : mt.lo;
-            if (!below && !above) tbl = (k0 + jl + x <= qrow) ? mt.hi : mt.lo;
-            s[kb][8 * t + x] = mask_score(s[kb][8 * t + x], tbl, kc, kc, mt.rsh);
-          }
+          for (int r = 0; r < 16; ++r) s[kb][qb][r] = mask_bit(s[kb][qb][r], w, 16 * (r >> 3) + (r & 7));
         }
       }
     }
-    // running max of this lane's row; rescale only when it grows by > 2^8
-    float mx = NEG_INF;
+    // running max of this lane's rows; rescale only when it grows by > 2^8
+    float ms[QB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int qb = 0; qb < QB; ++qb) {
+      float mx = NEG_INF;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-    mx = xhalf_max(mx);
-    const float m_new = fmaxf(m_ref, mx);
-    if ((m_new - m_ref) * sl2 > 8.f) {  // false for -inf - -inf (NaN); per lane
-      const float alpha = (m_ref == NEG_INF) ? 0.f : fast_exp2((m_ref - m_new) * sl2);
-      m_ref = m_new;
-      l0 *= alpha;
-      l1 *= alpha;
-      le0 *= alpha;
-      le1 *= alpha;
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int db = 0; db < DB; ++db) o[db] *= alpha;
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][qb][r]);
+      mx = xhalf_max(mx);
+      const float m_new = fmaxf(m_ref[qb], mx);
+      if ((m_new - m_ref[qb]) * sl2 > 8.f) {  // false for -inf - -inf (NaN); per lane
+        const float alpha = (m_ref[qb] == NEG_INF) ? 0.f : fast_exp2((m_ref[qb] - m_new) * sl2);
+        m_ref[qb] = m_new;
+        l0[qb] *= alpha;
+        l1[qb] *= alpha;
+        le0[qb] *= alpha;
+        le1[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[qb][db] *= alpha;
+      }
+      ms[qb] = (m_ref[qb] == NEG_INF) ? 0.f : m_ref[qb] * sl2;
     }
-    const float ms = (m_ref == NEG_INF) ? 0.f : m_ref * sl2;
 
     // softmax of tile e (VALU) alongside S of tile e+1 (MFMA; computed from
     // the other K buffer even past the last tile, where it is simply unused)
-    u32x4 pk[2][2];
+    u32x4 pk[QB][2][2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      float p[16];
+    for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(s[kb][r], sl2, -ms));
+      for (int kb = 0; kb < 2; ++kb) {
+        float p[16];
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        le0 += p[r];
-        le1 += p[r + 1];
-      }
+        for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(s[kb][qb][r], sl2, -ms[qb]));
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        pk[kb][t] = u32x4{pack2<E>(p[8 * t + 0], p[8 * t + 1]), pack2<E>(p[8 * t + 2], p[8 * t + 3]),
-                          pack2<E>(p[8 * t + 4], p[8 * t + 5]), pack2<E>(p[8 * t + 6], p[8 * t + 7])};
-        l0 = acc_pair<E>(pk[kb][t][0], l0);
-        l1 = acc_pair<E>(pk[kb][t][1], l1);
-        l0 = acc_pair<E>(pk[kb][t][2], l0);
-        l1 = acc_pair<E>(pk[kb][t][3], l1);
+        for (int r = 0; r < 16; r += 2) {
+          le0[qb] += p[r];
+          le1[qb] += p[r + 1];
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          pk[qb][kb][t] = u32x4{pack2<E>(p[8 * t + 0], p[8 * t + 1]), pack2<E>(p[8 * t + 2], p[8 * t + 3]),
+                                pack2<E>(p[8 * t + 4], p[8 * t + 5]), pack2<E>(p[8 * t + 6], p[8 * t + 7])};
+          l0[qb] = acc_pair<E>(pk[qb][kb][t][0], l0[qb]);
+          l1[qb] = acc_pair<E>(pk[qb][kb][t][1], l1[qb]);
+          l0[qb] = acc_pair<E>(pk[qb][kb][t][2], l0[qb]);
+          l1[qb] = acc_pair<E>(pk[qb][kb][t][3], l1[qb]);
+        }
       }
     }
     scores(s_k[buf ^ 1], s);
-    // O^T += V^T P^T for tile e
+    // O^T += V^T P^T for tile e, each V^T operand read once for the QB blocks
+    // and FWD_PFV steps ahead of its MFMA (steps: t4 = i / DB, db = i % DB)
     const uint8_t* vt = s_v[buf];
-#pragma unroll
-    for (int t4 = 0; t4 < 4; ++t4) {
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
+    {
+      constexpr int NV = 4 * DB, PFV = FWD_PFV < NV ? FWD_PFV : NV;
+      auto read_v = [&](int i) {
+        const int t4 = i / DB, db = i % DB;
         const u32x2 lo = ds_read_tr16(vt + vaddr[db][0] + t4 * 16 * TL::ROWB);
         const u32x2 hi = ds_read_tr16(vt + vaddr[db][1] + t4 * 16 * TL::ROWB);
-        o[db] = mfma32x32x16<E>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[t4 >> 1][t4 & 1], o[db]);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      };
+      u32x4 vv[PFV];
+#pragma unroll
+      for (int i = 0; i < PFV; ++i) vv[i] = read_v(i);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int t4 = i / DB, db = i % DB;
+        __builtin_amdgcn_sched_barrier(0x406);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) o[qb][db] = mfma32x32x16<E>(vv[i % PFV], pk[qb][t4 >> 1][t4 & 1], o[qb][db]);
+        if (i + PFV < NV) vv[i % PFV] = read_v(i + PFV);
       }
+      __builtin_amdgcn_sched_barrier(0x406);
     }
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) bits[qb] = bits_next[qb];
   }
 
   // ---- epilogue: normalise, store O and LSE ----
   // O is normalised by the sum of the ROUNDED P that entered P V (exact
   // convex weights); LSE by the exact fp32 sum, which is what the backward's
   // recomputed P = exp2(S c - LSE) must sum to
-  const float l_tot = xhalf_sum(l0 + l1);
-  const float l_exact = xhalf_sum(le0 + le1);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (qvalid) {
-    uint16_t* og = static_cast<uint16_t*>(a.o) + b * a.o_strides[0] + h * a.o_strides[1] + qrow * a.o_strides[2];
-    // optional rounding residual O - bf16(O), so the backward's Delta can be
-    // formed from O to ~16 significant bits (contiguous [B, H, T, D])
-    uint16_t* lg = a.o_lo == nullptr ? nullptr
-                                     : static_cast<uint16_t*>(a.o_lo) + (int64_t(bh) * T + qrow) * D;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
+  for (int qb = 0; qb < QB; ++qb) {
+    const float l_tot = xhalf_sum(l0[qb] + l1[qb]);
+    const float l_exact = xhalf_sum(le0[qb] + le1[qb]);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    if (qvalid[qb]) {
+      const int row = qrow[qb];
+      uint16_t* og = static_cast<uint16_t*>(a.o) + b * a.o_strides[0] + h * a.o_strides[1] + row * a.o_strides[2];
+      // optional rounding residual O - bf16(O), so the backward's Delta can be
+      // formed from O to ~16 significant bits (contiguous [B, H, T, D])
+      uint16_t* lg = a.o_lo == nullptr ? nullptr
+                                       : static_cast<uint16_t*>(a.o_lo) + (int64_t(bh) * T + row) * D;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = 32 * db + 8 * g + 4 * hf;
-        float f[4];
+      for (int db = 0; db < DB; ++db) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) f[i] = o[db][4 * g + i] * inv;
-        const u32x2 w = {pack2<E>(f[0], f[1]), pack2<E>(f[2], f[3])};
-        *reinterpret_cast<u32x2*>(og + d0) = w;
-        if (lg != nullptr) {
-          const u32x2 r = {pack2<E>(f[0] - to_f32<E>(uint16_t(w[0] & 0xFFFFu)), f[1] - to_f32<E>(uint16_t(w[0] >> 16))),
-                           pack2<E>(f[2] - to_f32<E>(uint16_t(w[1] & 0xFFFFu)), f[3] - to_f32<E>(uint16_t(w[1] >> 16)))};
-          *reinterpret_cast<u32x2*>(lg + d0) = r;
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = 32 * db + 8 * g + 4 * hf;
+          float f[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) f[i] = o[qb][db][4 * g + i] * inv;
+          const u32x2 w = {pack2<E>(f[0], f[1]), pack2<E>(f[2], f[3])};
+          *reinterpret_cast<u32x2*>(og + d0) = w;
+          if (lg != nullptr) {
+            const u32x2 r = {pack2<E>(f[0] - to_f32<E>(uint16_t(w[0] & 0xFFFFu)), f[1] - to_f32<E>(uint16_t(w[0] >> 16))),
+                             pack2<E>(f[2] - to_f32<E>(uint16_t(w[1] & 0xFFFFu)), f[3] - to_f32<E>(uint16_t(w[1] >> 16)))};
+            *reinterpret_cast<u32x2*>(lg + d0) = r;
+          }
         }
       }
+      if (a.lse != nullptr && hf == 0)
+        a.lse[int64_t(bh) * T + row] = l_exact > 0.f ? m_ref[qb] * sl2 + fast_log2(l_exact) : NEG_INF;
     }
-    if (a.lse != nullptr && hf == 0)
-      a.lse[int64_t(bh) * T + qrow] = l_exact > 0.f ? m_ref * sl2 + fast_log2(l_exact) : NEG_INF;
   }
 }
 
 template <class E, int D, bool Q8 = false>
 static void launch_fwd_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
+  constexpr int QB = FWD_QB;
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const int nQB = L.n_fwd_blocks;
   const unsigned grid = unsigned(a.B) * a.H * nQB;
-  hipLaunchKernelGGL((k_fwd<E, D, Q8>), dim3(grid), dim3(256), 0, st, a,
-                     reinterpret_cast<const uint32_t*>(plan + L.codes),
+  hipLaunchKernelGGL((k_fwd<E, D, Q8, QB>), dim3(grid), dim3(256 / QB), 0, st, a,
+                     reinterpret_cast<const uint64_t*>(plan + L.qbits),
                      reinterpret_cast<const uint32_t*>(plan + L.fwd_list),
                      reinterpret_cast<const int32_t*>(plan + L.fwd_count), L.nT, nQB);
 }

@@ -18,8 +18,17 @@ inline int fwd_rows_per_block(int /*D*/) { return 128; }
 inline int dq_rows_per_block(int /*D*/) { return 128; }
 inline int dkdv_keys_per_block(int /*D*/) { return 128; }
 
+// Work-list entry: (tile << 8) | class of group member r in bits 2r..2r+1
+// (r < 4: the row blocks of the list's group), so a wave reads its own
+// member's class (FULL: no mask, EMPTY: nothing allowed, PARTIAL: bit masks).
+KD_DEV inline uint32_t entry_tile(uint32_t e) { return e >> 8; }
+KD_DEV inline uint32_t entry_class(uint32_t e, int r) { return (e >> (2 * r)) & 3u; }
+KD_DEV inline bool entry_full(uint32_t e, int group) {
+  return (e & 0xFFu) == (0xAAu & ((1u << (2 * group)) - 1u));
+}
+
 struct PlanLayout {
-  size_t codes, rep, cls, nnz, fwd_list, fwd_count, dq_list, dq_count, dkdv_list, dkdv_count, total;
+  size_t codes, rep, cls, nnz, fwd_list, fwd_count, dq_list, dq_count, dkdv_list, dkdv_count, qbits, kbits, total;
   int nT, fwd_group, dq_group, dkdv_group, n_fwd_blocks, n_dq_blocks, n_dkdv_blocks;
 };
 

@@ -7,8 +7,12 @@
 //   codes   u32 [B, T]            token code (layout in kd_common.h)
 //   cls     u8  [B, nT, nT]       0 EMPTY / 1 PARTIAL / 2 FULL per 64x64 tile
 //   nnz     i32 [B, nT, nT]       allowed entries per tile
-//   lists   u32 [B, nRB, nT]      per row block: (tile << 1) | full, ascending
+//   lists   u32 [B, nRB, nT]      per row block: (tile << 8) | member classes, ascending
 //   counts  i32 [B, nRB]
+//   qbits   u64 [B, nT, nT, 64]   PARTIAL tiles: row r's allowed keys (bit j = key 64 kt + j)
+//   kbits   u64 [B, nT, nT, 64]   PARTIAL tiles: key r's allowed queries (bit i = query 64 qt + i)
+// The bit masks let the attention kernels mask a PARTIAL tile with two VALU
+// ops per score instead of re-evaluating the rule.
 #include "kd_internal.h"
 
 namespace kd {
@@ -90,9 +94,11 @@ __global__ void k_codes(MetaArgs m, const uint32_t* rep, uint32_t* codes) {
 }
 
 // ---- 64x64 tile classifier ---------------------------------------------
-// One wave per tile: lane = query row, loop over the tile's 64 keys.
+// One wave per tile: lane = query row, loop over the tile's 64 keys, building
+// the row's 64-bit mask; PARTIAL tiles also store the row masks and, through
+// 64 ballots (column j of the tile = ballot of bit j), the column masks.
 __global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, int nT, uint8_t* cls,
-                                                 int32_t* nnz) {
+                                                 int32_t* nnz, uint64_t* qbits, uint64_t* kbits) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int qt = blockIdx.y, b = blockIdx.z;
   const int kt0 = blockIdx.x * 4;
@@ -106,13 +112,29 @@ __global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, i
   if (kt >= nT) return;
   const int i = qt * 64 + lane;
   const uint32_t qc = (i < T) ? codes[int64_t(b) * T + i] : 0u;
-  int cnt = 0;
-  for (int x = 0; x < 64; ++x) cnt += allow(qc, s_k[wave * 64 + x], i, kt * 64 + x) ? 1 : 0;
+  uint32_t lo = 0, hi = 0;
+#pragma unroll 8
+  for (int x = 0; x < 32; ++x) {
+    lo |= uint32_t(allow(qc, s_k[wave * 64 + x], i, kt * 64 + x)) << x;
+    hi |= uint32_t(allow(qc, s_k[wave * 64 + 32 + x], i, kt * 64 + 32 + x)) << x;
+  }
+  int cnt = __builtin_popcount(lo) + __builtin_popcount(hi);
   for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off);
+  const int64_t o = (int64_t(b) * nT + qt) * nT + kt;
+  const uint8_t k = cnt == 0 ? TILE_EMPTY : (cnt == 64 * 64 ? TILE_FULL : TILE_PARTIAL);
   if (lane == 0) {
-    const int64_t o = (int64_t(b) * nT + qt) * nT + kt;
-    cls[o] = cnt == 0 ? TILE_EMPTY : (cnt == 64 * 64 ? TILE_FULL : TILE_PARTIAL);
+    cls[o] = k;
     if (nnz != nullptr) nnz[o] = cnt;
+  }
+  if (k == TILE_PARTIAL) {  // wave-uniform
+    const uint64_t row = (uint64_t(hi) << 32) | lo;
+    qbits[o * 64 + lane] = row;
+    uint64_t col = 0;
+    for (int j = 0; j < 64; ++j) {
+      const uint64_t bj = __builtin_amdgcn_ballot_w64(((row >> j) & 1u) != 0);
+      if (lane == j) col = bj;
+    }
+    kbits[o * 64 + lane] = col;
   }
 }
 
@@ -140,21 +162,20 @@ __global__ __launch_bounds__(64) void k_lists(const uint8_t* __restrict__ cls, i
   int n = 0;
   for (int c0 = 0; c0 < nT; c0 += 64) {
     const int c = c0 + lane;
-    bool any_ne = false, all_full = true;
+    bool any_ne = false;
+    uint32_t classes = 0;
     if (c < nT) {
       for (int r = 0; r < sp.group; ++r) {
         const int row = rb * sp.group + r;
         uint8_t k = TILE_EMPTY;
         if (row < nT) k = sp.by_key ? base[int64_t(c) * nT + row] : base[int64_t(row) * nT + c];
         any_ne |= (k != TILE_EMPTY);
-        all_full &= (k == TILE_FULL);
+        classes |= uint32_t(k) << (2 * r);
       }
-    } else {
-      all_full = false;
     }
     const uint64_t m = __builtin_amdgcn_ballot_w64(any_ne);
     const int pos = n + __builtin_popcountll(m & ((uint64_t(1) << lane) - 1));
-    if (any_ne) out[pos] = (uint32_t(c) << 1) | (all_full ? 1u : 0u);
+    if (any_ne) out[pos] = (uint32_t(c) << 8) | classes;
     n += __builtin_popcountll(m);
   }
   for (int c = n + lane; c < nT; c += 64) out[c] = 0;
@@ -207,6 +228,8 @@ PlanLayout plan_layout(int B, int T, int D) {
   L.dq_count = take(size_t(B) * nq * 4);
   L.dkdv_list = take(size_t(B) * nk * nT * 4);
   L.dkdv_count = take(size_t(B) * nk * 4);
+  L.qbits = take(BTT * 64 * 8);
+  L.kbits = take(BTT * 64 * 8);
   L.total = off;
   return L;
 }
@@ -224,7 +247,8 @@ int launch_plan(const MetaArgs& m, uint8_t* plan, hipStream_t st) {
     hipLaunchKernelGGL(k_span_rep, dim3(nchunk, nchunk, m.B), dim3(256), 0, st, m, rep);
   }
   hipLaunchKernelGGL(k_codes, dim3(unsigned((BT + 255) / 256)), dim3(256), 0, st, m, rep, codes);
-  hipLaunchKernelGGL(k_tilemap, dim3((L.nT + 3) / 4, L.nT, m.B), dim3(256), 0, st, codes, m.T, L.nT, cls, nnz);
+  hipLaunchKernelGGL(k_tilemap, dim3((L.nT + 3) / 4, L.nT, m.B), dim3(256), 0, st, codes, m.T, L.nT, cls, nnz,
+                     reinterpret_cast<uint64_t*>(plan + L.qbits), reinterpret_cast<uint64_t*>(plan + L.kbits));
   ListSpecs specs;
   specs.l[0] = {reinterpret_cast<uint32_t*>(plan + L.fwd_list), reinterpret_cast<int32_t*>(plan + L.fwd_count),
                 L.fwd_group, 0, L.n_fwd_blocks};

@@ -107,10 +107,16 @@ struct ScoreOp;
 template <class E, int D>
 struct ScoreOp<E, D, false> {
   using TL = Tile<D>;
+  using A = u32x4;  // one k-step's A operand
   static constexpr int ROW_BYTES = D * 2;
   static constexpr int NK = D / 16;
   u32x4 b[NK];
   int addr[NK];
+  // k-step st of rows 32 kb + sigma(c): read it, then multiply it in
+  KD_DEV A read_a(const uint8_t* tile, int kb, int st) const {
+    return *reinterpret_cast<const u32x4*>(tile + addr[st] + kb * 32 * TL::ROWB);
+  }
+  KD_DEV f32x16 mma_a(const A& a, int st, const f32x16& c) const { return mfma32x32x16<E>(a, b[st], c); }
   KD_DEV void load_b(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, int hf) {
 #pragma unroll
     for (int st = 0; st < NK; ++st) b[st] = buf_load16(rs, row_off + (16 * st + 8 * hf) * 2);
@@ -125,15 +131,35 @@ struct ScoreOp<E, D, false> {
     for (int st = 0; st < NK; ++st)
       s = mfma32x32x16<E>(*reinterpret_cast<const u32x4*>(tile + addr[st] + kb * 32 * TL::ROWB), b[st], s);
   }
+  // s[q] += X[32 kb + rows] Y_q^T for N B operands sharing each A read
+  // (addresses of op[0]; every op was init()-ed with the same row)
+  template <int N>
+  KD_DEV static void mma_n(const uint8_t* tile, int kb, const ScoreOp (&op)[N], f32x16 (&s)[N]) {
+#pragma unroll
+    for (int st = 0; st < NK; ++st) {
+      const u32x4 av = *reinterpret_cast<const u32x4*>(tile + op[0].addr[st] + kb * 32 * TL::ROWB);
+#pragma unroll
+      for (int q = 0; q < N; ++q) s[q] = mfma32x32x16<E>(av, op[q].b[st], s[q]);
+    }
+  }
 };
 
 template <class E, int D>
 struct ScoreOp<E, D, true> {
   using TL = Tile<D / 2>;  // D bytes per row, laid out as D/2 16-bit columns
+  using A = i32x8;
   static constexpr int ROW_BYTES = D;
   static constexpr int NK = D / 64;
   i32x8 b[NK];
   int addr[NK][2];
+  KD_DEV A read_a(const uint8_t* tile, int kb, int st) const {
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(tile + addr[st][0] + kb * 32 * TL::ROWB);
+    const u32x4 hi = *reinterpret_cast<const u32x4*>(tile + addr[st][1] + kb * 32 * TL::ROWB);
+    return i32x8{int(lo[0]), int(lo[1]), int(lo[2]), int(lo[3]), int(hi[0]), int(hi[1]), int(hi[2]), int(hi[3])};
+  }
+  KD_DEV f32x16 mma_a(const A& a, int st, const f32x16& c) const {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b[st], c, 0, 0, 0, 127, 0, 127);
+  }
   KD_DEV void load_b(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, int hf) {
 #pragma unroll
     for (int st = 0; st < NK; ++st) {
@@ -156,6 +182,18 @@ struct ScoreOp<E, D, true> {
       const u32x4 hi = *reinterpret_cast<const u32x4*>(tile + addr[st][1] + kb * 32 * TL::ROWB);
       const i32x8 av = {int(lo[0]), int(lo[1]), int(lo[2]), int(lo[3]), int(hi[0]), int(hi[1]), int(hi[2]), int(hi[3])};
       s = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, b[st], s, 0, 0, 0, 127, 0, 127);
+    }
+  }
+  template <int N>
+  KD_DEV static void mma_n(const uint8_t* tile, int kb, const ScoreOp (&op)[N], f32x16 (&s)[N]) {
+#pragma unroll
+    for (int st = 0; st < NK; ++st) {
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(tile + op[0].addr[st][0] + kb * 32 * TL::ROWB);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(tile + op[0].addr[st][1] + kb * 32 * TL::ROWB);
+      const i32x8 av = {int(lo[0]), int(lo[1]), int(lo[2]), int(lo[3]), int(hi[0]), int(hi[1]), int(hi[2]), int(hi[3])};
+#pragma unroll
+      for (int q = 0; q < N; ++q)
+        s[q] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, op[q].b[st], s[q], 0, 0, 0, 127, 0, 127);
     }
   }
 };

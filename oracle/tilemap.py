@@ -46,7 +46,8 @@ def q_lists(cls: np.ndarray, rq: int):
     """Per q-block (``rq`` base q-tiles) list of non-empty base k-tiles.
 
     Returns ``(entries [B, nQB, nK] uint32, counts [B, nQB] int32)``; entry =
-    ``(k_tile << 1) | is_full`` in ascending k order, zero padded.
+    ``(k_tile << 8) | sum_r class(q-tile rq*block + r, k_tile) << 2r`` in
+    ascending k order, zero padded; a member past the last tile is EMPTY.
     """
     B, nQ, nK = cls.shape
     nqb = -(-nQ // rq)
@@ -54,13 +55,16 @@ def q_lists(cls: np.ndarray, rq: int):
     pad[:, :nQ] = cls
     grp = pad.reshape(B, nqb, rq, nK).transpose(0, 1, 3, 2)  # [B, nqb, nK, rq]
     comb = _combine(grp)
+    members = np.zeros((B, nqb, nK), dtype=np.uint32)
+    for r in range(rq):
+        members |= grp[..., r].astype(np.uint32) << (2 * r)
     entries = np.zeros((B, nqb, nK), dtype=np.uint32)
     counts = np.zeros((B, nqb), dtype=np.int32)
     for b in range(B):
         for q in range(nqb):
             ks = np.nonzero(comb[b, q] != EMPTY)[0]
             counts[b, q] = len(ks)
-            entries[b, q, :len(ks)] = (ks.astype(np.uint32) << 1) | (comb[b, q, ks] == FULL)
+            entries[b, q, :len(ks)] = (ks.astype(np.uint32) << 8) | members[b, q, ks]
     return entries, counts
 
 
@@ -68,9 +72,28 @@ def k_lists(cls: np.ndarray, rk: int):
     """Per k-block (``rk`` base k-tiles) list of non-empty base q-tiles.
 
     Returns ``(entries [B, nKB, nQ] uint32, counts [B, nKB] int32)``; entry =
-    ``(q_tile << 1) | is_full`` in ascending q order, zero padded.
+    ``(q_tile << 8) | sum_r class(q_tile, k-tile rk*block + r) << 2r``.
     """
     return q_lists(np.ascontiguousarray(cls.transpose(0, 2, 1)), rk)
+
+
+def tile_bits(mask: np.ndarray, tile: int = 64):
+    """Row and column bit masks of every 64x64 tile of a ``[B, T, T]`` mask.
+
+    Returns ``(qbits, kbits)``, both ``[B, nT, nT, 64]`` uint64: ``qbits[b, qt,
+    kt, r]`` has bit ``j`` set iff query ``64 qt + r`` may see key ``64 kt + j``;
+    ``kbits[b, qt, kt, r]`` has bit ``i`` set iff query ``64 qt + i`` may see key
+    ``64 kt + r``.  Entries past T are not allowed.
+    """
+    B, T, _ = mask.shape
+    n = -(-T // tile)
+    pad = np.zeros((B, n * tile, n * tile), dtype=bool)
+    pad[:, :T, :T] = mask
+    tiles = pad.reshape(B, n, tile, n, tile).transpose(0, 1, 3, 2, 4)  # [B, qt, kt, row, col]
+    weights = np.left_shift(np.uint64(1), np.arange(tile, dtype=np.uint64))
+    qbits = (tiles.astype(np.uint64) * weights).sum(axis=-1, dtype=np.uint64)
+    kbits = (tiles.transpose(0, 1, 2, 4, 3).astype(np.uint64) * weights).sum(axis=-1, dtype=np.uint64)
+    return qbits, kbits
 
 
 def useful_entries(mask: np.ndarray) -> int:

@@ -42,6 +42,11 @@ def _check_plan(p, mask):
         ent, counts = fn(cls, group)
         np.testing.assert_array_equal(p[f"{name}_count"], counts, err_msg=name)
         np.testing.assert_array_equal(p[f"{name}_list"].view(np.uint32), ent, err_msg=name)
+    # row / column bit masks, bit-exact on every PARTIAL tile (the only ones the kernels read)
+    qbits, kbits = tilemap.tile_bits(mask, 64)
+    part = cls == tilemap.PARTIAL
+    np.testing.assert_array_equal(p["qbits"].view(np.uint64)[part], qbits[part], err_msg="qbits")
+    np.testing.assert_array_equal(p["kbits"].view(np.uint64)[part], kbits[part], err_msg="kbits")
 
 
 @pytest.mark.parametrize("T,causal", [(256, True), (2048, True), (200, False), (1, True), (77, True)])

@@ -154,15 +154,25 @@ def test_classify_and_lists_bruteforce():
             kent, kcnt = tilemap.k_lists(cls, rq)
             for b in range(2):
                 for blk in range(cnt.shape[1]):
-                    rows = [r for r in range(blk * rq, blk * rq + rq) if r < n]
-                    want = [(c << 1) | int(all(cls[b, r, c] == 2 for r in rows) and len(rows) == rq)
-                            for c in range(n) if any(cls[b, r, c] != 0 for r in rows)]
+                    rows = list(range(blk * rq, blk * rq + rq))  # members past n are EMPTY
+                    want = [(c << 8) | sum(int(cls[b, r, c]) << (2 * i) for i, r in enumerate(rows) if r < n)
+                            for c in range(n) if any(cls[b, r, c] != 0 for r in rows if r < n)]
                     assert ent[b, blk, : cnt[b, blk]].tolist() == want
                 for blk in range(kcnt.shape[1]):
-                    cols = [r for r in range(blk * rq, blk * rq + rq) if r < n]
-                    want = [(r << 1) | int(all(cls[b, r, c] == 2 for c in cols) and len(cols) == rq)
-                            for r in range(n) if any(cls[b, r, c] != 0 for c in cols)]
+                    cols = list(range(blk * rq, blk * rq + rq))
+                    want = [(r << 8) | sum(int(cls[b, r, c]) << (2 * i) for i, c in enumerate(cols) if c < n)
+                            for r in range(n) if any(cls[b, r, c] != 0 for c in cols if c < n)]
                     assert kent[b, blk, : kcnt[b, blk]].tolist() == want
+        qbits, kbits = tilemap.tile_bits(m, 64)
+        for b in range(2):  # brute force over every entry of every tile
+            for i in range(T):
+                for j in range(T):
+                    qt, r, kt, x = i // 64, i % 64, j // 64, j % 64
+                    assert bool((int(qbits[b, qt, kt, r]) >> x) & 1) == bool(m[b, i, j])
+                    assert bool((int(kbits[b, qt, kt, x]) >> r) & 1) == bool(m[b, i, j])
+        pad_q = qbits[:, -1, -1, (T - 1) % 64 + 1:] if T % 64 else None
+        if pad_q is not None:
+            assert not pad_q.any()  # rows past T see nothing
 
 
 # ----------------------------------------------------------------- attention
