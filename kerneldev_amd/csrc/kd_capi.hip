@@ -105,6 +105,7 @@ int kd_hadamard(const kd_rot_args* a, void* stream) {
   if (a->D != 64 && a->D != 128) return fail(KD_ERR_UNSUPPORTED, "head dim must be 64 or 128");
   if (a->dtype != KD_BF16 && a->dtype != KD_F16) return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16 or fp16");
   if (a->signs == nullptr) return fail(KD_ERR_INVALID, "signs is NULL");
+  if (int64_t(a->B) * a->H > 65535) return fail(KD_ERR_UNSUPPORTED, "B * H must be <= 65535");
   int r;
   if ((r = check_tensor(a->x, a->x_strides, "x", a->T, a->D)) || (r = check_tensor(a->y, a->y_strides, "y", a->T, a->D)))
     return r;

@@ -13,47 +13,58 @@
 // strides 1, 2, 4 stay inside a lane, strides 8 .. d/2 pair lane t with
 // lane t ^ (h / 8).  Optionally the kernel also records max |y| per (b, h)
 // (the absmax the fp8 path scales by).
+#include <type_traits>
+
 #include "kd_internal.h"
 
 namespace kd {
 
-constexpr int HAD_ITERS = 16;  // rows per thread (one chunk per block)
 
-// One block transforms a contiguous chunk of ITERS * RPB rows, RPB per
-// iteration, with the next iteration's row loaded while the current one is
-// transformed.  The optional absmax is kept per thread as (b*H + h, max) over
-// its rows, then reduced over the block, so a chunk inside one head costs one
-// atomic (chunks that straddle heads flush per thread).
-template <class E, int D, bool INV>
+// Lane exchanges inside a row's D/8 lanes through DPP (no LDS traffic):
+// partner lane l ^ m for m = 1, 2 (quad_perm), 4 (half-row mirror, then
+// quad reverse) and 8 (row mirror, then half-row mirror).
+template <int M>
+KD_DEV float xor_lane(float v) {
+  const int x = __float_as_int(v);
+  if constexpr (M == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));
+  if constexpr (M == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
+  if constexpr (M == 4) {
+    const int t = __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    return __int_as_float(__builtin_amdgcn_mov_dpp(t, 0x1B, 0xF, 0xF, false));  // quad_perm [3,2,1,0]
+  }
+  const int t = __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false);  // row_mirror
+  return __int_as_float(__builtin_amdgcn_mov_dpp(t, 0x141, 0xF, 0xF, false));
+}
+
+// One block = ITERS x RPB consecutive rows of one (b, h) (grid: row chunks x
+// B*H), so the row index needs no division and the optional absmax is one
+// block reduction and one atomic per block.  Without the absmax a block does
+// one RPB-row step; with it, 16 steps, so that each (b, h) collects few
+// atomics.
+template <class E, int D, bool INV, int ITERS>
 __global__ __launch_bounds__(256) void k_hadamard(kd_rot_args a) {
   constexpr int TPR = D / 8;         // lanes per row
-  constexpr int RPB = 256 / TPR;     // rows per iteration
-  constexpr int ITERS = HAD_ITERS;
+  constexpr int RPB = 256 / TPR;     // rows per step
   const int tid = threadIdx.x, seg = tid % TPR;
-  const int64_t nrows = int64_t(a.B) * a.H * a.T;
-  const int64_t row0 = int64_t(blockIdx.x) * (ITERS * RPB) + tid / TPR;
-
+  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const uint16_t* xb = static_cast<const uint16_t*>(a.x) + b * a.x_strides[0] + h * a.x_strides[1] + seg * 8;
+  uint16_t* yb = static_cast<uint16_t*>(a.y) + b * a.y_strides[0] + h * a.y_strides[1] + seg * 8;
   float sg[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) sg[j] = a.signs[seg * 8 + j];
-
-  auto src = [&](int64_t row) {
-    const int64_t r = row < nrows ? row : nrows - 1;  // idle lanes still join the shuffles
-    const int t = int(r % a.T), bh = int(r / a.T), b = bh / a.H, h = bh % a.H;
-    return static_cast<const uint16_t*>(a.x) + b * a.x_strides[0] + h * a.x_strides[1] + t * a.x_strides[2] +
-           seg * 8;
-  };
-  int run_bh = -1;
-  float run_m = 0.f;
-  u32x4 xv = *reinterpret_cast<const u32x4*>(src(row0));
+  float m = 0.f;  // max |y| of the rounded outputs of this lane's rows
+  const int t0 = blockIdx.x * (ITERS * RPB) + tid / TPR;
+  u32x4 xv = *reinterpret_cast<const u32x4*>(xb + int64_t(t0 < a.T ? t0 : a.T - 1) * a.x_strides[2]);
+#pragma unroll 1
   for (int it = 0; it < ITERS; ++it) {
-    const int64_t row = row0 + int64_t(it) * RPB;
-    if (row - (tid / TPR) >= nrows) break;  // block-uniform: the chunk ran past the end
+    const int t = t0 + it * RPB;
+    if (t - tid / TPR >= a.T) break;  // block-uniform: the chunk ran past the end
+    const bool valid = t < a.T;       // idle lanes still join the exchanges
     u32x4 nxt = xv;
-    if (it + 1 < ITERS) nxt = *reinterpret_cast<const u32x4*>(src(row + RPB));
-    const bool valid = row < nrows;
-    const int64_t r = valid ? row : nrows - 1;
-    const int t = int(r % a.T), bh = int(r / a.T), b = bh / a.H, h = bh % a.H;
+    if (it + 1 < ITERS) {
+      const int tn = t + RPB;
+      nxt = *reinterpret_cast<const u32x4*>(xb + int64_t(tn < a.T ? tn : a.T - 1) * a.x_strides[2]);
+    }
     float y[8];
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -75,16 +86,18 @@ __global__ __launch_bounds__(256) void k_hadamard(kd_rot_args a) {
         y[j + hs] = u - v;
       }
     }
-    // cross-lane butterflies, strides 8 .. D/2
+    // cross-lane butterflies, strides 8 .. D/2: the lower lane of a pair keeps
+    // y + partner, the upper one partner - y; fma(y, +-1, partner) is exactly that sum
+    auto cross = [&](auto m_tag) {
+      constexpr int M = decltype(m_tag)::value;
+      const float sgn = (seg & M) ? -1.f : 1.f;
 #pragma unroll
-    for (int m = 1; m < TPR; m <<= 1) {
-      const bool upper = (seg & m) != 0;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float other = __shfl_xor(y[j], m, TPR);
-        y[j] = upper ? other - y[j] : y[j] + other;
-      }
-    }
+      for (int j = 0; j < 8; ++j) y[j] = __builtin_fmaf(y[j], sgn, xor_lane<M>(y[j]));
+    };
+    cross(std::integral_constant<int, 1>{});
+    cross(std::integral_constant<int, 2>{});
+    cross(std::integral_constant<int, 4>{});
+    if constexpr (TPR == 16) cross(std::integral_constant<int, 8>{});
     // fp32(1 / sqrt(D)), correctly rounded
     constexpr float scale = D == 64 ? 0x1p-3f : 0x1.6a09e6p-4f;
 #pragma unroll
@@ -97,48 +110,26 @@ __global__ __launch_bounds__(256) void k_hadamard(kd_rot_args a) {
 #pragma unroll
     for (int w = 0; w < 4; ++w) out[w] = pack2<E>(y[2 * w], y[2 * w + 1]);
     if (valid) {
-      uint16_t* yp = static_cast<uint16_t*>(a.y) + b * a.y_strides[0] + h * a.y_strides[1] +
-                     t * a.y_strides[2] + seg * 8;
-      *reinterpret_cast<u32x4*>(yp) = out;
-    }
-    if (a.amax != nullptr && valid) {
-      // |y| of the ROUNDED output (this lane's 8 elements)
-      float m = 0.f;
+      *reinterpret_cast<u32x4*>(yb + int64_t(t) * a.y_strides[2]) = out;
+      if (a.amax != nullptr) {
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        m = fmaxf(m, fabsf(to_f32<E>(uint16_t(out[w] & 0xFFFFu))));
-        m = fmaxf(m, fabsf(to_f32<E>(uint16_t(out[w] >> 16))));
+        for (int w = 0; w < 4; ++w) {
+          m = fmaxf(m, fabsf(to_f32<E>(uint16_t(out[w] & 0xFFFFu))));
+          m = fmaxf(m, fabsf(to_f32<E>(uint16_t(out[w] >> 16))));
+        }
       }
-      if (bh != run_bh) {
-        if (run_bh >= 0) atomicMax(reinterpret_cast<unsigned int*>(a.amax) + run_bh, __float_as_uint(run_m));
-        run_bh = bh;
-        run_m = 0.f;
-      }
-      run_m = fmaxf(run_m, m);
     }
     xv = nxt;
   }
-  if (a.amax == nullptr) return;
-  // block reduction when every thread's last head is the same (the usual case)
-  __shared__ int s_bh[256];
-  __shared__ float s_m[256];
-  s_bh[tid] = run_bh;
-  s_m[tid] = run_m;
-  __syncthreads();
-  const int bh0 = s_bh[0];
-  bool same = true;
-  for (int i = 0; i < 256; i += 64) same = same && __all(s_bh[i + (tid & 63)] == bh0);
-  if (same) {
-    if (bh0 < 0) return;
-    if (tid < 64) {
-      float m = fmaxf(fmaxf(s_m[tid], s_m[tid + 64]), fmaxf(s_m[tid + 128], s_m[tid + 192]));
+  if (a.amax == nullptr) return;  // uniform
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-      if (tid == 0) atomicMax(reinterpret_cast<unsigned int*>(a.amax) + bh0, __float_as_uint(m));
-    }
-  } else if (run_bh >= 0) {
-    atomicMax(reinterpret_cast<unsigned int*>(a.amax) + run_bh, __float_as_uint(run_m));
-  }
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  __shared__ float s_m[4];
+  if ((tid & 63) == 0) s_m[tid >> 6] = m;
+  __syncthreads();
+  if (tid == 0)
+    atomicMax(reinterpret_cast<unsigned int*>(a.amax) + bh,
+              __float_as_uint(fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]))));
 }
 
 // ---- fp8 e4m3 quantisation per (b, h) -----------------------------------
@@ -200,9 +191,16 @@ int launch_quant(const kd_quant_args& a, hipStream_t st) {
 
 template <class E, int D, bool INV>
 static void launch_rot_t(const kd_rot_args& a, hipStream_t st) {
-  constexpr int CHUNK = HAD_ITERS * (256 / (D / 8));
-  const int64_t rows = int64_t(a.B) * a.H * a.T;
-  hipLaunchKernelGGL((k_hadamard<E, D, INV>), dim3(unsigned((rows + CHUNK - 1) / CHUNK)), dim3(256), 0, st, a);
+  constexpr int RPB = 256 / (D / 8);
+  const dim3 block(256);
+  if (a.amax == nullptr) {
+    hipLaunchKernelGGL((k_hadamard<E, D, INV, 1>), dim3(unsigned((a.T + RPB - 1) / RPB), unsigned(a.B * a.H)), block,
+                       0, st, a);
+  } else {
+    constexpr int CH = 16 * RPB;
+    hipLaunchKernelGGL((k_hadamard<E, D, INV, 16>), dim3(unsigned((a.T + CH - 1) / CH), unsigned(a.B * a.H)), block,
+                       0, st, a);
+  }
 }
 
 int launch_hadamard(const kd_rot_args& a, hipStream_t st) {
