@@ -21,11 +21,11 @@
 // dK/dV kernel: 4 wave pairs x 32 keys per workgroup, 64 queries per step:
 //   S = Q K^T,  dP = dO V^T                (A = Q, dO rows from LDS; B = K, V regs)
 //   dV^T += dO^T P,  dK^T += Q^T dS        (A = dO^T, Q^T read transposed)
-// with S/P/dV on one wave of a pair and dP/dS/dK on the other.
+// with S/P/dV on one wave of a pair and dP/dS/dK (one tile behind) on the other.
 // Both keep the accumulated gradient transposed in registers so the MFMA
 // output of one product is the register-resident B operand of the next, and
 // both stream their tiles global -> LDS with buffer_load ... lds into the
-// swizzled layout of kd_tile.h, double buffered.
+// swizzled layout of kd_tile.h (double buffered; dK/dV's Q triple buffered).
 #include "kd_tile.h"
 
 namespace kd {
@@ -257,27 +257,30 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
 // The two waves of a pair split the work of their keys by role:
 //   role 0 ("P wave"):  S = Q K^T, P = exp2(S c - LSE)   -> dV^T += dO^T P
 //   role 1 ("dS wave"): dP = dO V^T, dS = P (dP - Delta) -> dK^T += Q^T dS
-// P goes from the P wave to the dS wave through LDS, lane to lane (both
-// waves hold the same MFMA output layout).  Each wave keeps one B operand
-// (K or V) and one accumulator (dV^T or dK^T) in registers, so a pair needs
-// about half the registers of one wave doing all four products, and the
-// pair shares a SIMD (waves w and w + 4), so one wave's VALU softmax runs
-// under the other's MFMAs.
+// P goes from the P wave to the dS wave through LDS (bf16, as the MFMA takes
+// it), lane to lane: both waves hold the same MFMA output layout.  Each wave
+// keeps one B operand (K or V) and one accumulator (dV^T or dK^T) in
+// registers, so a pair needs about half the registers of one wave doing all
+// four products; the pair shares a SIMD (waves w and w + 4).
+// The dS wave runs one query tile behind: in step e the P wave handles tile
+// e while the dS wave computes dP of tile e and finishes dS / dK of tile
+// e - 1 with the P written in step e - 1.  So one barrier per step orders
+// everything (tile e landed, P(e-1) written, P(e-2) and tile e-2 released),
+// at the price of a third Q buffer (dK reads Q of tile e - 1).
 template <class E, int D, bool Q8>
 __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __restrict__ kbits,
                                                  const uint32_t* __restrict__ list,
                                                  const int32_t* __restrict__ count, int nT, int nKB) {
   constexpr int NW = 8;
   using TL = Tile<D, NW>;
-  using SO8 = ScoreOp<E, D, true>;  // fp8 S = Q8 K8^T of the P waves
-  using TQ8 = Tile<Q8 ? D / 2 : D, NW>;  // only instantiated at D = 128 for fp8
+  using TQ8 = Tile<Q8 ? D / 2 : D, NW>;  // fp8 Q tiles (D bytes a row); only used at D = 128
   constexpr int DS = D / 16, DB = D / 32, NL = TL::LOADS_PER_WAVE, NL8 = TQ8::LOADS_PER_WAVE;
-  __shared__ __attribute__((aligned(1024))) uint8_t s_q[2][TL::BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_q[3][TL::BYTES];     // tile e % 3
   __shared__ __attribute__((aligned(1024))) uint8_t s_q8[Q8 ? 2 : 1][Q8 ? TQ8::BYTES : 16];
-  __shared__ __attribute__((aligned(1024))) uint8_t s_do[2][TL::BYTES];
-  __shared__ __attribute__((aligned(1024))) float s_p[4][2 * 16][64];  // [pair][register][lane]
+  __shared__ __attribute__((aligned(1024))) uint8_t s_do[2][TL::BYTES];    // tile e % 2
+  __shared__ __attribute__((aligned(1024))) u32x4 s_p[2][4][4][64];       // [e % 2][pair][k-step][lane]
   __shared__ __attribute__((aligned(256))) float s_lse[2][64];
-  __shared__ __attribute__((aligned(256))) float s_delta[2][64];
+  __shared__ __attribute__((aligned(256))) float s_delta[3][64];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
   const int pair = wave & 3, role = wave >> 2;
@@ -303,9 +306,15 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   const int krow = kblock * 128 + pair * 32 + c;
   const bool kvalid = krow < T;
   u32x4 bf[DS];
-  SO8 so8;  // fp8: the P waves' B operand is this lane's row of K8 instead
   if (Q8 && role == 0) {
-    so8.load_b(make_rsrc(a.k8 + int64_t(bh) * T * D, uint32_t(T) * D), uint32_t(krow) * D, hf);
+    // fp8: the P waves' B operand is this lane's row of K8; k-step st (64
+    // bytes) takes bytes 64 st + 32 hf .. + 31, kept in bf[2 st], bf[2 st + 1]
+    const auto rs8 = make_rsrc(a.k8 + int64_t(bh) * T * D, uint32_t(T) * D);
+#pragma unroll
+    for (int st = 0; st < D / 64; ++st) {
+      bf[2 * st] = buf_load16(rs8, uint32_t(krow) * D + 64 * st + 32 * hf);
+      bf[2 * st + 1] = buf_load16(rs8, uint32_t(krow) * D + 64 * st + 32 * hf + 16);
+    }
   } else {
     const auto rs_b = role == 0 ? make_rsrc(kg, uint32_t(T) * krb) : make_rsrc(vg, uint32_t(T) * vrb);
     const uint32_t brb = role == 0 ? krb : vrb;
@@ -326,15 +335,15 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   TL::load_offsets(wave, lane, dorb, dooff);
   TQ8::load_offsets(wave, lane, uint32_t(D), q8off);
   const auto rs_q8 = make_rsrc(Q8 ? a.q8 + int64_t(bh) * T * D : nullptr, Q8 ? uint32_t(T) * D : 0u);
-  auto load_tile = [&](int qt, int buf) {
-    const uint32_t q0 = uint32_t(qt) * 64u;
-    TL::load(rs_q, q0 * qrb, qoff, s_q[buf], wave);
-    TL::load(rs_do, q0 * dorb, dooff, s_do[buf], wave);
-    if constexpr (Q8) TQ8::load(rs_q8, q0 * uint32_t(D), q8off, s_q8[buf], wave);
+  auto load_tile = [&](int e) {
+    const uint32_t q0 = entry_tile(ent[e]) * 64u;
+    TL::load(rs_q, q0 * qrb, qoff, s_q[e % 3], wave);
+    TL::load(rs_do, q0 * dorb, dooff, s_do[e & 1], wave);
+    if constexpr (Q8) TQ8::load(rs_q8, q0 * uint32_t(D), q8off, s_q8[e & 1], wave);
     if (wave == 0)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, (lds_t*)&s_lse[buf][0], 4, (q0 + lane) * 4u, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, (lds_t*)&s_lse[e & 1][0], 4, (q0 + lane) * 4u, 0, 0, 0);
     else if (wave == 1)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_dl, (lds_t*)&s_delta[buf][0], 4, (q0 + lane) * 4u, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_dl, (lds_t*)&s_delta[e % 3][0], 4, (q0 + lane) * 4u, 0, 0, 0);
   };
   // a PARTIAL tile's column mask (P waves only), fetched one step ahead of its use
   auto load_bits = [&](int e, uint64_t& bits) {
@@ -343,7 +352,6 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   };
 
   const int srow = sigma(c);
-  if constexpr (Q8) so8.init(srow, hf);
   int raddr[DS];
 #pragma unroll
   for (int st = 0; st < DS; ++st) raddr[st] = TL::at(srow, 2 * st + hf);
@@ -355,94 +363,10 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   f32x16 acc[DB];  // dV^T (role 0) or dK^T (role 1)
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
-  float* xp = &s_p[pair][0][lane];
 
-  uint64_t bits = 0, bits_next = 0;
-  if (n > 0) {
-    load_tile(int(entry_tile(ent[0])), 0);
-    load_bits(0, bits);
-  }
-
-  for (int e = 0; e < n; ++e) {
-    const int buf = e & 1;
-    const uint32_t cur = ent[e];
-    wait_vmem();
-    __syncthreads();  // tile e landed; every wave is done with tile e-1 and its P
-    if (e + 1 < n) {
-      load_tile(int(entry_tile(ent[e + 1])), buf ^ 1);
-      load_bits(e + 1, bits_next);
-    }
-    const uint8_t* qt = s_q[buf];
-    const uint8_t* dot = s_do[buf];
-    // A operands: rows of Q (role 0) or dO (role 1); transposed dO (role 0) or Q (role 1)
-    const uint8_t* arow = role == 0 ? qt : dot;
-    const uint8_t* atr = role == 0 ? dot : qt;
-
-    // S (role 0) or dP (role 1) for the two 32-query halves; register r of
-    // x[qb] holds query 32 qb + 16 (r / 8) + 8 hf + r % 8 of this lane's key
-    f32x16 x[2] = {f32x16{}, f32x16{}};
-    if (Q8 && role == 0) {
-      so8.mma(s_q8[buf & (Q8 ? 1 : 0)], 0, x[0]);
-      so8.mma(s_q8[buf & (Q8 ? 1 : 0)], 1, x[1]);
-    } else {
-#pragma unroll
-      for (int st = 0; st < DS; ++st) {
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          const u32x4 ar = *reinterpret_cast<const u32x4*>(arow + raddr[st] + qb * 32 * TL::ROWB);
-          x[qb] = mfma32x32x16<E>(ar, bf[st], x[qb]);
-        }
-      }
-    }
-    u32x4 bop[2][2];  // packed P (role 0) or dS (role 1): B operand of k-step 2 qb + t
-    if (role == 0) {
-      const uint32_t mcls = entry_class(cur, member);
-      if (mcls != TILE_FULL) {  // wave-uniform.  Register r of x[qb] holds query 32 qb + 16 (r / 8) + 8 hf + r % 8
-        const uint64_t colbits = mcls == TILE_PARTIAL ? bits : 0u;  // EMPTY: nothing allowed
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          const uint32_t w = uint32_t(colbits >> (32 * qb)) >> (8 * hf);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) x[qb][r] = mask_bit(x[qb][r], w, 16 * (r >> 3) + (r & 7));
-        }
-      }
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int ql = 32 * qb + 16 * t + 8 * hf;
-          const f32x4 l0 = *reinterpret_cast<const f32x4*>(&s_lse[buf][ql]);
-          const f32x4 l1 = *reinterpret_cast<const f32x4*>(&s_lse[buf][ql + 4]);
-          float p[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            p[j] = fast_exp2(__builtin_fmaf(x[qb][8 * t + j], sl2, -(j < 4 ? l0[j] : l1[j - 4])));
-            xp[(16 * qb + 8 * t + j) * 64] = p[j];
-          }
-          bop[qb][t] = u32x4{pack2<E>(p[0], p[1]), pack2<E>(p[2], p[3]), pack2<E>(p[4], p[5]),
-                             pack2<E>(p[6], p[7])};
-        }
-    }
-    __syncthreads();  // P of this tile visible to the dS waves
-    if (role == 1) {
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int ql = 32 * qb + 16 * t + 8 * hf;
-          const f32x4 d0 = *reinterpret_cast<const f32x4*>(&s_delta[buf][ql]);
-          const f32x4 d1 = *reinterpret_cast<const f32x4*>(&s_delta[buf][ql + 4]);
-          float ds[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float p = xp[(16 * qb + 8 * t + j) * 64];
-            ds[j] = p * (x[qb][8 * t + j] - (j < 4 ? d0[j] : d1[j - 4]));
-          }
-          bop[qb][t] = u32x4{pack2<E>(ds[0], ds[1]), pack2<E>(ds[2], ds[3]), pack2<E>(ds[4], ds[5]),
-                             pack2<E>(ds[6], ds[7])};
-        }
-    }
-    // acc^T += A^T bop over the 64 queries (k-steps 2 qb + t)
+  // acc^T += A^T bop over the 64 queries of a tile (k-steps 2 qb + t), A^T
+  // read transposed from tile `at`
+  auto accumulate = [&](const uint8_t* at, const u32x4 (&bop)[2][2]) {
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
@@ -450,10 +374,122 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
           const int off = (2 * qb + t) * 16 * TL::ROWB;
-          const u32x2 lo = ds_read_tr16(atr + taddr[db][0] + off);
-          const u32x2 hi = ds_read_tr16(atr + taddr[db][1] + off);
+          const u32x2 lo = ds_read_tr16(at + taddr[db][0] + off);
+          const u32x2 hi = ds_read_tr16(at + taddr[db][1] + off);
           acc[db] = mfma32x32x16<E>(u32x4{lo[0], lo[1], hi[0], hi[1]}, bop[qb][t], acc[db]);
         }
+  };
+  // x[qb] += (rows of tile `ar`) B^T; register r of x[qb] holds query
+  // 32 qb + 16 (r / 8) + 8 hf + r % 8 of this lane's key
+  auto rows_times_b = [&](const uint8_t* ar, f32x16 (&x)[2]) {
+    x[0] = f32x16{};
+    x[1] = f32x16{};
+#pragma unroll
+    for (int st = 0; st < DS; ++st) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const u32x4 av = *reinterpret_cast<const u32x4*>(ar + raddr[st] + qb * 32 * TL::ROWB);
+        x[qb] = mfma32x32x16<E>(av, bf[st], x[qb]);
+      }
+    }
+  };
+
+  uint64_t bits = 0, bits_next = 0;
+  if (n > 0) {
+    load_tile(0);
+    load_bits(0, bits);
+  }
+  // S of tile e (P waves), or dP of tile e carried into step e + 1 (dS
+  // waves): one register set for both roles
+  f32x16 x[2] = {f32x16{}, f32x16{}};
+
+  for (int e = 0; e <= n; ++e) {
+    wait_vmem();
+    __syncthreads();  // tile e landed, P(e-1) written; P(e-2) and tile e-2 released
+    if (e + 1 < n) {
+      load_tile(e + 1);
+      load_bits(e + 1, bits_next);
+    }
+    const int pb = e & 1;
+    if (role == 0) {
+      if (e < n) {
+        if constexpr (Q8) {  // S = Q8 K8^T on the fp8 MFMA; A = Q8 rows, 32 bytes per lane and k-step
+          const uint8_t* t8 = s_q8[pb & (Q8 ? 1 : 0)];
+          x[0] = f32x16{};
+          x[1] = f32x16{};
+#pragma unroll
+          for (int st = 0; st < D / 64; ++st) {
+            const int a0 = TQ8::at(srow, 4 * st + 2 * hf), a1 = TQ8::at(srow, 4 * st + 2 * hf + 1);
+            const i32x8 bv = {int(bf[2 * st][0]), int(bf[2 * st][1]), int(bf[2 * st][2]), int(bf[2 * st][3]),
+                              int(bf[2 * st + 1][0]), int(bf[2 * st + 1][1]), int(bf[2 * st + 1][2]),
+                              int(bf[2 * st + 1][3])};
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+              const u32x4 lo = *reinterpret_cast<const u32x4*>(t8 + a0 + qb * 32 * TQ8::ROWB);
+              const u32x4 hi = *reinterpret_cast<const u32x4*>(t8 + a1 + qb * 32 * TQ8::ROWB);
+              const i32x8 av = {int(lo[0]), int(lo[1]), int(lo[2]), int(lo[3]),
+                                int(hi[0]), int(hi[1]), int(hi[2]), int(hi[3])};
+              x[qb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, x[qb], 0, 0, 0, 127, 0, 127);
+            }
+          }
+        } else {
+          rows_times_b(s_q[e % 3], x);
+        }
+        const uint32_t mcls = entry_class(ent[e], member);
+        if (mcls != TILE_FULL) {  // wave-uniform
+          const uint64_t colbits = mcls == TILE_PARTIAL ? bits : 0u;  // EMPTY: nothing allowed
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) {
+            const uint32_t w = uint32_t(colbits >> (32 * qb)) >> (8 * hf);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) x[qb][r] = mask_bit(x[qb][r], w, 16 * (r >> 3) + (r & 7));
+          }
+        }
+        u32x4 bop[2][2];  // packed P: B operand of k-step 2 qb + t
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int ql = 32 * qb + 16 * t + 8 * hf;
+            const f32x4 l0 = *reinterpret_cast<const f32x4*>(&s_lse[pb][ql]);
+            const f32x4 l1 = *reinterpret_cast<const f32x4*>(&s_lse[pb][ql + 4]);
+            float p[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+              p[j] = fast_exp2(__builtin_fmaf(x[qb][8 * t + j], sl2, -(j < 4 ? l0[j] : l1[j - 4])));
+            bop[qb][t] = u32x4{pack2<E>(p[0], p[1]), pack2<E>(p[2], p[3]), pack2<E>(p[4], p[5]),
+                               pack2<E>(p[6], p[7])};
+            s_p[pb][pair][2 * qb + t][lane] = bop[qb][t];
+          }
+        accumulate(s_do[pb], bop);  // dV^T += dO^T P
+      }
+    } else {
+      if (e >= 1) {  // dS and dK of tile e - 1
+        const int pslot = (e + 2) % 3;
+        u32x4 dsb[2][2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int ql = 32 * qb + 16 * t + 8 * hf;
+            const f32x4 d0 = *reinterpret_cast<const f32x4*>(&s_delta[pslot][ql]);
+            const f32x4 d1 = *reinterpret_cast<const f32x4*>(&s_delta[pslot][ql + 4]);
+            const u32x4 pw = s_p[pb ^ 1][pair][2 * qb + t][lane];
+            float ds[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const uint32_t w = pw[j >> 1];
+              const float p = to_f32<E>(uint16_t((j & 1) ? (w >> 16) : (w & 0xFFFFu)));
+              ds[j] = p * (x[qb][8 * t + j] - (j < 4 ? d0[j] : d1[j - 4]));
+            }
+            dsb[qb][t] = u32x4{pack2<E>(ds[0], ds[1]), pack2<E>(ds[2], ds[3]), pack2<E>(ds[4], ds[5]),
+                               pack2<E>(ds[6], ds[7])};
+          }
+        accumulate(s_q[pslot], dsb);  // dK^T += Q^T dS
+        __builtin_amdgcn_sched_barrier(0x406);  // keep dS of tile e - 1 apart from dP of tile e (registers)
+      }
+      if (e < n) rows_times_b(s_do[pb], x);  // dP of tile e
+    }
     bits = bits_next;
   }
 
