@@ -28,6 +28,13 @@
 // swizzled layout of kd_tile.h (double buffered; dK/dV's Q triple buffered).
 #include "kd_tile.h"
 
+#ifndef DKDV_PF
+#define DKDV_PF 3
+#endif
+#ifndef DQ_PF
+#define DQ_PF 3
+#endif
+
 namespace kd {
 
 // ---------------------------------------------------------------- Delta ----
@@ -197,16 +204,38 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
     const uint8_t* kt = s_k[buf];
     const uint8_t* vt = s_v[buf];
 
-    f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
-    so.mma(Q8 ? s_k8[buf & (Q8 ? 1 : 0)] : kt, 0, s[0]);
-    so.mma(Q8 ? s_k8[buf & (Q8 ? 1 : 0)] : kt, 1, s[1]);
+    // S^T = K Q^T and dP^T = V dO^T; A operands (K / K8 and V rows) are read
+    // DQ_PF steps ahead of their MFMAs, steps i: kb = i & 1, st = i >> 1; the
+    // sched_barriers keep LDS reads and MFMAs in that order
+    f32x16 s[2], dp[2];
+    {
+      const uint8_t* st_tile = Q8 ? s_k8[buf & (Q8 ? 1 : 0)] : kt;
+      constexpr int NS = 2 * SO::NK, PF = DQ_PF < NS ? DQ_PF : NS;
+      typename SO::A av[PF];
 #pragma unroll
-    for (int st = 0; st < DS; ++st) {
+      for (int i = 0; i < PF; ++i) av[i] = so.read_a(st_tile, i & 1, i >> 1);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const u32x4 av = *reinterpret_cast<const u32x4*>(vt + raddr[st] + kb * 32 * TL::ROWB);
-        dp[kb] = mfma32x32x16<E>(av, dof[st], dp[kb]);
+      for (int i = 0; i < NS; ++i) {
+        __builtin_amdgcn_sched_barrier(0x406);
+        s[i & 1] = so.mma_a(av[i % PF], i >> 1, (i >> 1) == 0 ? f32x16{} : s[i & 1]);
+        if (i + PF < NS) av[i % PF] = so.read_a(st_tile, (i + PF) & 1, (i + PF) >> 1);
       }
+    }
+    {
+      constexpr int NS = 2 * DS, PF = DQ_PF;
+      auto read = [&](int i) {
+        return *reinterpret_cast<const u32x4*>(vt + raddr[i >> 1] + (i & 1) * 32 * TL::ROWB);
+      };
+      u32x4 av[PF];
+#pragma unroll
+      for (int i = 0; i < PF; ++i) av[i] = read(i);
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        __builtin_amdgcn_sched_barrier(0x406);
+        dp[i & 1] = mfma32x32x16<E>(av[i % PF], dof[i >> 1], (i >> 1) == 0 ? f32x16{} : dp[i & 1]);
+        if (i + PF < NS) av[i % PF] = read(i + PF);
+      }
+      __builtin_amdgcn_sched_barrier(0x406);
     }
     const uint32_t mcls = entry_class(cur, member);
     if (mcls != TILE_FULL) {  // wave-uniform.  Register r of s[kb] holds key 32 kb + 16 (r / 8) + 8 hf + r % 8
@@ -232,16 +261,26 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
         dsb[kb][t] = u32x4{pack2<E>(ds[8 * t + 0], ds[8 * t + 1]), pack2<E>(ds[8 * t + 2], ds[8 * t + 3]),
                            pack2<E>(ds[8 * t + 4], ds[8 * t + 5]), pack2<E>(ds[8 * t + 6], ds[8 * t + 7])};
     }
-    // dQ^T += K^T dS^T
-#pragma unroll
-    for (int t4 = 0; t4 < 4; ++t4) {
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
+    // dQ^T += K^T dS^T, K^T read transposed DQ_PF steps ahead (steps: t4 = i / DB, db = i % DB)
+    {
+      constexpr int NS = 4 * DB, PF = DQ_PF;
+      auto read = [&](int i) {
+        const int t4 = i / DB, db = i % DB;
         const u32x2 lo = ds_read_tr16(kt + taddr[db][0] + t4 * 16 * TL::ROWB);
         const u32x2 hi = ds_read_tr16(kt + taddr[db][1] + t4 * 16 * TL::ROWB);
-        const u32x4 ak = {lo[0], lo[1], hi[0], hi[1]};
-        acc[db] = mfma32x32x16<E>(ak, dsb[t4 >> 1][t4 & 1], acc[db]);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      };
+      u32x4 av[PF];
+#pragma unroll
+      for (int i = 0; i < PF; ++i) av[i] = read(i);
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int t4 = i / DB, db = i % DB;
+        __builtin_amdgcn_sched_barrier(0x406);
+        acc[db] = mfma32x32x16<E>(av[i % PF], dsb[t4 >> 1][t4 & 1], acc[db]);
+        if (i + PF < NS) av[i % PF] = read(i + PF);
       }
+      __builtin_amdgcn_sched_barrier(0x406);
     }
     bits = bits_next;
   }
@@ -364,34 +403,51 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
 
-  // acc^T += A^T bop over the 64 queries of a tile (k-steps 2 qb + t), A^T
-  // read transposed from tile `at`
+  // Both products below read their A operands from LDS DKDV_PF steps ahead of
+  // the MFMA that uses them; the sched_barriers keep LDS reads and MFMAs in
+  // that order (VALU and SALU work may move across), which also bounds the
+  // registers held by operands in flight.
+  constexpr int PF = DKDV_PF;
+  // acc^T += A^T bop over the 64 queries of a tile (k-steps k4 = 2 qb + t),
+  // A^T read transposed from tile `at`; steps i = 4 k4 ... ordered (k4, db)
   auto accumulate = [&](const uint8_t* at, const u32x4 (&bop)[2][2]) {
+    constexpr int NS = 4 * DB;
+    auto read = [&](int i) {
+      const int k4 = i / DB, db = i % DB, off = k4 * 16 * TL::ROWB;
+      const u32x2 lo = ds_read_tr16(at + taddr[db][0] + off);
+      const u32x2 hi = ds_read_tr16(at + taddr[db][1] + off);
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
+    u32x4 av[PF];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+    for (int i = 0; i < PF; ++i) av[i] = read(i);
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const int off = (2 * qb + t) * 16 * TL::ROWB;
-          const u32x2 lo = ds_read_tr16(at + taddr[db][0] + off);
-          const u32x2 hi = ds_read_tr16(at + taddr[db][1] + off);
-          acc[db] = mfma32x32x16<E>(u32x4{lo[0], lo[1], hi[0], hi[1]}, bop[qb][t], acc[db]);
-        }
+    for (int i = 0; i < NS; ++i) {
+      const int k4 = i / DB, db = i % DB;
+      __builtin_amdgcn_sched_barrier(0x406);
+      acc[db] = mfma32x32x16<E>(av[i % PF], bop[k4 >> 1][k4 & 1], acc[db]);
+      if (i + PF < NS) av[i % PF] = read(i + PF);
+    }
+    __builtin_amdgcn_sched_barrier(0x406);
   };
   // x[qb] += (rows of tile `ar`) B^T; register r of x[qb] holds query
-  // 32 qb + 16 (r / 8) + 8 hf + r % 8 of this lane's key
+  // 32 qb + 16 (r / 8) + 8 hf + r % 8 of this lane's key; steps i = (st, qb)
   auto rows_times_b = [&](const uint8_t* ar, f32x16 (&x)[2]) {
-    x[0] = f32x16{};
-    x[1] = f32x16{};
+    constexpr int NS = 2 * DS;
+    auto read = [&](int i) {
+      return *reinterpret_cast<const u32x4*>(ar + raddr[i >> 1] + (i & 1) * 32 * TL::ROWB);
+    };
+    u32x4 av[PF];
 #pragma unroll
-    for (int st = 0; st < DS; ++st) {
+    for (int i = 0; i < PF; ++i) av[i] = read(i);
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        const u32x4 av = *reinterpret_cast<const u32x4*>(ar + raddr[st] + qb * 32 * TL::ROWB);
-        x[qb] = mfma32x32x16<E>(av, bf[st], x[qb]);
-      }
+    for (int i = 0; i < NS; ++i) {
+      const int st = i >> 1, qb = i & 1;
+      __builtin_amdgcn_sched_barrier(0x406);
+      x[qb] = mfma32x32x16<E>(av[i % PF], bf[st], st == 0 ? f32x16{} : x[qb]);
+      if (i + PF < NS) av[i % PF] = read(i + PF);
     }
+    __builtin_amdgcn_sched_barrier(0x406);
   };
 
   uint64_t bits = 0, bits_next = 0;
@@ -486,7 +542,6 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
                                pack2<E>(ds[6], ds[7])};
           }
         accumulate(s_q[pslot], dsb);  // dK^T += Q^T dS
-        __builtin_amdgcn_sched_barrier(0x406);  // keep dS of tile e - 1 apart from dP of tile e (registers)
       }
       if (e < n) rows_times_b(s_do[pb], x);  // dP of tile e
     }
