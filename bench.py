@@ -52,8 +52,11 @@ USEFUL_FWD, USEFUL_BWD = 4, 10
 
 # HBM bytes per launch of the attention kernels on config 4 (Hadamard on), from
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs scaled by a 1 GiB copy's counts
-# (profiles/attn_config4_hbm_traffic.md); re-measured whenever the kernels change.
-CONFIG4_TRAFFIC_BYTES = {"fwd": 966.8e6, "dq": 952.7e6, "dkdv": 1231.7e6}
+# (profiles/attn_config4_{bf16,fp8_e4m3}_hbm_traffic.md); re-measured whenever the kernels change.
+CONFIG4_TRAFFIC_BYTES = {
+    "bf16": {"fwd": 958.2e6, "dq": 972.7e6, "dkdv": 1183.2e6},
+    "fp8_e4m3": {"fwd": 701.1e6, "dq": 1035.6e6, "dkdv": 1407.1e6},
+}
 
 
 def parse():
@@ -319,7 +322,7 @@ def main():
     dom = max(("fwd", "dq", "dkdv"), key=lambda n: per_kernel[n])
     dom_flops = KERNEL_FLOPS_PER_ENTRY[dom] * D * H * nnz
     achieved = dom_flops / (per_kernel[dom] * 1e-3) / 1e12
-    traffic = CONFIG4_TRAFFIC_BYTES.get(dom) if (args.config == 4 and hadamard and not fp8) else None
+    traffic = CONFIG4_TRAFFIC_BYTES[args.qk_dtype].get(dom) if (args.config == 4 and hadamard) else None
     peak = PEAK_BF16_TFLOPS
     if fp8:
         # the Q K^T share (2d of the kernel's flops per entry) runs at the fp8
