@@ -28,7 +28,8 @@ KD_DEV inline bool entry_full(uint32_t e, int group) {
 }
 
 struct PlanLayout {
-  size_t codes, rep, cls, nnz, fwd_list, fwd_count, dq_list, dq_count, dkdv_list, dkdv_count, qbits, kbits, total;
+  size_t codes, rep, runs, run_sid, run_count, cls, nnz, fwd_list, fwd_count, dq_list, dq_count, dkdv_list, dkdv_count,
+      qbits, kbits, total;
   int nT, fwd_group, dq_group, dkdv_group, n_fwd_blocks, n_dq_blocks, n_dkdv_blocks;
 };
 

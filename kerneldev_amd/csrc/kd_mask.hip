@@ -19,13 +19,10 @@ namespace kd {
 
 // ---- span-group representative -------------------------------------------
 // rep[b][j] = min { t : S_t & sid_t > 0 & sid_t == sid_j } for eligible j
-// (S_j & sid_j > 0).  Brute force over the lower triangle of 256x256 chunk
-// pairs with an atomic min; exact for any int64 span ids.
-
-__global__ void k_fill_u32(uint32_t* p, int64_t n, uint32_t v) {
-  int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = v;
-}
+// (S_j & sid_j > 0).  That minimum is always the start of a run of equal
+// eligible ids, so one pass lists each row's run starts (and their ids) in
+// ascending order, and each eligible token takes the first listed run with
+// its id: O(T * runs) instead of O(T^2), exact for any int64 span ids.
 
 KD_DEV int64_t load_sid(const MetaArgs& m, int b, int t) {
   if (m.span_id == nullptr) return 0;
@@ -41,26 +38,47 @@ KD_DEV bool eligible(const MetaArgs& m, int b, int t, int64_t* sid) {
   return m.span_id != nullptr && load_flag(m.in_span, m.in_span_strides, b, t) && *sid > 0;
 }
 
-__global__ __launch_bounds__(256) void k_span_rep(MetaArgs m, uint32_t* rep) {
-  const int jc = blockIdx.x, tc = blockIdx.y, b = blockIdx.z;
-  if (tc > jc) return;
-  __shared__ int64_t s_sid[256];
-  __shared__ int s_ok[256];
-  const int t = tc * 256 + threadIdx.x;
-  int64_t sid_t = 0;
-  s_ok[threadIdx.x] = (t < m.T) && eligible(m, b, t, &sid_t);
-  s_sid[threadIdx.x] = sid_t;
-  __syncthreads();
-  const int j = jc * 256 + threadIdx.x;
-  if (j >= m.T) return;
-  int64_t sid_j;
-  if (!eligible(m, b, j, &sid_j)) return;
-  for (int x = 0; x < 256; ++x) {
-    if (s_ok[x] && s_sid[x] == sid_j) {
-      atomicMin(&rep[int64_t(b) * m.T + j], uint32_t(tc * 256 + x));
+// One workgroup per batch row: ballot-compact the run starts chunk by chunk.
+__global__ __launch_bounds__(256) void k_runs(MetaArgs m, uint32_t* runs, int64_t* run_sid, int32_t* run_count) {
+  const int b = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  __shared__ int s_cnt[4];
+  uint32_t* out = runs + int64_t(b) * m.T;
+  int64_t* out_sid = run_sid + int64_t(b) * m.T;
+  int total = 0;
+  for (int t0 = 0; t0 < m.T; t0 += 256) {
+    const int t = t0 + tid;
+    int64_t sid = 0, prev = 0;
+    bool start = false;
+    if (t < m.T && eligible(m, b, t, &sid)) start = !(t > 0 && eligible(m, b, t - 1, &prev) && prev == sid);
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(start);
+    if (lane == 0) s_cnt[wave] = __builtin_popcountll(bal);
+    __syncthreads();
+    int pos = total + __builtin_popcountll(bal & ((uint64_t(1) << lane) - 1));
+    for (int w = 0; w < wave; ++w) pos += s_cnt[w];
+    if (start) {
+      out[pos] = uint32_t(t);
+      out_sid[pos] = sid;
+    }
+    total += s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
+    __syncthreads();
+  }
+  if (tid == 0) run_count[b] = total;
+}
+
+__global__ void k_rep(MetaArgs m, const uint32_t* runs, const int64_t* run_sid, const int32_t* run_count,
+                      uint32_t* rep) {
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= int64_t(m.B) * m.T) return;
+  const int b = int(idx / m.T), j = int(idx % m.T);
+  int64_t sid;
+  if (!eligible(m, b, j, &sid)) return;
+  const int n = run_count[b];
+  const int64_t* rs = run_sid + int64_t(b) * m.T;
+  for (int i = 0; i < n; ++i)
+    if (rs[i] == sid) {  // always found: j's own run is listed
+      rep[idx] = runs[int64_t(b) * m.T + i];
       return;
     }
-  }
 }
 
 // ---- token codes -------------------------------------------------------
@@ -94,6 +112,25 @@ __global__ void k_codes(MetaArgs m, const uint32_t* rep, uint32_t* codes) {
 }
 
 // ---- 64x64 tile classifier ---------------------------------------------
+// The rule in table form for a fixed query code: bit F of `lo` says whether a
+// key with flag nibble F is seen (A_i & F_j != 0); `hi` adds C_j for a context
+// query, used where i >= j (C & C & i >= j); both are stored twice so that the
+// key code's low 5 bits index them.  `rsh` = R_i << 8, or a value no code
+// matches when R_i = 0, so ((kc ^ rsh) < 256) is exactly "same span".
+struct QTab {
+  uint32_t lo, hi, rsh;
+};
+KD_DEV QTab qtab(uint32_t qc) {
+  const uint32_t A = (qc >> 4) & 15u;
+  const uint32_t t = ((A & FLAG_P) ? 0xAAAAu : 0u) | ((A & FLAG_S) ? 0xCCCCu : 0u) |
+                     ((A & FLAG_M) ? 0xF0F0u : 0u) | ((A & FLAG_C) ? 0xFF00u : 0u);
+  const uint32_t th = t | ((qc & FLAG_C) ? 0xFF00u : 0u);
+  const uint32_t R = qc >> 8;
+  return QTab{t * 0x10001u, th * 0x10001u, R ? (R << 8) : 0xFFFFFF00u};
+}
+KD_DEV uint32_t qtab_allow(const QTab& q, uint32_t kc, bool i_ge_j) {
+  return ((((i_ge_j ? q.hi : q.lo) >> (kc & 31u)) & 1u) | ((kc ^ q.rsh) < 256u ? 1u : 0u));
+}
 // One wave per tile: lane = query row, loop over the tile's 64 keys, building
 // the row's 64-bit mask; PARTIAL tiles also store the row masks and, through
 // 64 ballots (column j of the tile = ballot of bit j), the column masks.
@@ -112,11 +149,21 @@ __global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, i
   if (kt >= nT) return;
   const int i = qt * 64 + lane;
   const uint32_t qc = (i < T) ? codes[int64_t(b) * T + i] : 0u;
+  const QTab q = qtab(qc);
   uint32_t lo = 0, hi = 0;
+  if (kt != qt) {  // off the diagonal every key is on one side of every query
+    const bool below = kt < qt;
 #pragma unroll 8
-  for (int x = 0; x < 32; ++x) {
-    lo |= uint32_t(allow(qc, s_k[wave * 64 + x], i, kt * 64 + x)) << x;
-    hi |= uint32_t(allow(qc, s_k[wave * 64 + 32 + x], i, kt * 64 + 32 + x)) << x;
+    for (int x = 0; x < 32; ++x) {
+      lo |= qtab_allow(q, s_k[wave * 64 + x], below) << x;
+      hi |= qtab_allow(q, s_k[wave * 64 + 32 + x], below) << x;
+    }
+  } else {
+#pragma unroll 8
+    for (int x = 0; x < 32; ++x) {
+      lo |= qtab_allow(q, s_k[wave * 64 + x], lane >= x) << x;
+      hi |= qtab_allow(q, s_k[wave * 64 + 32 + x], lane >= 32 + x) << x;
+    }
   }
   int cnt = __builtin_popcount(lo) + __builtin_popcount(hi);
   for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off);
@@ -214,6 +261,9 @@ PlanLayout plan_layout(int B, int T, int D) {
   const size_t BT = size_t(B) * T, BTT = size_t(B) * nT * nT;
   L.codes = take(BT * 4);
   L.rep = take(BT * 4);
+  L.runs = take(BT * 4);
+  L.run_sid = take(BT * 8);
+  L.run_count = take(size_t(B) * 4);
   L.cls = take(BTT);
   L.nnz = take(BTT * 4);
   const int nf = (nT + L.fwd_group - 1) / L.fwd_group;
@@ -241,10 +291,12 @@ int launch_plan(const MetaArgs& m, uint8_t* plan, hipStream_t st) {
   uint8_t* cls = plan + L.cls;
   int32_t* nnz = reinterpret_cast<int32_t*>(plan + L.nnz);
   const int64_t BT = int64_t(m.B) * m.T;
-  const int nchunk = (m.T + 255) / 256;
   if (m.mode == KD_MODE_FORMULA && m.span_id != nullptr && m.in_span != nullptr) {
-    hipLaunchKernelGGL(k_fill_u32, dim3(unsigned((BT + 255) / 256)), dim3(256), 0, st, rep, BT, 0xFFFFFFFFu);
-    hipLaunchKernelGGL(k_span_rep, dim3(nchunk, nchunk, m.B), dim3(256), 0, st, m, rep);
+    uint32_t* runs = reinterpret_cast<uint32_t*>(plan + L.runs);
+    int64_t* run_sid = reinterpret_cast<int64_t*>(plan + L.run_sid);
+    int32_t* run_count = reinterpret_cast<int32_t*>(plan + L.run_count);
+    hipLaunchKernelGGL(k_runs, dim3(unsigned(m.B)), dim3(256), 0, st, m, runs, run_sid, run_count);
+    hipLaunchKernelGGL(k_rep, dim3(unsigned((BT + 255) / 256)), dim3(256), 0, st, m, runs, run_sid, run_count, rep);
   }
   hipLaunchKernelGGL(k_codes, dim3(unsigned((BT + 255) / 256)), dim3(256), 0, st, m, rep, codes);
   hipLaunchKernelGGL(k_tilemap, dim3((L.nT + 3) / 4, L.nT, m.B), dim3(256), 0, st, codes, m.T, L.nT, cls, nnz,
