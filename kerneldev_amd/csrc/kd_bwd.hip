@@ -314,12 +314,17 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   using TL = Tile<D, NW>;
   using TQ8 = Tile<Q8 ? D / 2 : D, NW>;  // fp8 Q tiles (D bytes a row); only used at D = 128
   constexpr int DS = D / 16, DB = D / 32, NL = TL::LOADS_PER_WAVE, NL8 = TQ8::LOADS_PER_WAVE;
-  __shared__ __attribute__((aligned(1024))) uint8_t s_q[3][TL::BYTES];     // tile e % 3
-  __shared__ __attribute__((aligned(1024))) uint8_t s_q8[Q8 ? 2 : 1][Q8 ? TQ8::BYTES : 16];
-  __shared__ __attribute__((aligned(1024))) uint8_t s_do[2][TL::BYTES];    // tile e % 2
+  // Tiles are loaded PD steps ahead (2; the fp8 variant's extra Q8 tiles
+  // leave LDS for 1).  Slot counts follow from who reads what when: in step
+  // e the P waves read Q(e), dO(e), LSE(e); the dS waves dO(e), Q(e-1),
+  // Delta(e-1); a load issued in step e must not overwrite any of those.
+  constexpr int PD = Q8 ? 1 : 2, NQ = PD + 2, NDO = PD + 1, NLS = PD + 1, NDL = PD + 2;
+  __shared__ __attribute__((aligned(1024))) uint8_t s_q[NQ][TL::BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_q8[Q8 ? NDO : 1][Q8 ? TQ8::BYTES : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_do[NDO][TL::BYTES];
   __shared__ __attribute__((aligned(1024))) u32x4 s_p[2][4][4][64];       // [e % 2][pair][k-step][lane]
-  __shared__ __attribute__((aligned(256))) float s_lse[2][64];
-  __shared__ __attribute__((aligned(256))) float s_delta[3][64];
+  __shared__ __attribute__((aligned(256))) float s_lse[NLS][64];
+  __shared__ __attribute__((aligned(256))) float s_delta[NDL][64];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
   const int pair = wave & 3, role = wave >> 2;
@@ -374,15 +379,24 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   TL::load_offsets(wave, lane, dorb, dooff);
   TQ8::load_offsets(wave, lane, uint32_t(D), q8off);
   const auto rs_q8 = make_rsrc(Q8 ? a.q8 + int64_t(bh) * T * D : nullptr, Q8 ? uint32_t(T) * D : 0u);
+  // tile e's copies: NL + NL (+ NL8) buffer loads per wave, + 1 on waves 0 and 1
   auto load_tile = [&](int e) {
     const uint32_t q0 = entry_tile(ent[e]) * 64u;
-    TL::load(rs_q, q0 * qrb, qoff, s_q[e % 3], wave);
-    TL::load(rs_do, q0 * dorb, dooff, s_do[e & 1], wave);
-    if constexpr (Q8) TQ8::load(rs_q8, q0 * uint32_t(D), q8off, s_q8[e & 1], wave);
+    TL::load(rs_q, q0 * qrb, qoff, s_q[e % NQ], wave);
+    TL::load(rs_do, q0 * dorb, dooff, s_do[e % NDO], wave);
+    if constexpr (Q8) TQ8::load(rs_q8, q0 * uint32_t(D), q8off, s_q8[e % NDO], wave);
     if (wave == 0)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, (lds_t*)&s_lse[e & 1][0], 4, (q0 + lane) * 4u, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, (lds_t*)&s_lse[e % NLS][0], 4, (q0 + lane) * 4u, 0, 0, 0);
     else if (wave == 1)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_dl, (lds_t*)&s_delta[e % 3][0], 4, (q0 + lane) * 4u, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_dl, (lds_t*)&s_delta[e % NDL][0], 4, (q0 + lane) * 4u, 0, 0, 0);
+  };
+  // Wait until tile e's loads (and older ones) have landed while tile e+1's,
+  // issued last, may still be in flight: vector memory loads retire in order.
+  constexpr int NTL = 2 * NL + (Q8 ? NL8 : 0);
+  auto wait_tile = [&](bool next_in_flight) {
+    if (!next_in_flight) wait_vmem();
+    else if (wave < 2) wait_vmem_n<NTL + 1>();
+    else wait_vmem_n<NTL>();
   };
   // a PARTIAL tile's column mask (P waves only), fetched one step ahead of its use
   auto load_bits = [&](int e, uint64_t& bits) {
@@ -452,25 +466,25 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
 
   uint64_t bits = 0, bits_next = 0;
   if (n > 0) {
-    load_tile(0);
     load_bits(0, bits);
+    load_tile(0);
   }
+  for (int e = 1; e < PD && e < n; ++e) load_tile(e);
   // S of tile e (P waves), or dP of tile e carried into step e + 1 (dS
   // waves): one register set for both roles
   f32x16 x[2] = {f32x16{}, f32x16{}};
 
   for (int e = 0; e <= n; ++e) {
-    wait_vmem();
-    __syncthreads();  // tile e landed, P(e-1) written; P(e-2) and tile e-2 released
-    if (e + 1 < n) {
-      load_tile(e + 1);
-      load_bits(e + 1, bits_next);
-    }
+    // tiles up to e landed (tile e + PD - 1 may be in flight when PD = 2)
+    wait_tile(PD == 2 && e + 1 < n);
+    __syncthreads();  // tile e landed, P(e-1) written; P(e-2) and the slots of tile e+PD released
+    if (e + 1 < n) load_bits(e + 1, bits_next);  // issued before the tile loads (see wait_tile)
+    if (e + PD < n) load_tile(e + PD);
     const int pb = e & 1;
     if (role == 0) {
       if (e < n) {
         if constexpr (Q8) {  // S = Q8 K8^T on the fp8 MFMA; A = Q8 rows, 32 bytes per lane and k-step
-          const uint8_t* t8 = s_q8[pb & (Q8 ? 1 : 0)];
+          const uint8_t* t8 = s_q8[Q8 ? e % NDO : 0];
           x[0] = f32x16{};
           x[1] = f32x16{};
 #pragma unroll
@@ -489,7 +503,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
             }
           }
         } else {
-          rows_times_b(s_q[e % 3], x);
+          rows_times_b(s_q[e % NQ], x);
         }
         const uint32_t mcls = entry_class(ent[e], member);
         if (mcls != TILE_FULL) {  // wave-uniform
@@ -507,8 +521,8 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
             const int ql = 32 * qb + 16 * t + 8 * hf;
-            const f32x4 l0 = *reinterpret_cast<const f32x4*>(&s_lse[pb][ql]);
-            const f32x4 l1 = *reinterpret_cast<const f32x4*>(&s_lse[pb][ql + 4]);
+            const f32x4 l0 = *reinterpret_cast<const f32x4*>(&s_lse[e % NLS][ql]);
+            const f32x4 l1 = *reinterpret_cast<const f32x4*>(&s_lse[e % NLS][ql + 4]);
             float p[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j)
@@ -517,19 +531,19 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
                                pack2<E>(p[6], p[7])};
             s_p[pb][pair][2 * qb + t][lane] = bop[qb][t];
           }
-        accumulate(s_do[pb], bop);  // dV^T += dO^T P
+        accumulate(s_do[e % NDO], bop);  // dV^T += dO^T P
       }
     } else {
       if (e >= 1) {  // dS and dK of tile e - 1
-        const int pslot = (e + 2) % 3;
+        const int qprev = (e - 1) % NQ, dprev = (e - 1) % NDL;
         u32x4 dsb[2][2];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
             const int ql = 32 * qb + 16 * t + 8 * hf;
-            const f32x4 d0 = *reinterpret_cast<const f32x4*>(&s_delta[pslot][ql]);
-            const f32x4 d1 = *reinterpret_cast<const f32x4*>(&s_delta[pslot][ql + 4]);
+            const f32x4 d0 = *reinterpret_cast<const f32x4*>(&s_delta[dprev][ql]);
+            const f32x4 d1 = *reinterpret_cast<const f32x4*>(&s_delta[dprev][ql + 4]);
             const u32x4 pw = s_p[pb ^ 1][pair][2 * qb + t][lane];
             float ds[8];
 #pragma unroll
@@ -541,9 +555,9 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
             dsb[qb][t] = u32x4{pack2<E>(ds[0], ds[1]), pack2<E>(ds[2], ds[3]), pack2<E>(ds[4], ds[5]),
                                pack2<E>(ds[6], ds[7])};
           }
-        accumulate(s_q[pslot], dsb);  // dK^T += Q^T dS
+        accumulate(s_q[qprev], dsb);  // dK^T += Q^T dS
       }
-      if (e < n) rows_times_b(s_do[pb], x);  // dP of tile e
+      if (e < n) rows_times_b(s_do[e % NDO], x);  // dP of tile e
     }
     bits = bits_next;
   }

@@ -89,6 +89,9 @@ KD_DEV u32x2 ds_read_tr16(const uint8_t* p) {
 }
 
 KD_DEV void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// wait until at most N vector memory loads of this wave are outstanding
+template <int N>
+KD_DEV void wait_vmem_n() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
