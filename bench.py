@@ -205,8 +205,7 @@ class Step:
             out.append(("quant", quant))
         out += [
             ("fwd", lambda: ck(L.kd_attn_fwd(a, self.pptr, self.sptr), "fwd")),
-            ("delta", lambda: ck(L.kd_attn_bwd_delta(a, self.sptr), "delta")),
-            ("dq", lambda: ck(L.kd_attn_bwd_dq(a, self.pptr, self.sptr), "dq")),
+            ("dq", lambda: ck(L.kd_attn_bwd_dq_delta(a, self.pptr, self.sptr), "dq")),  # with Delta
             ("dkdv", lambda: ck(L.kd_attn_bwd_dkdv(a, self.pptr, self.sptr), "dkdv")),
         ]
         if self.hadamard:

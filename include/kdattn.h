@@ -158,11 +158,17 @@ int kd_attn_bwd_delta(const kd_attn_args *a, void *stream);
  * _flash_attn_bwd (original_kernel.py:1173-1336). */
 int kd_attn_bwd_dq(const kd_attn_args *a, const void *plan, void *stream);
 
+/* dQ that computes Delta and the LSE copy itself (from a->o, a->o_lo, a->lse)
+ * and stores both halves of a->delta for kd_attn_bwd_dkdv: the work of
+ * _flash_attn_bwd_precompute (original_kernel.py:649-710) and of the dQ
+ * workers (:1173-1336) in one pass. */
+int kd_attn_bwd_dq_delta(const kd_attn_args *a, const void *plan, void *stream);
+
 /* dK and dV.  Replaces the dK/dV workers of _flash_attn_bwd
  * (original_kernel.py:1339-1525). */
 int kd_attn_bwd_dkdv(const kd_attn_args *a, const void *plan, void *stream);
 
-/* Whole backward: Delta, then dQ and dK/dV.  Replaces
+/* Whole backward: dQ with Delta (kd_attn_bwd_dq_delta), then dK/dV.  Replaces
  * attention_backward_adapter (original_kernel.py:1806-1898). */
 int kd_attn_bwd(const kd_attn_args *a, const void *plan, void *stream);
 

@@ -93,6 +93,7 @@ SIGNATURES = {
     "kd_attn_fwd": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
     "kd_attn_bwd_delta": (c_int, [POINTER(AttnArgs), c_void_p]),
     "kd_attn_bwd_dq": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
+    "kd_attn_bwd_dq_delta": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
     "kd_attn_bwd_dkdv": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
     "kd_attn_bwd": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
     "kd_mask_dense": (c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p,

@@ -109,7 +109,8 @@ KD_DEV void tr_addrs(int lane, int (&addr)[D / 32][2]) {
 template <class E, int D, bool Q8>
 __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __restrict__ qbits,
                                                const uint32_t* __restrict__ list,
-                                               const int32_t* __restrict__ count, int nT, int nQB) {
+                                               const int32_t* __restrict__ count, int nT, int nQB,
+                                               bool fuse_delta) {
   using TL = Tile<D>;
   using SO = ScoreOp<E, D, Q8>;  // S^T = K Q^T (16-bit, or fp8 from the K8 tile)
   using TK8 = typename ScoreOp<E, D, true>::TL;
@@ -146,8 +147,40 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
 #pragma unroll
   for (int st = 0; st < DS; ++st) dof[st] = buf_load16(rs_do, uint32_t(qrow) * dorb + (16 * st + 8 * hf) * 2);
   const float INF = __builtin_inff();
-  const float lse = qvalid ? a.delta[BHT + int64_t(bh) * T + qrow] : INF;
-  const float delta = qvalid ? a.delta[int64_t(bh) * T + qrow] : 0.f;
+  float lse, delta;
+  if (fuse_delta) {  // uniform: compute this row's Delta and LSE copy here, for the dK/dV kernel too
+    // Delta = sum_d dO (O + O_lo) over this lane's 64 elements, then the other half-wave's
+    const uint16_t* og = static_cast<const uint16_t*>(a.o) + b * a.o_strides[0] + h * a.o_strides[1];
+    const uint32_t orb = uint32_t(a.o_strides[2]) * 2u;
+    const auto rs_o = make_rsrc(og, uint32_t(T) * orb);
+    // o_lo is contiguous [B, H, T, D]; without it the empty resource reads zeros
+    const uint16_t* lg = a.o_lo == nullptr ? nullptr : static_cast<const uint16_t*>(a.o_lo) + int64_t(bh) * T * D;
+    const auto rs_lo = make_rsrc(lg, lg == nullptr ? 0u : uint32_t(T) * D * 2u);
+    float sum = 0.f;
+#pragma unroll
+    for (int st = 0; st < DS; ++st) {
+      const uint32_t col = (16 * st + 8 * hf) * 2;
+      const u32x4 ov = buf_load16(rs_o, uint32_t(qrow) * orb + col);
+      const u32x4 lv = buf_load16(rs_lo, uint32_t(qrow) * D * 2u + col);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float o0 = to_f32<E>(uint16_t(ov[w] & 0xFFFFu)) + to_f32<E>(uint16_t(lv[w] & 0xFFFFu));
+        const float o1 = to_f32<E>(uint16_t(ov[w] >> 16)) + to_f32<E>(uint16_t(lv[w] >> 16));
+        sum += o0 * to_f32<E>(uint16_t(dof[st][w] & 0xFFFFu));
+        sum += o1 * to_f32<E>(uint16_t(dof[st][w] >> 16));
+      }
+    }
+    delta = xhalf_sum(sum);
+    const float l = qvalid ? a.lse[int64_t(bh) * T + qrow] : -INF;
+    lse = (l == -INF) ? INF : l;
+    if (qvalid && hf == 0) {
+      a.delta[int64_t(bh) * T + qrow] = delta;
+      a.delta[BHT + int64_t(bh) * T + qrow] = lse;
+    }
+  } else {
+    lse = qvalid ? a.delta[BHT + int64_t(bh) * T + qrow] : INF;
+    delta = qvalid ? a.delta[int64_t(bh) * T + qrow] : 0.f;
+  }
   // this wave's rows lie in q-tile 2 qblock + member; its row masks per key tile
   const int member = wave >> 1;
   const uint64_t* qbits_row = qbits + (int64_t(b) * nT + 2 * qblock + member) * nT * 64 + 32 * (wave & 1) + c;
@@ -578,12 +611,12 @@ static void launch_delta_t(const AttnArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((k_delta<E, D>), dim3(unsigned((rows + RPB - 1) / RPB)), dim3(256), 0, st, a);
 }
 template <class E, int D, bool Q8 = false>
-static void launch_dq_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
+static void launch_dq_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_delta) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dq_blocks;
   hipLaunchKernelGGL((k_dq<E, D, Q8>), dim3(grid), dim3(256), 0, st, a, reinterpret_cast<const uint64_t*>(plan + L.qbits),
                      reinterpret_cast<const uint32_t*>(plan + L.dq_list),
-                     reinterpret_cast<const int32_t*>(plan + L.dq_count), L.nT, L.n_dq_blocks);
+                     reinterpret_cast<const int32_t*>(plan + L.dq_count), L.nT, L.n_dq_blocks, fuse_delta);
 }
 template <class E, int D, bool Q8 = false>
 static void launch_dkdv_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
@@ -610,9 +643,9 @@ int launch_delta(const AttnArgs& a, hipStream_t st) {
   KD_DISPATCH(launch_delta_t, a, st);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
-int launch_dq(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
-  if (a.q8 != nullptr) launch_dq_t<BF16, 128, true>(a, plan, st);  // fp8 QK^T (checked by the C ABI)
-  else KD_DISPATCH(launch_dq_t, a, plan, st);
+int launch_dq(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_delta) {
+  if (a.q8 != nullptr) launch_dq_t<BF16, 128, true>(a, plan, st, fuse_delta);  // fp8 QK^T (checked by the C ABI)
+  else KD_DISPATCH(launch_dq_t, a, plan, st, fuse_delta);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 int launch_dkdv(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {

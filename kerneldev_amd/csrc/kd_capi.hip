@@ -196,7 +196,7 @@ int kd_attn_bwd_dq(const kd_attn_args* a, const void* plan, void* stream) {
   int r = check_bwd(a, plan);
   if (r) return r;
   if ((r = check_tensor(a->dq, a->dq_strides, "dq", a->T, a->D))) return r;
-  r = kd::launch_dq(*a, static_cast<const uint8_t*>(plan), as_stream(stream));
+  r = kd::launch_dq(*a, static_cast<const uint8_t*>(plan), as_stream(stream), false);
   return r ? fail(r, "kernel launch failed (dq)") : KD_OK;
 }
 
@@ -208,12 +208,19 @@ int kd_attn_bwd_dkdv(const kd_attn_args* a, const void* plan, void* stream) {
   return r ? fail(r, "kernel launch failed (dkdv)") : KD_OK;
 }
 
+int kd_attn_bwd_dq_delta(const kd_attn_args* a, const void* plan, void* stream) {
+  int r = check_bwd(a, plan);
+  if (r) return r;
+  if ((r = check_tensor(a->o, a->o_strides, "o", a->T, a->D)) || (r = check_tensor(a->dq, a->dq_strides, "dq", a->T, a->D)))
+    return r;
+  if (a->o_lo != nullptr && !aligned16(a->o_lo)) return fail(KD_ERR_INVALID, "o_lo must be 16-byte aligned");
+  r = kd::launch_dq(*a, static_cast<const uint8_t*>(plan), as_stream(stream), true);
+  return r ? fail(r, "kernel launch failed (dq)") : KD_OK;
+}
+
 int kd_attn_bwd(const kd_attn_args* a, const void* plan, void* stream) {
-  int r = kd_attn_bwd_delta(a, stream);
-  if (r) return r;
-  r = kd_attn_bwd_dq(a, plan, stream);
-  if (r) return r;
-  return kd_attn_bwd_dkdv(a, plan, stream);
+  const int r = kd_attn_bwd_dq_delta(a, plan, stream);
+  return r ? r : kd_attn_bwd_dkdv(a, plan, stream);
 }
 
 int kd_mask_dense(const void* plan, int32_t B, int32_t H, int32_t T, int32_t D, uint8_t* out,

@@ -39,7 +39,9 @@ int launch_mask_dense(const uint32_t* codes, int B, int H, int T, uint8_t* out, 
                       hipStream_t st);
 int launch_fwd(const AttnArgs& a, const uint8_t* plan, hipStream_t st);
 int launch_delta(const AttnArgs& a, hipStream_t st);
-int launch_dq(const AttnArgs& a, const uint8_t* plan, hipStream_t st);
+// fuse_delta: the dQ kernel also computes Delta and the LSE copy (k_delta's
+// job) for its rows and stores them for the dK/dV kernel
+int launch_dq(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_delta);
 int launch_dkdv(const AttnArgs& a, const uint8_t* plan, hipStream_t st);
 int launch_hadamard(const kd_rot_args& a, hipStream_t st);
 int launch_quant(const kd_quant_args& a, hipStream_t st);

@@ -202,6 +202,43 @@ def test_config4_cocktail_hadamard_fp8(dev):
     _case(inp, dev, heads=[(0, 5), (1, 30)], scaled=True, hadamard=True, hadamard_seed=0, qk_dtype="fp8_e4m3")
 
 
+def test_split_backward_entry_points_match_fused(dev):
+    """kd_attn_bwd_delta + kd_attn_bwd_dq + kd_attn_bwd_dkdv == kd_attn_bwd (Delta fused into dQ)."""
+    import ctypes
+
+    from kerneldev_amd import _lib
+    from kerneldev_amd.attention import _attn_args, _fwd_op, _ptr, _strides3
+
+    tokens, in_span, span_id, is_prefix = cocktail_batch(2, 1024, CONFIG3_LAYOUT, seed=21)
+    q, k, v, do = (x.to(dev) for x in qkvdo(2, 2, 1024, 128, seed=22))
+    meta = [x.to(dev) for x in (in_span, span_id, is_prefix)]
+    sc = 128 ** -0.5
+    o, lse, plan, o_lo = _fwd_op(q, k, v, None, *meta, sc, 0, True)
+    lib = _lib.load()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    outs = []
+    for split in (False, True):
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        delta = torch.empty((2,) + tuple(q.shape[:3]), dtype=torch.float32, device=dev)
+        a = _attn_args(q, k, v, sc)
+        a.o, a.o_strides, a.lse, a.o_lo = o.data_ptr(), _strides3(o), lse.data_ptr(), o_lo.data_ptr()
+        a.dout, a.do_strides = do.data_ptr(), _strides3(do)
+        a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+        a.dq_strides, a.dk_strides, a.dv_strides = _strides3(dq), _strides3(dk), _strides3(dv)
+        a.delta = delta.data_ptr()
+        if split:
+            _lib.check(lib.kd_attn_bwd_delta(ctypes.byref(a), stream), "delta")
+            _lib.check(lib.kd_attn_bwd_dq(ctypes.byref(a), _ptr(plan), stream), "dq")
+            _lib.check(lib.kd_attn_bwd_dkdv(ctypes.byref(a), _ptr(plan), stream), "dkdv")
+        else:
+            _lib.check(lib.kd_attn_bwd(ctypes.byref(a), _ptr(plan), stream), "bwd")
+        torch.cuda.synchronize()
+        outs.append((dq, dk, dv, delta))
+    # the two Delta sums differ in order only: gradients agree to within a bf16 ulp
+    for name, x, y in zip(("dq", "dk", "dv", "delta"), outs[0], outs[1]):
+        assert_close(name, x, y, max_abs=1e-4, rel_rms=1e-3)
+
+
 def test_deterministic(dev):
     inp = config_inputs(3, seed=1)
     a = run_gpu(inp, dev)
