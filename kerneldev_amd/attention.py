@@ -98,6 +98,13 @@ def _attn_args(q, k, v, sm_scale) -> AttnArgs:
 
 
 # ----------------------------------------------------------------- custom ops
+def _new_out(B, H, T, D, q, bthd: bool) -> torch.Tensor:
+    """O as [B, H, T, D]: contiguous, or a view of [B, T, H, D] memory (bthd)."""
+    if bthd:
+        return torch.empty((B, T, H, D), dtype=q.dtype, device=q.device).transpose(1, 2)
+    return torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
+
+
 def _set_fp8(a: AttnArgs, fp8):
     """Point the kernels at the fp8 copies ``(q8, k8, q_scale, k_scale)``, or not."""
     if fp8 is None:
@@ -122,10 +129,11 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
             is_prefix: torch.Tensor | None, sm_scale: float, mode: int, need_lo: bool,
             q8: torch.Tensor | None = None, k8: torch.Tensor | None = None,
             q_scale: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
+            bthd: bool = False,
             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     B, H, T, D = q.shape
     plan = build_plan(B, T, D, q.device, mode, in_span, span_id, is_prefix, lens)
-    o = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
+    o = _new_out(B, H, T, D, q, bthd)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
     # rounding residual of O, kept for the backward's Delta (see kd_bwd.hip)
     o_lo = torch.empty((B, H, T, D) if need_lo else (0,), dtype=q.dtype, device=q.device)
@@ -140,9 +148,9 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
 
 @_fwd_op.register_fake
 def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8=None, k8=None,
-              q_scale=None, k_scale=None):
+              q_scale=None, k_scale=None, bthd=False):
     B, H, T, D = q.shape
-    return (torch.empty((B, H, T, D), dtype=q.dtype, device=q.device),
+    return (_new_out(B, H, T, D, q, bthd),
             torch.empty((B, H, T), dtype=torch.float32, device=q.device),
             torch.empty(_lib.plan_bytes(B, T, D), dtype=torch.uint8, device=q.device),
             torch.empty((B, H, T, D) if need_lo else (0,), dtype=q.dtype, device=q.device))
@@ -179,7 +187,7 @@ def _bwd_fake(q, k, v, o, lse, do, plan, sm_scale, o_lo, q8=None, k8=None, q_sca
 
 
 def _setup_context(ctx, inputs, output):
-    q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8, k8, q_scale, k_scale = inputs
+    q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8, k8, q_scale, k_scale, bthd = inputs
     o, lse, plan, o_lo = output
     ctx.fp8 = q8 is not None
     extra = (q8, k8, q_scale, k_scale) if ctx.fp8 else ()
@@ -193,7 +201,7 @@ def _backward(ctx, do, dlse, dplan, do_lo):
     # dK = dS^T Q from the 16-bit operands: the straight-through estimator.
     q, k, v, o, lse, plan, o_lo, *extra = ctx.saved_tensors
     dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, ctx.sm_scale, o_lo, *extra)
-    return dq, dk, dv, None, None, None, None, None, None, None, None, None, None, None
+    return dq, dk, dv, None, None, None, None, None, None, None, None, None, None, None, None
 
 
 _fwd_op.register_autograd(_backward, setup_context=_setup_context)
@@ -232,6 +240,7 @@ def flash_attention(
     hadamard: bool = False,
     hadamard_seed: int | None = None,
     qk_dtype: str = "bf16",
+    out_layout: str = "bhtd",
 ):
     """Hierarchical-mask flash attention on MI355X (same contract as the reference).
 
@@ -246,7 +255,10 @@ def flash_attention(
     ``diag(s) H_d / sqrt(d)`` with signs ``generate_hadamard_signs(d,
     hadamard_seed)`` before the product (exact in real arithmetic);
     ``qk_dtype="fp8_e4m3"`` additionally runs Q K^T on fp8 with per-(b, h)
-    absmax scales.
+    absmax scales.  ``out_layout="bthd"`` returns O as a ``[B, H, T, d]`` view of
+    ``[B, T, H, d]`` memory, so that ``o.transpose(1, 2).reshape(B, T, H * d)``
+    -- what ``MultiHeadAttention`` feeds ``o_proj`` (model.py:95) -- is a view;
+    the default is the reference's contiguous O.
 
     Returns ``O``, ``(O, LSE)``, ``(O, mask)`` or ``((O, LSE), mask)`` as at
     ``:2083-2089``; LSE is fp32 ``[B, H, T]`` in log2 units, mask is bool
@@ -267,6 +279,8 @@ def flash_attention(
         raise ValueError(f"precision must be 'ieee' or 'tf32', got {precision!r}")
     if lens is not None and (lens.dtype != torch.int32 or lens.dim() != 1 or lens.shape[0] != B):
         raise ValueError("lens must be an int32 tensor of shape [batch]")
+    if out_layout not in ("bhtd", "bthd"):
+        raise ValueError(f"out_layout must be 'bhtd' or 'bthd', got {out_layout!r}")
     if qk_dtype not in ("bf16", "fp8_e4m3"):
         raise ValueError(f"qk_dtype must be 'bf16' or 'fp8_e4m3', got {qk_dtype!r}")
     if not q.is_cuda:
@@ -313,7 +327,7 @@ def flash_attention(
 
     need_lo = torch.is_grad_enabled() and any(x.requires_grad for x in (q, k, v))
     o, lse, plan, _ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode), need_lo,
-                              *fp8)
+                              *(fp8 or (None, None, None, None)), bthd=out_layout == "bthd")
     if in_dtype == torch.float32:
         o = o.to(torch.float32)
 

@@ -7,7 +7,8 @@ RMSNorm -> SwiGLU -> residual, a final RMSNorm, a head tied to the token
 embedding, N(0, 0.02) init (``:174-178``).  Attention goes through
 ``flash_attention`` with the mask metadata, exactly as ``model.py:73-96``
 calls it; the q/k/v projections are handed over as strided ``[B, H, L, d]``
-views of ``[B, L, H, d]``, without copies.
+views of ``[B, L, H, d]``, without copies, and O comes back in ``[B, L, H, d]``
+memory (``out_layout="bthd"``), so ``o_proj`` reads it without a copy either.
 
 The cocktail-party head (``model.py:243-295``) scores the hidden state at the
 first ``[MASK]`` against the mean hidden state of each span's interior
@@ -73,8 +74,11 @@ class MultiHeadAttention(nn.Module):
         q = self.q_proj(x).view(shape).transpose(1, 2)
         k = self.k_proj(x).view(shape).transpose(1, 2)
         v = self.v_proj(x).view(shape).transpose(1, 2)
+        # flash_attention writes O straight into [B, L, H, d] memory, so the
+        # transpose + reshape below is a view rather than model.py:95's copy
+        extra = {"out_layout": "bthd"} if self.attention is flash_attention else {}
         out = self.attention(q, k, v, lens=None, causal=self.causal, attention_mask=None,
-                             in_span=in_span, span_id=span_id, is_prefix=is_prefix)
+                             in_span=in_span, span_id=span_id, is_prefix=is_prefix, **extra)
         return self.o_proj(out.transpose(1, 2).reshape(B, L, -1))
 
 

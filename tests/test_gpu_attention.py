@@ -202,6 +202,26 @@ def test_config4_cocktail_hadamard_fp8(dev):
     _case(inp, dev, heads=[(0, 5), (1, 30)], scaled=True, hadamard=True, hadamard_seed=0, qk_dtype="fp8_e4m3")
 
 
+def test_out_layout_bthd(dev):
+    """O in [B, T, H, d] memory: same values and gradients as the default layout."""
+    tokens, in_span, span_id, is_prefix = cocktail_batch(2, 512, CONFIG3_LAYOUT, seed=23)
+    base = qkvdo(2, 3, 512, 64, seed=24)
+    meta = dict(in_span=in_span.to(dev), span_id=span_id.to(dev), is_prefix=is_prefix.to(dev))
+    res = []
+    for layout in ("bhtd", "bthd"):
+        q, k, v = (x.to(dev).requires_grad_(True) for x in base[:3])
+        o = flash_attention(q, k, v, out_layout=layout, **meta)
+        if layout == "bthd":
+            assert o.shape == (2, 3, 512, 64) and o.transpose(1, 2).is_contiguous()
+        else:
+            assert o.is_contiguous()
+        o.backward(base[3].to(dev))
+        torch.cuda.synchronize()
+        res.append((o.detach(), q.grad, k.grad, v.grad))
+    for x, y in zip(res[0], res[1]):
+        assert torch.equal(x, y)
+
+
 def test_split_backward_entry_points_match_fused(dev):
     """kd_attn_bwd_delta + kd_attn_bwd_dq + kd_attn_bwd_dkdv == kd_attn_bwd (Delta fused into dQ)."""
     import ctypes
