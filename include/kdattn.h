@@ -65,6 +65,22 @@ typedef struct kd_meta_args {
   int32_t pad_;
 } kd_meta_args;
 
+/* Token rows for kd_plan_build_tokens: ids of data_builder.py:44-52
+ * ([PAD]=0, [CLS]=1, [MASK]=2, [SPAN]=3, [ES]=4, [MASKQ]=5, bytes + 6). */
+#define KD_RULE_COLLATE 0   /* data_builder.py:603-643: [SPAN]..[ES] inclusive, first [MASKQ] -> -1 */
+#define KD_RULE_FALLBACK 1  /* model.py:209-240: [ES] outside its span, every [MASKQ] -> -1 */
+#define KD_RULE_TEACHER 2   /* train_loop.py:406-435: prefix only */
+typedef struct kd_token_args {
+  const void *tokens;       /* int64 or int32 [B, T] */
+  int64_t tokens_strides[2];
+  int32_t tokens_dtype;     /* KD_I64 / KD_I32 */
+  int32_t rule;             /* KD_RULE_* */
+  const int32_t *lens;      /* int32 [B] or NULL */
+  int64_t lens_stride;
+  int32_t B, T, D;
+  int32_t pad_;
+} kd_token_args;
+
 /* Attention operands (forward and backward share one struct). */
 typedef struct kd_attn_args {
   const void *q, *k, *v;        /* [B, H, T, D] */
@@ -125,6 +141,7 @@ const char *kd_last_error_string(void);
 /* sizeof(kd_meta_args), sizeof(kd_attn_args): lets bindings check layouts. */
 void kd_struct_sizes(size_t *meta, size_t *attn);
 void kd_struct_sizes2(size_t *rot, size_t *quant);
+void kd_struct_sizes3(size_t *tokens);
 
 /* Workspace ("plan") bytes for B sequences of length T at head dim D, and
  * the byte offsets of its sections (codes, class map, per-tile allowed
@@ -143,6 +160,13 @@ int kd_plan_layout(int32_t B, int32_t T, int32_t D, int64_t *offsets);
  * per-block work lists.  Mask rules: original_kernel.py:478-517, with lens
  * (:299-303, :517) and the no-metadata fallbacks (:512-515). */
 int kd_plan_build(const kd_meta_args *meta, void *plan, void *stream);
+
+/* The plan straight from token ids: is_prefix, in_span and span_id are derived
+ * on the device by the chosen rule (written into the plan's own workspace) and
+ * the plan is then built as kd_plan_build would from them.  Replaces the
+ * per-token Python loops with host syncs at data_builder.py:603-643,
+ * model.py:209-240 and train_loop.py:406-435 ahead of the mask evaluation. */
+int kd_plan_build_tokens(const kd_token_args *t, void *plan, void *stream);
 
 /* Forward: O and LSE.  Replaces attention_forward_adapter's launch of
  * _flash_attn_fwd (original_kernel.py:1697-1778, kernel :279-626). */

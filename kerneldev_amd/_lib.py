@@ -68,6 +68,17 @@ class RotArgs(ctypes.Structure):
     ]
 
 
+class TokenArgs(ctypes.Structure):
+    """Mirror of ``kd_token_args``."""
+
+    _fields_ = [
+        ("tokens", c_void_p), ("tokens_strides", c_int64 * 2),
+        ("tokens_dtype", c_int32), ("rule", c_int32),
+        ("lens", c_void_p), ("lens_stride", c_int64),
+        ("B", c_int32), ("T", c_int32), ("D", c_int32), ("pad_", c_int32),
+    ]
+
+
 class QuantArgs(ctypes.Structure):
     """Mirror of ``kd_quant_args``."""
 
@@ -85,6 +96,8 @@ SIGNATURES = {
     "kd_last_error_string": (c_char_p, []),
     "kd_struct_sizes": (None, [POINTER(c_size_t), POINTER(c_size_t)]),
     "kd_struct_sizes2": (None, [POINTER(c_size_t), POINTER(c_size_t)]),
+    "kd_struct_sizes3": (None, [POINTER(c_size_t)]),
+    "kd_plan_build_tokens": (c_int, [POINTER(TokenArgs), c_void_p, c_void_p]),
     "kd_hadamard": (c_int, [POINTER(RotArgs), c_void_p]),
     "kd_quant_fp8": (c_int, [POINTER(QuantArgs), c_void_p]),
     "kd_plan_bytes": (c_int64, [c_int32, c_int32, c_int32]),
@@ -125,8 +138,11 @@ def load():
     lib.kd_struct_sizes(ctypes.byref(ms), ctypes.byref(as_))
     rs, qs = c_size_t(), c_size_t()
     lib.kd_struct_sizes2(ctypes.byref(rs), ctypes.byref(qs))
+    ts = c_size_t()
+    lib.kd_struct_sizes3(ctypes.byref(ts))
     if (ms.value != ctypes.sizeof(MetaArgs) or as_.value != ctypes.sizeof(AttnArgs)
-            or rs.value != ctypes.sizeof(RotArgs) or qs.value != ctypes.sizeof(QuantArgs)):
+            or rs.value != ctypes.sizeof(RotArgs) or qs.value != ctypes.sizeof(QuantArgs)
+            or ts.value != ctypes.sizeof(TokenArgs)):
         raise ImportError(
             f"struct layout mismatch: C meta={ms.value} attn={as_.value} rot={rs.value} quant={qs.value}, "
             f"ctypes meta={ctypes.sizeof(MetaArgs)} attn={ctypes.sizeof(AttnArgs)} "

@@ -86,6 +86,50 @@ def build_plan(B, T, D, device, mode, in_span=None, span_id=None, is_prefix=None
     return plan
 
 
+RULES = {"collate": 0, "fallback": 1, "teacher_forcing": 2}  # KD_RULE_*
+
+
+class AttentionPlan:
+    """The tile plan of one mask, built once and passed to any number of
+    ``flash_attention(..., plan=...)`` calls on ``[B, *, T, D]`` operands --
+    e.g. every layer of one model forward, which share the tokens' mask."""
+
+    def __init__(self, tensor: torch.Tensor, B: int, T: int, D: int):
+        self.tensor, self.B, self.T, self.D = tensor, B, T, D
+
+
+def build_plan_from_tokens(tokens: torch.Tensor, head_dim: int, rule: str = "collate",
+                           lens: torch.Tensor | None = None) -> AttentionPlan:
+    """Plan straight from token ids ``[B, T]`` on the device (``kd_plan_build_tokens``).
+
+    The metadata rule is one of ``derive_metadata``'s (``"collate"``,
+    ``"fallback"``, ``"teacher_forcing"``); the result equals building the plan
+    from ``derive_metadata(tokens, rule)``, with no host sync and no metadata
+    tensors.
+    """
+    if tokens.dim() != 2 or tokens.dtype not in (torch.int64, torch.int32) or not tokens.is_cuda:
+        raise ValueError("tokens must be an int64 / int32 [B, T] GPU tensor")
+    if rule not in RULES:
+        raise ValueError(f"unknown metadata rule {rule!r}")
+    if head_dim not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head_dim must be one of {SUPPORTED_HEAD_DIMS}")
+    if lens is not None and (lens.dtype != torch.int32 or lens.dim() != 1 or lens.shape[0] != tokens.shape[0]):
+        raise ValueError("lens must be an int32 tensor of shape [batch]")
+    B, T = tokens.shape
+    plan = torch.empty(_lib.plan_bytes(B, T, head_dim), dtype=torch.uint8, device=tokens.device)
+    t = _lib.TokenArgs()
+    t.tokens = tokens.data_ptr()
+    t.tokens_strides[0], t.tokens_strides[1] = tokens.stride()
+    t.tokens_dtype = _lib.KD_I64 if tokens.dtype == torch.int64 else _lib.KD_I32
+    t.rule = RULES[rule]
+    if lens is not None:
+        t.lens, t.lens_stride = lens.data_ptr(), lens.stride(0)
+    t.B, t.T, t.D = B, T, head_dim
+    _lib.check(_lib.load().kd_plan_build_tokens(ctypes.byref(t), _ptr(plan), _stream(tokens.device)),
+               "kd_plan_build_tokens")
+    return AttentionPlan(plan, B, T, head_dim)
+
+
 def _attn_args(q, k, v, sm_scale) -> AttnArgs:
     a = AttnArgs()
     B, H, T, D = q.shape
@@ -129,10 +173,11 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
             is_prefix: torch.Tensor | None, sm_scale: float, mode: int, need_lo: bool,
             q8: torch.Tensor | None = None, k8: torch.Tensor | None = None,
             q_scale: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
-            bthd: bool = False,
+            bthd: bool = False, plan_in: torch.Tensor | None = None,
             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     B, H, T, D = q.shape
-    plan = build_plan(B, T, D, q.device, mode, in_span, span_id, is_prefix, lens)
+    # a caller's plan is used as is (and not returned: outputs may not alias inputs)
+    plan = plan_in if plan_in is not None else build_plan(B, T, D, q.device, mode, in_span, span_id, is_prefix, lens)
     o = _new_out(B, H, T, D, q, bthd)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
     # rounding residual of O, kept for the backward's Delta (see kd_bwd.hip)
@@ -143,16 +188,16 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
     a.lse = lse.data_ptr()
     a.o_lo = o_lo.data_ptr() if need_lo else None
     _lib.check(_lib.load().kd_attn_fwd(ctypes.byref(a), _ptr(plan), _stream(q.device)), "kd_attn_fwd")
-    return o, lse, plan, o_lo
+    return o, lse, (plan if plan_in is None else plan.new_empty(0)), o_lo
 
 
 @_fwd_op.register_fake
 def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8=None, k8=None,
-              q_scale=None, k_scale=None, bthd=False):
+              q_scale=None, k_scale=None, bthd=False, plan_in=None):
     B, H, T, D = q.shape
     return (_new_out(B, H, T, D, q, bthd),
             torch.empty((B, H, T), dtype=torch.float32, device=q.device),
-            torch.empty(_lib.plan_bytes(B, T, D), dtype=torch.uint8, device=q.device),
+            torch.empty(_lib.plan_bytes(B, T, D) if plan_in is None else 0, dtype=torch.uint8, device=q.device),
             torch.empty((B, H, T, D) if need_lo else (0,), dtype=q.dtype, device=q.device))
 
 
@@ -187,8 +232,10 @@ def _bwd_fake(q, k, v, o, lse, do, plan, sm_scale, o_lo, q8=None, k8=None, q_sca
 
 
 def _setup_context(ctx, inputs, output):
-    q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8, k8, q_scale, k_scale, bthd = inputs
+    q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8, k8, q_scale, k_scale, bthd, plan_in = inputs
     o, lse, plan, o_lo = output
+    if plan_in is not None:
+        plan = plan_in
     ctx.fp8 = q8 is not None
     extra = (q8, k8, q_scale, k_scale) if ctx.fp8 else ()
     ctx.save_for_backward(q, k, v, o, lse, plan, o_lo, *extra)
@@ -201,7 +248,7 @@ def _backward(ctx, do, dlse, dplan, do_lo):
     # dK = dS^T Q from the 16-bit operands: the straight-through estimator.
     q, k, v, o, lse, plan, o_lo, *extra = ctx.saved_tensors
     dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, ctx.sm_scale, o_lo, *extra)
-    return dq, dk, dv, None, None, None, None, None, None, None, None, None, None, None, None
+    return dq, dk, dv, None, None, None, None, None, None, None, None, None, None, None, None, None
 
 
 _fwd_op.register_autograd(_backward, setup_context=_setup_context)
@@ -241,6 +288,7 @@ def flash_attention(
     hadamard_seed: int | None = None,
     qk_dtype: str = "bf16",
     out_layout: str = "bhtd",
+    plan: AttentionPlan | None = None,
 ):
     """Hierarchical-mask flash attention on MI355X (same contract as the reference).
 
@@ -258,7 +306,9 @@ def flash_attention(
     absmax scales.  ``out_layout="bthd"`` returns O as a ``[B, H, T, d]`` view of
     ``[B, T, H, d]`` memory, so that ``o.transpose(1, 2).reshape(B, T, H * d)``
     -- what ``MultiHeadAttention`` feeds ``o_proj`` (model.py:95) -- is a view;
-    the default is the reference's contiguous O.
+    the default is the reference's contiguous O.  ``plan`` (from
+    ``build_plan_from_tokens``) replaces the metadata arguments with a plan
+    built once and shared, e.g. by all layers of a model.
 
     Returns ``O``, ``(O, LSE)``, ``(O, mask)`` or ``((O, LSE), mask)`` as at
     ``:2083-2089``; LSE is fp32 ``[B, H, T]`` in log2 units, mask is bool
@@ -279,6 +329,12 @@ def flash_attention(
         raise ValueError(f"precision must be 'ieee' or 'tf32', got {precision!r}")
     if lens is not None and (lens.dtype != torch.int32 or lens.dim() != 1 or lens.shape[0] != B):
         raise ValueError("lens must be an int32 tensor of shape [batch]")
+    if plan is not None:
+        if any(x is not None for x in (in_span, span_id, is_prefix, lens, attention_mask)):
+            raise ValueError("plan replaces in_span / span_id / is_prefix / lens / attention_mask")
+        if (plan.B, plan.T, plan.D) != (B, T, D) or plan.tensor.device != q.device:
+            raise ValueError(f"plan is for [B, T, D] = {[plan.B, plan.T, plan.D]} on {plan.tensor.device}, "
+                             f"not {[B, T, D]} on {q.device}")
     if out_layout not in ("bhtd", "bthd"):
         raise ValueError(f"out_layout must be 'bhtd' or 'bthd', got {out_layout!r}")
     if qk_dtype not in ("bf16", "fp8_e4m3"):
@@ -326,8 +382,11 @@ def flash_attention(
         fp8 = (q8, k8, q_scale, k_scale)
 
     need_lo = torch.is_grad_enabled() and any(x.requires_grad for x in (q, k, v))
-    o, lse, plan, _ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode), need_lo,
-                              *(fp8 or (None, None, None, None)), bthd=out_layout == "bthd")
+    o, lse, plan_t, _ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode), need_lo,
+                                *(fp8 or (None, None, None, None)), bthd=out_layout == "bthd",
+                                plan_in=None if plan is None else plan.tensor)
+    if plan is not None:
+        plan_t = plan.tensor
     if in_dtype == torch.float32:
         o = o.to(torch.float32)
 
@@ -335,7 +394,7 @@ def flash_attention(
     if return_attention_mask:
         mask = torch.empty((B, H, T, T), dtype=torch.bool, device=device)
         st = (ctypes.c_int64 * 4)(*mask.stride())
-        _lib.check(_lib.load().kd_mask_dense(_ptr(plan), B, H, T, D, _ptr(mask), st, _stream(device)),
+        _lib.check(_lib.load().kd_mask_dense(_ptr(plan_t), B, H, T, D, _ptr(mask), st, _stream(device)),
                    "kd_mask_dense")
     if return_attention_mask:
         if return_lse:

@@ -85,6 +85,26 @@ void kd_struct_sizes2(size_t* rot, size_t* quant) {
   if (quant) *quant = sizeof(kd_quant_args);
 }
 
+void kd_struct_sizes3(size_t* tokens) {
+  if (tokens) *tokens = sizeof(kd_token_args);
+}
+
+int kd_plan_build_tokens(const kd_token_args* t, void* plan, void* stream) {
+  if (t == nullptr || plan == nullptr) return fail(KD_ERR_INVALID, "args or plan is NULL");
+  if (!aligned16(plan)) return fail(KD_ERR_INVALID, "plan must be 16-byte aligned");
+  if (t->B < 1 || t->T < 1) return fail(KD_ERR_INVALID, "B and T must be >= 1");
+  if (t->T > (1 << 24) - 2) return fail(KD_ERR_UNSUPPORTED, "T must be < 2^24 - 1");
+  if (t->tokens == nullptr) return fail(KD_ERR_INVALID, "tokens is NULL");
+  if (t->tokens_dtype != KD_I64 && t->tokens_dtype != KD_I32)
+    return fail(KD_ERR_INVALID, "tokens dtype must be int64 or int32");
+  if (t->rule != KD_RULE_COLLATE && t->rule != KD_RULE_FALLBACK && t->rule != KD_RULE_TEACHER)
+    return fail(KD_ERR_INVALID, "unknown metadata rule");
+  if (t->tokens_strides[0] < 0 || t->tokens_strides[1] < 0) return fail(KD_ERR_INVALID, "negative token strides");
+  if (t->lens != nullptr && t->lens_stride < 0) return fail(KD_ERR_INVALID, "negative lens stride");
+  const int r = kd::launch_plan_tokens(*t, static_cast<uint8_t*>(plan), as_stream(stream));
+  return r ? fail(r, "kernel launch failed (plan from tokens)") : KD_OK;
+}
+
 int kd_quant_fp8(const kd_quant_args* a, void* stream) {
   if (a == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
   if (a->B < 1 || a->H < 1 || a->T < 1) return fail(KD_ERR_INVALID, "B, H and T must be >= 1");

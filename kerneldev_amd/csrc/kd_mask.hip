@@ -81,6 +81,74 @@ __global__ void k_rep(MetaArgs m, const uint32_t* runs, const int64_t* run_sid, 
     }
 }
 
+// ---- token ids -> metadata (kd_plan_build_tokens) -------------------------
+// One workgroup per batch row; thread i scans a contiguous segment of it.
+// Segment counts of [SPAN] and [ES] are prefix-summed over the threads and the
+// first [CLS] / [MASKQ] are block minima; a second pass then writes, with
+// n_span(t), n_es(t) the inclusive counts up to t:
+//   collate   in_span = n_span(t) - n_es(t-1) > 0   ([SPAN] .. [ES] inclusive)
+//   fallback  in_span = n_span(t) - n_es(t) > 0     ([ES] falls outside)
+//   span_id = in_span ? n_span(t) : 0, and -1 at [MASKQ] (collate: the first)
+//   is_prefix = t <= first [CLS] (none without a [CLS])
+// -- the cumulative-count forms of data_builder.py:603-643 and model.py:209-240.
+enum : int64_t { TOK_CLS = 1, TOK_SPAN = 3, TOK_ES = 4, TOK_MASKQ = 5 };
+
+__global__ __launch_bounds__(256) void k_token_meta(kd_token_args a, uint8_t* in_span, int64_t* span_id,
+                                                    uint8_t* is_prefix) {
+  const int b = blockIdx.x, tid = threadIdx.x, T = a.T;
+  const int seg = (T + 255) / 256, t0 = min(T, tid * seg), t1 = min(T, t0 + seg);
+  auto tok = [&](int t) -> int64_t {
+    const int64_t off = int64_t(b) * a.tokens_strides[0] + int64_t(t) * a.tokens_strides[1];
+    return a.tokens_dtype == KD_I64 ? static_cast<const int64_t*>(a.tokens)[off]
+                                    : int64_t(static_cast<const int32_t*>(a.tokens)[off]);
+  };
+  int ns = 0, ne = 0, first_cls = T, first_mq = T;
+  for (int t = t0; t < t1; ++t) {
+    const int64_t x = tok(t);
+    ns += x == TOK_SPAN;
+    ne += x == TOK_ES;
+    if (x == TOK_CLS && first_cls == T) first_cls = t;
+    if (x == TOK_MASKQ && first_mq == T) first_mq = t;
+  }
+  __shared__ int s_ns[256], s_ne[256], s_cls[256], s_mq[256];
+  s_ns[tid] = ns;
+  s_ne[tid] = ne;
+  s_cls[tid] = first_cls;
+  s_mq[tid] = first_mq;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {  // inclusive scans and minima (Hillis-Steele)
+    int a_ns = 0, a_ne = 0, a_c = T, a_m = T;
+    if (tid >= off) {
+      a_ns = s_ns[tid - off];
+      a_ne = s_ne[tid - off];
+    }
+    a_c = s_cls[tid ^ off];
+    a_m = s_mq[tid ^ off];
+    __syncthreads();
+    s_ns[tid] += a_ns;
+    s_ne[tid] += a_ne;
+    s_cls[tid] = min(s_cls[tid], a_c);
+    s_mq[tid] = min(s_mq[tid], a_m);
+    __syncthreads();
+  }
+  const int cls = s_cls[tid], mq = s_mq[tid];  // block minima (butterfly: every thread holds them)
+  int n_span = s_ns[tid] - ns, n_es = s_ne[tid] - ne;  // counts before t0
+  const bool spans = a.rule != KD_RULE_TEACHER;
+  for (int t = t0; t < t1; ++t) {
+    const int64_t x = tok(t);
+    const int es_before = n_es;
+    n_span += x == TOK_SPAN;
+    n_es += x == TOK_ES;
+    const bool in = spans && (n_span - (a.rule == KD_RULE_COLLATE ? es_before : n_es)) > 0;
+    int64_t sid = in ? n_span : 0;
+    if (spans && x == TOK_MASKQ && (a.rule == KD_RULE_FALLBACK || t == mq)) sid = -1;
+    const int64_t o = int64_t(b) * T + t;
+    in_span[o] = in ? 1 : 0;
+    span_id[o] = sid;
+    is_prefix[o] = (cls < T && t <= cls) ? 1 : 0;
+  }
+}
+
 // ---- token codes -------------------------------------------------------
 __global__ void k_codes(MetaArgs m, const uint32_t* rep, uint32_t* codes) {
   const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -264,6 +332,9 @@ PlanLayout plan_layout(int B, int T, int D) {
   L.runs = take(BT * 4);
   L.run_sid = take(BT * 8);
   L.run_count = take(size_t(B) * 4);
+  L.tok_in_span = take(BT);
+  L.tok_span_id = take(BT * 8);
+  L.tok_prefix = take(BT);
   L.cls = take(BTT);
   L.nnz = take(BTT * 4);
   const int nf = (nT + L.fwd_group - 1) / L.fwd_group;
@@ -311,6 +382,31 @@ int launch_plan(const MetaArgs& m, uint8_t* plan, hipStream_t st) {
   const int max_rb = std::max(L.n_fwd_blocks, std::max(L.n_dq_blocks, L.n_dkdv_blocks));
   hipLaunchKernelGGL(k_lists, dim3(unsigned(m.B * max_rb), 3), dim3(64), 0, st, cls, m.B, L.nT, specs);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
+}
+
+int launch_plan_tokens(const kd_token_args& t, uint8_t* plan, hipStream_t st) {
+  const PlanLayout L = plan_layout(t.B, t.T, t.D);
+  MetaArgs m{};
+  m.in_span = plan + L.tok_in_span;
+  m.in_span_strides[0] = t.T;
+  m.in_span_strides[1] = 1;
+  m.span_id = plan + L.tok_span_id;
+  m.span_id_strides[0] = t.T;
+  m.span_id_strides[1] = 1;
+  m.span_id_dtype = KD_I64;
+  m.is_prefix = plan + L.tok_prefix;
+  m.is_prefix_strides[0] = t.T;
+  m.is_prefix_strides[1] = 1;
+  m.mode = KD_MODE_FORMULA;
+  m.lens = t.lens;
+  m.lens_stride = t.lens_stride;
+  m.B = t.B;
+  m.T = t.T;
+  m.D = t.D;
+  hipLaunchKernelGGL(k_token_meta, dim3(unsigned(t.B)), dim3(256), 0, st, t, plan + L.tok_in_span,
+                     reinterpret_cast<int64_t*>(plan + L.tok_span_id), plan + L.tok_prefix);
+  if (hipGetLastError() != hipSuccess) return KD_ERR_LAUNCH;
+  return launch_plan(m, plan, st);
 }
 
 int launch_mask_dense(const uint32_t* codes, int B, int H, int T, uint8_t* out, const int64_t* s,

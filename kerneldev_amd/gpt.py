@@ -26,7 +26,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .attention import flash_attention
+from .attention import AttentionPlan, build_plan, build_plan_from_tokens, flash_attention, mask_mode
 from .metadata import CLS, ES, MASK, MASKQ, SPAN, derive_metadata
 
 VOCAB = 256 + 6  # byte tokens + [PAD] [CLS] [MASK] [SPAN] [ES] [MASKQ] (data_builder.py:44-52)
@@ -68,17 +68,19 @@ class MultiHeadAttention(nn.Module):
         self.o_proj = nn.Linear(dim, dim, bias=False)
         self.attention = attention or flash_attention
 
-    def forward(self, x, in_span, span_id, is_prefix):
+    def forward(self, x, in_span, span_id, is_prefix, plan=None):
         B, L, _ = x.shape
         shape = (B, L, self.n_heads, self.head_dim)
         q = self.q_proj(x).view(shape).transpose(1, 2)
         k = self.k_proj(x).view(shape).transpose(1, 2)
         v = self.v_proj(x).view(shape).transpose(1, 2)
-        # flash_attention writes O straight into [B, L, H, d] memory, so the
-        # transpose + reshape below is a view rather than model.py:95's copy
-        extra = {"out_layout": "bthd"} if self.attention is flash_attention else {}
-        out = self.attention(q, k, v, lens=None, causal=self.causal, attention_mask=None,
-                             in_span=in_span, span_id=span_id, is_prefix=is_prefix, **extra)
+        if plan is not None:  # the model's shared plan stands for the metadata
+            # flash_attention writes O straight into [B, L, H, d] memory, so the
+            # transpose + reshape below is a view rather than model.py:95's copy
+            out = flash_attention(q, k, v, causal=self.causal, plan=plan, out_layout="bthd")
+        else:
+            out = self.attention(q, k, v, lens=None, causal=self.causal, attention_mask=None,
+                                 in_span=in_span, span_id=span_id, is_prefix=is_prefix)
         return self.o_proj(out.transpose(1, 2).reshape(B, L, -1))
 
 
@@ -89,8 +91,8 @@ class Block(nn.Module):
         self.attn = MultiHeadAttention(dim, n_heads, causal, attention)
         self.mlp = SwiGLU(dim, hidden)
 
-    def forward(self, x, in_span, span_id, is_prefix):
-        x = x + self.attn(self.norm1(x), in_span, span_id, is_prefix)
+    def forward(self, x, in_span, span_id, is_prefix, plan=None):
+        x = x + self.attn(self.norm1(x), in_span, span_id, is_prefix, plan)
         return x + self.mlp(self.norm2(x))
 
 
@@ -110,18 +112,34 @@ class GPTModel(nn.Module):
             if isinstance(m, (nn.Linear, nn.Embedding)):
                 nn.init.normal_(m.weight, mean=0.0, std=0.02)
 
-    def hidden(self, tokens, in_span, span_id, is_prefix):
+    def hidden(self, tokens, in_span, span_id, is_prefix, plan=None):
         pos = torch.arange(tokens.shape[1], device=tokens.device)
         h = self.token_emb(tokens) + self.pos_emb(pos)[None]
         for blk in self.blocks:
-            h = blk(h, in_span, span_id, is_prefix)
+            h = blk(h, in_span, span_id, is_prefix, plan)
         return self.norm_out(h)
+
+    def plan(self, tokens, in_span=None, span_id=None, is_prefix=None) -> AttentionPlan | None:
+        """One tile plan for every layer: from the given metadata (the training
+        path's collate metadata, model.py:197-201), else straight from the tokens
+        by the model's fallback rule (model.py:209-240) on the device.  None when
+        the blocks run an injected reference attention."""
+        attn = self.blocks[0].attn
+        if attn.attention is not flash_attention:
+            return None
+        B, T = tokens.shape
+        if in_span is None or span_id is None or is_prefix is None:
+            return build_plan_from_tokens(tokens, attn.head_dim, rule="fallback")
+        mode = mask_mode(in_span, span_id, is_prefix, None, attn.causal)
+        return AttentionPlan(build_plan(B, T, attn.head_dim, tokens.device, mode, in_span, span_id, is_prefix),
+                             B, T, attn.head_dim)
 
     def forward(self, tokens, correct_idx=None, in_span=None, span_id=None, is_prefix=None, targets=None):
         """Cocktail-party scores and loss, or LM logits and loss (model.py:180-314)."""
-        if in_span is None or span_id is None or is_prefix is None:
+        plan = self.plan(tokens, in_span, span_id, is_prefix)
+        if plan is None and (in_span is None or span_id is None or is_prefix is None):
             in_span, span_id, is_prefix = derive_metadata(tokens, rule="fallback")
-        h = self.hidden(tokens, in_span, span_id, is_prefix)
+        h = self.hidden(tokens, in_span, span_id, is_prefix, plan)
         if (tokens == MASK).any() and (tokens == SPAN).any() and (tokens == ES).any():
             scores = span_scores(tokens, h)
             loss = F.cross_entropy(scores, correct_idx) if correct_idx is not None else None

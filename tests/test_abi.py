@@ -87,6 +87,12 @@ def test_bad_arguments_return_status_without_gpu():
     m = _lib.MetaArgs()
     m.B, m.T, m.mode = 1, 8, 7
     assert lib.kd_plan_build(ctypes.byref(m), ctypes.c_void_p(256), null) == _lib.KD_ERR_INVALID
+    t = _lib.TokenArgs()
+    t.B, t.T, t.D, t.rule = 1, 8, 64, 0
+    assert lib.kd_plan_build_tokens(ctypes.byref(t), ctypes.c_void_p(256), null) == _lib.KD_ERR_INVALID  # no tokens
+    t.tokens, t.rule = 64, 9
+    assert lib.kd_plan_build_tokens(ctypes.byref(t), ctypes.c_void_p(256), null) == _lib.KD_ERR_INVALID
+    assert "rule" in lib.kd_last_error_string().decode()
 
 
 def test_python_boundary_validation():

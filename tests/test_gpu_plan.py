@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from kerneldev_amd import build_plan, flash_attention, plan_views
+from kerneldev_amd import build_plan, build_plan_from_tokens, derive_metadata, flash_attention, plan_views
 from kerneldev_amd.attention import mask_mode
 from kerneldev_amd.synth import CONFIG3_LAYOUT, CONFIG4_LAYOUT, cocktail_batch
 from oracle import tilemap
@@ -125,3 +125,63 @@ def test_return_attention_mask_bit_exact(dev, T):
     got = mask.cpu().numpy()
     for h in range(3):
         np.testing.assert_array_equal(got[:, h], ref)
+
+
+def _token_batches():
+    """Well-formed cocktail rows, and random rows over the special ids (nested
+    [SPAN]s, [ES] before [SPAN], several [CLS] / [MASKQ], none at all)."""
+    tokens, _, _, _ = cocktail_batch(3, 1024, CONFIG3_LAYOUT, seed=31)
+    rng = np.random.default_rng(32)
+    rand = rng.choice(np.array([0, 1, 2, 3, 4, 5, 40, 41, 42]), size=(3, 777), p=[.1, .02, .02, .08, .08, .02, .3, .3, .08])
+    rand[2, :] = 50  # no special token at all
+    return [tokens, torch.from_numpy(rand).to(torch.int32)]
+
+
+@pytest.mark.parametrize("rule", ["collate", "fallback", "teacher_forcing"])
+def test_plan_from_tokens_equals_plan_from_metadata(dev, rule):
+    """kd_plan_build_tokens == kd_plan_build(derive_metadata(tokens, rule)), every section."""
+    for tokens in _token_batches():
+        print(f"plan from tokens rule={rule} shape={tuple(tokens.shape)} {tokens.dtype}", flush=True)
+        tk = tokens.to(dev)
+        B, T = tk.shape
+        for D in (64, 128):
+            lens = torch.tensor([T, T // 2, 1][:B], dtype=torch.int32, device=dev)
+            for ln in (None, lens):
+                got = build_plan_from_tokens(tk, D, rule=rule, lens=ln)
+                meta = derive_metadata(tk, rule=rule)
+                want = build_plan(B, T, D, dev, 0, *meta, lens=ln)
+                torch.cuda.synchronize()
+                pg = plan_views(got.tensor, B, T, D)
+                pw = plan_views(want, B, T, D)
+                part = pw["cls"] == 1
+                for key in ("codes", "cls", "nnz", "fwd_list", "fwd_count", "dq_list", "dq_count", "dkdv_list",
+                            "dkdv_count"):
+                    assert torch.equal(pg[key], pw[key]), (rule, D, key)
+                for key in ("qbits", "kbits"):
+                    assert torch.equal(pg[key][part], pw[key][part]), (rule, D, key)
+
+
+def test_flash_attention_with_shared_plan(dev):
+    """flash_attention(plan=...) == flash_attention(metadata) bit for bit, forward and backward."""
+    tokens, in_span, span_id, is_prefix = cocktail_batch(2, 1024, CONFIG3_LAYOUT, seed=33)
+    from kerneldev_amd.synth import qkvdo
+
+    q0, k0, v0, do = (x.to(dev) for x in qkvdo(2, 3, 1024, 64, seed=34))
+    plan = build_plan_from_tokens(tokens.to(dev), 64, rule="collate")
+    meta = [x.to(dev) for x in derive_metadata(tokens.to(dev), rule="collate")]
+    res = []
+    for use_plan in (False, True):
+        q, k, v = (x.detach().requires_grad_(True) for x in (q0, k0, v0))
+        if use_plan:
+            o = flash_attention(q, k, v, plan=plan)
+        else:
+            o = flash_attention(q, k, v, in_span=meta[0], span_id=meta[1], is_prefix=meta[2])
+        o.backward(do)
+        torch.cuda.synchronize()
+        res.append((o.detach(), q.grad, k.grad, v.grad))
+    for x, y in zip(*res):
+        assert torch.equal(x, y)
+    with pytest.raises(ValueError, match="plan replaces"):
+        flash_attention(q0, k0, v0, plan=plan, in_span=meta[0])
+    with pytest.raises(ValueError, match="plan is for"):
+        flash_attention(q0[:, :, :512], k0[:, :, :512], v0[:, :, :512], plan=plan)
