@@ -77,8 +77,8 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
   const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_strides[0] + h * a.v_strides[1];
   const uint32_t vrb = uint32_t(a.v_strides[2]) * 2u;
   const auto rs_q = make_rsrc(qs_base, uint32_t(T) * qrb);
-  const auto rs_k = make_rsrc(ks_base, uint32_t(T) * krb);
-  const auto rs_v = make_rsrc(vg, uint32_t(T) * vrb);
+  const u32x4 rs_k = rsrc_words(ks_base, uint32_t(T) * krb);
+  const u32x4 rs_v = rsrc_words(vg, uint32_t(T) * vrb);
 
   // ---- this lane's query rows, one per 32-row block qb (B operands of S^T,
   // kept in registers): i_lo[qb] + c ----
@@ -108,11 +108,11 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
   // tile e is softmaxed), so they are loaded separately.
   auto load_k = [&](int e) {
     const uint32_t k0 = entry_tile(ent[e]) * 64u;
-    TK::load(rs_k, k0 * krb, koff, s_k[e & 1], wave);
+    TK::load_async(rs_k, k0 * krb, koff, lds_addr(s_k[e & 1]), wave);
   };
   auto load_v = [&](int e) {
     const uint32_t k0 = entry_tile(ent[e]) * 64u;
-    TL::load(rs_v, k0 * vrb, voff, s_v[e & 1], wave);
+    TL::load_async(rs_v, k0 * vrb, voff, lds_addr(s_v[e & 1]), wave);
   };
   // the row masks of a PARTIAL tile for this lane's rows (q-block rows 32 qb
   // apart), fetched one step ahead of their use
@@ -183,6 +183,11 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
     if (n > 1) load_k(1);
     load_bits(0, bits);
     wait_vmem();
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      so[qb].settle();
+      settle(bits[qb]);
+    }
     __syncthreads();
     scores(s_k[0], s);
   }
@@ -190,8 +195,13 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
   for (int e = 0; e < n; ++e) {
     const int buf = e & 1;
     const uint32_t cur = ent[e];
+    // The tile copies are inline asm (see dma_b128), so the compiler sees no
+    // load in flight and places no wait of its own before the LDS reads of
+    // this step: the copies issued below stay in flight for the whole step.
     wait_vmem();
-    __syncthreads();  // V(e) and K(e+1) landed; every wave is done with K(e) and V(e-1)
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) settle(bits[qb]);  // the compiler's wait for the mask load falls here
+    barrier_raw();  // V(e) and K(e+1) landed; every wave is done with K(e) and V(e-1)
     if (e + 1 < n) {
       load_v(e + 1);
       load_bits(e + 1, bits_next);

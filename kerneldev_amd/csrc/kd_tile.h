@@ -17,6 +17,8 @@
 // for D = 64 (8 chunks per 128-byte row, two rows per bank sweep)
 // swz(r) = 4 ((r >> 1) & 1) + ((r >> 2) & 3).
 #pragma once
+#include <type_traits>
+
 #include "kd_internal.h"
 
 namespace kd {
@@ -31,6 +33,29 @@ KD_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 
 KD_DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// make_rsrc's four descriptor words, for the inline-asm loads below
+KD_DEV u32x4 rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  auto u = [](uint32_t x) { return uint32_t(__builtin_amdgcn_readfirstlane(int(x))); };
+  return u32x4{u(uint32_t(a)), u(uint32_t(a >> 32) & 0xFFFFu), u(bytes), 0x00020000u};
+}
+
+// One wave-wide global -> LDS copy of 16 bytes per lane (buffer_load_dwordx4
+// ... lds, LDS address m0 + 16 lane) issued as inline asm.  Through the
+// builtin, the compiler treats LDS as written by a load in flight and makes
+// every later LDS read wait for all outstanding loads (s_waitcnt vmcnt(0)),
+// which drains tile prefetches meant to stay in flight for longer.  Hidden
+// from the compiler, the copies are ordered by the caller: wait_vmem_n /
+// wait_vmem before barrier_raw, and no copy into a slot until every wave has
+// passed the barrier after its last read of that slot.  The s_nop gives the
+// wait states an LDS DMA needs after an SALU write of m0 (1) and after a VALU
+// write (v_readfirstlane) of an SGPR it reads (5), which the compiler's hazard
+// check does not see inside the asm.
+KD_DEV void dma_b128(const u32x4& rs, uint32_t voff, uint32_t m0v) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "s"(m0v)
+               : "memory", "m0");
 }
 
 template <int D, int NW = 4>  // NW: waves that share the copy of one tile
@@ -61,6 +86,14 @@ struct Tile {
       off[j] = uint32_t(r) * row_bytes + uint32_t(chunk) * 16u;
     }
   }
+  // This wave's share of the tile load through dma_b128 (invisible to the
+  // compiler's wait insertion; see there).  lds_tile: LDS byte address.
+  KD_DEV static void load_async(const u32x4& rs, uint32_t tile_off, const uint32_t (&off)[LOADS_PER_WAVE],
+                                uint32_t lds_tile, int wave) {
+    const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_tile + uint32_t(wave * LOADS_PER_WAVE) * 1024u)));
+#pragma unroll
+    for (int j = 0; j < LOADS_PER_WAVE; ++j) dma_b128(rs, off[j] + tile_off, m + uint32_t(j) * 1024u);
+  }
   // Issue this wave's share of the tile load (asynchronous; vmcnt tracks it).
   KD_DEV static void load(__amdgpu_buffer_rsrc_t rs, uint32_t tile_off, const uint32_t (&off)[LOADS_PER_WAVE],
                           uint8_t* lds_tile, int wave) {
@@ -86,6 +119,32 @@ KD_DEV float xhalf_sum(float x) {
 KD_DEV u32x2 ds_read_tr16(const uint8_t* p) {
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4 __attribute__((address_space(3)))*)(p));
   return __builtin_bit_cast(u32x2, v);
+}
+
+// LDS byte address of a pointer into __shared__ memory
+KD_DEV uint32_t lds_addr(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t*)(p)));
+}
+
+// s_barrier without the release/acquire fences of __syncthreads(): those make
+// the compiler wait for every outstanding load first (s_waitcnt vmcnt(0)),
+// including tile loads meant to stay in flight across the barrier.  The caller
+// orders memory itself: it has consumed its own LDS reads and waited (with
+// wait_vmem / wait_vmem_n) for the loads other waves will read.
+KD_DEV void barrier_raw() { asm volatile("s_barrier" ::: "memory"); }
+
+// Ends the compiler's tracking of a load into v: placed where the load is
+// known complete (after wait_vmem), the compiler puts its own wait for it
+// here, and none at later uses.
+template <class T>
+KD_DEV void settle(T& v) { asm volatile("" : "+v"(v)); }
+
+template <int I, int N, class F>
+KD_DEV void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
 }
 
 KD_DEV void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
@@ -127,6 +186,14 @@ struct ScoreOp<E, D, false> {
   KD_DEV void init(int srow, int hf) {
 #pragma unroll
     for (int st = 0; st < NK; ++st) addr[st] = TL::at(srow, 2 * st + hf);
+  }
+  // Call once load_b's loads are known complete (after a wait_vmem): from
+  // here on the compiler treats b as plain registers and places no wait for
+  // them later, where it cannot see that no load is pending (the inline-asm
+  // tile copies are invisible to it, so it would wait for those too).
+  KD_DEV void settle() {
+#pragma unroll
+    for (int st = 0; st < NK; ++st) asm volatile("" : "+v"(b[st]));
   }
   // s += X[32 kb + rows] Y^T
   KD_DEV void mma(const uint8_t* tile, int kb, f32x16& s) const {
@@ -178,6 +245,11 @@ struct ScoreOp<E, D, true> {
       addr[st][1] = TL::at(srow, 4 * st + 2 * hf + 1);
     }
   }
+  KD_DEV void settle() {
+#pragma unroll
+    for (int st = 0; st < NK; ++st) asm volatile("" : "+v"(b[st]));
+  }
+
   KD_DEV void mma(const uint8_t* tile, int kb, f32x16& s) const {
 #pragma unroll
     for (int st = 0; st < NK; ++st) {
