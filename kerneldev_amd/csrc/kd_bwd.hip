@@ -118,6 +118,13 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
   __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][TL::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][TL::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_k8[Q8 ? 2 : 1][Q8 ? TK8::BYTES : 16];
+  // each wave's row masks of a PARTIAL tile, copied by the wave itself into
+  // one of two slots (masks of tile e+1 copied in step e).  The fp8 variant's
+  // tiles fill the 80 KB that two workgroups a CU allow: it loads the masks
+  // into registers instead (the compiler then waits for the tile copies
+  // issued with them at their first use)
+  constexpr bool LDS_BITS = !Q8;
+  __shared__ __attribute__((aligned(256))) uint64_t s_bits[LDS_BITS ? 2 : 1][LDS_BITS ? 4 : 1][32];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
   const int T = a.T, H = a.H;
@@ -134,8 +141,8 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
                  krb = uint32_t(a.k_strides[2]) * 2u, vrb = uint32_t(a.v_strides[2]) * 2u;
   const auto rs_q = make_rsrc(qg, uint32_t(T) * qrb);
   const auto rs_do = make_rsrc(dog, uint32_t(T) * dorb);
-  const auto rs_k = make_rsrc(kg, uint32_t(T) * krb);
-  const auto rs_v = make_rsrc(vg, uint32_t(T) * vrb);
+  const u32x4 rs_k = rsrc_words(kg, uint32_t(T) * krb);
+  const u32x4 rs_v = rsrc_words(vg, uint32_t(T) * vrb);
   const int64_t BHT = int64_t(a.B) * H * T;
 
   const int qrow = qblock * 128 + wave * 32 + c;
@@ -183,6 +190,11 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
   }
   // this wave's rows lie in q-tile 2 qblock + member; its row masks per key tile
   const int member = wave >> 1;
+  // qbits of batch row b: [nT q-tiles][nT key tiles][64 rows]; this wave's 32
+  // rows of key tile 0 start at byte bits_off0 (+ 4 lane: the lane's dword)
+  const u32x4 rs_bits = rsrc_words(qbits + int64_t(b) * nT * nT * 64, uint32_t(nT) * uint32_t(nT) * 512u);
+  const uint32_t bits_off0 =
+      (uint32_t(2 * qblock + member) * uint32_t(nT) * 64u + 32u * uint32_t(wave & 1)) * 8u + uint32_t(lane) * 4u;
   const uint64_t* qbits_row = qbits + (int64_t(b) * nT + 2 * qblock + member) * nT * 64 + 32 * (wave & 1) + c;
 
   const int lbase = b * nQB + qblock;
@@ -193,16 +205,29 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
   TL::load_offsets(wave, lane, krb, koff);
   TL::load_offsets(wave, lane, vrb, voff);
   TK8::load_offsets(wave, lane, uint32_t(D), k8off);
-  const auto rs_k8 = make_rsrc(Q8 ? a.k8 + int64_t(bh) * T * D : nullptr, Q8 ? uint32_t(T) * D : 0u);
+  const u32x4 rs_k8 = rsrc_words(Q8 ? a.k8 + int64_t(bh) * T * D : nullptr, Q8 ? uint32_t(T) * D : 0u);
+  // inline-asm copies (dma_b128): the compiler places no wait for them
+  // before this step's LDS reads, so tile e+1 loads during all of step e
   auto load_tile = [&](int kt, int buf) {
     const uint32_t k0 = uint32_t(kt) * 64u;
-    TL::load(rs_k, k0 * krb, koff, s_k[buf], wave);
-    TL::load(rs_v, k0 * vrb, voff, s_v[buf], wave);
-    if constexpr (Q8) TK8::load(rs_k8, k0 * uint32_t(D), k8off, s_k8[buf], wave);
+    TL::load_async(rs_k, k0 * krb, koff, lds_addr(s_k[buf]), wave);
+    TL::load_async(rs_v, k0 * vrb, voff, lds_addr(s_v[buf]), wave);
+    if constexpr (Q8) TK8::load_async(rs_k8, k0 * uint32_t(D), k8off, lds_addr(s_k8[buf]), wave);
   };
-  // a PARTIAL tile's row mask, fetched one step ahead of its use
-  auto load_bits = [&](int e, uint64_t& bits) {
-    if (entry_class(ent[e], member) == TILE_PARTIAL) bits = qbits_row[int64_t(entry_tile(ent[e])) * 64];
+  // a PARTIAL tile's row masks, copied one step ahead of their use into the
+  // wave's LDS slot (a register load would be waited for by the compiler
+  // together with the tile copies issued after it)
+  uint64_t bits = 0, bits_next = 0;  // the register-mask variant
+  auto load_bits = [&](int e) {
+    const uint32_t en = ent[e];
+    if (entry_class(en, member) == TILE_PARTIAL) {  // wave-uniform
+      if constexpr (LDS_BITS) {
+        const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_bits[e & 1][wave][0]))));
+        dma_b32(rs_bits, bits_off0 + entry_tile(en) * 512u, m);
+      } else {
+        (e == 0 ? bits : bits_next) = qbits_row[int64_t(entry_tile(en)) * 64];
+      }
+    }
   };
 
   const int srow = sigma(c);
@@ -219,20 +244,28 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
 
-  uint64_t bits = 0, bits_next = 0;
   if (n > 0) {
     load_tile(int(entry_tile(ent[0])), 0);
-    load_bits(0, bits);
+    load_bits(0);
   }
+  // every register load of the prologue is complete here: the compiler's
+  // waits for them fall here, none later in the loop (see settle)
+  wait_vmem();
+  so.settle();
+#pragma unroll
+  for (int st = 0; st < DS; ++st) settle(dof[st]);
+  settle(lse);
+  settle(delta);
 
   for (int e = 0; e < n; ++e) {
     const int buf = e & 1;
     const uint32_t cur = ent[e];
     wait_vmem();
-    __syncthreads();
+    if constexpr (!LDS_BITS) settle(bits);
+    barrier_raw();  // tile e (and this wave's masks) landed for every wave; every wave is done with tile e-1
     if (e + 1 < n) {
       load_tile(int(entry_tile(ent[e + 1])), buf ^ 1);
-      load_bits(e + 1, bits_next);
+      load_bits(e + 1);
     }
     const uint8_t* kt = s_k[buf];
     const uint8_t* vt = s_v[buf];
@@ -272,7 +305,8 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
     }
     const uint32_t mcls = entry_class(cur, member);
     if (mcls != TILE_FULL) {  // wave-uniform.  Register r of s[kb] holds key 32 kb + 16 (r / 8) + 8 hf + r % 8
-      const uint64_t rowbits = mcls == TILE_PARTIAL ? bits : 0u;  // EMPTY: nothing allowed
+      uint64_t rowbits = 0;  // EMPTY: nothing allowed
+      if (mcls == TILE_PARTIAL) rowbits = LDS_BITS ? s_bits[LDS_BITS ? buf : 0][LDS_BITS ? wave : 0][c] : bits;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const uint32_t w = uint32_t(rowbits >> (32 * kb)) >> (8 * hf);
@@ -280,6 +314,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
         for (int r = 0; r < 16; ++r) s[kb][r] = mask_bit(s[kb][r], w, 16 * (r >> 3) + (r & 7));
       }
     }
+
     u32x4 dsb[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -315,7 +350,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
       }
       __builtin_amdgcn_sched_barrier(0x406);
     }
-    bits = bits_next;
+    if constexpr (!LDS_BITS) bits = bits_next;
   }
 
   if (qvalid) {
@@ -358,6 +393,8 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   __shared__ __attribute__((aligned(1024))) u32x4 s_p[2][4][4][64];       // [e % 2][pair][k-step][lane]
   __shared__ __attribute__((aligned(256))) float s_lse[NLS][64];
   __shared__ __attribute__((aligned(256))) float s_delta[NDL][64];
+  // each P wave's column masks of a PARTIAL tile, copied with the tile
+  __shared__ __attribute__((aligned(256))) uint64_t s_bits[NLS][4][32];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
   const int pair = wave & 3, role = wave >> 2;
@@ -373,11 +410,11 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_strides[0] + h * a.v_strides[1];
   const uint32_t qrb = uint32_t(a.q_strides[2]) * 2u, dorb = uint32_t(a.do_strides[2]) * 2u,
                  krb = uint32_t(a.k_strides[2]) * 2u, vrb = uint32_t(a.v_strides[2]) * 2u;
-  const auto rs_q = make_rsrc(qg, uint32_t(T) * qrb);
-  const auto rs_do = make_rsrc(dog, uint32_t(T) * dorb);
+  const u32x4 rs_q = rsrc_words(qg, uint32_t(T) * qrb);
+  const u32x4 rs_do = rsrc_words(dog, uint32_t(T) * dorb);
   const int64_t BHT = int64_t(a.B) * H * T;
-  const auto rs_lse = make_rsrc(a.delta + BHT + int64_t(bh) * T, uint32_t(T) * 4u);
-  const auto rs_dl = make_rsrc(a.delta + int64_t(bh) * T, uint32_t(T) * 4u);
+  const u32x4 rs_lse = rsrc_words(a.delta + BHT + int64_t(bh) * T, uint32_t(T) * 4u);
+  const u32x4 rs_dl = rsrc_words(a.delta + int64_t(bh) * T, uint32_t(T) * 4u);
 
   // this lane's key and its B operand: K for the P wave, V for the dS wave
   const int krow = kblock * 128 + pair * 32 + c;
@@ -401,7 +438,10 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   // this pair's keys lie in k-tile 2 kblock + member; the column masks of its
   // PARTIAL tiles give, per key, the allowed queries of a q-tile
   const int member = pair >> 1;
-  const uint64_t* kbits_col = kbits + (int64_t(b) * nT * nT + 2 * kblock + member) * 64 + 32 * (pair & 1) + c;
+  // kbits of batch row b: [nT q-tiles][nT key tiles][64 keys]; this pair's
+  // 32 keys of q-tile 0 start at byte bits_off0 (+ 4 lane: the lane's dword)
+  const u32x4 rs_bits = rsrc_words(kbits + int64_t(b) * nT * nT * 64, uint32_t(nT) * uint32_t(nT) * 512u);
+  const uint32_t bits_off0 = (uint32_t(2 * kblock + member) * 64u + 32u * uint32_t(pair & 1)) * 8u + uint32_t(lane) * 4u;
 
   const int lbase = b * nKB + kblock;
   const int n = count[lbase];
@@ -411,30 +451,33 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   TL::load_offsets(wave, lane, qrb, qoff);
   TL::load_offsets(wave, lane, dorb, dooff);
   TQ8::load_offsets(wave, lane, uint32_t(D), q8off);
-  const auto rs_q8 = make_rsrc(Q8 ? a.q8 + int64_t(bh) * T * D : nullptr, Q8 ? uint32_t(T) * D : 0u);
-  // tile e's copies: NL + NL (+ NL8) buffer loads per wave, + 1 on waves 0 and 1
+  const u32x4 rs_q8 = rsrc_words(Q8 ? a.q8 + int64_t(bh) * T * D : nullptr, Q8 ? uint32_t(T) * D : 0u);
+  // Tile e's copies, all inline asm (dma_b128 / dma_b32: the compiler places
+  // no waits for them, so they stay in flight until wait_tile): first the P
+  // waves' column masks of a PARTIAL tile, then NL + NL (+ NL8) tile loads per
+  // wave, then LSE (wave 4) and Delta (wave 5), one load each.
   auto load_tile = [&](int e) {
-    const uint32_t q0 = entry_tile(ent[e]) * 64u;
-    TL::load(rs_q, q0 * qrb, qoff, s_q[e % NQ], wave);
-    TL::load(rs_do, q0 * dorb, dooff, s_do[e % NDO], wave);
-    if constexpr (Q8) TQ8::load(rs_q8, q0 * uint32_t(D), q8off, s_q8[e % NDO], wave);
-    if (wave == 0)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, (lds_t*)&s_lse[e % NLS][0], 4, (q0 + lane) * 4u, 0, 0, 0);
-    else if (wave == 1)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_dl, (lds_t*)&s_delta[e % NDL][0], 4, (q0 + lane) * 4u, 0, 0, 0);
+    const uint32_t en = ent[e], qt = entry_tile(en), q0 = qt * 64u;
+    if (role == 0 && entry_class(en, member) == TILE_PARTIAL) {  // wave-uniform
+      const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_bits[e % NLS][pair][0]))));
+      dma_b32(rs_bits, bits_off0 + qt * uint32_t(nT) * 512u, m);
+    }
+    TL::load_async(rs_q, q0 * qrb, qoff, lds_addr(s_q[e % NQ]), wave);
+    TL::load_async(rs_do, q0 * dorb, dooff, lds_addr(s_do[e % NDO]), wave);
+    if constexpr (Q8) TQ8::load_async(rs_q8, q0 * uint32_t(D), q8off, lds_addr(s_q8[e % NDO]), wave);
+    if (wave == 4)
+      dma_b32(rs_lse, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_lse[e % NLS][0])))));
+    else if (wave == 5)
+      dma_b32(rs_dl, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_delta[e % NDL][0])))));
   };
   // Wait until tile e's loads (and older ones) have landed while tile e+1's,
   // issued last, may still be in flight: vector memory loads retire in order.
+  // (A mask copy precedes the tile loads, so it is never among the last.)
   constexpr int NTL = 2 * NL + (Q8 ? NL8 : 0);
   auto wait_tile = [&](bool next_in_flight) {
     if (!next_in_flight) wait_vmem();
-    else if (wave < 2) wait_vmem_n<NTL + 1>();
+    else if (wave == 4 || wave == 5) wait_vmem_n<NTL + 1>();
     else wait_vmem_n<NTL>();
-  };
-  // a PARTIAL tile's column mask (P waves only), fetched one step ahead of its use
-  auto load_bits = [&](int e, uint64_t& bits) {
-    if (role == 0 && entry_class(ent[e], member) == TILE_PARTIAL)
-      bits = kbits_col[int64_t(entry_tile(ent[e])) * nT * 64];
   };
 
   const int srow = sigma(c);
@@ -497,11 +540,13 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
     __builtin_amdgcn_sched_barrier(0x406);
   };
 
-  uint64_t bits = 0, bits_next = 0;
-  if (n > 0) {
-    load_bits(0, bits);
-    load_tile(0);
-  }
+  if (n > 0) load_tile(0);
+  // the B operand's register loads are complete here: the compiler's wait
+  // for them falls here, not at their first use (where it would also wait
+  // for the copies of tile 1)
+  wait_vmem();
+#pragma unroll
+  for (int st = 0; st < DS; ++st) settle(bf[st]);
   for (int e = 1; e < PD && e < n; ++e) load_tile(e);
   // S of tile e (P waves), or dP of tile e carried into step e + 1 (dS
   // waves): one register set for both roles
@@ -510,8 +555,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   for (int e = 0; e <= n; ++e) {
     // tiles up to e landed (tile e + PD - 1 may be in flight when PD = 2)
     wait_tile(PD == 2 && e + 1 < n);
-    __syncthreads();  // tile e landed, P(e-1) written; P(e-2) and the slots of tile e+PD released
-    if (e + 1 < n) load_bits(e + 1, bits_next);  // issued before the tile loads (see wait_tile)
+    barrier_lds();  // tile e landed, P(e-1) written; P(e-2) and the slots of tile e+PD released
     if (e + PD < n) load_tile(e + PD);
     const int pb = e & 1;
     if (role == 0) {
@@ -540,7 +584,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
         }
         const uint32_t mcls = entry_class(ent[e], member);
         if (mcls != TILE_FULL) {  // wave-uniform
-          const uint64_t colbits = mcls == TILE_PARTIAL ? bits : 0u;  // EMPTY: nothing allowed
+          const uint64_t colbits = mcls == TILE_PARTIAL ? s_bits[e % NLS][pair][c] : 0u;  // EMPTY: nothing allowed
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
             const uint32_t w = uint32_t(colbits >> (32 * qb)) >> (8 * hf);
@@ -592,7 +636,6 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
       }
       if (e < n) rows_times_b(s_do[e % NDO], x);  // dP of tile e
     }
-    bits = bits_next;
   }
 
   if (kvalid) {

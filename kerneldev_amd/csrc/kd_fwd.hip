@@ -56,6 +56,8 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
   constexpr int NLK = TK::LOADS_PER_WAVE;
   __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][TK::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][TL::BYTES];
+  // each wave's row masks of a PARTIAL tile (copied by the wave itself)
+  __shared__ __attribute__((aligned(256))) uint64_t s_bits[2][NW][32 * QB];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
   const int T = a.T, H = a.H;
@@ -95,7 +97,11 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
   }
   // this wave's rows lie in q-tile 2 qblock + member of the block (group of 2)
   const int member = (wave * QB) >> 1;
-  const uint64_t* qbits_row = qbits + (int64_t(b) * nT + 2 * qblock + member) * nT * 64 + 32 * ((wave * QB) & 1) + c;
+  // qbits of batch row b: [nT q-tiles][nT key tiles][64 rows]; this wave's
+  // 32 QB rows of key tile 0 start at byte bits_off0 (+ 4 lane: the lane's dword)
+  const u32x4 rs_bits = rsrc_words(qbits + int64_t(b) * nT * nT * 64, uint32_t(nT) * uint32_t(nT) * 512u);
+  const uint32_t bits_off0 = (uint32_t(2 * qblock + member) * uint32_t(nT) * 64u + 32u * uint32_t((wave * QB) & 1)) * 8u +
+                             uint32_t(lane) * 4u;
 
   const int lbase = b * nQB + qblock;
   const int n = count[lbase];
@@ -114,14 +120,15 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
     const uint32_t k0 = entry_tile(ent[e]) * 64u;
     TL::load_async(rs_v, k0 * vrb, voff, lds_addr(s_v[e & 1]), wave);
   };
-  // the row masks of a PARTIAL tile for this lane's rows (q-block rows 32 qb
-  // apart), fetched one step ahead of their use
-  auto load_bits = [&](int e, uint64_t (&bits)[QB]) {
+  // the row masks of this wave's rows in a PARTIAL tile, copied to the
+  // wave's own LDS slot one step ahead of their use (a register load would
+  // be waited for by the compiler, together with the tile copies after it)
+  auto load_bits = [&](int e) {
     const uint32_t en = ent[e];
     if (entry_class(en, member) == TILE_PARTIAL) {  // wave-uniform
-      const uint64_t* p = qbits_row + int64_t(entry_tile(en)) * 64;
+      const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_bits[e & 1][wave][0]))));
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) bits[qb] = p[32 * qb];
+      for (int qb = 0; qb < QB; ++qb) dma_b32(rs_bits, bits_off0 + entry_tile(en) * 512u + 256u * qb, m + 256u * qb);
     }
   };
 
@@ -174,20 +181,14 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
   }
 
   f32x16 s[2][QB];
-  uint64_t bits[QB], bits_next[QB];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) bits[qb] = bits_next[qb] = 0;
   if (n > 0) {
     load_k(0);
     load_v(0);
     if (n > 1) load_k(1);
-    load_bits(0, bits);
+    load_bits(0);
     wait_vmem();
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      so[qb].settle();
-      settle(bits[qb]);
-    }
+    for (int qb = 0; qb < QB; ++qb) so[qb].settle();  // the compiler's wait for the Q rows falls here
     __syncthreads();
     scores(s_k[0], s);
   }
@@ -199,12 +200,10 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
     // load in flight and places no wait of its own before the LDS reads of
     // this step: the copies issued below stay in flight for the whole step.
     wait_vmem();
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) settle(bits[qb]);  // the compiler's wait for the mask load falls here
-    barrier_raw();  // V(e) and K(e+1) landed; every wave is done with K(e) and V(e-1)
+    barrier_raw();  // V(e), K(e+1) and the masks landed; every wave is done with K(e) and V(e-1)
     if (e + 1 < n) {
       load_v(e + 1);
-      load_bits(e + 1, bits_next);
+      load_bits(e + 1);
     }
     if (e + 2 < n) load_k(e + 2);
 
@@ -213,7 +212,7 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
       // of the tile: bit 16 (r / 8) + r % 8 of word kb of the row mask shifted by 8 hf
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
-        const uint64_t rowbits = mcls == TILE_PARTIAL ? bits[qb] : 0u;  // EMPTY: nothing allowed
+        const uint64_t rowbits = mcls == TILE_PARTIAL ? s_bits[buf][wave][32 * qb + c] : 0u;  // EMPTY: nothing allowed
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
           const uint32_t w = uint32_t(rowbits >> (32 * kb)) >> (8 * hf);
@@ -297,8 +296,6 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
       }
       __builtin_amdgcn_sched_barrier(0x406);
     }
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) bits[qb] = bits_next[qb];
   }
 
   // ---- epilogue: normalise, store O and LSE ----

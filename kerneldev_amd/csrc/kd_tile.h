@@ -126,12 +126,21 @@ KD_DEV uint32_t lds_addr(const void* p) {
   return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t*)(p)));
 }
 
+// dma_b128's 4-byte form: lane i copies 4 bytes to LDS address m0 + 4 i
+KD_DEV void dma_b32(const u32x4& rs, uint32_t voff, uint32_t m0v) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "s"(m0v)
+               : "memory", "m0");
+}
+
 // s_barrier without the release/acquire fences of __syncthreads(): those make
 // the compiler wait for every outstanding load first (s_waitcnt vmcnt(0)),
 // including tile loads meant to stay in flight across the barrier.  The caller
 // orders memory itself: it has consumed its own LDS reads and waited (with
 // wait_vmem / wait_vmem_n) for the loads other waves will read.
 KD_DEV void barrier_raw() { asm volatile("s_barrier" ::: "memory"); }
+// barrier_raw that first completes this wave's LDS writes (s_waitcnt
+// lgkmcnt(0)), for steps where waves hand data to each other through LDS
+KD_DEV void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Ends the compiler's tracking of a load into v: placed where the load is
 // known complete (after wait_vmem), the compiler puts its own wait for it
