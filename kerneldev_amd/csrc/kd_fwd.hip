@@ -170,12 +170,12 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
   // the fp8 product carries the dequantisation scales of Q and K
   const float sl2 = a.sm_scale * 1.4426950408889634f * (Q8 ? a.q_scale[bh] * a.k_scale[bh] : 1.f);
   const float NEG_INF = -__builtin_inff();
-  float m_ref[QB], l0[QB], l1[QB], le0[QB], le1[QB];
+  float m_ref[QB], l0[QB], l1[QB];
   f32x16 o[QB][DB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     m_ref[qb] = NEG_INF;
-    l0[qb] = l1[qb] = le0[qb] = le1[qb] = 0.f;
+    l0[qb] = l1[qb] = 0.f;
 #pragma unroll
     for (int db = 0; db < DB; ++db) o[qb][db] = f32x16{};
   }
@@ -237,8 +237,6 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
         m_ref[qb] = m_new;
         l0[qb] *= alpha;
         l1[qb] *= alpha;
-        le0[qb] *= alpha;
-        le1[qb] *= alpha;
 #pragma unroll
         for (int db = 0; db < DB; ++db) o[qb][db] *= alpha;
       }
@@ -255,11 +253,6 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
         float p[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(s[kb][qb][r], sl2, -ms[qb]));
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-          le0[qb] += p[r];
-          le1[qb] += p[r + 1];
-        }
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           pk[qb][kb][t] = u32x4{pack2<E>(p[8 * t + 0], p[8 * t + 1]), pack2<E>(p[8 * t + 2], p[8 * t + 3]),
@@ -299,13 +292,12 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
   }
 
   // ---- epilogue: normalise, store O and LSE ----
-  // O is normalised by the sum of the ROUNDED P that entered P V (exact
-  // convex weights); LSE by the exact fp32 sum, which is what the backward's
-  // recomputed P = exp2(S c - LSE) must sum to
+  // O and LSE use the row sum of the ROUNDED P that entered P V (summed two
+  // at a time by v_dot2c): O's weights then sum to exactly 1, and the sum
+  // costs half an instruction per score instead of one fp32 add
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const float l_tot = xhalf_sum(l0[qb] + l1[qb]);
-    const float l_exact = xhalf_sum(le0[qb] + le1[qb]);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     if (qvalid[qb]) {
       const int row = qrow[qb];
@@ -332,7 +324,7 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
         }
       }
       if (a.lse != nullptr && hf == 0)
-        a.lse[int64_t(bh) * T + row] = l_exact > 0.f ? m_ref[qb] * sl2 + fast_log2(l_exact) : NEG_INF;
+        a.lse[int64_t(bh) * T + row] = l_tot > 0.f ? m_ref[qb] * sl2 + fast_log2(l_tot) : NEG_INF;
     }
   }
 }
