@@ -112,21 +112,22 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
   TL::load_offsets(wave, lane, vrb, voff);
   // K tiles run one step ahead of V tiles (S of tile e+1 is computed while
   // tile e is softmaxed), so they are loaded separately.
-  auto load_k = [&](int e) {
+  // slot = e & 1 (passed as a constant by the unrolled loop)
+  auto load_k = [&](int e, int slot) {
     const uint32_t k0 = entry_tile(ent[e]) * 64u;
-    TK::load_async(rs_k, k0 * krb, koff, lds_addr(s_k[e & 1]), wave);
+    TK::load_async(rs_k, k0 * krb, koff, lds_addr(s_k[slot]), wave);
   };
-  auto load_v = [&](int e) {
+  auto load_v = [&](int e, int slot) {
     const uint32_t k0 = entry_tile(ent[e]) * 64u;
-    TL::load_async(rs_v, k0 * vrb, voff, lds_addr(s_v[e & 1]), wave);
+    TL::load_async(rs_v, k0 * vrb, voff, lds_addr(s_v[slot]), wave);
   };
   // the row masks of this wave's rows in a PARTIAL tile, copied to the
   // wave's own LDS slot one step ahead of their use (a register load would
   // be waited for by the compiler, together with the tile copies after it)
-  auto load_bits = [&](int e) {
+  auto load_bits = [&](int e, int slot) {
     const uint32_t en = ent[e];
     if (entry_class(en, member) == TILE_PARTIAL) {  // wave-uniform
-      const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_bits[e & 1][wave][0]))));
+      const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_bits[slot][wave][0]))));
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) dma_b32(rs_bits, bits_off0 + entry_tile(en) * 512u + 256u * qb, m + 256u * qb);
     }
@@ -182,10 +183,10 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
 
   f32x16 s[2][QB];
   if (n > 0) {
-    load_k(0);
-    load_v(0);
-    if (n > 1) load_k(1);
-    load_bits(0);
+    load_k(0, 0);
+    load_v(0, 0);
+    if (n > 1) load_k(1, 1);
+    load_bits(0, 0);
     wait_vmem();
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) so[qb].settle();  // the compiler's wait for the Q rows falls here
@@ -193,8 +194,10 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
     scores(s_k[0], s);
   }
 
-  for (int e = 0; e < n; ++e) {
-    const int buf = e & 1;
+  // One step per key tile; unrolled by two so that the buffer of each step is
+  // a constant and every LDS address is a fixed register plus an immediate.
+  auto step = [&](const int e, auto buf_c) {
+    constexpr int buf = decltype(buf_c)::value;  // == e & 1
     const uint32_t cur = ent[e];
     // The tile copies are inline asm (see dma_b128), so the compiler sees no
     // load in flight and places no wait of its own before the LDS reads of
@@ -202,10 +205,10 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
     wait_vmem();
     barrier_raw();  // V(e), K(e+1) and the masks landed; every wave is done with K(e) and V(e-1)
     if (e + 1 < n) {
-      load_v(e + 1);
-      load_bits(e + 1);
+      load_v(e + 1, buf ^ 1);
+      load_bits(e + 1, buf ^ 1);
     }
-    if (e + 2 < n) load_k(e + 2);
+    if (e + 2 < n) load_k(e + 2, buf);
 
     const uint32_t mcls = entry_class(cur, member);
     if (mcls != TILE_FULL) {  // wave-uniform.  Register r of s[kb][qb] holds key 32 kb + 16 (r / 8) + 8 hf + r % 8
@@ -289,6 +292,10 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
       }
       __builtin_amdgcn_sched_barrier(0x406);
     }
+  };
+  for (int e = 0; e < n; e += 2) {
+    step(e, std::integral_constant<int, 0>{});
+    if (e + 1 < n) step(e + 1, std::integral_constant<int, 1>{});
   }
 
   // ---- epilogue: normalise, store O and LSE ----
