@@ -218,11 +218,11 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
   // wave's LDS slot (a register load would be waited for by the compiler
   // together with the tile copies issued after it)
   uint64_t bits = 0, bits_next = 0;  // the register-mask variant
-  auto load_bits = [&](int e) {
+  auto load_bits = [&](int e, int slot) {  // slot = e & 1
     const uint32_t en = ent[e];
     if (entry_class(en, member) == TILE_PARTIAL) {  // wave-uniform
       if constexpr (LDS_BITS) {
-        const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_bits[e & 1][wave][0]))));
+        const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_bits[slot][wave][0]))));
         dma_b32(rs_bits, bits_off0 + entry_tile(en) * 512u, m);
       } else {
         (e == 0 ? bits : bits_next) = qbits_row[int64_t(entry_tile(en)) * 64];
@@ -246,7 +246,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
 
   if (n > 0) {
     load_tile(int(entry_tile(ent[0])), 0);
-    load_bits(0);
+    load_bits(0, 0);
   }
   // every register load of the prologue is complete here: the compiler's
   // waits for them fall here, none later in the loop (see settle)
@@ -257,15 +257,17 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
   settle(lse);
   settle(delta);
 
-  for (int e = 0; e < n; ++e) {
-    const int buf = e & 1;
+  // One step per key tile; unrolled by two so that the buffer of each step is
+  // a constant and every LDS address is a fixed register plus an immediate.
+  auto step = [&](const int e, auto buf_c) {
+    constexpr int buf = decltype(buf_c)::value;  // == e & 1
     const uint32_t cur = ent[e];
     wait_vmem();
     if constexpr (!LDS_BITS) settle(bits);
     barrier_raw();  // tile e (and this wave's masks) landed for every wave; every wave is done with tile e-1
     if (e + 1 < n) {
       load_tile(int(entry_tile(ent[e + 1])), buf ^ 1);
-      load_bits(e + 1);
+      load_bits(e + 1, buf ^ 1);
     }
     const uint8_t* kt = s_k[buf];
     const uint8_t* vt = s_v[buf];
@@ -275,7 +277,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
     // sched_barriers keep LDS reads and MFMAs in that order
     f32x16 s[2], dp[2];
     {
-      const uint8_t* st_tile = Q8 ? s_k8[buf & (Q8 ? 1 : 0)] : kt;
+      const uint8_t* st_tile = Q8 ? s_k8[Q8 ? buf : 0] : kt;
       constexpr int NS = 2 * SO::NK, PF = DQ_PF < NS ? DQ_PF : NS;
       typename SO::A av[PF];
 #pragma unroll
@@ -351,6 +353,10 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
       __builtin_amdgcn_sched_barrier(0x406);
     }
     if constexpr (!LDS_BITS) bits = bits_next;
+  };
+  for (int e = 0; e < n; e += 2) {
+    step(e, std::integral_constant<int, 0>{});
+    if (e + 1 < n) step(e + 1, std::integral_constant<int, 1>{});
   }
 
   if (qvalid) {
