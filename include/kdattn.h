@@ -132,6 +132,35 @@ typedef struct kd_quant_args {
   int32_t pad_;
 } kd_quant_args;
 
+/* Cocktail-party head (model.py:263-298): per row, the hidden state at the
+ * first [MASK] (h_ctx, zero if none) is scored against the mean hidden state
+ * of each span's interior.  The j-th [SPAN] of a row pairs with the row's
+ * j-th [ES] (the reference zips the two position lists, :287-291); the
+ * interior is [pos([SPAN]_j) + 1, pos([ES]_j)), and a pair without a partner
+ * or with an empty interior scores 0 (the reference's zero h_spans row,
+ * :285, :292).  kd_span_scores fills the forward outputs; kd_span_scores_bwd
+ * turns d scores into d h, reading the forward's outputs. */
+typedef struct kd_span_args {
+  const void *tokens;       /* int64 or int32 [B, T] (ids of data_builder.py:44-52) */
+  int64_t tokens_strides[2];
+  int32_t tokens_dtype;     /* KD_I64 / KD_I32 */
+  int32_t dtype;            /* KD_BF16 / KD_F16: h and dh */
+  const void *h;            /* [B, T, D] hidden states, unit d stride */
+  int64_t h_strides[2];     /* (b, t) in elements */
+  int32_t B, T, D;
+  int32_t n_spans;          /* score columns, 1 .. 8192; the reference's max_spans = the
+                               largest per-row [SPAN] count (spans past n_spans are dropped) */
+  float *scores;            /* out [B, n_spans] */
+  float *h_ctx;             /* out [B, D] */
+  float *h_spans;           /* out [B, n_spans, D] span means (0 where none) */
+  int32_t *span_lo;         /* out [B, n_spans]: interior [lo, hi); lo == hi where none */
+  int32_t *span_hi;
+  int32_t *mask_pos;        /* out [B]: first [MASK] position or -1 */
+  const float *dscores;     /* bwd in [B, n_spans] */
+  void *dh;                 /* bwd out [B, T, D] (dtype), every element written */
+  int64_t dh_strides[2];    /* (b, t) in elements, unit d stride */
+} kd_span_args;
+
 /* Library version (major*10000 + minor*100 + patch). */
 int kd_version(void);
 
@@ -212,6 +241,18 @@ int kd_hadamard(const kd_rot_args *a, void *stream);
  * attention kernels (kd_attn_args.q8 / k8).  No counterpart in the reference,
  * which has no fp8 path; the operation is specified by the build. */
 int kd_quant_fp8(const kd_quant_args *a, void *stream);
+
+/* Cocktail-party head forward: span_lo/hi, mask_pos, h_ctx, h_spans and
+ * scores.  Replaces the Python double loop and einsum of GPTModel.forward
+ * (model.py:263-298). */
+int kd_span_scores(const kd_span_args *a, void *stream);
+
+/* Its backward: dh = d scores / d h times dscores, from the forward's
+ * span_lo/hi, mask_pos, h_ctx and h_spans (the autograd of model.py:287-296). */
+int kd_span_scores_bwd(const kd_span_args *a, void *stream);
+
+/* sizeof(kd_span_args), for binding checks. */
+void kd_struct_sizes4(size_t *span);
 
 #ifdef __cplusplus
 }

@@ -90,6 +90,19 @@ class QuantArgs(ctypes.Structure):
     ]
 
 
+class SpanArgs(ctypes.Structure):
+    """Mirror of ``kd_span_args``."""
+
+    _fields_ = [
+        ("tokens", c_void_p), ("tokens_strides", c_int64 * 2), ("tokens_dtype", c_int32), ("dtype", c_int32),
+        ("h", c_void_p), ("h_strides", c_int64 * 2),
+        ("B", c_int32), ("T", c_int32), ("D", c_int32), ("n_spans", c_int32),
+        ("scores", c_void_p), ("h_ctx", c_void_p), ("h_spans", c_void_p),
+        ("span_lo", c_void_p), ("span_hi", c_void_p), ("mask_pos", c_void_p),
+        ("dscores", c_void_p), ("dh", c_void_p), ("dh_strides", c_int64 * 2),
+    ]
+
+
 # name -> (restype, argtypes); every symbol include/kdattn.h declares
 SIGNATURES = {
     "kd_version": (c_int, []),
@@ -97,6 +110,9 @@ SIGNATURES = {
     "kd_struct_sizes": (None, [POINTER(c_size_t), POINTER(c_size_t)]),
     "kd_struct_sizes2": (None, [POINTER(c_size_t), POINTER(c_size_t)]),
     "kd_struct_sizes3": (None, [POINTER(c_size_t)]),
+    "kd_struct_sizes4": (None, [POINTER(c_size_t)]),
+    "kd_span_scores": (c_int, [POINTER(SpanArgs), c_void_p]),
+    "kd_span_scores_bwd": (c_int, [POINTER(SpanArgs), c_void_p]),
     "kd_plan_build_tokens": (c_int, [POINTER(TokenArgs), c_void_p, c_void_p]),
     "kd_hadamard": (c_int, [POINTER(RotArgs), c_void_p]),
     "kd_quant_fp8": (c_int, [POINTER(QuantArgs), c_void_p]),
@@ -138,15 +154,17 @@ def load():
     lib.kd_struct_sizes(ctypes.byref(ms), ctypes.byref(as_))
     rs, qs = c_size_t(), c_size_t()
     lib.kd_struct_sizes2(ctypes.byref(rs), ctypes.byref(qs))
-    ts = c_size_t()
+    ts, ss = c_size_t(), c_size_t()
     lib.kd_struct_sizes3(ctypes.byref(ts))
+    lib.kd_struct_sizes4(ctypes.byref(ss))
     if (ms.value != ctypes.sizeof(MetaArgs) or as_.value != ctypes.sizeof(AttnArgs)
             or rs.value != ctypes.sizeof(RotArgs) or qs.value != ctypes.sizeof(QuantArgs)
-            or ts.value != ctypes.sizeof(TokenArgs)):
+            or ts.value != ctypes.sizeof(TokenArgs) or ss.value != ctypes.sizeof(SpanArgs)):
         raise ImportError(
-            f"struct layout mismatch: C meta={ms.value} attn={as_.value} rot={rs.value} quant={qs.value}, "
-            f"ctypes meta={ctypes.sizeof(MetaArgs)} attn={ctypes.sizeof(AttnArgs)} "
-            f"rot={ctypes.sizeof(RotArgs)} quant={ctypes.sizeof(QuantArgs)}")
+            f"struct layout mismatch: C meta={ms.value} attn={as_.value} rot={rs.value} quant={qs.value} "
+            f"tokens={ts.value} span={ss.value}, ctypes meta={ctypes.sizeof(MetaArgs)} "
+            f"attn={ctypes.sizeof(AttnArgs)} rot={ctypes.sizeof(RotArgs)} quant={ctypes.sizeof(QuantArgs)} "
+            f"tokens={ctypes.sizeof(TokenArgs)} span={ctypes.sizeof(SpanArgs)}")
     _lib = lib
     return lib
 

@@ -506,7 +506,8 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   constexpr int PF = DKDV_PF;
   // acc^T += A^T bop over the 64 queries of a tile (k-steps k4 = 2 qb + t),
   // A^T read transposed from tile `at`; steps i = 4 k4 ... ordered (k4, db)
-  auto accumulate = [&](const uint8_t* at, const u32x4 (&bop)[2][2]) {
+  auto accumulate = [&](const uint8_t* at_g, const u32x4 (&bop)[2][2]) {
+    lds_u8* at = to_lds(at_g);
     constexpr int NS = 4 * DB;
     auto read = [&](int i) {
       const int k4 = i / DB, db = i % DB, off = k4 * 16 * TL::ROWB;
@@ -528,10 +529,11 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   };
   // x[qb] += (rows of tile `ar`) B^T; register r of x[qb] holds query
   // 32 qb + 16 (r / 8) + 8 hf + r % 8 of this lane's key; steps i = (st, qb)
-  auto rows_times_b = [&](const uint8_t* ar, f32x16 (&x)[2]) {
+  auto rows_times_b = [&](const uint8_t* ar_g, f32x16 (&x)[2]) {
+    lds_u8* ar = to_lds(ar_g);
     constexpr int NS = 2 * DS;
     auto read = [&](int i) {
-      return *reinterpret_cast<const u32x4*>(ar + raddr[i >> 1] + (i & 1) * 32 * TL::ROWB);
+      return ds_read16(ar + raddr[i >> 1] + (i & 1) * 32 * TL::ROWB);
     };
     u32x4 av[PF];
 #pragma unroll

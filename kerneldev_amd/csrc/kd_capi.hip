@@ -72,11 +72,24 @@ int check_common(const kd_attn_args* a) {
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+int check_span(const kd_span_args* a) {
+  if (a == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
+  if (a->B < 1 || a->T < 1 || a->D < 1) return fail(KD_ERR_INVALID, "B, T and D must be >= 1");
+  if (a->B > 65535) return fail(KD_ERR_UNSUPPORTED, "B must be <= 65535");
+  if (a->n_spans < 1 || a->n_spans > 8192) return fail(KD_ERR_UNSUPPORTED, "n_spans must be in 1 .. 8192");
+  if (a->dtype != KD_BF16 && a->dtype != KD_F16) return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16 or fp16");
+  if (a->tokens_dtype != KD_I64 && a->tokens_dtype != KD_I32) return fail(KD_ERR_INVALID, "bad tokens dtype");
+  if (a->tokens == nullptr || a->h == nullptr) return fail(KD_ERR_INVALID, "tokens and h are required");
+  if (a->tokens_strides[0] < 0 || a->tokens_strides[1] < 0) return fail(KD_ERR_INVALID, "negative token strides");
+  if (a->h_strides[0] < 0 || a->h_strides[1] < a->D) return fail(KD_ERR_INVALID, "bad h strides");
+  return KD_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
-int kd_version(void) { return 200; }
+int kd_version(void) { return 201; }
 
 const char* kd_last_error_string(void) { return g_err.c_str(); }
 
@@ -92,6 +105,31 @@ void kd_struct_sizes2(size_t* rot, size_t* quant) {
 
 void kd_struct_sizes3(size_t* tokens) {
   if (tokens) *tokens = sizeof(kd_token_args);
+}
+
+void kd_struct_sizes4(size_t* span) {
+  if (span) *span = sizeof(kd_span_args);
+}
+
+int kd_span_scores(const kd_span_args* a, void* stream) {
+  int r;
+  if ((r = check_span(a))) return r;
+  if (a->scores == nullptr || a->h_ctx == nullptr || a->h_spans == nullptr || a->span_lo == nullptr ||
+      a->span_hi == nullptr || a->mask_pos == nullptr)
+    return fail(KD_ERR_INVALID, "scores, h_ctx, h_spans, span_lo, span_hi and mask_pos are required");
+  r = kd::launch_span(*a, as_stream(stream));
+  return r ? fail(r, "kernel launch failed (span scores)") : KD_OK;
+}
+
+int kd_span_scores_bwd(const kd_span_args* a, void* stream) {
+  int r;
+  if ((r = check_span(a))) return r;
+  if (a->dscores == nullptr || a->h_ctx == nullptr || a->h_spans == nullptr || a->span_lo == nullptr ||
+      a->span_hi == nullptr || a->mask_pos == nullptr || a->dh == nullptr)
+    return fail(KD_ERR_INVALID, "dscores, h_ctx, h_spans, span_lo, span_hi, mask_pos and dh are required");
+  if (a->dh_strides[0] < 0 || a->dh_strides[1] < a->D) return fail(KD_ERR_INVALID, "bad dh strides");
+  r = kd::launch_span_bwd(*a, as_stream(stream));
+  return r ? fail(r, "kernel launch failed (span scores backward)") : KD_OK;
 }
 
 int kd_plan_build_tokens(const kd_token_args* t, void* plan, void* stream) {

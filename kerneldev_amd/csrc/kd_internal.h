@@ -46,6 +46,8 @@ int launch_dq(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_
 int launch_dkdv(const AttnArgs& a, const uint8_t* plan, hipStream_t st);
 int launch_hadamard(const kd_rot_args& a, hipStream_t st);
 int launch_quant(const kd_quant_args& a, hipStream_t st);
+int launch_span(const kd_span_args& a, hipStream_t st);
+int launch_span_bwd(const kd_span_args& a, hipStream_t st);
 
 // Linear workgroup id -> work index so that each XCD (workgroups are dealt
 // round-robin over the 8 XCDs) receives one contiguous range of work items,

@@ -1,0 +1,174 @@
+// Cocktail-party head on gfx950: first-[MASK] context vector, span-interior
+// means and their scores (model.py:263-298), forward and backward.
+//
+// The reference builds h_spans with a Python double loop over rows and over
+// the zipped [SPAN] / [ES] position lists, taking x_embed[i, st+1:ed].mean(0)
+// when st + 1 < ed (model.py:287-293), and scores each span by its dot
+// product with the hidden state at the row's first [MASK] (:264-270, :296).
+// Here one workgroup per row finds the positions (block scans give the j-th
+// [SPAN] and the j-th [ES] of the row), one workgroup per (row, span) sums the
+// interior in fp32 in ascending position order, and the backward spreads
+// d score over the interior rows and the [MASK] row in a fixed order, so the
+// results are deterministic.
+#include "kd_internal.h"
+
+namespace kd {
+
+namespace {
+
+constexpr int TOK_MASK = 2, TOK_SPAN = 3, TOK_ES = 4;  // data_builder.py:44-52
+
+KD_DEV int64_t token_at(const kd_span_args& a, int b, int t) {
+  const int64_t off = int64_t(b) * a.tokens_strides[0] + int64_t(t) * a.tokens_strides[1];
+  return a.tokens_dtype == KD_I64 ? static_cast<const int64_t*>(a.tokens)[off]
+                                  : int64_t(static_cast<const int32_t*>(a.tokens)[off]);
+}
+
+template <class E>
+KD_DEV float h_at(const kd_span_args& a, int b, int t, int d) {
+  const uint16_t* p = static_cast<const uint16_t*>(a.h) + int64_t(b) * a.h_strides[0] + int64_t(t) * a.h_strides[1] + d;
+  return to_f32<E>(*p);
+}
+
+// Inclusive block scan of one int per thread (16 waves of 64 = 1024 threads).
+KD_DEV int block_scan(int v, int* s_warp) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(v, o, 64);
+    if (lane >= o) v += u;
+  }
+  if (lane == 63) s_warp[wave] = v;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += s_warp[w];
+  __syncthreads();
+  return v + base;
+}
+
+// One workgroup (1024 threads) per row: positions of the j-th [SPAN] and the
+// j-th [ES], then the interiors [lo, hi) of the zipped pairs and the first [MASK].
+__global__ __launch_bounds__(1024) void k_span_find(kd_span_args a) {
+  extern __shared__ int s_pos[];  // [0, n): j-th [SPAN] position, [n, 2n): j-th [ES] position
+  __shared__ int s_warp[16];
+  __shared__ int s_mask;
+  const int b = blockIdx.x, n = a.n_spans, T = a.T;
+  for (int j = threadIdx.x; j < 2 * n; j += blockDim.x) s_pos[j] = -1;
+  if (threadIdx.x == 0) s_mask = T;
+  __syncthreads();
+  // contiguous chunk of positions per thread, so ordinals follow position order
+  const int per = (T + blockDim.x - 1) / blockDim.x;
+  const int t0 = threadIdx.x * per, t1 = min(T, t0 + per);
+  int ns = 0, ne = 0, first_mask = T;
+  for (int t = t0; t < t1; ++t) {
+    const int64_t tok = token_at(a, b, t);
+    ns += tok == TOK_SPAN;
+    ne += tok == TOK_ES;
+    if (tok == TOK_MASK && first_mask == T) first_mask = t;
+  }
+  const int js = block_scan(ns, s_warp) - ns;  // exclusive: ordinal of this chunk's first [SPAN]
+  const int je = block_scan(ne, s_warp) - ne;
+  if (first_mask < T) atomicMin(&s_mask, first_mask);
+  int cs = js, ce = je;
+  for (int t = t0; t < t1; ++t) {
+    const int64_t tok = token_at(a, b, t);
+    if (tok == TOK_SPAN) {
+      if (cs < n) s_pos[cs] = t;  // spans past n_spans are dropped
+      ++cs;
+    } else if (tok == TOK_ES) {
+      if (ce < n) s_pos[n + ce] = t;
+      ++ce;
+    }
+  }
+  __syncthreads();
+  for (int j = threadIdx.x; j < n; j += blockDim.x) {
+    const int st = s_pos[j], ed = s_pos[n + j];
+    const bool ok = st >= 0 && ed >= 0 && st + 1 < ed;  // zip pairs only; `if st + 1 < ed` (model.py:292)
+    a.span_lo[int64_t(b) * n + j] = ok ? st + 1 : 0;
+    a.span_hi[int64_t(b) * n + j] = ok ? ed : 0;
+  }
+  if (threadIdx.x == 0) a.mask_pos[b] = s_mask < T ? s_mask : -1;
+}
+
+// Fixed-order block sum (256 threads) of one float per thread.
+KD_DEV float block_sum256(float v, float* s_red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  if (lane == 0) s_red[wave] = v;
+  __syncthreads();
+  const float r = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+  __syncthreads();
+  return r;
+}
+
+// grid (n_spans + 1, B): block j < n pools span j and scores it; block n
+// writes h_ctx.
+template <class E>
+__global__ __launch_bounds__(256) void k_span_pool(kd_span_args a) {
+  __shared__ float s_red[4];
+  const int j = blockIdx.x, b = blockIdx.y, n = a.n_spans, D = a.D;
+  const int mp = a.mask_pos[b];
+  if (j == n) {
+    for (int d = threadIdx.x; d < D; d += 256) a.h_ctx[int64_t(b) * D + d] = mp >= 0 ? h_at<E>(a, b, mp, d) : 0.f;
+    return;
+  }
+  const int lo = a.span_lo[int64_t(b) * n + j], hi = a.span_hi[int64_t(b) * n + j];
+  const float cnt = float(hi - lo);
+  float part = 0.f;
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float acc = 0.f;
+    for (int t = lo; t < hi; ++t) acc += h_at<E>(a, b, t, d);
+    const float mean = hi > lo ? acc / cnt : 0.f;
+    a.h_spans[(int64_t(b) * n + j) * D + d] = mean;
+    part = __builtin_fmaf(mean, mp >= 0 ? h_at<E>(a, b, mp, d) : 0.f, part);
+  }
+  const float s = block_sum256(part, s_red);
+  if (threadIdx.x == 0) a.scores[int64_t(b) * n + j] = s;
+}
+
+// grid (ceil(T / 64), B): rows t0 .. t0+63 of dh in full.
+//   dh[t] = sum_{j: lo_j <= t < hi_j} ds_j h_ctx / (hi_j - lo_j)   (ascending j)
+//         + [t == mask] sum_j ds_j h_span_j                          (ascending j)
+template <class E>
+__global__ __launch_bounds__(256) void k_span_bwd(kd_span_args a) {
+  constexpr int ROWS = 64;
+  const int b = blockIdx.y, t0 = blockIdx.x * ROWS, n = a.n_spans, D = a.D;
+  const int t1 = min(a.T, t0 + ROWS);
+  const int mp = a.mask_pos[b];
+  const int32_t* lo = a.span_lo + int64_t(b) * n;
+  const int32_t* hi = a.span_hi + int64_t(b) * n;
+  const float* ds = a.dscores + int64_t(b) * n;
+  for (int t = t0; t < t1; ++t) {
+    uint16_t* out = static_cast<uint16_t*>(a.dh) + int64_t(b) * a.dh_strides[0] + int64_t(t) * a.dh_strides[1];
+    for (int d = threadIdx.x; d < D; d += 256) {
+      float g = 0.f;
+      const float c = a.h_ctx[int64_t(b) * D + d];
+      for (int j = 0; j < n; ++j)
+        if (lo[j] <= t && t < hi[j]) g += ds[j] * c / float(hi[j] - lo[j]);
+      if (t == mp)
+        for (int j = 0; j < n; ++j) g = __builtin_fmaf(ds[j], a.h_spans[(int64_t(b) * n + j) * D + d], g);
+      out[d] = uint16_t(pack2<E>(g, 0.f) & 0xFFFFu);
+    }
+  }
+}
+
+}  // namespace
+
+int launch_span(const kd_span_args& a, hipStream_t st) {
+  hipLaunchKernelGGL(k_span_find, dim3(unsigned(a.B)), dim3(1024), size_t(2) * a.n_spans * sizeof(int), st, a);
+  if (a.dtype == KD_BF16)
+    hipLaunchKernelGGL(k_span_pool<BF16>, dim3(unsigned(a.n_spans + 1), unsigned(a.B)), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(k_span_pool<F16>, dim3(unsigned(a.n_spans + 1), unsigned(a.B)), dim3(256), 0, st, a);
+  return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
+}
+
+int launch_span_bwd(const kd_span_args& a, hipStream_t st) {
+  const dim3 grid(unsigned((a.T + 63) / 64), unsigned(a.B));
+  if (a.dtype == KD_BF16) hipLaunchKernelGGL(k_span_bwd<BF16>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(k_span_bwd<F16>, grid, dim3(256), 0, st, a);
+  return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
+}
+
+}  // namespace kd

@@ -121,6 +121,17 @@ KD_DEV u32x2 ds_read_tr16(const uint8_t* p) {
   return __builtin_bit_cast(u32x2, v);
 }
 
+// Pointers into LDS typed as such: offsets added to them stay 32-bit LDS
+// addresses (a register plus the instruction's immediate offset), where a
+// generic pointer is converted back to LDS after every addition.
+typedef const __attribute__((address_space(3))) uint8_t lds_u8;
+KD_DEV lds_u8* to_lds(const uint8_t* p) { return (lds_u8*)(p); }
+KD_DEV u32x2 ds_read_tr16(lds_u8* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4 __attribute__((address_space(3)))*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+KD_DEV u32x4 ds_read16(lds_u8* p) { return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(p); }
+
 // LDS byte address of a pointer into __shared__ memory
 KD_DEV uint32_t lds_addr(const void* p) {
   return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t*)(p)));

@@ -10,12 +10,13 @@ calls it; the q/k/v projections are handed over as strided ``[B, H, L, d]``
 views of ``[B, L, H, d]``, without copies, and O comes back in ``[B, L, H, d]``
 memory (``out_layout="bthd"``), so ``o_proj`` reads it without a copy either.
 
-The cocktail-party head (``model.py:243-295``) scores the hidden state at the
+The cocktail-party head (``model.py:250-298``) scores the hidden state at the
 first ``[MASK]`` against the mean hidden state of each span's interior
 (``[SPAN] x.. [ES]`` minus the markers) and takes the cross entropy against
 ``correct_idx``; spans a row does not have score 0, as the reference's
-zero-padded ``h_spans`` do.  Here the span means are one ``index_add_`` instead
-of the reference's Python double loop, and the scores are formed in fp32.
+zero-padded ``h_spans`` do.  The pooling and the scores run in the
+``kd_span_scores`` kernels (``span_head.py``) instead of the reference's Python
+double loop, and the scores are fp32.
 
 ``attention`` is injectable so a test can run the same weights through a
 dense fp32 reference attention.
@@ -27,7 +28,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .attention import AttentionPlan, build_plan, build_plan_from_tokens, flash_attention, mask_mode
-from .metadata import CLS, ES, MASK, MASKQ, SPAN, derive_metadata
+from .metadata import CLS, MASKQ, SPAN, derive_metadata
+from .span_head import has_cocktail_layout, span_scores
 
 VOCAB = 256 + 6  # byte tokens + [PAD] [CLS] [MASK] [SPAN] [ES] [MASKQ] (data_builder.py:44-52)
 
@@ -140,7 +142,7 @@ class GPTModel(nn.Module):
         if plan is None and (in_span is None or span_id is None or is_prefix is None):
             in_span, span_id, is_prefix = derive_metadata(tokens, rule="fallback")
         h = self.hidden(tokens, in_span, span_id, is_prefix, plan)
-        if (tokens == MASK).any() and (tokens == SPAN).any() and (tokens == ES).any():
+        if has_cocktail_layout(tokens):
             scores = span_scores(tokens, h)
             loss = F.cross_entropy(scores, correct_idx) if correct_idx is not None else None
             return scores, loss
@@ -149,30 +151,6 @@ class GPTModel(nn.Module):
         if targets is not None:
             loss = F.cross_entropy(logits.view(-1, logits.size(-1)), targets.view(-1), ignore_index=0)
         return logits, loss
-
-
-def span_scores(tokens: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
-    """``<h at first [MASK], mean h over each span's interior>`` per row and span."""
-    B, T, D = h.shape
-    is_mask = tokens == MASK
-    first = is_mask & (torch.cumsum(is_mask.to(torch.int32), dim=1) == 1)
-    h_ctx = (h * first[..., None].to(h.dtype)).sum(dim=1)  # zero row if no [MASK]
-    starts = (tokens == SPAN).to(torch.int64)
-    sid = torch.cumsum(starts, dim=1)  # span j (1-based) from its [SPAN] on
-    ends = torch.cumsum((tokens == ES).to(torch.int64), dim=1)
-    inside = (sid > ends) & (tokens != SPAN)  # strictly between [SPAN] and its [ES]
-    n_spans = int(starts.sum(dim=1).max().item())
-    slot = torch.where(inside, torch.arange(B, device=h.device)[:, None] * n_spans + sid - 1,
-                       torch.full_like(sid, B * n_spans))
-    acc = torch.zeros(B * n_spans + 1, D, dtype=torch.float32, device=h.device)
-    acc.index_add_(0, slot.view(-1), h.reshape(-1, D).float())
-    cnt = torch.zeros(B * n_spans + 1, dtype=torch.float32, device=h.device)
-    cnt.index_add_(0, slot.view(-1), torch.ones(B * T, dtype=torch.float32, device=h.device))
-    h_spans = (acc[:-1] / cnt[:-1].clamp_min(1.0)[:, None]).view(B, n_spans, D)
-    # scores in fp32: at random init they are O(500) and nearly equal, so a
-    # bf16 product (spacing 2 there) would decide the loss by its rounding;
-    # [B, n, D] @ [B, D, 1] with a contiguous right operand
-    return torch.bmm(h_spans, h_ctx.float().unsqueeze(-1).contiguous()).squeeze(-1)
 
 
 def config5_batch(B=8, L=2048, seed=0):

@@ -20,8 +20,8 @@ attention  -- dense masked attention forward/backward on the CPU
               baseline that follows ``original_kernel.py:2002-2032``.
 hadamard   -- Sylvester Walsh-Hadamard transform with random signs.
 fp8        -- OCP e4m3fn round-to-nearest-even quantisation, bit level.
-gpt        -- the config-5 GPT model restated in fp32 on the CPU
-              (``model.py:31-117``, ``:127-314``).
+span_head  -- the cocktail-party head's span pooling and scores
+              (restates ``model.py:263-296``, Python loops kept).
 
 Pinning: every function above is checked in ``tests/test_oracle_*.py``
 against closed forms, hand-built truth tables, brute force on tiny inputs,

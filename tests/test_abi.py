@@ -93,6 +93,20 @@ def test_bad_arguments_return_status_without_gpu():
     t.tokens, t.rule = 64, 9
     assert lib.kd_plan_build_tokens(ctypes.byref(t), ctypes.c_void_p(256), null) == _lib.KD_ERR_INVALID
     assert "rule" in lib.kd_last_error_string().decode()
+    sp = _lib.SpanArgs()
+    assert lib.kd_span_scores(None, null) == _lib.KD_ERR_INVALID
+    sp.B, sp.T, sp.D, sp.n_spans, sp.dtype = 2, 16, 64, 0, _lib.KD_BF16
+    assert lib.kd_span_scores(ctypes.byref(sp), null) == _lib.KD_ERR_UNSUPPORTED  # n_spans 0
+    sp.n_spans = 3
+    assert lib.kd_span_scores(ctypes.byref(sp), null) == _lib.KD_ERR_INVALID  # tokens / h missing
+    sp.tokens, sp.h = 64, 128
+    sp.tokens_strides[:] = [16, 1]
+    sp.h_strides[:] = [1024, 32]  # t stride < D
+    assert lib.kd_span_scores(ctypes.byref(sp), null) == _lib.KD_ERR_INVALID
+    sp.h_strides[:] = [1024, 64]
+    assert lib.kd_span_scores(ctypes.byref(sp), null) == _lib.KD_ERR_INVALID  # outputs missing
+    assert lib.kd_span_scores_bwd(ctypes.byref(sp), null) == _lib.KD_ERR_INVALID  # dscores / dh missing
+    assert "dh" in lib.kd_last_error_string().decode()
 
 
 def test_python_boundary_validation():
