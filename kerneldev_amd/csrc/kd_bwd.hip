@@ -462,19 +462,26 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   // no waits for them, so they stay in flight until wait_tile): first the P
   // waves' column masks of a PARTIAL tile, then NL + NL (+ NL8) tile loads per
   // wave, then LSE (wave 4) and Delta (wave 5), one load each.
-  auto load_tile = [&](int e) {
+  // Slots of tile e: e % NQ, e % NDO (Q8 tiles too), e % NLS (LSE, masks),
+  // e % NDL; the loop keeps them as wrapping counters (uniform, no division).
+  struct Slots { int q, d, ls, dl; };
+  auto wrap = [](int x, int m) { return x >= m ? x - m : x; };
+  auto ahead = [&](const Slots& s, int k) {  // slots of tile e + k (k < every slot count)
+    return Slots{wrap(s.q + k, NQ), wrap(s.d + k, NDO), wrap(s.ls + k, NLS), wrap(s.dl + k, NDL)};
+  };
+  auto load_tile = [&](int e, const Slots& sl) {
     const uint32_t en = ent[e], qt = entry_tile(en), q0 = qt * 64u;
     if (role == 0 && entry_class(en, member) == TILE_PARTIAL) {  // wave-uniform
-      const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_bits[e % NLS][pair][0]))));
+      const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_bits[sl.ls][pair][0]))));
       dma_b32(rs_bits, bits_off0 + qt * uint32_t(nT) * 512u, m);
     }
-    TL::load_async(rs_q, q0 * qrb, qoff, lds_addr(s_q[e % NQ]), wave);
-    TL::load_async(rs_do, q0 * dorb, dooff, lds_addr(s_do[e % NDO]), wave);
-    if constexpr (Q8) TQ8::load_async(rs_q8, q0 * uint32_t(D), q8off, lds_addr(s_q8[e % NDO]), wave);
+    TL::load_async(rs_q, q0 * qrb, qoff, lds_addr(s_q[sl.q]), wave);
+    TL::load_async(rs_do, q0 * dorb, dooff, lds_addr(s_do[sl.d]), wave);
+    if constexpr (Q8) TQ8::load_async(rs_q8, q0 * uint32_t(D), q8off, lds_addr(s_q8[Q8 ? sl.d : 0]), wave);
     if (wave == 4)
-      dma_b32(rs_lse, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_lse[e % NLS][0])))));
+      dma_b32(rs_lse, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_lse[sl.ls][0])))));
     else if (wave == 5)
-      dma_b32(rs_dl, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_delta[e % NDL][0])))));
+      dma_b32(rs_dl, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_delta[sl.dl][0])))));
   };
   // Wait until tile e's loads (and older ones) have landed while tile e+1's,
   // issued last, may still be in flight: vector memory loads retire in order.
@@ -509,10 +516,16 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   auto accumulate = [&](const uint8_t* at_g, const u32x4 (&bop)[2][2]) {
     lds_u8* at = to_lds(at_g);
     constexpr int NS = 4 * DB;
+    lds_u8* pa[DB][2];  // one address per (db, half); the k-step offsets are immediates
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      pa[db][0] = at + taddr[db][0];
+      pa[db][1] = at + taddr[db][1];
+    }
     auto read = [&](int i) {
       const int k4 = i / DB, db = i % DB, off = k4 * 16 * TL::ROWB;
-      const u32x2 lo = ds_read_tr16(at + taddr[db][0] + off);
-      const u32x2 hi = ds_read_tr16(at + taddr[db][1] + off);
+      const u32x2 lo = ds_read_tr16(pa[db][0] + off);
+      const u32x2 hi = ds_read_tr16(pa[db][1] + off);
       return u32x4{lo[0], lo[1], hi[0], hi[1]};
     };
     u32x4 av[PF];
@@ -532,9 +545,10 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   auto rows_times_b = [&](const uint8_t* ar_g, f32x16 (&x)[2]) {
     lds_u8* ar = to_lds(ar_g);
     constexpr int NS = 2 * DS;
-    auto read = [&](int i) {
-      return ds_read16(ar + raddr[i >> 1] + (i & 1) * 32 * TL::ROWB);
-    };
+    lds_u8* pr[DS];  // one address per k-step; the 32-row offset is an immediate
+#pragma unroll
+    for (int st = 0; st < DS; ++st) pr[st] = ar + raddr[st];
+    auto read = [&](int i) { return ds_read16(pr[i >> 1] + (i & 1) * 32 * TL::ROWB); };
     u32x4 av[PF];
 #pragma unroll
     for (int i = 0; i < PF; ++i) av[i] = read(i);
@@ -548,14 +562,15 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
     __builtin_amdgcn_sched_barrier(0x406);
   };
 
-  if (n > 0) load_tile(0);
+  Slots sl{0, 0, 0, 0};  // slots of tile e (e = 0 here)
+  if (n > 0) load_tile(0, sl);
   // the B operand's register loads are complete here: the compiler's wait
   // for them falls here, not at their first use (where it would also wait
   // for the copies of tile 1)
   wait_vmem();
 #pragma unroll
   for (int st = 0; st < DS; ++st) settle(bf[st]);
-  for (int e = 1; e < PD && e < n; ++e) load_tile(e);
+  for (int e = 1; e < PD && e < n; ++e) load_tile(e, ahead(sl, e));
   // S of tile e (P waves), or dP of tile e carried into step e + 1 (dS
   // waves): one register set for both roles
   f32x16 x[2] = {f32x16{}, f32x16{}};
@@ -564,12 +579,12 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
     // tiles up to e landed (tile e + PD - 1 may be in flight when PD = 2)
     wait_tile(PD == 2 && e + 1 < n);
     barrier_lds();  // tile e landed, P(e-1) written; P(e-2) and the slots of tile e+PD released
-    if (e + PD < n) load_tile(e + PD);
+    if (e + PD < n) load_tile(e + PD, ahead(sl, PD));
     const int pb = e & 1;
     if (role == 0) {
       if (e < n) {
         if constexpr (Q8) {  // S = Q8 K8^T on the fp8 MFMA; A = Q8 rows, 32 bytes per lane and k-step
-          const uint8_t* t8 = s_q8[Q8 ? e % NDO : 0];
+          const uint8_t* t8 = s_q8[Q8 ? sl.d : 0];
           x[0] = f32x16{};
           x[1] = f32x16{};
 #pragma unroll
@@ -588,11 +603,11 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
             }
           }
         } else {
-          rows_times_b(s_q[e % NQ], x);
+          rows_times_b(s_q[sl.q], x);
         }
         const uint32_t mcls = entry_class(ent[e], member);
         if (mcls != TILE_FULL) {  // wave-uniform
-          const uint64_t colbits = mcls == TILE_PARTIAL ? s_bits[e % NLS][pair][c] : 0u;  // EMPTY: nothing allowed
+          const uint64_t colbits = mcls == TILE_PARTIAL ? s_bits[sl.ls][pair][c] : 0u;  // EMPTY: nothing allowed
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
             const uint32_t w = uint32_t(colbits >> (32 * qb)) >> (8 * hf);
@@ -606,8 +621,8 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
             const int ql = 32 * qb + 16 * t + 8 * hf;
-            const f32x4 l0 = *reinterpret_cast<const f32x4*>(&s_lse[e % NLS][ql]);
-            const f32x4 l1 = *reinterpret_cast<const f32x4*>(&s_lse[e % NLS][ql + 4]);
+            const f32x4 l0 = *reinterpret_cast<const f32x4*>(&s_lse[sl.ls][ql]);
+            const f32x4 l1 = *reinterpret_cast<const f32x4*>(&s_lse[sl.ls][ql + 4]);
             float p[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j)
@@ -616,11 +631,11 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
                                pack2<E>(p[6], p[7])};
             s_p[pb][pair][2 * qb + t][lane] = bop[qb][t];
           }
-        accumulate(s_do[e % NDO], bop);  // dV^T += dO^T P
+        accumulate(s_do[sl.d], bop);  // dV^T += dO^T P
       }
     } else {
       if (e >= 1) {  // dS and dK of tile e - 1
-        const int qprev = (e - 1) % NQ, dprev = (e - 1) % NDL;
+        const int qprev = wrap(sl.q + NQ - 1, NQ), dprev = wrap(sl.dl + NDL - 1, NDL);
         u32x4 dsb[2][2];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
@@ -642,8 +657,9 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
           }
         accumulate(s_q[qprev], dsb);  // dK^T += Q^T dS
       }
-      if (e < n) rows_times_b(s_do[e % NDO], x);  // dP of tile e
+      if (e < n) rows_times_b(s_do[sl.d], x);  // dP of tile e
     }
+    sl = ahead(sl, 1);
   }
 
   if (kvalid) {
