@@ -126,7 +126,10 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
   constexpr bool LDS_BITS = !Q8;
   __shared__ __attribute__((aligned(256))) uint64_t s_bits[LDS_BITS ? 2 : 1][LDS_BITS ? 4 : 1][32];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
+  // the wave index through readfirstlane: uniform, so the role and slot
+  // arithmetic derived from it stays scalar
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, hf = lane >> 5,
+            c = lane & 31;
   const int T = a.T, H = a.H;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
   const int hb = work / nQB;  // head-major: each XCD's range holds every batch row of its heads
@@ -402,6 +405,8 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   // each P wave's column masks of a PARTIAL tile, copied with the tile
   __shared__ __attribute__((aligned(256))) uint64_t s_bits[NLS][4][32];
 
+  // (the wave index stays a vector value here: made uniform, the two roles'
+  // registers are allocated apart and the kernel spills)
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
   const int pair = wave & 3, role = wave >> 2;
   const int T = a.T, H = a.H;
@@ -436,7 +441,9 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
       bf[2 * st + 1] = buf_load16(rs8, uint32_t(krow) * D + 64 * st + 32 * hf + 16);
     }
   } else {
-    const auto rs_b = role == 0 ? make_rsrc(kg, uint32_t(T) * krb) : make_rsrc(vg, uint32_t(T) * vrb);
+    // (a uniform role for the select: a per-lane buffer resource would need a readfirstlane loop per load)
+    const bool p_wave = __builtin_amdgcn_readfirstlane(role) == 0;
+    const auto rs_b = p_wave ? make_rsrc(kg, uint32_t(T) * krb) : make_rsrc(vg, uint32_t(T) * vrb);
     const uint32_t brb = role == 0 ? krb : vrb;
 #pragma unroll
     for (int st = 0; st < DS; ++st) bf[st] = buf_load16(rs_b, uint32_t(krow) * brb + (16 * st + 8 * hf) * 2);

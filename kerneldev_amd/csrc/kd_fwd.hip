@@ -59,7 +59,10 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
   // each wave's row masks of a PARTIAL tile (copied by the wave itself)
   __shared__ __attribute__((aligned(256))) uint64_t s_bits[2][NW][32 * QB];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, c = lane & 31;
+  // the wave index through readfirstlane: uniform, so the role and slot
+  // arithmetic derived from it stays scalar
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, hf = lane >> 5,
+            c = lane & 31;
   const int T = a.T, H = a.H;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
   const int hb = work / nQB;  // head-major: each XCD's range holds every batch row of its heads
