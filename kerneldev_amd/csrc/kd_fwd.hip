@@ -25,10 +25,10 @@
 // textbook loop.  Each wave masks by the class of its own 64-row q-tile
 // against the key tile (from the list entry): FULL tiles skip the mask,
 // PARTIAL ones apply the plan's 64-bit row masks (two VALU ops per score,
-// fetched one step ahead), EMPTY ones mask everything.
-// O is normalised by the sum of the ROUNDED P that enters P V, so it is an
-// exact convex combination of V rows up to the final rounding even when one
-// key dominates the row; LSE uses the exact fp32 sum.
+// copied one step ahead into the wave's own LDS slot), EMPTY ones mask
+// everything.  O is normalised by the sum of the ROUNDED P that enters P V,
+// so it is an exact convex combination of V rows up to the final rounding
+// even when one key dominates the row; LSE uses the same sum.
 #include "kd_tile.h"
 
 namespace kd {
