@@ -636,9 +636,16 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
               p[j] = fast_exp2(__builtin_fmaf(x[qb][8 * t + j], sl2, -(j < 4 ? l0[j] : l1[j - 4])));
             bop[qb][t] = u32x4{pack2<E>(p[0], p[1]), pack2<E>(p[2], p[3]), pack2<E>(p[4], p[5]),
                                pack2<E>(p[6], p[7])};
-            s_p[pb][pair][2 * qb + t][lane] = bop[qb][t];
           }
         accumulate(s_do[sl.d], bop);  // dV^T += dO^T P
+        // P for the dS wave (read after the next barrier).  Written after the
+        // MFMAs: LDS stores may not cross the product's scheduling fences, so
+        // stores placed before it would hold all of P's VALU work ahead of the
+        // first MFMA.
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) s_p[pb][pair][2 * qb + t][lane] = bop[qb][t];
       }
     } else {
       if (e >= 1) {  // dS and dK of tile e - 1
