@@ -275,6 +275,12 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
     const uint8_t* kt = s_k[buf];
     const uint8_t* vt = s_v[buf];
 
+    // the row mask is read first: LDS reads cannot cross the products'
+    // scheduling fences, and the mask must not hold back the softmax below
+    const uint32_t mcls = entry_class(cur, member);
+    uint64_t rowbits = 0;  // EMPTY: nothing allowed
+    if (mcls == TILE_PARTIAL) rowbits = LDS_BITS ? s_bits[LDS_BITS ? buf : 0][LDS_BITS ? wave : 0][c] : bits;
+
     // S^T = K Q^T and dP^T = V dO^T; A operands (K / K8 and V rows) are read
     // DQ_PF steps ahead of their MFMAs, steps i: kb = i & 1, st = i >> 1; the
     // sched_barriers keep LDS reads and MFMAs in that order
@@ -291,7 +297,22 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
         s[i & 1] = so.mma_a(av[i % PF], i >> 1, (i >> 1) == 0 ? f32x16{} : s[i & 1]);
         if (i + PF < NS) av[i % PF] = so.read_a(st_tile, (i + PF) & 1, (i + PF) >> 1);
       }
+      __builtin_amdgcn_sched_barrier(0x406);
     }
+    if (mcls != TILE_FULL) {  // wave-uniform.  Register r of s[kb] holds key 32 kb + 16 (r / 8) + 8 hf + r % 8
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const uint32_t w = uint32_t(rowbits >> (32 * kb)) >> (8 * hf);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[kb][r] = mask_bit(s[kb][r], w, 16 * (r >> 3) + (r & 7));
+      }
+    }
+    // P = exp2(S c - LSE), in place: independent of dP, so this VALU work can
+    // interleave with the dP MFMAs that follow in the same basic block
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kb][r] = fast_exp2(__builtin_fmaf(s[kb][r], sl2, -lse));
     {
       constexpr int NS = 2 * DS, PF = DQ_PF;
       auto read = [&](int i) {
@@ -308,27 +329,12 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
       }
       __builtin_amdgcn_sched_barrier(0x406);
     }
-    const uint32_t mcls = entry_class(cur, member);
-    if (mcls != TILE_FULL) {  // wave-uniform.  Register r of s[kb] holds key 32 kb + 16 (r / 8) + 8 hf + r % 8
-      uint64_t rowbits = 0;  // EMPTY: nothing allowed
-      if (mcls == TILE_PARTIAL) rowbits = LDS_BITS ? s_bits[LDS_BITS ? buf : 0][LDS_BITS ? wave : 0][c] : bits;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const uint32_t w = uint32_t(rowbits >> (32 * kb)) >> (8 * hf);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[kb][r] = mask_bit(s[kb][r], w, 16 * (r >> 3) + (r & 7));
-      }
-    }
-
     u32x4 dsb[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       float ds[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(__builtin_fmaf(s[kb][r], sl2, -lse));
-        ds[r] = p * (dp[kb][r] - delta);
-      }
+      for (int r = 0; r < 16; ++r) ds[r] = s[kb][r] * (dp[kb][r] - delta);
 #pragma unroll
       for (int t = 0; t < 2; ++t)
         dsb[kb][t] = u32x4{pack2<E>(ds[8 * t + 0], ds[8 * t + 1]), pack2<E>(ds[8 * t + 2], ds[8 * t + 3]),
