@@ -93,7 +93,8 @@ typedef struct kd_attn_args {
   void *dq, *dk, *dv;           /* [B, H, T, D] (bwd) */
   int64_t dq_strides[3], dk_strides[3], dv_strides[3];
   float *delta;                 /* fp32 workspace of 2 * B*H*T (bwd): Delta [B, H, T],
-                                   then LSE with -inf replaced by +inf [B, H, T] */
+                                   then -LSE / c [B, H, T] with c the score scale (sm_scale log2 e, times
+                                   q_scale k_scale with fp8 scores; -inf for fully masked rows) */
   void *o_lo;                   /* optional contiguous [B, H, T, D], dtype of o: the
                                    forward writes O_fp32 - O there, the backward's Delta
                                    reads it; NULL to skip */

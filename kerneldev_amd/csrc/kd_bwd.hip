@@ -37,6 +37,19 @@
 
 namespace kd {
 
+// The workspace's second half holds, per row, -LSE / c with c the score scale
+// (sm_scale log2 e, times q_scale k_scale for fp8 scores) and -inf for fully
+// masked rows.  The dK/dV kernel starts each S accumulator from it, so that
+// its P = exp2(c (S - LSE / c)) is one multiply and one exp2, and the LSE
+// values are read before the product instead of between the product and the
+// exponentials.
+KD_DEV float score_scale(const AttnArgs& a, int bh) {
+  return a.sm_scale * 1.4426950408889634f * (a.q8 != nullptr ? a.q_scale[bh] * a.k_scale[bh] : 1.f);
+}
+KD_DEV float lse_neg_scaled(const AttnArgs& a, int bh, float l) {
+  return l == -__builtin_inff() ? -__builtin_inff() : -l * (1.f / score_scale(a, bh));
+}
+
 // ---------------------------------------------------------------- Delta ----
 template <class E, int D>
 __global__ __launch_bounds__(256) void k_delta(AttnArgs a) {
@@ -70,8 +83,7 @@ __global__ __launch_bounds__(256) void k_delta(AttnArgs a) {
   for (int off = TPR / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
   if (row < nrows && seg == 0) {
     a.delta[row] = sum;
-    const float l = a.lse[row];
-    a.delta[nrows + row] = (l == -__builtin_inff()) ? __builtin_inff() : l;
+    a.delta[nrows + row] = lse_neg_scaled(a, int(row / a.T), a.lse[row]);
   }
 }
 
@@ -185,10 +197,11 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
     lse = (l == -INF) ? INF : l;
     if (qvalid && hf == 0) {
       a.delta[int64_t(bh) * T + qrow] = delta;
-      a.delta[BHT + int64_t(bh) * T + qrow] = lse;
+      a.delta[BHT + int64_t(bh) * T + qrow] = lse_neg_scaled(a, bh, l);
     }
   } else {
-    lse = qvalid ? a.delta[BHT + int64_t(bh) * T + qrow] : INF;
+    const float l = qvalid ? a.lse[int64_t(bh) * T + qrow] : -INF;
+    lse = (l == -INF) ? INF : l;  // exp2(S c - inf) = 0: fully masked rows get no gradient
     delta = qvalid ? a.delta[int64_t(bh) * T + qrow] : 0.f;
   }
   // this wave's rows lie in q-tile 2 qblock + member; its row masks per key tile
@@ -555,7 +568,8 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   };
   // x[qb] += (rows of tile `ar`) B^T; register r of x[qb] holds query
   // 32 qb + 16 (r / 8) + 8 hf + r % 8 of this lane's key; steps i = (st, qb)
-  auto rows_times_b = [&](const uint8_t* ar_g, f32x16 (&x)[2]) {
+  // from_x: accumulate onto x's current content instead of zero
+  auto rows_times_b = [&](const uint8_t* ar_g, f32x16 (&x)[2], bool from_x) {
     lds_u8* ar = to_lds(ar_g);
     constexpr int NS = 2 * DS;
     lds_u8* pr[DS];  // one address per k-step; the 32-row offset is an immediate
@@ -569,7 +583,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
     for (int i = 0; i < NS; ++i) {
       const int st = i >> 1, qb = i & 1;
       __builtin_amdgcn_sched_barrier(0x406);
-      x[qb] = mfma32x32x16<E>(av[i % PF], bf[st], st == 0 ? f32x16{} : x[qb]);
+      x[qb] = mfma32x32x16<E>(av[i % PF], bf[st], (st == 0 && !from_x) ? f32x16{} : x[qb]);
       if (i + PF < NS) av[i % PF] = read(i + PF);
     }
     __builtin_amdgcn_sched_barrier(0x406);
@@ -596,10 +610,23 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
     const int pb = e & 1;
     if (role == 0) {
       if (e < n) {
+        // S starts from -LSE / c of its query (register r of x[qb]: query
+        // 32 qb + 16 (r / 8) + 8 hf + r % 8), so that P = exp2(c x)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int ql = 32 * qb + 16 * t + 8 * hf;
+            const f32x4 l0 = *reinterpret_cast<const f32x4*>(&s_lse[sl.ls][ql]);
+            const f32x4 l1 = *reinterpret_cast<const f32x4*>(&s_lse[sl.ls][ql + 4]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              x[qb][8 * t + j] = l0[j];
+              x[qb][8 * t + 4 + j] = l1[j];
+            }
+          }
         if constexpr (Q8) {  // S = Q8 K8^T on the fp8 MFMA; A = Q8 rows, 32 bytes per lane and k-step
           const uint8_t* t8 = s_q8[Q8 ? sl.d : 0];
-          x[0] = f32x16{};
-          x[1] = f32x16{};
 #pragma unroll
           for (int st = 0; st < D / 64; ++st) {
             const int a0 = TQ8::at(srow, 4 * st + 2 * hf), a1 = TQ8::at(srow, 4 * st + 2 * hf + 1);
@@ -616,7 +643,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
             }
           }
         } else {
-          rows_times_b(s_q[sl.q], x);
+          rows_times_b(s_q[sl.q], x, true);
         }
         const uint32_t mcls = entry_class(ent[e], member);
         if (mcls != TILE_FULL) {  // wave-uniform
@@ -633,13 +660,9 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
         for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            const int ql = 32 * qb + 16 * t + 8 * hf;
-            const f32x4 l0 = *reinterpret_cast<const f32x4*>(&s_lse[sl.ls][ql]);
-            const f32x4 l1 = *reinterpret_cast<const f32x4*>(&s_lse[sl.ls][ql + 4]);
             float p[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-              p[j] = fast_exp2(__builtin_fmaf(x[qb][8 * t + j], sl2, -(j < 4 ? l0[j] : l1[j - 4])));
+            for (int j = 0; j < 8; ++j) p[j] = fast_exp2(x[qb][8 * t + j] * sl2);
             bop[qb][t] = u32x4{pack2<E>(p[0], p[1]), pack2<E>(p[2], p[3]), pack2<E>(p[4], p[5]),
                                pack2<E>(p[6], p[7])};
           }
@@ -677,7 +700,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
           }
         accumulate(s_q[qprev], dsb);  // dK^T += Q^T dS
       }
-      if (e < n) rows_times_b(s_do[sl.d], x);  // dP of tile e
+      if (e < n) rows_times_b(s_do[sl.d], x, false);  // dP of tile e
     }
     sl = ahead(sl, 1);
   }
