@@ -92,7 +92,7 @@ typedef struct kd_attn_args {
   int64_t do_strides[3];
   void *dq, *dk, *dv;           /* [B, H, T, D] (bwd) */
   int64_t dq_strides[3], dk_strides[3], dv_strides[3];
-  float *delta;                 /* fp32 workspace of 2 * B*H*T (bwd): Delta [B, H, T],
+  float *delta;                 /* fp32 workspace of 2 * B*H*T (bwd): -Delta [B, H, T],
                                    then -LSE / c [B, H, T] with c the score scale (sm_scale log2 e, times
                                    q_scale k_scale with fp8 scores; -inf for fully masked rows) */
   void *o_lo;                   /* optional contiguous [B, H, T, D], dtype of o: the
@@ -202,10 +202,11 @@ int kd_plan_build_tokens(const kd_token_args *t, void *plan, void *stream);
  * _flash_attn_fwd (original_kernel.py:1697-1778, kernel :279-626). */
 int kd_attn_fwd(const kd_attn_args *a, const void *plan, void *stream);
 
-/* Delta = rowsum(O * dO) in fp32 into a->delta[0 : B*H*T], and the backward's
- * copy of a->lse (fully masked rows: +inf) into a->delta[B*H*T : 2*B*H*T].
- * Replaces _flash_attn_bwd_precompute (original_kernel.py:649-710, launch
- * :1829-1846).  kd_attn_bwd_dq / _dkdv read both halves. */
+/* -Delta = -rowsum(O * dO) in fp32 into a->delta[0 : B*H*T], and -LSE / c
+ * (the form kd_attn_bwd_dkdv starts its score accumulators from; -inf for
+ * fully masked rows) into a->delta[B*H*T : 2*B*H*T].  Replaces
+ * _flash_attn_bwd_precompute (original_kernel.py:649-710, launch :1829-1846).
+ * kd_attn_bwd_dq reads the first half, kd_attn_bwd_dkdv both. */
 int kd_attn_bwd_delta(const kd_attn_args *a, void *stream);
 
 /* dQ from the saved LSE and Delta.  Replaces the dQ workers of

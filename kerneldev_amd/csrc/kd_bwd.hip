@@ -37,7 +37,8 @@
 
 namespace kd {
 
-// The workspace's second half holds, per row, -LSE / c with c the score scale
+// The workspace holds -Delta per row (dK/dV starts its dP accumulators from
+// it), then -LSE / c with c the score scale
 // (sm_scale log2 e, times q_scale k_scale for fp8 scores) and -inf for fully
 // masked rows.  The dK/dV kernel starts each S accumulator from it, so that
 // its P = exp2(c (S - LSE / c)) is one multiply and one exp2, and the LSE
@@ -82,7 +83,7 @@ __global__ __launch_bounds__(256) void k_delta(AttnArgs a) {
 #pragma unroll
   for (int off = TPR / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
   if (row < nrows && seg == 0) {
-    a.delta[row] = sum;
+    a.delta[row] = -sum;
     a.delta[nrows + row] = lse_neg_scaled(a, int(row / a.T), a.lse[row]);
   }
 }
@@ -196,13 +197,13 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
     const float l = qvalid ? a.lse[int64_t(bh) * T + qrow] : -INF;
     lse = (l == -INF) ? INF : l;
     if (qvalid && hf == 0) {
-      a.delta[int64_t(bh) * T + qrow] = delta;
+      a.delta[int64_t(bh) * T + qrow] = -delta;
       a.delta[BHT + int64_t(bh) * T + qrow] = lse_neg_scaled(a, bh, l);
     }
   } else {
     const float l = qvalid ? a.lse[int64_t(bh) * T + qrow] : -INF;
     lse = (l == -INF) ? INF : l;  // exp2(S c - inf) = 0: fully masked rows get no gradient
-    delta = qvalid ? a.delta[int64_t(bh) * T + qrow] : 0.f;
+    delta = qvalid ? -a.delta[int64_t(bh) * T + qrow] : 0.f;
   }
   // this wave's rows lie in q-tile 2 qblock + member; its row masks per key tile
   const int member = wave >> 1;
@@ -678,29 +679,41 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
       }
     } else {
       if (e >= 1) {  // dS and dK of tile e - 1
-        const int qprev = wrap(sl.q + NQ - 1, NQ), dprev = wrap(sl.dl + NDL - 1, NDL);
+        const int qprev = wrap(sl.q + NQ - 1, NQ);
         u32x4 dsb[2][2];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            const int ql = 32 * qb + 16 * t + 8 * hf;
-            const f32x4 d0 = *reinterpret_cast<const f32x4*>(&s_delta[dprev][ql]);
-            const f32x4 d1 = *reinterpret_cast<const f32x4*>(&s_delta[dprev][ql + 4]);
             const u32x4 pw = s_p[pb ^ 1][pair][2 * qb + t][lane];
             float ds[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
               const uint32_t w = pw[j >> 1];
               const float p = to_f32<E>(uint16_t((j & 1) ? (w >> 16) : (w & 0xFFFFu)));
-              ds[j] = p * (x[qb][8 * t + j] - (j < 4 ? d0[j] : d1[j - 4]));
+              ds[j] = p * x[qb][8 * t + j];  // x = dP - Delta (the product started from -Delta)
             }
             dsb[qb][t] = u32x4{pack2<E>(ds[0], ds[1]), pack2<E>(ds[2], ds[3]), pack2<E>(ds[4], ds[5]),
                                pack2<E>(ds[6], ds[7])};
           }
         accumulate(s_q[qprev], dsb);  // dK^T += Q^T dS
       }
-      if (e < n) rows_times_b(s_do[sl.d], x, false);  // dP of tile e
+      if (e < n) {  // dP of tile e, started from -Delta of its query (register layout as for S)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int ql = 32 * qb + 16 * t + 8 * hf;
+            const f32x4 d0 = *reinterpret_cast<const f32x4*>(&s_delta[sl.dl][ql]);
+            const f32x4 d1 = *reinterpret_cast<const f32x4*>(&s_delta[sl.dl][ql + 4]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              x[qb][8 * t + j] = d0[j];
+              x[qb][8 * t + 4 + j] = d1[j];
+            }
+          }
+        rows_times_b(s_do[sl.d], x, true);
+      }
     }
     sl = ahead(sl, 1);
   }
