@@ -205,6 +205,11 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
     lse = (l == -INF) ? INF : l;  // exp2(S c - inf) = 0: fully masked rows get no gradient
     delta = qvalid ? -a.delta[int64_t(bh) * T + qrow] : 0.f;
   }
+  // dP^T accumulators start from -Delta (every register of a lane holds its
+  // query's value), so dS = P dP needs no subtraction per score
+  f32x16 neg_delta;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) neg_delta[r] = -delta;
   // this wave's rows lie in q-tile 2 qblock + member; its row masks per key tile
   const int member = wave >> 1;
   // qbits of batch row b: [nT q-tiles][nT key tiles][64 rows]; this wave's 32
@@ -338,7 +343,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
         __builtin_amdgcn_sched_barrier(0x406);
-        dp[i & 1] = mfma32x32x16<E>(av[i % PF], dof[i >> 1], (i >> 1) == 0 ? f32x16{} : dp[i & 1]);
+        dp[i & 1] = mfma32x32x16<E>(av[i % PF], dof[i >> 1], (i >> 1) == 0 ? neg_delta : dp[i & 1]);
         if (i + PF < NS) av[i % PF] = read(i + PF);
       }
       __builtin_amdgcn_sched_barrier(0x406);
@@ -348,7 +353,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
     for (int kb = 0; kb < 2; ++kb) {
       float ds[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ds[r] = s[kb][r] * (dp[kb][r] - delta);
+      for (int r = 0; r < 16; ++r) ds[r] = s[kb][r] * dp[kb][r];  // dp = dP - Delta
 #pragma unroll
       for (int t = 0; t < 2; ++t)
         dsb[kb][t] = u32x4{pack2<E>(ds[8 * t + 0], ds[8 * t + 1]), pack2<E>(ds[8 * t + 2], ds[8 * t + 3]),
