@@ -110,6 +110,23 @@ KD_DEV int sigma(int rho) { return (rho & ~12) | ((rho & 4) << 1) | ((rho & 8) >
 KD_DEV float wave_max32(float v) { return fmaxf(v, __shfl_xor(v, 32)); }
 KD_DEV float wave_sum32(float v) { return v + __shfl_xor(v, 32); }
 
+// Inclusive scan of one int per thread over the workgroup (up to 16 waves;
+// s_warp: 16 ints of LDS).  Every thread must call it.
+KD_DEV int block_scan(int v, int* s_warp) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(v, o, 64);
+    if (lane >= o) v += u;
+  }
+  if (lane == 63) s_warp[wave] = v;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += s_warp[w];
+  __syncthreads();
+  return v + base;
+}
+
 KD_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 KD_DEV float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 

@@ -38,31 +38,37 @@ KD_DEV bool eligible(const MetaArgs& m, int b, int t, int64_t* sid) {
   return m.span_id != nullptr && load_flag(m.in_span, m.in_span_strides, b, t) && *sid > 0;
 }
 
-// One workgroup per batch row: ballot-compact the run starts chunk by chunk.
-__global__ __launch_bounds__(256) void k_runs(MetaArgs m, uint32_t* runs, int64_t* run_sid, int32_t* run_count) {
-  const int b = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  __shared__ int s_cnt[4];
-  uint32_t* out = runs + int64_t(b) * m.T;
-  int64_t* out_sid = run_sid + int64_t(b) * m.T;
-  int total = 0;
-  for (int t0 = 0; t0 < m.T; t0 += 256) {
-    const int t = t0 + tid;
-    int64_t sid = 0, prev = 0;
-    bool start = false;
-    if (t < m.T && eligible(m, b, t, &sid)) start = !(t > 0 && eligible(m, b, t - 1, &prev) && prev == sid);
-    const uint64_t bal = __builtin_amdgcn_ballot_w64(start);
-    if (lane == 0) s_cnt[wave] = __builtin_popcountll(bal);
-    __syncthreads();
-    int pos = total + __builtin_popcountll(bal & ((uint64_t(1) << lane) - 1));
-    for (int w = 0; w < wave; ++w) pos += s_cnt[w];
-    if (start) {
-      out[pos] = uint32_t(t);
-      out_sid[pos] = sid;
+// One 1024-thread workgroup per batch row; thread i takes a contiguous
+// segment, counts its run starts, and a block scan gives each segment its
+// first output slot, so the list comes out in ascending order.
+__global__ __launch_bounds__(1024) void k_runs(MetaArgs m, uint32_t* runs, int64_t* run_sid, int32_t* run_count) {
+  __shared__ int s_warp[16];
+  const int b = blockIdx.x, tid = threadIdx.x, T = m.T;
+  const int seg = (T + 1023) / 1024, t0 = min(T, tid * seg), t1 = min(T, t0 + seg);
+  uint32_t* out = runs + int64_t(b) * T;
+  int64_t* out_sid = run_sid + int64_t(b) * T;
+  // a run starts at an eligible token whose predecessor is not eligible with the same id
+  auto scan = [&](auto&& emit) {
+    int64_t prev = 0;
+    bool prev_el = t0 > 0 && t0 < T && eligible(m, b, t0 - 1, &prev);
+    for (int t = t0; t < t1; ++t) {
+      int64_t sid;
+      const bool el = eligible(m, b, t, &sid);
+      if (el && !(prev_el && prev == sid)) emit(t, sid);
+      prev_el = el;
+      prev = sid;
     }
-    total += s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
-    __syncthreads();
-  }
-  if (tid == 0) run_count[b] = total;
+  };
+  int cnt = 0;
+  scan([&](int, int64_t) { ++cnt; });
+  const int incl = block_scan(cnt, s_warp);
+  int pos = incl - cnt;
+  scan([&](int t, int64_t sid) {
+    out[pos] = uint32_t(t);
+    out_sid[pos] = sid;
+    ++pos;
+  });
+  if (tid == int(blockDim.x) - 1) run_count[b] = incl;
 }
 
 __global__ void k_rep(MetaArgs m, const uint32_t* runs, const int64_t* run_sid, const int32_t* run_count,
@@ -366,7 +372,7 @@ int launch_plan(const MetaArgs& m, uint8_t* plan, hipStream_t st) {
     uint32_t* runs = reinterpret_cast<uint32_t*>(plan + L.runs);
     int64_t* run_sid = reinterpret_cast<int64_t*>(plan + L.run_sid);
     int32_t* run_count = reinterpret_cast<int32_t*>(plan + L.run_count);
-    hipLaunchKernelGGL(k_runs, dim3(unsigned(m.B)), dim3(256), 0, st, m, runs, run_sid, run_count);
+    hipLaunchKernelGGL(k_runs, dim3(unsigned(m.B)), dim3(1024), 0, st, m, runs, run_sid, run_count);
     hipLaunchKernelGGL(k_rep, dim3(unsigned((BT + 255) / 256)), dim3(256), 0, st, m, runs, run_sid, run_count, rep);
   }
   hipLaunchKernelGGL(k_codes, dim3(unsigned((BT + 255) / 256)), dim3(256), 0, st, m, rep, codes);

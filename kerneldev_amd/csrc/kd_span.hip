@@ -30,22 +30,6 @@ KD_DEV float h_at(const kd_span_args& a, int b, int t, int d) {
   return to_f32<E>(*p);
 }
 
-// Inclusive block scan of one int per thread (16 waves of 64 = 1024 threads).
-KD_DEV int block_scan(int v, int* s_warp) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(v, o, 64);
-    if (lane >= o) v += u;
-  }
-  if (lane == 63) s_warp[wave] = v;
-  __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wave; ++w) base += s_warp[w];
-  __syncthreads();
-  return v + base;
-}
-
 // One workgroup (1024 threads) per row: positions of the j-th [SPAN] and the
 // j-th [ES], then the interiors [lo, hi) of the zipped pairs and the first [MASK].
 __global__ __launch_bounds__(1024) void k_span_find(kd_span_args a) {
