@@ -176,11 +176,14 @@ void kd_struct_sizes3(size_t *tokens);
 /* Workspace ("plan") bytes for B sequences of length T at head dim D, and
  * the byte offsets of its sections (codes, class map, per-tile allowed
  * counts, the forward / dQ / dK-dV work lists, and the 64-bit row / column
- * masks of PARTIAL tiles).  offsets[] receives 19 int64: codes, rep, cls,
- * nnz, fwd_list, fwd_count, dq_list, dq_count, dkdv_list, dkdv_count, nT,
- * fwd_group, dq_group, dkdv_group, n_fwd_blocks, n_dq_blocks, n_dkdv_blocks,
- * qbits, kbits.  A list entry is (tile << 8) | the class of group member r in
- * bits 2r..2r+1.  Replaces the per-tile mask evaluation of
+ * masks of PARTIAL tiles, the work orders).  offsets[] receives 21 int64:
+ * codes, rep, cls, nnz, fwd_list, fwd_count, dq_list, dq_count, dkdv_list,
+ * dkdv_count, nT, fwd_group, dq_group, dkdv_group, n_fwd_blocks, n_dq_blocks,
+ * n_dkdv_blocks, qbits, kbits, fwd_order, dq_order.  A list entry is
+ * (tile << 8) | the class of group member r in bits 2r..2r+1.  A work order
+ * (u32 [B n]) lists the items b n + block of the forward or dQ list by
+ * descending list length (equal lengths in ascending item order); those
+ * kernels take each head's blocks in that order.  Replaces the per-tile mask evaluation of
  * original_kernel.py:457-517 (the reference has no tile map). */
 int64_t kd_plan_bytes(int32_t B, int32_t T, int32_t D);
 int kd_plan_layout(int32_t B, int32_t T, int32_t D, int64_t *offsets);

@@ -186,7 +186,7 @@ def plan_bytes(B: int, T: int, D: int) -> int:
 
 PLAN_FIELDS = ("codes", "rep", "cls", "nnz", "fwd_list", "fwd_count", "dq_list", "dq_count",
                "dkdv_list", "dkdv_count", "nT", "fwd_group", "dq_group", "dkdv_group",
-               "n_fwd_blocks", "n_dq_blocks", "n_dkdv_blocks", "qbits", "kbits")
+               "n_fwd_blocks", "n_dq_blocks", "n_dkdv_blocks", "qbits", "kbits", "fwd_order", "dq_order")
 
 
 def plan_layout(B: int, T: int, D: int) -> dict:

@@ -428,6 +428,9 @@ def plan_views(plan: torch.Tensor, B: int, T: int, D: int) -> dict:
         # row / column bit masks, meaningful for PARTIAL tiles only
         "qbits": view(L["qbits"], B * nT * nT * 64, torch.int64).view(B, nT, nT, 64),
         "kbits": view(L["kbits"], B * nT * nT * 64, torch.int64).view(B, nT, nT, 64),
+        # work orders: items b n + block by descending list length
+        "fwd_order": view(L["fwd_order"], B * nf, torch.int32),
+        "dq_order": view(L["dq_order"], B * nq, torch.int32),
         "layout": L,
     }
 

@@ -122,7 +122,8 @@ KD_DEV void tr_addrs(int lane, int (&addr)[D / 32][2]) {
 template <class E, int D, bool Q8>
 __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __restrict__ qbits,
                                                const uint32_t* __restrict__ list,
-                                               const int32_t* __restrict__ count, int nT, int nQB,
+                                               const int32_t* __restrict__ count,
+                                               const uint32_t* __restrict__ order, int nT, int nQB,
                                                bool fuse_delta) {
   using TL = Tile<D>;
   using SO = ScoreOp<E, D, Q8>;  // S^T = K Q^T (16-bit, or fp8 from the K8 tile)
@@ -145,9 +146,9 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
             c = lane & 31;
   const int T = a.T, H = a.H;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
-  const int hb = work / nQB;  // head-major: each XCD's range holds every batch row of its heads
-  const int qblock = nQB - 1 - (work % nQB);
-  const int b = hb % a.B, h = hb / a.B, bh = b * H + h;
+  const int h = work / (a.B * nQB);  // head-major, then the plan's longest-first order
+  const int item = int(order[work - h * (a.B * nQB)]);
+  const int b = item / nQB, qblock = item - b * nQB, bh = b * H + h;
 
   const uint16_t* qg = static_cast<const uint16_t*>(a.q) + b * a.q_strides[0] + h * a.q_strides[1];
   const uint16_t* dog = static_cast<const uint16_t*>(a.dout) + b * a.do_strides[0] + h * a.do_strides[1];
@@ -219,7 +220,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
       (uint32_t(2 * qblock + member) * uint32_t(nT) * 64u + 32u * uint32_t(wave & 1)) * 8u + uint32_t(lane) * 4u;
   const uint64_t* qbits_row = qbits + (int64_t(b) * nT + 2 * qblock + member) * nT * 64 + 32 * (wave & 1) + c;
 
-  const int lbase = b * nQB + qblock;
+  const int lbase = item;  // b nQB + qblock
   const int n = count[lbase];
   const uint32_t* ent = list + int64_t(lbase) * nT;
 
@@ -436,7 +437,10 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   const int pair = wave & 3, role = wave >> 2;
   const int T = a.T, H = a.H;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
-  const int hb = work / nKB;  // head-major: each XCD's range holds every batch row of its heads
+  // head-major, then batch row, then ascending key block: the longest-first
+  // order of the forward and dQ measured no better here (one workgroup per CU
+  // already balances well, and mixing batch rows spreads the Q / dO reads)
+  const int hb = work / nKB;
   const int kblock = work % nKB;
   const int b = hb % a.B, h = hb / a.B, bh = b * H + h;
 
@@ -744,7 +748,8 @@ static void launch_dq_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st, 
   const unsigned grid = unsigned(a.B) * a.H * L.n_dq_blocks;
   hipLaunchKernelGGL((k_dq<E, D, Q8>), dim3(grid), dim3(256), 0, st, a, reinterpret_cast<const uint64_t*>(plan + L.qbits),
                      reinterpret_cast<const uint32_t*>(plan + L.dq_list),
-                     reinterpret_cast<const int32_t*>(plan + L.dq_count), L.nT, L.n_dq_blocks, fuse_delta);
+                     reinterpret_cast<const int32_t*>(plan + L.dq_count),
+                     reinterpret_cast<const uint32_t*>(plan + L.dq_order), L.nT, L.n_dq_blocks, fuse_delta);
 }
 template <class E, int D, bool Q8 = false>
 static void launch_dkdv_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {

@@ -46,7 +46,8 @@ namespace kd {
 template <class E, int D, bool Q8, int QB>
 __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, const uint64_t* __restrict__ qbits,
                                                                 const uint32_t* __restrict__ list,
-                                                                const int32_t* __restrict__ count, int nT, int nQB) {
+                                                                const int32_t* __restrict__ count,
+                                                                const uint32_t* __restrict__ order, int nT, int nQB) {
   constexpr int NW = 4 / QB;        // waves per 128-row q-block; each owns 32 QB rows
   using TL = Tile<D, NW>;           // V tiles (and K tiles on the 16-bit path)
   using SO = ScoreOp<E, D, Q8>;     // S^T = K Q^T, 16-bit or fp8
@@ -65,9 +66,9 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
             c = lane & 31;
   const int T = a.T, H = a.H;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
-  const int hb = work / nQB;  // head-major: each XCD's range holds every batch row of its heads
-  const int qblock = nQB - 1 - (work % nQB);  // heaviest (latest) q-blocks first
-  const int b = hb % a.B, h = hb / a.B, bh = b * H + h;
+  const int h = work / (a.B * nQB);  // head-major, then the plan's longest-first order
+  const int item = int(order[work - h * (a.B * nQB)]);
+  const int b = item / nQB, qblock = item - b * nQB, bh = b * H + h;
 
   // Q and K as the score product sees them: the 16-bit inputs, or their
   // contiguous fp8 copies (kd_quant_fp8)
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
   const uint32_t bits_off0 = (uint32_t(2 * qblock + member) * uint32_t(nT) * 64u + 32u * uint32_t((wave * QB) & 1)) * 8u +
                              uint32_t(lane) * 4u;
 
-  const int lbase = b * nQB + qblock;
+  const int lbase = item;  // b nQB + qblock
   const int n = count[lbase];
   const uint32_t* ent = list + int64_t(lbase) * nT;
 
@@ -348,7 +349,8 @@ static void launch_fwd_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st)
   hipLaunchKernelGGL((k_fwd<E, D, Q8, QB>), dim3(grid), dim3(256 / QB), 0, st, a,
                      reinterpret_cast<const uint64_t*>(plan + L.qbits),
                      reinterpret_cast<const uint32_t*>(plan + L.fwd_list),
-                     reinterpret_cast<const int32_t*>(plan + L.fwd_count), L.nT, nQB);
+                     reinterpret_cast<const int32_t*>(plan + L.fwd_count),
+                     reinterpret_cast<const uint32_t*>(plan + L.fwd_order), L.nT, nQB);
 }
 
 int launch_fwd(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {

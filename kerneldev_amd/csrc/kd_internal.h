@@ -29,7 +29,7 @@ KD_DEV inline bool entry_full(uint32_t e, int group) {
 
 struct PlanLayout {
   size_t codes, rep, runs, run_sid, run_count, tok_in_span, tok_span_id, tok_prefix, cls, nnz, fwd_list, fwd_count, dq_list, dq_count, dkdv_list, dkdv_count,
-      qbits, kbits, total;
+      qbits, kbits, fwd_order, dq_order, total;
   int nT, fwd_group, dq_group, dkdv_group, n_fwd_blocks, n_dq_blocks, n_dkdv_blocks;
 };
 
@@ -51,10 +51,10 @@ int launch_span_bwd(const kd_span_args& a, hipStream_t st);
 
 // Linear workgroup id -> work index so that each XCD (workgroups are dealt
 // round-robin over the 8 XCDs) receives one contiguous range of work items,
-// i.e. the q- or k-blocks of the same (b, h) share that XCD's L2.  The
-// kernels order work head-major (h, then b, then block), so that with H a
-// multiple of 8 every XCD gets the same mix of batch rows (whose masks, and
-// so whose amounts of work, differ).
+// i.e. the blocks of the same head share that XCD's L2.  The kernels order
+// work head-major (so every XCD gets the same mix of batch rows): the forward
+// and dQ take each head's (b, block) items in the plan's longest-first work
+// order, the dK/dV kernel by batch row, then block.
 KD_DEV int xcd_remap(int wg, int n) {
   constexpr int NX = 8;
   const int per = n / NX;

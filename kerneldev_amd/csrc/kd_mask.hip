@@ -303,6 +303,34 @@ __global__ __launch_bounds__(64) void k_lists(const uint8_t* __restrict__ cls, i
   if (lane == 0) sp.counts[idx] = n;
 }
 
+// ---- work order ----------------------------------------------------------
+// Forward and dQ lists: the B n items (b, block) = b n + block sorted by descending list
+// length, equal lengths in ascending item order: item i goes to position
+// #{j : c_j > c_i or (c_j == c_i and j < i)}.  The attention kernels take
+// each head's blocks in this order, so the longest ones start first and the
+// short ones fill the end of every XCD's range (longest-first list
+// scheduling), instead of a fixed block order whose longest blocks may come
+// last.
+struct OrderSpecs {
+  const int32_t* counts[2];
+  uint32_t* order[2];
+  int n[2];
+};
+
+__global__ __launch_bounds__(256) void k_order(OrderSpecs specs) {
+  const int y = blockIdx.y, n = specs.n[y];
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int32_t* c = specs.counts[y];
+  const int ci = c[i];
+  int rank = 0;
+  for (int j = 0; j < n; ++j) {
+    const int cj = c[j];
+    rank += (cj > ci || (cj == ci && j < i)) ? 1 : 0;
+  }
+  specs.order[y][rank] = uint32_t(i);
+}
+
 // ---- dense mask output (return_attention_mask) -------------------------
 __global__ void k_mask_dense(const uint32_t* codes, int B, int H, int T, uint8_t* out, int64_t sb,
                              int64_t sh, int64_t sq, int64_t sk) {
@@ -357,6 +385,8 @@ PlanLayout plan_layout(int B, int T, int D) {
   L.dkdv_count = take(size_t(B) * nk * 4);
   L.qbits = take(BTT * 64 * 8);
   L.kbits = take(BTT * 64 * 8);
+  L.fwd_order = take(size_t(B) * nf * 4);
+  L.dq_order = take(size_t(B) * nq * 4);
   L.total = off;
   return L;
 }
@@ -387,6 +417,15 @@ int launch_plan(const MetaArgs& m, uint8_t* plan, hipStream_t st) {
                 L.dkdv_group, 1, L.n_dkdv_blocks};
   const int max_rb = std::max(L.n_fwd_blocks, std::max(L.n_dq_blocks, L.n_dkdv_blocks));
   hipLaunchKernelGGL(k_lists, dim3(unsigned(m.B * max_rb), 3), dim3(64), 0, st, cls, m.B, L.nT, specs);
+  OrderSpecs os;
+  uint32_t* const ords[2] = {reinterpret_cast<uint32_t*>(plan + L.fwd_order), reinterpret_cast<uint32_t*>(plan + L.dq_order)};
+  for (int y = 0; y < 2; ++y) {
+    os.counts[y] = specs.l[y].counts;
+    os.order[y] = ords[y];
+    os.n[y] = m.B * specs.l[y].nrb;
+  }
+  hipLaunchKernelGGL(k_order, dim3(unsigned((m.B * std::max(L.n_fwd_blocks, L.n_dq_blocks) + 255) / 256), 2), dim3(256),
+                     0, st, os);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 

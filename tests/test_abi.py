@@ -47,6 +47,9 @@ def test_plan_sizes_and_layout_offsets():
     offs = [L[k] for k in _lib.PLAN_FIELDS[:10]]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
     assert _lib.plan_bytes(2, 8192, 128) > L["dkdv_count"]
+    tail = [L[k] for k in ("kbits", "fwd_order", "dq_order")]
+    assert tail == sorted(tail) and all(o % 256 == 0 for o in tail)
+    assert _lib.plan_bytes(2, 8192, 128) >= L["dq_order"] + 4 * 2 * L["n_dq_blocks"]
 
 
 def test_bad_arguments_return_status_without_gpu():

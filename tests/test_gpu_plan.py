@@ -42,6 +42,9 @@ def _check_plan(p, mask):
         ent, counts = fn(cls, group)
         np.testing.assert_array_equal(p[f"{name}_count"], counts, err_msg=name)
         np.testing.assert_array_equal(p[f"{name}_list"].view(np.uint32), ent, err_msg=name)
+        if name != "dkdv":  # work order: descending count, ties by ascending item (a stable sort of -count)
+            flat = np.asarray(counts).reshape(-1)
+            np.testing.assert_array_equal(p[f"{name}_order"], np.argsort(-flat, kind="stable"), err_msg=name)
     # row / column bit masks, bit-exact on every PARTIAL tile (the only ones the kernels read)
     qbits, kbits = tilemap.tile_bits(mask, 64)
     part = cls == tilemap.PARTIAL
