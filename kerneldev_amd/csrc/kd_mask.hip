@@ -186,28 +186,15 @@ __global__ void k_codes(MetaArgs m, const uint32_t* rep, uint32_t* codes) {
 }
 
 // ---- 64x64 tile classifier ---------------------------------------------
-// The rule in table form for a fixed query code: bit F of `lo` says whether a
-// key with flag nibble F is seen (A_i & F_j != 0); `hi` adds C_j for a context
-// query, used where i >= j (C & C & i >= j); both are stored twice so that the
-// key code's low 5 bits index them.  `rsh` = R_i << 8, or a value no code
-// matches when R_i = 0, so ((kc ^ rsh) < 256) is exactly "same span".
-struct QTab {
-  uint32_t lo, hi, rsh;
-};
-KD_DEV QTab qtab(uint32_t qc) {
-  const uint32_t A = (qc >> 4) & 15u;
-  const uint32_t t = ((A & FLAG_P) ? 0xAAAAu : 0u) | ((A & FLAG_S) ? 0xCCCCu : 0u) |
-                     ((A & FLAG_M) ? 0xF0F0u : 0u) | ((A & FLAG_C) ? 0xFF00u : 0u);
-  const uint32_t th = t | ((qc & FLAG_C) ? 0xFF00u : 0u);
-  const uint32_t R = qc >> 8;
-  return QTab{t * 0x10001u, th * 0x10001u, R ? (R << 8) : 0xFFFFFF00u};
-}
-KD_DEV uint32_t qtab_allow(const QTab& q, uint32_t kc, bool i_ge_j) {
-  return ((((i_ge_j ? q.hi : q.lo) >> (kc & 31u)) & 1u) | ((kc ^ q.rsh) < 256u ? 1u : 0u));
-}
-// One wave per tile: lane = query row, loop over the tile's 64 keys, building
-// the row's 64-bit mask; PARTIAL tiles also store the row masks and, through
-// 64 ballots (column j of the tile = ballot of bit j), the column masks.
+// One wave per tile.  The row mask of query lane i over the tile's 64 keys is
+// built from wave-wide ballots instead of 64 per-key tests: with F_j the key
+// flags and A_i the query's allowed flags, A_i & F_j != 0 selects the ballot
+// of keys carrying each flag of A_i; context queries add context keys at
+// j <= i (all of them below the diagonal, none above); and for the same-span
+// term the wave walks the distinct span representatives among the tile's keys
+// (usually one to three), one ballot each.  That is the rule of allow(), term
+// for term.  PARTIAL tiles also store the row masks and, through 64 ballots
+// (column j of the tile = ballot of bit j), the column masks.
 __global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, int nT, uint8_t* cls,
                                                  int32_t* nnz, uint64_t* qbits, uint64_t* kbits) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -223,23 +210,28 @@ __global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, i
   if (kt >= nT) return;
   const int i = qt * 64 + lane;
   const uint32_t qc = (i < T) ? codes[int64_t(b) * T + i] : 0u;
-  const QTab q = qtab(qc);
-  uint32_t lo = 0, hi = 0;
-  if (kt != qt) {  // off the diagonal every key is on one side of every query
-    const bool below = kt < qt;
-#pragma unroll 8
-    for (int x = 0; x < 32; ++x) {
-      lo |= qtab_allow(q, s_k[wave * 64 + x], below) << x;
-      hi |= qtab_allow(q, s_k[wave * 64 + 32 + x], below) << x;
-    }
-  } else {
-#pragma unroll 8
-    for (int x = 0; x < 32; ++x) {
-      lo |= qtab_allow(q, s_k[wave * 64 + x], lane >= x) << x;
-      hi |= qtab_allow(q, s_k[wave * 64 + 32 + x], lane >= 32 + x) << x;
-    }
+  const uint32_t kc = s_k[wave * 64 + lane];  // key j = 64 kt + lane (code 0 past T: allows nothing)
+  const uint32_t A = (qc >> 4) & 15u;
+  const uint64_t kp = __builtin_amdgcn_ballot_w64((kc & FLAG_P) != 0u);
+  const uint64_t ks = __builtin_amdgcn_ballot_w64((kc & FLAG_S) != 0u);
+  const uint64_t km = __builtin_amdgcn_ballot_w64((kc & FLAG_M) != 0u);
+  const uint64_t kcx = __builtin_amdgcn_ballot_w64((kc & FLAG_C) != 0u);
+  uint64_t row = ((A & FLAG_P) ? kp : 0u) | ((A & FLAG_S) ? ks : 0u) | ((A & FLAG_M) ? km : 0u) |
+                 ((A & FLAG_C) ? kcx : 0u);
+  if (qc & FLAG_C) {  // C & C & i >= j
+    const uint64_t le = lane == 63 ? ~uint64_t(0) : (uint64_t(2) << lane) - 1u;  // keys j <= i on the diagonal
+    row |= kcx & (kt < qt ? ~uint64_t(0) : (kt == qt ? le : uint64_t(0)));
   }
-  int cnt = __builtin_popcount(lo) + __builtin_popcount(hi);
+  // same span: R_i != 0 and R_j == R_i, one ballot per distinct R_j of the tile
+  const uint32_t kr = kc >> 8, qr = qc >> 8;
+  uint64_t todo = __builtin_amdgcn_ballot_w64(kr != 0u);
+  while (todo != 0u) {  // uniform
+    const uint32_t v = uint32_t(__builtin_amdgcn_readlane(int(kr), int(__builtin_ctzll(todo))));
+    const uint64_t same = __builtin_amdgcn_ballot_w64(kr == v);
+    todo &= ~same;
+    if (qr == v) row |= same;
+  }
+  int cnt = __builtin_popcountll(row);
   for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off);
   const int64_t o = (int64_t(b) * nT + qt) * nT + kt;
   const uint8_t k = cnt == 0 ? TILE_EMPTY : (cnt == 64 * 64 ? TILE_FULL : TILE_PARTIAL);
@@ -248,7 +240,6 @@ __global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, i
     if (nnz != nullptr) nnz[o] = cnt;
   }
   if (k == TILE_PARTIAL) {  // wave-uniform
-    const uint64_t row = (uint64_t(hi) << 32) | lo;
     qbits[o * 64 + lane] = row;
     uint64_t col = 0;
     for (int j = 0; j < 64; ++j) {
