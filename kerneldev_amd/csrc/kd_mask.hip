@@ -71,20 +71,15 @@ __global__ __launch_bounds__(1024) void k_runs(MetaArgs m, uint32_t* runs, int64
   if (tid == int(blockDim.x) - 1) run_count[b] = incl;
 }
 
-__global__ void k_rep(MetaArgs m, const uint32_t* runs, const int64_t* run_sid, const int32_t* run_count,
-                      uint32_t* rep) {
-  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (idx >= int64_t(m.B) * m.T) return;
-  const int b = int(idx / m.T), j = int(idx % m.T);
-  int64_t sid;
-  if (!eligible(m, b, j, &sid)) return;
+// The representative of eligible token t of row b: the first listed run
+// with its id (always found: t's own run is listed).
+KD_DEV uint32_t run_rep(const MetaArgs& m, const uint32_t* runs, const int64_t* run_sid, const int32_t* run_count,
+                        int b, int64_t sid) {
   const int n = run_count[b];
   const int64_t* rs = run_sid + int64_t(b) * m.T;
-  for (int i = 0; i < n; ++i)
-    if (rs[i] == sid) {  // always found: j's own run is listed
-      rep[idx] = runs[int64_t(b) * m.T + i];
-      return;
-    }
+  int i = 0;
+  while (i < n - 1 && rs[i] != sid) ++i;
+  return runs[int64_t(b) * m.T + i];
 }
 
 // ---- token ids -> metadata (kd_plan_build_tokens) -------------------------
@@ -156,7 +151,10 @@ __global__ __launch_bounds__(256) void k_token_meta(kd_token_args a, uint8_t* in
 }
 
 // ---- token codes -------------------------------------------------------
-__global__ void k_codes(MetaArgs m, const uint32_t* rep, uint32_t* codes) {
+// runs / run_sid / run_count: the run-start lists of k_runs (formula mode
+// with span ids); rep receives each eligible token's representative.
+__global__ void k_codes(MetaArgs m, const uint32_t* runs, const int64_t* run_sid, const int32_t* run_count,
+                        uint32_t* rep, uint32_t* codes) {
   const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= int64_t(m.B) * m.T) return;
   const int b = int(idx / m.T), t = int(idx % m.T);
@@ -179,7 +177,11 @@ __global__ void k_codes(MetaArgs m, const uint32_t* rep, uint32_t* codes) {
       if (S) acc |= FLAG_C;               // span_to_context
       if (M) acc |= FLAG_S | FLAG_P;      // maskq_to_spans, maskq_to_cls
       code = (P ? FLAG_P : 0u) | (S ? FLAG_S : 0u) | (M ? FLAG_M : 0u) | (C ? FLAG_C : 0u) | (acc << 4);
-      if (m.span_id != nullptr && S && sid > 0) code |= (rep[idx] + 1u) << 8;  // same_span
+      if (m.span_id != nullptr && S && sid > 0) {  // same_span: eligible, so k_runs listed its run
+        const uint32_t r = run_rep(m, runs, run_sid, run_count, b, sid);
+        rep[idx] = r;
+        code |= (r + 1u) << 8;
+      }
     }
   }
   codes[idx] = code;
@@ -389,14 +391,14 @@ int launch_plan(const MetaArgs& m, uint8_t* plan, hipStream_t st) {
   uint8_t* cls = plan + L.cls;
   int32_t* nnz = reinterpret_cast<int32_t*>(plan + L.nnz);
   const int64_t BT = int64_t(m.B) * m.T;
-  if (m.mode == KD_MODE_FORMULA && m.span_id != nullptr && m.in_span != nullptr) {
-    uint32_t* runs = reinterpret_cast<uint32_t*>(plan + L.runs);
-    int64_t* run_sid = reinterpret_cast<int64_t*>(plan + L.run_sid);
-    int32_t* run_count = reinterpret_cast<int32_t*>(plan + L.run_count);
+  uint32_t* runs = reinterpret_cast<uint32_t*>(plan + L.runs);
+  int64_t* run_sid = reinterpret_cast<int64_t*>(plan + L.run_sid);
+  int32_t* run_count = reinterpret_cast<int32_t*>(plan + L.run_count);
+  // (k_codes reads the run lists only for eligible tokens, which exist only in this mode)
+  if (m.mode == KD_MODE_FORMULA && m.span_id != nullptr && m.in_span != nullptr)
     hipLaunchKernelGGL(k_runs, dim3(unsigned(m.B)), dim3(1024), 0, st, m, runs, run_sid, run_count);
-    hipLaunchKernelGGL(k_rep, dim3(unsigned((BT + 255) / 256)), dim3(256), 0, st, m, runs, run_sid, run_count, rep);
-  }
-  hipLaunchKernelGGL(k_codes, dim3(unsigned((BT + 255) / 256)), dim3(256), 0, st, m, rep, codes);
+  hipLaunchKernelGGL(k_codes, dim3(unsigned((BT + 255) / 256)), dim3(256), 0, st, m, runs, run_sid, run_count, rep,
+                     codes);
   hipLaunchKernelGGL(k_tilemap, dim3((L.nT + 3) / 4, L.nT, m.B), dim3(256), 0, st, codes, m.T, L.nT, cls, nnz,
                      reinterpret_cast<uint64_t*>(plan + L.qbits), reinterpret_cast<uint64_t*>(plan + L.kbits));
   ListSpecs specs;
