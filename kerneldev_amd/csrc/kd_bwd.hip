@@ -327,14 +327,13 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
         for (int r = 0; r < 16; ++r) s[kb][r] = mask_bit(s[kb][r], w, 16 * (r >> 3) + (r & 7));
       }
     }
-    // P = exp2(S c - LSE), in place: independent of dP, so this VALU work can
-    // interleave with the dP MFMAs that follow in the same basic block
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kb][r] = fast_exp2(__builtin_fmaf(s[kb][r], sl2, -lse));
+    // dP^T, started from -Delta, with P = exp2(S c - LSE) computed in place
+    // between its MFMAs: EPI exponentials after each MFMA, held there by
+    // fences that only scalar work may cross (left free, the scheduler puts
+    // all of them ahead of the first dP MFMA)
     {
       constexpr int NS = 2 * DS, PF = DQ_PF;
+      constexpr int EPI = 32 / NS;  // exponentials per dP step
       auto read = [&](int i) {
         return *reinterpret_cast<const u32x4*>(vt + raddr[i >> 1] + (i & 1) * 32 * TL::ROWB);
       };
@@ -343,11 +342,16 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
       for (int i = 0; i < PF; ++i) av[i] = read(i);
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
-        __builtin_amdgcn_sched_barrier(0x406);
+        __builtin_amdgcn_sched_barrier(0x4);
         dp[i & 1] = mfma32x32x16<E>(av[i % PF], dof[i >> 1], (i >> 1) == 0 ? neg_delta : dp[i & 1]);
         if (i + PF < NS) av[i % PF] = read(i + PF);
+#pragma unroll
+        for (int u = 0; u < EPI; ++u) {
+          const int kb = i & 1, r = EPI * (i >> 1) + u;
+          s[kb][r] = fast_exp2(__builtin_fmaf(s[kb][r], sl2, -lse));
+        }
       }
-      __builtin_amdgcn_sched_barrier(0x406);
+      __builtin_amdgcn_sched_barrier(0x4);
     }
     u32x4 dsb[2][2];
 #pragma unroll
