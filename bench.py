@@ -54,8 +54,8 @@ USEFUL_FWD, USEFUL_BWD = 4, 10
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs scaled by a 1 GiB copy's counts
 # (profiles/attn_config4_{bf16,fp8_e4m3}_hbm_traffic.md); re-measured whenever the kernels change.
 CONFIG4_TRAFFIC_BYTES = {
-    "bf16": {"fwd": 934.8e6, "dq": 1339.4e6, "dkdv": 1106.8e6},
-    "fp8_e4m3": {"fwd": 696.8e6, "dq": 1433.1e6, "dkdv": 1221.5e6},
+    "bf16": {"fwd": 1057.7e6, "dq": 1435.8e6, "dkdv": 1103.9e6},
+    "fp8_e4m3": {"fwd": 807.0e6, "dq": 1527.8e6, "dkdv": 1216.1e6},
 }
 
 
