@@ -41,12 +41,6 @@ KD_DEV bool allow(uint32_t qc, uint32_t kc, int i, int j) {
          (((qc >> 8) != 0u) & ((qc >> 8) == (kc >> 8)));
 }
 
-// Host-and-device version for the classifier (same expression).
-__host__ __device__ inline bool allow_hd(uint32_t qc, uint32_t kc, int i, int j) {
-  return (((qc >> 4) & kc & 0xFu) != 0u) || (((qc & kc & FLAG_C) != 0u) && (i >= j)) ||
-         (((qc >> 8) != 0u) && ((qc >> 8) == (kc >> 8)));
-}
-
 // s if bit `pos` of w is set, else -inf (v_bfe_i32 + v_bfi_b32).
 KD_DEV float mask_bit(float s, uint32_t w, int pos) {
   const uint32_t m = uint32_t(__builtin_amdgcn_sbfe(int(w), pos, 1u));
@@ -78,25 +72,11 @@ template <> KD_DEV uint32_t pack2<F16>(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
 }
 
-// Sum of the two 16-bit values packed in one dword, in fp32 (exact).
-template <class E> KD_DEV float sum2(uint32_t w);
-template <> KD_DEV float sum2<BF16>(uint32_t w) {
-  return __uint_as_float(w << 16) + __uint_as_float(w & 0xFFFF0000u);
-}
-template <> KD_DEV float sum2<F16>(uint32_t w) {
-  const f16x2 h = __builtin_bit_cast(f16x2, w);
-  return float(h[0]) + float(h[1]);
-}
-
 template <class E> KD_DEV float to_f32(uint16_t bits);
 template <> KD_DEV float to_f32<BF16>(uint16_t bits) { return __uint_as_float(uint32_t(bits) << 16); }
 template <> KD_DEV float to_f32<F16>(uint16_t bits) {
   return float(__builtin_bit_cast(_Float16, bits));
 }
-
-// Lo/hi 16-bit halves of two dwords packed into one dword (v_perm_b32).
-KD_DEV uint32_t pack_lo(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x05040100u); }
-KD_DEV uint32_t pack_hi(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x07060302u); }
 
 // Row permutation used for the A operand of 32x32 MFMAs whose output feeds the
 // next MFMA's B operand straight from registers.  The 32x32 f32 accumulator
@@ -107,8 +87,6 @@ KD_DEV uint32_t pack_hi(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y
 // must supply for k-step t of the following 32x32x16 MFMA.
 KD_DEV int sigma(int rho) { return (rho & ~12) | ((rho & 4) << 1) | ((rho & 8) >> 1); }
 
-KD_DEV float wave_max32(float v) { return fmaxf(v, __shfl_xor(v, 32)); }
-KD_DEV float wave_sum32(float v) { return v + __shfl_xor(v, 32); }
 
 // Inclusive scan of one int per thread over the workgroup (up to 16 waves;
 // s_warp: 16 ints of LDS).  Every thread must call it.

@@ -159,14 +159,6 @@ KD_DEV void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" :::
 template <class T>
 KD_DEV void settle(T& v) { asm volatile("" : "+v"(v)); }
 
-template <int I, int N, class F>
-KD_DEV void static_for(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_for<I + 1, N>(f);
-  }
-}
-
 KD_DEV void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // wait until at most N vector memory loads of this wave are outstanding
 template <int N>
@@ -215,23 +207,6 @@ struct ScoreOp<E, D, false> {
 #pragma unroll
     for (int st = 0; st < NK; ++st) asm volatile("" : "+v"(b[st]));
   }
-  // s += X[32 kb + rows] Y^T
-  KD_DEV void mma(const uint8_t* tile, int kb, f32x16& s) const {
-#pragma unroll
-    for (int st = 0; st < NK; ++st)
-      s = mfma32x32x16<E>(*reinterpret_cast<const u32x4*>(tile + addr[st] + kb * 32 * TL::ROWB), b[st], s);
-  }
-  // s[q] += X[32 kb + rows] Y_q^T for N B operands sharing each A read
-  // (addresses of op[0]; every op was init()-ed with the same row)
-  template <int N>
-  KD_DEV static void mma_n(const uint8_t* tile, int kb, const ScoreOp (&op)[N], f32x16 (&s)[N]) {
-#pragma unroll
-    for (int st = 0; st < NK; ++st) {
-      const u32x4 av = *reinterpret_cast<const u32x4*>(tile + op[0].addr[st] + kb * 32 * TL::ROWB);
-#pragma unroll
-      for (int q = 0; q < N; ++q) s[q] = mfma32x32x16<E>(av, op[q].b[st], s[q]);
-    }
-  }
 };
 
 template <class E, int D>
@@ -268,28 +243,6 @@ struct ScoreOp<E, D, true> {
   KD_DEV void settle() {
 #pragma unroll
     for (int st = 0; st < NK; ++st) asm volatile("" : "+v"(b[st]));
-  }
-
-  KD_DEV void mma(const uint8_t* tile, int kb, f32x16& s) const {
-#pragma unroll
-    for (int st = 0; st < NK; ++st) {
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(tile + addr[st][0] + kb * 32 * TL::ROWB);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(tile + addr[st][1] + kb * 32 * TL::ROWB);
-      const i32x8 av = {int(lo[0]), int(lo[1]), int(lo[2]), int(lo[3]), int(hi[0]), int(hi[1]), int(hi[2]), int(hi[3])};
-      s = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, b[st], s, 0, 0, 0, 127, 0, 127);
-    }
-  }
-  template <int N>
-  KD_DEV static void mma_n(const uint8_t* tile, int kb, const ScoreOp (&op)[N], f32x16 (&s)[N]) {
-#pragma unroll
-    for (int st = 0; st < NK; ++st) {
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(tile + op[0].addr[st][0] + kb * 32 * TL::ROWB);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(tile + op[0].addr[st][1] + kb * 32 * TL::ROWB);
-      const i32x8 av = {int(lo[0]), int(lo[1]), int(lo[2]), int(lo[3]), int(hi[0]), int(hi[1]), int(hi[2]), int(hi[3])};
-#pragma unroll
-      for (int q = 0; q < N; ++q)
-        s[q] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, op[q].b[st], s[q], 0, 0, 0, 127, 0, 127);
-    }
   }
 };
 
