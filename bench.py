@@ -8,7 +8,8 @@ every input already resident in HBM: tile classifier (plan), forward, Delta,
 dQ and dK/dV -- the launches ``flash_attention()`` followed by ``backward()``
 issues, called through the C ABI on preallocated buffers.  Config 4 (the
 metric's workload) includes its Hadamard incoherent processing: Q and K are
-rotated before the forward and dQ, dK rotated back after the backward.
+rotated before the forward, and the dQ and dK/dV kernels rotate dQ, dK back in
+their epilogues (``dqk_signs``), as ``flash_attention(..., hadamard=True)`` does.
 The timed region is bracketed by ``torch.cuda.synchronize()``; HIP events on
 the launch stream sit between the five kernels of every timed step, so each
 kernel's average duration is measured live.
@@ -107,11 +108,11 @@ class Step:
         self.hadamard = hadamard
         self.fp8 = qk_dtype == "fp8_e4m3"
         if hadamard:
-            # Q' = Q R, K' = K R before attention; dQ = dQ' R^T, dK = dK' R^T after
+            # Q' = Q R, K' = K R before attention; the backward kernels return
+            # dQ = dQ' R^T, dK = dK' R^T (dqk_signs)
             self.signs = generate_hadamard_signs(D, 0, device=dev)
             self.q_in, self.k_in = q, k
             q, k = torch.empty_like(q), torch.empty_like(k)
-            self.dq_in, self.dk_in = torch.empty_like(q), torch.empty_like(k)
             self.rot = [self._rot_args(_lib, _dtype_code, _strides3, src, dst, inverse)
                         for src, dst, inverse in ((self.q_in, q, 0), (self.k_in, k, 0))]
         self.shape = (B, H, T, D)
@@ -134,6 +135,8 @@ class Step:
         a.dq_strides, a.dk_strides, a.dv_strides = _strides3(self.dq), _strides3(self.dk), _strides3(self.dv)
         a.delta = self.delta.data_ptr()
         a.o_lo = self.o_lo.data_ptr()
+        if hadamard:
+            a.dqk_signs = self.signs.data_ptr()
         if self.fp8:
             # e4m3 copies of Q' and K' with per-(b, h) scales; the absmax comes
             # from the rotation pass (Hadamard) or one torch reduction
@@ -166,12 +169,9 @@ class Step:
             m.span_id_strides[0], m.span_id_strides[1] = t.stride()
             m.span_id_dtype = _lib.KD_I64 if t.dtype == torch.int64 else _lib.KD_I32
         self.margs = m
-        if hadamard:
-            self.unrot = [self._rot_args(_lib, _dtype_code, _strides3, src, dst, 1)
-                          for src, dst in ((self.dq, self.dq_in), (self.dk, self.dk_in))]
-            if self.fp8:
-                for i, r in enumerate(self.rot):
-                    r.amax = self.amax[i].data_ptr()
+        if hadamard and self.fp8:
+            for i, r in enumerate(self.rot):
+                r.amax = self.amax[i].data_ptr()
         self.stream = torch.cuda.current_stream(dev)
         self.sptr = ctypes.c_void_p(self.stream.cuda_stream)
         self.pptr = ctypes.c_void_p(self.plan.data_ptr())
@@ -208,9 +208,6 @@ class Step:
             ("dq", lambda: ck(L.kd_attn_bwd_dq_delta(a, self.pptr, self.sptr), "dq")),  # with Delta
             ("dkdv", lambda: ck(L.kd_attn_bwd_dkdv(a, self.pptr, self.sptr), "dkdv")),
         ]
-        if self.hadamard:
-            out.append(("unrot_dqdk",
-                        lambda: [ck(L.kd_hadamard(ctypes.byref(r), self.sptr), "unrot") for r in self.unrot]))
         return tuple(out)
 
     def run(self, events=None):

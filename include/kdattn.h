@@ -102,6 +102,10 @@ typedef struct kd_attn_args {
                                    [B, H, T, D] (kd_quant_fp8): when both are given, S = Q K^T
                                    is computed from them on fp8 MFMA, times q_scale * k_scale */
   const float *q_scale, *k_scale; /* [B, H] dequantisation scales of q8 / k8 */
+  const float *dqk_signs;       /* optional [D] of +1 / -1 (bwd): q and k are rotated inputs
+                                   Q R, K R with R = diag(signs) H_D / sqrt(D) (kd_hadamard), and
+                                   dQ, dK are returned for the unrotated Q, K, i.e. times R^T,
+                                   applied in the kernels' epilogues; NULL: dQ, dK as computed */
   int32_t B, H, T, D;
   int32_t dtype;                /* KD_BF16 / KD_F16 */
   float sm_scale;

@@ -173,11 +173,18 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
             is_prefix: torch.Tensor | None, sm_scale: float, mode: int, need_lo: bool,
             q8: torch.Tensor | None = None, k8: torch.Tensor | None = None,
             q_scale: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
-            bthd: bool = False, plan_in: torch.Tensor | None = None,
-            ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+            bthd: bool = False, plan_in: torch.Tensor | None = None, signs: torch.Tensor | None = None,
+            ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     B, H, T, D = q.shape
     # a caller's plan is used as is (and not returned: outputs may not alias inputs)
     plan = plan_in if plan_in is not None else build_plan(B, T, D, q.device, mode, in_span, span_id, is_prefix, lens)
+    # signs: attention of Q R and K R (returned for the backward, which hands
+    # back dQ, dK for q, k themselves)
+    q_r, k_r = q.new_empty(0), k.new_empty(0)  # distinct tensors: outputs may not alias
+    if signs is not None:
+        from .hadamard import _launch
+        q = q_r = _launch(q, signs, False)
+        k = k_r = _launch(k, signs, False)
     o = _new_out(B, H, T, D, q, bthd)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
     # rounding residual of O, kept for the backward's Delta (see kd_bwd.hip)
@@ -188,17 +195,20 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
     a.lse = lse.data_ptr()
     a.o_lo = o_lo.data_ptr() if need_lo else None
     _lib.check(_lib.load().kd_attn_fwd(ctypes.byref(a), _ptr(plan), _stream(q.device)), "kd_attn_fwd")
-    return o, lse, (plan if plan_in is None else plan.new_empty(0)), o_lo
+    return o, lse, (plan if plan_in is None else plan.new_empty(0)), o_lo, q_r, k_r
 
 
 @_fwd_op.register_fake
 def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8=None, k8=None,
-              q_scale=None, k_scale=None, bthd=False, plan_in=None):
+              q_scale=None, k_scale=None, bthd=False, plan_in=None, signs=None):
     B, H, T, D = q.shape
+    rot_shape = (B, H, T, D) if signs is not None else (0,)
     return (_new_out(B, H, T, D, q, bthd),
             torch.empty((B, H, T), dtype=torch.float32, device=q.device),
             torch.empty(_lib.plan_bytes(B, T, D) if plan_in is None else 0, dtype=torch.uint8, device=q.device),
-            torch.empty((B, H, T, D) if need_lo else (0,), dtype=q.dtype, device=q.device))
+            torch.empty((B, H, T, D) if need_lo else (0,), dtype=q.dtype, device=q.device),
+            torch.empty(rot_shape, dtype=q.dtype, device=q.device),
+            torch.empty(rot_shape, dtype=k.dtype, device=k.device))
 
 
 @torch.library.custom_op("kdattn::bwd", mutates_args=(), device_types=("cuda",))
@@ -206,6 +216,7 @@ def _bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, 
             do: torch.Tensor, plan: torch.Tensor, sm_scale: float, o_lo: torch.Tensor,
             q8: torch.Tensor | None = None, k8: torch.Tensor | None = None,
             q_scale: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
+            dqk_signs: torch.Tensor | None = None,
             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     B, H, T, D = q.shape
     do = _kernel_ready(do)
@@ -222,33 +233,42 @@ def _bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, 
     a.delta = delta.data_ptr()
     a.o_lo = o_lo.data_ptr() if o_lo.numel() > 0 else None
     _set_fp8(a, _fp8_tuple(q8, k8, q_scale, k_scale))
+    a.dqk_signs = dqk_signs.data_ptr() if dqk_signs is not None else None
     _lib.check(_lib.load().kd_attn_bwd(ctypes.byref(a), _ptr(plan), _stream(q.device)), "kd_attn_bwd")
     return dq, dk, dv
 
 
 @_bwd_op.register_fake
-def _bwd_fake(q, k, v, o, lse, do, plan, sm_scale, o_lo, q8=None, k8=None, q_scale=None, k_scale=None):
+def _bwd_fake(q, k, v, o, lse, do, plan, sm_scale, o_lo, q8=None, k8=None, q_scale=None, k_scale=None,
+              dqk_signs=None):
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
 def _setup_context(ctx, inputs, output):
-    q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8, k8, q_scale, k_scale, bthd, plan_in = inputs
-    o, lse, plan, o_lo = output
+    (q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8, k8, q_scale, k_scale, bthd, plan_in,
+     signs) = inputs
+    o, lse, plan, o_lo, q_r, k_r = output
     if plan_in is not None:
         plan = plan_in
+    ctx.mark_non_differentiable(q_r, k_r)
     ctx.fp8 = q8 is not None
+    ctx.rot = signs is not None
+    if ctx.rot:  # the backward recomputes from the rotated operands and rotates dQ, dK back
+        q, k = q_r, k_r
     extra = (q8, k8, q_scale, k_scale) if ctx.fp8 else ()
-    ctx.save_for_backward(q, k, v, o, lse, plan, o_lo, *extra)
+    ctx.save_for_backward(q, k, v, o, lse, plan, o_lo, *((signs,) if ctx.rot else ()), *extra)
     ctx.sm_scale = sm_scale
 
 
-def _backward(ctx, do, dlse, dplan, do_lo):
+def _backward(ctx, do, dlse, dplan, do_lo, dq_r, dk_r):
     # dlse is ignored, as in original_kernel.py:1965-1992.  With fp8 scores the
     # backward recomputes P from the same fp8 Q8 K8^T and forms dQ = dS K,
     # dK = dS^T Q from the 16-bit operands: the straight-through estimator.
-    q, k, v, o, lse, plan, o_lo, *extra = ctx.saved_tensors
-    dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, ctx.sm_scale, o_lo, *extra)
-    return dq, dk, dv, None, None, None, None, None, None, None, None, None, None, None, None, None
+    q, k, v, o, lse, plan, o_lo, *rest = ctx.saved_tensors
+    signs = rest.pop(0) if ctx.rot else None
+    fp8 = tuple(rest) if ctx.fp8 else (None, None, None, None)
+    dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, ctx.sm_scale, o_lo, *fp8, dqk_signs=signs)
+    return dq, dk, dv, None, None, None, None, None, None, None, None, None, None, None, None, None, None
 
 
 _fwd_op.register_autograd(_backward, setup_context=_setup_context)
@@ -363,18 +383,21 @@ def flash_attention(
         q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
     elif in_dtype not in (torch.bfloat16, torch.float16):
         raise ValueError(f"unsupported dtype {in_dtype}")
-    from .hadamard import generate_hadamard_signs, hadamard_absmax, hadamard_transform, quantize_fp8
+    from .hadamard import generate_hadamard_signs, hadamard_absmax, quantize_fp8
 
     amax_q = amax_k = None
+    fused_signs = None
     if hadamard:
-        # (Q R)(K R)^T = Q K^T with R = diag(s) H_d / sqrt(d); autograd maps
-        # dQ' and dK' back through R^T (hadamard.py).  For fp8 the rotation
-        # pass also yields the per-(b, h) absmax the scales need.
+        # (Q R)(K R)^T = Q K^T with R = diag(s) H_d / sqrt(d).  16-bit scores:
+        # the attention op rotates Q and K itself and its backward kernels
+        # return dQ' R^T, dK' R^T directly.  fp8: the rotation pass also yields
+        # the per-(b, h) absmax the scales need, and autograd maps dQ', dK'
+        # back through R^T (hadamard.py).
         signs = generate_hadamard_signs(D, hadamard_seed, device=device)
         if qk_dtype == "fp8_e4m3":
             (q, amax_q), (k, amax_k) = hadamard_absmax(q, signs), hadamard_absmax(k, signs)
         else:
-            q, k = hadamard_transform(q, signs), hadamard_transform(k, signs)
+            fused_signs = signs
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     fp8 = ()
     if qk_dtype == "fp8_e4m3":
@@ -382,9 +405,9 @@ def flash_attention(
         fp8 = (q8, k8, q_scale, k_scale)
 
     need_lo = torch.is_grad_enabled() and any(x.requires_grad for x in (q, k, v))
-    o, lse, plan_t, _ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode), need_lo,
-                                *(fp8 or (None, None, None, None)), bthd=out_layout == "bthd",
-                                plan_in=None if plan is None else plan.tensor)
+    o, lse, plan_t, *_ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode), need_lo,
+                                 *(fp8 or (None, None, None, None)), bthd=out_layout == "bthd",
+                                 plan_in=None if plan is None else plan.tensor, signs=fused_signs)
     if plan is not None:
         plan_t = plan.tensor
     if in_dtype == torch.float32:

@@ -102,6 +102,45 @@ KD_DEV void store_rows_T(uint16_t* g, const f32x16 (&acc)[D / 32], float scale, 
   }
 }
 
+// The rows of a transposed accumulator times R^T, R = diag(s) H_D / sqrt(D)
+// (the inverse of kd_hadamard's rotation), stored like store_rows_T: the
+// Walsh-Hadamard butterflies over d in registers, then the signs and
+// scale / sqrt(D).  Lane half hf holds d = 32 db + 8 gg + 4 hf + i in
+// register r = 16 db + 4 gg + i of acc, so bits 0, 1, 3, 4, 5, 6 of d pair
+// registers of the lane and bit 2 pairs the two lane halves.
+template <class E, int D>
+KD_DEV void store_rows_T_unrot(uint16_t* g, f32x16 (&acc)[D / 32], float scale, int hf, const float* signs) {
+  constexpr int NR = D / 2;
+#pragma unroll
+  for (int bit = 1; bit < NR; bit <<= 1)
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+      if (!(r & bit)) {
+        const float x = acc[r >> 4][r & 15], y = acc[(r | bit) >> 4][(r | bit) & 15];
+        acc[r >> 4][r & 15] = x + y;
+        acc[(r | bit) >> 4][(r | bit) & 15] = x - y;
+      }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {  // p[0]: the value of the hf = 0 lane, p[1]: of the hf = 1 lane
+    const float x = acc[r >> 4][r & 15];
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    acc[r >> 4][r & 15] = hf ? __uint_as_float(p[0]) - __uint_as_float(p[1]) : __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  }
+  const float c = scale * (D == 128 ? 0.088388347648318440f : 0.125f);  // scale / sqrt(D)
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+    for (int gg = 0; gg < 4; ++gg) {
+      const int d0 = 32 * db + 8 * gg + 4 * hf;
+      float f[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) f[i] = acc[db][4 * gg + i] * (signs[d0 + i] * c);
+      const u32x2 w = {pack2<E>(f[0], f[1]), pack2<E>(f[2], f[3])};
+      *reinterpret_cast<u32x2*>(g + d0) = w;
+    }
+  }
+}
+
 // Byte offsets of the transposed A-operand reads (tile^T, 32 columns x 16 rows
 // per MFMA k-step) for this lane: [db][half], k-step ks adds ks * 16 rows.
 template <int D>
@@ -394,7 +433,8 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
 
   if (qvalid) {
     uint16_t* g = static_cast<uint16_t*>(a.dq) + b * a.dq_strides[0] + h * a.dq_strides[1] + qrow * a.dq_strides[2];
-    store_rows_T<E, D>(g, acc, a.sm_scale, hf);
+    if (a.dqk_signs != nullptr) store_rows_T_unrot<E, D>(g, acc, a.sm_scale, hf, a.dqk_signs);
+    else store_rows_T<E, D>(g, acc, a.sm_scale, hf);
   }
 }
 
@@ -735,7 +775,10 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
     uint16_t* g = role == 0
         ? static_cast<uint16_t*>(a.dv) + b * a.dv_strides[0] + h * a.dv_strides[1] + krow * a.dv_strides[2]
         : static_cast<uint16_t*>(a.dk) + b * a.dk_strides[0] + h * a.dk_strides[1] + krow * a.dk_strides[2];
-    store_rows_T<E, D>(g, acc, role == 0 ? 1.f : a.sm_scale, hf);
+    if (__builtin_amdgcn_readfirstlane(role) == 1 && a.dqk_signs != nullptr)  // dK, rotated back
+      store_rows_T_unrot<E, D>(g, acc, a.sm_scale, hf, a.dqk_signs);
+    else
+      store_rows_T<E, D>(g, acc, role == 0 ? 1.f : a.sm_scale, hf);
   }
 }
 

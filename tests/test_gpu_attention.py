@@ -233,7 +233,7 @@ def test_split_backward_entry_points_match_fused(dev):
     q, k, v, do = (x.to(dev) for x in qkvdo(2, 2, 1024, 128, seed=22))
     meta = [x.to(dev) for x in (in_span, span_id, is_prefix)]
     sc = 128 ** -0.5
-    o, lse, plan, o_lo = _fwd_op(q, k, v, None, *meta, sc, 0, True)
+    o, lse, plan, o_lo, *_ = _fwd_op(q, k, v, None, *meta, sc, 0, True)
     lib = _lib.load()
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     outs = []

@@ -76,3 +76,53 @@ def test_attention_with_hadamard_matches_unrotated_reference(dev):
     assert_close("dq", qd.grad, ref["dq"])
     assert_close("dk", kd.grad, ref["dk"])
     assert_close("dv", vd.grad, ref["dv"])
+
+
+def test_backward_epilogue_rotation_matches_separate_pass(dev):
+    """kd_attn_bwd with dqk_signs == kd_attn_bwd, then kd_hadamard(inverse) on dQ', dK'.
+
+    The epilogue rotates the fp32 accumulators and rounds once; the separate
+    pass rounds dQ' to bf16 first, so the two differ by bf16 roundings only:
+    rel-RMS <= 4e-3 and max-abs <= 2^-6 max|ref|.  dV is untouched (bit-equal).
+    """
+    import ctypes
+
+    from kerneldev_amd import _lib, hadamard_transform
+    from kerneldev_amd.attention import _attn_args, _fwd_op, _ptr, _strides3
+    from kerneldev_amd.synth import CONFIG3_LAYOUT, cocktail_batch, qkvdo
+
+    print("epilogue rotation vs separate inverse pass, D = 64 and 128", flush=True)
+    for D in (64, 128):
+        tokens, in_span, span_id, is_prefix = cocktail_batch(2, 1024, CONFIG3_LAYOUT, seed=31)
+        q, k, v, do = (x.to(dev) for x in qkvdo(2, 2, 1024, D, seed=32))
+        signs = generate_hadamard_signs(D, 5, device=dev)
+        qr, kr = hadamard_transform(q, signs), hadamard_transform(k, signs)
+        meta = [x.to(dev) for x in (in_span, span_id, is_prefix)]
+        sc = D ** -0.5
+        o, lse, plan, o_lo, *_ = _fwd_op(qr, kr, v, None, *meta, sc, 0, True)
+        lib = _lib.load()
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        outs = []
+        for fused in (False, True):
+            dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+            delta = torch.empty((2,) + tuple(q.shape[:3]), dtype=torch.float32, device=dev)
+            a = _attn_args(qr, kr, v, sc)
+            a.o, a.o_strides, a.lse, a.o_lo = o.data_ptr(), _strides3(o), lse.data_ptr(), o_lo.data_ptr()
+            a.dout, a.do_strides = do.data_ptr(), _strides3(do)
+            a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+            a.dq_strides, a.dk_strides, a.dv_strides = _strides3(dq), _strides3(dk), _strides3(dv)
+            a.delta = delta.data_ptr()
+            a.dqk_signs = signs.data_ptr() if fused else None
+            _lib.check(lib.kd_attn_bwd(ctypes.byref(a), _ptr(plan), stream), "bwd")
+            if not fused:
+                dq, dk = hadamard_transform(dq, signs, inverse=True), hadamard_transform(dk, signs, inverse=True)
+            torch.cuda.synchronize()
+            outs.append((dq, dk, dv))
+        (dq0, dk0, dv0), (dq1, dk1, dv1) = outs
+        assert torch.equal(dv0, dv1)
+        for name, x, ref in (("dq", dq1, dq0), ("dk", dk1, dk0)):
+            x, ref = x.double(), ref.double()
+            diff = (x - ref).abs()
+            rr = diff.pow(2).mean().sqrt() / ref.pow(2).mean().sqrt()
+            print(f"  D={D} {name}: max_abs={diff.max().item():.3e} rel_rms={rr.item():.3e}", flush=True)
+            assert diff.max() <= 2.0 ** -6 * ref.abs().max() and rr <= 4e-3, name
