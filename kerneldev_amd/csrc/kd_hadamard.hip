@@ -39,8 +39,8 @@ KD_DEV float xor_lane(float v) {
 // One block = ITERS x RPB consecutive rows of one (b, h) (grid: row chunks x
 // B*H), so the row index needs no division and the optional absmax is one
 // block reduction and one atomic per block.  Without the absmax a block does
-// one RPB-row step; with it, 16 steps, so that each (b, h) collects few
-// atomics.
+// two RPB-row steps (measured 5% faster than one); with it, 16 steps, so that
+// each (b, h) collects few atomics.
 template <class E, int D, bool INV, int ITERS>
 __global__ __launch_bounds__(256) void k_hadamard(kd_rot_args a) {
   constexpr int TPR = D / 8;         // lanes per row
@@ -194,8 +194,9 @@ static void launch_rot_t(const kd_rot_args& a, hipStream_t st) {
   constexpr int RPB = 256 / (D / 8);
   const dim3 block(256);
   if (a.amax == nullptr) {
-    hipLaunchKernelGGL((k_hadamard<E, D, INV, 1>), dim3(unsigned((a.T + RPB - 1) / RPB), unsigned(a.B * a.H)), block,
-                       0, st, a);
+    // two row steps per block, the second row's load issued before the first's butterflies
+    hipLaunchKernelGGL((k_hadamard<E, D, INV, 2>), dim3(unsigned((a.T + 2 * RPB - 1) / (2 * RPB)), unsigned(a.B * a.H)),
+                       block, 0, st, a);
   } else {
     constexpr int CH = 16 * RPB;
     hipLaunchKernelGGL((k_hadamard<E, D, INV, 16>), dim3(unsigned((a.T + CH - 1) / CH), unsigned(a.B * a.H)), block,
