@@ -271,8 +271,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the attention path has no "
-                                   "cross-GPU component here (see the sharding note in DESIGN.md); "
-                                   "run with --gpus 1"}))
+                                   "cross-GPU component (every (b, h) head is independent, so heads "
+                                   "would shard across GPUs without communication); run with --gpus 1"}))
         sys.exit(2)
 
     import torch
