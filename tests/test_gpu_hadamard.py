@@ -126,3 +126,23 @@ def test_backward_epilogue_rotation_matches_separate_pass(dev):
             rr = diff.pow(2).mean().sqrt() / ref.pow(2).mean().sqrt()
             print(f"  D={D} {name}: max_abs={diff.max().item():.3e} rel_rms={rr.item():.3e}", flush=True)
             assert diff.max() <= 2.0 ** -6 * ref.abs().max() and rr <= 4e-3, name
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_attention_with_hadamard_fp16_ragged_lens(dev, D):
+    """The fused path (rotation inside the attention op, dQ / dK rotated back in
+    the backward epilogues) on fp16, a ragged T and lens with padded rows."""
+    T = 333
+    print(f"attention hadamard fp16 causal T={T} D={D}", flush=True)
+    q, k, v, do = (x.to(torch.float16) for x in qkvdo(2, 3, T, D, seed=41))
+    lens = torch.tensor([T, 200], dtype=torch.int32)
+    qd, kd, vd = (x.to(dev).requires_grad_(True) for x in (q, k, v))
+    o = flash_attention(qd, kd, vd, lens=lens.to(dev), causal=True, hadamard=True, hadamard_seed=9)
+    o.backward(do.to(dev))
+    torch.cuda.synchronize()
+    mask = oracle_mask(dict(q=q, causal=True), T, lens=lens)
+    ref = oracle_fwd_bwd(q, k, v, do, mask, D ** -0.5)
+    assert_close("o", o, ref["o"])
+    assert_close("dq", qd.grad, ref["dq"])
+    assert_close("dk", kd.grad, ref["dk"])
+    assert_close("dv", vd.grad, ref["dv"])
