@@ -174,17 +174,27 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
             q8: torch.Tensor | None = None, k8: torch.Tensor | None = None,
             q_scale: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
             bthd: bool = False, plan_in: torch.Tensor | None = None, signs: torch.Tensor | None = None,
-            ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+            quant_fp8: bool = False,
+            ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                       torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     B, H, T, D = q.shape
     # a caller's plan is used as is (and not returned: outputs may not alias inputs)
     plan = plan_in if plan_in is not None else build_plan(B, T, D, q.device, mode, in_span, span_id, is_prefix, lens)
-    # signs: attention of Q R and K R (returned for the backward, which hands
-    # back dQ, dK for q, k themselves)
-    q_r, k_r = q.new_empty(0), k.new_empty(0)  # distinct tensors: outputs may not alias
+    # signs: attention of Q R and K R, returned for the backward (which hands
+    # back dQ, dK for q, k themselves); with quant_fp8 the scores come from
+    # e4m3 copies of Q R and K R, scaled by the rotation pass's absmax, also
+    # returned.  Every unused output is its own empty tensor (outputs may not alias).
+    q_r, k_r = q.new_empty(0), k.new_empty(0)
+    q8_o, k8_o = q.new_empty(0, dtype=torch.uint8), k.new_empty(0, dtype=torch.uint8)
+    qs_o, ks_o = q.new_empty(0, dtype=torch.float32), k.new_empty(0, dtype=torch.float32)
     if signs is not None:
-        from .hadamard import _launch
-        q = q_r = _launch(q, signs, False)
-        k = k_r = _launch(k, signs, False)
+        from .hadamard import _launch, _quant_op
+        amax = torch.zeros((2, B, H), dtype=torch.float32, device=q.device) if quant_fp8 else None
+        q = q_r = _launch(q, signs, False, None if amax is None else amax[0])
+        k = k_r = _launch(k, signs, False, None if amax is None else amax[1])
+        if quant_fp8:
+            (q8_o, qs_o), (k8_o, ks_o) = _quant_op(q_r, amax[0]), _quant_op(k_r, amax[1])
+            q8, k8, q_scale, k_scale = q8_o, k8_o, qs_o, ks_o
     o = _new_out(B, H, T, D, q, bthd)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
     # rounding residual of O, kept for the backward's Delta (see kd_bwd.hip)
@@ -195,20 +205,26 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
     a.lse = lse.data_ptr()
     a.o_lo = o_lo.data_ptr() if need_lo else None
     _lib.check(_lib.load().kd_attn_fwd(ctypes.byref(a), _ptr(plan), _stream(q.device)), "kd_attn_fwd")
-    return o, lse, (plan if plan_in is None else plan.new_empty(0)), o_lo, q_r, k_r
+    return o, lse, (plan if plan_in is None else plan.new_empty(0)), o_lo, q_r, k_r, q8_o, k8_o, qs_o, ks_o
 
 
 @_fwd_op.register_fake
 def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8=None, k8=None,
-              q_scale=None, k_scale=None, bthd=False, plan_in=None, signs=None):
+              q_scale=None, k_scale=None, bthd=False, plan_in=None, signs=None, quant_fp8=False):
     B, H, T, D = q.shape
     rot_shape = (B, H, T, D) if signs is not None else (0,)
+    q8_shape = (B, H, T, D) if signs is not None and quant_fp8 else (0,)
+    sc_shape = (B, H) if signs is not None and quant_fp8 else (0,)
     return (_new_out(B, H, T, D, q, bthd),
             torch.empty((B, H, T), dtype=torch.float32, device=q.device),
             torch.empty(_lib.plan_bytes(B, T, D) if plan_in is None else 0, dtype=torch.uint8, device=q.device),
             torch.empty((B, H, T, D) if need_lo else (0,), dtype=q.dtype, device=q.device),
             torch.empty(rot_shape, dtype=q.dtype, device=q.device),
-            torch.empty(rot_shape, dtype=k.dtype, device=k.device))
+            torch.empty(rot_shape, dtype=k.dtype, device=k.device),
+            torch.empty(q8_shape, dtype=torch.uint8, device=q.device),
+            torch.empty(q8_shape, dtype=torch.uint8, device=q.device),
+            torch.empty(sc_shape, dtype=torch.float32, device=q.device),
+            torch.empty(sc_shape, dtype=torch.float32, device=q.device))
 
 
 @torch.library.custom_op("kdattn::bwd", mutates_args=(), device_types=("cuda",))
@@ -246,11 +262,13 @@ def _bwd_fake(q, k, v, o, lse, do, plan, sm_scale, o_lo, q8=None, k8=None, q_sca
 
 def _setup_context(ctx, inputs, output):
     (q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8, k8, q_scale, k_scale, bthd, plan_in,
-     signs) = inputs
-    o, lse, plan, o_lo, q_r, k_r = output
+     signs, quant_fp8) = inputs
+    o, lse, plan, o_lo, q_r, k_r, q8_o, k8_o, qs_o, ks_o = output
     if plan_in is not None:
         plan = plan_in
-    ctx.mark_non_differentiable(q_r, k_r)
+    ctx.mark_non_differentiable(q_r, k_r, q8_o, k8_o, qs_o, ks_o)
+    if signs is not None and quant_fp8:
+        q8, k8, q_scale, k_scale = q8_o, k8_o, qs_o, ks_o
     ctx.fp8 = q8 is not None
     ctx.rot = signs is not None
     if ctx.rot:  # the backward recomputes from the rotated operands and rotates dQ, dK back
@@ -260,7 +278,7 @@ def _setup_context(ctx, inputs, output):
     ctx.sm_scale = sm_scale
 
 
-def _backward(ctx, do, dlse, dplan, do_lo, dq_r, dk_r):
+def _backward(ctx, do, dlse, dplan, do_lo, *_unused):
     # dlse is ignored, as in original_kernel.py:1965-1992.  With fp8 scores the
     # backward recomputes P from the same fp8 Q8 K8^T and forms dQ = dS K,
     # dK = dS^T Q from the 16-bit operands: the straight-through estimator.
@@ -268,7 +286,7 @@ def _backward(ctx, do, dlse, dplan, do_lo, dq_r, dk_r):
     signs = rest.pop(0) if ctx.rot else None
     fp8 = tuple(rest) if ctx.fp8 else (None, None, None, None)
     dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, ctx.sm_scale, o_lo, *fp8, dqk_signs=signs)
-    return dq, dk, dv, None, None, None, None, None, None, None, None, None, None, None, None, None, None
+    return (dq, dk, dv) + (None,) * 15
 
 
 _fwd_op.register_autograd(_backward, setup_context=_setup_context)
@@ -383,31 +401,26 @@ def flash_attention(
         q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
     elif in_dtype not in (torch.bfloat16, torch.float16):
         raise ValueError(f"unsupported dtype {in_dtype}")
-    from .hadamard import generate_hadamard_signs, hadamard_absmax, quantize_fp8
+    from .hadamard import generate_hadamard_signs, quantize_fp8
 
-    amax_q = amax_k = None
     fused_signs = None
     if hadamard:
-        # (Q R)(K R)^T = Q K^T with R = diag(s) H_d / sqrt(d).  16-bit scores:
-        # the attention op rotates Q and K itself and its backward kernels
-        # return dQ' R^T, dK' R^T directly.  fp8: the rotation pass also yields
-        # the per-(b, h) absmax the scales need, and autograd maps dQ', dK'
-        # back through R^T (hadamard.py).
-        signs = generate_hadamard_signs(D, hadamard_seed, device=device)
-        if qk_dtype == "fp8_e4m3":
-            (q, amax_q), (k, amax_k) = hadamard_absmax(q, signs), hadamard_absmax(k, signs)
-        else:
-            fused_signs = signs
+        # (Q R)(K R)^T = Q K^T with R = diag(s) H_d / sqrt(d).  The attention
+        # op rotates Q and K itself (fp8: the rotation pass also yields the
+        # per-(b, h) absmax that scales the e4m3 copies), and its backward
+        # kernels return dQ' R^T, dK' R^T directly.
+        fused_signs = generate_hadamard_signs(D, hadamard_seed, device=device)
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     fp8 = ()
-    if qk_dtype == "fp8_e4m3":
-        (q8, q_scale), (k8, k_scale) = quantize_fp8(q, amax_q), quantize_fp8(k, amax_k)
+    if qk_dtype == "fp8_e4m3" and not hadamard:  # with Hadamard the op quantises Q R, K R itself
+        (q8, q_scale), (k8, k_scale) = quantize_fp8(q), quantize_fp8(k)
         fp8 = (q8, k8, q_scale, k_scale)
 
     need_lo = torch.is_grad_enabled() and any(x.requires_grad for x in (q, k, v))
     o, lse, plan_t, *_ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode), need_lo,
                                  *(fp8 or (None, None, None, None)), bthd=out_layout == "bthd",
-                                 plan_in=None if plan is None else plan.tensor, signs=fused_signs)
+                                 plan_in=None if plan is None else plan.tensor, signs=fused_signs,
+                                 quant_fp8=hadamard and qk_dtype == "fp8_e4m3")
     if plan is not None:
         plan_t = plan.tensor
     if in_dtype == torch.float32:
