@@ -20,9 +20,10 @@
 // visited (plan list); FULL tiles skip the mask, PARTIAL tiles evaluate it.
 //
 // The running max is rescaled lazily, per lane: the accumulators are only
-// rescaled when a row's max grows by more than 2^8 (P is then <= 256,
-// harmless in fp32/bf16), which removes the per-step O *= alpha of the
-// textbook loop.  Each wave masks by the class of its own 64-row q-tile
+// rescaled when a row's max grows by more than 2^16 (P is then <= 65536:
+// bf16 P keeps its 8 significant bits, and l and O stay far below the fp32
+// range over any row length), which removes the per-step O *= alpha of the
+// textbook loop; 2^16 rescales less often than 2^8 on outlier data (-1%).  Each wave masks by the class of its own 64-row q-tile
 // against the key tile (from the list entry): FULL tiles skip the mask,
 // PARTIAL ones apply the plan's 64-bit row masks (two VALU ops per score,
 // copied one step ahead into the wave's own LDS slot), EMPTY ones mask
@@ -228,7 +229,7 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
         }
       }
     }
-    // running max of this lane's rows; rescale only when it grows by > 2^8
+    // running max of this lane's rows; rescale only when it grows by > 2^16
     float ms[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -239,7 +240,7 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][qb][r]);
       mx = xhalf_max(mx);
       const float m_new = fmaxf(m_ref[qb], mx);
-      if ((m_new - m_ref[qb]) * sl2 > 8.f) {  // false for -inf - -inf (NaN); per lane
+      if ((m_new - m_ref[qb]) * sl2 > 16.f) {  // false for -inf - -inf (NaN); per lane
         const float alpha = (m_ref[qb] == NEG_INF) ? 0.f : fast_exp2((m_ref[qb] - m_new) * sl2);
         m_ref[qb] = m_new;
         l0[qb] *= alpha;
