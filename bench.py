@@ -55,8 +55,8 @@ USEFUL_FWD, USEFUL_BWD = 4, 10
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs scaled by a 1 GiB copy's counts
 # (profiles/attn_config4_{bf16,fp8_e4m3}_hbm_traffic.md); re-measured whenever the kernels change.
 CONFIG4_TRAFFIC_BYTES = {
-    "bf16": {"fwd": 1063.6e6, "dq": 1483.5e6, "dkdv": 1111.8e6},
-    "fp8_e4m3": {"fwd": 813.5e6, "dq": 1539.2e6, "dkdv": 1230.8e6},
+    "bf16": {"fwd": 1062.7e6, "dq": 1480.4e6, "dkdv": 1113.3e6},
+    "fp8_e4m3": {"fwd": 807.7e6, "dq": 1544.3e6, "dkdv": 1226.9e6},
 }
 
 
