@@ -277,3 +277,21 @@ def test_config1_against_golden_fixture(dev):
     for key in ("o", "dq", "dk", "dv"):
         assert_close(key, got[key][0, 0], torch.from_numpy(fx[key]))
     assert_close("lse", got["lse"][0, 0], torch.from_numpy(fx["lse"]), out_dtype=torch.float32)
+
+
+@pytest.mark.parametrize("T", [1, 17, 63, 65, 130])
+@pytest.mark.parametrize("causal", [True, False])
+def test_tiny_and_ragged_lengths(dev, T, causal):
+    """Single rows and lengths just off the 64-row tile boundary (partial last tiles, empty groups)."""
+    q, k, v, do = qkvdo(2, 2, T, 64, seed=50 + T)
+    _case(dict(name=f"T{T} causal={causal}", q=q, k=k, v=v, do=do, causal=causal), dev)
+
+
+def test_cocktail_ragged_hadamard_fp8(dev):
+    """The fused rotation + fp8 path on a ragged hierarchical batch (T = 777)."""
+    tokens, in_span, span_id, is_prefix = cocktail_batch(2, 1024, CONFIG3_LAYOUT, seed=60)
+    T = 777
+    in_span, span_id, is_prefix = in_span[:, :T], span_id[:, :T], is_prefix[:, :T]
+    q, k, v, do = qkvdo(2, 2, T, 128, seed=61)
+    _case(dict(name="cocktail ragged fp8+hadamard", q=q, k=k, v=v, do=do, in_span=in_span, span_id=span_id,
+               is_prefix=is_prefix), dev, qk_dtype="fp8_e4m3", hadamard=True, hadamard_seed=7)
