@@ -74,6 +74,9 @@ def parse():
                     help="config 4 without the Hadamard rotation of Q and K")
     ap.add_argument("--qk-dtype", default="bf16", choices=("bf16", "fp8_e4m3"),
                     help="config 4's second run: Q K^T on fp8 e4m3 with per-(b, h) scales")
+    ap.add_argument("--precision", default="tf32", choices=("tf32", "ieee", "bf16"),
+                    help="flash_attention's precision: tf32 / ieee (the default kernels, P and dS as "
+                         "16-bit hi + lo pairs) or the extension bf16 (P and dS rounded once)")
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU baseline leg (profiling runs)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -95,11 +98,11 @@ def cpu_threads() -> int:
 class Step:
     """Preallocated buffers and the five launches of one fwd+bwd pass."""
 
-    def __init__(self, inp, dev, hadamard=False, qk_dtype="bf16"):
+    def __init__(self, inp, dev, hadamard=False, qk_dtype="bf16", precision="tf32"):
         import torch
 
         from kerneldev_amd import _lib, generate_hadamard_signs
-        from kerneldev_amd.attention import _attn_args, _dtype_code, _strides3, mask_mode
+        from kerneldev_amd.attention import PRECISIONS, _attn_args, _dtype_code, _strides3, mask_mode
 
         self.torch, self.lib, self.dev = torch, _lib.load(), dev
         self._check = _lib.check
@@ -126,7 +129,7 @@ class Step:
         self.o_lo = torch.empty_like(q)  # O's rounding residual, kept for Delta (training step)
         self.dq, self.dk, self.dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
         self.inputs = (q, k, v, do)
-        a = _attn_args(q, k, v, D ** -0.5)
+        a = _attn_args(q, k, v, D ** -0.5, PRECISIONS[precision])
         a.dtype = _dtype_code(q.dtype)
         a.o, a.o_strides = self.o.data_ptr(), _strides3(self.o)
         a.lse = self.lse.data_ptr()
@@ -287,7 +290,7 @@ def main():
     if fp8 and D != 128:
         print(json.dumps({"error": "the fp8 QK^T path is built for head_dim 128 (config 4)"}))
         sys.exit(2)
-    st = Step(inp, dev, hadamard=hadamard, qk_dtype=args.qk_dtype)
+    st = Step(inp, dev, hadamard=hadamard, qk_dtype=args.qk_dtype, precision=args.precision)
     if args.calibrate_copy_mib > 0:
         n = args.calibrate_copy_mib << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -364,6 +367,7 @@ def main():
             "event_ms_per_step": round(event_ms, 4),
             "hadamard": hadamard,
             "qk_dtype": args.qk_dtype,
+            "precision": args.precision,
         },
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -40,6 +40,12 @@ extern "C" {
 /* element dtypes */
 #define KD_BF16 0
 #define KD_F16 1
+/* arithmetic of the softmax weights P and the score gradients dS inside the
+ * attention kernels (kd_attn_args.precision) */
+#define KD_PREC_SPLIT 0  /* P and dS enter their products (P V, dV, dQ, dK) as a 16-bit pair
+                            hi + lo, ~16 significant bits (default) */
+#define KD_PREC_SINGLE 1 /* P and dS rounded once to the input type (8 significant bits for
+                            bf16, as the reference's forward rounds P to V's dtype) */
 /* span_id index dtypes */
 #define KD_I64 0
 #define KD_I32 1
@@ -109,6 +115,8 @@ typedef struct kd_attn_args {
   int32_t B, H, T, D;
   int32_t dtype;                /* KD_BF16 / KD_F16 */
   float sm_scale;
+  int32_t precision;            /* KD_PREC_SPLIT (0, default) / KD_PREC_SINGLE */
+  int32_t pad_;
 } kd_attn_args;
 
 /* Walsh-Hadamard rotation of [B, H, T, D] rows (incoherent processing). */

@@ -20,6 +20,7 @@ KD_OK, KD_ERR_INVALID, KD_ERR_UNSUPPORTED, KD_ERR_LAUNCH = 0, -1, -2, -3
 KD_BF16, KD_F16 = 0, 1
 KD_I64, KD_I32 = 0, 1
 KD_MODE_FORMULA, KD_MODE_CAUSAL, KD_MODE_ALL = 0, 1, 2
+KD_PREC_SPLIT, KD_PREC_SINGLE = 0, 1
 
 I64x2 = c_int64 * 2
 I64x3 = c_int64 * 3
@@ -54,6 +55,7 @@ class AttnArgs(ctypes.Structure):
         ("dqk_signs", c_void_p),
         ("B", c_int32), ("H", c_int32), ("T", c_int32), ("D", c_int32),
         ("dtype", c_int32), ("sm_scale", c_float),
+        ("precision", c_int32), ("pad_", c_int32),
     ]
 
 

@@ -25,6 +25,14 @@ from ._lib import AttnArgs, MetaArgs
 SUPPORTED_HEAD_DIMS = (64, 128)
 REFERENCE_HEAD_DIMS = (16, 32, 64, 128, 256)  # original_kernel.py:1720
 
+# precision -> arithmetic of P and dS in the kernels.  The reference rounds P
+# to V's dtype for P V (original_kernel.py:566-571) and keeps P and dS in fp32
+# for its backward dots, taken as tf32 or ieee (:1331-1333, :1517-1523); the
+# split kernels carry P and dS as a 16-bit hi + lo pair (~16 significant
+# bits) in all four products, at or above the reference on each.  "bf16" (an
+# extension) rounds P and dS once to the input type: faster, 8 significant bits.
+PRECISIONS = {"ieee": _lib.KD_PREC_SPLIT, "tf32": _lib.KD_PREC_SPLIT, "bf16": _lib.KD_PREC_SINGLE}
+
 
 def _stream(device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
@@ -130,12 +138,13 @@ def build_plan_from_tokens(tokens: torch.Tensor, head_dim: int, rule: str = "col
     return AttentionPlan(plan, B, T, head_dim)
 
 
-def _attn_args(q, k, v, sm_scale) -> AttnArgs:
+def _attn_args(q, k, v, sm_scale, prec=_lib.KD_PREC_SPLIT) -> AttnArgs:
     a = AttnArgs()
     B, H, T, D = q.shape
     a.B, a.H, a.T, a.D = B, H, T, D
     a.dtype = _dtype_code(q.dtype)
     a.sm_scale = float(sm_scale)
+    a.precision = int(prec)
     a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
     a.q_strides, a.k_strides, a.v_strides = _strides3(q), _strides3(k), _strides3(v)
     return a
@@ -174,7 +183,7 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
             q8: torch.Tensor | None = None, k8: torch.Tensor | None = None,
             q_scale: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
             bthd: bool = False, plan_in: torch.Tensor | None = None, signs: torch.Tensor | None = None,
-            quant_fp8: bool = False,
+            quant_fp8: bool = False, prec: int = 0,
             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
                        torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     B, H, T, D = q.shape
@@ -199,7 +208,7 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
     lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
     # rounding residual of O, kept for the backward's Delta (see kd_bwd.hip)
     o_lo = torch.empty((B, H, T, D) if need_lo else (0,), dtype=q.dtype, device=q.device)
-    a = _attn_args(q, k, v, sm_scale)
+    a = _attn_args(q, k, v, sm_scale, prec)
     _set_fp8(a, _fp8_tuple(q8, k8, q_scale, k_scale))
     a.o, a.o_strides = o.data_ptr(), _strides3(o)
     a.lse = lse.data_ptr()
@@ -210,7 +219,7 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
 
 @_fwd_op.register_fake
 def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8=None, k8=None,
-              q_scale=None, k_scale=None, bthd=False, plan_in=None, signs=None, quant_fp8=False):
+              q_scale=None, k_scale=None, bthd=False, plan_in=None, signs=None, quant_fp8=False, prec=0):
     B, H, T, D = q.shape
     rot_shape = (B, H, T, D) if signs is not None else (0,)
     q8_shape = (B, H, T, D) if signs is not None and quant_fp8 else (0,)
@@ -232,7 +241,7 @@ def _bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, 
             do: torch.Tensor, plan: torch.Tensor, sm_scale: float, o_lo: torch.Tensor,
             q8: torch.Tensor | None = None, k8: torch.Tensor | None = None,
             q_scale: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
-            dqk_signs: torch.Tensor | None = None,
+            dqk_signs: torch.Tensor | None = None, prec: int = 0,
             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     B, H, T, D = q.shape
     do = _kernel_ready(do)
@@ -240,7 +249,7 @@ def _bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, 
     dk = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
     dv = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
     delta = torch.empty((2, B, H, T), dtype=torch.float32, device=q.device)  # Delta, LSE for bwd
-    a = _attn_args(q, k, v, sm_scale)
+    a = _attn_args(q, k, v, sm_scale, prec)
     a.o, a.o_strides = o.data_ptr(), _strides3(o)
     a.lse = lse.data_ptr()
     a.dout, a.do_strides = do.data_ptr(), _strides3(do)
@@ -256,13 +265,13 @@ def _bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, 
 
 @_bwd_op.register_fake
 def _bwd_fake(q, k, v, o, lse, do, plan, sm_scale, o_lo, q8=None, k8=None, q_scale=None, k_scale=None,
-              dqk_signs=None):
+              dqk_signs=None, prec=0):
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
 def _setup_context(ctx, inputs, output):
     (q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8, k8, q_scale, k_scale, bthd, plan_in,
-     signs, quant_fp8) = inputs
+     signs, quant_fp8, prec) = inputs
     o, lse, plan, o_lo, q_r, k_r, q8_o, k8_o, qs_o, ks_o = output
     if plan_in is not None:
         plan = plan_in
@@ -276,6 +285,7 @@ def _setup_context(ctx, inputs, output):
     extra = (q8, k8, q_scale, k_scale) if ctx.fp8 else ()
     ctx.save_for_backward(q, k, v, o, lse, plan, o_lo, *((signs,) if ctx.rot else ()), *extra)
     ctx.sm_scale = sm_scale
+    ctx.prec = prec
 
 
 def _backward(ctx, do, dlse, dplan, do_lo, *_unused):
@@ -285,8 +295,8 @@ def _backward(ctx, do, dlse, dplan, do_lo, *_unused):
     q, k, v, o, lse, plan, o_lo, *rest = ctx.saved_tensors
     signs = rest.pop(0) if ctx.rot else None
     fp8 = tuple(rest) if ctx.fp8 else (None, None, None, None)
-    dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, ctx.sm_scale, o_lo, *fp8, dqk_signs=signs)
-    return (dq, dk, dv) + (None,) * 15
+    dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, ctx.sm_scale, o_lo, *fp8, dqk_signs=signs, prec=ctx.prec)
+    return (dq, dk, dv) + (None,) * 16
 
 
 _fwd_op.register_autograd(_backward, setup_context=_setup_context)
@@ -332,8 +342,12 @@ def flash_attention(
 
     Args mirror ``original_kernel.py:2096-2112``.  ``autotune`` and
     ``prescale_qk`` are accepted and ignored (tile shapes are compile-time
-    constants here and the scale is always applied in fp32); ``precision``
-    must be ``"ieee"`` or ``"tf32"``.  ``attention_mask``'s contents are not
+    constants here and the scale is always applied in fp32).  ``precision``
+    is ``"ieee"`` or ``"tf32"`` as in the reference; both run the kernels that
+    carry P and dS as 16-bit hi + lo pairs (about 16 significant bits in P V,
+    dV, dQ and dK, at or above the reference's bf16 P V and tf32 / ieee
+    backward dots).  The extension ``"bf16"`` rounds P and dS once to the
+    input type instead (faster; 8 significant bits with bf16 inputs).  ``attention_mask``'s contents are not
     read, exactly as in the reference: when it is given without metadata the
     mask formula runs with default metadata, i.e. ``i >= j``.
 
@@ -363,8 +377,8 @@ def flash_attention(
         raise ValueError("q, k and v must share head_dim")
     if k.shape != q.shape or v.shape != q.shape:
         raise ValueError("q, k and v must have the same [B, H, T, d] shape")
-    if precision not in ("ieee", "tf32"):
-        raise ValueError(f"precision must be 'ieee' or 'tf32', got {precision!r}")
+    if precision not in PRECISIONS:
+        raise ValueError(f"precision must be 'ieee' or 'tf32' (or the extension 'bf16'), got {precision!r}")
     if lens is not None and (lens.dtype != torch.int32 or lens.dim() != 1 or lens.shape[0] != B):
         raise ValueError("lens must be an int32 tensor of shape [batch]")
     if plan is not None:
@@ -420,7 +434,7 @@ def flash_attention(
     o, lse, plan_t, *_ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode), need_lo,
                                  *(fp8 or (None, None, None, None)), bthd=out_layout == "bthd",
                                  plan_in=None if plan is None else plan.tensor, signs=fused_signs,
-                                 quant_fp8=hadamard and qk_dtype == "fp8_e4m3")
+                                 quant_fp8=hadamard and qk_dtype == "fp8_e4m3", prec=PRECISIONS[precision])
     if plan is not None:
         plan_t = plan.tensor
     if in_dtype == torch.float32:

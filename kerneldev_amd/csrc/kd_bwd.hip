@@ -158,7 +158,7 @@ KD_DEV void tr_addrs(int lane, int (&addr)[D / 32][2]) {
 }
 
 // ------------------------------------------------------------------- dQ ----
-template <class E, int D, bool Q8>
+template <class E, int D, bool Q8, bool SP>
 __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __restrict__ qbits,
                                                const uint32_t* __restrict__ list,
                                                const int32_t* __restrict__ count,
@@ -392,16 +392,20 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
       }
       __builtin_amdgcn_sched_barrier(0x4);
     }
+    // dS packed for the MFMA and, with SP, its rounding residual: dQ takes
+    // dS to ~16 significant bits as two products
     u32x4 dsb[2][2];
+    u32x4 dsl[SP ? 2 : 1][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       float ds[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) ds[r] = s[kb][r] * dp[kb][r];  // dp = dP - Delta
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-        dsb[kb][t] = u32x4{pack2<E>(ds[8 * t + 0], ds[8 * t + 1]), pack2<E>(ds[8 * t + 2], ds[8 * t + 3]),
-                           pack2<E>(ds[8 * t + 4], ds[8 * t + 5]), pack2<E>(ds[8 * t + 6], ds[8 * t + 7])};
+      for (int t = 0; t < 2; ++t) {
+        dsb[kb][t] = pack8<E>(ds + 8 * t);
+        if constexpr (SP) dsl[kb][t] = pack8_residual<E>(ds + 8 * t, dsb[kb][t]);
+      }
     }
     // dQ^T += K^T dS^T, K^T read transposed DQ_PF steps ahead (steps: t4 = i / DB, db = i % DB)
     {
@@ -420,6 +424,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
         const int t4 = i / DB, db = i % DB;
         __builtin_amdgcn_sched_barrier(0x406);
         acc[db] = mfma32x32x16<E>(av[i % PF], dsb[t4 >> 1][t4 & 1], acc[db]);
+        if constexpr (SP) acc[db] = mfma32x32x16<E>(av[i % PF], dsl[t4 >> 1][t4 & 1], acc[db]);
         if (i + PF < NS) av[i % PF] = read(i + PF);
       }
       __builtin_amdgcn_sched_barrier(0x406);
@@ -453,7 +458,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
 // e - 1 with the P written in step e - 1.  So one barrier per step orders
 // everything (tile e landed, P(e-1) written, P(e-2) and tile e-2 released),
 // at the price of a third Q buffer (dK reads Q of tile e - 1).
-template <class E, int D, bool Q8>
+template <class E, int D, bool Q8, bool SP>
 __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __restrict__ kbits,
                                                  const uint32_t* __restrict__ list,
                                                  const int32_t* __restrict__ count, int nT, int nKB) {
@@ -461,15 +466,21 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   using TL = Tile<D, NW>;
   using TQ8 = Tile<Q8 ? D / 2 : D, NW>;  // fp8 Q tiles (D bytes a row); only used at D = 128
   constexpr int DS = D / 16, DB = D / 32, NL = TL::LOADS_PER_WAVE, NL8 = TQ8::LOADS_PER_WAVE;
-  // Tiles are loaded PD steps ahead (2; the fp8 variant's extra Q8 tiles
-  // leave LDS for 1).  Slot counts follow from who reads what when: in step
-  // e the P waves read Q(e), dO(e), LSE(e); the dS waves dO(e), Q(e-1),
-  // Delta(e-1); a load issued in step e must not overwrite any of those.
-  constexpr int PD = Q8 ? 1 : 2, NQ = PD + 2, NDO = PD + 1, NLS = PD + 1, NDL = PD + 2;
+  // Tiles are loaded PD steps ahead: 2, or 1 where the fp8 variant's Q8
+  // tiles or SP's fp32 P exchange take the LDS.  Slot counts follow from who
+  // reads what when: in step e the P waves read Q(e) (fp8: Q8(e)), dO(e),
+  // LSE(e); the dS waves dO(e), Q(e-1), Delta(e-1); a load issued in step e
+  // must not overwrite any of those.  The fp8 variant's 16-bit Q tile feeds
+  // only the dK product, one step later, so its copy of tile e is issued in
+  // step e itself, into one of two slots.
+  constexpr int PD = (Q8 || SP) ? 1 : 2, NQ = Q8 ? 2 : PD + 2, NDO = PD + 1, NLS = PD + 1, NDL = PD + 2;
   __shared__ __attribute__((aligned(1024))) uint8_t s_q[NQ][TL::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_q8[Q8 ? NDO : 1][Q8 ? TQ8::BYTES : 16];
   __shared__ __attribute__((aligned(1024))) uint8_t s_do[NDO][TL::BYTES];
-  __shared__ __attribute__((aligned(1024))) u32x4 s_p[2][4][4][64];       // [e % 2][pair][k-step][lane]
+  // P from the P wave to the dS wave, [e % 2][pair][k-step][lane]: packed
+  // 16-bit P, or with SP the fp32 P (two u32x4 per k-step), so that dS = P (dP
+  // - Delta) keeps P's full precision
+  __shared__ __attribute__((aligned(1024))) u32x4 s_p[2][4][SP ? 8 : 4][64];
   __shared__ __attribute__((aligned(256))) float s_lse[NLS][64];
   __shared__ __attribute__((aligned(256))) float s_delta[NDL][64];
   // each P wave's column masks of a PARTIAL tile, copied with the tile
@@ -555,7 +566,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
       const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_bits[sl.ls][pair][0]))));
       dma_b32(rs_bits, bits_off0 + qt * uint32_t(nT) * 512u, m);
     }
-    TL::load_async(rs_q, q0 * qrb, qoff, lds_addr(s_q[sl.q]), wave);
+    if constexpr (!Q8) TL::load_async(rs_q, q0 * qrb, qoff, lds_addr(s_q[sl.q]), wave);
     TL::load_async(rs_do, q0 * dorb, dooff, lds_addr(s_do[sl.d]), wave);
     if constexpr (Q8) TQ8::load_async(rs_q8, q0 * uint32_t(D), q8off, lds_addr(s_q8[Q8 ? sl.d : 0]), wave);
     if (wave == 4)
@@ -563,10 +574,16 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
     else if (wave == 5)
       dma_b32(rs_dl, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_delta[sl.dl][0])))));
   };
+  // fp8: the 16-bit Q tile of tile e (the dK product's operand in step e + 1)
+  auto load_q16 = [&](int e, const Slots& sl) {
+    const uint32_t q0 = entry_tile(ent[e]) * 64u;
+    TL::load_async(rs_q, q0 * qrb, qoff, lds_addr(s_q[sl.q]), wave);
+  };
   // Wait until tile e's loads (and older ones) have landed while tile e+1's,
   // issued last, may still be in flight: vector memory loads retire in order.
   // (A mask copy precedes the tile loads, so it is never among the last.)
-  constexpr int NTL = 2 * NL + (Q8 ? NL8 : 0);
+  // Only used with PD = 2, i.e. neither fp8 nor SP.
+  constexpr int NTL = 2 * NL;
   auto wait_tile = [&](bool next_in_flight) {
     if (!next_in_flight) wait_vmem();
     else if (wave == 4 || wave == 5) wait_vmem_n<NTL + 1>();
@@ -593,7 +610,9 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   constexpr int PF = DKDV_PF;
   // acc^T += A^T bop over the 64 queries of a tile (k-steps k4 = 2 qb + t),
   // A^T read transposed from tile `at`; steps i = 4 k4 ... ordered (k4, db)
-  auto accumulate = [&](const uint8_t* at_g, const u32x4 (&bop)[2][2]) {
+  // With SP, bopl holds the residual of bop and enters the same accumulator
+  // through a second MFMA on the same A operand.
+  auto accumulate = [&](const uint8_t* at_g, const u32x4 (&bop)[2][2], const u32x4 (&bopl)[2][2]) {
     lds_u8* at = to_lds(at_g);
     constexpr int NS = 4 * DB;
     lds_u8* pa[DB][2];  // one address per (db, half); the k-step offsets are immediates
@@ -616,6 +635,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
       const int k4 = i / DB, db = i % DB;
       __builtin_amdgcn_sched_barrier(0x406);
       acc[db] = mfma32x32x16<E>(av[i % PF], bop[k4 >> 1][k4 & 1], acc[db]);
+      if constexpr (SP) acc[db] = mfma32x32x16<E>(av[i % PF], bopl[k4 >> 1][k4 & 1], acc[db]);
       if (i + PF < NS) av[i % PF] = read(i + PF);
     }
     __builtin_amdgcn_sched_barrier(0x406);
@@ -661,6 +681,9 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
     wait_tile(PD == 2 && e + 1 < n);
     barrier_lds();  // tile e landed, P(e-1) written; P(e-2) and the slots of tile e+PD released
     if (e + PD < n) load_tile(e + PD, ahead(sl, PD));
+    if constexpr (Q8) {
+      if (e < n) load_q16(e, sl);  // read by the dS waves in step e + 1
+    }
     const int pb = e & 1;
     if (role == 0) {
       if (e < n) {
@@ -709,7 +732,8 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
             for (int r = 0; r < 16; ++r) x[qb][r] = mask_bit(x[qb][r], w, 16 * (r >> 3) + (r & 7));
           }
         }
-        u32x4 bop[2][2];  // packed P: B operand of k-step 2 qb + t
+        u32x4 bop[2][2];                // packed P: B operand of k-step 2 qb + t
+        u32x4 bopl[2][2];               // SP: its rounding residual (unused otherwise)
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
@@ -717,39 +741,60 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
             float p[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) p[j] = fast_exp2(x[qb][8 * t + j] * sl2);
-            bop[qb][t] = u32x4{pack2<E>(p[0], p[1]), pack2<E>(p[2], p[3]), pack2<E>(p[4], p[5]),
-                               pack2<E>(p[6], p[7])};
+            bop[qb][t] = pack8<E>(p);
+            if constexpr (SP) {
+              bopl[qb][t] = pack8_residual<E>(p, bop[qb][t]);
+              // the fp32 P for the dS wave, stored as it is formed (holding
+              // it across the dV MFMAs would take 32 more registers)
+              s_p[pb][pair][2 * (2 * qb + t)][lane] = u32x4{__float_as_uint(p[0]), __float_as_uint(p[1]),
+                                                            __float_as_uint(p[2]), __float_as_uint(p[3])};
+              s_p[pb][pair][2 * (2 * qb + t) + 1][lane] = u32x4{__float_as_uint(p[4]), __float_as_uint(p[5]),
+                                                                __float_as_uint(p[6]), __float_as_uint(p[7])};
+            }
           }
-        accumulate(s_do[sl.d], bop);  // dV^T += dO^T P
-        // P for the dS wave (read after the next barrier).  Written after the
-        // MFMAs: LDS stores may not cross the product's scheduling fences, so
-        // stores placed before it would hold all of P's VALU work ahead of the
-        // first MFMA.
+        accumulate(s_do[sl.d], bop, bopl);  // dV^T += dO^T P
+        // 16-bit P for the dS wave (read after the next barrier).  Written
+        // after the MFMAs: LDS stores may not cross the product's scheduling
+        // fences, so stores placed before it would hold all of P's VALU work
+        // ahead of the first MFMA.
+        if constexpr (!SP) {
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+          for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-          for (int t = 0; t < 2; ++t) s_p[pb][pair][2 * qb + t][lane] = bop[qb][t];
+            for (int t = 0; t < 2; ++t) s_p[pb][pair][2 * qb + t][lane] = bop[qb][t];
+        }
       }
     } else {
       if (e >= 1) {  // dS and dK of tile e - 1
         const int qprev = wrap(sl.q + NQ - 1, NQ);
         u32x4 dsb[2][2];
+        u32x4 dsl[2][2];  // SP: dS's rounding residual (unused otherwise)
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            const u32x4 pw = s_p[pb ^ 1][pair][2 * qb + t][lane];
             float ds[8];
+            if constexpr (SP) {
+              const u32x4 p0 = s_p[pb ^ 1][pair][2 * (2 * qb + t)][lane];
+              const u32x4 p1 = s_p[pb ^ 1][pair][2 * (2 * qb + t) + 1][lane];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const uint32_t w = pw[j >> 1];
-              const float p = to_f32<E>(uint16_t((j & 1) ? (w >> 16) : (w & 0xFFFFu)));
-              ds[j] = p * x[qb][8 * t + j];  // x = dP - Delta (the product started from -Delta)
+              for (int j = 0; j < 4; ++j) {
+                ds[j] = __uint_as_float(p0[j]) * x[qb][8 * t + j];  // x = dP - Delta
+                ds[4 + j] = __uint_as_float(p1[j]) * x[qb][8 * t + 4 + j];
+              }
+            } else {
+              const u32x4 pw = s_p[pb ^ 1][pair][2 * qb + t][lane];
+#pragma unroll
+              for (int j = 0; j < 8; ++j) {
+                const uint32_t w = pw[j >> 1];
+                const float p = to_f32<E>(uint16_t((j & 1) ? (w >> 16) : (w & 0xFFFFu)));
+                ds[j] = p * x[qb][8 * t + j];  // x = dP - Delta (the product started from -Delta)
+              }
             }
-            dsb[qb][t] = u32x4{pack2<E>(ds[0], ds[1]), pack2<E>(ds[2], ds[3]), pack2<E>(ds[4], ds[5]),
-                               pack2<E>(ds[6], ds[7])};
+            dsb[qb][t] = pack8<E>(ds);
+            if constexpr (SP) dsl[qb][t] = pack8_residual<E>(ds, dsb[qb][t]);
           }
-        accumulate(s_q[qprev], dsb);  // dK^T += Q^T dS
+        accumulate(s_q[qprev], dsb, dsl);  // dK^T += Q^T dS
       }
       if (e < n) {  // dP of tile e, started from -Delta of its query (register layout as for S)
 #pragma unroll
@@ -789,23 +834,34 @@ static void launch_delta_t(const AttnArgs& a, hipStream_t st) {
   const int64_t rows = int64_t(a.B) * a.H * a.T;
   hipLaunchKernelGGL((k_delta<E, D>), dim3(unsigned((rows + RPB - 1) / RPB)), dim3(256), 0, st, a);
 }
-template <class E, int D, bool Q8 = false>
-static void launch_dq_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_delta) {
+template <class E, int D, bool Q8, bool SP>
+static void launch_dq_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_delta) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dq_blocks;
-  hipLaunchKernelGGL((k_dq<E, D, Q8>), dim3(grid), dim3(256), 0, st, a, reinterpret_cast<const uint64_t*>(plan + L.qbits),
+  hipLaunchKernelGGL((k_dq<E, D, Q8, SP>), dim3(grid), dim3(256), 0, st, a, reinterpret_cast<const uint64_t*>(plan + L.qbits),
                      reinterpret_cast<const uint32_t*>(plan + L.dq_list),
                      reinterpret_cast<const int32_t*>(plan + L.dq_count),
                      reinterpret_cast<const uint32_t*>(plan + L.dq_order), L.nT, L.n_dq_blocks, fuse_delta);
 }
 template <class E, int D, bool Q8 = false>
-static void launch_dkdv_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
+static void launch_dq_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_delta) {
+  if (a.precision == KD_PREC_SINGLE) launch_dq_s<E, D, Q8, false>(a, plan, st, fuse_delta);
+  else launch_dq_s<E, D, Q8, true>(a, plan, st, fuse_delta);
+}
+template <class E, int D, bool Q8, bool SP>
+static void launch_dkdv_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dkdv_blocks;
-  hipLaunchKernelGGL((k_dkdv<E, D, Q8>), dim3(grid), dim3(512), 0, st, a,
+  hipLaunchKernelGGL((k_dkdv<E, D, Q8, SP>), dim3(grid), dim3(512), 0, st, a,
                      reinterpret_cast<const uint64_t*>(plan + L.kbits),
                      reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
                      reinterpret_cast<const int32_t*>(plan + L.dkdv_count), L.nT, L.n_dkdv_blocks);
+}
+
+template <class E, int D, bool Q8 = false>
+static void launch_dkdv_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
+  if (a.precision == KD_PREC_SINGLE) launch_dkdv_s<E, D, Q8, false>(a, plan, st);
+  else launch_dkdv_s<E, D, Q8, true>(a, plan, st);
 }
 
 #define KD_DISPATCH(FN, ...)                                         \

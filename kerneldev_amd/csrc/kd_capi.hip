@@ -67,6 +67,8 @@ int check_common(const kd_attn_args* a) {
   if (a->dtype != KD_BF16 && a->dtype != KD_F16) return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16 or fp16");
   if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale))
     return fail(KD_ERR_INVALID, "sm_scale must be finite and > 0");
+  if (a->precision != KD_PREC_SPLIT && a->precision != KD_PREC_SINGLE)
+    return fail(KD_ERR_INVALID, "precision must be KD_PREC_SPLIT or KD_PREC_SINGLE");
   return KD_OK;
 }
 

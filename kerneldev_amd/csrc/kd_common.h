@@ -78,6 +78,22 @@ template <> KD_DEV float to_f32<F16>(uint16_t bits) {
   return float(__builtin_bit_cast(_Float16, bits));
 }
 
+// The rounding residual of a packed pair: with w = pack2<E>(lo, hi), returns
+// pack2<E>(lo - lo_w, hi - hi_w) where lo_w, hi_w are w's two values, so the
+// pair (w, residual) carries lo and hi to about twice the type's significant
+// bits (w + residual, as two MFMAs into one fp32 accumulator).
+template <class E> KD_DEV uint32_t pack2_residual(float lo, float hi, uint32_t w) {
+  return pack2<E>(lo - to_f32<E>(uint16_t(w & 0xFFFFu)), hi - to_f32<E>(uint16_t(w >> 16)));
+}
+// Eight fp32 values as a 16-bit MFMA operand (u32x4), and their residual
+template <class E> KD_DEV u32x4 pack8(const float* p) {
+  return u32x4{pack2<E>(p[0], p[1]), pack2<E>(p[2], p[3]), pack2<E>(p[4], p[5]), pack2<E>(p[6], p[7])};
+}
+template <class E> KD_DEV u32x4 pack8_residual(const float* p, const u32x4& w) {
+  return u32x4{pack2_residual<E>(p[0], p[1], w[0]), pack2_residual<E>(p[2], p[3], w[1]),
+               pack2_residual<E>(p[4], p[5], w[2]), pack2_residual<E>(p[6], p[7], w[3])};
+}
+
 // Row permutation used for the A operand of 32x32 MFMAs whose output feeds the
 // next MFMA's B operand straight from registers.  The 32x32 f32 accumulator
 // gives lane (h = lane/32, c = lane%32) the rows 8g + 4h + i (g, i in 0..3).

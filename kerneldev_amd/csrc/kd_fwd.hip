@@ -20,10 +20,16 @@
 // visited (plan list); FULL tiles skip the mask, PARTIAL tiles evaluate it.
 //
 // The running max is rescaled lazily, per lane: the accumulators are only
-// rescaled when a row's max grows by more than 2^16 (P is then <= 65536:
-// bf16 P keeps its 8 significant bits, and l and O stay far below the fp32
-// range over any row length), which removes the per-step O *= alpha of the
-// textbook loop; 2^16 rescales less often than 2^8 on outlier data (-1%).  Each wave masks by the class of its own 64-row q-tile
+// rescaled when a row's max grows by more than 2^R log2 units (rescale_log2),
+// which removes the per-step O *= alpha of the textbook loop.  Without a
+// rescale every P = exp2(S c - m_ref c) of the step is <= 2^R (up to the fp32
+// rounding of the exponent, < 2^-10 absolute at |S c| < 2^13, and v_exp_f32's
+// 1 ulp), and P is packed to the input type before P V:
+//   bf16: R = 16, P <= 65536 (bf16 reaches 3.4e38; a high threshold rescales
+//         less often than 2^8 on outlier data, -1%);
+//   fp16: R = 15, P <= 32768 * (1 + 2^-9) < 65504, the fp16 maximum (R = 16
+//         would round P in (65519.5, 65536] to +inf, and O to NaN).
+// l and O stay far below the fp32 range over any row length.  Each wave masks by the class of its own 64-row q-tile
 // against the key tile (from the list entry): FULL tiles skip the mask,
 // PARTIAL ones apply the plan's 64-bit row masks (two VALU ops per score,
 // copied one step ahead into the wave's own LDS slot), EMPTY ones mask
@@ -33,6 +39,11 @@
 #include "kd_tile.h"
 
 namespace kd {
+
+// largest log2 growth of a row's max that is absorbed without rescaling (see above)
+template <class E> constexpr float rescale_log2();
+template <> constexpr float rescale_log2<BF16>() { return 16.f; }
+template <> constexpr float rescale_log2<F16>() { return 15.f; }
 
 #ifndef FWD_QB
 #define FWD_QB 1
@@ -44,7 +55,7 @@ namespace kd {
 #define FWD_PFV 4
 #endif
 
-template <class E, int D, bool Q8, int QB>
+template <class E, int D, bool Q8, int QB, bool SP>
 __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, const uint64_t* __restrict__ qbits,
                                                                 const uint32_t* __restrict__ list,
                                                                 const int32_t* __restrict__ count,
@@ -229,7 +240,7 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
         }
       }
     }
-    // running max of this lane's rows; rescale only when it grows by > 2^16
+    // running max of this lane's rows; rescale only when it grows by > rescale_log2 (P bound)
     float ms[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -240,7 +251,7 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][qb][r]);
       mx = xhalf_max(mx);
       const float m_new = fmaxf(m_ref[qb], mx);
-      if ((m_new - m_ref[qb]) * sl2 > 16.f) {  // false for -inf - -inf (NaN); per lane
+      if ((m_new - m_ref[qb]) * sl2 > rescale_log2<E>()) {  // false for -inf - -inf (NaN); per lane
         const float alpha = (m_ref[qb] == NEG_INF) ? 0.f : fast_exp2((m_ref[qb] - m_new) * sl2);
         m_ref[qb] = m_new;
         l0[qb] *= alpha;
@@ -253,7 +264,10 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
 
     // softmax of tile e (VALU) alongside S of tile e+1 (MFMA; computed from
     // the other K buffer even past the last tile, where it is simply unused)
+    // P packed for the MFMA (pk) and, with SP, its rounding residual (pl):
+    // P V is then formed as pk V + pl V, P carried to ~16 significant bits
     u32x4 pk[QB][2][2];
+    u32x4 pl[SP ? QB : 1][2][2];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
@@ -263,12 +277,18 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
         for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(s[kb][qb][r], sl2, -ms[qb]));
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          pk[qb][kb][t] = u32x4{pack2<E>(p[8 * t + 0], p[8 * t + 1]), pack2<E>(p[8 * t + 2], p[8 * t + 3]),
-                                pack2<E>(p[8 * t + 4], p[8 * t + 5]), pack2<E>(p[8 * t + 6], p[8 * t + 7])};
+          pk[qb][kb][t] = pack8<E>(p + 8 * t);
           l0[qb] = acc_pair<E>(pk[qb][kb][t][0], l0[qb]);
           l1[qb] = acc_pair<E>(pk[qb][kb][t][1], l1[qb]);
           l0[qb] = acc_pair<E>(pk[qb][kb][t][2], l0[qb]);
           l1[qb] = acc_pair<E>(pk[qb][kb][t][3], l1[qb]);
+          if constexpr (SP) {
+            pl[qb][kb][t] = pack8_residual<E>(p + 8 * t, pk[qb][kb][t]);
+            l0[qb] = acc_pair<E>(pl[qb][kb][t][0], l0[qb]);
+            l1[qb] = acc_pair<E>(pl[qb][kb][t][1], l1[qb]);
+            l0[qb] = acc_pair<E>(pl[qb][kb][t][2], l0[qb]);
+            l1[qb] = acc_pair<E>(pl[qb][kb][t][3], l1[qb]);
+          }
         }
       }
     }
@@ -292,7 +312,10 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
         const int t4 = i / DB, db = i % DB;
         __builtin_amdgcn_sched_barrier(0x406);
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) o[qb][db] = mfma32x32x16<E>(vv[i % PFV], pk[qb][t4 >> 1][t4 & 1], o[qb][db]);
+        for (int qb = 0; qb < QB; ++qb) {
+          o[qb][db] = mfma32x32x16<E>(vv[i % PFV], pk[qb][t4 >> 1][t4 & 1], o[qb][db]);
+          if constexpr (SP) o[qb][db] = mfma32x32x16<E>(vv[i % PFV], pl[qb][t4 >> 1][t4 & 1], o[qb][db]);
+        }
         if (i + PFV < NV) vv[i % PFV] = read_v(i + PFV);
       }
       __builtin_amdgcn_sched_barrier(0x406);
@@ -329,8 +352,7 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
           const u32x2 w = {pack2<E>(f[0], f[1]), pack2<E>(f[2], f[3])};
           *reinterpret_cast<u32x2*>(og + d0) = w;
           if (lg != nullptr) {
-            const u32x2 r = {pack2<E>(f[0] - to_f32<E>(uint16_t(w[0] & 0xFFFFu)), f[1] - to_f32<E>(uint16_t(w[0] >> 16))),
-                             pack2<E>(f[2] - to_f32<E>(uint16_t(w[1] & 0xFFFFu)), f[3] - to_f32<E>(uint16_t(w[1] >> 16)))};
+            const u32x2 r = {pack2_residual<E>(f[0], f[1], w[0]), pack2_residual<E>(f[2], f[3], w[1])};
             *reinterpret_cast<u32x2*>(lg + d0) = r;
           }
         }
@@ -341,28 +363,34 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
   }
 }
 
-template <class E, int D, bool Q8 = false>
+template <class E, int D, bool Q8, bool SP>
 static void launch_fwd_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   constexpr int QB = FWD_QB;
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const int nQB = L.n_fwd_blocks;
   const unsigned grid = unsigned(a.B) * a.H * nQB;
-  hipLaunchKernelGGL((k_fwd<E, D, Q8, QB>), dim3(grid), dim3(256 / QB), 0, st, a,
+  hipLaunchKernelGGL((k_fwd<E, D, Q8, QB, SP>), dim3(grid), dim3(256 / QB), 0, st, a,
                      reinterpret_cast<const uint64_t*>(plan + L.qbits),
                      reinterpret_cast<const uint32_t*>(plan + L.fwd_list),
                      reinterpret_cast<const int32_t*>(plan + L.fwd_count),
                      reinterpret_cast<const uint32_t*>(plan + L.fwd_order), L.nT, nQB);
 }
 
+template <class E, int D, bool Q8 = false>
+static void launch_fwd_p(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
+  if (a.precision == KD_PREC_SINGLE) launch_fwd_t<E, D, Q8, false>(a, plan, st);
+  else launch_fwd_t<E, D, Q8, true>(a, plan, st);
+}
+
 int launch_fwd(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   if (a.q8 != nullptr) {  // fp8 QK^T: bf16, head dim 128 (checked by the C ABI)
-    launch_fwd_t<BF16, 128, true>(a, plan, st);
+    launch_fwd_p<BF16, 128, true>(a, plan, st);
   } else if (a.dtype == KD_BF16) {
-    if (a.D == 64) launch_fwd_t<BF16, 64>(a, plan, st);
-    else launch_fwd_t<BF16, 128>(a, plan, st);
+    if (a.D == 64) launch_fwd_p<BF16, 64>(a, plan, st);
+    else launch_fwd_p<BF16, 128>(a, plan, st);
   } else {
-    if (a.D == 64) launch_fwd_t<F16, 64>(a, plan, st);
-    else launch_fwd_t<F16, 128>(a, plan, st);
+    if (a.D == 64) launch_fwd_p<F16, 64>(a, plan, st);
+    else launch_fwd_p<F16, 128>(a, plan, st);
   }
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }

@@ -73,9 +73,20 @@ def assert_close(name, x, ref, max_abs=MAX_ABS, rel_rms=REL_RMS, out_dtype=None)
     ma, rr, ex = errors(x, ref, out_dtype)
     assert np.isfinite(ma), f"{name}: non-finite values"
     assert ex <= max_abs and rr <= rel_rms, (
-        f"{name}: max_abs={ma:.3e} (beyond 1 ulp: {ex:.3e}) rel_rms={rr:.3e} max|ref|={ref.abs().max().item():.3e}")
+        f"{name}: max_abs={ma:.3e} (beyond 1 ulp: {ex:.3e}) rel_rms={rr:.3e} max|ref|={ref.abs().max().item():.3e}"
+        f" worst element: {worst_element(x, ref, out_dtype)}")
     print(f"  {name}: max_abs={ma:.3e} beyond_ulp={ex:.3e} rel_rms={rr:.3e}")
     return ma, rr
+
+
+def worst_element(x, ref, out_dtype=None):
+    """Index, value and reference of the element furthest beyond one output ulp."""
+    out_dtype = out_dtype or x.dtype
+    xd, rd = x.detach().double().cpu(), ref.detach().double().cpu()
+    ex = ((xd - rd).abs() - ulp(rd, out_dtype)).flatten()
+    i = int(ex.argmax())
+    idx = np.unravel_index(i, tuple(rd.shape))
+    return f"at {tuple(int(j) for j in idx)} got {xd.flatten()[i].item():.6g} ref {rd.flatten()[i].item():.6g}"
 
 
 def oracle_mask(inp, T, lens=None, attention_mask_given=False):

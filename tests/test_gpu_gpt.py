@@ -2,35 +2,34 @@
 64, SwiGLU 2048, vocab 262) through the MI355X attention, against the same
 bf16 weights with a dense fp32 masked reference attention.
 
-Only the attention differs between the two runs: the reference upcasts q/k/v
-to fp32, applies torch SDPA with the dense hierarchical mask (the oracle's
-formula) and casts back.  Compared: the final hidden states, the
-cocktail-party span scores, and -- for a well-conditioned objective -- the
-next-token loss through the tied head and every parameter's gradient.  (At
-random init the span scores are O(500) and equal to within a few units, so
-the cocktail-party cross entropy is decided by differences far below the
-bf16 spacing of the hidden states; its gradient is not a useful comparison.)
+Only the attention differs between the runs: the references upcast q/k/v to
+fp32 (or fp64), apply torch SDPA with the dense hierarchical mask (the
+oracle's formula) and cast back.
 """
 import copy
 
 import pytest
 import torch
-import torch.nn.functional as F
 
-from kerneldev_amd.gpt import GPTModel, config5_batch, span_scores
+from kerneldev_amd.gpt import GPTModel, config5_batch
 from oracle.mask import dense_mask
 
 pytestmark = pytest.mark.gpu
 
 
-def dense_reference_attention(q, k, v, lens=None, causal=True, attention_mask=None, in_span=None, span_id=None,
-                              is_prefix=None):
-    B, H, T, D = q.shape
-    m = torch.from_numpy(dense_mask(T, B=B, in_span=in_span.cpu().numpy(), span_id=span_id.cpu().numpy(),
-                                    is_prefix=is_prefix.cpu().numpy())).to(q.device)
-    o = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float(), attn_mask=m[:, None],
-                                                         scale=D ** -0.5)
-    return o.to(q.dtype)
+def dense_attention(dtype):
+    """Dense masked attention on the GPU in ``dtype`` (torch SDPA, math backend)
+    with the oracle's mask, cast back to the model dtype."""
+    def attention(q, k, v, lens=None, causal=True, attention_mask=None, in_span=None, span_id=None,
+                  is_prefix=None):
+        B, H, T, D = q.shape
+        m = torch.from_numpy(dense_mask(T, B=B, in_span=in_span.cpu().numpy(), span_id=span_id.cpu().numpy(),
+                                        is_prefix=is_prefix.cpu().numpy())).to(q.device)
+        with torch.nn.attention.sdpa_kernel(torch.nn.attention.SDPBackend.MATH):
+            o = torch.nn.functional.scaled_dot_product_attention(q.to(dtype), k.to(dtype), v.to(dtype),
+                                                                 attn_mask=m[:, None], scale=D ** -0.5)
+        return o.to(q.dtype)
+    return attention
 
 
 def _rel(a, b):
@@ -38,44 +37,99 @@ def _rel(a, b):
     return ((a - b).pow(2).mean().sqrt() / b.pow(2).mean().sqrt().clamp_min(1e-30)).item()
 
 
-def _step(model, batch, dev):
+def _forward_step(model, batch, dev, cotangent):
+    """GPTModel.forward (the path training takes: shared plan, bthd output,
+    cocktail-party head) and a backward of <scores, cotangent>."""
     tokens, in_span, span_id, is_prefix, correct = (x.to(dev) for x in batch)
     model.zero_grad(set_to_none=True)
-    h = model.hidden(tokens, in_span, span_id, is_prefix)
-    scores = span_scores(tokens, h)
-    logits = model.head(h).float()
-    loss = F.cross_entropy(logits[:, :-1].reshape(-1, logits.shape[-1]), tokens[:, 1:].reshape(-1), ignore_index=0)
-    loss.backward()
+    captured = {}
+    hook = model.norm_out.register_forward_hook(lambda mod, inp, out: captured.__setitem__("h", out))
+    try:
+        scores, loss = model(tokens, correct_idx=correct, in_span=in_span, span_id=span_id, is_prefix=is_prefix)
+    finally:
+        hook.remove()
+    (scores.float() * cotangent.to(dev)).sum().backward()
     torch.cuda.synchronize()
-    return (h.detach(), scores.detach(), loss.detach(),
+    return (captured["h"].detach(), scores.detach().float(), loss.detach().float(),
             {n: p.grad.detach().float() for n, p in model.named_parameters()})
 
 
-def test_config5_training_step_matches_dense_reference(dev):
+def test_config5_forward_step_matches_dense_reference(dev):
+    """Config 5 as specified: B = 8 sequences of L = 2048 through GPTModel.forward.
+
+    Three copies of one bf16 model run the same forward and backward: with
+    kdattn (one plan for all layers from the collate metadata, O in
+    [B, L, H, d] memory), with the dense fp32 masked attention the north_star
+    names as the reference, and with the same attention in fp64 (the exact
+    attention, up to the final bf16 cast).  Compared: the final hidden states,
+    the span scores, the cocktail-party loss, and every parameter's gradient of
+    <scores, g> for a seeded cotangent g.
+
+    Bar.  Every other op of the model rounds to bf16, so a change of attention
+    at the level of one rounding becomes bf16 noise downstream: the fp32
+    reference itself sits about 1e-2 (rel-RMS) from the fp64 model in the
+    hidden states and up to 1.5e-2 in the gradients.  kdattn must be as close
+    to the fp64 model as the fp32 reference is: its rel-RMS at most 1.25x the
+    reference's for the hidden states, the scores, and the median and the
+    largest over the gradient tensors, and at most 1.5x on any single gradient
+    tensor (each such figure is one sample of rounding noise); and the hidden
+    states within 1e-2 of the reference.  |d loss| is at most twice the largest score difference
+    (cross entropy is 2-Lipschitz in the max norm of the scores).  The loss's own
+    gradient is not compared: at random init the scores are O(500) and equal
+    to within a few units, so softmax(scores) turns bf16 noise in the hidden
+    states into O(1) changes of d loss / d scores.
+    """
     torch.manual_seed(0)
     model = GPTModel().to(dev).to(torch.bfloat16)
-    ref = copy.deepcopy(model)
-    for blk in ref.blocks:
-        blk.attn.attention = dense_reference_attention
-    batch = config5_batch(B=2, L=2048, seed=3)
-    print("config5 step: kdattn", flush=True)
-    h, sc, loss, grads = _step(model, batch, dev)
-    print("config5 step: dense fp32 reference attention", flush=True)
-    h_r, sc_r, loss_r, grads_r = _step(ref, batch, dev)
-    rel_h = _rel(h, h_r)
-    sc_err = (sc - sc_r).abs().max().item()
-    print(f"  hidden rel-RMS {rel_h:.3e}; span scores max|diff| {sc_err:.3e} of max {sc_r.abs().max().item():.1f}; "
-          f"loss {loss.item():.6f} ref {loss_r.item():.6f}")
-    assert rel_h <= 1e-2
-    assert sc_err <= 2e-2 * max(1.0, sc_r.abs().max().item())
-    assert torch.isfinite(loss) and abs(loss.item() - loss_r.item()) <= 1e-3 * abs(loss_r.item())
-    worst, worst_name = 0.0, ""
-    for name, g in grads.items():
-        rel = _rel(g, grads_r[name])
-        if rel > worst:
-            worst, worst_name = rel, name
-    print(f"  worst per-parameter grad rel-RMS {worst:.3e} ({worst_name})")
-    assert worst <= 2e-2, f"{worst_name}: grad rel-RMS {worst:.3e}"
+    refs = {}
+    for name, dt in (("fp32", torch.float32), ("fp64", torch.float64)):
+        refs[name] = copy.deepcopy(model)
+        for blk in refs[name].blocks:
+            blk.attn.attention = dense_attention(dt)
+    batch = config5_batch(B=8, L=2048, seed=3)
+    n_spans = int((batch[0] == 3).sum(dim=1).max())
+    g = torch.randn(8, n_spans, generator=torch.Generator("cpu").manual_seed(5))
+    print("config5 B=8 L=2048 GPTModel.forward: kdattn (plan + bthd)", flush=True)
+    kd = _forward_step(model, batch, dev, g)
+    out = {}
+    for name, m in refs.items():
+        print(f"config5 B=8 L=2048 GPTModel.forward: dense {name} attention", flush=True)
+        out[name] = _forward_step(m, batch, dev, g)
+    r32, r64 = out["fp32"], out["fp64"]
+    failures = []
+
+    def check(what, got, ref32, exact, factor=1.25):
+        e_kd, e_32 = _rel(got, exact), _rel(ref32, exact)
+        ok = e_kd <= factor * e_32 + 1e-6
+        if not ok:
+            failures.append(f"{what}: kdattn {e_kd:.3e} vs fp32 reference {e_32:.3e} (from fp64)")
+        return e_kd, e_32
+
+    e_kd, e_32 = check("hidden", kd[0], r32[0], r64[0])
+    rel_h = _rel(kd[0], r32[0])
+    print(f"  hidden rel-RMS from fp64: kdattn {e_kd:.3e}, fp32 reference {e_32:.3e}; kdattn vs fp32 {rel_h:.3e}")
+    e_kd, e_32 = check("scores", kd[1], r32[1], r64[1])
+    sc_err = (kd[1] - r32[1]).abs().max().item()
+    print(f"  scores rel-RMS from fp64: kdattn {e_kd:.3e}, fp32 reference {e_32:.3e}; max|diff| vs fp32 "
+          f"{sc_err:.3e} of max {r32[1].abs().max().item():.1f}")
+    d_loss = abs(kd[2].item() - r32[2].item())
+    print(f"  loss {kd[2].item():.6f}, fp32 reference {r32[2].item():.6f}, fp64 {r64[2].item():.6f}")
+    ratios = {}
+    for name in kd[3]:
+        e_kd, e_32 = check(name, kd[3][name], r32[3][name], r64[3][name], factor=1.5)
+        ratios[name] = (e_kd, e_32)
+    for stat, pick in (("median", lambda v: sorted(v)[len(v) // 2]), ("max", max)):
+        s_kd, s_32 = pick([v[0] for v in ratios.values()]), pick([v[1] for v in ratios.values()])
+        print(f"  gradient rel-RMS from fp64, {stat} over tensors: kdattn {s_kd:.3e}, fp32 reference {s_32:.3e}")
+        if s_kd > 1.25 * s_32 + 1e-6:
+            failures.append(f"gradient {stat}: kdattn {s_kd:.3e} vs fp32 reference {s_32:.3e}")
+    worst = max(ratios, key=lambda n: ratios[n][0] / max(ratios[n][1], 1e-30))
+    print(f"  gradients: worst ratio {ratios[worst][0] / ratios[worst][1]:.3f} at {worst} "
+          f"(kdattn {ratios[worst][0]:.3e}, fp32 reference {ratios[worst][1]:.3e} from fp64); max kdattn "
+          f"{max(v[0] for v in ratios.values()):.3e}, max fp32 reference {max(v[1] for v in ratios.values()):.3e}")
+    assert rel_h <= 1e-2, f"hidden rel-RMS vs the fp32 reference {rel_h:.3e}"
+    assert torch.isfinite(kd[2]) and d_loss <= 2 * sc_err + 1e-6
+    assert not failures, "; ".join(failures)
 
 
 def test_config5_full_batch_step_runs(dev):

@@ -133,6 +133,40 @@ def test_metadata_edge_cases():
     assert s2[2].tolist() == [0, 0, -1, -1]
 
 
+def _malformed_rows(seed, B=4, T=300):
+    rng = np.random.default_rng(seed)
+    ids = np.array([PAD, CLS, MASK, SPAN, ES, MASKQ, 40, 41, 42])
+    rows = rng.choice(ids, size=(B, T), p=[.1, .02, .02, .08, .08, .02, .3, .3, .08])
+    rows[-1, :] = 50  # no special token at all
+    return rows
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_fallback_and_teacher_rules_vs_vectorised_restatement(seed):
+    """The per-token oracle rules against a second, vectorised restatement of
+    model.py:217-233 (cumsum expressions as written there) and
+    train_loop.py:406-435, on rows with nested / unpaired [SPAN] [ES], several
+    [CLS] and [MASKQ], and none at all."""
+    rows = _malformed_rows(seed)
+    x = torch.from_numpy(rows)
+    in_span = (torch.cumsum((x == SPAN).int(), dim=1) - torch.cumsum((x == ES).int(), dim=1)) > 0
+    span_id = torch.cumsum((x == SPAN).int(), dim=1).to(torch.int64)
+    span_id[~in_span] = 0
+    span_id[x == MASKQ] = -1
+    is_prefix = torch.zeros_like(in_span)
+    for b in range(x.shape[0]):
+        pos = (x[b] == CLS).nonzero(as_tuple=True)[0]
+        if len(pos) > 0:
+            is_prefix[b, :pos[0].item() + 1] = True
+    f_in, f_sid, f_pre = metadata.fallback_metadata(rows)
+    np.testing.assert_array_equal(f_in, in_span.numpy())
+    np.testing.assert_array_equal(f_sid, span_id.numpy())
+    np.testing.assert_array_equal(f_pre, is_prefix.numpy())
+    t_in, t_sid, t_pre = metadata.teacher_forcing_metadata(rows)
+    assert not t_in.any() and not t_sid.any()
+    np.testing.assert_array_equal(t_pre, is_prefix.numpy())
+
+
 # ------------------------------------------------------------------ tile map
 def test_classify_and_lists_bruteforce():
     rng = np.random.default_rng(2)
