@@ -242,6 +242,18 @@ int kd_attn_bwd_dkdv(const kd_attn_args *a, const void *plan, void *stream);
  * attention_backward_adapter (original_kernel.py:1806-1898). */
 int kd_attn_bwd(const kd_attn_args *a, const void *plan, void *stream);
 
+/* The whole backward as kd_attn_bwd, with a->delta ignored: its workspace
+ * (2 * B*H*T floats) lives in a library-owned device array of
+ * KD_NOALLOC_WORKSPACE_FLOATS floats (16 MiB) on each GPU, held until the
+ * process ends, and no call allocates.  No counterpart in the reference: this
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc).  B*H*T above
+ * KD_NOALLOC_WORKSPACE_FLOATS / 2 returns KD_ERR_UNSUPPORTED.  Every call on one
+ * GPU uses that GPU's one array, so calls that overlap on one GPU (other
+ * streams or threads) race and must be ordered by the caller. */
+#define KD_NOALLOC_WORKSPACE_FLOATS (1 << 22)
+int kd_attn_bwd_noalloc(const kd_attn_args *a, const void *plan, void *stream);
+
 /* Dense bool mask [B, H, T, T] (element strides b, h, q, k) from the plan's
  * codes.  Replaces the RETURN_ATTENTION_MASK store of _flash_attn_fwd
  * (original_kernel.py:519-545). */

@@ -21,6 +21,7 @@ KD_BF16, KD_F16 = 0, 1
 KD_I64, KD_I32 = 0, 1
 KD_MODE_FORMULA, KD_MODE_CAUSAL, KD_MODE_ALL = 0, 1, 2
 KD_PREC_SPLIT, KD_PREC_SINGLE = 0, 1
+KD_NOALLOC_WORKSPACE_FLOATS = 1 << 22
 
 I64x2 = c_int64 * 2
 I64x3 = c_int64 * 3
@@ -128,6 +129,7 @@ SIGNATURES = {
     "kd_attn_bwd_dq_delta": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
     "kd_attn_bwd_dkdv": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
     "kd_attn_bwd": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
+    "kd_attn_bwd_noalloc": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
     "kd_mask_dense": (c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p,
                               POINTER(c_int64), c_void_p]),
 }

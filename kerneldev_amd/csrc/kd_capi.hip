@@ -289,6 +289,21 @@ int kd_attn_bwd(const kd_attn_args* a, const void* plan, void* stream) {
   return r ? r : kd_attn_bwd_dkdv(a, plan, stream);
 }
 
+int kd_attn_bwd_noalloc(const kd_attn_args* a, const void* plan, void* stream) {
+  if (a == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
+  if (a->B >= 1 && a->H >= 1 && a->T >= 1 &&
+      2 * int64_t(a->B) * a->H * a->T > int64_t(KD_NOALLOC_WORKSPACE_FLOATS))
+    return fail(KD_ERR_UNSUPPORTED,
+                "kd_attn_bwd_noalloc: B * H * T exceeds the workspace (KD_NOALLOC_WORKSPACE_FLOATS / 2 rows)");
+  kd_attn_args w = *a;
+  const char* err = nullptr;
+  float* ws = nullptr;
+  int r = kd::noalloc_workspace(&ws, &err);
+  if (r) return fail(r, err);
+  w.delta = ws;
+  return kd_attn_bwd(&w, plan, stream);
+}
+
 int kd_mask_dense(const void* plan, int32_t B, int32_t H, int32_t T, int32_t D, uint8_t* out,
                   const int64_t* strides, void* stream) {
   if (plan == nullptr || out == nullptr || strides == nullptr) return fail(KD_ERR_INVALID, "NULL argument");

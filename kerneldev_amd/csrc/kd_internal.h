@@ -48,6 +48,9 @@ int launch_hadamard(const kd_rot_args& a, hipStream_t st);
 int launch_quant(const kd_quant_args& a, hipStream_t st);
 int launch_span(const kd_span_args& a, hipStream_t st);
 int launch_span_bwd(const kd_span_args& a, hipStream_t st);
+// Device address of the no-allocation workspace on the current device
+// (kd_noalloc.hip); KD_OK, or a status with *err set.
+int noalloc_workspace(float** out, const char** err);
 
 // Linear workgroup id -> work index so that each XCD (workgroups are dealt
 // round-robin over the 8 XCDs) receives one contiguous range of work items,

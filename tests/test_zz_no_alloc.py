@@ -1,0 +1,62 @@
+"""GPU: kd_attn_bwd_noalloc (workspace in the library's device array) against
+kd_attn_bwd (caller's workspace), through the C ABI, on two calls in a row --
+the second smaller -- so the array's contents from the first call must not
+leak into the second.  Both run the same kernels on the same inputs, so dQ,
+dK and dV must agree bit for bit.
+"""
+import ctypes
+
+import pytest
+import torch
+
+from kerneldev_amd import _lib
+from kerneldev_amd.attention import _attn_args, _fwd_op, _ptr, _strides3
+from kerneldev_amd.synth import CONFIG3_LAYOUT, cocktail_batch, qkvdo
+
+pytestmark = pytest.mark.gpu
+
+
+def _backward_both(dev, B, H, T, D, seed):
+    tokens, in_span, span_id, is_prefix = cocktail_batch(B, 1024, CONFIG3_LAYOUT, seed=seed)
+    meta = [x[:, :T].to(dev) for x in (in_span, span_id, is_prefix)]
+    q, k, v, do = (x.to(dev) for x in qkvdo(B, H, T, D, seed=seed + 1))
+    sc = D ** -0.5
+    o, lse, plan, o_lo, *_ = _fwd_op(q, k, v, None, *meta, sc, 0, True)
+    lib = _lib.load()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    outs = []
+    for noalloc in (False, True):
+        dq, dk, dv = torch.full_like(q, float("nan")), torch.full_like(k, float("nan")), torch.full_like(v, float("nan"))
+        a = _attn_args(q, k, v, sc)
+        a.o, a.o_strides, a.lse, a.o_lo = o.data_ptr(), _strides3(o), lse.data_ptr(), o_lo.data_ptr()
+        a.dout, a.do_strides = do.data_ptr(), _strides3(do)
+        a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+        a.dq_strides, a.dk_strides, a.dv_strides = _strides3(dq), _strides3(dk), _strides3(dv)
+        if noalloc:
+            a.delta = None  # ignored: the library's own workspace is used
+            _lib.check(lib.kd_attn_bwd_noalloc(ctypes.byref(a), _ptr(plan), stream), "kd_attn_bwd_noalloc")
+        else:
+            delta = torch.empty((2, B, H, T), dtype=torch.float32, device=dev)
+            a.delta = delta.data_ptr()
+            _lib.check(lib.kd_attn_bwd(ctypes.byref(a), _ptr(plan), stream), "kd_attn_bwd")
+        torch.cuda.synchronize()
+        outs.append((dq, dk, dv))
+    return outs
+
+
+def test_noalloc_backward_matches_allocating_entry_point(dev):
+    for B, H, T, D, seed in ((2, 4, 1024, 128, 80), (1, 2, 300, 64, 82)):
+        print(f"noalloc backward B={B} H={H} T={T} D={D}", flush=True)
+        ref, got = _backward_both(dev, B, H, T, D, seed)
+        for name, x, y in zip(("dq", "dk", "dv"), ref, got):
+            assert torch.isfinite(y).all(), name
+            assert torch.equal(x, y), f"{name} differs (B={B} T={T} D={D})"
+
+
+def test_noalloc_rejects_oversized_workspace():
+    lib = _lib.load()
+    a = _lib.AttnArgs()
+    a.B, a.H, a.T, a.D = 64, 64, 8192, 128  # 2 B H T floats > KD_NOALLOC_WORKSPACE_FLOATS
+    assert 2 * a.B * a.H * a.T > _lib.KD_NOALLOC_WORKSPACE_FLOATS
+    assert lib.kd_attn_bwd_noalloc(ctypes.byref(a), None, None) == _lib.KD_ERR_UNSUPPORTED
+    assert "exceeds the workspace" in lib.kd_last_error_string().decode()
