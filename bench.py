@@ -77,14 +77,63 @@ def parse():
     ap.add_argument("--precision", default="tf32", choices=("tf32", "ieee", "bf16"),
                     help="flash_attention's precision: tf32 / ieee (the default kernels, P and dS as "
                          "16-bit hi + lo pairs) or the extension bf16 (P and dS rounded once)")
+    ap.add_argument("--no-fp8-run", action="store_true",
+                    help="config 4: skip the second (fp8 e4m3 QK^T) run reported beside the bf16 line")
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU baseline leg (profiling runs)")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0,
-                    help="target CPU time of the baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=25.0,
+                    help="CPU time bound of the baseline (it stops after the head that crosses it)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one device-to-device copy of this many MiB before timing, as the "
                          "known-size reference for HBM traffic counters")
     return ap.parse_args()
+
+
+def blended_peak(flops_per_entry: int) -> float:
+    """Peak for a kernel doing ``flops_per_entry`` d-units per entry of which the
+    2 d of Q K^T run on fp8 MFMA and the rest on bf16: the time-weighted blend."""
+    f = flops_per_entry
+    return f / (2 / PEAK_FP8_TFLOPS + (f - 2) / PEAK_BF16_TFLOPS)
+
+
+def step_blended_peak() -> float:
+    """The same blend for a whole fp8 step: Q K^T in the forward, dQ and dK/dV
+    kernels (3 x 2 d) at fp8, the other 8 d of the 14 d useful at bf16 (the
+    recomputations are not counted, as in ``value``)."""
+    useful = USEFUL_FWD + USEFUL_BWD
+    return useful / (6 / PEAK_FP8_TFLOPS + (useful - 6) / PEAK_BF16_TFLOPS)
+
+
+def measure(torch, st, steps: int, warmup: int):
+    """Warm up, then time ``steps`` steps between two synchronisations, with HIP
+    events on the launch stream between the kernels of every step.
+    Returns (ms per step, {kernel: mean ms}, event ms per step, nnz per head)."""
+    for _ in range(max(0, warmup)):
+        st.run()
+    torch.cuda.synchronize()
+    nnz = st.nnz_total()
+    names = [n for n, _ in st.launches()]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        st.run(evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_kernel = {n: statistics.mean(evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(steps))
+                  for j, n in enumerate(names)}
+    event_ms = statistics.mean(evs[i][0].elapsed_time(evs[i][-1]) for i in range(steps))
+    return 1e3 * wall / steps, per_kernel, event_ms, nnz
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_threads() -> int:
@@ -261,7 +310,13 @@ def cpu_baseline(inp, budget_s: float):
         "value": flops / elapsed / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
+        "cpu_model": cpu_model(),
         "kind": "port",
+        # value is the measured rate over the heads timed (useful flops of
+        # those heads / their summed time), not extrapolated from them
+        "extrapolated": False,
+        "heads_timed": len(done),
+        "heads_total": B * H,
         "sample": (f"{len(done)} of {B * H} (b, h) heads of the same inputs, fp32 eager "
                    f"torch SDPA with the dense hierarchical bool mask, fwd+bwd via autograd, "
                    f"{elapsed:.1f} s"),
@@ -299,23 +354,7 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    for _ in range(max(0, args.warmup)):
-        st.run()
-    torch.cuda.synchronize()
-    nnz = st.nnz_total()
-
-    names = [n for n, _ in st.launches()]
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        st.run(evs[i])
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = 1e3 * wall / args.steps
-    per_kernel = {n: statistics.mean(evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(args.steps))
-                  for j, n in enumerate(names)}
-    event_ms = statistics.mean(evs[i][0].elapsed_time(evs[i][-1]) for i in range(args.steps))
+    ms_step, per_kernel, event_ms, nnz = measure(torch, st, args.steps, args.warmup)
 
     useful = (USEFUL_FWD + USEFUL_BWD) * D * H * nnz
     value = useful / (ms_step * 1e-3) / 1e12
@@ -324,18 +363,36 @@ def main():
     dom_flops = KERNEL_FLOPS_PER_ENTRY[dom] * D * H * nnz
     achieved = dom_flops / (per_kernel[dom] * 1e-3) / 1e12
     traffic = CONFIG4_TRAFFIC_BYTES[args.qk_dtype].get(dom) if (args.config == 4 and hadamard) else None
-    peak = PEAK_BF16_TFLOPS
-    if fp8:
-        # the Q K^T share (2d of the kernel's flops per entry) runs at the fp8
-        # peak, the rest at the bf16 peak: the time-weighted blend
-        f = KERNEL_FLOPS_PER_ENTRY[dom]
-        peak = f / (2 / PEAK_FP8_TFLOPS + (f - 2) / PEAK_BF16_TFLOPS)
+    peak = blended_peak(KERNEL_FLOPS_PER_ENTRY[dom]) if fp8 else PEAK_BF16_TFLOPS
     roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                 "peak": round(peak, 1), "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                 "traffic": traffic, "avg_launch_ms": round(per_kernel[dom], 4),
                 "algorithmic_tflop_per_launch": round(dom_flops / 1e12, 4)}
     kernel_tflops = {n: round(KERNEL_FLOPS_PER_ENTRY[n] * D * H * nnz / (per_kernel[n] * 1e-3) / 1e12, 1)
                      for n in ("fwd", "dq", "dkdv")}
+
+    # config 4's second run (BASELINE: "once in bf16 and once with fp8 e4m3
+    # QK^T"), timed in the same invocation and reported beside the bf16 line
+    fp8_run = None
+    if args.config == 4 and not fp8 and hadamard and not args.no_fp8_run:
+        del st
+        torch.cuda.empty_cache()
+        st8 = Step(inp, dev, hadamard=True, qk_dtype="fp8_e4m3", precision=args.precision)
+        ms8, pk8, _, nnz8 = measure(torch, st8, args.steps, args.warmup)
+        del st8
+        dom8 = max(("fwd", "dq", "dkdv"), key=lambda n: pk8[n])
+        ach8 = KERNEL_FLOPS_PER_ENTRY[dom8] * D * H * nnz8 / (pk8[dom8] * 1e-3) / 1e12
+        val8 = useful / (ms8 * 1e-3) / 1e12
+        fp8_run = {
+            "qk_dtype": "fp8_e4m3", "ms_per_step": round(ms8, 4), "value": round(val8, 2), "unit": "TFLOP/s",
+            "frac_of_bf16_peak": round(val8 / PEAK_BF16_TFLOPS, 4),
+            # the whole step against the peak blended over its kernels' flops:
+            # Q K^T (2d of the 14d per entry, in the three kernels) at the fp8 peak
+            "frac_of_blended_peak": round(val8 / step_blended_peak(), 4),
+            "kernel_ms": {n: round(x, 4) for n, x in pk8.items()},
+            "dominant_kernel": dom8, "dominant_frac_of_blended_peak": round(ach8 / blended_peak(
+                KERNEL_FLOPS_PER_ENTRY[dom8]), 4),
+        }
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -370,6 +427,7 @@ def main():
             "precision": args.precision,
         },
         "roofline": roofline,
+        "fp8_run": fp8_run,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -189,6 +189,24 @@ def plan_bytes(B: int, T: int, D: int) -> int:
     return int(n)
 
 
+def plan_nbytes(B, T, D):
+    """kd_plan_bytes restated in integer arithmetic that also accepts torch
+    SymInts (the custom ops' fake kernels size the plan with it under
+    torch.compile with dynamic shapes).  Sections in kd_plan_layout's order,
+    each rounded up to 256 bytes; the work lists group two 64-row tiles."""
+    def r(x):
+        return ((x + 255) // 256) * 256
+
+    nT = (T + 63) // 64
+    nb = (nT + 1) // 2  # blocks of the forward, dQ and dK/dV lists
+    BT, BTT = B * T, B * nT * nT
+    return (r(BT * 4) + r(BT * 4) + r(BT * 4) + r(BT * 8) + r(B * 4) + r(BT) + r(BT * 8) + r(BT)
+            + r(BTT) + r(BTT * 4)
+            + 3 * (r(B * nb * nT * 4) + r(B * nb * 4))
+            + r(BTT * 512) + r(BTT * 512)
+            + 2 * r(B * nb * 4))
+
+
 PLAN_FIELDS = ("codes", "rep", "cls", "nnz", "fwd_list", "fwd_count", "dq_list", "dq_count",
                "dkdv_list", "dkdv_count", "nT", "fwd_group", "dq_group", "dkdv_group",
                "n_fwd_blocks", "n_dq_blocks", "n_dkdv_blocks", "qbits", "kbits", "fwd_order", "dq_order")

@@ -74,7 +74,9 @@ def _mode(in_span, span_id, is_prefix, has_attention_mask, causal) -> int:
 def build_plan(B, T, D, device, mode, in_span=None, span_id=None, is_prefix=None, lens=None):
     """Run ``kd_plan_build`` and return the plan as a uint8 device tensor."""
     lib = _lib.load()
-    plan = torch.empty(_lib.plan_bytes(B, T, D), dtype=torch.uint8, device=device)
+    # zero-filled: the build leaves the bit masks of non-PARTIAL tiles and the
+    # section padding unwritten, and an op's outputs should not carry stale bytes
+    plan = torch.zeros(_lib.plan_bytes(B, T, D), dtype=torch.uint8, device=device)
     m = MetaArgs()
     m.B, m.T, m.D, m.mode = B, T, D, mode
     if in_span is not None:
@@ -124,7 +126,7 @@ def build_plan_from_tokens(tokens: torch.Tensor, head_dim: int, rule: str = "col
     if lens is not None and (lens.dtype != torch.int32 or lens.dim() != 1 or lens.shape[0] != tokens.shape[0]):
         raise ValueError("lens must be an int32 tensor of shape [batch]")
     B, T = tokens.shape
-    plan = torch.empty(_lib.plan_bytes(B, T, head_dim), dtype=torch.uint8, device=tokens.device)
+    plan = torch.zeros(_lib.plan_bytes(B, T, head_dim), dtype=torch.uint8, device=tokens.device)
     t = _lib.TokenArgs()
     t.tokens = tokens.data_ptr()
     t.tokens_strides[0], t.tokens_strides[1] = tokens.stride()
@@ -187,6 +189,9 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
                        torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     B, H, T, D = q.shape
+    # layouts the kernels take (unit d-stride, aligned, 8-element strides);
+    # anything else is copied here, inside the op, where the data is real
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     # a caller's plan is used as is (and not returned: outputs may not alias inputs)
     plan = plan_in if plan_in is not None else build_plan(B, T, D, q.device, mode, in_span, span_id, is_prefix, lens)
     # signs: attention of Q R and K R, returned for the backward (which hands
@@ -226,7 +231,7 @@ def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_l
     sc_shape = (B, H) if signs is not None and quant_fp8 else (0,)
     return (_new_out(B, H, T, D, q, bthd),
             torch.empty((B, H, T), dtype=torch.float32, device=q.device),
-            torch.empty(_lib.plan_bytes(B, T, D) if plan_in is None else 0, dtype=torch.uint8, device=q.device),
+            torch.empty(_lib.plan_nbytes(B, T, D) if plan_in is None else 0, dtype=torch.uint8, device=q.device),
             torch.empty((B, H, T, D) if need_lo else (0,), dtype=q.dtype, device=q.device),
             torch.empty(rot_shape, dtype=q.dtype, device=q.device),
             torch.empty(rot_shape, dtype=k.dtype, device=k.device),
@@ -244,7 +249,7 @@ def _bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, 
             dqk_signs: torch.Tensor | None = None, prec: int = 0,
             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     B, H, T, D = q.shape
-    do = _kernel_ready(do)
+    q, k, v, o, do = (_kernel_ready(x) for x in (q, k, v, o, do))
     dq = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
     dk = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
     dv = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
@@ -424,7 +429,6 @@ def flash_attention(
         # per-(b, h) absmax that scales the e4m3 copies), and its backward
         # kernels return dQ' R^T, dK' R^T directly.
         fused_signs = generate_hadamard_signs(D, hadamard_seed, device=device)
-    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     fp8 = ()
     if qk_dtype == "fp8_e4m3" and not hadamard:  # with Hadamard the op quantises Q R, K R itself
         (q8, q_scale), (k8, k_scale) = quantize_fp8(q), quantize_fp8(k)

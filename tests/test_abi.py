@@ -129,3 +129,11 @@ def test_python_boundary_validation():
     with pytest.raises(ValueError, match="qk_dtype"):
         flash_attention(q, q, q, qk_dtype="int8")
     assert 32 in REFERENCE_HEAD_DIMS and 256 in REFERENCE_HEAD_DIMS
+
+
+def test_python_plan_size_matches_the_library():
+    """plan_nbytes (the fake kernels' SymInt-friendly plan size) == kd_plan_bytes."""
+    for B in (1, 2, 3, 8):
+        for T in (1, 17, 63, 64, 65, 127, 128, 129, 300, 1024, 8192, 8193):
+            for D in (64, 128):
+                assert _lib.plan_nbytes(B, T, D) == _lib.plan_bytes(B, T, D), (B, T, D)

@@ -236,6 +236,54 @@ def test_config4_cocktail_hadamard_fp8(dev):
     _case(inp, dev, heads=[(0, 5), (1, 30)], hadamard=True, hadamard_seed=0, qk_dtype="fp8_e4m3")
 
 
+def _rel_rms(x, ref):
+    x, ref = x.detach().double().cpu(), ref.detach().double().cpu()
+    return ((x - ref).pow(2).mean().sqrt() / ref.pow(2).mean().sqrt()).item()
+
+
+def test_fp8_error_against_unquantised_oracle(dev):
+    """What e4m3 scores cost on config 4 (20-sigma outlier channels), with and
+    without the Hadamard rotation, against the UNQUANTISED fp64 oracle.
+
+    Bar (fixed before measuring): the kernel adds nothing beyond the
+    quantisation -- per tensor, the GPU fp8 run's rel-RMS is at most that of
+    the oracle fed the same e4m3 operands (the method's own error) + 1e-2.
+    """
+    inp = config_inputs(4, seed=0)
+    heads = [(1, 17)]
+    T, D = inp["q"].shape[2], inp["q"].shape[3]
+    sc = D ** -0.5
+    q, k, v, do = (select_heads(inp[x], heads) for x in ("q", "k", "v", "do"))
+    mask = np.stack([oracle_mask(inp, T)[b] for b, _ in heads])
+    print("fp8 vs unquantised: exact oracle", flush=True)
+    exact = oracle_fwd_bwd(q, k, v, do, mask, sc)
+    table, failures = [], []
+    for hadamard in (False, True):
+        print(f"fp8 vs unquantised: hadamard={hadamard}", flush=True)
+        got = run_gpu(inp, dev, qk_dtype="fp8_e4m3", hadamard=hadamard, hadamard_seed=0)
+        qs, ks, rot = q, k, None
+        if hadamard:
+            signs = generate_hadamard_signs(D, 0).numpy()
+            rot = torch.from_numpy(ref_h.rotation_matrix(signs))
+            qs = torch.from_numpy(ref_h.rotate_fp32(q.float().numpy(), signs)).to(q.dtype)
+            ks = torch.from_numpy(ref_h.rotate_fp32(k.float().numpy(), signs)).to(k.dtype)
+        meth = oracle_fwd_bwd(qs, ks, v, do, mask, sc, score_q=fp8_scores(qs), score_k=fp8_scores(ks))
+        if rot is not None:
+            meth["dq"] = meth["dq"] @ rot.T
+            meth["dk"] = meth["dk"] @ rot.T
+        for key in ("o", "dq", "dk", "dv"):
+            e_gpu = _rel_rms(select_heads(got[key], heads), exact[key])
+            e_meth = _rel_rms(meth[key], exact[key])
+            table.append((hadamard, key, e_gpu, e_meth))
+            if not e_gpu <= e_meth + 1e-2:
+                failures.append(f"hadamard={hadamard} {key}: gpu {e_gpu:.3e} > e4m3 method {e_meth:.3e} + 1e-2")
+    print("  rel-RMS against the unquantised fp64 oracle, config 4 head (1, 17):")
+    print("  hadamard  tensor  gpu_fp8    oracle_e4m3")
+    for hadamard, key, e_gpu, e_meth in table:
+        print(f"  {str(hadamard):8s}  {key:6s}  {e_gpu:.3e}  {e_meth:.3e}")
+    assert not failures, "; ".join(failures)
+
+
 def test_out_layout_bthd(dev):
     """O written into [B, T, H, d] memory (model.py:95's layout), against the oracle,
     with model-layout strided q/k/v views in (model.py:76-78)."""

@@ -1,0 +1,71 @@
+"""GPU: the kdattn custom ops trace like the reference's (original_kernel.py:2035-2036
+runs its op inside torch.compile(fullgraph=True, dynamic=True), with fake
+implementations at :1781-1803 and :1901-1923).
+
+* torch.library.opcheck on kdattn::fwd, kdattn::bwd, kdattn::rot and kdattn::quant:
+  schema, autograd registration, fake kernels against the real outputs, and
+  AOT dispatch with dynamic shapes.
+* flash_attention under torch.compile(fullgraph=True), static and dynamic
+  shapes, forward and backward: bit for bit the eager result.
+"""
+import pytest
+import torch
+
+from kerneldev_amd import flash_attention, generate_hadamard_signs
+from kerneldev_amd.attention import _bwd_op, _fwd_op, _lib
+from kerneldev_amd.hadamard import _quant_op, _rot_op
+from kerneldev_amd.synth import CONFIG3_LAYOUT, cocktail_batch, qkvdo
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(dev, B=2, H=2, T=320, D=64, seed=90):
+    _, in_span, span_id, is_prefix = cocktail_batch(B, 1024, CONFIG3_LAYOUT, seed=seed)
+    meta = [x[:, :T].contiguous().to(dev) for x in (in_span, span_id, is_prefix)]
+    q, k, v, do = (x.to(dev) for x in qkvdo(B, H, T, D, seed=seed + 1))
+    return q, k, v, do, meta
+
+
+def test_opcheck_forward_and_backward_ops(dev):
+    q, k, v, do, meta = _inputs(dev)
+    sc = q.shape[-1] ** -0.5
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
+    print("opcheck kdattn::fwd", flush=True)
+    torch.library.opcheck(_fwd_op, (qg, kg, vg, None, *meta, sc, _lib.KD_MODE_FORMULA, True))
+    o, lse, plan, o_lo, *_ = _fwd_op(q, k, v, None, *meta, sc, _lib.KD_MODE_FORMULA, True)
+    print("opcheck kdattn::bwd", flush=True)
+    torch.library.opcheck(_bwd_op, (q, k, v, o, lse, do, plan, sc, o_lo))
+
+
+def test_opcheck_rotation_and_quantiser_ops(dev):
+    q, *_ = _inputs(dev, D=128)
+    signs = generate_hadamard_signs(128, 3, device=dev)
+    print("opcheck kdattn::rot", flush=True)
+    torch.library.opcheck(_rot_op, (q.clone().requires_grad_(True), signs, False))
+    amax = q.float().abs().amax(dim=(2, 3)).contiguous()
+    print("opcheck kdattn::quant", flush=True)
+    torch.library.opcheck(_quant_op, (q, amax))
+
+
+def _fwd_bwd(fn, q, k, v, do, meta):
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
+    o, lse = fn(qg, kg, vg, *meta)
+    o.backward(do)
+    torch.cuda.synchronize()
+    return o.detach(), lse.detach(), qg.grad, kg.grad, vg.grad
+
+
+@pytest.mark.parametrize("dynamic", [False, True])
+def test_compiled_flash_attention_matches_eager(dev, dynamic):
+    def attn(q, k, v, in_span, span_id, is_prefix):
+        return flash_attention(q, k, v, in_span=in_span, span_id=span_id, is_prefix=is_prefix, return_lse=True)
+
+    torch._dynamo.reset()
+    compiled = torch.compile(attn, fullgraph=True, dynamic=dynamic)
+    for T in (320, 200):  # a second length re-uses (dynamic) or re-traces (static) the graph
+        q, k, v, do, meta = _inputs(dev, T=T)
+        print(f"torch.compile dynamic={dynamic} T={T}", flush=True)
+        want = _fwd_bwd(attn, q, k, v, do, meta)
+        got = _fwd_bwd(compiled, q, k, v, do, meta)
+        for name, x, y in zip(("o", "lse", "dq", "dk", "dv"), got, want):
+            assert torch.equal(x, y), f"{name} differs between compiled and eager (T={T})"
