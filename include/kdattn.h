@@ -17,7 +17,11 @@
  *   - Tensors [B, H, T, D] are given by a base pointer and element strides for
  *     (b, h, t); the d stride must be 1, base pointers 16-byte aligned, the
  *     (b, h, t) strides multiples of 8 elements, the t stride >= D and
- *     T * t_stride * 2 < 2^31 bytes.
+ *     T * t_stride * element size < 2^31 bytes.
+ *   - Head dims 16, 32, 64, 128, 256 (original_kernel.py:1720).  bf16 / fp16
+ *     at D = 64, 128 run on the MFMA kernels; fp32 inputs (any D) and 16-bit
+ *     inputs at D = 16, 32, 256 run on fp32 vector-ALU kernels (no fp8 scores,
+ *     no dqk_signs there; precision is then always full fp32).
  *   - LSE is stored in log2 units (LSE2 = log2 sum_j exp2(S_ij * sm_scale *
  *     log2 e)), as the reference stores it (original_kernel.py:603-604).
  *     Fully masked rows get O = 0, LSE = -inf and zero gradients.
@@ -40,6 +44,7 @@ extern "C" {
 /* element dtypes */
 #define KD_BF16 0
 #define KD_F16 1
+#define KD_F32 2 /* attention only: computed in fp32 on the vector ALUs */
 /* arithmetic of the softmax weights P and the score gradients dS inside the
  * attention kernels (kd_attn_args.precision) */
 #define KD_PREC_SPLIT 0  /* P and dS enter their products (P V, dV, dQ, dK) as a 16-bit pair
@@ -113,7 +118,7 @@ typedef struct kd_attn_args {
                                    dQ, dK are returned for the unrotated Q, K, i.e. times R^T,
                                    applied in the kernels' epilogues; NULL: dQ, dK as computed */
   int32_t B, H, T, D;
-  int32_t dtype;                /* KD_BF16 / KD_F16 */
+  int32_t dtype;                /* KD_BF16 / KD_F16 / KD_F32 */
   float sm_scale;
   int32_t precision;            /* KD_PREC_SPLIT (0, default) / KD_PREC_SINGLE */
   int32_t pad_;

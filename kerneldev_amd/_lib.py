@@ -17,7 +17,7 @@ LIB_NAME = "libkdattn.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 KD_OK, KD_ERR_INVALID, KD_ERR_UNSUPPORTED, KD_ERR_LAUNCH = 0, -1, -2, -3
-KD_BF16, KD_F16 = 0, 1
+KD_BF16, KD_F16, KD_F32 = 0, 1, 2
 KD_I64, KD_I32 = 0, 1
 KD_MODE_FORMULA, KD_MODE_CAUSAL, KD_MODE_ALL = 0, 1, 2
 KD_PREC_SPLIT, KD_PREC_SINGLE = 0, 1

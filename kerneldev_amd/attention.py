@@ -22,8 +22,12 @@ import torch
 from . import _lib
 from ._lib import AttnArgs, MetaArgs
 
-SUPPORTED_HEAD_DIMS = (64, 128)
 REFERENCE_HEAD_DIMS = (16, 32, 64, 128, 256)  # original_kernel.py:1720
+SUPPORTED_HEAD_DIMS = REFERENCE_HEAD_DIMS
+# bf16 / fp16 at these head dims run on the MFMA kernels (fused Hadamard
+# epilogues, fp8 scores at 128); fp32 inputs and the other head dims run on
+# the fp32 vector-ALU kernels (kd_simt.hip)
+MFMA_HEAD_DIMS = (64, 128)
 
 # precision -> arithmetic of P and dS in the kernels.  The reference rounds P
 # to V's dtype for P V (original_kernel.py:566-571) and keeps P and dS in fp32
@@ -51,7 +55,7 @@ def _kernel_ready(x: torch.Tensor) -> torch.Tensor:
     """Unit d-stride, 16-byte aligned base, 8-element-multiple strides, rows that do not overlap."""
     s = x.stride()
     if (s[3] != 1 or x.data_ptr() % 16 != 0 or any(st % 8 for st in s[:3]) or s[2] < x.shape[3]
-            or x.shape[2] * s[2] * 2 >= 2 ** 31):
+            or x.shape[2] * s[2] * x.element_size() >= 2 ** 31):
         x = x.contiguous()
     return x
 
@@ -61,7 +65,9 @@ def _dtype_code(dt) -> int:
         return _lib.KD_BF16
     if dt == torch.float16:
         return _lib.KD_F16
-    raise ValueError(f"kernel dtype must be bf16 or fp16, got {dt}")
+    if dt == torch.float32:
+        return _lib.KD_F32
+    raise ValueError(f"kernel dtype must be bf16, fp16 or fp32, got {dt}")
 
 
 def _mode(in_span, span_id, is_prefix, has_attention_mask, causal) -> int:
@@ -376,8 +382,6 @@ def flash_attention(
     B, H, T, D = q.shape
     if D not in REFERENCE_HEAD_DIMS:
         raise ValueError(f"head_dim must be one of {REFERENCE_HEAD_DIMS}, got {D}")
-    if D not in SUPPORTED_HEAD_DIMS:
-        raise ValueError(f"head_dim {D} is not built for gfx950 (supported: {SUPPORTED_HEAD_DIMS})")
     if k.shape[-1] != D or v.shape[-1] != D:
         raise ValueError("q, k and v must share head_dim")
     if k.shape != q.shape or v.shape != q.shape:
@@ -414,27 +418,35 @@ def flash_attention(
     mode = _mode(in_span, span_id, is_prefix, attention_mask is not None, causal)
 
     in_dtype = q.dtype
-    if in_dtype == torch.float32:
-        # CDNA4 has no tf32 MFMA: fp32 inputs are computed on bf16 MFMA with
-        # fp32 accumulation and the results cast back to fp32.
-        q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
-    elif in_dtype not in (torch.bfloat16, torch.float16):
+    if in_dtype not in (torch.bfloat16, torch.float16, torch.float32):
         raise ValueError(f"unsupported dtype {in_dtype}")
-    from .hadamard import generate_hadamard_signs, quantize_fp8
+    if qk_dtype == "fp8_e4m3" and in_dtype == torch.float32:
+        # fp8 scores come from bf16 operands: fp32 inputs are rounded to bf16
+        # for this path and O cast back
+        q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+    from .hadamard import _rot_op, generate_hadamard_signs, quantize_fp8
 
     fused_signs = None
     if hadamard:
-        # (Q R)(K R)^T = Q K^T with R = diag(s) H_d / sqrt(d).  The attention
-        # op rotates Q and K itself (fp8: the rotation pass also yields the
-        # per-(b, h) absmax that scales the e4m3 copies), and its backward
-        # kernels return dQ' R^T, dK' R^T directly.
-        fused_signs = generate_hadamard_signs(D, hadamard_seed, device=device)
+        # (Q R)(K R)^T = Q K^T with R = diag(s) H_d / sqrt(d).  On the MFMA
+        # kernels the attention op rotates Q and K itself (fp8: the rotation
+        # pass also yields the per-(b, h) absmax that scales the e4m3 copies),
+        # and its backward kernels return dQ' R^T, dK' R^T directly.  Elsewhere
+        # (fp32, other head dims) Q and K go through the differentiable
+        # rotation op first.
+        signs = generate_hadamard_signs(D, hadamard_seed, device=device)
+        if q.dtype != torch.float32 and D in MFMA_HEAD_DIMS:
+            fused_signs = signs
+        else:
+            q, k = _rot_op(q, signs, False), _rot_op(k, signs, False)
     fp8 = ()
     if qk_dtype == "fp8_e4m3" and not hadamard:  # with Hadamard the op quantises Q R, K R itself
         (q8, q_scale), (k8, k_scale) = quantize_fp8(q), quantize_fp8(k)
         fp8 = (q8, k8, q_scale, k_scale)
 
-    need_lo = torch.is_grad_enabled() and any(x.requires_grad for x in (q, k, v))
+    # O's rounding residual, kept for the backward's Delta (16-bit O only)
+    need_lo = (q.dtype != torch.float32 and torch.is_grad_enabled()
+               and any(x.requires_grad for x in (q, k, v)))
     o, lse, plan_t, *_ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode), need_lo,
                                  *(fp8 or (None, None, None, None)), bthd=out_layout == "bthd",
                                  plan_in=None if plan is None else plan.tensor, signs=fused_signs,

@@ -876,15 +876,21 @@ static void launch_dkdv_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st
   } while (0)
 
 int launch_delta(const AttnArgs& a, hipStream_t st) {
+  if (use_simt(a)) return launch_simt_kernel(1, a, nullptr, st);
   KD_DISPATCH(launch_delta_t, a, st);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 int launch_dq(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_delta) {
+  if (use_simt(a)) {
+    const int r = fuse_delta ? launch_simt_kernel(1, a, plan, st) : KD_OK;
+    return r ? r : launch_simt_kernel(2, a, plan, st);
+  }
   if (a.q8 != nullptr) launch_dq_t<BF16, 128, true>(a, plan, st, fuse_delta);  // fp8 QK^T (checked by the C ABI)
   else KD_DISPATCH(launch_dq_t, a, plan, st, fuse_delta);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 int launch_dkdv(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
+  if (use_simt(a)) return launch_simt_kernel(3, a, plan, st);
   if (a.q8 != nullptr) launch_dkdv_t<BF16, 128, true>(a, plan, st);  // fp8 QK^T (checked by the C ABI)
   else KD_DISPATCH(launch_dkdv_t, a, plan, st);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;

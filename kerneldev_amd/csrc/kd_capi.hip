@@ -27,7 +27,7 @@ bool strides_ok(const int64_t* s) {
 // Largest element offset reachable by a [B, H, T, D] view (for int32 safety
 // of the in-kernel index math the offsets are int64; this only rejects
 // negative / overlapping-by-construction layouts).
-int check_tensor(const void* p, const int64_t* s, const char* name, int T = 1, int D = 0) {
+int check_tensor(const void* p, const int64_t* s, const char* name, int T = 1, int D = 0, int esize = 2) {
   if (p == nullptr) {
     g_err = std::string(name) + " is NULL";
     return KD_ERR_INVALID;
@@ -45,8 +45,8 @@ int check_tensor(const void* p, const int64_t* s, const char* name, int T = 1, i
     return KD_ERR_INVALID;
   }
   // kernels address one (b, h) slice through a buffer resource of 32-bit size
-  if (int64_t(T) * s[2] * 2 >= (int64_t(1) << 31)) {
-    g_err = std::string(name) + ": T * t_stride * 2 bytes must be < 2^31 per (b, h) slice";
+  if (int64_t(T) * s[2] * esize >= (int64_t(1) << 31)) {
+    g_err = std::string(name) + ": T * t_stride * element size must be < 2^31 bytes per (b, h) slice";
     return KD_ERR_UNSUPPORTED;
   }
   return KD_OK;
@@ -63,8 +63,12 @@ int check_common(const kd_attn_args* a) {
   const int64_t nT = (a->T + 63) / 64;
   if (nT * nT * 512 > int64_t(0xFFFFFFFFu))
     return fail(KD_ERR_UNSUPPORTED, "T too large: ceil(T / 64)^2 * 512 bytes of tile masks must fit in 32 bits");
-  if (a->D != 64 && a->D != 128) return fail(KD_ERR_UNSUPPORTED, "head dim must be 64 or 128");
-  if (a->dtype != KD_BF16 && a->dtype != KD_F16) return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16 or fp16");
+  if (a->D != 16 && a->D != 32 && a->D != 64 && a->D != 128 && a->D != 256)
+    return fail(KD_ERR_UNSUPPORTED, "head dim must be 16, 32, 64, 128 or 256");
+  if (a->dtype != KD_BF16 && a->dtype != KD_F16 && a->dtype != KD_F32)
+    return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16, fp16 or fp32");
+  if (kd::use_simt(*a) && a->dqk_signs != nullptr)
+    return fail(KD_ERR_UNSUPPORTED, "dqk_signs is built for bf16 / fp16 at head dim 64 or 128");
   if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale))
     return fail(KD_ERR_INVALID, "sm_scale must be finite and > 0");
   if (a->precision != KD_PREC_SPLIT && a->precision != KD_PREC_SINGLE)
@@ -73,6 +77,8 @@ int check_common(const kd_attn_args* a) {
 }
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+int esz(const kd_attn_args* a) { return a->dtype == KD_F32 ? 4 : 2; }
 
 int check_span(const kd_span_args* a) {
   if (a == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
@@ -167,12 +173,16 @@ int kd_quant_fp8(const kd_quant_args* a, void* stream) {
 int kd_hadamard(const kd_rot_args* a, void* stream) {
   if (a == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
   if (a->B < 1 || a->H < 1 || a->T < 1) return fail(KD_ERR_INVALID, "B, H and T must be >= 1");
-  if (a->D != 64 && a->D != 128) return fail(KD_ERR_UNSUPPORTED, "head dim must be 64 or 128");
-  if (a->dtype != KD_BF16 && a->dtype != KD_F16) return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16 or fp16");
+  if (a->D != 16 && a->D != 32 && a->D != 64 && a->D != 128 && a->D != 256)
+    return fail(KD_ERR_UNSUPPORTED, "head dim must be 16, 32, 64, 128 or 256");
+  if (a->dtype != KD_BF16 && a->dtype != KD_F16 && a->dtype != KD_F32)
+    return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16, fp16 or fp32");
   if (a->signs == nullptr) return fail(KD_ERR_INVALID, "signs is NULL");
   if (int64_t(a->B) * a->H > 65535) return fail(KD_ERR_UNSUPPORTED, "B * H must be <= 65535");
   int r;
-  if ((r = check_tensor(a->x, a->x_strides, "x", a->T, a->D)) || (r = check_tensor(a->y, a->y_strides, "y", a->T, a->D)))
+  const int es = a->dtype == KD_F32 ? 4 : 2;
+  if ((r = check_tensor(a->x, a->x_strides, "x", a->T, a->D, es)) ||
+      (r = check_tensor(a->y, a->y_strides, "y", a->T, a->D, es)))
     return r;
   if (a->x == a->y) return fail(KD_ERR_INVALID, "x and y must not alias");
   r = kd::launch_hadamard(*a, as_stream(stream));
@@ -227,8 +237,8 @@ int kd_attn_fwd(const kd_attn_args* a, const void* plan, void* stream) {
   if (r) return r;
   if ((r = check_fp8(a))) return r;
   if (plan == nullptr) return fail(KD_ERR_INVALID, "plan is NULL");
-  if ((r = check_tensor(a->q, a->q_strides, "q", a->T, a->D)) || (r = check_tensor(a->k, a->k_strides, "k", a->T, a->D)) ||
-      (r = check_tensor(a->v, a->v_strides, "v", a->T, a->D)) || (r = check_tensor(a->o, a->o_strides, "o", a->T, a->D)))
+  if ((r = check_tensor(a->q, a->q_strides, "q", a->T, a->D, esz(a))) || (r = check_tensor(a->k, a->k_strides, "k", a->T, a->D, esz(a))) ||
+      (r = check_tensor(a->v, a->v_strides, "v", a->T, a->D, esz(a))) || (r = check_tensor(a->o, a->o_strides, "o", a->T, a->D, esz(a))))
     return r;
   if (a->o_lo != nullptr && !aligned16(a->o_lo)) return fail(KD_ERR_INVALID, "o_lo must be 16-byte aligned");
   r = kd::launch_fwd(*a, static_cast<const uint8_t*>(plan), as_stream(stream));
@@ -238,7 +248,7 @@ int kd_attn_fwd(const kd_attn_args* a, const void* plan, void* stream) {
 int kd_attn_bwd_delta(const kd_attn_args* a, void* stream) {
   int r = check_common(a);
   if (r) return r;
-  if ((r = check_tensor(a->o, a->o_strides, "o", a->T, a->D)) || (r = check_tensor(a->dout, a->do_strides, "dout", a->T, a->D)))
+  if ((r = check_tensor(a->o, a->o_strides, "o", a->T, a->D, esz(a))) || (r = check_tensor(a->dout, a->do_strides, "dout", a->T, a->D, esz(a))))
     return r;
   if (a->delta == nullptr || a->lse == nullptr) return fail(KD_ERR_INVALID, "delta and lse are required");
   if (a->o_lo != nullptr && !aligned16(a->o_lo)) return fail(KD_ERR_INVALID, "o_lo must be 16-byte aligned");
@@ -252,8 +262,8 @@ static int check_bwd(const kd_attn_args* a, const void* plan) {
   if ((r = check_fp8(a))) return r;
   if (plan == nullptr) return fail(KD_ERR_INVALID, "plan is NULL");
   if (a->lse == nullptr || a->delta == nullptr) return fail(KD_ERR_INVALID, "lse and delta are required");
-  if ((r = check_tensor(a->q, a->q_strides, "q", a->T, a->D)) || (r = check_tensor(a->k, a->k_strides, "k", a->T, a->D)) ||
-      (r = check_tensor(a->v, a->v_strides, "v", a->T, a->D)) || (r = check_tensor(a->dout, a->do_strides, "dout", a->T, a->D)))
+  if ((r = check_tensor(a->q, a->q_strides, "q", a->T, a->D, esz(a))) || (r = check_tensor(a->k, a->k_strides, "k", a->T, a->D, esz(a))) ||
+      (r = check_tensor(a->v, a->v_strides, "v", a->T, a->D, esz(a))) || (r = check_tensor(a->dout, a->do_strides, "dout", a->T, a->D, esz(a))))
     return r;
   return KD_OK;
 }
@@ -261,7 +271,7 @@ static int check_bwd(const kd_attn_args* a, const void* plan) {
 int kd_attn_bwd_dq(const kd_attn_args* a, const void* plan, void* stream) {
   int r = check_bwd(a, plan);
   if (r) return r;
-  if ((r = check_tensor(a->dq, a->dq_strides, "dq", a->T, a->D))) return r;
+  if ((r = check_tensor(a->dq, a->dq_strides, "dq", a->T, a->D, esz(a)))) return r;
   r = kd::launch_dq(*a, static_cast<const uint8_t*>(plan), as_stream(stream), false);
   return r ? fail(r, "kernel launch failed (dq)") : KD_OK;
 }
@@ -269,7 +279,7 @@ int kd_attn_bwd_dq(const kd_attn_args* a, const void* plan, void* stream) {
 int kd_attn_bwd_dkdv(const kd_attn_args* a, const void* plan, void* stream) {
   int r = check_bwd(a, plan);
   if (r) return r;
-  if ((r = check_tensor(a->dk, a->dk_strides, "dk", a->T, a->D)) || (r = check_tensor(a->dv, a->dv_strides, "dv", a->T, a->D))) return r;
+  if ((r = check_tensor(a->dk, a->dk_strides, "dk", a->T, a->D, esz(a))) || (r = check_tensor(a->dv, a->dv_strides, "dv", a->T, a->D, esz(a)))) return r;
   r = kd::launch_dkdv(*a, static_cast<const uint8_t*>(plan), as_stream(stream));
   return r ? fail(r, "kernel launch failed (dkdv)") : KD_OK;
 }
@@ -277,7 +287,7 @@ int kd_attn_bwd_dkdv(const kd_attn_args* a, const void* plan, void* stream) {
 int kd_attn_bwd_dq_delta(const kd_attn_args* a, const void* plan, void* stream) {
   int r = check_bwd(a, plan);
   if (r) return r;
-  if ((r = check_tensor(a->o, a->o_strides, "o", a->T, a->D)) || (r = check_tensor(a->dq, a->dq_strides, "dq", a->T, a->D)))
+  if ((r = check_tensor(a->o, a->o_strides, "o", a->T, a->D, esz(a))) || (r = check_tensor(a->dq, a->dq_strides, "dq", a->T, a->D, esz(a))))
     return r;
   if (a->o_lo != nullptr && !aligned16(a->o_lo)) return fail(KD_ERR_INVALID, "o_lo must be 16-byte aligned");
   r = kd::launch_dq(*a, static_cast<const uint8_t*>(plan), as_stream(stream), true);

@@ -50,6 +50,7 @@ KD_DEV float mask_bit(float s, uint32_t w, int pos) {
 // Element types -----------------------------------------------------------
 struct BF16 {};
 struct F16 {};
+struct F32 {};  // fp32 operands (the vector-ALU kernels of kd_simt.hip)
 
 template <class E> KD_DEV f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c);
 template <> KD_DEV f32x16 mfma32x32x16<BF16>(u32x4 a, u32x4 b, f32x16 c) {

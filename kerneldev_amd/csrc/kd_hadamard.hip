@@ -9,9 +9,9 @@
 // Evaluation order is fixed so the result is bit-identical to the CPU
 // restatement: signs (exact), butterflies h = 1, 2, ..., d/2 each rounded to
 // fp32 ((a, b) -> (a + b, a - b)), one multiply by fp32(1/sqrt(d)), one
-// rounding to the output dtype.  D/8 lanes hold one row, 8 elements each:
-// strides 1, 2, 4 stay inside a lane, strides 8 .. d/2 pair lane t with
-// lane t ^ (h / 8).  Optionally the kernel also records max |y| per (b, h)
+// rounding to the output dtype (none for fp32).  D/8 lanes hold one row
+// (D = 16 .. 256), 8 elements each: strides 1, 2, 4 stay inside a lane,
+// strides 8 .. d/2 pair lane t with lane t ^ (h / 8).  Optionally the kernel also records max |y| per (b, h)
 // (the absmax the fp8 path scales by).
 #include <type_traits>
 
@@ -22,7 +22,8 @@ namespace kd {
 
 // Lane exchanges inside a row's D/8 lanes through DPP (no LDS traffic):
 // partner lane l ^ m for m = 1, 2 (quad_perm), 4 (half-row mirror, then
-// quad reverse) and 8 (row mirror, then half-row mirror).
+// quad reverse) and 8 (row mirror, then half-row mirror); 16 (D = 256, rows
+// of 32 lanes) crosses DPP rows and goes through ds_bpermute.
 template <int M>
 KD_DEV float xor_lane(float v) {
   const int x = __float_as_int(v);
@@ -32,8 +33,56 @@ KD_DEV float xor_lane(float v) {
     const int t = __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false);  // row_half_mirror
     return __int_as_float(__builtin_amdgcn_mov_dpp(t, 0x1B, 0xF, 0xF, false));  // quad_perm [3,2,1,0]
   }
-  const int t = __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false);  // row_mirror
-  return __int_as_float(__builtin_amdgcn_mov_dpp(t, 0x141, 0xF, 0xF, false));
+  if constexpr (M == 8) {
+    const int t = __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false);  // row_mirror
+    return __int_as_float(__builtin_amdgcn_mov_dpp(t, 0x141, 0xF, 0xF, false));
+  }
+  return __shfl_xor(v, M, 64);
+}
+
+// Eight consecutive elements of a row: one 16-byte word for 16-bit types, two for fp32.
+template <class E> struct Row8 { u32x4 w[1]; };
+template <> struct Row8<F32> { u32x4 w[2]; };
+template <class E> KD_DEV Row8<E> load_row8(const void* base, int64_t off) {  // off in elements
+  Row8<E> r;
+  constexpr int NW = sizeof(Row8<E>) / 16;
+  const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const char*>(base) + off * (NW == 1 ? 2 : 4));
+#pragma unroll
+  for (int k = 0; k < NW; ++k) r.w[k] = p[k];
+  return r;
+}
+template <class E> KD_DEV void unpack_row8(const Row8<E>& r, float (&y)[8]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    y[2 * w] = to_f32<E>(uint16_t(r.w[0][w] & 0xFFFFu));
+    y[2 * w + 1] = to_f32<E>(uint16_t(r.w[0][w] >> 16));
+  }
+}
+template <> KD_DEV void unpack_row8<F32>(const Row8<F32>& r, float (&y)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = __uint_as_float(r.w[j >> 2][j & 3]);
+}
+// round y to E, store it, and max |stored value| into m
+template <class E> KD_DEV void store_row8(void* base, int64_t off, const float (&y)[8], float& m) {
+  u32x4 out;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) out[w] = pack2<E>(y[2 * w], y[2 * w + 1]);
+  *reinterpret_cast<u32x4*>(static_cast<char*>(base) + off * 2) = out;
+#pragma unroll
+  for (int w = 0; w < 4; ++w)
+    m = fmaxf(m, fmaxf(fabsf(to_f32<E>(uint16_t(out[w] & 0xFFFFu))), fabsf(to_f32<E>(uint16_t(out[w] >> 16)))));
+}
+template <> KD_DEV void store_row8<F32>(void* base, int64_t off, const float (&y)[8], float& m) {
+  u32x4* p = reinterpret_cast<u32x4*>(static_cast<char*>(base) + off * 4);
+  p[0] = u32x4{__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]), __float_as_uint(y[3])};
+  p[1] = u32x4{__float_as_uint(y[4]), __float_as_uint(y[5]), __float_as_uint(y[6]), __float_as_uint(y[7])};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(y[j]));
+}
+
+// fp32(1 / sqrt(D)), correctly rounded
+template <int D> constexpr float inv_sqrt_d() {
+  return D == 16 ? 0x1p-2f : D == 32 ? 0x1.6a09e6p-3f : D == 64 ? 0x1p-3f : D == 128 ? 0x1.6a09e6p-4f : 0x1p-4f;
 }
 
 // One block = ITERS x RPB consecutive rows of one (b, h) (grid: row chunks x
@@ -47,30 +96,26 @@ __global__ __launch_bounds__(256) void k_hadamard(kd_rot_args a) {
   constexpr int RPB = 256 / TPR;     // rows per step
   const int tid = threadIdx.x, seg = tid % TPR;
   const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-  const uint16_t* xb = static_cast<const uint16_t*>(a.x) + b * a.x_strides[0] + h * a.x_strides[1] + seg * 8;
-  uint16_t* yb = static_cast<uint16_t*>(a.y) + b * a.y_strides[0] + h * a.y_strides[1] + seg * 8;
+  const int64_t xb = b * a.x_strides[0] + h * a.x_strides[1] + seg * 8;  // element offsets
+  const int64_t yb = b * a.y_strides[0] + h * a.y_strides[1] + seg * 8;
   float sg[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) sg[j] = a.signs[seg * 8 + j];
   float m = 0.f;  // max |y| of the rounded outputs of this lane's rows
   const int t0 = blockIdx.x * (ITERS * RPB) + tid / TPR;
-  u32x4 xv = *reinterpret_cast<const u32x4*>(xb + int64_t(t0 < a.T ? t0 : a.T - 1) * a.x_strides[2]);
+  Row8<E> xv = load_row8<E>(a.x, xb + int64_t(t0 < a.T ? t0 : a.T - 1) * a.x_strides[2]);
 #pragma unroll 1
   for (int it = 0; it < ITERS; ++it) {
     const int t = t0 + it * RPB;
     if (t - tid / TPR >= a.T) break;  // block-uniform: the chunk ran past the end
     const bool valid = t < a.T;       // idle lanes still join the exchanges
-    u32x4 nxt = xv;
+    Row8<E> nxt = xv;
     if (it + 1 < ITERS) {
       const int tn = t + RPB;
-      nxt = *reinterpret_cast<const u32x4*>(xb + int64_t(tn < a.T ? tn : a.T - 1) * a.x_strides[2]);
+      nxt = load_row8<E>(a.x, xb + int64_t(tn < a.T ? tn : a.T - 1) * a.x_strides[2]);
     }
     float y[8];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      y[2 * w] = to_f32<E>(uint16_t(xv[w] & 0xFFFFu));
-      y[2 * w + 1] = to_f32<E>(uint16_t(xv[w] >> 16));
-    }
+    unpack_row8<E>(xv, y);
     if (!INV) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) y[j] *= sg[j];
@@ -94,30 +139,22 @@ __global__ __launch_bounds__(256) void k_hadamard(kd_rot_args a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) y[j] = __builtin_fmaf(y[j], sgn, xor_lane<M>(y[j]));
     };
-    cross(std::integral_constant<int, 1>{});
-    cross(std::integral_constant<int, 2>{});
-    cross(std::integral_constant<int, 4>{});
-    if constexpr (TPR == 16) cross(std::integral_constant<int, 8>{});
-    // fp32(1 / sqrt(D)), correctly rounded
-    constexpr float scale = D == 64 ? 0x1p-3f : 0x1.6a09e6p-4f;
+    if constexpr (TPR > 1) cross(std::integral_constant<int, 1>{});
+    if constexpr (TPR > 2) cross(std::integral_constant<int, 2>{});
+    if constexpr (TPR > 4) cross(std::integral_constant<int, 4>{});
+    if constexpr (TPR > 8) cross(std::integral_constant<int, 8>{});
+    if constexpr (TPR > 16) cross(std::integral_constant<int, 16>{});
+    constexpr float scale = inv_sqrt_d<D>();
 #pragma unroll
     for (int j = 0; j < 8; ++j) y[j] *= scale;
     if (INV) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) y[j] *= sg[j];
     }
-    u32x4 out;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) out[w] = pack2<E>(y[2 * w], y[2 * w + 1]);
     if (valid) {
-      *reinterpret_cast<u32x4*>(yb + int64_t(t) * a.y_strides[2]) = out;
-      if (a.amax != nullptr) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          m = fmaxf(m, fabsf(to_f32<E>(uint16_t(out[w] & 0xFFFFu))));
-          m = fmaxf(m, fabsf(to_f32<E>(uint16_t(out[w] >> 16))));
-        }
-      }
+      float mm = 0.f;
+      store_row8<E>(a.y, yb + int64_t(t) * a.y_strides[2], y, mm);
+      if (a.amax != nullptr) m = fmaxf(m, mm);
     }
     xv = nxt;
   }
@@ -204,16 +241,27 @@ static void launch_rot_t(const kd_rot_args& a, hipStream_t st) {
   }
 }
 
-int launch_hadamard(const kd_rot_args& a, hipStream_t st) {
-#define KD_ROT(E_, D_)                                          \
-  if (a.inverse) launch_rot_t<E_, D_, true>(a, st);             \
-  else launch_rot_t<E_, D_, false>(a, st);
-  if (a.dtype == KD_BF16) {
-    if (a.D == 64) { KD_ROT(BF16, 64) } else { KD_ROT(BF16, 128) }
-  } else {
-    if (a.D == 64) { KD_ROT(F16, 64) } else { KD_ROT(F16, 128) }
+template <class E, bool INV>
+static void launch_rot_d(const kd_rot_args& a, hipStream_t st) {
+  switch (a.D) {
+    case 16: launch_rot_t<E, 16, INV>(a, st); break;
+    case 32: launch_rot_t<E, 32, INV>(a, st); break;
+    case 64: launch_rot_t<E, 64, INV>(a, st); break;
+    case 128: launch_rot_t<E, 128, INV>(a, st); break;
+    default: launch_rot_t<E, 256, INV>(a, st); break;
   }
-#undef KD_ROT
+}
+
+template <class E>
+static void launch_rot_e(const kd_rot_args& a, hipStream_t st) {
+  if (a.inverse) launch_rot_d<E, true>(a, st);
+  else launch_rot_d<E, false>(a, st);
+}
+
+int launch_hadamard(const kd_rot_args& a, hipStream_t st) {
+  if (a.dtype == KD_BF16) launch_rot_e<BF16>(a, st);
+  else if (a.dtype == KD_F16) launch_rot_e<F16>(a, st);
+  else launch_rot_e<F32>(a, st);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 

@@ -48,6 +48,10 @@ int launch_hadamard(const kd_rot_args& a, hipStream_t st);
 int launch_quant(const kd_quant_args& a, hipStream_t st);
 int launch_span(const kd_span_args& a, hipStream_t st);
 int launch_span_bwd(const kd_span_args& a, hipStream_t st);
+// fp32 vector-ALU attention (kd_simt.hip) for fp32 inputs and head dims the
+// MFMA kernels are not built for; which: 0 forward, 1 Delta, 2 dQ, 3 dK/dV
+bool use_simt(const AttnArgs& a);
+int launch_simt_kernel(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st);
 // Device address of the no-allocation workspace on the current device
 // (kd_noalloc.hip); KD_OK, or a status with *err set.
 int noalloc_workspace(float** out, const char** err);

@@ -132,10 +132,10 @@ def _quant_fake(x, amax):
 def _check(x: torch.Tensor, signs: torch.Tensor):
     if x.dim() != 4:
         raise ValueError("x must be [batch, heads, time, head_dim]")
-    if x.shape[-1] not in (64, 128):
-        raise ValueError(f"head_dim must be 64 or 128 for the gfx950 transform, got {x.shape[-1]}")
-    if x.dtype not in (torch.bfloat16, torch.float16):
-        raise ValueError(f"x must be bf16 or fp16, got {x.dtype}")
+    if x.shape[-1] not in (16, 32, 64, 128, 256):
+        raise ValueError(f"head_dim must be 16, 32, 64, 128 or 256 for the gfx950 transform, got {x.shape[-1]}")
+    if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError(f"x must be bf16, fp16 or fp32, got {x.dtype}")
     if not x.is_cuda:
         raise ValueError("hadamard_transform runs on the GPU only (no CPU fallback)")
     if signs.shape != (x.shape[-1],) or signs.dtype != torch.float32 or signs.device != x.device:

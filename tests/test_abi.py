@@ -60,6 +60,12 @@ def test_bad_arguments_return_status_without_gpu():
     a = _lib.AttnArgs()
     a.B, a.H, a.T, a.D, a.dtype, a.sm_scale = 1, 1, 16, 96, _lib.KD_BF16, 0.1
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_UNSUPPORTED
+    a.D, a.dtype = 64, 5
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_UNSUPPORTED
+    a.D, a.dtype, a.dqk_signs = 256, _lib.KD_BF16, 64  # the fused un-rotation is built for D 64 / 128
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_UNSUPPORTED
+    assert "dqk_signs" in lib.kd_last_error_string().decode()
+    a.dqk_signs = None
     a.D = 64
     a.sm_scale = float("nan")
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_INVALID
@@ -80,8 +86,12 @@ def test_bad_arguments_return_status_without_gpu():
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_INVALID  # no scales
     assert "scale" in lib.kd_last_error_string().decode()
     r = _lib.RotArgs()
-    r.B, r.H, r.T, r.D, r.dtype = 1, 1, 4, 32, _lib.KD_BF16
-    assert lib.kd_hadamard(ctypes.byref(r), null) == _lib.KD_ERR_UNSUPPORTED
+    r.B, r.H, r.T, r.D, r.dtype = 1, 1, 4, 48, _lib.KD_BF16
+    assert lib.kd_hadamard(ctypes.byref(r), null) == _lib.KD_ERR_UNSUPPORTED  # not a power of two
+    r.D, r.dtype = 32, 3
+    assert lib.kd_hadamard(ctypes.byref(r), null) == _lib.KD_ERR_UNSUPPORTED  # unknown dtype
+    r.dtype = _lib.KD_F32
+    assert lib.kd_hadamard(ctypes.byref(r), null) == _lib.KD_ERR_INVALID  # signs missing
     qa = _lib.QuantArgs()
     qa.B, qa.H, qa.T, qa.D, qa.dtype = 1, 1, 4, 128, _lib.KD_BF16
     assert lib.kd_quant_fp8(ctypes.byref(qa), null) == _lib.KD_ERR_INVALID  # amax / scale / y missing
@@ -118,9 +128,6 @@ def test_python_boundary_validation():
         flash_attention(q, q, q)
     with pytest.raises(ValueError, match="head_dim"):
         z = torch.zeros(1, 2, 16, 48)
-        flash_attention(z, z, z)
-    with pytest.raises(ValueError, match="not built"):
-        z = torch.zeros(1, 2, 16, 32)  # allowed by the reference, not built for gfx950
         flash_attention(z, z, z)
     with pytest.raises(ValueError, match="precision"):
         flash_attention(q, q, q, precision="fp16")

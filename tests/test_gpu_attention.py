@@ -112,6 +112,72 @@ def test_cocktail_small(dev, D):
                is_prefix=is_prefix), dev)
 
 
+def _other_dims_case(D, causal_only, seed):
+    if causal_only:
+        q, k, v, do = qkvdo(2, 3, 200, D, seed=seed)
+        return dict(name=f"causal D{D}", q=q, k=k, v=v, do=do, causal=True)
+    tokens, in_span, span_id, is_prefix = cocktail_batch(2, 1024, CONFIG3_LAYOUT, seed=seed)
+    T = 700
+    q, k, v, do = qkvdo(2, 2, T, D, seed=seed + 1)
+    return dict(name=f"cocktail D{D}", q=q, k=k, v=v, do=do, in_span=in_span[:, :T], span_id=span_id[:, :T],
+                is_prefix=is_prefix[:, :T])
+
+
+@pytest.mark.parametrize("D", [16, 32, 256])
+@pytest.mark.parametrize("causal_only", [True, False])
+def test_other_head_dims(dev, D, causal_only):
+    """The head dims original_kernel.py:1720 accepts beyond 64 / 128 (fp32 vector-ALU kernels)."""
+    _case(_other_dims_case(D, causal_only, seed=40 + D), dev)
+
+
+@pytest.mark.parametrize("D", [32, 256])
+def test_other_head_dims_with_hadamard(dev, D):
+    """Hadamard at head dims without the fused epilogues: rotation op, then attention."""
+    _case(_other_dims_case(D, False, seed=41 + D), dev, hadamard=True, hadamard_seed=5)
+
+
+def _rel_rms_fp64(x, ref):
+    x, ref = x.detach().double().cpu(), ref.detach().double().cpu()
+    return ((x - ref).pow(2).mean().sqrt() / ref.pow(2).mean().sqrt()).item()
+
+
+@pytest.mark.parametrize("precision", ["ieee", "tf32"])
+def test_config1_fp32_precision_against_golden_fixture(dev, precision):
+    """fp32 inputs get fp32 arithmetic: rel-RMS <= 1e-5 (ieee) / 1e-3 (tf32's
+    10-bit mantissa) against the committed fp64 golden vectors, and the
+    precision argument is honoured rather than narrowed to bf16."""
+    import os
+
+    fx = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config1_b0h0.npz"))
+    inp = config_inputs(1, seed=0)
+    assert inp["q"].dtype == torch.float32
+    got = run_gpu(inp, dev, precision=precision)
+    bar = 1e-5 if precision == "ieee" else 1e-3
+    for key in ("o", "dq", "dk", "dv", "lse"):
+        assert got[key].dtype == torch.float32
+        rel = _rel_rms_fp64(got[key][0, 0], torch.from_numpy(fx[key]))
+        print(f"  {precision} {key}: rel-RMS {rel:.3e} (bar {bar:g})")
+        assert rel <= bar, f"{key}: {rel:.3e}"
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
+def test_fp32_inputs_every_head_dim(dev, D):
+    """fp32 attention at every head dim against the fp64 oracle at rel-RMS <= 1e-5."""
+    inp = _other_dims_case(D, False, seed=60 + D)
+    inp = {k_: (v_.float() if torch.is_tensor(v_) and v_.is_floating_point() else v_) for k_, v_ in inp.items()}
+    got = run_gpu(inp, dev, precision="ieee")
+    T = inp["q"].shape[2]
+    mask = oracle_mask(inp, T)
+    ref = oracle_fwd_bwd(inp["q"], inp["k"], inp["v"], inp["do"], mask, D ** -0.5)
+    for key in ("o", "dq", "dk", "dv"):
+        rel = _rel_rms_fp64(got[key], ref[key])
+        print(f"  fp32 D={D} {key}: rel-RMS {rel:.3e}")
+        assert rel <= 1e-5, f"{key}: {rel:.3e}"
+    fin = torch.isfinite(ref["lse"])
+    assert torch.equal(torch.isfinite(got["lse"].cpu()), fin)
+    assert _rel_rms_fp64(got["lse"].cpu()[fin], ref["lse"][fin]) <= 1e-5
+
+
 def test_fp16(dev):
     tokens, in_span, span_id, is_prefix = cocktail_batch(2, 512, CONFIG3_LAYOUT, seed=6)
     q, k, v, do = qkvdo(2, 2, 512, 64, seed=7, dtype=torch.float16)

@@ -20,8 +20,8 @@ def _expected(x_cpu, signs, inverse):
     return torch.from_numpy(y).to(x_cpu.dtype)
 
 
-@pytest.mark.parametrize("D", [64, 128])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_rotation_bit_exact(dev, D, dtype, inverse):
     print(f"hadamard D={D} {dtype} inverse={inverse}", flush=True)
@@ -32,7 +32,8 @@ def test_rotation_bit_exact(dev, D, dtype, inverse):
     y = hadamard_transform(x.to(dev), signs.to(dev), inverse=inverse)
     torch.cuda.synchronize()
     want = _expected(x, signs, inverse)
-    assert torch.equal(y.cpu().view(torch.int16), want.view(torch.int16))
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    assert torch.equal(y.cpu().view(bits), want.view(bits))
 
 
 def test_rotation_strided_input_and_absmax(dev):
