@@ -191,16 +191,17 @@ void kd_struct_sizes2(size_t *rot, size_t *quant);
 void kd_struct_sizes3(size_t *tokens);
 
 /* Workspace ("plan") bytes for B sequences of length T at head dim D, and
- * the byte offsets of its sections (codes, class map, per-tile allowed
- * counts, the forward / dQ / dK-dV work lists, and the 64-bit row / column
- * masks of PARTIAL tiles, the work orders).  offsets[] receives 21 int64:
- * codes, rep, cls, nnz, fwd_list, fwd_count, dq_list, dq_count, dkdv_list,
- * dkdv_count, nT, fwd_group, dq_group, dkdv_group, n_fwd_blocks, n_dq_blocks,
- * n_dkdv_blocks, qbits, kbits, fwd_order, dq_order.  A list entry is
- * (tile << 8) | the class of group member r in bits 2r..2r+1.  A work order
- * (u32 [B n]) lists the items b n + block of the forward or dQ list by
- * descending list length (equal lengths in ascending item order); those
- * kernels take each head's blocks in that order.  Replaces the per-tile mask evaluation of
+ * the byte offsets of its sections (token codes, class map, per-tile allowed
+ * counts, the forward / dQ / dK-dV work lists, the work orders).  offsets[]
+ * receives 19 int64: codes, rep, cls, nnz, fwd_list, fwd_count, dq_list,
+ * dq_count, dkdv_list, dkdv_count, nT, fwd_group, dq_group, dkdv_group,
+ * n_fwd_blocks, n_dq_blocks, n_dkdv_blocks, fwd_order, dq_order.  A list
+ * entry is (tile << 8) | the class of group member r in bits 2r..2r+1.  A
+ * work order (u32 [B n]) lists the items b n + block of the forward or dQ
+ * list by descending list length (equal lengths in ascending item order);
+ * those kernels take each head's blocks in that order.  The plan holds no
+ * per-element masks (the kernels build PARTIAL tiles' masks from the codes),
+ * so it takes O(B T + B nT^2) bytes.  Replaces the per-tile mask evaluation of
  * original_kernel.py:457-517 (the reference has no tile map). */
 int64_t kd_plan_bytes(int32_t B, int32_t T, int32_t D);
 int kd_plan_layout(int32_t B, int32_t T, int32_t D, int64_t *offsets);
@@ -258,6 +259,14 @@ int kd_attn_bwd(const kd_attn_args *a, const void *plan, void *stream);
  * streams or threads) race and must be ordered by the caller. */
 #define KD_NOALLOC_WORKSPACE_FLOATS (1 << 22)
 int kd_attn_bwd_noalloc(const kd_attn_args *a, const void *plan, void *stream);
+
+/* The 64-bit masks of every 64x64 tile of a built plan, from the same
+ * functions the attention kernels apply to PARTIAL tiles: rows [B, nT, nT, 64]
+ * (bit j of entry r: query 64 qt + r may see key 64 kt + j) and cols
+ * [B, nT, nT, 64] (bit r of entry j: query 64 qt + r may see key 64 kt + j).
+ * An inspection aid (the kernels never store them); no reference counterpart,
+ * the reference evaluates original_kernel.py:478-517 per element. */
+int kd_tile_masks(const void *plan, int32_t B, int32_t T, int32_t D, uint64_t *rows, uint64_t *cols, void *stream);
 
 /* Dense bool mask [B, H, T, T] (element strides b, h, q, k) from the plan's
  * codes.  Replaces the RETURN_ATTENTION_MASK store of _flash_attn_fwd

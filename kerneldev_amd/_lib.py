@@ -132,6 +132,7 @@ SIGNATURES = {
     "kd_attn_bwd_noalloc": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
     "kd_mask_dense": (c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p,
                               POINTER(c_int64), c_void_p]),
+    "kd_tile_masks": (c_int, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
 }
 
 _lib = None
@@ -203,13 +204,12 @@ def plan_nbytes(B, T, D):
     return (r(BT * 4) + r(BT * 4) + r(BT * 4) + r(BT * 8) + r(B * 4) + r(BT) + r(BT * 8) + r(BT)
             + r(BTT) + r(BTT * 4)
             + 3 * (r(B * nb * nT * 4) + r(B * nb * 4))
-            + r(BTT * 512) + r(BTT * 512)
             + 2 * r(B * nb * 4))
 
 
 PLAN_FIELDS = ("codes", "rep", "cls", "nnz", "fwd_list", "fwd_count", "dq_list", "dq_count",
                "dkdv_list", "dkdv_count", "nT", "fwd_group", "dq_group", "dkdv_group",
-               "n_fwd_blocks", "n_dq_blocks", "n_dkdv_blocks", "qbits", "kbits", "fwd_order", "dq_order")
+               "n_fwd_blocks", "n_dq_blocks", "n_dkdv_blocks", "fwd_order", "dq_order")
 
 
 def plan_layout(B: int, T: int, D: int) -> dict:

@@ -472,7 +472,7 @@ def flash_attention(
 
 
 def plan_views(plan: torch.Tensor, B: int, T: int, D: int) -> dict:
-    """Typed views of a plan tensor's sections (codes, class map, lists, tile bit masks)."""
+    """Typed views of a plan tensor's sections (codes, class map, lists, work orders)."""
     L = _lib.plan_layout(B, T, D)
     nT = L["nT"]
 
@@ -491,14 +491,24 @@ def plan_views(plan: torch.Tensor, B: int, T: int, D: int) -> dict:
         "dq_count": view(L["dq_count"], B * nq, torch.int32).view(B, nq),
         "dkdv_list": view(L["dkdv_list"], B * nk * nT, torch.int32).view(B, nk, nT),
         "dkdv_count": view(L["dkdv_count"], B * nk, torch.int32).view(B, nk),
-        # row / column bit masks, meaningful for PARTIAL tiles only
-        "qbits": view(L["qbits"], B * nT * nT * 64, torch.int64).view(B, nT, nT, 64),
-        "kbits": view(L["kbits"], B * nT * nT * 64, torch.int64).view(B, nT, nT, 64),
         # work orders: items b n + block by descending list length
         "fwd_order": view(L["fwd_order"], B * nf, torch.int32),
         "dq_order": view(L["dq_order"], B * nq, torch.int32),
         "layout": L,
     }
+
+
+def tile_masks(plan: torch.Tensor, B: int, T: int, D: int):
+    """Every 64x64 tile's row and column bit masks ``(rows, cols)``, int64
+    ``[B, nT, nT, 64]`` each, from the functions the kernels apply to PARTIAL
+    tiles (``kd_tile_masks``): bit j of ``rows[b, qt, kt, r]`` = query 64 qt + r
+    may see key 64 kt + j; bit r of ``cols[b, qt, kt, j]`` = the same pair."""
+    nT = (T + 63) // 64
+    rows = torch.empty((B, nT, nT, 64), dtype=torch.int64, device=plan.device)
+    cols = torch.empty_like(rows)
+    _lib.check(_lib.load().kd_tile_masks(_ptr(plan), B, T, D, _ptr(rows), _ptr(cols), _stream(plan.device)),
+               "kd_tile_masks")
+    return rows, cols
 
 
 def mask_mode(in_span=None, span_id=None, is_prefix=None, attention_mask=None, causal=True) -> int:

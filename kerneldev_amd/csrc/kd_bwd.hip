@@ -159,7 +159,7 @@ KD_DEV void tr_addrs(int lane, int (&addr)[D / 32][2]) {
 
 // ------------------------------------------------------------------- dQ ----
 template <class E, int D, bool Q8, bool SP>
-__global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __restrict__ qbits,
+__global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __restrict__ codes,
                                                const uint32_t* __restrict__ list,
                                                const int32_t* __restrict__ count,
                                                const uint32_t* __restrict__ order, int nT, int nQB,
@@ -171,13 +171,13 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
   __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][TL::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][TL::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_k8[Q8 ? 2 : 1][Q8 ? TK8::BYTES : 16];
-  // each wave's row masks of a PARTIAL tile, copied by the wave itself into
-  // one of two slots (masks of tile e+1 copied in step e).  The fp8 variant's
-  // tiles fill the 80 KB that two workgroups a CU allow: it loads the masks
-  // into registers instead (the compiler then waits for the tile copies
-  // issued with them at their first use)
-  constexpr bool LDS_BITS = !Q8;
-  __shared__ __attribute__((aligned(256))) uint64_t s_bits[LDS_BITS ? 2 : 1][LDS_BITS ? 4 : 1][32];
+  // the 64 key codes of each step's tile (lane = key), from which PARTIAL
+  // tiles build their row masks (query_row_mask), copied one step ahead by
+  // wave 0 into one of two slots.  The fp8 variant's tiles fill the 80 KB
+  // that two workgroups a CU allow: it loads the codes into a register one
+  // step ahead instead (settled at the step's start, see settle)
+  constexpr bool LDS_CODES = !Q8;
+  __shared__ __attribute__((aligned(256))) uint32_t s_kc[LDS_CODES ? 2 : 1][64];
 
   // the wave index through readfirstlane: uniform, so the role and slot
   // arithmetic derived from it stays scalar
@@ -250,14 +250,12 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
   f32x16 neg_delta;
 #pragma unroll
   for (int r = 0; r < 16; ++r) neg_delta[r] = -delta;
-  // this wave's rows lie in q-tile 2 qblock + member; its row masks per key tile
+  // this wave's rows lie in q-tile 2 qblock + member (the member's class per key tile)
   const int member = wave >> 1;
-  // qbits of batch row b: [nT q-tiles][nT key tiles][64 rows]; this wave's 32
-  // rows of key tile 0 start at byte bits_off0 (+ 4 lane: the lane's dword)
-  const u32x4 rs_bits = rsrc_words(qbits + int64_t(b) * nT * nT * 64, uint32_t(nT) * uint32_t(nT) * 512u);
-  const uint32_t bits_off0 =
-      (uint32_t(2 * qblock + member) * uint32_t(nT) * 64u + 32u * uint32_t(wave & 1)) * 8u + uint32_t(lane) * 4u;
-  const uint64_t* qbits_row = qbits + (int64_t(b) * nT + 2 * qblock + member) * nT * 64 + 32 * (wave & 1) + c;
+  // token codes of batch row b (reads past T return 0: allow nothing)
+  const u32x4 rs_codes = rsrc_words(codes + int64_t(b) * T, uint32_t(T) * 4u);
+  const uint32_t* codes_b = codes + int64_t(b) * T;
+  uint32_t qcode = qvalid ? codes_b[qrow] : 0u;
 
   const int lbase = item;  // b nQB + qblock
   const int n = count[lbase];
@@ -276,19 +274,16 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
     TL::load_async(rs_v, k0 * vrb, voff, lds_addr(s_v[buf]), wave);
     if constexpr (Q8) TK8::load_async(rs_k8, k0 * uint32_t(D), k8off, lds_addr(s_k8[buf]), wave);
   };
-  // a PARTIAL tile's row masks, copied one step ahead of their use into the
-  // wave's LDS slot (a register load would be waited for by the compiler
-  // together with the tile copies issued after it)
-  uint64_t bits = 0, bits_next = 0;  // the register-mask variant
-  auto load_bits = [&](int e, int slot) {  // slot = e & 1
-    const uint32_t en = ent[e];
-    if (entry_class(en, member) == TILE_PARTIAL) {  // wave-uniform
-      if constexpr (LDS_BITS) {
-        const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_bits[slot][wave][0]))));
-        dma_b32(rs_bits, bits_off0 + entry_tile(en) * 512u, m);
-      } else {
-        (e == 0 ? bits : bits_next) = qbits_row[int64_t(entry_tile(en)) * 64];
-      }
+  // tile e's key codes, copied one step ahead of their use into LDS (a
+  // register load would be waited for by the compiler together with the tile
+  // copies issued after it), or into a register in the fp8 variant
+  uint32_t kc_reg = 0, kc_next = 0;
+  auto load_codes = [&](int e, int slot) {  // slot = e & 1
+    const uint32_t j = entry_tile(ent[e]) * 64u + uint32_t(lane);
+    if constexpr (LDS_CODES) {
+      if (wave == 0) dma_b32(rs_codes, j * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_kc[slot][0])))));
+    } else {
+      (e == 0 ? kc_reg : kc_next) = j < uint32_t(T) ? codes_b[j] : 0u;
     }
   };
 
@@ -308,7 +303,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
 
   if (n > 0) {
     load_tile(int(entry_tile(ent[0])), 0);
-    load_bits(0, 0);
+    load_codes(0, 0);
   }
   // every register load of the prologue is complete here: the compiler's
   // waits for them fall here, none later in the loop (see settle)
@@ -318,6 +313,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
   for (int st = 0; st < DS; ++st) settle(dof[st]);
   settle(lse);
   settle(delta);
+  settle(qcode);
 
   // One step per key tile; unrolled by two so that the buffer of each step is
   // a constant and every LDS address is a fixed register plus an immediate.
@@ -325,20 +321,22 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
     constexpr int buf = decltype(buf_c)::value;  // == e & 1
     const uint32_t cur = ent[e];
     wait_vmem();
-    if constexpr (!LDS_BITS) settle(bits);
-    barrier_raw();  // tile e (and this wave's masks) landed for every wave; every wave is done with tile e-1
+    if constexpr (!LDS_CODES) settle(kc_reg);
+    barrier_raw();  // tile e (and its key codes) landed for every wave; every wave is done with tile e-1
     if (e + 1 < n) {
       load_tile(int(entry_tile(ent[e + 1])), buf ^ 1);
-      load_bits(e + 1, buf ^ 1);
+      load_codes(e + 1, buf ^ 1);
     }
     const uint8_t* kt = s_k[buf];
     const uint8_t* vt = s_v[buf];
 
-    // the row mask is read first: LDS reads cannot cross the products'
+    // the row mask is formed first: LDS reads cannot cross the products'
     // scheduling fences, and the mask must not hold back the softmax below
     const uint32_t mcls = entry_class(cur, member);
     uint64_t rowbits = 0;  // EMPTY: nothing allowed
-    if (mcls == TILE_PARTIAL) rowbits = LDS_BITS ? s_bits[LDS_BITS ? buf : 0][LDS_BITS ? wave : 0][c] : bits;
+    if (mcls == TILE_PARTIAL)  // wave-uniform
+      rowbits = query_row_mask(qcode, qrow, LDS_CODES ? s_kc[LDS_CODES ? buf : 0][lane] : kc_reg,
+                               int(entry_tile(cur)) * 64);
 
     // S^T = K Q^T and dP^T = V dO^T; A operands (K / K8 and V rows) are read
     // DQ_PF steps ahead of their MFMAs, steps i: kb = i & 1, st = i >> 1; the
@@ -429,7 +427,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
       }
       __builtin_amdgcn_sched_barrier(0x406);
     }
-    if constexpr (!LDS_BITS) bits = bits_next;
+    if constexpr (!LDS_CODES) kc_reg = kc_next;
   };
   for (int e = 0; e < n; e += 2) {
     step(e, std::integral_constant<int, 0>{});
@@ -459,7 +457,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint64_t* __res
 // everything (tile e landed, P(e-1) written, P(e-2) and tile e-2 released),
 // at the price of a third Q buffer (dK reads Q of tile e - 1).
 template <class E, int D, bool Q8, bool SP>
-__global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __restrict__ kbits,
+__global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __restrict__ codes,
                                                  const uint32_t* __restrict__ list,
                                                  const int32_t* __restrict__ count, int nT, int nKB) {
   constexpr int NW = 8;
@@ -483,8 +481,9 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   __shared__ __attribute__((aligned(1024))) u32x4 s_p[2][4][SP ? 8 : 4][64];
   __shared__ __attribute__((aligned(256))) float s_lse[NLS][64];
   __shared__ __attribute__((aligned(256))) float s_delta[NDL][64];
-  // each P wave's column masks of a PARTIAL tile, copied with the tile
-  __shared__ __attribute__((aligned(256))) uint64_t s_bits[NLS][4][32];
+  // the 64 query codes of each step's q-tile (lane = query), from which the P
+  // waves build a PARTIAL tile's column masks (key_col_mask); copied with the tile
+  __shared__ __attribute__((aligned(256))) uint32_t s_qc[NLS][64];
 
   // (the wave index stays a vector value here: made uniform, the two roles'
   // registers are allocated apart and the kernel spills)
@@ -532,13 +531,12 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
 #pragma unroll
     for (int st = 0; st < DS; ++st) bf[st] = buf_load16(rs_b, uint32_t(krow) * brb + (16 * st + 8 * hf) * 2);
   }
-  // this pair's keys lie in k-tile 2 kblock + member; the column masks of its
-  // PARTIAL tiles give, per key, the allowed queries of a q-tile
+  // this pair's keys lie in k-tile 2 kblock + member (the member's class per
+  // q-tile); a PARTIAL tile's column masks, per key, come from the codes of
+  // the key and of the q-tile's queries (reads past T return 0: allow nothing)
   const int member = pair >> 1;
-  // kbits of batch row b: [nT q-tiles][nT key tiles][64 keys]; this pair's
-  // 32 keys of q-tile 0 start at byte bits_off0 (+ 4 lane: the lane's dword)
-  const u32x4 rs_bits = rsrc_words(kbits + int64_t(b) * nT * nT * 64, uint32_t(nT) * uint32_t(nT) * 512u);
-  const uint32_t bits_off0 = (uint32_t(2 * kblock + member) * 64u + 32u * uint32_t(pair & 1)) * 8u + uint32_t(lane) * 4u;
+  const u32x4 rs_codes = rsrc_words(codes + int64_t(b) * T, uint32_t(T) * 4u);
+  uint32_t kcode = kvalid ? codes[int64_t(b) * T + krow] : 0u;
 
   const int lbase = b * nKB + kblock;
   const int n = count[lbase];
@@ -562,10 +560,6 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   };
   auto load_tile = [&](int e, const Slots& sl) {
     const uint32_t en = ent[e], qt = entry_tile(en), q0 = qt * 64u;
-    if (role == 0 && entry_class(en, member) == TILE_PARTIAL) {  // wave-uniform
-      const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_bits[sl.ls][pair][0]))));
-      dma_b32(rs_bits, bits_off0 + qt * uint32_t(nT) * 512u, m);
-    }
     if constexpr (!Q8) TL::load_async(rs_q, q0 * qrb, qoff, lds_addr(s_q[sl.q]), wave);
     TL::load_async(rs_do, q0 * dorb, dooff, lds_addr(s_do[sl.d]), wave);
     if constexpr (Q8) TQ8::load_async(rs_q8, q0 * uint32_t(D), q8off, lds_addr(s_q8[Q8 ? sl.d : 0]), wave);
@@ -573,6 +567,8 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
       dma_b32(rs_lse, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_lse[sl.ls][0])))));
     else if (wave == 5)
       dma_b32(rs_dl, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_delta[sl.dl][0])))));
+    else if (wave == 6)
+      dma_b32(rs_codes, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_qc[sl.ls][0])))));
   };
   // fp8: the 16-bit Q tile of tile e (the dK product's operand in step e + 1)
   auto load_q16 = [&](int e, const Slots& sl) {
@@ -581,12 +577,12 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   };
   // Wait until tile e's loads (and older ones) have landed while tile e+1's,
   // issued last, may still be in flight: vector memory loads retire in order.
-  // (A mask copy precedes the tile loads, so it is never among the last.)
+  // Waves 4, 5 and 6 issue one more load per tile (LSE, Delta, query codes).
   // Only used with PD = 2, i.e. neither fp8 nor SP.
   constexpr int NTL = 2 * NL;
   auto wait_tile = [&](bool next_in_flight) {
     if (!next_in_flight) wait_vmem();
-    else if (wave == 4 || wave == 5) wait_vmem_n<NTL + 1>();
+    else if (wave == 4 || wave == 5 || wave == 6) wait_vmem_n<NTL + 1>();
     else wait_vmem_n<NTL>();
   };
 
@@ -671,6 +667,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
   wait_vmem();
 #pragma unroll
   for (int st = 0; st < DS; ++st) settle(bf[st]);
+  settle(kcode);
   for (int e = 1; e < PD && e < n; ++e) load_tile(e, ahead(sl, e));
   // S of tile e (P waves), or dP of tile e carried into step e + 1 (dS
   // waves): one register set for both roles
@@ -724,7 +721,9 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint64_t* __r
         }
         const uint32_t mcls = entry_class(ent[e], member);
         if (mcls != TILE_FULL) {  // wave-uniform
-          const uint64_t colbits = mcls == TILE_PARTIAL ? s_bits[sl.ls][pair][c] : 0u;  // EMPTY: nothing allowed
+          const uint64_t colbits = mcls == TILE_PARTIAL  // EMPTY: nothing allowed
+                                       ? key_col_mask(kcode, krow, s_qc[sl.ls][lane], int(entry_tile(ent[e])) * 64)
+                                       : 0u;
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
             const uint32_t w = uint32_t(colbits >> (32 * qb)) >> (8 * hf);
@@ -838,7 +837,7 @@ template <class E, int D, bool Q8, bool SP>
 static void launch_dq_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_delta) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dq_blocks;
-  hipLaunchKernelGGL((k_dq<E, D, Q8, SP>), dim3(grid), dim3(256), 0, st, a, reinterpret_cast<const uint64_t*>(plan + L.qbits),
+  hipLaunchKernelGGL((k_dq<E, D, Q8, SP>), dim3(grid), dim3(256), 0, st, a, reinterpret_cast<const uint32_t*>(plan + L.codes),
                      reinterpret_cast<const uint32_t*>(plan + L.dq_list),
                      reinterpret_cast<const int32_t*>(plan + L.dq_count),
                      reinterpret_cast<const uint32_t*>(plan + L.dq_order), L.nT, L.n_dq_blocks, fuse_delta);
@@ -853,7 +852,7 @@ static void launch_dkdv_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dkdv_blocks;
   hipLaunchKernelGGL((k_dkdv<E, D, Q8, SP>), dim3(grid), dim3(512), 0, st, a,
-                     reinterpret_cast<const uint64_t*>(plan + L.kbits),
+                     reinterpret_cast<const uint32_t*>(plan + L.codes),
                      reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
                      reinterpret_cast<const int32_t*>(plan + L.dkdv_count), L.nT, L.n_dkdv_blocks);
 }

@@ -197,13 +197,12 @@ int64_t kd_plan_bytes(int32_t B, int32_t T, int32_t D) {
 int kd_plan_layout(int32_t B, int32_t T, int32_t D, int64_t* off) {
   if (off == nullptr || B < 1 || T < 1) return fail(KD_ERR_INVALID, "bad plan_layout arguments");
   const kd::PlanLayout L = kd::plan_layout(B, T, D);
-  const int64_t v[21] = {int64_t(L.codes),     int64_t(L.rep),        int64_t(L.cls),     int64_t(L.nnz),
+  const int64_t v[19] = {int64_t(L.codes),     int64_t(L.rep),        int64_t(L.cls),     int64_t(L.nnz),
                          int64_t(L.fwd_list),  int64_t(L.fwd_count),  int64_t(L.dq_list), int64_t(L.dq_count),
                          int64_t(L.dkdv_list), int64_t(L.dkdv_count), L.nT,               L.fwd_group,
                          L.dq_group,           L.dkdv_group,          L.n_fwd_blocks,     L.n_dq_blocks,
-                         L.n_dkdv_blocks,      int64_t(L.qbits),      int64_t(L.kbits),   int64_t(L.fwd_order),
-                         int64_t(L.dq_order)};
-  for (int i = 0; i < 21; ++i) off[i] = v[i];
+                         L.n_dkdv_blocks,      int64_t(L.fwd_order),  int64_t(L.dq_order)};
+  for (int i = 0; i < 19; ++i) off[i] = v[i];
   return KD_OK;
 }
 
@@ -312,6 +311,14 @@ int kd_attn_bwd_noalloc(const kd_attn_args* a, const void* plan, void* stream) {
   if (r) return fail(r, err);
   w.delta = ws;
   return kd_attn_bwd(&w, plan, stream);
+}
+
+int kd_tile_masks(const void* plan, int32_t B, int32_t T, int32_t D, uint64_t* rows, uint64_t* cols, void* stream) {
+  if (plan == nullptr || rows == nullptr || cols == nullptr) return fail(KD_ERR_INVALID, "NULL argument");
+  if (B < 1 || T < 1) return fail(KD_ERR_INVALID, "B and T must be >= 1");
+  if (T > (1 << 24) - 2) return fail(KD_ERR_UNSUPPORTED, "T must be < 2^24 - 1");
+  const int r = kd::launch_tile_masks(static_cast<const uint8_t*>(plan), B, T, D, rows, cols, as_stream(stream));
+  return r ? fail(r, "kernel launch failed (tile masks)") : KD_OK;
 }
 
 int kd_mask_dense(const void* plan, int32_t B, int32_t H, int32_t T, int32_t D, uint8_t* out,

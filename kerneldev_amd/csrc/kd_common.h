@@ -41,6 +41,64 @@ KD_DEV bool allow(uint32_t qc, uint32_t kc, int i, int j) {
          (((qc >> 8) != 0u) & ((qc >> 8) == (kc >> 8)));
 }
 
+// The 64-bit masks of a PARTIAL tile, built in the kernels from token codes
+// with wave ballots (the rule of allow(), term for term; the plan keeps only
+// codes, classes and lists).  Every lane of the wave must call them
+// (uniform control flow): lane l supplies the code of the other side's token
+// 64 tile + l, 0 past T or seq_len, which allows nothing.
+//
+// query_row_mask: bit j = allow(i, k0 + j) for this lane's query i (code qc)
+// over keys k0 .. k0 + 63, kc = code of key k0 + lane.
+KD_DEV uint64_t query_row_mask(uint32_t qc, int i, uint32_t kc, int k0) {
+  const uint32_t A = (qc >> 4) & 15u;
+  const uint64_t kp = __builtin_amdgcn_ballot_w64((kc & FLAG_P) != 0u);
+  const uint64_t ks = __builtin_amdgcn_ballot_w64((kc & FLAG_S) != 0u);
+  const uint64_t km = __builtin_amdgcn_ballot_w64((kc & FLAG_M) != 0u);
+  const uint64_t kx = __builtin_amdgcn_ballot_w64((kc & FLAG_C) != 0u);
+  uint64_t row = ((A & FLAG_P) ? kp : 0u) | ((A & FLAG_S) ? ks : 0u) | ((A & FLAG_M) ? km : 0u) |
+                 ((A & FLAG_C) ? kx : 0u);
+  if (qc & FLAG_C) {  // C & C & i >= j: keys k0 .. i
+    const int d = i - k0;
+    row |= kx & (d >= 63 ? ~uint64_t(0) : (d < 0 ? uint64_t(0) : (uint64_t(2) << d) - 1u));
+  }
+  // same span: R_i != 0 and R_j == R_i, one ballot per distinct R_j of the tile
+  const uint32_t kr = kc >> 8, qr = qc >> 8;
+  uint64_t todo = __builtin_amdgcn_ballot_w64(kr != 0u);
+  while (todo != 0u) {  // uniform, at most 64 iterations
+    const uint32_t v = uint32_t(__builtin_amdgcn_readlane(int(kr), int(__builtin_ctzll(todo))));
+    const uint64_t same = __builtin_amdgcn_ballot_w64(kr == v);
+    todo &= ~same;
+    if (qr == v) row |= same;
+  }
+  return row;
+}
+
+// key_col_mask: bit r = allow(q0 + r, j) for this lane's key j (code kc) over
+// queries q0 .. q0 + 63, qc = code of query q0 + lane.
+KD_DEV uint64_t key_col_mask(uint32_t kc, int j, uint32_t qc, int q0) {
+  const uint32_t A = (qc >> 4) & 15u;
+  const uint64_t ap = __builtin_amdgcn_ballot_w64((A & FLAG_P) != 0u);
+  const uint64_t as = __builtin_amdgcn_ballot_w64((A & FLAG_S) != 0u);
+  const uint64_t am = __builtin_amdgcn_ballot_w64((A & FLAG_M) != 0u);
+  const uint64_t ac = __builtin_amdgcn_ballot_w64((A & FLAG_C) != 0u);
+  uint64_t col = ((kc & FLAG_P) ? ap : 0u) | ((kc & FLAG_S) ? as : 0u) | ((kc & FLAG_M) ? am : 0u) |
+                 ((kc & FLAG_C) ? ac : 0u);
+  const uint64_t qx = __builtin_amdgcn_ballot_w64((qc & FLAG_C) != 0u);
+  if (kc & FLAG_C) {  // C & C & i >= j: queries j .. q0 + 63
+    const int d = j - q0;
+    col |= qx & (d <= 0 ? ~uint64_t(0) : (d > 63 ? uint64_t(0) : ~((uint64_t(1) << d) - 1u)));
+  }
+  const uint32_t kr = kc >> 8, qr = qc >> 8;
+  uint64_t todo = __builtin_amdgcn_ballot_w64(qr != 0u);
+  while (todo != 0u) {  // uniform, at most 64 iterations
+    const uint32_t v = uint32_t(__builtin_amdgcn_readlane(int(qr), int(__builtin_ctzll(todo))));
+    const uint64_t same = __builtin_amdgcn_ballot_w64(qr == v);
+    todo &= ~same;
+    if (kr == v) col |= same;
+  }
+  return col;
+}
+
 // s if bit `pos` of w is set, else -inf (v_bfe_i32 + v_bfi_b32).
 KD_DEV float mask_bit(float s, uint32_t w, int pos) {
   const uint32_t m = uint32_t(__builtin_amdgcn_sbfe(int(w), pos, 1u));

@@ -31,9 +31,9 @@
 //         would round P in (65519.5, 65536] to +inf, and O to NaN).
 // l and O stay far below the fp32 range over any row length.  Each wave masks by the class of its own 64-row q-tile
 // against the key tile (from the list entry): FULL tiles skip the mask,
-// PARTIAL ones apply the plan's 64-bit row masks (two VALU ops per score,
-// copied one step ahead into the wave's own LDS slot), EMPTY ones mask
-// everything.  O is normalised by the sum of the ROUNDED P that enters P V,
+// PARTIAL ones build 64-bit row masks from the token codes (query_row_mask:
+// a few wave ballots per tile) and apply them (two VALU ops per score),
+// EMPTY ones mask everything.  O is normalised by the sum of the ROUNDED P that enters P V,
 // so it is an exact convex combination of V rows up to the final rounding
 // even when one key dominates the row; LSE uses the same sum.
 #include "kd_tile.h"
@@ -56,7 +56,7 @@ template <> constexpr float rescale_log2<F16>() { return 15.f; }
 #endif
 
 template <class E, int D, bool Q8, int QB, bool SP>
-__global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, const uint64_t* __restrict__ qbits,
+__global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, const uint32_t* __restrict__ codes,
                                                                 const uint32_t* __restrict__ list,
                                                                 const int32_t* __restrict__ count,
                                                                 const uint32_t* __restrict__ order, int nT, int nQB) {
@@ -69,8 +69,8 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
   constexpr int NLK = TK::LOADS_PER_WAVE;
   __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][TK::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][TL::BYTES];
-  // each wave's row masks of a PARTIAL tile (copied by the wave itself)
-  __shared__ __attribute__((aligned(256))) uint64_t s_bits[2][NW][32 * QB];
+  // the token codes of each step's 64 keys (copied one step ahead by wave 0)
+  __shared__ __attribute__((aligned(256))) uint32_t s_kc[2][64];
 
   // the wave index through readfirstlane: uniform, so the role and slot
   // arithmetic derived from it stays scalar
@@ -113,11 +113,12 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
   }
   // this wave's rows lie in q-tile 2 qblock + member of the block (group of 2)
   const int member = (wave * QB) >> 1;
-  // qbits of batch row b: [nT q-tiles][nT key tiles][64 rows]; this wave's
-  // 32 QB rows of key tile 0 start at byte bits_off0 (+ 4 lane: the lane's dword)
-  const u32x4 rs_bits = rsrc_words(qbits + int64_t(b) * nT * nT * 64, uint32_t(nT) * uint32_t(nT) * 512u);
-  const uint32_t bits_off0 = (uint32_t(2 * qblock + member) * uint32_t(nT) * 64u + 32u * uint32_t((wave * QB) & 1)) * 8u +
-                             uint32_t(lane) * 4u;
+  // token codes of batch row b (reads past T return 0: allow nothing); the
+  // row mask of a PARTIAL tile is built from them (query_row_mask)
+  const u32x4 rs_codes = rsrc_words(codes + int64_t(b) * T, uint32_t(T) * 4u);
+  uint32_t qcode[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) qcode[qb] = qvalid[qb] ? codes[int64_t(b) * T + qrow[qb]] : 0u;
 
   const int lbase = item;  // b nQB + qblock
   const int n = count[lbase];
@@ -137,16 +138,13 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
     const uint32_t k0 = entry_tile(ent[e]) * 64u;
     TL::load_async(rs_v, k0 * vrb, voff, lds_addr(s_v[slot]), wave);
   };
-  // the row masks of this wave's rows in a PARTIAL tile, copied to the
-  // wave's own LDS slot one step ahead of their use (a register load would
-  // be waited for by the compiler, together with the tile copies after it)
-  auto load_bits = [&](int e, int slot) {
-    const uint32_t en = ent[e];
-    if (entry_class(en, member) == TILE_PARTIAL) {  // wave-uniform
-      const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_bits[slot][wave][0]))));
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) dma_b32(rs_bits, bits_off0 + entry_tile(en) * 512u + 256u * qb, m + 256u * qb);
-    }
+  // the 64 key codes of tile e, copied to LDS one step ahead of their use
+  // by wave 0 (a register load would be waited for by the compiler, together
+  // with the tile copies after it)
+  auto load_codes = [&](int e, int slot) {
+    if (wave == 0)
+      dma_b32(rs_codes, (entry_tile(ent[e]) * 64u + uint32_t(lane)) * 4u,
+              uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_kc[slot][0])))));
   };
 
   // V^T operand via transposed reads: group g = lane / 16 covers d columns
@@ -202,10 +200,13 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
     load_k(0, 0);
     load_v(0, 0);
     if (n > 1) load_k(1, 1);
-    load_bits(0, 0);
+    load_codes(0, 0);
     wait_vmem();
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) so[qb].settle();  // the compiler's wait for the Q rows falls here
+    for (int qb = 0; qb < QB; ++qb) {
+      so[qb].settle();  // the compiler's wait for the Q rows (and query codes) falls here
+      settle(qcode[qb]);
+    }
     __syncthreads();
     scores(s_k[0], s);
   }
@@ -222,7 +223,7 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
     barrier_raw();  // V(e), K(e+1) and the masks landed; every wave is done with K(e) and V(e-1)
     if (e + 1 < n) {
       load_v(e + 1, buf ^ 1);
-      load_bits(e + 1, buf ^ 1);
+      load_codes(e + 1, buf ^ 1);
     }
     if (e + 2 < n) load_k(e + 2, buf);
 
@@ -231,7 +232,9 @@ __global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, c
       // of the tile: bit 16 (r / 8) + r % 8 of word kb of the row mask shifted by 8 hf
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
-        const uint64_t rowbits = mcls == TILE_PARTIAL ? s_bits[buf][wave][32 * qb + c] : 0u;  // EMPTY: nothing allowed
+        const uint64_t rowbits = mcls == TILE_PARTIAL  // EMPTY: nothing allowed
+                                     ? query_row_mask(qcode[qb], qrow[qb], s_kc[buf][lane], int(entry_tile(cur)) * 64)
+                                     : 0u;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
           const uint32_t w = uint32_t(rowbits >> (32 * kb)) >> (8 * hf);
@@ -370,7 +373,7 @@ static void launch_fwd_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st)
   const int nQB = L.n_fwd_blocks;
   const unsigned grid = unsigned(a.B) * a.H * nQB;
   hipLaunchKernelGGL((k_fwd<E, D, Q8, QB, SP>), dim3(grid), dim3(256 / QB), 0, st, a,
-                     reinterpret_cast<const uint64_t*>(plan + L.qbits),
+                     reinterpret_cast<const uint32_t*>(plan + L.codes),
                      reinterpret_cast<const uint32_t*>(plan + L.fwd_list),
                      reinterpret_cast<const int32_t*>(plan + L.fwd_count),
                      reinterpret_cast<const uint32_t*>(plan + L.fwd_order), L.nT, nQB);

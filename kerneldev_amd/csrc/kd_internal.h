@@ -29,13 +29,14 @@ KD_DEV inline bool entry_full(uint32_t e, int group) {
 
 struct PlanLayout {
   size_t codes, rep, runs, run_sid, run_count, tok_in_span, tok_span_id, tok_prefix, cls, nnz, fwd_list, fwd_count, dq_list, dq_count, dkdv_list, dkdv_count,
-      qbits, kbits, fwd_order, dq_order, total;
+      fwd_order, dq_order, total;
   int nT, fwd_group, dq_group, dkdv_group, n_fwd_blocks, n_dq_blocks, n_dkdv_blocks;
 };
 
 PlanLayout plan_layout(int B, int T, int D);
 int launch_plan(const MetaArgs& m, uint8_t* plan, hipStream_t st);
 int launch_plan_tokens(const kd_token_args& t, uint8_t* plan, hipStream_t st);
+int launch_tile_masks(const uint8_t* plan, int B, int T, int D, uint64_t* rows, uint64_t* cols, hipStream_t st);
 int launch_mask_dense(const uint32_t* codes, int B, int H, int T, uint8_t* out, const int64_t* strides,
                       hipStream_t st);
 int launch_fwd(const AttnArgs& a, const uint8_t* plan, hipStream_t st);

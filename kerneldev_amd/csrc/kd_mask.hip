@@ -9,10 +9,11 @@
 //   nnz     i32 [B, nT, nT]       allowed entries per tile
 //   lists   u32 [B, nRB, nT]      per row block: (tile << 8) | member classes, ascending
 //   counts  i32 [B, nRB]
-//   qbits   u64 [B, nT, nT, 64]   PARTIAL tiles: row r's allowed keys (bit j = key 64 kt + j)
-//   kbits   u64 [B, nT, nT, 64]   PARTIAL tiles: key r's allowed queries (bit i = query 64 qt + i)
-// The bit masks let the attention kernels mask a PARTIAL tile with two VALU
-// ops per score instead of re-evaluating the rule.
+// The plan stores no per-element masks: the attention kernels build a
+// PARTIAL tile's 64-bit row or column masks from the token codes with a few
+// wave ballots (query_row_mask / key_col_mask, kd_common.h) and then mask it
+// with two VALU ops per score, so the plan grows with B T + B nT^2 bytes
+// rather than B nT^2 512.  kd_tile_masks materialises those masks.
 #include "kd_internal.h"
 
 namespace kd {
@@ -194,11 +195,11 @@ __global__ void k_codes(MetaArgs m, const uint32_t* runs, const int64_t* run_sid
 // of keys carrying each flag of A_i; context queries add context keys at
 // j <= i (all of them below the diagonal, none above); and for the same-span
 // term the wave walks the distinct span representatives among the tile's keys
-// (usually one to three), one ballot each.  That is the rule of allow(), term
-// for term.  PARTIAL tiles also store the row masks and, through 64 ballots
-// (column j of the tile = ballot of bit j), the column masks.
+// (usually one to three), one ballot each: query_row_mask, the function the
+// forward and dQ kernels use for PARTIAL tiles.  That is the rule of allow(),
+// term for term.
 __global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, int nT, uint8_t* cls,
-                                                 int32_t* nnz, uint64_t* qbits, uint64_t* kbits) {
+                                                 int32_t* nnz) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int qt = blockIdx.y, b = blockIdx.z;
   const int kt0 = blockIdx.x * 4;
@@ -213,26 +214,7 @@ __global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, i
   const int i = qt * 64 + lane;
   const uint32_t qc = (i < T) ? codes[int64_t(b) * T + i] : 0u;
   const uint32_t kc = s_k[wave * 64 + lane];  // key j = 64 kt + lane (code 0 past T: allows nothing)
-  const uint32_t A = (qc >> 4) & 15u;
-  const uint64_t kp = __builtin_amdgcn_ballot_w64((kc & FLAG_P) != 0u);
-  const uint64_t ks = __builtin_amdgcn_ballot_w64((kc & FLAG_S) != 0u);
-  const uint64_t km = __builtin_amdgcn_ballot_w64((kc & FLAG_M) != 0u);
-  const uint64_t kcx = __builtin_amdgcn_ballot_w64((kc & FLAG_C) != 0u);
-  uint64_t row = ((A & FLAG_P) ? kp : 0u) | ((A & FLAG_S) ? ks : 0u) | ((A & FLAG_M) ? km : 0u) |
-                 ((A & FLAG_C) ? kcx : 0u);
-  if (qc & FLAG_C) {  // C & C & i >= j
-    const uint64_t le = lane == 63 ? ~uint64_t(0) : (uint64_t(2) << lane) - 1u;  // keys j <= i on the diagonal
-    row |= kcx & (kt < qt ? ~uint64_t(0) : (kt == qt ? le : uint64_t(0)));
-  }
-  // same span: R_i != 0 and R_j == R_i, one ballot per distinct R_j of the tile
-  const uint32_t kr = kc >> 8, qr = qc >> 8;
-  uint64_t todo = __builtin_amdgcn_ballot_w64(kr != 0u);
-  while (todo != 0u) {  // uniform
-    const uint32_t v = uint32_t(__builtin_amdgcn_readlane(int(kr), int(__builtin_ctzll(todo))));
-    const uint64_t same = __builtin_amdgcn_ballot_w64(kr == v);
-    todo &= ~same;
-    if (qr == v) row |= same;
-  }
+  const uint64_t row = query_row_mask(qc, i, kc, kt * 64);
   int cnt = __builtin_popcountll(row);
   for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off);
   const int64_t o = (int64_t(b) * nT + qt) * nT + kt;
@@ -241,15 +223,23 @@ __global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, i
     cls[o] = k;
     if (nnz != nullptr) nnz[o] = cnt;
   }
-  if (k == TILE_PARTIAL) {  // wave-uniform
-    qbits[o * 64 + lane] = row;
-    uint64_t col = 0;
-    for (int j = 0; j < 64; ++j) {
-      const uint64_t bj = __builtin_amdgcn_ballot_w64(((row >> j) & 1u) != 0);
-      if (lane == j) col = bj;
-    }
-    kbits[o * 64 + lane] = col;
-  }
+}
+
+// ---- tile masks (inspection) -----------------------------------------------
+// Every tile's 64 row masks and 64 column masks, from the same functions the
+// attention kernels use for PARTIAL tiles.  One wave per tile: lane r is row
+// r for query_row_mask and key r for key_col_mask.
+__global__ __launch_bounds__(256) void k_tile_masks(const uint32_t* codes, int T, int nT, uint64_t* rows,
+                                                    uint64_t* cols) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int qt = blockIdx.y, b = blockIdx.z, kt = blockIdx.x * 4 + wave;
+  if (kt >= nT) return;  // wave-uniform
+  const uint32_t* cb = codes + int64_t(b) * T;
+  const int i = qt * 64 + lane, j = kt * 64 + lane;
+  const uint32_t qc = i < T ? cb[i] : 0u, kc = j < T ? cb[j] : 0u;
+  const int64_t o = ((int64_t(b) * nT + qt) * nT + kt) * 64 + lane;
+  rows[o] = query_row_mask(qc, i, kc, kt * 64);
+  cols[o] = key_col_mask(kc, j, qc, qt * 64);
 }
 
 // ---- per-row-block work lists ------------------------------------------
@@ -376,8 +366,6 @@ PlanLayout plan_layout(int B, int T, int D) {
   L.dq_count = take(size_t(B) * nq * 4);
   L.dkdv_list = take(size_t(B) * nk * nT * 4);
   L.dkdv_count = take(size_t(B) * nk * 4);
-  L.qbits = take(BTT * 64 * 8);
-  L.kbits = take(BTT * 64 * 8);
   L.fwd_order = take(size_t(B) * nf * 4);
   L.dq_order = take(size_t(B) * nq * 4);
   L.total = off;
@@ -399,8 +387,7 @@ int launch_plan(const MetaArgs& m, uint8_t* plan, hipStream_t st) {
     hipLaunchKernelGGL(k_runs, dim3(unsigned(m.B)), dim3(1024), 0, st, m, runs, run_sid, run_count);
   hipLaunchKernelGGL(k_codes, dim3(unsigned((BT + 255) / 256)), dim3(256), 0, st, m, runs, run_sid, run_count, rep,
                      codes);
-  hipLaunchKernelGGL(k_tilemap, dim3((L.nT + 3) / 4, L.nT, m.B), dim3(256), 0, st, codes, m.T, L.nT, cls, nnz,
-                     reinterpret_cast<uint64_t*>(plan + L.qbits), reinterpret_cast<uint64_t*>(plan + L.kbits));
+  hipLaunchKernelGGL(k_tilemap, dim3((L.nT + 3) / 4, L.nT, m.B), dim3(256), 0, st, codes, m.T, L.nT, cls, nnz);
   ListSpecs specs;
   specs.l[0] = {reinterpret_cast<uint32_t*>(plan + L.fwd_list), reinterpret_cast<int32_t*>(plan + L.fwd_count),
                 L.fwd_group, 0, L.n_fwd_blocks};
@@ -445,6 +432,13 @@ int launch_plan_tokens(const kd_token_args& t, uint8_t* plan, hipStream_t st) {
                      reinterpret_cast<int64_t*>(plan + L.tok_span_id), plan + L.tok_prefix);
   if (hipGetLastError() != hipSuccess) return KD_ERR_LAUNCH;
   return launch_plan(m, plan, st);
+}
+
+int launch_tile_masks(const uint8_t* plan, int B, int T, int D, uint64_t* rows, uint64_t* cols, hipStream_t st) {
+  const PlanLayout L = plan_layout(B, T, D);
+  hipLaunchKernelGGL(k_tile_masks, dim3((L.nT + 3) / 4, L.nT, B), dim3(256), 0, st,
+                     reinterpret_cast<const uint32_t*>(plan + L.codes), T, L.nT, rows, cols);
+  return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 
 int launch_mask_dense(const uint32_t* codes, int B, int H, int T, uint8_t* out, const int64_t* s,

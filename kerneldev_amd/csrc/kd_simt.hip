@@ -9,8 +9,8 @@
 //   dQ        P = exp2(S c - LSE), dS = P (dP - Delta), dQ = sm_scale dS K  (:1173-1336)
 //   dK / dV   dV = P^T dO, dK = sm_scale dS^T Q            (:1339-1525)
 // c = sm_scale log2(e) in fp32.  Only non-empty 64 x 64 tiles are visited;
-// PARTIAL tiles take the plan's 64-bit row masks (forward, dQ) or column masks
-// (dK / dV), FULL tiles none.
+// PARTIAL tiles evaluate the mask rule allow() per score from the plan's token
+// codes, FULL tiles skip it.
 //
 // Layout: one workgroup per (64-row tile, b, h).  G = max(1, D / 32) lanes
 // share one row, each owning DL = D / G (16 or 32) consecutive columns in registers;
@@ -74,15 +74,19 @@ KD_DEV void fill_vec(float* s, const float* base, int r0, int T, int tid, int nt
   for (int r = tid; r < Shape<64>::SUB; r += nt) s[r] = r0 + r < T ? base[r0 + r] : dflt;
 }
 
-KD_DEV bool bit(uint64_t w, int j) { return (w >> j) & 1u; }
+// token codes of rows r0 .. r0 + SUB - 1 (0 past T: allow nothing)
+KD_DEV void fill_codes(uint32_t* s, const uint32_t* base, int r0, int T, int tid, int nt) {
+  for (int r = tid; r < Shape<64>::SUB; r += nt) s[r] = r0 + r < T ? base[r0 + r] : 0u;
+}
 
 // ------------------------------------------------------------------ forward
 template <class E, int D>
 __global__ __launch_bounds__(Shape<D>::NT) void k_fwd_simt(AttnArgs a, const uint8_t* __restrict__ cls,
-                                                           const uint64_t* __restrict__ qbits, int nT) {
+                                                           const uint32_t* __restrict__ codes, int nT) {
   using S = Shape<D>;
   constexpr int G = S::G, DL = S::DL, SUB = S::SUB;
   __shared__ float sk[SUB][D], sv[SUB][D];
+  __shared__ uint32_t skc[SUB];
   const int qt = blockIdx.x, b = blockIdx.y, h = blockIdx.z, bh = b * a.H + h;
   const int tid = threadIdx.x, row = tid / G, g = tid % G, i = qt * 64 + row, T = a.T;
   const bool valid = i < T;
@@ -97,15 +101,19 @@ __global__ __launch_bounds__(Shape<D>::NT) void k_fwd_simt(AttnArgs a, const uin
     o[d] = 0.f;
   }
   float m = -__builtin_inff(), l = 0.f;
+  const uint32_t* codes_b = codes + int64_t(b) * T;
+  const uint32_t qc = valid ? codes_b[i] : 0u;
   const int64_t trow = int64_t(b) * nT + qt;
   for (int kt = 0; kt < nT; ++kt) {
     const uint8_t cl = cls[trow * nT + kt];
     if (cl == TILE_EMPTY) continue;  // uniform
-    const uint64_t rb = cl == TILE_FULL ? ~uint64_t(0) : qbits[(trow * nT + kt) * 64 + row];
+    const bool partial = cl == TILE_PARTIAL;
     for (int half = 0; half < 2; ++half) {
+      const int j0 = kt * 64 + half * SUB;
       __syncthreads();
-      fill<E, D>(sk, kb, a.k_strides[2], kt * 64 + half * SUB, T, tid);
-      fill<E, D>(sv, vb, a.v_strides[2], kt * 64 + half * SUB, T, tid);
+      fill<E, D>(sk, kb, a.k_strides[2], j0, T, tid);
+      fill<E, D>(sv, vb, a.v_strides[2], j0, T, tid);
+      fill_codes(skc, codes_b, j0, T, tid, S::NT);
       __syncthreads();
       float s[SUB];  // fully unrolled loops keep s in registers
       float mx = -__builtin_inff();
@@ -115,7 +123,7 @@ __global__ __launch_bounds__(Shape<D>::NT) void k_fwd_simt(AttnArgs a, const uin
 #pragma unroll
         for (int d = 0; d < DL; ++d) acc = __builtin_fmaf(q[d], sk[j][g * DL + d], acc);
         acc = group_sum<G>(acc);
-        s[j] = bit(rb, half * SUB + j) ? acc : -__builtin_inff();
+        s[j] = (!partial || allow(qc, skc[j], i, j0 + j)) ? acc : -__builtin_inff();
         mx = fmaxf(mx, s[j]);
       }
       const float m_new = fmaxf(m, mx);
@@ -169,10 +177,11 @@ __global__ __launch_bounds__(256) void k_delta_simt(AttnArgs a) {
 // ----------------------------------------------------------------------- dQ
 template <class E, int D>
 __global__ __launch_bounds__(Shape<D>::NT) void k_dq_simt(AttnArgs a, const uint8_t* __restrict__ cls,
-                                                          const uint64_t* __restrict__ qbits, int nT) {
+                                                          const uint32_t* __restrict__ codes, int nT) {
   using S = Shape<D>;
   constexpr int G = S::G, DL = S::DL, SUB = S::SUB;
   __shared__ float sk[SUB][D], sv[SUB][D];
+  __shared__ uint32_t skc[SUB];
   const int qt = blockIdx.x, b = blockIdx.y, h = blockIdx.z, bh = b * a.H + h;
   const int tid = threadIdx.x, row = tid / G, g = tid % G, i = qt * 64 + row, T = a.T;
   const bool valid = i < T;
@@ -192,15 +201,19 @@ __global__ __launch_bounds__(Shape<D>::NT) void k_dq_simt(AttnArgs a, const uint
   const float l = valid ? a.lse[int64_t(bh) * T + i] : -__builtin_inff();
   const float lse = l == -__builtin_inff() ? __builtin_inff() : l;  // fully masked rows: P = 0
   const float delta = valid ? -a.delta[int64_t(bh) * T + i] : 0.f;
+  const uint32_t* codes_b = codes + int64_t(b) * T;
+  const uint32_t qc = valid ? codes_b[i] : 0u;
   const int64_t trow = int64_t(b) * nT + qt;
   for (int kt = 0; kt < nT; ++kt) {
     const uint8_t cl = cls[trow * nT + kt];
     if (cl == TILE_EMPTY) continue;
-    const uint64_t rb = cl == TILE_FULL ? ~uint64_t(0) : qbits[(trow * nT + kt) * 64 + row];
+    const bool partial = cl == TILE_PARTIAL;
     for (int half = 0; half < 2; ++half) {
+      const int j0 = kt * 64 + half * SUB;
       __syncthreads();
-      fill<E, D>(sk, kb, a.k_strides[2], kt * 64 + half * SUB, T, tid);
-      fill<E, D>(sv, vb, a.v_strides[2], kt * 64 + half * SUB, T, tid);
+      fill<E, D>(sk, kb, a.k_strides[2], j0, T, tid);
+      fill<E, D>(sv, vb, a.v_strides[2], j0, T, tid);
+      fill_codes(skc, codes_b, j0, T, tid, S::NT);
       __syncthreads();
 #pragma unroll 2
       for (int j = 0; j < SUB; ++j) {
@@ -212,7 +225,7 @@ __global__ __launch_bounds__(Shape<D>::NT) void k_dq_simt(AttnArgs a, const uint
         }
         s = group_sum<G>(s);
         dp = group_sum<G>(dp);
-        const float p = bit(rb, half * SUB + j) ? fast_exp2(s - lse) : 0.f;
+        const float p = (!partial || allow(qc, skc[j], i, j0 + j)) ? fast_exp2(s - lse) : 0.f;
         const float ds = p * (dp - delta);
 #pragma unroll
         for (int d = 0; d < DL; ++d) dq[d] = __builtin_fmaf(ds, sk[j][g * DL + d], dq[d]);
@@ -228,11 +241,12 @@ __global__ __launch_bounds__(Shape<D>::NT) void k_dq_simt(AttnArgs a, const uint
 // -------------------------------------------------------------------- dK/dV
 template <class E, int D>
 __global__ __launch_bounds__(Shape<D>::NT) void k_dkdv_simt(AttnArgs a, const uint8_t* __restrict__ cls,
-                                                            const uint64_t* __restrict__ kbits, int nT) {
+                                                            const uint32_t* __restrict__ codes, int nT) {
   using S = Shape<D>;
   constexpr int G = S::G, DL = S::DL, SUB = S::SUB;
   __shared__ float sq[SUB][D], sdo[SUB][D];
   __shared__ float slse[SUB], sdl[SUB];
+  __shared__ uint32_t sqc[SUB];
   const int kt = blockIdx.x, b = blockIdx.y, h = blockIdx.z, bh = b * a.H + h;
   const int tid = threadIdx.x, row = tid / G, g = tid % G, j = kt * 64 + row, T = a.T;
   const bool valid = j < T;
@@ -251,18 +265,21 @@ __global__ __launch_bounds__(Shape<D>::NT) void k_dkdv_simt(AttnArgs a, const ui
   }
   const float* lse_g = a.lse + int64_t(bh) * T;
   const float* dl_g = a.delta + int64_t(bh) * T;  // -Delta
+  const uint32_t* codes_b = codes + int64_t(b) * T;
+  const uint32_t kc = valid ? codes_b[j] : 0u;
   for (int qt = 0; qt < nT; ++qt) {
     const int64_t trow = int64_t(b) * nT + qt;
     const uint8_t cl = cls[trow * nT + kt];
     if (cl == TILE_EMPTY) continue;
-    // column masks: bit r of kbits[.., kt, key] = query 64 qt + r may see this key
-    const uint64_t cb = cl == TILE_FULL ? ~uint64_t(0) : kbits[(trow * nT + kt) * 64 + row];
+    const bool partial = cl == TILE_PARTIAL;
     for (int half = 0; half < 2; ++half) {
+      const int i0 = qt * 64 + half * SUB;
       __syncthreads();
-      fill<E, D>(sq, qb, a.q_strides[2], qt * 64 + half * SUB, T, tid);
-      fill<E, D>(sdo, dob, a.do_strides[2], qt * 64 + half * SUB, T, tid);
-      fill_vec(slse, lse_g, qt * 64 + half * SUB, T, tid, S::NT, -__builtin_inff());
-      fill_vec(sdl, dl_g, qt * 64 + half * SUB, T, tid, S::NT, 0.f);
+      fill<E, D>(sq, qb, a.q_strides[2], i0, T, tid);
+      fill<E, D>(sdo, dob, a.do_strides[2], i0, T, tid);
+      fill_vec(slse, lse_g, i0, T, tid, S::NT, -__builtin_inff());
+      fill_vec(sdl, dl_g, i0, T, tid, S::NT, 0.f);
+      fill_codes(sqc, codes_b, i0, T, tid, S::NT);
       __syncthreads();
 #pragma unroll 2
       for (int r = 0; r < SUB; ++r) {
@@ -275,7 +292,8 @@ __global__ __launch_bounds__(Shape<D>::NT) void k_dkdv_simt(AttnArgs a, const ui
         s = group_sum<G>(s);
         dp = group_sum<G>(dp);
         const float l = slse[r];
-        const float p = (bit(cb, half * SUB + r) && l != -__builtin_inff()) ? fast_exp2(s - l) : 0.f;
+        const bool ok = !partial || allow(sqc[r], kc, i0 + r, j);
+        const float p = (ok && l != -__builtin_inff()) ? fast_exp2(s - l) : 0.f;
         const float ds = p * (dp + sdl[r]);  // sdl holds -Delta
 #pragma unroll
         for (int d = 0; d < DL; ++d) {
@@ -301,15 +319,14 @@ static void launch_simt(int which, const AttnArgs& a, const uint8_t* plan, hipSt
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const dim3 grid(unsigned(L.nT), unsigned(a.B), unsigned(a.H));
   const uint8_t* cls = plan + L.cls;
-  const uint64_t* qbits = reinterpret_cast<const uint64_t*>(plan + L.qbits);
-  const uint64_t* kbits = reinterpret_cast<const uint64_t*>(plan + L.kbits);
-  if (which == 0) hipLaunchKernelGGL((k_fwd_simt<E, D>), grid, dim3(Shape<D>::NT), 0, st, a, cls, qbits, L.nT);
+  const uint32_t* codes = reinterpret_cast<const uint32_t*>(plan + L.codes);
+  if (which == 0) hipLaunchKernelGGL((k_fwd_simt<E, D>), grid, dim3(Shape<D>::NT), 0, st, a, cls, codes, L.nT);
   if (which == 1) {
     const int64_t rows = int64_t(a.B) * a.H * a.T;
     hipLaunchKernelGGL((k_delta_simt<E, D>), dim3(unsigned((rows + 255) / 256)), dim3(256), 0, st, a);
   }
-  if (which == 2) hipLaunchKernelGGL((k_dq_simt<E, D>), grid, dim3(Shape<D>::NT), 0, st, a, cls, qbits, L.nT);
-  if (which == 3) hipLaunchKernelGGL((k_dkdv_simt<E, D>), grid, dim3(Shape<D>::NT), 0, st, a, cls, kbits, L.nT);
+  if (which == 2) hipLaunchKernelGGL((k_dq_simt<E, D>), grid, dim3(Shape<D>::NT), 0, st, a, cls, codes, L.nT);
+  if (which == 3) hipLaunchKernelGGL((k_dkdv_simt<E, D>), grid, dim3(Shape<D>::NT), 0, st, a, cls, codes, L.nT);
 }
 
 template <class E>

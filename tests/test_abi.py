@@ -47,7 +47,7 @@ def test_plan_sizes_and_layout_offsets():
     offs = [L[k] for k in _lib.PLAN_FIELDS[:10]]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
     assert _lib.plan_bytes(2, 8192, 128) > L["dkdv_count"]
-    tail = [L[k] for k in ("kbits", "fwd_order", "dq_order")]
+    tail = [L[k] for k in ("dkdv_count", "fwd_order", "dq_order")]
     assert tail == sorted(tail) and all(o % 256 == 0 for o in tail)
     assert _lib.plan_bytes(2, 8192, 128) >= L["dq_order"] + 4 * 2 * L["n_dq_blocks"]
 
@@ -136,6 +136,12 @@ def test_python_boundary_validation():
     with pytest.raises(ValueError, match="qk_dtype"):
         flash_attention(q, q, q, qk_dtype="int8")
     assert 32 in REFERENCE_HEAD_DIMS and 256 in REFERENCE_HEAD_DIMS
+
+
+def test_plan_is_linear_in_tiles_not_elements():
+    """No per-element masks: config 4's plan is under 1 MiB, a B=8, L=32768 plan under 64 MiB."""
+    assert _lib.plan_bytes(2, 8192, 128) < 1 << 20
+    assert _lib.plan_bytes(8, 32768, 128) < 64 << 20
 
 
 def test_python_plan_size_matches_the_library():

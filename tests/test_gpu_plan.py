@@ -10,12 +10,21 @@ import pytest
 import torch
 
 from kerneldev_amd import build_plan, build_plan_from_tokens, derive_metadata, flash_attention, plan_views
-from kerneldev_amd.attention import mask_mode
+from kerneldev_amd.attention import mask_mode, tile_masks
 from kerneldev_amd.synth import CONFIG3_LAYOUT, CONFIG4_LAYOUT, cocktail_batch
 from oracle import metadata, tilemap
 from oracle.mask import dense_mask
 
 pytestmark = pytest.mark.gpu
+
+
+def _views(plan, B, T, D):
+    """The plan's sections, plus every tile's row / column masks as the kernels build them."""
+    out = {k: (v.cpu().numpy() if torch.is_tensor(v) else v) for k, v in plan_views(plan, B, T, D).items()}
+    rows, cols = tile_masks(plan, B, T, D)
+    torch.cuda.synchronize()
+    out["qbits"], out["kbits"] = rows.cpu().numpy(), cols.cpu().numpy()
+    return out
 
 
 def _device_plan(dev, B, T, D, in_span=None, span_id=None, is_prefix=None, lens=None, causal=True,
@@ -24,7 +33,7 @@ def _device_plan(dev, B, T, D, in_span=None, span_id=None, is_prefix=None, lens=
     mode = mask_mode(in_span, span_id, is_prefix, True if attention_mask_given else None, causal)
     plan = build_plan(B, T, D, dev, mode, to(in_span), to(span_id), to(is_prefix), to(lens))
     torch.cuda.synchronize()
-    return {k: (v.cpu().numpy() if torch.is_tensor(v) else v) for k, v in plan_views(plan, B, T, D).items()}
+    return _views(plan, B, T, D)
 
 
 def _check_plan(p, mask):
@@ -45,11 +54,11 @@ def _check_plan(p, mask):
         if name != "dkdv":  # work order: descending count, ties by ascending item (a stable sort of -count)
             flat = np.asarray(counts).reshape(-1)
             np.testing.assert_array_equal(p[f"{name}_order"], np.argsort(-flat, kind="stable"), err_msg=name)
-    # row / column bit masks, bit-exact on every PARTIAL tile (the only ones the kernels read)
+    # row / column bit masks as the kernels build them from the codes (kd_tile_masks),
+    # bit-exact on every tile (the kernels use them on PARTIAL tiles)
     qbits, kbits = tilemap.tile_bits(mask, 64)
-    part = cls == tilemap.PARTIAL
-    np.testing.assert_array_equal(p["qbits"].view(np.uint64)[part], qbits[part], err_msg="qbits")
-    np.testing.assert_array_equal(p["kbits"].view(np.uint64)[part], kbits[part], err_msg="kbits")
+    np.testing.assert_array_equal(p["qbits"].view(np.uint64), qbits, err_msg="row masks")
+    np.testing.assert_array_equal(p["kbits"].view(np.uint64), kbits, err_msg="column masks")
 
 
 @pytest.mark.parametrize("T,causal", [(256, True), (2048, True), (200, False), (1, True), (77, True)])
@@ -166,8 +175,7 @@ def test_plan_from_tokens_against_oracle(dev, rule):
             for ln in (None, lens):
                 got = build_plan_from_tokens(tk, D, rule=rule, lens=None if ln is None else torch.from_numpy(ln).to(dev))
                 torch.cuda.synchronize()
-                p = {k: (v.cpu().numpy() if torch.is_tensor(v) else v)
-                     for k, v in plan_views(got.tensor, B, T, D).items()}
+                p = _views(got.tensor, B, T, D)
                 m = dense_mask(T, B=B, in_span=in_span, span_id=span_id, is_prefix=is_prefix, lens=ln)
                 _check_plan(p, m)
 
