@@ -279,7 +279,7 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
   // copies issued after it), or into a register in the fp8 variant
   uint32_t kc_reg = 0, kc_next = 0;
   auto load_codes = [&](int e, int slot) {  // slot = e & 1
-    const uint32_t j = entry_tile(ent[e]) * 64u + uint32_t(lane);
+    const uint32_t j = entry_tile(ent[e]) * 64u + uint32_t(lane_here());
     if constexpr (LDS_CODES) {
       if (wave == 0) dma_b32(rs_codes, j * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_kc[slot][0])))));
     } else {
@@ -334,9 +334,11 @@ __global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __res
     // scheduling fences, and the mask must not hold back the softmax below
     const uint32_t mcls = entry_class(cur, member);
     uint64_t rowbits = 0;  // EMPTY: nothing allowed
-    if (mcls == TILE_PARTIAL)  // wave-uniform
-      rowbits = query_row_mask(qcode, qrow, LDS_CODES ? s_kc[LDS_CODES ? buf : 0][lane] : kc_reg,
-                               int(entry_tile(cur)) * 64);
+    if (mcls == TILE_PARTIAL) {  // wave-uniform
+      const int l = lane_here();  // (lane-derived values are recomputed here, not kept live)
+      rowbits = query_row_mask(qcode, qblock * 128 + wave * 32 + (l & 31),
+                               LDS_CODES ? s_kc[LDS_CODES ? buf : 0][l] : kc_reg, int(entry_tile(cur)) * 64);
+    }
 
     // S^T = K Q^T and dP^T = V dO^T; A operands (K / K8 and V rows) are read
     // DQ_PF steps ahead of their MFMAs, steps i: kb = i & 1, st = i >> 1; the
@@ -558,8 +560,8 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   auto ahead = [&](const Slots& s, int k) {  // slots of tile e + k (k < every slot count)
     return Slots{wrap(s.q + k, NQ), wrap(s.d + k, NDO), wrap(s.ls + k, NLS), wrap(s.dl + k, NDL)};
   };
-  auto load_tile = [&](int e, const Slots& sl) {
-    const uint32_t en = ent[e], qt = entry_tile(en), q0 = qt * 64u;
+  auto load_tile = [&](uint32_t en, const Slots& sl) {  // en: the tile's list entry
+    const uint32_t q0 = entry_tile(en) * 64u;
     if constexpr (!Q8) TL::load_async(rs_q, q0 * qrb, qoff, lds_addr(s_q[sl.q]), wave);
     TL::load_async(rs_do, q0 * dorb, dooff, lds_addr(s_do[sl.d]), wave);
     if constexpr (Q8) TQ8::load_async(rs_q8, q0 * uint32_t(D), q8off, lds_addr(s_q8[Q8 ? sl.d : 0]), wave);
@@ -571,8 +573,8 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
       dma_b32(rs_codes, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_qc[sl.ls][0])))));
   };
   // fp8: the 16-bit Q tile of tile e (the dK product's operand in step e + 1)
-  auto load_q16 = [&](int e, const Slots& sl) {
-    const uint32_t q0 = entry_tile(ent[e]) * 64u;
+  auto load_q16 = [&](uint32_t en, const Slots& sl) {
+    const uint32_t q0 = entry_tile(en) * 64u;
     TL::load_async(rs_q, q0 * qrb, qoff, lds_addr(s_q[sl.q]), wave);
   };
   // Wait until tile e's loads (and older ones) have landed while tile e+1's,
@@ -659,8 +661,16 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
     __builtin_amdgcn_sched_barrier(0x406);
   };
 
+  // list entries e .. e + PD - 1 at the start of step e, carried in SGPRs:
+  // each step loads one entry (e + PD, for its tile copy) next to the copy,
+  // and the P waves' class of tile e is not re-read from memory inside the
+  // products, where a scalar load in flight would make every LDS wait there
+  // wait for all outstanding LDS reads (scalar loads complete out of order)
+  uint32_t pend[PD];
+#pragma unroll
+  for (int i = 0; i < PD; ++i) pend[i] = i < n ? ent[i] : 0u;
   Slots sl{0, 0, 0, 0};  // slots of tile e (e = 0 here)
-  if (n > 0) load_tile(0, sl);
+  if (n > 0) load_tile(pend[0], sl);
   // the B operand's register loads are complete here: the compiler's wait
   // for them falls here, not at their first use (where it would also wait
   // for the copies of tile 1)
@@ -668,7 +678,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
 #pragma unroll
   for (int st = 0; st < DS; ++st) settle(bf[st]);
   settle(kcode);
-  for (int e = 1; e < PD && e < n; ++e) load_tile(e, ahead(sl, e));
+  if (PD > 1 && n > 1) load_tile(pend[PD > 1 ? 1 : 0], ahead(sl, 1));
   // S of tile e (P waves), or dP of tile e carried into step e + 1 (dS
   // waves): one register set for both roles
   f32x16 x[2] = {f32x16{}, f32x16{}};
@@ -677,9 +687,17 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
     // tiles up to e landed (tile e + PD - 1 may be in flight when PD = 2)
     wait_tile(PD == 2 && e + 1 < n);
     barrier_lds();  // tile e landed, P(e-1) written; P(e-2) and the slots of tile e+PD released
-    if (e + PD < n) load_tile(e + PD, ahead(sl, PD));
+    uint32_t en = pend[0];  // entry of tile e (e < n)
+    asm volatile("" : "+s"(en));
+    {
+      const uint32_t en_pd = e + PD < n ? ent[e + PD] : 0u;
+      if (e + PD < n) load_tile(en_pd, ahead(sl, PD));
+#pragma unroll
+      for (int i = 0; i + 1 < PD; ++i) pend[i] = pend[i + 1];
+      pend[PD - 1] = en_pd;
+    }
     if constexpr (Q8) {
-      if (e < n) load_q16(e, sl);  // read by the dS waves in step e + 1
+      if (e < n) load_q16(en, sl);  // read by the dS waves in step e + 1
     }
     const int pb = e & 1;
     if (role == 0) {
@@ -719,10 +737,10 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
         } else {
           rows_times_b(s_q[sl.q], x, true);
         }
-        const uint32_t mcls = entry_class(ent[e], member);
+        const uint32_t mcls = entry_class(en, member);
         if (mcls != TILE_FULL) {  // wave-uniform
           const uint64_t colbits = mcls == TILE_PARTIAL  // EMPTY: nothing allowed
-                                       ? key_col_mask(kcode, krow, s_qc[sl.ls][lane], int(entry_tile(ent[e])) * 64)
+                                       ? key_col_mask(kcode, krow, s_qc[sl.ls][lane], int(entry_tile(en)) * 64)
                                        : 0u;
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {

@@ -159,6 +159,19 @@ KD_DEV void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" :::
 template <class T>
 KD_DEV void settle(T& v) { asm volatile("" : "+v"(v)); }
 
+// The lane index, computed where it is used (two VALU ops).  Values derived
+// from the lane and needed only on rare paths of a step loop (a PARTIAL
+// tile's mask) are better recomputed from this than kept live: at the
+// kernels' register budget the compiler spills them, and a spill reload in
+// the loop carries an s_waitcnt vmcnt(0) that also waits for the tile copies
+// in flight.  Being volatile, it is neither hoisted nor merged with the
+// prologue's lane index.
+KD_DEV int lane_here() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 KD_DEV void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // wait until at most N vector memory loads of this wave are outstanding
 template <int N>
