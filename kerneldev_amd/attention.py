@@ -28,6 +28,12 @@ SUPPORTED_HEAD_DIMS = REFERENCE_HEAD_DIMS
 # epilogues, fp8 scores at 128); fp32 inputs and the other head dims run on
 # the fp32 vector-ALU kernels (kd_simt.hip)
 MFMA_HEAD_DIMS = (64, 128)
+# 16-bit inputs with these head dims run on the d = 64 MFMA kernels, zero-
+# padded: zero columns change no score (S = Q K^T), O's extra columns are
+# P 0 = 0 and the gradients' extra columns are dropped by the pad's autograd.
+# Twice the matrix work of a native kernel, an order of magnitude ahead of
+# the fp32 vector-ALU kernels that the C ABI runs them on.
+PADDED_HEAD_DIMS = {16: 64, 32: 64}
 
 # precision -> arithmetic of P and dS in the kernels.  The reference rounds P
 # to V's dtype for P V (original_kernel.py:566-571) and keeps P and dS in fp32
@@ -439,6 +445,9 @@ def flash_attention(
             fused_signs = signs
         else:
             q, k = _rot_op(q, signs, False), _rot_op(k, signs, False)
+    pad_to = PADDED_HEAD_DIMS.get(D, 0) if q.dtype != torch.float32 else 0
+    if pad_to:  # after the rotation, which acts on the caller's head dim
+        q, k, v = (torch.nn.functional.pad(x, (0, pad_to - D)) for x in (q, k, v))
     fp8 = ()
     if qk_dtype == "fp8_e4m3" and not hadamard:  # with Hadamard the op quantises Q R, K R itself
         (q8, q_scale), (k8, k_scale) = quantize_fp8(q), quantize_fp8(k)
@@ -453,6 +462,8 @@ def flash_attention(
                                  quant_fp8=hadamard and qk_dtype == "fp8_e4m3", prec=PRECISIONS[precision])
     if plan is not None:
         plan_t = plan.tensor
+    if pad_to:
+        o = o[..., :D]
     if in_dtype == torch.float32:
         o = o.to(torch.float32)
 

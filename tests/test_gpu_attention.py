@@ -130,8 +130,28 @@ def _other_dims_case(D, causal_only, seed):
 @pytest.mark.parametrize("D", [16, 32, 256])
 @pytest.mark.parametrize("causal_only", [True, False])
 def test_other_head_dims(dev, D, causal_only):
-    """The head dims original_kernel.py:1720 accepts beyond 64 / 128 (fp32 vector-ALU kernels)."""
+    """The head dims original_kernel.py:1720 accepts beyond 64 / 128: 16 and 32
+    zero-padded onto the d = 64 MFMA kernels, 256 on the fp32 vector-ALU kernels."""
     _case(_other_dims_case(D, causal_only, seed=40 + D), dev)
+
+
+@pytest.mark.parametrize("D", [16, 32])
+def test_small_head_dims_on_the_vector_alu_kernels(dev, D):
+    """flash_attention runs 16-bit d = 16, 32 zero-padded on the d = 64 MFMA
+    kernels; the C ABI itself runs them on the fp32 vector-ALU kernels, called
+    here directly through the ops with the unpadded operands."""
+    from kerneldev_amd.attention import _bwd_op, _fwd_op
+    from kerneldev_amd import _lib
+
+    inp = _other_dims_case(D, False, seed=70 + D)
+    print(f"vector-ALU kernels, bf16 D={D}", flush=True)
+    q, k, v, do = (inp[x].to(dev) for x in ("q", "k", "v", "do"))
+    meta = [inp[n].to(dev) for n in ("in_span", "span_id", "is_prefix")]
+    sc = D ** -0.5
+    o, lse, plan, o_lo, *_ = _fwd_op(q, k, v, None, *meta, sc, _lib.KD_MODE_FORMULA, True)
+    dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, sc, o_lo)
+    torch.cuda.synchronize()
+    compare({"o": o, "lse": lse, "dq": dq, "dk": dk, "dv": dv}, _reference(inp))
 
 
 @pytest.mark.parametrize("D", [32, 256])
