@@ -19,9 +19,10 @@
  *     (b, h, t) strides multiples of 8 elements, the t stride >= D and
  *     T * t_stride * element size < 2^31 bytes.
  *   - Head dims 16, 32, 64, 128, 256 (original_kernel.py:1720).  bf16 / fp16
- *     at D = 64, 128 run on the MFMA kernels; fp32 inputs (any D) and 16-bit
- *     inputs at D = 16, 32, 256 run on fp32 vector-ALU kernels (no fp8 scores,
- *     no dqk_signs there; precision is then always full fp32).
+ *     at D = 64, 128, 256 run on the MFMA kernels (dqk_signs at 64, 128 only);
+ *     fp32 inputs (any D) and 16-bit inputs at D = 16, 32 run on fp32
+ *     vector-ALU kernels (no fp8 scores, no dqk_signs there; precision is then
+ *     always full fp32).
  *   - LSE is stored in log2 units (LSE2 = log2 sum_j exp2(S_ij * sm_scale *
  *     log2 e)), as the reference stores it (original_kernel.py:603-604).
  *     Fully masked rows get O = 0, LSE = -inf and zero gradients.

@@ -126,7 +126,7 @@ KD_DEV void store_rows_T_unrot(uint16_t* g, f32x16 (&acc)[D / 32], float scale, 
     const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     acc[r >> 4][r & 15] = hf ? __uint_as_float(p[0]) - __uint_as_float(p[1]) : __uint_as_float(p[0]) + __uint_as_float(p[1]);
   }
-  const float c = scale * (D == 128 ? 0.088388347648318440f : 0.125f);  // scale / sqrt(D)
+  const float c = scale * (D == 256 ? 0.0625f : D == 128 ? 0.088388347648318440f : 0.125f);  // scale / sqrt(D)
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
@@ -159,7 +159,7 @@ KD_DEV void tr_addrs(int lane, int (&addr)[D / 32][2]) {
 
 // ------------------------------------------------------------------- dQ ----
 template <class E, int D, bool Q8, bool SP>
-__global__ __launch_bounds__(256, 2) void k_dq(AttnArgs a, const uint32_t* __restrict__ codes,
+__global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const uint32_t* __restrict__ codes,
                                                const uint32_t* __restrict__ list,
                                                const int32_t* __restrict__ count,
                                                const uint32_t* __restrict__ order, int nT, int nQB,
@@ -844,6 +844,224 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   }
 }
 
+// ---------------------------------------------- dK/dV at head dim 256 ------
+// At D = 256 a 64-row tile is 32 KiB and the wave-pair kernel fits neither
+// the LDS nor 256 registers per wave.  Here one wave per SIMD (4 waves, up to
+// 512 registers) does all four products of its 32 keys, for the columns
+// [D0, D0 + DH) of dK and dV: S^T and dP^T over the full head dim (B
+// operands: this lane's K and V rows, 2 x 64 registers), then P, dS in
+// registers and dV^T, dK^T for DH columns (A operands: dO^T and Q^T column
+// blocks, read transposed).  Two launches (D0 = 0, 128) give the whole
+// gradient, each recomputing S and dP.  Tiles are copied one step ahead into
+// two slots (2 x 2 x 32 KiB).
+template <class E, int D, bool SP, int DH, int D0>
+__global__ __launch_bounds__(256, 1) void k_dkdv_wide(AttnArgs a, const uint32_t* __restrict__ codes,
+                                                      const uint32_t* __restrict__ list,
+                                                      const int32_t* __restrict__ count, int nT, int nKB) {
+  using TL = Tile<D, 4>;
+  constexpr int DS = D / 16, NL = TL::LOADS_PER_WAVE;
+  constexpr int HB = DH / 32, HB0 = D0 / 32;  // column blocks of this launch
+  constexpr int NSL = 2;                      // slots per stream (copies one step ahead)
+  __shared__ __attribute__((aligned(1024))) uint8_t s_q[NSL][TL::BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_do[NSL][TL::BYTES];
+  __shared__ __attribute__((aligned(256))) float s_lse[NSL][64];
+  __shared__ __attribute__((aligned(256))) float s_delta[NSL][64];
+  __shared__ __attribute__((aligned(256))) uint32_t s_qc[NSL][64];
+
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, hf = lane >> 5,
+            c = lane & 31;
+  const int T = a.T, H = a.H;
+  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int hb = work / nKB;
+  const int kblock = work % nKB;
+  const int b = hb % a.B, h = hb / a.B, bh = b * H + h;
+
+  const uint16_t* qg = static_cast<const uint16_t*>(a.q) + b * a.q_strides[0] + h * a.q_strides[1];
+  const uint16_t* dog = static_cast<const uint16_t*>(a.dout) + b * a.do_strides[0] + h * a.do_strides[1];
+  const uint16_t* kg = static_cast<const uint16_t*>(a.k) + b * a.k_strides[0] + h * a.k_strides[1];
+  const uint16_t* vg = static_cast<const uint16_t*>(a.v) + b * a.v_strides[0] + h * a.v_strides[1];
+  const uint32_t qrb = uint32_t(a.q_strides[2]) * 2u, dorb = uint32_t(a.do_strides[2]) * 2u,
+                 krb = uint32_t(a.k_strides[2]) * 2u, vrb = uint32_t(a.v_strides[2]) * 2u;
+  const u32x4 rs_q = rsrc_words(qg, uint32_t(T) * qrb);
+  const u32x4 rs_do = rsrc_words(dog, uint32_t(T) * dorb);
+  const int64_t BHT = int64_t(a.B) * H * T;
+  const u32x4 rs_lse = rsrc_words(a.delta + BHT + int64_t(bh) * T, uint32_t(T) * 4u);
+  const u32x4 rs_dl = rsrc_words(a.delta + int64_t(bh) * T, uint32_t(T) * 4u);
+  const u32x4 rs_codes = rsrc_words(codes + int64_t(b) * T, uint32_t(T) * 4u);
+
+  const int krow = kblock * 128 + wave * 32 + c;
+  const bool kvalid = krow < T;
+  u32x4 bk[DS], bv[DS];  // this lane's K and V rows (B operands of S^T, dP^T)
+  {
+    const auto rk = make_rsrc(kg, uint32_t(T) * krb), rv = make_rsrc(vg, uint32_t(T) * vrb);
+#pragma unroll
+    for (int st = 0; st < DS; ++st) {
+      bk[st] = buf_load16(rk, uint32_t(krow) * krb + (16 * st + 8 * hf) * 2);
+      bv[st] = buf_load16(rv, uint32_t(krow) * vrb + (16 * st + 8 * hf) * 2);
+    }
+  }
+  const int member = wave >> 1;
+  uint32_t kcode = kvalid ? codes[int64_t(b) * T + krow] : 0u;
+
+  const int lbase = b * nKB + kblock;
+  const int n = count[lbase];
+  const uint32_t* ent = list + int64_t(lbase) * nT;
+
+  uint32_t qoff[NL], dooff[NL];
+  TL::load_offsets(wave, lane, qrb, qoff);
+  TL::load_offsets(wave, lane, dorb, dooff);
+  auto load_tile = [&](uint32_t en, int slot) {
+    const uint32_t q0 = entry_tile(en) * 64u;
+    TL::load_async(rs_q, q0 * qrb, qoff, lds_addr(s_q[slot]), wave);
+    TL::load_async(rs_do, q0 * dorb, dooff, lds_addr(s_do[slot]), wave);
+    if (wave == 1)
+      dma_b32(rs_lse, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_lse[slot][0])))));
+    else if (wave == 2)
+      dma_b32(rs_dl, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_delta[slot][0])))));
+    else if (wave == 3)
+      dma_b32(rs_codes, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_qc[slot][0])))));
+  };
+
+  const int srow = sigma(c);
+  int raddr[DS];
+#pragma unroll
+  for (int st = 0; st < DS; ++st) raddr[st] = TL::at(srow, 2 * st + hf);
+  int taddr_all[D / 32][2];
+  tr_addrs<D>(lane, taddr_all);
+  int taddr[HB][2];
+#pragma unroll
+  for (int db = 0; db < HB; ++db) {
+    taddr[db][0] = taddr_all[HB0 + db][0];
+    taddr[db][1] = taddr_all[HB0 + db][1];
+  }
+
+  const float sl2 = a.sm_scale * 1.4426950408889634f;
+  f32x16 acc_v[HB], acc_k[HB];  // dV^T, dK^T for this launch's columns
+#pragma unroll
+  for (int db = 0; db < HB; ++db) acc_v[db] = acc_k[db] = f32x16{};
+
+  constexpr int PF = DKDV_PF;
+  auto rows_times_b = [&](const uint8_t* ar_g, const u32x4 (&bop)[DS], f32x16 (&x)[2]) {
+    lds_u8* ar = to_lds(ar_g);
+    constexpr int NS = 2 * DS;
+    auto read = [&](int i) { return ds_read16(ar + raddr[i >> 1] + (i & 1) * 32 * TL::ROWB); };
+    u32x4 av[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) av[i] = read(i);
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      __builtin_amdgcn_sched_barrier(0x406);
+      x[i & 1] = mfma32x32x16<E>(av[i % PF], bop[i >> 1], x[i & 1]);
+      if (i + PF < NS) av[i % PF] = read(i + PF);
+    }
+    __builtin_amdgcn_sched_barrier(0x406);
+  };
+  auto accumulate = [&](const uint8_t* at_g, f32x16 (&acc)[HB], const u32x4 (&bop)[2][2],
+                        const u32x4 (&bopl)[2][2]) {
+    lds_u8* at = to_lds(at_g);
+    constexpr int NS = 4 * HB;
+    auto read = [&](int i) {
+      const int k4 = i / HB, db = i % HB, off = k4 * 16 * TL::ROWB;
+      const u32x2 lo = ds_read_tr16(at + taddr[db][0] + off);
+      const u32x2 hi = ds_read_tr16(at + taddr[db][1] + off);
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
+    u32x4 av[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) av[i] = read(i);
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const int k4 = i / HB, db = i % HB;
+      __builtin_amdgcn_sched_barrier(0x406);
+      acc[db] = mfma32x32x16<E>(av[i % PF], bop[k4 >> 1][k4 & 1], acc[db]);
+      if constexpr (SP) acc[db] = mfma32x32x16<E>(av[i % PF], bopl[k4 >> 1][k4 & 1], acc[db]);
+      if (i + PF < NS) av[i % PF] = read(i + PF);
+    }
+    __builtin_amdgcn_sched_barrier(0x406);
+  };
+  auto splat_rows = [&](const float* v, f32x16 (&x)[2]) {
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int ql = 32 * qb + 16 * t + 8 * hf;
+        const f32x4 l0 = *reinterpret_cast<const f32x4*>(&v[ql]);
+        const f32x4 l1 = *reinterpret_cast<const f32x4*>(&v[ql + 4]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          x[qb][8 * t + j] = l0[j];
+          x[qb][8 * t + 4 + j] = l1[j];
+        }
+      }
+  };
+
+  if (n > 0) load_tile(ent[0], 0);
+  wait_vmem();
+#pragma unroll
+  for (int st = 0; st < DS; ++st) {
+    settle(bk[st]);
+    settle(bv[st]);
+  }
+  settle(kcode);
+  uint32_t en_cur = n > 0 ? ent[0] : 0u, en_next = n > 1 ? ent[1] : 0u;  // entries of tiles e, e + 1
+
+  int slot = 0;
+  for (int e = 0; e < n; ++e) {
+    wait_vmem();   // tile e landed (the only copy in flight)
+    barrier_lds(); // ... for every wave; every wave is done with tile e - 1
+    uint32_t en = en_cur;
+    asm volatile("" : "+s"(en));
+    if (e + 1 < n) load_tile(en_next, slot ^ 1);
+    en_cur = en_next;
+    en_next = e + 2 < n ? ent[e + 2] : 0u;
+    f32x16 x[2], y[2];  // S^T - LSE / c and dP^T - Delta
+    splat_rows(s_lse[slot], x);
+    splat_rows(s_delta[slot], y);
+    rows_times_b(s_q[slot], bk, x);
+    rows_times_b(s_do[slot], bv, y);
+    const uint32_t mcls = entry_class(en, member);
+    if (mcls != TILE_FULL) {  // wave-uniform
+      const uint64_t colbits = mcls == TILE_PARTIAL  // EMPTY: nothing allowed
+                                   ? key_col_mask(kcode, krow, s_qc[slot][lane], int(entry_tile(en)) * 64)
+                                   : 0u;
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const uint32_t w = uint32_t(colbits >> (32 * qb)) >> (8 * hf);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[qb][r] = mask_bit(x[qb][r], w, 16 * (r >> 3) + (r & 7));
+      }
+    }
+    u32x4 pb[2][2], pl[2][2], sb[2][2], sl_[2][2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        float p[8], ds[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          p[j] = fast_exp2(x[qb][8 * t + j] * sl2);
+          ds[j] = p[j] * y[qb][8 * t + j];
+        }
+        pb[qb][t] = pack8<E>(p);
+        sb[qb][t] = pack8<E>(ds);
+        if constexpr (SP) {
+          pl[qb][t] = pack8_residual<E>(p, pb[qb][t]);
+          sl_[qb][t] = pack8_residual<E>(ds, sb[qb][t]);
+        }
+      }
+    accumulate(s_do[slot], acc_v, pb, pl);  // dV^T += dO^T P
+    accumulate(s_q[slot], acc_k, sb, sl_);  // dK^T += Q^T dS
+    slot ^= 1;
+  }
+
+  if (kvalid) {
+    uint16_t* gv = static_cast<uint16_t*>(a.dv) + b * a.dv_strides[0] + h * a.dv_strides[1] + krow * a.dv_strides[2];
+    uint16_t* gk = static_cast<uint16_t*>(a.dk) + b * a.dk_strides[0] + h * a.dk_strides[1] + krow * a.dk_strides[2];
+    store_rows_T<E, DH>(gv + D0, acc_v, 1.f, hf);
+    store_rows_T<E, DH>(gk + D0, acc_k, a.sm_scale, hf);
+  }
+}
+
 // -------------------------------------------------------------- launchers --
 template <class E, int D>
 static void launch_delta_t(const AttnArgs& a, hipStream_t st) {
@@ -869,10 +1087,20 @@ template <class E, int D, bool Q8, bool SP>
 static void launch_dkdv_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dkdv_blocks;
-  hipLaunchKernelGGL((k_dkdv<E, D, Q8, SP>), dim3(grid), dim3(512), 0, st, a,
-                     reinterpret_cast<const uint32_t*>(plan + L.codes),
-                     reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
-                     reinterpret_cast<const int32_t*>(plan + L.dkdv_count), L.nT, L.n_dkdv_blocks);
+  if constexpr (D == 256) {  // two launches, the column halves of dK and dV
+    auto* codes = reinterpret_cast<const uint32_t*>(plan + L.codes);
+    auto* list = reinterpret_cast<const uint32_t*>(plan + L.dkdv_list);
+    auto* cnt = reinterpret_cast<const int32_t*>(plan + L.dkdv_count);
+    hipLaunchKernelGGL((k_dkdv_wide<E, D, SP, 128, 0>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, L.nT,
+                       L.n_dkdv_blocks);
+    hipLaunchKernelGGL((k_dkdv_wide<E, D, SP, 128, 128>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, L.nT,
+                       L.n_dkdv_blocks);
+  } else {
+    hipLaunchKernelGGL((k_dkdv<E, D, Q8, SP>), dim3(grid), dim3(512), 0, st, a,
+                       reinterpret_cast<const uint32_t*>(plan + L.codes),
+                       reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
+                       reinterpret_cast<const int32_t*>(plan + L.dkdv_count), L.nT, L.n_dkdv_blocks);
+  }
 }
 
 template <class E, int D, bool Q8 = false>
@@ -885,10 +1113,12 @@ static void launch_dkdv_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st
   do {                                                               \
     if (a.dtype == KD_BF16) {                                        \
       if (a.D == 64) FN<BF16, 64>(__VA_ARGS__);                      \
-      else FN<BF16, 128>(__VA_ARGS__);                               \
+      else if (a.D == 128) FN<BF16, 128>(__VA_ARGS__);               \
+      else FN<BF16, 256>(__VA_ARGS__);                               \
     } else {                                                         \
       if (a.D == 64) FN<F16, 64>(__VA_ARGS__);                       \
-      else FN<F16, 128>(__VA_ARGS__);                                \
+      else if (a.D == 128) FN<F16, 128>(__VA_ARGS__);                \
+      else FN<F16, 256>(__VA_ARGS__);                                \
     }                                                                \
   } while (0)
 

@@ -67,7 +67,7 @@ int check_common(const kd_attn_args* a) {
     return fail(KD_ERR_UNSUPPORTED, "head dim must be 16, 32, 64, 128 or 256");
   if (a->dtype != KD_BF16 && a->dtype != KD_F16 && a->dtype != KD_F32)
     return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16, fp16 or fp32");
-  if (kd::use_simt(*a) && a->dqk_signs != nullptr)
+  if (a->dqk_signs != nullptr && (kd::use_simt(*a) || a->D == 256))
     return fail(KD_ERR_UNSUPPORTED, "dqk_signs is built for bf16 / fp16 at head dim 64 or 128");
   if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale))
     return fail(KD_ERR_INVALID, "sm_scale must be finite and > 0");

@@ -56,7 +56,7 @@ template <> constexpr float rescale_log2<F16>() { return 15.f; }
 #endif
 
 template <class E, int D, bool Q8, int QB, bool SP>
-__global__ __launch_bounds__(256 / QB, QB == 1 ? 2 : 1) void k_fwd(AttnArgs a, const uint32_t* __restrict__ codes,
+__global__ __launch_bounds__(256 / QB, (QB == 1 && D <= 128) ? 2 : 1) void k_fwd(AttnArgs a, const uint32_t* __restrict__ codes,
                                                                 const uint32_t* __restrict__ list,
                                                                 const int32_t* __restrict__ count,
                                                                 const uint32_t* __restrict__ order, int nT, int nQB) {
@@ -391,10 +391,12 @@ int launch_fwd(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
     launch_fwd_p<BF16, 128, true>(a, plan, st);
   } else if (a.dtype == KD_BF16) {
     if (a.D == 64) launch_fwd_p<BF16, 64>(a, plan, st);
-    else launch_fwd_p<BF16, 128>(a, plan, st);
+    else if (a.D == 128) launch_fwd_p<BF16, 128>(a, plan, st);
+    else launch_fwd_p<BF16, 256>(a, plan, st);
   } else {
     if (a.D == 64) launch_fwd_p<F16, 64>(a, plan, st);
-    else launch_fwd_p<F16, 128>(a, plan, st);
+    else if (a.D == 128) launch_fwd_p<F16, 128>(a, plan, st);
+    else launch_fwd_p<F16, 256>(a, plan, st);
   }
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }

@@ -340,7 +340,7 @@ static void launch_simt_d(int which, const AttnArgs& a, const uint8_t* plan, hip
   }
 }
 
-bool use_simt(const AttnArgs& a) { return a.dtype == KD_F32 || (a.D != 64 && a.D != 128); }
+bool use_simt(const AttnArgs& a) { return a.dtype == KD_F32 || (a.D != 64 && a.D != 128 && a.D != 256); }
 
 // which: 0 forward, 1 Delta, 2 dQ, 3 dK/dV
 int launch_simt_kernel(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st) {

@@ -69,7 +69,9 @@ struct Tile {
   static_assert(LOADS % NW == 0, "tile copy must split evenly over the waves");
 
   KD_DEV static int swz(int r) {
-    if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+    // D = 256: 512-byte rows meet the banks as 256-byte rows do, so the
+    // D = 128 swizzle (low four chunk bits) serves them too
+    if constexpr (D >= 128) return ((r & 3) << 2) | ((r >> 2) & 3);
     else return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
   }
   // byte offset of (row, 16-byte chunk) inside the tile
