@@ -158,7 +158,10 @@ KD_DEV void tr_addrs(int lane, int (&addr)[D / 32][2]) {
 }
 
 // ------------------------------------------------------------------- dQ ----
-template <class E, int D, bool Q8, bool SP>
+// DH, D0: this launch accumulates dQ's columns [D0, D0 + DH) (D = 256 runs
+// two launches of 128 columns, each recomputing S and dP, so that the dQ
+// accumulators fit next to the operands of the full head dim)
+template <class E, int D, bool Q8, bool SP, int DH = D, int D0 = 0>
 __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const uint32_t* __restrict__ codes,
                                                const uint32_t* __restrict__ list,
                                                const int32_t* __restrict__ count,
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
   using TL = Tile<D>;
   using SO = ScoreOp<E, D, Q8>;  // S^T = K Q^T (16-bit, or fp8 from the K8 tile)
   using TK8 = typename ScoreOp<E, D, true>::TL;
-  constexpr int DS = D / 16, DB = D / 32, NL = TL::LOADS_PER_WAVE, NL8 = TK8::LOADS_PER_WAVE;
+  constexpr int DS = D / 16, DB = DH / 32, NL = TL::LOADS_PER_WAVE, NL8 = TK8::LOADS_PER_WAVE;
   __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][TL::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][TL::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_k8[Q8 ? 2 : 1][Q8 ? TK8::BYTES : 16];
@@ -292,8 +295,14 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
   int raddr[DS];
 #pragma unroll
   for (int st = 0; st < DS; ++st) raddr[st] = TL::at(srow, 2 * st + hf);
-  int taddr[DB][2];
-  tr_addrs<D>(lane, taddr);
+  int taddr_all[D / 32][2];
+  tr_addrs<D>(lane, taddr_all);
+  int taddr[DB][2];  // the column blocks of this launch
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    taddr[db][0] = taddr_all[D0 / 32 + db][0];
+    taddr[db][1] = taddr_all[D0 / 32 + db][1];
+  }
 
   // the fp8 product carries the dequantisation scales of Q and K
   const float sl2 = a.sm_scale * 1.4426950408889634f * (Q8 ? a.q_scale[bh] * a.k_scale[bh] : 1.f);
@@ -438,8 +447,12 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
 
   if (qvalid) {
     uint16_t* g = static_cast<uint16_t*>(a.dq) + b * a.dq_strides[0] + h * a.dq_strides[1] + qrow * a.dq_strides[2];
-    if (a.dqk_signs != nullptr) store_rows_T_unrot<E, D>(g, acc, a.sm_scale, hf, a.dqk_signs);
-    else store_rows_T<E, D>(g, acc, a.sm_scale, hf);
+    if constexpr (DH == D) {
+      if (a.dqk_signs != nullptr) store_rows_T_unrot<E, D>(g, acc, a.sm_scale, hf, a.dqk_signs);
+      else store_rows_T<E, D>(g, acc, a.sm_scale, hf);
+    } else {
+      store_rows_T<E, DH>(g + D0, acc, a.sm_scale, hf);  // (no dqk_signs at split widths)
+    }
   }
 }
 
@@ -1073,10 +1086,19 @@ template <class E, int D, bool Q8, bool SP>
 static void launch_dq_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_delta) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dq_blocks;
-  hipLaunchKernelGGL((k_dq<E, D, Q8, SP>), dim3(grid), dim3(256), 0, st, a, reinterpret_cast<const uint32_t*>(plan + L.codes),
-                     reinterpret_cast<const uint32_t*>(plan + L.dq_list),
-                     reinterpret_cast<const int32_t*>(plan + L.dq_count),
-                     reinterpret_cast<const uint32_t*>(plan + L.dq_order), L.nT, L.n_dq_blocks, fuse_delta);
+  auto* codes = reinterpret_cast<const uint32_t*>(plan + L.codes);
+  auto* list = reinterpret_cast<const uint32_t*>(plan + L.dq_list);
+  auto* cnt = reinterpret_cast<const int32_t*>(plan + L.dq_count);
+  auto* order = reinterpret_cast<const uint32_t*>(plan + L.dq_order);
+  if constexpr (D == 256) {  // two launches, the column halves of dQ; the first forms Delta
+    hipLaunchKernelGGL((k_dq<E, D, Q8, SP, 128, 0>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, order, L.nT,
+                       L.n_dq_blocks, fuse_delta);
+    hipLaunchKernelGGL((k_dq<E, D, Q8, SP, 128, 128>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, order, L.nT,
+                       L.n_dq_blocks, false);
+  } else {
+    hipLaunchKernelGGL((k_dq<E, D, Q8, SP>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, order, L.nT,
+                       L.n_dq_blocks, fuse_delta);
+  }
 }
 template <class E, int D, bool Q8 = false>
 static void launch_dq_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_delta) {
