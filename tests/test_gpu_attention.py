@@ -208,6 +208,15 @@ def test_fp16(dev):
     _case(dict(name="fp16", q=q, k=k, v=v, do=do, in_span=in_span, span_id=span_id, is_prefix=is_prefix), dev)
 
 
+@pytest.mark.parametrize("D", [32, 128, 256])
+def test_fp16_head_dims(dev, D):
+    """fp16 on the d = 128 and 256 kernels and, zero-padded, the d = 64 ones (d = 32)."""
+    tokens, in_span, span_id, is_prefix = cocktail_batch(2, 512, CONFIG3_LAYOUT, seed=8 + D)
+    q, k, v, do = qkvdo(2, 2, 384, D, seed=9 + D, dtype=torch.float16)
+    _case(dict(name=f"fp16 D{D}", q=q, k=k, v=v, do=do, in_span=in_span[:, :384], span_id=span_id[:, :384],
+               is_prefix=is_prefix[:, :384]), dev)
+
+
 def test_fp16_row_max_jump_below_rescale(dev):
     """fp16 rows whose max jumps by 14.0-15.9998 log2 units from key tile 0 to 1.
 
