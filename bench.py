@@ -55,8 +55,8 @@ USEFUL_FWD, USEFUL_BWD = 4, 10
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs scaled by a 1 GiB copy's counts
 # (profiles/attn_config4_{bf16,fp8_e4m3}_hbm_traffic.md); re-measured whenever the kernels change.
 CONFIG4_TRAFFIC_BYTES = {
-    "bf16": {"fwd": 1140.4e6, "dq": 1507.8e6, "dkdv": 1086.6e6},
-    "fp8_e4m3": {"fwd": 832.0e6, "dq": 1613.8e6, "dkdv": 1201.6e6},
+    "bf16": {"fwd": 1142.0e6, "dq": 1481.6e6, "dkdv": 1081.9e6},
+    "fp8_e4m3": {"fwd": 834.1e6, "dq": 1610.8e6, "dkdv": 1198.4e6},
 }
 
 
