@@ -440,6 +440,9 @@ def main():
             "useful_tflop_per_step": round(useful / 1e12, 4),
             "frac_of_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
             "kernel_ms": {n: round(x, 4) for n, x in per_kernel.items()},
+            # forward = plan + rotation (+ quantisation) + forward kernel; backward = dQ (with Delta) + dK/dV
+            "fwd_ms": round(sum(x for n, x in per_kernel.items() if n not in ("dq", "dkdv")), 4),
+            "bwd_ms": round(per_kernel["dq"] + per_kernel["dkdv"], 4),
             "kernel_algorithmic_tflops": kernel_tflops,
             "event_ms_per_step": round(event_ms, 4),
             "hadamard": hadamard,
