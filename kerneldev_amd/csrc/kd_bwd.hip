@@ -31,6 +31,11 @@
 #ifndef DKDV_PF
 #define DKDV_PF 3
 #endif
+// 1: dK/dV at D = 64 on k_dkdv_wide (each wave all four products, two waves
+// per SIMD); 0: on the wave-pair kernel
+#ifndef DKDV64_FUSED
+#define DKDV64_FUSED 1
+#endif
 #ifndef DQ_PF
 #define DQ_PF 3
 #endif
@@ -868,7 +873,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
 // gradient, each recomputing S and dP.  Tiles are copied one step ahead into
 // two slots (2 x 2 x 32 KiB).
 template <class E, int D, bool SP, int DH, int D0>
-__global__ __launch_bounds__(256, 1) void k_dkdv_wide(AttnArgs a, const uint32_t* __restrict__ codes,
+__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, const uint32_t* __restrict__ codes,
                                                       const uint32_t* __restrict__ list,
                                                       const int32_t* __restrict__ count, int nT, int nKB) {
   using TL = Tile<D, 4>;
@@ -1109,7 +1114,12 @@ template <class E, int D, bool Q8, bool SP>
 static void launch_dkdv_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dkdv_blocks;
-  if constexpr (D == 256) {  // two launches, the column halves of dK and dV
+  if constexpr (D == 64 && DKDV64_FUSED) {  // one launch, all four products per wave
+    hipLaunchKernelGGL((k_dkdv_wide<E, D, SP, 64, 0>), dim3(grid), dim3(256), 0, st, a,
+                       reinterpret_cast<const uint32_t*>(plan + L.codes),
+                       reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
+                       reinterpret_cast<const int32_t*>(plan + L.dkdv_count), L.nT, L.n_dkdv_blocks);
+  } else if constexpr (D == 256) {  // two launches, the column halves of dK and dV
     auto* codes = reinterpret_cast<const uint32_t*>(plan + L.codes);
     auto* list = reinterpret_cast<const uint32_t*>(plan + L.dkdv_list);
     auto* cnt = reinterpret_cast<const int32_t*>(plan + L.dkdv_count);
