@@ -862,10 +862,14 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   }
 }
 
-// ---------------------------------------------- dK/dV at head dim 256 ------
-// At D = 256 a 64-row tile is 32 KiB and the wave-pair kernel fits neither
-// the LDS nor 256 registers per wave.  Here one wave per SIMD (4 waves, up to
-// 512 registers) does all four products of its 32 keys, for the columns
+// ------------------------------------------ dK/dV at head dims 64 and 256 --
+// Each wave does all four products of its 32 keys (4 waves, 128 keys per
+// workgroup), P and dS stay in registers, nothing goes through LDS between
+// waves.  At D = 64 that fits 256 registers: two waves per SIMD and two
+// workgroups per CU (the pair kernel's fp32 P exchange, 64 KiB whatever the
+// head dim, holds it to one).  At D = 256 a 64-row tile is 32 KiB and the
+// wave-pair kernel fits neither the LDS nor 256 registers per wave; there it
+// runs one wave per SIMD (up to 512 registers) for the columns
 // [D0, D0 + DH) of dK and dV: S^T and dP^T over the full head dim (B
 // operands: this lane's K and V rows, 2 x 64 registers), then P, dS in
 // registers and dV^T, dK^T for DH columns (A operands: dO^T and Q^T column
@@ -1076,7 +1080,12 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
     uint16_t* gv = static_cast<uint16_t*>(a.dv) + b * a.dv_strides[0] + h * a.dv_strides[1] + krow * a.dv_strides[2];
     uint16_t* gk = static_cast<uint16_t*>(a.dk) + b * a.dk_strides[0] + h * a.dk_strides[1] + krow * a.dk_strides[2];
     store_rows_T<E, DH>(gv + D0, acc_v, 1.f, hf);
-    store_rows_T<E, DH>(gk + D0, acc_k, a.sm_scale, hf);
+    if constexpr (DH == D) {  // all columns here: dK can be rotated back (dqk_signs)
+      if (a.dqk_signs != nullptr) store_rows_T_unrot<E, D>(gk, acc_k, a.sm_scale, hf, a.dqk_signs);
+      else store_rows_T<E, D>(gk, acc_k, a.sm_scale, hf);
+    } else {
+      store_rows_T<E, DH>(gk + D0, acc_k, a.sm_scale, hf);  // (no dqk_signs at split widths)
+    }
   }
 }
 
