@@ -483,7 +483,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   constexpr int NW = 8;
   using TL = Tile<D, NW>;
   using TQ8 = Tile<Q8 ? D / 2 : D, NW>;  // fp8 Q tiles (D bytes a row); only used at D = 128
-  constexpr int DS = D / 16, DB = D / 32, NL = TL::LOADS_PER_WAVE, NL8 = TQ8::LOADS_PER_WAVE;
+  constexpr int DS = D / 16, DB = D / 32;
   // Tiles are loaded PD steps ahead: 2, or 1 where the fp8 variant's Q8
   // tiles or SP's fp32 P exchange take the LDS.  Slot counts follow from who
   // reads what when: in step e the P waves read Q(e) (fp8: Q8(e)), dO(e),
@@ -562,15 +562,19 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   const int n = count[lbase];
   const uint32_t* ent = list + int64_t(lbase) * nT;
 
-  uint32_t qoff[NL], dooff[NL], q8off[NL8];
-  TL::load_offsets(wave, lane, qrb, qoff);
-  TL::load_offsets(wave, lane, dorb, dooff);
-  TQ8::load_offsets(wave, lane, uint32_t(D), q8off);
+  // The P waves make every copy (the four of them share each tile): the dS
+  // waves carry the longer chain of a step, the P waves wait for them at the
+  // barrier, so the copies' issue time is taken from the P waves' slack.
+  // The per-lane copy offsets are recomputed at each copy from the lane id
+  // (lane_here: not hoisted), which costs a few VALU instructions of the P
+  // waves' slack instead of registers held across the loop.
+  using TC = Tile<D, 4>;
+  using TC8 = Tile<Q8 ? D / 2 : D, 4>;
   const u32x4 rs_q8 = rsrc_words(Q8 ? a.q8 + int64_t(bh) * T * D : nullptr, Q8 ? uint32_t(T) * D : 0u);
   // Tile e's copies, all inline asm (dma_b128 / dma_b32: the compiler places
-  // no waits for them, so they stay in flight until wait_tile): first the P
-  // waves' column masks of a PARTIAL tile, then NL + NL (+ NL8) tile loads per
-  // wave, then LSE (wave 4) and Delta (wave 5), one load each.
+  // no waits for them, so they stay in flight until wait_tile): per P wave
+  // 2 TC::LOADS_PER_WAVE tile loads (fp8: Q8 and dO), then LSE (wave 1),
+  // Delta (wave 2) and the query codes (wave 3), one load each.
   // Slots of tile e: e % NQ, e % NDO (Q8 tiles too), e % NLS (LSE, masks),
   // e % NDL; the loop keeps them as wrapping counters (uniform, no division).
   struct Slots { int q, d, ls, dl; };
@@ -578,31 +582,41 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   auto ahead = [&](const Slots& s, int k) {  // slots of tile e + k (k < every slot count)
     return Slots{wrap(s.q + k, NQ), wrap(s.d + k, NDO), wrap(s.ls + k, NLS), wrap(s.dl + k, NDL)};
   };
+  const bool copier = __builtin_amdgcn_readfirstlane(role) == 0;  // a P wave
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave), pair_u = wave_u & 3;
   auto load_tile = [&](uint32_t en, const Slots& sl) {  // en: the tile's list entry
+    if (!copier) return;
     const uint32_t q0 = entry_tile(en) * 64u;
-    if constexpr (!Q8) TL::load_async(rs_q, q0 * qrb, qoff, lds_addr(s_q[sl.q]), wave);
-    TL::load_async(rs_do, q0 * dorb, dooff, lds_addr(s_do[sl.d]), wave);
-    if constexpr (Q8) TQ8::load_async(rs_q8, q0 * uint32_t(D), q8off, lds_addr(s_q8[Q8 ? sl.d : 0]), wave);
-    if (wave == 4)
+    const int ln = lane_here();
+    const uint32_t lrow = TC::lane_row(pair_u, ln), c16 = TC::lane_chunk16(pair_u, ln);
+    if constexpr (!Q8) TC::load_async_rows(rs_q, q0 * qrb, lrow * qrb, c16, qrb, lds_addr(s_q[sl.q]), pair_u);
+    TC::load_async_rows(rs_do, q0 * dorb, lrow * dorb, c16, dorb, lds_addr(s_do[sl.d]), pair_u);
+    if constexpr (Q8)
+      TC8::load_async_rows(rs_q8, q0 * uint32_t(D), TC8::lane_row(pair_u, ln) * uint32_t(D),
+                           TC8::lane_chunk16(pair_u, ln), uint32_t(D), lds_addr(s_q8[Q8 ? sl.d : 0]), pair_u);
+    if (wave_u == 1)
       dma_b32(rs_lse, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_lse[sl.ls][0])))));
-    else if (wave == 5)
+    else if (wave_u == 2)
       dma_b32(rs_dl, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_delta[sl.dl][0])))));
-    else if (wave == 6)
+    else if (wave_u == 3)
       dma_b32(rs_codes, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_qc[sl.ls][0])))));
   };
   // fp8: the 16-bit Q tile of tile e (the dK product's operand in step e + 1)
   auto load_q16 = [&](uint32_t en, const Slots& sl) {
+    if (!copier) return;
     const uint32_t q0 = entry_tile(en) * 64u;
-    TL::load_async(rs_q, q0 * qrb, qoff, lds_addr(s_q[sl.q]), wave);
+    const int ln = lane_here();
+    TC::load_async_rows(rs_q, q0 * qrb, TC::lane_row(pair_u, ln) * qrb, TC::lane_chunk16(pair_u, ln), qrb,
+                        lds_addr(s_q[sl.q]), pair_u);
   };
   // Wait until tile e's loads (and older ones) have landed while tile e+1's,
   // issued last, may still be in flight: vector memory loads retire in order.
-  // Waves 4, 5 and 6 issue one more load per tile (LSE, Delta, query codes).
-  // Only used with PD = 2, i.e. neither fp8 nor SP.
-  constexpr int NTL = 2 * NL;
+  // Waves 1, 2 and 3 issue one more load per tile (LSE, Delta, query codes);
+  // the dS waves issue none.  Only used with PD = 2, i.e. neither fp8 nor SP.
+  constexpr int NTL = 2 * TC::LOADS_PER_WAVE;
   auto wait_tile = [&](bool next_in_flight) {
-    if (!next_in_flight) wait_vmem();
-    else if (wave == 4 || wave == 5 || wave == 6) wait_vmem_n<NTL + 1>();
+    if (!next_in_flight || !copier) wait_vmem();
+    else if (wave_u != 0) wait_vmem_n<NTL + 1>();
     else wait_vmem_n<NTL>();
   };
 
@@ -679,11 +693,12 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
     __builtin_amdgcn_sched_barrier(0x406);
   };
 
-  // list entries e .. e + PD - 1 at the start of step e, carried in SGPRs:
-  // each step loads one entry (e + PD, for its tile copy) next to the copy,
-  // and the P waves' class of tile e is not re-read from memory inside the
-  // products, where a scalar load in flight would make every LDS wait there
-  // wait for all outstanding LDS reads (scalar loads complete out of order)
+  // list entries e .. e + PD - 1 at the start of step e, carried in SGPRs,
+  // and en_next = entry e + PD (the tile step e copies), loaded at the end of
+  // step e - 1: the P waves' class of tile e is not re-read from memory
+  // inside the products, where a scalar load in flight would make every LDS
+  // wait there wait for all outstanding LDS reads (scalar loads complete out
+  // of order)
   uint32_t pend[PD];
 #pragma unroll
   for (int i = 0; i < PD; ++i) pend[i] = i < n ? ent[i] : 0u;
@@ -701,22 +716,17 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   // waves): one register set for both roles
   f32x16 x[2] = {f32x16{}, f32x16{}};
 
+  uint32_t en_next = PD < n ? ent[PD] : 0u;
   for (int e = 0; e <= n; ++e) {
     // tiles up to e landed (tile e + PD - 1 may be in flight when PD = 2)
     wait_tile(PD == 2 && e + 1 < n);
     barrier_lds();  // tile e landed, P(e-1) written; P(e-2) and the slots of tile e+PD released
     uint32_t en = pend[0];  // entry of tile e (e < n)
     asm volatile("" : "+s"(en));
-    {
-      const uint32_t en_pd = e + PD < n ? ent[e + PD] : 0u;
-      if (e + PD < n) load_tile(en_pd, ahead(sl, PD));
+    const uint32_t en_pd = en_next;  // entry of tile e + PD (loaded in step e - 1)
 #pragma unroll
-      for (int i = 0; i + 1 < PD; ++i) pend[i] = pend[i + 1];
-      pend[PD - 1] = en_pd;
-    }
-    if constexpr (Q8) {
-      if (e < n) load_q16(en, sl);  // read by the dS waves in step e + 1
-    }
+    for (int i = 0; i + 1 < PD; ++i) pend[i] = pend[i + 1];
+    pend[PD - 1] = en_pd;
     const int pb = e & 1;
     if (role == 0) {
       if (e < n) {
@@ -758,7 +768,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
         const uint32_t mcls = entry_class(en, member);
         if (mcls != TILE_FULL) {  // wave-uniform
           const uint64_t colbits = mcls == TILE_PARTIAL  // EMPTY: nothing allowed
-                                       ? key_col_mask(kcode, krow, s_qc[sl.ls][lane], int(entry_tile(en)) * 64)
+                                       ? key_col_mask(kcode, krow, s_qc[sl.ls][lane_here()], int(entry_tile(en)) * 64)
                                        : 0u;
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
@@ -767,6 +777,11 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
             for (int r = 0; r < 16; ++r) x[qb][r] = mask_bit(x[qb][r], w, 16 * (r >> 3) + (r & 7));
           }
         }
+        // this step's copies, after S (P waves only): tile e + PD into the
+        // slots the barrier released, and for fp8 the 16-bit Q of tile e,
+        // which the dS waves read in step e + 1
+        if (e + PD < n) load_tile(en_pd, ahead(sl, PD));
+        if constexpr (Q8) load_q16(en, sl);
         u32x4 bop[2][2];                // packed P: B operand of k-step 2 qb + t
         u32x4 bopl[2][2];               // SP: its rounding residual (unused otherwise)
 #pragma unroll
@@ -848,6 +863,12 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
         rows_times_b(s_do[sl.d], x, true);
       }
     }
+    // the entry of the tile the next step copies, loaded by the P waves after
+    // their products (a scalar load in flight would make every LDS wait in
+    // them wait for all outstanding LDS reads; here it completes while the
+    // P waves wait at the barrier)
+    __builtin_amdgcn_sched_barrier(0);
+    if (copier) en_next = e + 1 + PD < n ? ent[e + 1 + PD] : 0u;
     sl = ahead(sl, 1);
   }
 

@@ -96,6 +96,28 @@ struct Tile {
 #pragma unroll
     for (int j = 0; j < LOADS_PER_WAVE; ++j) dma_b128(rs, off[j] + tile_off, m + uint32_t(j) * 1024u);
   }
+  // The same copy with two per-lane registers instead of LOADS_PER_WAVE.  The
+  // rows of a wave's load j are those of its load 0 plus j RPL.  The wave's
+  // first row, j RPL and the lane's row within a load (lane / CPR) occupy
+  // disjoint bits, and swz is an XOR of selected row bits, so the swizzle of
+  // load j's row splits into a per-lane part (in c16) and a constant per j:
+  //   source offset of load j = arow + j RPL row_bytes + (c16 ^ swz(j RPL) << 4)
+  // with arow = lane_row(wave, lane) * row_bytes, c16 = lane_chunk16(wave, lane).
+  // (Everything stays in the VGPR offset, which the buffer's range check
+  // covers, so rows past the end still read as zero.)
+  static constexpr int RPL = 64 / CPR;  // rows per wave-wide load
+  KD_DEV static uint32_t lane_row(int wave, int lane) { return uint32_t(wave * LOADS_PER_WAVE * RPL + lane / CPR); }
+  KD_DEV static uint32_t lane_chunk16(int wave, int lane) {
+    return uint32_t(((lane % CPR) ^ swz(lane / CPR) ^ swz(wave * LOADS_PER_WAVE * RPL)) << 4);
+  }
+  KD_DEV static void load_async_rows(const u32x4& rs, uint32_t tile_off, uint32_t arow, uint32_t c16,
+                                     uint32_t row_bytes, uint32_t lds_tile, int wave) {
+    const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_tile + uint32_t(wave * LOADS_PER_WAVE) * 1024u)));
+#pragma unroll
+    for (int j = 0; j < LOADS_PER_WAVE; ++j)
+      dma_b128(rs, arow + (tile_off + uint32_t(j * RPL) * row_bytes) + (c16 ^ uint32_t(swz(j * RPL) << 4)),
+               m + uint32_t(j) * 1024u);
+  }
   // Issue this wave's share of the tile load (asynchronous; vmcnt tracks it).
   KD_DEV static void load(__amdgpu_buffer_rsrc_t rs, uint32_t tile_off, const uint32_t (&off)[LOADS_PER_WAVE],
                           uint8_t* lds_tile, int wave) {
