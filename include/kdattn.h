@@ -22,7 +22,9 @@
  *     at D = 64, 128, 256 run on the MFMA kernels (dqk_signs at 64, 128 only);
  *     fp32 inputs (any D) and 16-bit inputs at D = 16, 32 run on fp32
  *     vector-ALU kernels (no fp8 scores, no dqk_signs there; precision is then
- *     always full fp32).
+ *     always full fp32).  (The Python layer runs fp32 inputs at precision
+ *     "tf32" and D <= 64 as bf16 operands of three times the head dim on the
+ *     MFMA kernels instead, with dq_lo / dk_lo / dv_lo below.)
  *   - LSE is stored in log2 units (LSE2 = log2 sum_j exp2(S_ij * sm_scale *
  *     log2 e)), as the reference stores it (original_kernel.py:603-604).
  *     Fully masked rows get O = 0, LSE = -inf and zero gradients.
@@ -118,6 +120,10 @@ typedef struct kd_attn_args {
                                    Q R, K R with R = diag(signs) H_D / sqrt(D) (kd_hadamard), and
                                    dQ, dK are returned for the unrotated Q, K, i.e. times R^T,
                                    applied in the kernels' epilogues; NULL: dQ, dK as computed */
+  void *dq_lo, *dk_lo, *dv_lo;  /* optional contiguous [B, H, T, D] of the 16-bit dtype (bwd): the
+                                   rounding residuals dQ_fp32 - dQ (etc.), so that dq + dq_lo carries
+                                   the gradient to ~16 significant bits (as o_lo does for O); NULL to
+                                   skip; not with dqk_signs or fp32 inputs */
   int32_t B, H, T, D;
   int32_t dtype;                /* KD_BF16 / KD_F16 / KD_F32 */
   float sm_scale;

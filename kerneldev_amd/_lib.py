@@ -54,6 +54,7 @@ class AttnArgs(ctypes.Structure):
         ("delta", c_void_p), ("o_lo", c_void_p),
         ("q8", c_void_p), ("k8", c_void_p), ("q_scale", c_void_p), ("k_scale", c_void_p),
         ("dqk_signs", c_void_p),
+        ("dq_lo", c_void_p), ("dk_lo", c_void_p), ("dv_lo", c_void_p),
         ("B", c_int32), ("H", c_int32), ("T", c_int32), ("D", c_int32),
         ("dtype", c_int32), ("sm_scale", c_float),
         ("precision", c_int32), ("pad_", c_int32),

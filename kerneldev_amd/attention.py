@@ -9,6 +9,9 @@ shim over the C ABI of ``libkdattn.so``:
 * ``kdattn::fwd``  -> plan (codes, tile map, work lists) + forward kernel,
   returns ``(O, LSE2, plan)``; the plan is saved for the backward.
 * ``kdattn::bwd``  -> Delta, dQ and dK/dV kernels from the saved plan.
+* ``kdattn::fwd_x3`` / ``kdattn::bwd_x3`` -> the same kernels for fp32 inputs
+  at precision "tf32" and head dims up to 64, as three bf16 products per
+  product (see X3_HEAD_DIMS).
 
 There is no CPU or PyTorch fallback: a missing library raises.
 """
@@ -24,9 +27,10 @@ from ._lib import AttnArgs, MetaArgs
 
 REFERENCE_HEAD_DIMS = (16, 32, 64, 128, 256)  # original_kernel.py:1720
 SUPPORTED_HEAD_DIMS = REFERENCE_HEAD_DIMS
-# bf16 / fp16 at these head dims run on the MFMA kernels (fused Hadamard
-# epilogues, fp8 scores at 128); fp32 inputs and the other head dims run on
-# the fp32 vector-ALU kernels (kd_simt.hip)
+# bf16 / fp16 at these head dims run on the MFMA kernels with the fused
+# Hadamard epilogues (fp8 scores at 128); 256 runs there without them.  fp32
+# inputs run on the fp32 vector-ALU kernels (kd_simt.hip), except at precision
+# "tf32" and head dims up to 64 (X3_HEAD_DIMS)
 MFMA_HEAD_DIMS = (64, 128)
 # 16-bit inputs with these head dims run on the d = 64 MFMA kernels, zero-
 # padded: zero columns change no score (S = Q K^T), O's extra columns are
@@ -319,6 +323,123 @@ def _backward(ctx, do, dlse, dplan, do_lo, *_unused):
 _fwd_op.register_autograd(_backward, setup_context=_setup_context)
 
 
+# ---------------------------------------------- fp32 inputs on the MFMA kernels
+# For fp32 inputs at precision "tf32" (the reference's default) and head dims
+# up to 64, every product runs as three bf16 products on the MFMA kernels, on
+# operands of three times the head dim (zero-padded to a built one):
+#   Q' = [Qh, Qh, Ql], K' = [Kh, Kl, Kh]    Q' K'^T = Qh Kh^T + Qh Kl^T + Ql Kh^T
+#   V' = [Vh, Vl, Vh], dO' = [dOh, dOh, dOl] dP = dO' V'^T likewise; O = P V' in
+#                                            columns [0, d) plus [d, 2d)
+# with xh = bf16(x), xl = bf16(x - xh): each operand to ~16 significant bits,
+# and only the xl yl terms (~2^-16 relative) dropped -- more than the
+# reference's tf32 dots (10-bit mantissas, original_kernel.py:452, :1239,
+# :1331-1333, :1425, :1517-1523).  P and dS are split by the kernels as for
+# 16-bit inputs.  O and the gradients come back with their rounding residuals
+# (o_lo, dq_lo, dk_lo, dv_lo), so they too carry ~16 bits.  The gradients of
+# the copies that hold xh are the gradient of x (straight through the split):
+# dQ = dQ'[0, d) + dQ'[d, 2d), dK = dK'[0, d) + dK'[2d, 3d), dV likewise.
+X3_HEAD_DIMS = {16: 64, 32: 128, 64: 256}
+
+
+def _x3(x: torch.Tensor, pattern: str, Dp: int) -> torch.Tensor:
+    """[B, H, T, d] fp32 -> contiguous bf16 [B, H, T, Dp]: the parts named by pattern ('h', 'l'), then zeros."""
+    xh = x.to(torch.bfloat16)
+    xl = (x - xh.to(torch.float32)).to(torch.bfloat16)
+    parts = [xh if c == "h" else xl for c in pattern]
+    pad = Dp - len(pattern) * x.shape[-1]
+    if pad:
+        parts.append(xh.new_zeros(x.shape[:-1] + (pad,)))
+    return torch.cat(parts, dim=-1)
+
+
+def _hi_lo(hi: torch.Tensor, lo: torch.Tensor, d: int, second: int) -> torch.Tensor:
+    """fp32 (hi + lo)[..., 0:d] + (hi + lo)[..., second * d:(second + 1) * d]."""
+    x = hi.to(torch.float32).add_(lo.to(torch.float32))
+    return x[..., :d] + x[..., second * d:(second + 1) * d]
+
+
+@torch.library.custom_op("kdattn::fwd_x3", mutates_args=(), device_types=("cuda",))
+def _fwd_x3_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tensor | None,
+               in_span: torch.Tensor | None, span_id: torch.Tensor | None,
+               is_prefix: torch.Tensor | None, sm_scale: float, mode: int,
+               bthd: bool = False, plan_in: torch.Tensor | None = None,
+               ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    B, H, T, d = q.shape
+    Dp = X3_HEAD_DIMS[d]
+    qx, kx, vx = _x3(q, "hhl", Dp), _x3(k, "hlh", Dp), _x3(v, "hlh", Dp)
+    plan = plan_in if plan_in is not None else build_plan(B, T, Dp, q.device, mode, in_span, span_id, is_prefix, lens)
+    ox = torch.empty((B, H, T, Dp), dtype=torch.bfloat16, device=q.device)
+    ox_lo = torch.empty_like(ox)
+    lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+    a = _attn_args(qx, kx, vx, sm_scale, _lib.KD_PREC_SPLIT)
+    a.o, a.o_strides = ox.data_ptr(), _strides3(ox)
+    a.lse = lse.data_ptr()
+    a.o_lo = ox_lo.data_ptr()
+    _lib.check(_lib.load().kd_attn_fwd(ctypes.byref(a), _ptr(plan), _stream(q.device)), "kd_attn_fwd")
+    o = _new_out(B, H, T, d, q, bthd)
+    o.copy_(_hi_lo(ox, ox_lo, d, 1))
+    return o, lse, (plan if plan_in is None else plan.new_empty(0))
+
+
+@_fwd_x3_op.register_fake
+def _fwd_x3_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, bthd=False, plan_in=None):
+    B, H, T, d = q.shape
+    return (_new_out(B, H, T, d, q, bthd),
+            torch.empty((B, H, T), dtype=torch.float32, device=q.device),
+            torch.empty(_lib.plan_nbytes(B, T, X3_HEAD_DIMS[int(d)]) if plan_in is None else 0, dtype=torch.uint8,
+                        device=q.device))
+
+
+@torch.library.custom_op("kdattn::bwd_x3", mutates_args=(), device_types=("cuda",))
+def _bwd_x3_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, lse: torch.Tensor,
+               do: torch.Tensor, plan: torch.Tensor, sm_scale: float,
+               ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    B, H, T, d = q.shape
+    Dp = X3_HEAD_DIMS[d]
+    qx, kx, vx, dox = _x3(q, "hhl", Dp), _x3(k, "hlh", Dp), _x3(v, "hlh", Dp), _x3(do, "hhl", Dp)
+    # the workspace of kd_attn_bwd_dq / kd_attn_bwd_dkdv (kd_attn_args.delta):
+    # -Delta with Delta = rowsum(dO O) in fp32, then -LSE / c (-inf where LSE is)
+    ws = torch.empty((2, B, H, T), dtype=torch.float32, device=q.device)
+    torch.sum(do.to(torch.float32) * o.to(torch.float32), dim=-1, out=ws[0]).neg_()
+    c = torch.tensor(sm_scale, dtype=torch.float32) * torch.tensor(LOG2E, dtype=torch.float32)
+    ninf = torch.full_like(lse, -math.inf)
+    torch.where(lse == -math.inf, ninf, lse * (-(1.0 / c)).to(q.device), out=ws[1])
+    outs = [torch.empty((B, H, T, Dp), dtype=torch.bfloat16, device=q.device) for _ in range(6)]
+    dqx, dkx, dvx, dq_lo, dk_lo, dv_lo = outs
+    a = _attn_args(qx, kx, vx, sm_scale, _lib.KD_PREC_SPLIT)
+    a.lse = lse.data_ptr()
+    a.dout, a.do_strides = dox.data_ptr(), _strides3(dox)
+    a.dq, a.dk, a.dv = dqx.data_ptr(), dkx.data_ptr(), dvx.data_ptr()
+    a.dq_strides, a.dk_strides, a.dv_strides = _strides3(dqx), _strides3(dkx), _strides3(dvx)
+    a.dq_lo, a.dk_lo, a.dv_lo = dq_lo.data_ptr(), dk_lo.data_ptr(), dv_lo.data_ptr()
+    a.delta = ws.data_ptr()
+    lib, st = _lib.load(), _stream(q.device)
+    _lib.check(lib.kd_attn_bwd_dq(ctypes.byref(a), _ptr(plan), st), "kd_attn_bwd_dq")
+    _lib.check(lib.kd_attn_bwd_dkdv(ctypes.byref(a), _ptr(plan), st), "kd_attn_bwd_dkdv")
+    return _hi_lo(dqx, dq_lo, d, 1), _hi_lo(dkx, dk_lo, d, 2), _hi_lo(dvx, dv_lo, d, 2)
+
+
+@_bwd_x3_op.register_fake
+def _bwd_x3_fake(q, k, v, o, lse, do, plan, sm_scale):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def _setup_context_x3(ctx, inputs, output):
+    q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, bthd, plan_in = inputs
+    o, lse, plan = output
+    ctx.save_for_backward(q, k, v, o, lse, plan_in if plan_in is not None else plan)
+    ctx.sm_scale = sm_scale
+
+
+def _backward_x3(ctx, do, dlse, dplan):
+    q, k, v, o, lse, plan = ctx.saved_tensors
+    dq, dk, dv = _bwd_x3_op(q, k, v, o, lse, do, plan, ctx.sm_scale)
+    return (dq, dk, dv) + (None,) * 8
+
+
+_fwd_x3_op.register_autograd(_backward_x3, setup_context=_setup_context_x3)
+
+
 # -------------------------------------------------------------- public entry
 def _check_meta(name, t, B, T, device, dtypes):
     if t is None:
@@ -453,13 +574,18 @@ def flash_attention(
         (q8, q_scale), (k8, k_scale) = quantize_fp8(q), quantize_fp8(k)
         fp8 = (q8, k8, q_scale, k_scale)
 
-    # O's rounding residual, kept for the backward's Delta (16-bit O only)
-    need_lo = (q.dtype != torch.float32 and torch.is_grad_enabled()
-               and any(x.requires_grad for x in (q, k, v)))
-    o, lse, plan_t, *_ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode), need_lo,
-                                 *(fp8 or (None, None, None, None)), bthd=out_layout == "bthd",
-                                 plan_in=None if plan is None else plan.tensor, signs=fused_signs,
-                                 quant_fp8=hadamard and qk_dtype == "fp8_e4m3", prec=PRECISIONS[precision])
+    if q.dtype == torch.float32 and precision == "tf32" and D in X3_HEAD_DIMS:
+        # fp32 at the reference's default precision: bf16x3 on the MFMA kernels
+        o, lse, plan_t = _fwd_x3_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode),
+                                    bthd=out_layout == "bthd", plan_in=None if plan is None else plan.tensor)
+    else:
+        # O's rounding residual, kept for the backward's Delta (16-bit O only)
+        need_lo = (q.dtype != torch.float32 and torch.is_grad_enabled()
+                   and any(x.requires_grad for x in (q, k, v)))
+        o, lse, plan_t, *_ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode),
+                                     need_lo, *(fp8 or (None, None, None, None)), bthd=out_layout == "bthd",
+                                     plan_in=None if plan is None else plan.tensor, signs=fused_signs,
+                                     quant_fp8=hadamard and qk_dtype == "fp8_e4m3", prec=PRECISIONS[precision])
     if plan is not None:
         plan_t = plan.tensor
     if pad_to:

@@ -93,16 +93,24 @@ __global__ __launch_bounds__(256) void k_delta(AttnArgs a) {
   }
 }
 
+// A transposed accumulator's rows times scale, as the 16-bit type; with glo
+// also each value's rounding residual at the same offsets of glo (the
+// caller's contiguous residual row), so that g + glo carries the fp32 value to
+// about twice the type's significant bits
 template <class E, int D>
-KD_DEV void store_rows_T(uint16_t* g, const f32x16 (&acc)[D / 32], float scale, int hf) {
+KD_DEV void store_rows_T(uint16_t* g, const f32x16 (&acc)[D / 32], float scale, int hf, uint16_t* glo = nullptr) {
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
     for (int gg = 0; gg < 4; ++gg) {
       const int d0 = 32 * db + 8 * gg + 4 * hf;
-      u32x2 w = {pack2<E>(acc[db][4 * gg] * scale, acc[db][4 * gg + 1] * scale),
-                 pack2<E>(acc[db][4 * gg + 2] * scale, acc[db][4 * gg + 3] * scale)};
+      const float f[4] = {acc[db][4 * gg] * scale, acc[db][4 * gg + 1] * scale, acc[db][4 * gg + 2] * scale,
+                          acc[db][4 * gg + 3] * scale};
+      const u32x2 w = {pack2<E>(f[0], f[1]), pack2<E>(f[2], f[3])};
       *reinterpret_cast<u32x2*>(g + d0) = w;
+      if (glo != nullptr)
+        *reinterpret_cast<u32x2*>(glo + d0) = u32x2{pack2_residual<E>(f[0], f[1], w[0]),
+                                                    pack2_residual<E>(f[2], f[3], w[1])};
     }
   }
 }
@@ -452,11 +460,13 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
 
   if (qvalid) {
     uint16_t* g = static_cast<uint16_t*>(a.dq) + b * a.dq_strides[0] + h * a.dq_strides[1] + qrow * a.dq_strides[2];
+    uint16_t* glo = a.dq_lo == nullptr ? nullptr
+                                       : static_cast<uint16_t*>(a.dq_lo) + ((int64_t(b) * a.H + h) * a.T + qrow) * D;
     if constexpr (DH == D) {
       if (a.dqk_signs != nullptr) store_rows_T_unrot<E, D>(g, acc, a.sm_scale, hf, a.dqk_signs);
-      else store_rows_T<E, D>(g, acc, a.sm_scale, hf);
-    } else {
-      store_rows_T<E, DH>(g + D0, acc, a.sm_scale, hf);  // (no dqk_signs at split widths)
+      else store_rows_T<E, D>(g, acc, a.sm_scale, hf, glo);
+    } else {  // (no dqk_signs at split widths)
+      store_rows_T<E, DH>(g + D0, acc, a.sm_scale, hf, glo == nullptr ? nullptr : glo + D0);
     }
   }
 }
@@ -876,10 +886,12 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
     uint16_t* g = role == 0
         ? static_cast<uint16_t*>(a.dv) + b * a.dv_strides[0] + h * a.dv_strides[1] + krow * a.dv_strides[2]
         : static_cast<uint16_t*>(a.dk) + b * a.dk_strides[0] + h * a.dk_strides[1] + krow * a.dk_strides[2];
+    void* lo = role == 0 ? a.dv_lo : a.dk_lo;
+    uint16_t* glo = lo == nullptr ? nullptr : static_cast<uint16_t*>(lo) + ((int64_t(b) * H + h) * T + krow) * D;
     if (__builtin_amdgcn_readfirstlane(role) == 1 && a.dqk_signs != nullptr)  // dK, rotated back
       store_rows_T_unrot<E, D>(g, acc, a.sm_scale, hf, a.dqk_signs);
     else
-      store_rows_T<E, D>(g, acc, role == 0 ? 1.f : a.sm_scale, hf);
+      store_rows_T<E, D>(g, acc, role == 0 ? 1.f : a.sm_scale, hf, glo);
   }
 }
 
@@ -1100,12 +1112,15 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
   if (kvalid) {
     uint16_t* gv = static_cast<uint16_t*>(a.dv) + b * a.dv_strides[0] + h * a.dv_strides[1] + krow * a.dv_strides[2];
     uint16_t* gk = static_cast<uint16_t*>(a.dk) + b * a.dk_strides[0] + h * a.dk_strides[1] + krow * a.dk_strides[2];
-    store_rows_T<E, DH>(gv + D0, acc_v, 1.f, hf);
+    const int64_t lo_row = ((int64_t(b) * a.H + h) * a.T + krow) * D + D0;
+    uint16_t* gv_lo = a.dv_lo == nullptr ? nullptr : static_cast<uint16_t*>(a.dv_lo) + lo_row;
+    uint16_t* gk_lo = a.dk_lo == nullptr ? nullptr : static_cast<uint16_t*>(a.dk_lo) + lo_row;
+    store_rows_T<E, DH>(gv + D0, acc_v, 1.f, hf, gv_lo);
     if constexpr (DH == D) {  // all columns here: dK can be rotated back (dqk_signs)
       if (a.dqk_signs != nullptr) store_rows_T_unrot<E, D>(gk, acc_k, a.sm_scale, hf, a.dqk_signs);
-      else store_rows_T<E, D>(gk, acc_k, a.sm_scale, hf);
+      else store_rows_T<E, D>(gk, acc_k, a.sm_scale, hf, gk_lo);
     } else {
-      store_rows_T<E, DH>(gk + D0, acc_k, a.sm_scale, hf);  // (no dqk_signs at split widths)
+      store_rows_T<E, DH>(gk + D0, acc_k, a.sm_scale, hf, gk_lo);  // (no dqk_signs at split widths)
     }
   }
 }

@@ -97,7 +97,7 @@ int check_span(const kd_span_args* a) {
 
 extern "C" {
 
-int kd_version(void) { return 204; }
+int kd_version(void) { return 205; }
 
 const char* kd_last_error_string(void) { return g_err.c_str(); }
 
@@ -261,6 +261,13 @@ static int check_bwd(const kd_attn_args* a, const void* plan) {
   if ((r = check_fp8(a))) return r;
   if (plan == nullptr) return fail(KD_ERR_INVALID, "plan is NULL");
   if (a->lse == nullptr || a->delta == nullptr) return fail(KD_ERR_INVALID, "lse and delta are required");
+  if (a->dq_lo != nullptr || a->dk_lo != nullptr || a->dv_lo != nullptr) {
+    if (kd::use_simt(*a) || a->dqk_signs != nullptr)
+      return fail(KD_ERR_UNSUPPORTED, "dq_lo / dk_lo / dv_lo are built for bf16 / fp16 at head dim 64, 128 or 256, "
+                                      "without dqk_signs");
+    for (const void* p : {a->dq_lo, a->dk_lo, a->dv_lo})
+      if (p != nullptr && !aligned16(p)) return fail(KD_ERR_INVALID, "dq_lo, dk_lo and dv_lo must be 16-byte aligned");
+  }
   if ((r = check_tensor(a->q, a->q_strides, "q", a->T, a->D, esz(a))) || (r = check_tensor(a->k, a->k_strides, "k", a->T, a->D, esz(a))) ||
       (r = check_tensor(a->v, a->v_strides, "v", a->T, a->D, esz(a))) || (r = check_tensor(a->dout, a->do_strides, "dout", a->T, a->D, esz(a))))
     return r;

@@ -85,6 +85,14 @@ def test_bad_arguments_return_status_without_gpu():
     a.q_strides[:] = [1024, 1024, 128]
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_INVALID  # no scales
     assert "scale" in lib.kd_last_error_string().decode()
+    b = _lib.AttnArgs()  # the backward's rounding-residual outputs: 16-bit MFMA paths only, aligned
+    b.B, b.H, b.T, b.D, b.dtype, b.sm_scale = 1, 1, 16, 64, _lib.KD_F32, 0.125
+    b.lse, b.delta, b.dq_lo = 64, 64, 64
+    assert lib.kd_attn_bwd(ctypes.byref(b), ctypes.c_void_p(256), null) == _lib.KD_ERR_UNSUPPORTED
+    assert "dq_lo" in lib.kd_last_error_string().decode()
+    b.dtype, b.dq_lo, b.dv_lo = _lib.KD_BF16, None, 72
+    assert lib.kd_attn_bwd(ctypes.byref(b), ctypes.c_void_p(256), null) == _lib.KD_ERR_INVALID
+    assert "aligned" in lib.kd_last_error_string().decode()
     r = _lib.RotArgs()
     r.B, r.H, r.T, r.D, r.dtype = 1, 1, 4, 48, _lib.KD_BF16
     assert lib.kd_hadamard(ctypes.byref(r), null) == _lib.KD_ERR_UNSUPPORTED  # not a power of two

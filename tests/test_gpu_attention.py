@@ -202,6 +202,68 @@ def test_fp32_inputs_every_head_dim(dev, D):
     assert _rel_rms_fp64(got["lse"].cpu()[fin], ref["lse"][fin]) <= 1e-5
 
 
+def _check_fp32(got, ref, bar, what):
+    for key in ("o", "dq", "dk", "dv"):
+        assert got[key].dtype == torch.float32
+        rel = _rel_rms_fp64(got[key], ref[key])
+        print(f"  {what} {key}: rel-RMS {rel:.3e} (bar {bar:g})")
+        assert rel <= bar, f"{key}: {rel:.3e}"
+    fin = torch.isfinite(ref["lse"])
+    assert torch.equal(torch.isfinite(got["lse"].cpu()), fin)
+    assert _rel_rms_fp64(got["lse"].cpu()[fin], ref["lse"][fin]) <= bar
+
+
+@pytest.mark.parametrize("D", [16, 32, 64])
+@pytest.mark.parametrize("causal_only", [True, False])
+def test_fp32_tf32_on_the_mfma_kernels(dev, D, causal_only):
+    """fp32 inputs at precision "tf32" and d <= 64 run as three bf16 products per
+    product on the MFMA kernels (kdattn::fwd_x3 / bwd_x3): rel-RMS <= 1e-4
+    against the fp64 oracle, ten times inside tf32's 10-bit mantissa (measured
+    6e-6 to 9e-6)."""
+    inp = _other_dims_case(D, causal_only, seed=80 + D)
+    inp = {k_: (v_.float() if torch.is_tensor(v_) and v_.is_floating_point() else v_) for k_, v_ in inp.items()}
+    print(f"fp32 tf32 bf16x3 D={D} {inp['name']}", flush=True)
+    got = run_gpu(inp, dev, precision="tf32")
+    _check_fp32(got, _reference(inp), 1e-4, f"tf32 D={D}")
+
+
+def test_fp32_tf32_ops_directly(dev):
+    """The bf16x3 ops themselves, with the plan they build, against the oracle (and the
+    forward's LSE equal to what flash_attention returns for the same call)."""
+    from kerneldev_amd.attention import _bwd_x3_op, _fwd_x3_op
+    from kerneldev_amd import _lib
+
+    inp = _other_dims_case(64, False, seed=91)
+    inp = {k_: (v_.float() if torch.is_tensor(v_) and v_.is_floating_point() else v_) for k_, v_ in inp.items()}
+    q, k, v, do = (inp[x].to(dev) for x in ("q", "k", "v", "do"))
+    meta = [inp[n].to(dev) for n in ("in_span", "span_id", "is_prefix")]
+    o, lse, plan = _fwd_x3_op(q, k, v, None, *meta, 64 ** -0.5, _lib.KD_MODE_FORMULA)
+    dq, dk, dv = _bwd_x3_op(q, k, v, o, lse, do, plan, 64 ** -0.5)
+    torch.cuda.synchronize()
+    _check_fp32({"o": o, "lse": lse, "dq": dq, "dk": dk, "dv": dv}, _reference(inp), 1e-4, "ops")
+    assert torch.equal(run_gpu(inp, dev)["lse"], lse)
+
+
+def test_fp32_tf32_lens_hadamard_and_bthd(dev):
+    """The bf16x3 path with lens (fully masked rows: O = 0, LSE = -inf, zero
+    gradients), with the Hadamard rotation, and with out_layout="bthd"."""
+    q, k, v, do = qkvdo(3, 2, 300, 64, seed=12, dtype=torch.float32)
+    lens = torch.tensor([300, 129, 0], dtype=torch.int32)
+    inp = dict(name="lens fp32", q=q, k=k, v=v, do=do, causal=True)
+    got = run_gpu(inp, dev, lens=lens, precision="tf32")
+    _check_fp32(got, _reference(inp, lens=lens), 1e-4, "lens")
+    assert (got["o"][1, :, 129:] == 0).all() and (got["o"][2] == 0).all()
+    assert torch.isinf(got["lse"][2]).all() and (got["lse"][2] < 0).all()
+    assert (got["dq"][2] == 0).all() and (got["dk"][2] == 0).all() and (got["dv"][2] == 0).all()
+    inp = _other_dims_case(64, False, seed=93)
+    inp = {k_: (v_.float() if torch.is_tensor(v_) and v_.is_floating_point() else v_) for k_, v_ in inp.items()}
+    got = run_gpu(inp, dev, precision="tf32", hadamard=True, hadamard_seed=3)
+    _check_fp32(got, _reference(inp, hadamard=True, hadamard_seed=3), 1e-4, "hadamard")
+    got = run_gpu(inp, dev, precision="tf32", out_layout="bthd")
+    assert got["o"].transpose(1, 2).is_contiguous()
+    _check_fp32(got, _reference(inp), 1e-4, "bthd")
+
+
 def test_fp16(dev):
     tokens, in_span, span_id, is_prefix = cocktail_batch(2, 512, CONFIG3_LAYOUT, seed=6)
     q, k, v, do = qkvdo(2, 2, 512, 64, seed=7, dtype=torch.float16)

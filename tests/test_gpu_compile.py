@@ -2,7 +2,8 @@
 runs its op inside torch.compile(fullgraph=True, dynamic=True), with fake
 implementations at :1781-1803 and :1901-1923).
 
-* torch.library.opcheck on kdattn::fwd, kdattn::bwd, kdattn::rot and kdattn::quant:
+* torch.library.opcheck on kdattn::fwd, kdattn::bwd, kdattn::fwd_x3, kdattn::bwd_x3,
+  kdattn::rot and kdattn::quant:
   schema, autograd registration, fake kernels against the real outputs, and
   AOT dispatch with dynamic shapes.
 * flash_attention under torch.compile(fullgraph=True), static and dynamic
@@ -12,7 +13,7 @@ import pytest
 import torch
 
 from kerneldev_amd import flash_attention, generate_hadamard_signs
-from kerneldev_amd.attention import _bwd_op, _fwd_op, _lib
+from kerneldev_amd.attention import _bwd_op, _bwd_x3_op, _fwd_op, _fwd_x3_op, _lib
 from kerneldev_amd.hadamard import _quant_op, _rot_op
 from kerneldev_amd.synth import CONFIG3_LAYOUT, cocktail_batch, qkvdo
 
@@ -37,6 +38,18 @@ def test_opcheck_forward_and_backward_ops(dev):
     torch.library.opcheck(_bwd_op, (q, k, v, o, lse, do, plan, sc, o_lo))
 
 
+def test_opcheck_fp32_bf16x3_ops(dev):
+    q, k, v, do, meta = _inputs(dev)
+    q, k, v, do = (x.float() for x in (q, k, v, do))
+    sc = q.shape[-1] ** -0.5
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
+    print("opcheck kdattn::fwd_x3", flush=True)
+    torch.library.opcheck(_fwd_x3_op, (qg, kg, vg, None, *meta, sc, _lib.KD_MODE_FORMULA))
+    o, lse, plan = _fwd_x3_op(q, k, v, None, *meta, sc, _lib.KD_MODE_FORMULA)
+    print("opcheck kdattn::bwd_x3", flush=True)
+    torch.library.opcheck(_bwd_x3_op, (q, k, v, o, lse, do, plan, sc))
+
+
 def test_opcheck_rotation_and_quantiser_ops(dev):
     q, *_ = _inputs(dev, D=128)
     signs = generate_hadamard_signs(128, 3, device=dev)
@@ -55,8 +68,9 @@ def _fwd_bwd(fn, q, k, v, do, meta):
     return o.detach(), lse.detach(), qg.grad, kg.grad, vg.grad
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("dynamic", [False, True])
-def test_compiled_flash_attention_matches_eager(dev, dynamic):
+def test_compiled_flash_attention_matches_eager(dev, dynamic, dtype):
     def attn(q, k, v, in_span, span_id, is_prefix):
         return flash_attention(q, k, v, in_span=in_span, span_id=span_id, is_prefix=is_prefix, return_lse=True)
 
@@ -64,7 +78,8 @@ def test_compiled_flash_attention_matches_eager(dev, dynamic):
     compiled = torch.compile(attn, fullgraph=True, dynamic=dynamic)
     for T in (320, 200):  # a second length re-uses (dynamic) or re-traces (static) the graph
         q, k, v, do, meta = _inputs(dev, T=T)
-        print(f"torch.compile dynamic={dynamic} T={T}", flush=True)
+        q, k, v, do = (x.to(dtype) for x in (q, k, v, do))
+        print(f"torch.compile dynamic={dynamic} {dtype} T={T}", flush=True)
         want = _fwd_bwd(attn, q, k, v, do, meta)
         got = _fwd_bwd(compiled, q, k, v, do, meta)
         for name, x, y in zip(("o", "lse", "dq", "dk", "dv"), got, want):
