@@ -55,8 +55,8 @@ USEFUL_FWD, USEFUL_BWD = 4, 10
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs scaled by a 1 GiB copy's counts
 # (profiles/attn_config4_{bf16,fp8_e4m3}_hbm_traffic.md); re-measured whenever the kernels change.
 CONFIG4_TRAFFIC_BYTES = {
-    "bf16": {"fwd": 1142.8e6, "dq": 1492.7e6, "dkdv": 1093.4e6},
-    "fp8_e4m3": {"fwd": 831.5e6, "dq": 1610.4e6, "dkdv": 1202.3e6},
+    "bf16": {"fwd": 1145.0e6, "dq": 1496.9e6, "dkdv": 1093.9e6},
+    "fp8_e4m3": {"fwd": 832.2e6, "dq": 1608.8e6, "dkdv": 1204.8e6},
 }
 
 
