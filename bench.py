@@ -19,7 +19,8 @@ the forward and 10*d for the backward (``nnz`` is popcounted from the device
 tile map, whose bit-exactness the GPU tests check).  The roofline object
 reports the dominant kernel against MI355X's dense bf16 MFMA peak, and the
 CPU baseline is the eager dense-masked SDPA of the oracle, timed on a bounded
-sample of the same workload on this host's cores.
+sample of the same workload on this host's cores.  A vendor bf16 GEMM timed
+last (``gemm_ceiling``) shows the MFMA rate this GPU sustains under load.
 
 Prints ONE JSON line (rank 0).
 """
@@ -50,6 +51,13 @@ KERNEL_FLOPS_PER_ENTRY = {
     "dkdv": 8,  # S recompute, dP recompute, dV += P^T dO, dK += dS^T Q
 }
 USEFUL_FWD, USEFUL_BWD = 4, 10
+# MFMA work the kernels issue per allowed entry and head-dim unit: with split
+# precision (the default) the products that take P or dS run twice, on its
+# bf16 hi and lo halves; with the single rounding once (= the algorithmic work)
+KERNEL_MFMA_PER_ENTRY = {
+    "split": {"fwd": 6, "dq": 8, "dkdv": 12},
+    "single": dict(KERNEL_FLOPS_PER_ENTRY),
+}
 
 # HBM bytes per launch of the attention kernels on config 4 (Hadamard on), from
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs scaled by a 1 GiB copy's counts
@@ -85,6 +93,8 @@ def parse():
                     help="skip the CPU baseline leg (profiling runs)")
     ap.add_argument("--cpu-seconds", type=float, default=25.0,
                     help="CPU time bound of the baseline (it stops after the head that crosses it)")
+    ap.add_argument("--no-gemm-ceiling", action="store_true",
+                    help="skip the vendor bf16 GEMM timed after the attention runs")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one device-to-device copy of this many MiB before timing, as the "
                          "known-size reference for HBM traffic counters")
@@ -104,6 +114,30 @@ def step_blended_peak() -> float:
     recomputations are not counted, as in ``value``)."""
     useful = USEFUL_FWD + USEFUL_BWD
     return useful / (6 / PEAK_FP8_TFLOPS + (useful - 6) / PEAK_BF16_TFLOPS)
+
+
+def gemm_ceiling(torch, dev, iters: int = 30):
+    """A large bf16 GEMM through torch.matmul (hipBLASLt) on the same GPU, timed
+    with events: the MFMA rate a vendor-tuned kernel sustains at the clock the
+    chip holds under dense MFMA load.  Reported beside the published peak the
+    roofline is quoted against; it is no part of the attention step."""
+    m, n, k = 8192, 8192, 16384
+    a = torch.randn(m, k, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(k, n, device=dev, dtype=torch.bfloat16)
+    for _ in range(10):
+        c = a @ b
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(iters):
+        c = a @ b
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    del a, b, c
+    tflops = 2 * m * n * k / (ms * 1e-3) / 1e12
+    return {"value": round(tflops, 1), "unit": "TFLOP/s", "op": f"torch.matmul bf16 {m}x{n}x{k}",
+            "ms": round(ms, 4), "frac_of_bf16_peak": round(tflops / PEAK_BF16_TFLOPS, 4)}
 
 
 def measure(torch, st, steps: int, warmup: int):
@@ -372,6 +406,12 @@ def main():
                 "algorithmic_tflop_per_launch": round(dom_flops / 1e12, 4)}
     kernel_tflops = {n: round(KERNEL_FLOPS_PER_ENTRY[n] * D * H * nnz / (per_kernel[n] * 1e-3) / 1e12, 1)
                      for n in ("fwd", "dq", "dkdv")}
+    # the MFMA work each kernel issues on allowed entries (bf16 Q K^T runs only)
+    mfma_tflops = None
+    if not fp8:
+        work = KERNEL_MFMA_PER_ENTRY["single" if args.precision == "bf16" else "split"]
+        mfma_tflops = {n: round(work[n] * D * H * nnz / (per_kernel[n] * 1e-3) / 1e12, 1)
+                       for n in ("fwd", "dq", "dkdv")}
 
     # config 4's second run (BASELINE: "once in bf16 and once with fp8 e4m3
     # QK^T"), timed in the same invocation and reported beside the bf16 line
@@ -414,6 +454,14 @@ def main():
             "note": "P and dS rounded once (the reference's numerics); misses the per-element bar on config 4",
         }
 
+    gemm = None
+    if not args.no_gemm_ceiling:
+        torch.cuda.empty_cache()
+        gemm = gemm_ceiling(torch, dev)
+        gemm["frac_of_it_headline"] = round(value / gemm["value"], 4)
+        if mfma_tflops is not None:
+            gemm["frac_of_it_dominant_kernel_mfma_work"] = round(mfma_tflops[dom] / gemm["value"], 4)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(inp, args.cpu_seconds)
@@ -444,6 +492,7 @@ def main():
             "fwd_ms": round(sum(x for n, x in per_kernel.items() if n not in ("dq", "dkdv")), 4),
             "bwd_ms": round(per_kernel["dq"] + per_kernel["dkdv"], 4),
             "kernel_algorithmic_tflops": kernel_tflops,
+            "kernel_mfma_work_tflops": mfma_tflops,
             "event_ms_per_step": round(event_ms, 4),
             "hadamard": hadamard,
             "qk_dtype": args.qk_dtype,
@@ -452,6 +501,7 @@ def main():
         "roofline": roofline,
         "fp8_run": fp8_run,
         "single_rounding_run": single_run,
+        "gemm_ceiling": gemm,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
