@@ -58,11 +58,6 @@ int check_common(const kd_attn_args* a) {
   if (a->T > (1 << 24) - 2) return fail(KD_ERR_UNSUPPORTED, "T must be < 2^24 - 1");
   if (int64_t(a->B) * a->H * ((a->T + 63) / 64) > (int64_t(1) << 31) - 1)
     return fail(KD_ERR_UNSUPPORTED, "B * H * ceil(T / 64) exceeds the grid limit");
-  // the kernels copy tile masks through a buffer resource over one batch
-  // row's masks: ceil(T / 64)^2 tiles of 512 bytes, a 32-bit size
-  const int64_t nT = (a->T + 63) / 64;
-  if (nT * nT * 512 > int64_t(0xFFFFFFFFu))
-    return fail(KD_ERR_UNSUPPORTED, "T too large: ceil(T / 64)^2 * 512 bytes of tile masks must fit in 32 bits");
   if (a->D != 16 && a->D != 32 && a->D != 64 && a->D != 128 && a->D != 256)
     return fail(KD_ERR_UNSUPPORTED, "head dim must be 16, 32, 64, 128 or 256");
   if (a->dtype != KD_BF16 && a->dtype != KD_F16 && a->dtype != KD_F32)

@@ -1,4 +1,4 @@
-"""GPU: sequences past config 4's length (T = 16384 cocktail-party, T = 65536 causal).
+"""GPU: sequences past config 4's length (T = 16384 cocktail-party, T = 65536 and 196608 causal).
 
 Where the sizes grow -- 256 and 1024 key tiles per row, lists of that length
 in the plan, per-head byte offsets of 8-16 MiB in the buffer loads -- the
@@ -112,3 +112,21 @@ def test_causal_lens_64k(dev):
     refs = _reference(q[0, 0].float(), k[0, 0].float(), v[0, 0].float(), do[0, 0].float(), D ** -0.5, mask_rows)
     _check({nm: t[0, 0] for nm, t in got.items()}, refs)
     assert got["o"][0, 0, n:].abs().max().item() == 0.0
+
+
+def test_causal_196k(dev):
+    """Causal at T = 196608 (3072 key tiles per row, a 3072 x 3072 class map and lists of up to 3072
+    entries per block), past where a per-tile mask store would need more than 32 bits of bytes."""
+    T, H, D = 196608, 1, 64
+    q, k, v, do = (x.to(dev) for x in qkvdo(1, H, T, D, seed=8, scale=D ** -0.25))
+    print(f"causal B=1 H={H} T={T} D={D}: kernels", flush=True)
+    got = _run(q, k, v, do, causal=True)
+    cols = torch.arange(T, device=dev)
+
+    def mask_rows(r0, r1):
+        rows = torch.arange(r0, r1, device=dev)[:, None]
+        return rows >= cols[None, :r1], r1
+
+    print("  reference", flush=True)
+    refs = _reference(q[0, 0].float(), k[0, 0].float(), v[0, 0].float(), do[0, 0].float(), D ** -0.5, mask_rows)
+    _check({nm: t[0, 0] for nm, t in got.items()}, refs)
