@@ -20,11 +20,12 @@
  *     T * t_stride * element size < 2^31 bytes.
  *   - Head dims 16, 32, 64, 128, 256 (original_kernel.py:1720).  bf16 / fp16
  *     at D = 64, 128, 256 run on the MFMA kernels (dqk_signs at 64, 128 only);
- *     fp32 inputs (any D) and 16-bit inputs at D = 16, 32 run on fp32
- *     vector-ALU kernels (no fp8 scores, no dqk_signs there; precision is then
- *     always full fp32).  (The Python layer runs fp32 inputs at precision
- *     "tf32" and D <= 64 as bf16 operands of three times the head dim on the
- *     MFMA kernels instead, with dq_lo / dk_lo / dv_lo below.)
+ *     fp32 inputs at D = 32, 64, 128 on the fp32 MFMA kernels; fp32 at D = 16,
+ *     256 and 16-bit inputs at D = 16, 32 on fp32 vector-ALU kernels.  fp32
+ *     inputs get no fp8 scores and no dqk_signs, and precision is always full
+ *     fp32 for them.  (The Python layer runs fp32 inputs at precision "tf32"
+ *     and D = 16, 32 as bf16 operands of three times the head dim on the
+ *     16-bit MFMA kernels instead, with dq_lo / dk_lo / dv_lo below.)
  *   - LSE is stored in log2 units (LSE2 = log2 sum_j exp2(S_ij * sm_scale *
  *     log2 e)), as the reference stores it (original_kernel.py:603-604).
  *     Fully masked rows get O = 0, LSE = -inf and zero gradients.
@@ -47,7 +48,7 @@ extern "C" {
 /* element dtypes */
 #define KD_BF16 0
 #define KD_F16 1
-#define KD_F32 2 /* attention only: computed in fp32 on the vector ALUs */
+#define KD_F32 2 /* attention only: computed in fp32 (fp32 MFMA at D = 32, 64, 128) */
 /* arithmetic of the softmax weights P and the score gradients dS inside the
  * attention kernels (kd_attn_args.precision) */
 #define KD_PREC_SPLIT 0  /* P and dS enter their products (P V, dV, dQ, dK) as a 16-bit pair

@@ -9,9 +9,11 @@ shim over the C ABI of ``libkdattn.so``:
 * ``kdattn::fwd``  -> plan (codes, tile map, work lists) + forward kernel,
   returns ``(O, LSE2, plan)``; the plan is saved for the backward.
 * ``kdattn::bwd``  -> Delta, dQ and dK/dV kernels from the saved plan.
-* ``kdattn::fwd_x3`` / ``kdattn::bwd_x3`` -> the same kernels for fp32 inputs
-  at precision "tf32" and head dims up to 64, as three bf16 products per
-  product (see X3_HEAD_DIMS).
+* ``kdattn::fwd_x3`` / ``kdattn::bwd_x3`` -> the 16-bit kernels for fp32
+  inputs at precision "tf32" and head dims 16 and 32, as three bf16 products
+  per product (see X3_HEAD_DIMS).  Other fp32 inputs go through ``kdattn::fwd``
+  / ``::bwd`` to the fp32 MFMA kernels (head dims 32, 64, 128; 16 zero-padded
+  to 32) or the fp32 vector-ALU kernels (256).
 
 There is no CPU or PyTorch fallback: a missing library raises.
 """
@@ -29,9 +31,12 @@ REFERENCE_HEAD_DIMS = (16, 32, 64, 128, 256)  # original_kernel.py:1720
 SUPPORTED_HEAD_DIMS = REFERENCE_HEAD_DIMS
 # bf16 / fp16 at these head dims run on the MFMA kernels with the fused
 # Hadamard epilogues (fp8 scores at 128); 256 runs there without them.  fp32
-# inputs run on the fp32 vector-ALU kernels (kd_simt.hip), except at precision
-# "tf32" and head dims up to 64 (X3_HEAD_DIMS)
+# inputs run on the fp32 MFMA kernels (kd_f32mma.hip: head dims 32, 64, 128,
+# and 16 zero-padded to 32, FP32_PADDED_HEAD_DIMS), except at precision "tf32"
+# and head dims 16, 32 (X3_ROUTED_HEAD_DIMS: bf16x3, faster there), and on the
+# fp32 vector-ALU kernels (kd_simt.hip) at 256
 MFMA_HEAD_DIMS = (64, 128)
+FP32_PADDED_HEAD_DIMS = {16: 32}
 # 16-bit inputs with these head dims run on the d = 64 MFMA kernels, zero-
 # padded: zero columns change no score (S = Q K^T), O's extra columns are
 # P 0 = 0 and the gradients' extra columns are dropped by the pad's autograd.
@@ -339,6 +344,10 @@ _fwd_op.register_autograd(_backward, setup_context=_setup_context)
 # the copies that hold xh are the gradient of x (straight through the split):
 # dQ = dQ'[0, d) + dQ'[d, 2d), dK = dK'[0, d) + dK'[2d, 3d), dV likewise.
 X3_HEAD_DIMS = {16: 64, 32: 128, 64: 256}
+# where flash_attention takes this path: at head dim 64 and above the fp32
+# MFMA kernels are faster (causal B2 H8 T4096, fwd+bwd: d = 32 1.02 ms here
+# against 1.28 ms there, d = 64 2.14 against 1.93 ms) and exact in fp32
+X3_ROUTED_HEAD_DIMS = (16, 32)
 
 
 def _x3(x: torch.Tensor, pattern: str, Dp: int) -> torch.Tensor:
@@ -566,7 +575,11 @@ def flash_attention(
             fused_signs = signs
         else:
             q, k = _rot_op(q, signs, False), _rot_op(k, signs, False)
-    pad_to = PADDED_HEAD_DIMS.get(D, 0) if q.dtype != torch.float32 else 0
+    x3 = q.dtype == torch.float32 and precision == "tf32" and D in X3_ROUTED_HEAD_DIMS
+    if q.dtype != torch.float32:
+        pad_to = PADDED_HEAD_DIMS.get(D, 0)
+    else:
+        pad_to = 0 if x3 else FP32_PADDED_HEAD_DIMS.get(D, 0)
     if pad_to:  # after the rotation, which acts on the caller's head dim
         q, k, v = (torch.nn.functional.pad(x, (0, pad_to - D)) for x in (q, k, v))
     fp8 = ()
@@ -574,7 +587,7 @@ def flash_attention(
         (q8, q_scale), (k8, k_scale) = quantize_fp8(q), quantize_fp8(k)
         fp8 = (q8, k8, q_scale, k_scale)
 
-    if q.dtype == torch.float32 and precision == "tf32" and D in X3_HEAD_DIMS:
+    if x3:
         # fp32 at the reference's default precision: bf16x3 on the MFMA kernels
         o, lse, plan_t = _fwd_x3_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode),
                                     bthd=out_layout == "bthd", plan_in=None if plan is None else plan.tensor)

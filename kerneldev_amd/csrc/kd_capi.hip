@@ -92,7 +92,7 @@ int check_span(const kd_span_args* a) {
 
 extern "C" {
 
-int kd_version(void) { return 205; }
+int kd_version(void) { return 206; }
 
 const char* kd_last_error_string(void) { return g_err.c_str(); }
 

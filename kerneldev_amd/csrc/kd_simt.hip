@@ -1,9 +1,9 @@
 // Attention in fp32 arithmetic on the vector ALUs, for the cases the MFMA
-// kernels are not built for: fp32 inputs at any head dim (the reference's
-// precision="ieee" / "tf32" dots, original_kernel.py:452, :569, :1239,
-// :1331-1333, :1425, :1517-1523, here in full fp32), and bf16 / fp16 inputs
-// with head dim 16, 32 or 256 (the other sizes original_kernel.py:1720
-// accepts).  Same algebra, plan and masks as the MFMA kernels:
+// kernels are not built for: fp32 inputs at head dim 16 or 256 (the
+// reference's precision="ieee" / "tf32" dots, original_kernel.py:452, :569,
+// :1239, :1331-1333, :1425, :1517-1523, here in full fp32; kd_f32mma.hip takes
+// fp32 at 32, 64, 128), and bf16 / fp16 inputs with head dim 16 or 32 (the
+// other sizes original_kernel.py:1720 accepts), plus Delta for fp32 inputs.  Same algebra, plan and masks as the MFMA kernels:
 //   forward   O = softmax2(S c) V, LSE2 = m + log2 l      (:279-626)
 //   Delta     rowsum(O * dO), from O + O_lo for 16-bit O  (:649-710)
 //   dQ        P = exp2(S c - LSE), dS = P (dP - Delta), dQ = sm_scale dS K  (:1173-1336)
@@ -344,6 +344,7 @@ bool use_simt(const AttnArgs& a) { return a.dtype == KD_F32 || (a.D != 64 && a.D
 
 // which: 0 forward, 1 Delta, 2 dQ, 3 dK/dV
 int launch_simt_kernel(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
+  if (which != 1 && use_f32mma(a)) return launch_f32mma(which, a, plan, st);
   if (a.dtype == KD_F32) launch_simt_d<F32>(which, a, plan, st);
   else if (a.dtype == KD_BF16) launch_simt_d<BF16>(which, a, plan, st);
   else launch_simt_d<F16>(which, a, plan, st);

@@ -131,7 +131,7 @@ def _other_dims_case(D, causal_only, seed):
 @pytest.mark.parametrize("causal_only", [True, False])
 def test_other_head_dims(dev, D, causal_only):
     """The head dims original_kernel.py:1720 accepts beyond 64 / 128: 16 and 32
-    zero-padded onto the d = 64 MFMA kernels, 256 on the fp32 vector-ALU kernels."""
+    zero-padded onto the d = 64 MFMA kernels, 256 on its own MFMA kernels."""
     _case(_other_dims_case(D, causal_only, seed=40 + D), dev)
 
 
@@ -216,10 +216,10 @@ def _check_fp32(got, ref, bar, what):
 @pytest.mark.parametrize("D", [16, 32, 64])
 @pytest.mark.parametrize("causal_only", [True, False])
 def test_fp32_tf32_on_the_mfma_kernels(dev, D, causal_only):
-    """fp32 inputs at precision "tf32" and d <= 64 run as three bf16 products per
-    product on the MFMA kernels (kdattn::fwd_x3 / bwd_x3): rel-RMS <= 1e-4
-    against the fp64 oracle, ten times inside tf32's 10-bit mantissa (measured
-    6e-6 to 9e-6)."""
+    """fp32 inputs at precision "tf32": d = 16, 32 run as three bf16 products per
+    product on the 16-bit MFMA kernels (kdattn::fwd_x3 / bwd_x3; measured 6e-6
+    to 9e-6), d = 64 on the fp32 MFMA kernels; rel-RMS <= 1e-4 against the fp64
+    oracle, ten times inside tf32's 10-bit mantissa."""
     inp = _other_dims_case(D, causal_only, seed=80 + D)
     inp = {k_: (v_.float() if torch.is_tensor(v_) and v_.is_floating_point() else v_) for k_, v_ in inp.items()}
     print(f"fp32 tf32 bf16x3 D={D} {inp['name']}", flush=True)
@@ -227,27 +227,70 @@ def test_fp32_tf32_on_the_mfma_kernels(dev, D, causal_only):
     _check_fp32(got, _reference(inp), 1e-4, f"tf32 D={D}")
 
 
-def test_fp32_tf32_ops_directly(dev):
-    """The bf16x3 ops themselves, with the plan they build, against the oracle (and the
-    forward's LSE equal to what flash_attention returns for the same call)."""
-    from kerneldev_amd.attention import _bwd_x3_op, _fwd_x3_op
+@pytest.mark.parametrize("D", [32, 64])
+def test_fp32_tf32_ops_directly(dev, D):
+    """The bf16x3 ops themselves, with the plan they build, against the oracle (and,
+    where flash_attention takes them, d = 32, the forward's LSE equal to what it
+    returns for the same call; at d = 64 it takes the fp32 MFMA kernels)."""
+    from kerneldev_amd.attention import X3_ROUTED_HEAD_DIMS, _bwd_x3_op, _fwd_x3_op
     from kerneldev_amd import _lib
 
-    inp = _other_dims_case(64, False, seed=91)
+    inp = _other_dims_case(D, False, seed=91)
     inp = {k_: (v_.float() if torch.is_tensor(v_) and v_.is_floating_point() else v_) for k_, v_ in inp.items()}
     q, k, v, do = (inp[x].to(dev) for x in ("q", "k", "v", "do"))
     meta = [inp[n].to(dev) for n in ("in_span", "span_id", "is_prefix")]
-    o, lse, plan = _fwd_x3_op(q, k, v, None, *meta, 64 ** -0.5, _lib.KD_MODE_FORMULA)
-    dq, dk, dv = _bwd_x3_op(q, k, v, o, lse, do, plan, 64 ** -0.5)
+    o, lse, plan = _fwd_x3_op(q, k, v, None, *meta, D ** -0.5, _lib.KD_MODE_FORMULA)
+    dq, dk, dv = _bwd_x3_op(q, k, v, o, lse, do, plan, D ** -0.5)
     torch.cuda.synchronize()
     _check_fp32({"o": o, "lse": lse, "dq": dq, "dk": dk, "dv": dv}, _reference(inp), 1e-4, "ops")
-    assert torch.equal(run_gpu(inp, dev)["lse"], lse)
+    if D in X3_ROUTED_HEAD_DIMS:
+        assert torch.equal(run_gpu(inp, dev)["lse"], lse)
 
 
-def test_fp32_tf32_lens_hadamard_and_bthd(dev):
-    """The bf16x3 path with lens (fully masked rows: O = 0, LSE = -inf, zero
+@pytest.mark.parametrize("D", [16, 32, 64, 128])
+def test_fp32_on_the_fp32_mfma_kernels(dev, D):
+    """fp32 inputs at precision "ieee" run on the fp32 MFMA kernels (kd_f32mma.hip)
+    at head dims 32, 64, 128 (16 zero-padded to 32), and so does "tf32" at 64 and
+    128: ragged T with lens (an
+    empty batch row, a partial one), [B, T, H, D] memory viewed [B, H, T, D]
+    (model.py:76-78) with cocktail-party metadata; rel-RMS <= 1e-5 against the
+    fp64 oracle, exact zeros where nothing is allowed."""
+    q, k, v, do = qkvdo(3, 2, 300, D, seed=70 + D, dtype=torch.float32)
+    lens = torch.tensor([300, 129, 0], dtype=torch.int32)
+    inp = dict(name=f"lens fp32 D{D}", q=q, k=k, v=v, do=do, causal=True)
+    print(f"fp32 mfma D={D} lens", flush=True)
+    got = run_gpu(inp, dev, lens=lens, precision="ieee")
+    _check_fp32(got, _reference(inp, lens=lens), 1e-5, f"lens D={D}")
+    assert (got["o"][1, :, 129:] == 0).all() and (got["o"][2] == 0).all()
+    assert torch.isinf(got["lse"][2]).all() and (got["lse"][2] < 0).all()
+    assert (got["dq"][2] == 0).all() and (got["dk"][2] == 0).all() and (got["dv"][2] == 0).all()
+
+    B, L, H = 2, 650, 3
+    g = torch.Generator("cpu").manual_seed(77 + D)
+    base = [torch.randn(B, L, H, D, generator=g) for _ in range(4)]
+    _, in_span, span_id, is_prefix = cocktail_batch(B, 1024, CONFIG3_LAYOUT, seed=78 + D)
+    in_span, span_id, is_prefix = in_span[:, :L], span_id[:, :L], is_prefix[:, :L]
+    views = [x.to(dev).transpose(1, 2) for x in base]
+    cpu = [x.transpose(1, 2) for x in base]
+    mask = oracle_mask(dict(q=cpu[0], in_span=in_span, span_id=span_id, is_prefix=is_prefix), L)
+    ref = oracle_fwd_bwd(*cpu, mask, D ** -0.5)
+    for precision in (("ieee", "tf32") if D >= 64 else ("ieee",)):
+        print(f"fp32 mfma D={D} strided cocktail {precision}", flush=True)
+        q, k, v = (x.detach().clone().requires_grad_(True) for x in views[:3])
+        o, lse = flash_attention(q, k, v, in_span=in_span.to(dev), span_id=span_id.to(dev),
+                                 is_prefix=is_prefix.to(dev), return_lse=True, precision=precision)
+        o.backward(views[3])
+        torch.cuda.synchronize()
+        _check_fp32({"o": o, "lse": lse, "dq": q.grad, "dk": k.grad, "dv": v.grad}, ref, 1e-5,
+                    f"strided D={D} {precision}")
+
+
+@pytest.mark.parametrize("D", [32, 64])
+def test_fp32_tf32_lens_hadamard_and_bthd(dev, D):
+    """fp32 at precision "tf32" on the bf16x3 path (d = 32) and on the fp32 MFMA
+    kernels (d = 64) with lens (fully masked rows: O = 0, LSE = -inf, zero
     gradients), with the Hadamard rotation, and with out_layout="bthd"."""
-    q, k, v, do = qkvdo(3, 2, 300, 64, seed=12, dtype=torch.float32)
+    q, k, v, do = qkvdo(3, 2, 300, D, seed=12, dtype=torch.float32)
     lens = torch.tensor([300, 129, 0], dtype=torch.int32)
     inp = dict(name="lens fp32", q=q, k=k, v=v, do=do, causal=True)
     got = run_gpu(inp, dev, lens=lens, precision="tf32")
@@ -255,7 +298,7 @@ def test_fp32_tf32_lens_hadamard_and_bthd(dev):
     assert (got["o"][1, :, 129:] == 0).all() and (got["o"][2] == 0).all()
     assert torch.isinf(got["lse"][2]).all() and (got["lse"][2] < 0).all()
     assert (got["dq"][2] == 0).all() and (got["dk"][2] == 0).all() and (got["dv"][2] == 0).all()
-    inp = _other_dims_case(64, False, seed=93)
+    inp = _other_dims_case(D, False, seed=93)
     inp = {k_: (v_.float() if torch.is_tensor(v_) and v_.is_floating_point() else v_) for k_, v_ in inp.items()}
     got = run_gpu(inp, dev, precision="tf32", hadamard=True, hadamard_seed=3)
     _check_fp32(got, _reference(inp, hadamard=True, hadamard_seed=3), 1e-4, "hadamard")
