@@ -50,8 +50,6 @@ template <int D>
 struct F32Tile {
   using TL = Tile<2 * D, 4>;
   static constexpr int BYTES = TL::BYTES;
-  // byte offset of the 16-byte chunk holding floats 4 q .. 4 q + 3 of row r
-  KD_DEV static int chunk(int r, int q) { return TL::at(r, q); }
   // byte offset of float (r, col)
   KD_DEV static int at(int r, int col) { return TL::at(r, col >> 2) + ((col & 3) << 2); }
   // this wave's share of the copy of rows r0 .. r0 + 63 of a slice with
@@ -61,9 +59,6 @@ struct F32Tile {
     TL::load_async_rows(rs, r0 * row_bytes, arow, c16, row_bytes, lds_addr(lds_tile), wave);
   }
 };
-
-template <class V4>
-KD_DEV f32x4 as_f32x4(const V4& v) { return __builtin_bit_cast(f32x4, v); }
 
 // this lane's row x[row][.] in k-step order: out[4u + t] = x[row][8u + 4h + t] * scale
 template <int D>
@@ -85,8 +80,9 @@ KD_DEV void load_row(const float* base, int64_t row_stride, int row, bool valid,
 template <int D>
 KD_DEV f32x16 score_block(const uint8_t* tile, int kb, int c, int h, const float (&reg)[D / 2]) {
   f32x16 acc = {};
-  const uint8_t* row = tile + F32Tile<D>::chunk(32 * kb + c, 0) - ((0 ^ F32Tile<D>::TL::swz(32 * kb + c)) << 4);
-  const int sw = F32Tile<D>::TL::swz(32 * kb + c);
+  using TL = typename F32Tile<D>::TL;
+  const uint8_t* row = tile + (32 * kb + c) * TL::ROWB;  // chunk q of the row is at (q ^ swz) * 16
+  const int sw = TL::swz(32 * kb + c);
   f32x4 a = *reinterpret_cast<const f32x4*>(row + ((h ^ sw) << 4));
 #pragma unroll
   for (int u = 0; u < D / 8; ++u) {
