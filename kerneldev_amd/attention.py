@@ -449,6 +449,18 @@ def _backward_x3(ctx, do, dlse, dplan):
 _fwd_x3_op.register_autograd(_backward_x3, setup_context=_setup_context_x3)
 
 
+def head_dim_route(dtype: torch.dtype, D: int, precision: str) -> tuple[bool, int]:
+    """Which kernels flash_attention runs for inputs of this dtype and head dim:
+    (bf16x3 ops?, zero-padded head dim or 0).  16-bit d = 16, 32 pad to the d = 64
+    MFMA kernels; fp32 takes bf16x3 at "tf32" and d = 16, 32, else the C ABI's
+    fp32 kernels with d = 16 padded to 32 (the fp32 MFMA's smallest)."""
+    if dtype != torch.float32:
+        return False, PADDED_HEAD_DIMS.get(D, 0)
+    if precision == "tf32" and D in X3_ROUTED_HEAD_DIMS:
+        return True, 0
+    return False, FP32_PADDED_HEAD_DIMS.get(D, 0)
+
+
 # -------------------------------------------------------------- public entry
 def _check_meta(name, t, B, T, device, dtypes):
     if t is None:
@@ -575,11 +587,7 @@ def flash_attention(
             fused_signs = signs
         else:
             q, k = _rot_op(q, signs, False), _rot_op(k, signs, False)
-    x3 = q.dtype == torch.float32 and precision == "tf32" and D in X3_ROUTED_HEAD_DIMS
-    if q.dtype != torch.float32:
-        pad_to = PADDED_HEAD_DIMS.get(D, 0)
-    else:
-        pad_to = 0 if x3 else FP32_PADDED_HEAD_DIMS.get(D, 0)
+    x3, pad_to = head_dim_route(q.dtype, D, precision)
     if pad_to:  # after the rotation, which acts on the caller's head dim
         q, k, v = (torch.nn.functional.pad(x, (0, pad_to - D)) for x in (q, k, v))
     fp8 = ()

@@ -1,4 +1,5 @@
-"""CPU: the operand layout of the bf16x3 path for fp32 inputs (kerneldev_amd.attention).
+"""CPU: the operand layout of the bf16x3 path for fp32 inputs, and which kernels
+flash_attention picks per dtype and head dim (kerneldev_amd.attention).
 
 The kernels see Q' = [Qh, Qh, Ql], K' = [Kh, Kl, Kh], V' = [Vh, Vl, Vh],
 dO' = [dOh, dOh, dOl] (zero-padded) and compute every product of the
@@ -49,3 +50,16 @@ def test_hi_lo_adds_the_residual():
     want = (hi.float() + lo.float())[..., :16] + (hi.float() + lo.float())[..., 32:48]
     assert torch.equal(got, want)
     assert _rel(got.double(), (x[..., :16] + x[..., 32:48]).double()) < 2.0 ** -15
+
+
+def test_head_dim_route():
+    """flash_attention's choice of kernels per dtype, head dim and precision."""
+    from kerneldev_amd.attention import head_dim_route
+
+    bf, f32 = torch.bfloat16, torch.float32
+    assert head_dim_route(bf, 16, "tf32") == (False, 64) and head_dim_route(bf, 32, "bf16") == (False, 64)
+    assert head_dim_route(torch.float16, 128, "ieee") == (False, 0)
+    assert head_dim_route(f32, 16, "tf32") == (True, 0) and head_dim_route(f32, 32, "tf32") == (True, 0)
+    assert head_dim_route(f32, 64, "tf32") == (False, 0) and head_dim_route(f32, 128, "tf32") == (False, 0)
+    assert head_dim_route(f32, 16, "ieee") == (False, 32) and head_dim_route(f32, 32, "ieee") == (False, 0)
+    assert head_dim_route(f32, 256, "ieee") == (False, 0)
