@@ -110,9 +110,10 @@ typedef struct kd_attn_args {
   float *delta;                 /* fp32 workspace of 2 * B*H*T (bwd): -Delta [B, H, T],
                                    then -LSE / c [B, H, T] with c the score scale (sm_scale log2 e, times
                                    q_scale k_scale with fp8 scores; -inf for fully masked rows) */
-  void *o_lo;                   /* optional contiguous [B, H, T, D], dtype of o: the
-                                   forward writes O_fp32 - O there, the backward's Delta
-                                   reads it; NULL to skip */
+  void *o_lo;                   /* optional contiguous [B, H, T, D], dtype of o (bf16 /
+                                   fp16 only; NULL with fp32 inputs): the forward writes
+                                   O_fp32 - O there, the backward's Delta reads it; NULL
+                                   to skip */
   const uint8_t *q8, *k8;       /* optional fp8 e4m3 copies of q and k, contiguous
                                    [B, H, T, D] (kd_quant_fp8): when both are given, S = Q K^T
                                    is computed from them on fp8 MFMA, times q_scale * k_scale */

@@ -73,6 +73,15 @@ int check_common(const kd_attn_args* a) {
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// O's rounding residual exists for 16-bit O only: the fp32 kernels neither
+// write nor need it, and a stale buffer would enter Delta
+int check_o_lo(const kd_attn_args* a) {
+  if (a->o_lo == nullptr) return KD_OK;
+  if (a->dtype == KD_F32) return fail(KD_ERR_INVALID, "o_lo is for bf16 / fp16 O; pass NULL with fp32 inputs");
+  if (!aligned16(a->o_lo)) return fail(KD_ERR_INVALID, "o_lo must be 16-byte aligned");
+  return KD_OK;
+}
+
 int esz(const kd_attn_args* a) { return a->dtype == KD_F32 ? 4 : 2; }
 
 int check_span(const kd_span_args* a) {
@@ -234,7 +243,7 @@ int kd_attn_fwd(const kd_attn_args* a, const void* plan, void* stream) {
   if ((r = check_tensor(a->q, a->q_strides, "q", a->T, a->D, esz(a))) || (r = check_tensor(a->k, a->k_strides, "k", a->T, a->D, esz(a))) ||
       (r = check_tensor(a->v, a->v_strides, "v", a->T, a->D, esz(a))) || (r = check_tensor(a->o, a->o_strides, "o", a->T, a->D, esz(a))))
     return r;
-  if (a->o_lo != nullptr && !aligned16(a->o_lo)) return fail(KD_ERR_INVALID, "o_lo must be 16-byte aligned");
+  if ((r = check_o_lo(a))) return r;
   r = kd::launch_fwd(*a, static_cast<const uint8_t*>(plan), as_stream(stream));
   return r ? fail(r, "kernel launch failed (forward)") : KD_OK;
 }
@@ -245,7 +254,7 @@ int kd_attn_bwd_delta(const kd_attn_args* a, void* stream) {
   if ((r = check_tensor(a->o, a->o_strides, "o", a->T, a->D, esz(a))) || (r = check_tensor(a->dout, a->do_strides, "dout", a->T, a->D, esz(a))))
     return r;
   if (a->delta == nullptr || a->lse == nullptr) return fail(KD_ERR_INVALID, "delta and lse are required");
-  if (a->o_lo != nullptr && !aligned16(a->o_lo)) return fail(KD_ERR_INVALID, "o_lo must be 16-byte aligned");
+  if ((r = check_o_lo(a))) return r;
   r = kd::launch_delta(*a, as_stream(stream));
   return r ? fail(r, "kernel launch failed (delta)") : KD_OK;
 }
@@ -290,7 +299,7 @@ int kd_attn_bwd_dq_delta(const kd_attn_args* a, const void* plan, void* stream) 
   if (r) return r;
   if ((r = check_tensor(a->o, a->o_strides, "o", a->T, a->D, esz(a))) || (r = check_tensor(a->dq, a->dq_strides, "dq", a->T, a->D, esz(a))))
     return r;
-  if (a->o_lo != nullptr && !aligned16(a->o_lo)) return fail(KD_ERR_INVALID, "o_lo must be 16-byte aligned");
+  if ((r = check_o_lo(a))) return r;
   r = kd::launch_dq(*a, static_cast<const uint8_t*>(plan), as_stream(stream), true);
   return r ? fail(r, "kernel launch failed (dq)") : KD_OK;
 }

@@ -93,6 +93,13 @@ def test_bad_arguments_return_status_without_gpu():
     b.dtype, b.dq_lo, b.dv_lo = _lib.KD_BF16, None, 72
     assert lib.kd_attn_bwd(ctypes.byref(b), ctypes.c_void_p(256), null) == _lib.KD_ERR_INVALID
     assert "aligned" in lib.kd_last_error_string().decode()
+    c = _lib.AttnArgs()  # O's rounding residual is for 16-bit O: fp32 inputs with o_lo are refused
+    c.B, c.H, c.T, c.D, c.dtype, c.sm_scale = 1, 1, 16, 64, _lib.KD_F32, 0.125
+    c.q = c.k = c.v = c.o = c.o_lo = 64
+    for st in (c.q_strides, c.k_strides, c.v_strides, c.o_strides):
+        st[:] = [1024, 1024, 64]
+    assert lib.kd_attn_fwd(ctypes.byref(c), ctypes.c_void_p(256), null) == _lib.KD_ERR_INVALID
+    assert "o_lo" in lib.kd_last_error_string().decode()
     r = _lib.RotArgs()
     r.B, r.H, r.T, r.D, r.dtype = 1, 1, 4, 48, _lib.KD_BF16
     assert lib.kd_hadamard(ctypes.byref(r), null) == _lib.KD_ERR_UNSUPPORTED  # not a power of two
