@@ -84,3 +84,12 @@ def test_compiled_flash_attention_matches_eager(dev, dynamic, dtype):
         got = _fwd_bwd(compiled, q, k, v, do, meta)
         for name, x, y in zip(("o", "lse", "dq", "dk", "dv"), got, want):
             assert torch.equal(x, y), f"{name} differs between compiled and eager (T={T})"
+
+
+def test_timing_module_runs(dev):
+    """kerneldev_amd.timing (the fwd+bwd timer for shapes outside the benchmark) runs end to end."""
+    from kerneldev_amd.timing import time_step
+
+    for dtype in (torch.bfloat16, torch.float32):
+        s, nnz = time_step(1, 2, 200, 64, dtype, steps=1, warmup=1)
+        assert s > 0 and nnz == 2 * 200 * 201 // 2
