@@ -66,6 +66,23 @@ def build_library(verbose: bool = False) -> str:
     return LIB
 
 
+C_ABI_SRC = os.path.join(ROOT, "tests", "c_abi", "attn_from_c.c")
+C_ABI_BIN = os.path.join(ROOT, "tests", "c_abi", "attn_from_c")
+
+
+def build_c_abi_check(verbose: bool = False) -> str:
+    """The C caller of the library (tests/c_abi/attn_from_c.c), built with gcc
+    against the HIP runtime's C API and libkdattn.so (found through its rpath)."""
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    _run(["gcc", "-std=c11", "-O2", "-Wall", "-D__HIP_PLATFORM_AMD__", f"-I{rocm}/include",
+          f"-I{os.path.join(ROOT, 'include')}", C_ABI_SRC, "-o", C_ABI_BIN, f"-L{PKG}", "-lkdattn",
+          f"-L{rocm}/lib", "-lamdhip64", "-lm", "-Wl,-rpath,$ORIGIN/../../kerneldev_amd", f"-Wl,-rpath,{rocm}/lib"])
+    if verbose:
+        print(f"built {C_ABI_BIN}")
+    return C_ABI_BIN
+
+
 if __name__ == "__main__":
     build_library(verbose=True)
+    build_c_abi_check(verbose=True)
     sys.exit(0)

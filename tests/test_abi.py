@@ -165,3 +165,16 @@ def test_python_plan_size_matches_the_library():
         for T in (1, 17, 63, 64, 65, 127, 128, 129, 300, 1024, 8192, 8193):
             for D in (64, 128):
                 assert _lib.plan_nbytes(B, T, D) == _lib.plan_bytes(B, T, D), (B, T, D)
+
+
+def test_c_caller_is_built_against_the_library():
+    """The C test caller exists after the build and resolves libkdattn.so through its rpath."""
+    import shutil
+    import subprocess
+
+    from kerneldev_amd.build import C_ABI_BIN
+
+    assert os.path.exists(C_ABI_BIN)
+    if shutil.which("ldd"):
+        out = subprocess.run(["ldd", C_ABI_BIN], capture_output=True, text=True).stdout
+        assert "libkdattn.so =>" in out and "not found" not in out.split("libkdattn.so")[1].split("\n")[0]
