@@ -153,21 +153,35 @@ __global__ __launch_bounds__(Shape<D>::NT) void k_fwd_simt(AttnArgs a, const uin
 
 // -------------------------------------------------------------------- Delta
 // workspace: -Delta, then -LSE / c (the forms the MFMA dK/dV kernel reads);
-// the fp32 kernels read -Delta and the LSE itself
+// the fp32 kernels read -Delta and the LSE itself.  DeltaShape<D>::G lanes share
+// a row, each reading EL consecutive elements (coalesced), and the row's sum
+// ends in a G-lane xor reduction.
+template <int D> struct DeltaShape {
+  static constexpr int G = D >= 64 ? 16 : D / 4;  // lanes per row
+  static constexpr int EL = D / G;                // elements per lane (4 .. 16)
+  static constexpr int RPB = 256 / G;             // rows per 256-thread block
+};
 template <class E, int D>
 __global__ __launch_bounds__(256) void k_delta_simt(AttnArgs a) {
+  using S = DeltaShape<D>;
   const int64_t rows = int64_t(a.B) * a.H * a.T;
-  const int64_t r = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (r >= rows) return;
-  const int t = int(r % a.T), bh = int(r / a.T), b = bh / a.H, h = bh % a.H;
-  const int64_t ob = b * a.o_strides[0] + h * a.o_strides[1] + int64_t(t) * a.o_strides[2];
-  const int64_t db = b * a.do_strides[0] + h * a.do_strides[1] + int64_t(t) * a.do_strides[2];
+  const int64_t r = int64_t(blockIdx.x) * S::RPB + threadIdx.x / S::G;
+  const int g = threadIdx.x % S::G;
+  const bool valid = r < rows;  // (every lane takes part in the reduction below)
   float sum = 0.f;
-  for (int d = 0; d < D; ++d) {
-    float o = ld<E>(a.o, ob + d);
-    if (a.o_lo != nullptr) o += ld<E>(a.o_lo, r * D + d);  // F32 output: o_lo is never set
-    sum = __builtin_fmaf(o, ld<E>(a.dout, db + d), sum);
+  if (valid) {
+    const int t = int(r % a.T), bh = int(r / a.T), b = bh / a.H, h = bh % a.H;
+    const int64_t ob = b * a.o_strides[0] + h * a.o_strides[1] + int64_t(t) * a.o_strides[2] + g * S::EL;
+    const int64_t db = b * a.do_strides[0] + h * a.do_strides[1] + int64_t(t) * a.do_strides[2] + g * S::EL;
+#pragma unroll
+    for (int d = 0; d < S::EL; ++d) {
+      float o = ld<E>(a.o, ob + d);
+      if (a.o_lo != nullptr) o += ld<E>(a.o_lo, r * D + g * S::EL + d);  // 16-bit O only (the C ABI refuses it for fp32)
+      sum = __builtin_fmaf(o, ld<E>(a.dout, db + d), sum);
+    }
   }
+  sum = group_sum<S::G>(sum);
+  if (!valid || g != 0) return;
   const float c = a.sm_scale * 1.4426950408889634f;
   const float l = a.lse[r];
   a.delta[r] = -sum;
@@ -323,7 +337,8 @@ static void launch_simt(int which, const AttnArgs& a, const uint8_t* plan, hipSt
   if (which == 0) hipLaunchKernelGGL((k_fwd_simt<E, D>), grid, dim3(Shape<D>::NT), 0, st, a, cls, codes, L.nT);
   if (which == 1) {
     const int64_t rows = int64_t(a.B) * a.H * a.T;
-    hipLaunchKernelGGL((k_delta_simt<E, D>), dim3(unsigned((rows + 255) / 256)), dim3(256), 0, st, a);
+    constexpr int rpb = DeltaShape<D>::RPB;
+    hipLaunchKernelGGL((k_delta_simt<E, D>), dim3(unsigned((rows + rpb - 1) / rpb)), dim3(256), 0, st, a);
   }
   if (which == 2) hipLaunchKernelGGL((k_dq_simt<E, D>), grid, dim3(Shape<D>::NT), 0, st, a, cls, codes, L.nT);
   if (which == 3) hipLaunchKernelGGL((k_dkdv_simt<E, D>), grid, dim3(Shape<D>::NT), 0, st, a, cls, codes, L.nT);
