@@ -435,13 +435,21 @@ __global__ __launch_bounds__(256, D <= 32 ? 2 : 1) void k_dkdv_f32m(AttnArgs a, 
         const int row = 32 * qb + 8 * g + 4 * h;  // rows row .. row + 3 are registers 4 g .. 4 g + 3
         const f32x4 lv = *reinterpret_cast<const f32x4*>(&s_lse[slot][row]);
         const f32x4 dv4 = *reinterpret_cast<const f32x4*>(&s_dl[slot][row]);
-        u32x4 qc = {0u, 0u, 0u, 0u};
-        if (cls == TILE_PARTIAL) qc = *reinterpret_cast<const u32x4*>(&s_qc[slot][row]);
+        // (branch-free per element: bitwise logic and selects; the mask rule
+        // only in PARTIAL tiles, a wave-uniform branch)
+        bool ok[4];
+        if (full) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {  // (branch-free: bitwise logic and selects)
-          const bool ok = (lv[i] != -__builtin_inff()) & (full | allow(qc[i], kcode, q0 + row + i, k));
+          for (int i = 0; i < 4; ++i) ok[i] = lv[i] != -__builtin_inff();
+        } else {
+          const u32x4 qc = *reinterpret_cast<const u32x4*>(&s_qc[slot][row]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ok[i] = (lv[i] != -__builtin_inff()) & allow(qc[i], kcode, q0 + row + i, k);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
           const float ex = fast_exp2(s[4 * g + i] - lv[i]);
-          const float p = ok ? ex : 0.f;
+          const float p = ok[i] ? ex : 0.f;
           s[4 * g + i] = p;
           dp[4 * g + i] = p * (dp[4 * g + i] + dv4[i]);  // dS
         }
