@@ -18,7 +18,7 @@ from oracle import hadamard as ref_h
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 24
+N_CASES = 96
 
 
 def _draw(rng):

@@ -1,0 +1,33 @@
+"""CPU: the parity metric in tests/helpers.py (what the GPU tests assert with)."""
+import torch
+
+from helpers import REF_ZERO, assert_close, errors
+
+
+def test_relative_error_and_ulp_excess():
+    ref = torch.tensor([1.0, -2.0, 0.5, 4.0], dtype=torch.float64)
+    x = ref + torch.tensor([1e-3, 0.0, -1e-3, 0.0], dtype=torch.float64)
+    ma, rr, ex = errors(x, ref, out_dtype=torch.float32)
+    assert abs(ma - 1e-3) < 1e-12 and abs(ex - (1e-3 - 2.0 ** -24)) < 1e-12  # ulp of 0.5 in fp32
+    assert abs(rr - (2e-6 / 4) ** 0.5 / ((1 + 4 + 0.25 + 16) / 4) ** 0.5) < 1e-9
+    # one bf16 ulp at 4.0 is 2^-5: an error of 0.03 there is within it
+    _, _, ex = errors(torch.tensor([4.03], dtype=torch.float64), torch.tensor([4.0], dtype=torch.float64),
+                      out_dtype=torch.bfloat16)
+    assert ex == 0.0
+
+
+def test_zero_reference_has_no_relative_scale():
+    """A reference that is 0 to fp64 rounding (dQ with one allowed key per row) is checked by
+    the absolute bar only; a real error there still fails it."""
+    ref = torch.full((4, 8), 3e-16, dtype=torch.float64)
+    assert ref.pow(2).mean().sqrt().item() <= REF_ZERO
+    x = ref + 2e-7
+    ma, rr, _ = errors(x, ref, out_dtype=torch.float32)
+    assert rr == 0.0 and ma < 3e-7
+    assert_close("dq", x, ref, out_dtype=torch.float32)
+    try:
+        assert_close("dq", ref + 0.5, ref, out_dtype=torch.float32)
+    except AssertionError:
+        pass
+    else:
+        raise AssertionError("an absolute error of 0.5 passed")
