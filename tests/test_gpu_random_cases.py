@@ -1,10 +1,11 @@
-"""GPU: seeded random small cases through flash_attention against the fp64 oracle.
+"""GPU: seeded random cases through flash_attention against the fp64 oracle.
 
-Each case draws B, H, T (ragged, 1 .. 640), the head dim, the input dtype,
+Each small case draws B, H, T (ragged, 1 .. 640), the head dim, the input dtype,
 the precision, the mask mode (causal or not, cocktail-party metadata with
 int64 or int32 span ids, lens with empty rows) and Hadamard on or off, runs
 forward and backward and checks O, LSE, dQ, dK, dV against the oracle with
 the north_star bar (helpers.assert_close; fp32 results against the same bar).
+The long cases draw one head with T from 1000 to 4096 the same way.
 """
 import random
 
@@ -31,9 +32,30 @@ def _draw(rng):
                 lens=rng.random() < 0.3, hadamard=rng.random() < 0.3, seed=rng.randrange(1 << 20))
 
 
+N_LONG = 16
+
+
+def _draw_long(rng):
+    """Longer rows (T 1000-4096, ragged), head dims 64-256, one head."""
+    d = rng.choice([64, 128, 128, 256])
+    dtype = rng.choice([torch.bfloat16, torch.bfloat16, torch.float16, torch.float32])
+    precision = rng.choice(["tf32", "ieee", "bf16"]) if dtype != torch.float32 else rng.choice(["tf32", "ieee"])
+    return dict(B=rng.choice([1, 2]), H=1, T=rng.choice([1000, 1170, 2048, 3001, 4096]), d=d, dtype=dtype,
+                precision=precision, causal=rng.random() < 0.7, meta=rng.random() < 0.6, sid32=rng.random() < 0.5,
+                lens=rng.random() < 0.3, hadamard=rng.random() < 0.3, seed=rng.randrange(1 << 20))
+
+
 @pytest.mark.parametrize("case", range(N_CASES))
 def test_random_case(dev, case):
-    c = _draw(random.Random(1000 + case))
+    _run_case(dev, case, _draw(random.Random(1000 + case)))
+
+
+@pytest.mark.parametrize("case", range(N_LONG))
+def test_random_long_case(dev, case):
+    _run_case(dev, case, _draw_long(random.Random(5000 + case)))
+
+
+def _run_case(dev, case, c):
     B, H, T, d = c["B"], c["H"], c["T"], c["d"]
     print(f"random case {case}: {c}", flush=True)
     q, k, v, do = qkvdo(B, H, T, d, seed=c["seed"], dtype=torch.float32)
