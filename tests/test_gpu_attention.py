@@ -616,3 +616,23 @@ def test_cocktail_ragged_hadamard_fp8(dev):
     q, k, v, do = qkvdo(2, 2, T, 128, seed=61)
     _case(dict(name="cocktail ragged fp8+hadamard", q=q, k=k, v=v, do=do, in_span=in_span, span_id=span_id,
                is_prefix=is_prefix), dev, qk_dtype="fp8_e4m3", hadamard=True, hadamard_seed=7)
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_fp8_random_cases(dev, case):
+    """fp8 e4m3 scores on seeded random shapes: B, H, ragged T, causal or cocktail-party
+    metadata, Hadamard on or off, split or single rounding of P and dS; against the
+    oracle fed the same e4m3 operands."""
+    import random
+
+    rng = random.Random(100 + case)
+    B, H, T = rng.choice([1, 2]), rng.choice([1, 2]), rng.choice([64, 200, 513, 1024, 2048])
+    seed = rng.randrange(1 << 20)
+    q, k, v, do = qkvdo(B, H, T, 128, seed=seed, dtype=torch.bfloat16)
+    inp = dict(name=f"fp8 random {case} B{B} H{H} T{T}", q=q, k=k, v=v, do=do, causal=rng.random() < 0.6)
+    if rng.random() < 0.6:
+        _, in_span, span_id, is_prefix = cocktail_batch(B, max(T, 1170), CONFIG3_LAYOUT, seed=seed)
+        inp.update(in_span=in_span[:, :T].contiguous(), span_id=span_id[:, :T].contiguous(),
+                   is_prefix=is_prefix[:, :T].contiguous())
+    _case(inp, dev, qk_dtype="fp8_e4m3", hadamard=rng.random() < 0.5, hadamard_seed=case % 5,
+          precision=rng.choice(["tf32", "bf16"]))
