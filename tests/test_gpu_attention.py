@@ -636,3 +636,42 @@ def test_fp8_random_cases(dev, case):
                    is_prefix=is_prefix[:, :T].contiguous())
     _case(inp, dev, qk_dtype="fp8_e4m3", hadamard=rng.random() < 0.5, hadamard_seed=case % 5,
           precision=rng.choice(["tf32", "bf16"]))
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_strided_layouts_random(dev, case):
+    """q, k, v and dO as views of larger buffers: rows padded (t-stride d + 0 / 8 / 24) and
+    [B, T, H, d] or [B, H, T, d] memory, chosen per tensor; seeded B, H, ragged T, head dim and
+    dtype, causal or cocktail-party metadata; against the oracle on the same values."""
+    import random
+
+    rng = random.Random(200 + case)
+    B, H, T, D = rng.choice([1, 2, 3]), rng.choice([1, 2, 3]), rng.choice([33, 200, 640]), rng.choice([32, 64, 128, 256])
+    dtype = rng.choice([torch.bfloat16, torch.float16, torch.float32])
+    g = torch.Generator().manual_seed(200 + case)
+    xs = [torch.randn(B, H, T, D, generator=g).to(dtype) for _ in range(4)]
+
+    def strided(x):
+        pad = 8 * rng.choice([0, 1, 3])
+        if rng.random() < 0.5:  # [B, T, H, d + pad] memory
+            buf = torch.zeros(B, T, H, D + pad, dtype=dtype, device=dev)
+            buf[..., :D] = x.transpose(1, 2).to(dev)
+            return buf[..., :D].transpose(1, 2)
+        buf = torch.zeros(B, H, T, D + pad, dtype=dtype, device=dev)
+        buf[..., :D] = x.to(dev)
+        return buf[..., :D]
+
+    meta = {}
+    if rng.random() < 0.5:
+        _, in_span, span_id, is_prefix = cocktail_batch(B, 1170, CONFIG3_LAYOUT, seed=200 + case)
+        meta = dict(in_span=in_span[:, :T].contiguous(), span_id=span_id[:, :T].contiguous(),
+                    is_prefix=is_prefix[:, :T].contiguous())
+    views = [strided(x) for x in xs]
+    print(f"strided case {case}: B{B} H{H} T{T} D{D} {dtype} strides {[tuple(v.stride()) for v in views]}", flush=True)
+    q, k, v = (x.detach().requires_grad_(True) for x in views[:3])
+    o = flash_attention(q, k, v, causal=True, **{n: t.to(dev) for n, t in meta.items()})
+    o.backward(views[3])
+    torch.cuda.synchronize()
+    ref = oracle_fwd_bwd(xs[0], xs[1], xs[2], xs[3], oracle_mask(dict(q=xs[0], causal=True, **meta), T), D ** -0.5)
+    for name, got in (("o", o), ("dq", q.grad), ("dk", k.grad), ("dv", v.grad)):
+        assert_close(name, got, ref[name], out_dtype=dtype)
