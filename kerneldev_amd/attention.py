@@ -506,7 +506,12 @@ def flash_attention(
     carry P and dS as 16-bit hi + lo pairs (about 16 significant bits in P V,
     dV, dQ and dK, at or above the reference's bf16 P V and tf32 / ieee
     backward dots).  The extension ``"bf16"`` rounds P and dS once to the
-    input type instead (faster; 8 significant bits with bf16 inputs).  ``attention_mask``'s contents are not
+    input type instead (faster; 8 significant bits with bf16 inputs).  fp32
+    inputs get fp32 arithmetic at both "ieee" and "tf32": the fp32 MFMA
+    kernels at head dims 32, 64, 128 (16 zero-padded to 32) and the fp32
+    vector-ALU kernels at 256, except "tf32" at 16 and 32, which runs as bf16x3
+    on the 16-bit kernels (see head_dim_route).  O and the gradients stay fp32.
+    ``attention_mask``'s contents are not
     read, exactly as in the reference: when it is given without metadata the
     mask formula runs with default metadata, i.e. ``i >= j``.
 
