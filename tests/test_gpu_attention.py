@@ -675,3 +675,35 @@ def test_strided_layouts_random(dev, case):
     ref = oracle_fwd_bwd(xs[0], xs[1], xs[2], xs[3], oracle_mask(dict(q=xs[0], causal=True, **meta), T), D ** -0.5)
     for name, got in (("o", o), ("dq", q.grad), ("dk", k.grad), ("dv", v.grad)):
         assert_close(name, got, ref[name], out_dtype=dtype)
+
+
+def test_two_streams_at_once(dev):
+    """Calls on two streams in flight together give the same bits as one after the other: the
+    library keeps no state between calls and every launch goes to the caller's stream."""
+    cases = []
+    for seed in (301, 302):
+        _, in_span, span_id, is_prefix = cocktail_batch(2, 1024, CONFIG3_LAYOUT, seed=seed)
+        q, k, v, do = (x.to(dev) for x in qkvdo(2, 2, 1024, 128, seed=seed + 7))
+        cases.append((q, k, v, do, dict(in_span=in_span.to(dev), span_id=span_id.to(dev), is_prefix=is_prefix.to(dev))))
+
+    def run(q, k, v, do, meta):
+        ql, kl, vl = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
+        o = flash_attention(ql, kl, vl, **meta)
+        o.backward(do)
+        return [o.detach(), ql.grad, kl.grad, vl.grad]
+
+    serial = [run(*c) for c in cases]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device=dev) for _ in cases]
+    main = torch.cuda.current_stream(dev)
+    outs = []
+    for s, c in zip(streams, cases):
+        s.wait_stream(main)
+        with torch.cuda.stream(s):
+            outs.append(run(*c))
+    for s in streams:
+        main.wait_stream(s)
+    torch.cuda.synchronize()
+    for got, want in zip(outs, serial):
+        for g, w in zip(got, want):
+            assert torch.equal(g, w)
