@@ -707,3 +707,14 @@ def test_two_streams_at_once(dev):
     for got, want in zip(outs, serial):
         for g, w in zip(got, want):
             assert torch.equal(g, w)
+
+
+def test_many_heads_short_rows(dev):
+    """B = 64, H = 16, T = 96 (1024 (b, h) heads of two tiles each, one q-block per head): the
+    work order and remap over many small heads, checked on heads spread over the grid."""
+    q, k, v, do = qkvdo(64, 16, 96, 64, seed=411)
+    heads = [(0, 0), (7, 3), (31, 15), (40, 8), (63, 15)]
+    _case(dict(name="many heads", q=q, k=k, v=v, do=do, causal=True), dev, heads=heads)
+    tokens, in_span, span_id, is_prefix = cocktail_batch(64, 1170, CONFIG3_LAYOUT, seed=412)
+    _case(dict(name="many heads cocktail", q=q, k=k, v=v, do=do, in_span=in_span[:, :96].contiguous(),
+               span_id=span_id[:, :96].contiguous(), is_prefix=is_prefix[:, :96].contiguous()), dev, heads=heads)
