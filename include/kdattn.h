@@ -174,7 +174,7 @@ typedef struct kd_span_args {
   int32_t dtype;            /* KD_BF16 / KD_F16: h and dh */
   const void *h;            /* [B, T, D] hidden states, unit d stride */
   int64_t h_strides[2];     /* (b, t) in elements */
-  int32_t B, T, D;
+  int32_t B, T, D;          /* D <= 65536 */
   int32_t n_spans;          /* score columns, 1 .. 8192; the reference's max_spans = the
                                largest per-row [SPAN] count (spans past n_spans are dropped) */
   float *scores;            /* out [B, n_spans] */

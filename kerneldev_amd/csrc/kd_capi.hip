@@ -88,6 +88,7 @@ int check_span(const kd_span_args* a) {
   if (a == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
   if (a->B < 1 || a->T < 1 || a->D < 1) return fail(KD_ERR_INVALID, "B, T and D must be >= 1");
   if (a->B > 65535) return fail(KD_ERR_UNSUPPORTED, "B must be <= 65535");
+  if (a->D > 65536) return fail(KD_ERR_UNSUPPORTED, "D must be <= 65536");
   if (a->n_spans < 1 || a->n_spans > 8192) return fail(KD_ERR_UNSUPPORTED, "n_spans must be in 1 .. 8192");
   if (a->dtype != KD_BF16 && a->dtype != KD_F16) return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16 or fp16");
   if (a->tokens_dtype != KD_I64 && a->tokens_dtype != KD_I32) return fail(KD_ERR_INVALID, "bad tokens dtype");

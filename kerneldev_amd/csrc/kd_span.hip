@@ -6,10 +6,11 @@
 // when st + 1 < ed (model.py:287-293), and scores each span by its dot
 // product with the hidden state at the row's first [MASK] (:264-270, :296).
 // Here one workgroup per row finds the positions (block scans give the j-th
-// [SPAN] and the j-th [ES] of the row), one workgroup per (row, span) sums the
-// interior in fp32 in ascending position order, and the backward spreads
-// d score over the interior rows and the [MASK] row in a fixed order, so the
-// results are deterministic.
+// [SPAN] and the j-th [ES] of the row); one workgroup per (row, span, 256
+// columns) sums the interior in fp32 (eight waves over interleaved rows,
+// combined in a fixed order) and k_span_score dots the means with the context
+// vector.  The backward spreads d score over the interior rows and the [MASK]
+// row in a fixed order (one wave per row), so the results are deterministic.
 #include "kd_internal.h"
 
 namespace kd {
@@ -86,53 +87,104 @@ KD_DEV float block_sum256(float v, float* s_red) {
   return r;
 }
 
-// grid (n_spans + 1, B): block j < n pools span j and scores it; block n
-// writes h_ctx.
+// grid (n_spans + 1, B, ceil(D / 256)): block (j < n, b, c) averages span j's
+// interior over the columns [256 c, 256 c + 256); block (n, b, c) copies
+// those columns of h_ctx.  Wave w of 8 sums the rows lo + w, lo + w + 8, ...
+// (lane l: columns 256 c + l + 64 k, k < 4) and the eight partials combine in
+// a fixed order, ((w0 + w1) + (w2 + w3)) + ((w4 + w5) + (w6 + w7)).
 template <class E>
-__global__ __launch_bounds__(256) void k_span_pool(kd_span_args a) {
-  __shared__ float s_red[4];
-  const int j = blockIdx.x, b = blockIdx.y, n = a.n_spans, D = a.D;
-  const int mp = a.mask_pos[b];
+__global__ __launch_bounds__(512) void k_span_pool(kd_span_args a) {
+  __shared__ float s_part[8][256];
+  const int j = blockIdx.x, b = blockIdx.y, n = a.n_spans, D = a.D, d0 = blockIdx.z * 256;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (j == n) {
-    for (int d = threadIdx.x; d < D; d += 256) a.h_ctx[int64_t(b) * D + d] = mp >= 0 ? h_at<E>(a, b, mp, d) : 0.f;
+    const int mp = a.mask_pos[b];
+    const int d = d0 + int(threadIdx.x);
+    if (threadIdx.x < 256 && d < D) a.h_ctx[int64_t(b) * D + d] = mp >= 0 ? h_at<E>(a, b, mp, d) : 0.f;
     return;
   }
   const int lo = a.span_lo[int64_t(b) * n + j], hi = a.span_hi[int64_t(b) * n + j];
-  const float cnt = float(hi - lo);
-  float part = 0.f;
-  for (int d = threadIdx.x; d < D; d += 256) {
-    float acc = 0.f;
-    for (int t = lo; t < hi; ++t) acc += h_at<E>(a, b, t, d);
-    const float mean = hi > lo ? acc / cnt : 0.f;
-    a.h_spans[(int64_t(b) * n + j) * D + d] = mean;
-    part = __builtin_fmaf(mean, mp >= 0 ? h_at<E>(a, b, mp, d) : 0.f, part);
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int t = lo + wave; t < hi; t += 8) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int d = d0 + lane + 64 * k;
+      if (d < D) acc[k] += h_at<E>(a, b, t, d);
+    }
   }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) s_part[wave][lane + 64 * k] = acc[k];
+  __syncthreads();
+  const int d = d0 + int(threadIdx.x);
+  if (threadIdx.x < 256 && d < D) {
+    const int i = threadIdx.x;
+    const float sum = ((s_part[0][i] + s_part[1][i]) + (s_part[2][i] + s_part[3][i])) +
+                      ((s_part[4][i] + s_part[5][i]) + (s_part[6][i] + s_part[7][i]));
+    a.h_spans[(int64_t(b) * n + j) * D + d] = hi > lo ? sum / float(hi - lo) : 0.f;
+  }
+}
+
+// grid (n_spans, B): score of span j = sum_d h_span_j[d] h_ctx[d], thread i
+// over d = i + 256 k in ascending k, then a fixed-order block sum.
+__global__ __launch_bounds__(256) void k_span_score(kd_span_args a) {
+  __shared__ float s_red[4];
+  const int j = blockIdx.x, b = blockIdx.y, n = a.n_spans, D = a.D;
+  const float* hs = a.h_spans + (int64_t(b) * n + j) * D;
+  const float* hc = a.h_ctx + int64_t(b) * D;
+  float part = 0.f;
+  for (int d = threadIdx.x; d < D; d += 256) part = __builtin_fmaf(hs[d], hc[d], part);
   const float s = block_sum256(part, s_red);
   if (threadIdx.x == 0) a.scores[int64_t(b) * n + j] = s;
 }
 
-// grid (ceil(T / 64), B): rows t0 .. t0+63 of dh in full.
+// grid (ceil(T / 4), B), one wave per row t of dh, written in full:
 //   dh[t] = sum_{j: lo_j <= t < hi_j} ds_j h_ctx / (hi_j - lo_j)   (ascending j)
 //         + [t == mask] sum_j ds_j h_span_j                          (ascending j)
+// Columns go in groups of 512, lane l holding d0 + l + 64 k (k < 8).  The
+// spans containing t are found 64 at a time by a wave ballot over j and added
+// in ascending j; a row in no span (most rows) is written as zeros.
 template <class E>
 __global__ __launch_bounds__(256) void k_span_bwd(kd_span_args a) {
-  constexpr int ROWS = 64;
-  const int b = blockIdx.y, t0 = blockIdx.x * ROWS, n = a.n_spans, D = a.D;
-  const int t1 = min(a.T, t0 + ROWS);
+  const int lane = threadIdx.x & 63;
+  const int b = blockIdx.y, t = blockIdx.x * 4 + (threadIdx.x >> 6), n = a.n_spans, D = a.D;
+  if (t >= a.T) return;
   const int mp = a.mask_pos[b];
   const int32_t* lo = a.span_lo + int64_t(b) * n;
   const int32_t* hi = a.span_hi + int64_t(b) * n;
   const float* ds = a.dscores + int64_t(b) * n;
-  for (int t = t0; t < t1; ++t) {
-    uint16_t* out = static_cast<uint16_t*>(a.dh) + int64_t(b) * a.dh_strides[0] + int64_t(t) * a.dh_strides[1];
-    for (int d = threadIdx.x; d < D; d += 256) {
-      float g = 0.f;
-      const float c = a.h_ctx[int64_t(b) * D + d];
-      for (int j = 0; j < n; ++j)
-        if (lo[j] <= t && t < hi[j]) g += ds[j] * c / float(hi[j] - lo[j]);
-      if (t == mp)
-        for (int j = 0; j < n; ++j) g = __builtin_fmaf(ds[j], a.h_spans[(int64_t(b) * n + j) * D + d], g);
-      out[d] = uint16_t(pack2<E>(g, 0.f) & 0xFFFFu);
+  uint16_t* out = static_cast<uint16_t*>(a.dh) + int64_t(b) * a.dh_strides[0] + int64_t(t) * a.dh_strides[1];
+  for (int d0 = 0; d0 < D; d0 += 512) {
+    float c[8], g[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int d = d0 + lane + 64 * k;
+      c[k] = d < D ? a.h_ctx[int64_t(b) * D + d] : 0.f;
+      g[k] = 0.f;
+    }
+    for (int j0 = 0; j0 < n; j0 += 64) {
+      const int jl = j0 + lane;
+      const bool in = jl < n && lo[jl] <= t && t < hi[jl];
+      for (uint64_t m = __builtin_amdgcn_ballot_w64(in); m; m &= m - 1) {
+        const int j = j0 + __builtin_ctzll(m);
+        const float dsj = ds[j], len = float(hi[j] - lo[j]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) g[k] += dsj * c[k] / len;
+      }
+    }
+    if (t == mp)
+      for (int j = 0; j < n; ++j) {
+        const float dsj = ds[j];
+        const float* hs = a.h_spans + (int64_t(b) * n + j) * D;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int d = d0 + lane + 64 * k;
+          if (d < D) g[k] = __builtin_fmaf(dsj, hs[d], g[k]);
+        }
+      }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int d = d0 + lane + 64 * k;
+      if (d < D) out[d] = uint16_t(pack2<E>(g[k], 0.f) & 0xFFFFu);
     }
   }
 }
@@ -141,15 +193,17 @@ __global__ __launch_bounds__(256) void k_span_bwd(kd_span_args a) {
 
 int launch_span(const kd_span_args& a, hipStream_t st) {
   hipLaunchKernelGGL(k_span_find, dim3(unsigned(a.B)), dim3(1024), size_t(2) * a.n_spans * sizeof(int), st, a);
+  const dim3 pool(unsigned(a.n_spans + 1), unsigned(a.B), unsigned((a.D + 255) / 256));
   if (a.dtype == KD_BF16)
-    hipLaunchKernelGGL(k_span_pool<BF16>, dim3(unsigned(a.n_spans + 1), unsigned(a.B)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_span_pool<BF16>, pool, dim3(512), 0, st, a);
   else
-    hipLaunchKernelGGL(k_span_pool<F16>, dim3(unsigned(a.n_spans + 1), unsigned(a.B)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_span_pool<F16>, pool, dim3(512), 0, st, a);
+  hipLaunchKernelGGL(k_span_score, dim3(unsigned(a.n_spans), unsigned(a.B)), dim3(256), 0, st, a);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 
 int launch_span_bwd(const kd_span_args& a, hipStream_t st) {
-  const dim3 grid(unsigned((a.T + 63) / 64), unsigned(a.B));
+  const dim3 grid(unsigned((a.T + 3) / 4), unsigned(a.B));
   if (a.dtype == KD_BF16) hipLaunchKernelGGL(k_span_bwd<BF16>, grid, dim3(256), 0, st, a);
   else hipLaunchKernelGGL(k_span_bwd<F16>, grid, dim3(256), 0, st, a);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
