@@ -98,6 +98,23 @@ def test_malformed_rows_int32_tokens_strided_h(dev):
     _check(tokens, h, dev, seed=4, strided=True)
 
 
+def test_many_overlapping_spans_odd_width(dev):
+    """100 spans in a row (the backward's span ballot runs in two chunks of 64), a row
+    of 70 nested [SPAN]s then 70 [ES]s whose zipped interiors all overlap (a token
+    in up to 70 spans, added in ascending span order across the chunk boundary),
+    and widths that are not multiples of the kernels' 64- and 256-column chunks."""
+    T = 420
+    r0 = [MASK] + [SPAN, X, X, ES] * 100
+    r1 = [MASK] + [SPAN] * 70 + [X] * 5 + [ES] * 70
+    r2 = [X] * 3 + [MASK] + [SPAN, X, ES] * 40
+    rows = [r + [X] * (T - len(r)) for r in (r0, r1, r2)]
+    tokens = torch.tensor(rows, dtype=torch.int64)
+    g = torch.Generator().manual_seed(6)
+    for D in (300, 600):
+        h = torch.randn(3, T, D, generator=g).to(torch.bfloat16)
+        _check(tokens, h, dev, seed=D)
+
+
 def test_public_entry_and_errors(dev):
     tokens = torch.tensor([[MASK, SPAN, X, X, ES, X]], device=dev)
     h = torch.randn(1, 6, 64, device=dev).to(torch.bfloat16)
