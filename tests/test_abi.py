@@ -123,6 +123,9 @@ def test_bad_arguments_return_status_without_gpu():
     assert "rule" in lib.kd_last_error_string().decode()
     sp = _lib.SpanArgs()
     assert lib.kd_span_scores(None, null) == _lib.KD_ERR_INVALID
+    sp.B, sp.T, sp.D, sp.n_spans, sp.dtype = 2, 16, 65537, 3, _lib.KD_BF16
+    assert lib.kd_span_scores(ctypes.byref(sp), null) == _lib.KD_ERR_UNSUPPORTED  # D > 65536
+    assert lib.kd_span_scores_bwd(ctypes.byref(sp), null) == _lib.KD_ERR_UNSUPPORTED
     sp.B, sp.T, sp.D, sp.n_spans, sp.dtype = 2, 16, 64, 0, _lib.KD_BF16
     assert lib.kd_span_scores(ctypes.byref(sp), null) == _lib.KD_ERR_UNSUPPORTED  # n_spans 0
     sp.n_spans = 3
