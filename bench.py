@@ -262,7 +262,7 @@ class Step:
                 r.amax = self.amax[i].data_ptr()
         self.stream = torch.cuda.current_stream(dev)
         self.sptr = ctypes.c_void_p(self.stream.cuda_stream)
-        self.pptr = ctypes.c_void_p(self.plan.data_ptr())
+        self.pptr, self.pbytes = _lib.plan_ref(self.plan)
 
     def _rot_args(self, _lib, _dtype_code, _strides3, src, dst, inverse):
         r = _lib.RotArgs()
@@ -274,7 +274,7 @@ class Step:
 
     def launches(self):
         L, a, ck = self.lib, ctypes.byref(self.args), self._check
-        out = [("plan", lambda: ck(L.kd_plan_build(ctypes.byref(self.margs), self.pptr, self.sptr), "plan"))]
+        out = [("plan", lambda: ck(L.kd_plan_build(ctypes.byref(self.margs), self.pptr, self.pbytes, self.sptr), "plan"))]
         if self.hadamard:
             def rot():
                 if self.fp8:
@@ -292,9 +292,9 @@ class Step:
                     ck(L.kd_quant_fp8(ctypes.byref(qa), self.sptr), "quant")
             out.append(("quant", quant))
         out += [
-            ("fwd", lambda: ck(L.kd_attn_fwd(a, self.pptr, self.sptr), "fwd")),
-            ("dq", lambda: ck(L.kd_attn_bwd_dq_delta(a, self.pptr, self.sptr), "dq")),  # with Delta
-            ("dkdv", lambda: ck(L.kd_attn_bwd_dkdv(a, self.pptr, self.sptr), "dkdv")),
+            ("fwd", lambda: ck(L.kd_attn_fwd(a, self.pptr, self.pbytes, self.sptr), "fwd")),
+            ("dq", lambda: ck(L.kd_attn_bwd_dq_delta(a, self.pptr, self.pbytes, self.sptr), "dq")),  # with Delta
+            ("dkdv", lambda: ck(L.kd_attn_bwd_dkdv(a, self.pptr, self.pbytes, self.sptr), "dkdv")),
         ]
         return tuple(out)
 

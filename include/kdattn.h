@@ -199,7 +199,13 @@ void kd_struct_sizes(size_t *meta, size_t *attn);
 void kd_struct_sizes2(size_t *rot, size_t *quant);
 void kd_struct_sizes3(size_t *tokens);
 
-/* Workspace ("plan") bytes for B sequences of length T at head dim D, and
+/* Every entry point that reads or writes a plan takes the plan's size in bytes
+ * (plan_bytes) beside its pointer, and returns KD_ERR_INVALID, launching
+ * nothing, when it is below kd_plan_bytes(B, T, D) of the call's shape: the
+ * kernels index the plan by that layout.  The check is on the host, with no
+ * device access and no synchronisation.
+ *
+ * Workspace ("plan") bytes for B sequences of length T at head dim D, and
  * the byte offsets of its sections (token codes, class map, per-tile allowed
  * counts, the forward / dQ / dK-dV work lists, the work orders).  offsets[]
  * receives 19 int64: codes, rep, cls, nnz, fwd_list, fwd_count, dq_list,
@@ -219,18 +225,18 @@ int kd_plan_layout(int32_t B, int32_t T, int32_t D, int64_t *offsets);
  * 2 full, bit-exact against the dense mask), allowed-entry counts and the
  * per-block work lists.  Mask rules: original_kernel.py:478-517, with lens
  * (:299-303, :517) and the no-metadata fallbacks (:512-515). */
-int kd_plan_build(const kd_meta_args *meta, void *plan, void *stream);
+int kd_plan_build(const kd_meta_args *meta, void *plan, int64_t plan_bytes, void *stream);
 
 /* The plan straight from token ids: is_prefix, in_span and span_id are derived
  * on the device by the chosen rule (written into the plan's own workspace) and
  * the plan is then built as kd_plan_build would from them.  Replaces the
  * per-token Python loops with host syncs at data_builder.py:603-643,
  * model.py:209-240 and train_loop.py:406-435 ahead of the mask evaluation. */
-int kd_plan_build_tokens(const kd_token_args *t, void *plan, void *stream);
+int kd_plan_build_tokens(const kd_token_args *t, void *plan, int64_t plan_bytes, void *stream);
 
 /* Forward: O and LSE.  Replaces attention_forward_adapter's launch of
  * _flash_attn_fwd (original_kernel.py:1697-1778, kernel :279-626). */
-int kd_attn_fwd(const kd_attn_args *a, const void *plan, void *stream);
+int kd_attn_fwd(const kd_attn_args *a, const void *plan, int64_t plan_bytes, void *stream);
 
 /* -Delta = -rowsum(O * dO) in fp32 into a->delta[0 : B*H*T], and -LSE / c
  * (the form kd_attn_bwd_dkdv starts its score accumulators from; -inf for
@@ -241,21 +247,21 @@ int kd_attn_bwd_delta(const kd_attn_args *a, void *stream);
 
 /* dQ from the saved LSE and Delta.  Replaces the dQ workers of
  * _flash_attn_bwd (original_kernel.py:1173-1336). */
-int kd_attn_bwd_dq(const kd_attn_args *a, const void *plan, void *stream);
+int kd_attn_bwd_dq(const kd_attn_args *a, const void *plan, int64_t plan_bytes, void *stream);
 
 /* dQ that computes Delta and the LSE copy itself (from a->o, a->o_lo, a->lse)
  * and stores both halves of a->delta for kd_attn_bwd_dkdv: the work of
  * _flash_attn_bwd_precompute (original_kernel.py:649-710) and of the dQ
  * workers (:1173-1336) in one pass. */
-int kd_attn_bwd_dq_delta(const kd_attn_args *a, const void *plan, void *stream);
+int kd_attn_bwd_dq_delta(const kd_attn_args *a, const void *plan, int64_t plan_bytes, void *stream);
 
 /* dK and dV.  Replaces the dK/dV workers of _flash_attn_bwd
  * (original_kernel.py:1339-1525). */
-int kd_attn_bwd_dkdv(const kd_attn_args *a, const void *plan, void *stream);
+int kd_attn_bwd_dkdv(const kd_attn_args *a, const void *plan, int64_t plan_bytes, void *stream);
 
 /* Whole backward: dQ with Delta (kd_attn_bwd_dq_delta), then dK/dV.  Replaces
  * attention_backward_adapter (original_kernel.py:1806-1898). */
-int kd_attn_bwd(const kd_attn_args *a, const void *plan, void *stream);
+int kd_attn_bwd(const kd_attn_args *a, const void *plan, int64_t plan_bytes, void *stream);
 
 /* The whole backward as kd_attn_bwd, with a->delta ignored: its workspace
  * (2 * B*H*T floats) lives in a library-owned device array of
@@ -267,7 +273,7 @@ int kd_attn_bwd(const kd_attn_args *a, const void *plan, void *stream);
  * GPU uses that GPU's one array, so calls that overlap on one GPU (other
  * streams or threads) race and must be ordered by the caller. */
 #define KD_NOALLOC_WORKSPACE_FLOATS (1 << 22)
-int kd_attn_bwd_noalloc(const kd_attn_args *a, const void *plan, void *stream);
+int kd_attn_bwd_noalloc(const kd_attn_args *a, const void *plan, int64_t plan_bytes, void *stream);
 
 /* The 64-bit masks of every 64x64 tile of a built plan, from the same
  * functions the attention kernels apply to PARTIAL tiles: rows [B, nT, nT, 64]
@@ -275,12 +281,13 @@ int kd_attn_bwd_noalloc(const kd_attn_args *a, const void *plan, void *stream);
  * [B, nT, nT, 64] (bit r of entry j: query 64 qt + r may see key 64 kt + j).
  * An inspection aid (the kernels never store them); no reference counterpart,
  * the reference evaluates original_kernel.py:478-517 per element. */
-int kd_tile_masks(const void *plan, int32_t B, int32_t T, int32_t D, uint64_t *rows, uint64_t *cols, void *stream);
+int kd_tile_masks(const void *plan, int64_t plan_bytes, int32_t B, int32_t T, int32_t D, uint64_t *rows,
+                  uint64_t *cols, void *stream);
 
 /* Dense bool mask [B, H, T, T] (element strides b, h, q, k) from the plan's
  * codes.  Replaces the RETURN_ATTENTION_MASK store of _flash_attn_fwd
  * (original_kernel.py:519-545). */
-int kd_mask_dense(const void *plan, int32_t B, int32_t H, int32_t T, int32_t D, uint8_t *out,
+int kd_mask_dense(const void *plan, int64_t plan_bytes, int32_t B, int32_t H, int32_t T, int32_t D, uint8_t *out,
                   const int64_t *strides, void *stream);
 
 /* y = x R with R = diag(signs) H_D / sqrt(D) (or x R^T when inverse), per

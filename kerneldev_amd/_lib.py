@@ -118,22 +118,22 @@ SIGNATURES = {
     "kd_struct_sizes4": (None, [POINTER(c_size_t)]),
     "kd_span_scores": (c_int, [POINTER(SpanArgs), c_void_p]),
     "kd_span_scores_bwd": (c_int, [POINTER(SpanArgs), c_void_p]),
-    "kd_plan_build_tokens": (c_int, [POINTER(TokenArgs), c_void_p, c_void_p]),
+    "kd_plan_build_tokens": (c_int, [POINTER(TokenArgs), c_void_p, c_int64, c_void_p]),
     "kd_hadamard": (c_int, [POINTER(RotArgs), c_void_p]),
     "kd_quant_fp8": (c_int, [POINTER(QuantArgs), c_void_p]),
     "kd_plan_bytes": (c_int64, [c_int32, c_int32, c_int32]),
     "kd_plan_layout": (c_int, [c_int32, c_int32, c_int32, POINTER(c_int64)]),
-    "kd_plan_build": (c_int, [POINTER(MetaArgs), c_void_p, c_void_p]),
-    "kd_attn_fwd": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
+    "kd_plan_build": (c_int, [POINTER(MetaArgs), c_void_p, c_int64, c_void_p]),
+    "kd_attn_fwd": (c_int, [POINTER(AttnArgs), c_void_p, c_int64, c_void_p]),
     "kd_attn_bwd_delta": (c_int, [POINTER(AttnArgs), c_void_p]),
-    "kd_attn_bwd_dq": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
-    "kd_attn_bwd_dq_delta": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
-    "kd_attn_bwd_dkdv": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
-    "kd_attn_bwd": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
-    "kd_attn_bwd_noalloc": (c_int, [POINTER(AttnArgs), c_void_p, c_void_p]),
-    "kd_mask_dense": (c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p,
+    "kd_attn_bwd_dq": (c_int, [POINTER(AttnArgs), c_void_p, c_int64, c_void_p]),
+    "kd_attn_bwd_dq_delta": (c_int, [POINTER(AttnArgs), c_void_p, c_int64, c_void_p]),
+    "kd_attn_bwd_dkdv": (c_int, [POINTER(AttnArgs), c_void_p, c_int64, c_void_p]),
+    "kd_attn_bwd": (c_int, [POINTER(AttnArgs), c_void_p, c_int64, c_void_p]),
+    "kd_attn_bwd_noalloc": (c_int, [POINTER(AttnArgs), c_void_p, c_int64, c_void_p]),
+    "kd_mask_dense": (c_int, [c_void_p, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p,
                               POINTER(c_int64), c_void_p]),
-    "kd_tile_masks": (c_int, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
+    "kd_tile_masks": (c_int, [c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
 }
 
 _lib = None
@@ -182,6 +182,12 @@ def check(status: int, what: str):
         if status in (KD_ERR_INVALID, KD_ERR_UNSUPPORTED):
             raise ValueError(f"{what}: {msg}")
         raise KernelError(f"{what}: {msg} (status {status})")
+
+
+def plan_ref(plan) -> tuple:
+    """``(pointer, size in bytes)`` of a plan tensor, the pair every plan-taking
+    entry point receives (the library refuses a plan smaller than its shape needs)."""
+    return c_void_p(plan.data_ptr()), c_int64(plan.numel() * plan.element_size())
 
 
 def plan_bytes(B: int, T: int, D: int) -> int:

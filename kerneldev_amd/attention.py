@@ -113,7 +113,7 @@ def build_plan(B, T, D, device, mode, in_span=None, span_id=None, is_prefix=None
     if lens is not None:
         m.lens = lens.data_ptr()
         m.lens_stride = lens.stride(0)
-    _lib.check(lib.kd_plan_build(ctypes.byref(m), _ptr(plan), _stream(device)), "kd_plan_build")
+    _lib.check(lib.kd_plan_build(ctypes.byref(m), *_lib.plan_ref(plan), _stream(device)), "kd_plan_build")
     return plan
 
 
@@ -156,7 +156,7 @@ def build_plan_from_tokens(tokens: torch.Tensor, head_dim: int, rule: str = "col
     if lens is not None:
         t.lens, t.lens_stride = lens.data_ptr(), lens.stride(0)
     t.B, t.T, t.D = B, T, head_dim
-    _lib.check(_lib.load().kd_plan_build_tokens(ctypes.byref(t), _ptr(plan), _stream(tokens.device)),
+    _lib.check(_lib.load().kd_plan_build_tokens(ctypes.byref(t), *_lib.plan_ref(plan), _stream(tokens.device)),
                "kd_plan_build_tokens")
     return AttentionPlan(plan, B, T, head_dim)
 
@@ -239,7 +239,7 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
     a.o, a.o_strides = o.data_ptr(), _strides3(o)
     a.lse = lse.data_ptr()
     a.o_lo = o_lo.data_ptr() if need_lo else None
-    _lib.check(_lib.load().kd_attn_fwd(ctypes.byref(a), _ptr(plan), _stream(q.device)), "kd_attn_fwd")
+    _lib.check(_lib.load().kd_attn_fwd(ctypes.byref(a), *_lib.plan_ref(plan), _stream(q.device)), "kd_attn_fwd")
     return o, lse, (plan if plan_in is None else plan.new_empty(0)), o_lo, q_r, k_r, q8_o, k8_o, qs_o, ks_o
 
 
@@ -285,7 +285,7 @@ def _bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, 
     a.o_lo = o_lo.data_ptr() if o_lo.numel() > 0 else None
     _set_fp8(a, _fp8_tuple(q8, k8, q_scale, k_scale))
     a.dqk_signs = dqk_signs.data_ptr() if dqk_signs is not None else None
-    _lib.check(_lib.load().kd_attn_bwd(ctypes.byref(a), _ptr(plan), _stream(q.device)), "kd_attn_bwd")
+    _lib.check(_lib.load().kd_attn_bwd(ctypes.byref(a), *_lib.plan_ref(plan), _stream(q.device)), "kd_attn_bwd")
     return dq, dk, dv
 
 
@@ -384,7 +384,7 @@ def _fwd_x3_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Te
     a.o, a.o_strides = ox.data_ptr(), _strides3(ox)
     a.lse = lse.data_ptr()
     a.o_lo = ox_lo.data_ptr()
-    _lib.check(_lib.load().kd_attn_fwd(ctypes.byref(a), _ptr(plan), _stream(q.device)), "kd_attn_fwd")
+    _lib.check(_lib.load().kd_attn_fwd(ctypes.byref(a), *_lib.plan_ref(plan), _stream(q.device)), "kd_attn_fwd")
     o = _new_out(B, H, T, d, q, bthd)
     o.copy_(_hi_lo(ox, ox_lo, d, 1))
     return o, lse, (plan if plan_in is None else plan.new_empty(0))
@@ -423,8 +423,8 @@ def _bwd_x3_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tenso
     a.dq_lo, a.dk_lo, a.dv_lo = dq_lo.data_ptr(), dk_lo.data_ptr(), dv_lo.data_ptr()
     a.delta = ws.data_ptr()
     lib, st = _lib.load(), _stream(q.device)
-    _lib.check(lib.kd_attn_bwd_dq(ctypes.byref(a), _ptr(plan), st), "kd_attn_bwd_dq")
-    _lib.check(lib.kd_attn_bwd_dkdv(ctypes.byref(a), _ptr(plan), st), "kd_attn_bwd_dkdv")
+    _lib.check(lib.kd_attn_bwd_dq(ctypes.byref(a), *_lib.plan_ref(plan), st), "kd_attn_bwd_dq")
+    _lib.check(lib.kd_attn_bwd_dkdv(ctypes.byref(a), *_lib.plan_ref(plan), st), "kd_attn_bwd_dkdv")
     return _hi_lo(dqx, dq_lo, d, 1), _hi_lo(dkx, dk_lo, d, 2), _hi_lo(dvx, dv_lo, d, 2)
 
 
@@ -623,7 +623,7 @@ def flash_attention(
     if return_attention_mask:
         mask = torch.empty((B, H, T, T), dtype=torch.bool, device=device)
         st = (ctypes.c_int64 * 4)(*mask.stride())
-        _lib.check(_lib.load().kd_mask_dense(_ptr(plan_t), B, H, T, D, _ptr(mask), st, _stream(device)),
+        _lib.check(_lib.load().kd_mask_dense(*_lib.plan_ref(plan_t), B, H, T, D, _ptr(mask), st, _stream(device)),
                    "kd_mask_dense")
     if return_attention_mask:
         if return_lse:
@@ -669,7 +669,7 @@ def tile_masks(plan: torch.Tensor, B: int, T: int, D: int):
     nT = (T + 63) // 64
     rows = torch.empty((B, nT, nT, 64), dtype=torch.int64, device=plan.device)
     cols = torch.empty_like(rows)
-    _lib.check(_lib.load().kd_tile_masks(_ptr(plan), B, T, D, _ptr(rows), _ptr(cols), _stream(plan.device)),
+    _lib.check(_lib.load().kd_tile_masks(*_lib.plan_ref(plan), B, T, D, _ptr(rows), _ptr(cols), _stream(plan.device)),
                "kd_tile_masks")
     return rows, cols
 

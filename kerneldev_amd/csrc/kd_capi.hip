@@ -98,11 +98,27 @@ int check_span(const kd_span_args* a) {
   return KD_OK;
 }
 
+// A plan buffer handed in by the caller: present, aligned, and at least as
+// large as the layout of this shape needs (kd_plan_bytes).  The kernels index
+// the plan by that layout, so a smaller buffer is refused here, on the host,
+// before anything is launched.
+int check_plan(const void* plan, int64_t plan_bytes, int B, int T, int D) {
+  if (plan == nullptr) return fail(KD_ERR_INVALID, "plan is NULL");
+  if (!aligned16(plan)) return fail(KD_ERR_INVALID, "plan must be 16-byte aligned");
+  const int64_t need = int64_t(kd::plan_layout(B, T, D).total);
+  if (plan_bytes < need) {
+    g_err = "plan is " + std::to_string(plan_bytes) + " bytes; B = " + std::to_string(B) + ", T = " +
+            std::to_string(T) + " needs " + std::to_string(need) + " (kd_plan_bytes)";
+    return KD_ERR_INVALID;
+  }
+  return KD_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
-int kd_version(void) { return 206; }
+int kd_version(void) { return 30000; }
 
 const char* kd_last_error_string(void) { return g_err.c_str(); }
 
@@ -145,11 +161,11 @@ int kd_span_scores_bwd(const kd_span_args* a, void* stream) {
   return r ? fail(r, "kernel launch failed (span scores backward)") : KD_OK;
 }
 
-int kd_plan_build_tokens(const kd_token_args* t, void* plan, void* stream) {
-  if (t == nullptr || plan == nullptr) return fail(KD_ERR_INVALID, "args or plan is NULL");
-  if (!aligned16(plan)) return fail(KD_ERR_INVALID, "plan must be 16-byte aligned");
+int kd_plan_build_tokens(const kd_token_args* t, void* plan, int64_t plan_bytes, void* stream) {
+  if (t == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
   if (t->B < 1 || t->T < 1) return fail(KD_ERR_INVALID, "B and T must be >= 1");
   if (t->T > (1 << 24) - 2) return fail(KD_ERR_UNSUPPORTED, "T must be < 2^24 - 1");
+  if (int r = check_plan(plan, plan_bytes, t->B, t->T, t->D)) return r;
   if (t->tokens == nullptr) return fail(KD_ERR_INVALID, "tokens is NULL");
   if (t->tokens_dtype != KD_I64 && t->tokens_dtype != KD_I32)
     return fail(KD_ERR_INVALID, "tokens dtype must be int64 or int32");
@@ -211,11 +227,11 @@ int kd_plan_layout(int32_t B, int32_t T, int32_t D, int64_t* off) {
   return KD_OK;
 }
 
-int kd_plan_build(const kd_meta_args* m, void* plan, void* stream) {
-  if (m == nullptr || plan == nullptr) return fail(KD_ERR_INVALID, "meta or plan is NULL");
-  if (!aligned16(plan)) return fail(KD_ERR_INVALID, "plan must be 16-byte aligned");
+int kd_plan_build(const kd_meta_args* m, void* plan, int64_t plan_bytes, void* stream) {
+  if (m == nullptr) return fail(KD_ERR_INVALID, "meta is NULL");
   if (m->B < 1 || m->T < 1) return fail(KD_ERR_INVALID, "B and T must be >= 1");
   if (m->T > (1 << 24) - 2) return fail(KD_ERR_UNSUPPORTED, "T must be < 2^24 - 1");
+  if (int r = check_plan(plan, plan_bytes, m->B, m->T, m->D)) return r;
   if (m->mode != KD_MODE_FORMULA && m->mode != KD_MODE_CAUSAL && m->mode != KD_MODE_ALL)
     return fail(KD_ERR_INVALID, "unknown mask mode");
   if (m->span_id != nullptr && m->span_id_dtype != KD_I64 && m->span_id_dtype != KD_I32)
@@ -236,11 +252,11 @@ static int check_fp8(const kd_attn_args* a) {
   return KD_OK;
 }
 
-int kd_attn_fwd(const kd_attn_args* a, const void* plan, void* stream) {
+int kd_attn_fwd(const kd_attn_args* a, const void* plan, int64_t plan_bytes, void* stream) {
   int r = check_common(a);
   if (r) return r;
   if ((r = check_fp8(a))) return r;
-  if (plan == nullptr) return fail(KD_ERR_INVALID, "plan is NULL");
+  if ((r = check_plan(plan, plan_bytes, a->B, a->T, a->D))) return r;
   if ((r = check_tensor(a->q, a->q_strides, "q", a->T, a->D, esz(a))) || (r = check_tensor(a->k, a->k_strides, "k", a->T, a->D, esz(a))) ||
       (r = check_tensor(a->v, a->v_strides, "v", a->T, a->D, esz(a))) || (r = check_tensor(a->o, a->o_strides, "o", a->T, a->D, esz(a))))
     return r;
@@ -260,12 +276,14 @@ int kd_attn_bwd_delta(const kd_attn_args* a, void* stream) {
   return r ? fail(r, "kernel launch failed (delta)") : KD_OK;
 }
 
-static int check_bwd(const kd_attn_args* a, const void* plan) {
+// own_workspace: the library provides a->delta (kd_attn_bwd_noalloc)
+static int check_bwd(const kd_attn_args* a, const void* plan, int64_t plan_bytes, bool own_workspace = false) {
   int r = check_common(a);
   if (r) return r;
   if ((r = check_fp8(a))) return r;
-  if (plan == nullptr) return fail(KD_ERR_INVALID, "plan is NULL");
-  if (a->lse == nullptr || a->delta == nullptr) return fail(KD_ERR_INVALID, "lse and delta are required");
+  if ((r = check_plan(plan, plan_bytes, a->B, a->T, a->D))) return r;
+  if (a->lse == nullptr || (a->delta == nullptr && !own_workspace))
+    return fail(KD_ERR_INVALID, "lse and delta are required");
   if (a->dq_lo != nullptr || a->dk_lo != nullptr || a->dv_lo != nullptr) {
     if (kd::use_simt(*a) || a->dqk_signs != nullptr)
       return fail(KD_ERR_UNSUPPORTED, "dq_lo / dk_lo / dv_lo are built for bf16 / fp16 at head dim 64, 128 or 256, "
@@ -279,24 +297,24 @@ static int check_bwd(const kd_attn_args* a, const void* plan) {
   return KD_OK;
 }
 
-int kd_attn_bwd_dq(const kd_attn_args* a, const void* plan, void* stream) {
-  int r = check_bwd(a, plan);
+int kd_attn_bwd_dq(const kd_attn_args* a, const void* plan, int64_t plan_bytes, void* stream) {
+  int r = check_bwd(a, plan, plan_bytes);
   if (r) return r;
   if ((r = check_tensor(a->dq, a->dq_strides, "dq", a->T, a->D, esz(a)))) return r;
   r = kd::launch_dq(*a, static_cast<const uint8_t*>(plan), as_stream(stream), false);
   return r ? fail(r, "kernel launch failed (dq)") : KD_OK;
 }
 
-int kd_attn_bwd_dkdv(const kd_attn_args* a, const void* plan, void* stream) {
-  int r = check_bwd(a, plan);
+int kd_attn_bwd_dkdv(const kd_attn_args* a, const void* plan, int64_t plan_bytes, void* stream) {
+  int r = check_bwd(a, plan, plan_bytes);
   if (r) return r;
   if ((r = check_tensor(a->dk, a->dk_strides, "dk", a->T, a->D, esz(a))) || (r = check_tensor(a->dv, a->dv_strides, "dv", a->T, a->D, esz(a)))) return r;
   r = kd::launch_dkdv(*a, static_cast<const uint8_t*>(plan), as_stream(stream));
   return r ? fail(r, "kernel launch failed (dkdv)") : KD_OK;
 }
 
-int kd_attn_bwd_dq_delta(const kd_attn_args* a, const void* plan, void* stream) {
-  int r = check_bwd(a, plan);
+int kd_attn_bwd_dq_delta(const kd_attn_args* a, const void* plan, int64_t plan_bytes, void* stream) {
+  int r = check_bwd(a, plan, plan_bytes);
   if (r) return r;
   if ((r = check_tensor(a->o, a->o_strides, "o", a->T, a->D, esz(a))) || (r = check_tensor(a->dq, a->dq_strides, "dq", a->T, a->D, esz(a))))
     return r;
@@ -305,38 +323,59 @@ int kd_attn_bwd_dq_delta(const kd_attn_args* a, const void* plan, void* stream) 
   return r ? fail(r, "kernel launch failed (dq)") : KD_OK;
 }
 
-int kd_attn_bwd(const kd_attn_args* a, const void* plan, void* stream) {
-  const int r = kd_attn_bwd_dq_delta(a, plan, stream);
-  return r ? r : kd_attn_bwd_dkdv(a, plan, stream);
+// Every check of kd_attn_bwd_dq_delta and kd_attn_bwd_dkdv, so that the
+// whole backward is refused before either half is launched.
+static int check_bwd_all(const kd_attn_args* a, const void* plan, int64_t plan_bytes, bool own_workspace = false) {
+  int r = check_bwd(a, plan, plan_bytes, own_workspace);
+  if (r) return r;
+  if ((r = check_tensor(a->o, a->o_strides, "o", a->T, a->D, esz(a))) ||
+      (r = check_tensor(a->dq, a->dq_strides, "dq", a->T, a->D, esz(a))) ||
+      (r = check_tensor(a->dk, a->dk_strides, "dk", a->T, a->D, esz(a))) ||
+      (r = check_tensor(a->dv, a->dv_strides, "dv", a->T, a->D, esz(a))))
+    return r;
+  return check_o_lo(a);
 }
 
-int kd_attn_bwd_noalloc(const kd_attn_args* a, const void* plan, void* stream) {
+int kd_attn_bwd(const kd_attn_args* a, const void* plan, int64_t plan_bytes, void* stream) {
+  int r = check_bwd_all(a, plan, plan_bytes);
+  if (r) return r;
+  r = kd_attn_bwd_dq_delta(a, plan, plan_bytes, stream);
+  return r ? r : kd_attn_bwd_dkdv(a, plan, plan_bytes, stream);
+}
+
+int kd_attn_bwd_noalloc(const kd_attn_args* a, const void* plan, int64_t plan_bytes, void* stream) {
   if (a == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
   if (a->B >= 1 && a->H >= 1 && a->T >= 1 &&
       2 * int64_t(a->B) * a->H * a->T > int64_t(KD_NOALLOC_WORKSPACE_FLOATS))
     return fail(KD_ERR_UNSUPPORTED,
                 "kd_attn_bwd_noalloc: B * H * T exceeds the workspace (KD_NOALLOC_WORKSPACE_FLOATS / 2 rows)");
+  int r = check_bwd_all(a, plan, plan_bytes, true);  // every refusal before the device is touched
+  if (r) return r;
   kd_attn_args w = *a;
   const char* err = nullptr;
   float* ws = nullptr;
-  int r = kd::noalloc_workspace(&ws, &err);
+  r = kd::noalloc_workspace(&ws, &err);
   if (r) return fail(r, err);
   w.delta = ws;
-  return kd_attn_bwd(&w, plan, stream);
+  return kd_attn_bwd(&w, plan, plan_bytes, stream);
 }
 
-int kd_tile_masks(const void* plan, int32_t B, int32_t T, int32_t D, uint64_t* rows, uint64_t* cols, void* stream) {
-  if (plan == nullptr || rows == nullptr || cols == nullptr) return fail(KD_ERR_INVALID, "NULL argument");
+int kd_tile_masks(const void* plan, int64_t plan_bytes, int32_t B, int32_t T, int32_t D, uint64_t* rows,
+                  uint64_t* cols, void* stream) {
+  if (rows == nullptr || cols == nullptr) return fail(KD_ERR_INVALID, "NULL argument");
   if (B < 1 || T < 1) return fail(KD_ERR_INVALID, "B and T must be >= 1");
   if (T > (1 << 24) - 2) return fail(KD_ERR_UNSUPPORTED, "T must be < 2^24 - 1");
+  if (int r = check_plan(plan, plan_bytes, B, T, D)) return r;
   const int r = kd::launch_tile_masks(static_cast<const uint8_t*>(plan), B, T, D, rows, cols, as_stream(stream));
   return r ? fail(r, "kernel launch failed (tile masks)") : KD_OK;
 }
 
-int kd_mask_dense(const void* plan, int32_t B, int32_t H, int32_t T, int32_t D, uint8_t* out,
+int kd_mask_dense(const void* plan, int64_t plan_bytes, int32_t B, int32_t H, int32_t T, int32_t D, uint8_t* out,
                   const int64_t* strides, void* stream) {
-  if (plan == nullptr || out == nullptr || strides == nullptr) return fail(KD_ERR_INVALID, "NULL argument");
+  if (out == nullptr || strides == nullptr) return fail(KD_ERR_INVALID, "NULL argument");
   if (B < 1 || H < 1 || T < 1) return fail(KD_ERR_INVALID, "B, H and T must be >= 1");
+  if (T > (1 << 24) - 2) return fail(KD_ERR_UNSUPPORTED, "T must be < 2^24 - 1");
+  if (int r = check_plan(plan, plan_bytes, B, T, D)) return r;
   for (int i = 0; i < 4; ++i)
     if (strides[i] < 0) return fail(KD_ERR_INVALID, "mask strides must be non-negative");
   const kd::PlanLayout L = kd::plan_layout(B, T, D);

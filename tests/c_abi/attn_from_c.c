@@ -86,7 +86,7 @@ int main(void) {
     }
 
   /* the error path needs no GPU: a NULL argument struct is refused */
-  if (kd_attn_fwd(NULL, NULL, NULL) != KD_ERR_INVALID || strlen(kd_last_error_string()) == 0) {
+  if (kd_attn_fwd(NULL, NULL, 0, NULL) != KD_ERR_INVALID || strlen(kd_last_error_string()) == 0) {
     fprintf(stderr, "NULL args were not refused\n");
     return 1;
   }
@@ -118,7 +118,7 @@ int main(void) {
   m.T = T;
   m.D = D;
   m.mode = KD_MODE_CAUSAL;
-  KD_OK_OR_FAIL(kd_plan_build(&m, plan, NULL), "kd_plan_build");
+  KD_OK_OR_FAIL(kd_plan_build(&m, plan, pbytes, NULL), "kd_plan_build");
 
   kd_attn_args a;
   memset(&a, 0, sizeof a);
@@ -144,8 +144,14 @@ int main(void) {
   a.dtype = KD_BF16;
   a.sm_scale = scale;
   a.precision = KD_PREC_SPLIT;
-  KD_OK_OR_FAIL(kd_attn_fwd(&a, plan, NULL), "kd_attn_fwd");
-  KD_OK_OR_FAIL(kd_attn_bwd(&a, plan, NULL), "kd_attn_bwd");
+  /* a plan buffer smaller than the shape needs is refused before any launch */
+  if (kd_attn_fwd(&a, plan, pbytes - 1, NULL) != KD_ERR_INVALID ||
+      kd_attn_bwd(&a, plan, pbytes - 1, NULL) != KD_ERR_INVALID) {
+    fprintf(stderr, "an undersized plan was not refused\n");
+    return 1;
+  }
+  KD_OK_OR_FAIL(kd_attn_fwd(&a, plan, pbytes, NULL), "kd_attn_fwd");
+  KD_OK_OR_FAIL(kd_attn_bwd(&a, plan, pbytes, NULL), "kd_attn_bwd");
   HIP_OK(hipDeviceSynchronize());
   void* outs[4] = {o, dq, dk, dv};
   for (int i = 0; i < 4; ++i) {

@@ -13,6 +13,9 @@ import torch
 from kerneldev_amd import _lib, flash_attention
 from kerneldev_amd.attention import REFERENCE_HEAD_DIMS
 
+# a plan size no shape in these tests exceeds (the calls fail on other arguments first)
+BIG = 1 << 40
+
 HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "kdattn.h")
 
 
@@ -35,7 +38,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_struct_layouts_and_version():
     lib = _lib.load()  # load() itself checks the three struct sizes
-    assert lib.kd_version() >= 100
+    assert lib.kd_version() >= 30000  # 3.0: plan sizes at the boundary
     assert ctypes.sizeof(_lib.AttnArgs) % 8 == 0
 
 
@@ -55,50 +58,50 @@ def test_plan_sizes_and_layout_offsets():
 def test_bad_arguments_return_status_without_gpu():
     lib = _lib.load()
     null = ctypes.c_void_p(0)
-    assert lib.kd_attn_fwd(None, null, null) == _lib.KD_ERR_INVALID
+    assert lib.kd_attn_fwd(None, null, 0, null) == _lib.KD_ERR_INVALID
     assert "NULL" in lib.kd_last_error_string().decode()
     a = _lib.AttnArgs()
     a.B, a.H, a.T, a.D, a.dtype, a.sm_scale = 1, 1, 16, 96, _lib.KD_BF16, 0.1
-    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_UNSUPPORTED
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_UNSUPPORTED
     a.D, a.dtype = 64, 5
-    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_UNSUPPORTED
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_UNSUPPORTED
     a.D, a.dtype, a.dqk_signs = 256, _lib.KD_BF16, 64  # the fused un-rotation is built for D 64 / 128
-    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_UNSUPPORTED
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_UNSUPPORTED
     assert "dqk_signs" in lib.kd_last_error_string().decode()
     a.dqk_signs = None
     a.D = 64
     a.sm_scale = float("nan")
-    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_INVALID
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID
     a.sm_scale = 0.125
-    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_INVALID  # q is NULL
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID  # q is NULL
     a.q = a.k = a.v = a.o = 32
     a.q_strides[:] = [1024, 1024, 8]  # t stride < head dim: rows overlap
-    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_INVALID
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID
     assert "overlap" in lib.kd_last_error_string().decode()
     a.q_strides[:] = [1024, 1024, 64]
     a.q8 = 64  # fp8 operands: q8 without k8, then head dim 64
-    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_INVALID
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID
     assert "q8 and k8" in lib.kd_last_error_string().decode()
     a.k8 = 64
-    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_UNSUPPORTED
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_UNSUPPORTED
     a.D = 128
     a.q_strides[:] = [1024, 1024, 128]
-    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), null) == _lib.KD_ERR_INVALID  # no scales
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID  # no scales
     assert "scale" in lib.kd_last_error_string().decode()
     b = _lib.AttnArgs()  # the backward's rounding-residual outputs: 16-bit MFMA paths only, aligned
     b.B, b.H, b.T, b.D, b.dtype, b.sm_scale = 1, 1, 16, 64, _lib.KD_F32, 0.125
     b.lse, b.delta, b.dq_lo = 64, 64, 64
-    assert lib.kd_attn_bwd(ctypes.byref(b), ctypes.c_void_p(256), null) == _lib.KD_ERR_UNSUPPORTED
+    assert lib.kd_attn_bwd(ctypes.byref(b), ctypes.c_void_p(256), BIG, null) == _lib.KD_ERR_UNSUPPORTED
     assert "dq_lo" in lib.kd_last_error_string().decode()
     b.dtype, b.dq_lo, b.dv_lo = _lib.KD_BF16, None, 72
-    assert lib.kd_attn_bwd(ctypes.byref(b), ctypes.c_void_p(256), null) == _lib.KD_ERR_INVALID
+    assert lib.kd_attn_bwd(ctypes.byref(b), ctypes.c_void_p(256), BIG, null) == _lib.KD_ERR_INVALID
     assert "aligned" in lib.kd_last_error_string().decode()
     c = _lib.AttnArgs()  # O's rounding residual is for 16-bit O: fp32 inputs with o_lo are refused
     c.B, c.H, c.T, c.D, c.dtype, c.sm_scale = 1, 1, 16, 64, _lib.KD_F32, 0.125
     c.q = c.k = c.v = c.o = c.o_lo = 64
     for st in (c.q_strides, c.k_strides, c.v_strides, c.o_strides):
         st[:] = [1024, 1024, 64]
-    assert lib.kd_attn_fwd(ctypes.byref(c), ctypes.c_void_p(256), null) == _lib.KD_ERR_INVALID
+    assert lib.kd_attn_fwd(ctypes.byref(c), ctypes.c_void_p(256), BIG, null) == _lib.KD_ERR_INVALID
     assert "o_lo" in lib.kd_last_error_string().decode()
     r = _lib.RotArgs()
     r.B, r.H, r.T, r.D, r.dtype = 1, 1, 4, 48, _lib.KD_BF16
@@ -114,12 +117,12 @@ def test_bad_arguments_return_status_without_gpu():
     assert lib.kd_quant_fp8(ctypes.byref(qa), null) == _lib.KD_ERR_UNSUPPORTED
     m = _lib.MetaArgs()
     m.B, m.T, m.mode = 1, 8, 7
-    assert lib.kd_plan_build(ctypes.byref(m), ctypes.c_void_p(256), null) == _lib.KD_ERR_INVALID
+    assert lib.kd_plan_build(ctypes.byref(m), ctypes.c_void_p(256), BIG, null) == _lib.KD_ERR_INVALID
     t = _lib.TokenArgs()
     t.B, t.T, t.D, t.rule = 1, 8, 64, 0
-    assert lib.kd_plan_build_tokens(ctypes.byref(t), ctypes.c_void_p(256), null) == _lib.KD_ERR_INVALID  # no tokens
+    assert lib.kd_plan_build_tokens(ctypes.byref(t), ctypes.c_void_p(256), BIG, null) == _lib.KD_ERR_INVALID  # no tokens
     t.tokens, t.rule = 64, 9
-    assert lib.kd_plan_build_tokens(ctypes.byref(t), ctypes.c_void_p(256), null) == _lib.KD_ERR_INVALID
+    assert lib.kd_plan_build_tokens(ctypes.byref(t), ctypes.c_void_p(256), BIG, null) == _lib.KD_ERR_INVALID
     assert "rule" in lib.kd_last_error_string().decode()
     sp = _lib.SpanArgs()
     assert lib.kd_span_scores(None, null) == _lib.KD_ERR_INVALID
@@ -166,8 +169,54 @@ def test_python_plan_size_matches_the_library():
     """plan_nbytes (the fake kernels' SymInt-friendly plan size) == kd_plan_bytes."""
     for B in (1, 2, 3, 8):
         for T in (1, 17, 63, 64, 65, 127, 128, 129, 300, 1024, 8192, 8193):
-            for D in (64, 128):
+            for D in REFERENCE_HEAD_DIMS:
                 assert _lib.plan_nbytes(B, T, D) == _lib.plan_bytes(B, T, D), (B, T, D)
+
+
+def test_undersized_plan_is_refused_before_any_launch():
+    """Every entry point that reads or writes a plan refuses one smaller than
+    kd_plan_bytes of its shape, with KD_ERR_INVALID and a message naming both
+    sizes, before anything else is looked at that needs the GPU (there is none
+    here: a launch would return KD_ERR_LAUNCH)."""
+    lib = _lib.load()
+    null = ctypes.c_void_p(0)
+    B, H, T, D = 2, 3, 1000, 64
+    need = _lib.plan_bytes(B, T, D)
+    plan = ctypes.c_void_p(1 << 20)  # aligned stand-in; never dereferenced on the host
+    a = _lib.AttnArgs()
+    a.B, a.H, a.T, a.D, a.dtype, a.sm_scale = B, H, T, D, _lib.KD_BF16, 0.125
+    a.lse, a.delta = 256, 256
+    m = _lib.MetaArgs()
+    m.B, m.T, m.D, m.mode = B, T, D, _lib.KD_MODE_CAUSAL
+    t = _lib.TokenArgs()
+    t.B, t.T, t.D, t.tokens = B, T, D, 256
+    rows = ctypes.c_void_p(256)
+    st = (ctypes.c_int64 * 4)(1, 1, 1, 1)
+    calls = {
+        "kd_plan_build": lambda n: lib.kd_plan_build(ctypes.byref(m), plan, n, null),
+        "kd_plan_build_tokens": lambda n: lib.kd_plan_build_tokens(ctypes.byref(t), plan, n, null),
+        "kd_attn_fwd": lambda n: lib.kd_attn_fwd(ctypes.byref(a), plan, n, null),
+        "kd_attn_bwd_dq": lambda n: lib.kd_attn_bwd_dq(ctypes.byref(a), plan, n, null),
+        "kd_attn_bwd_dq_delta": lambda n: lib.kd_attn_bwd_dq_delta(ctypes.byref(a), plan, n, null),
+        "kd_attn_bwd_dkdv": lambda n: lib.kd_attn_bwd_dkdv(ctypes.byref(a), plan, n, null),
+        "kd_attn_bwd": lambda n: lib.kd_attn_bwd(ctypes.byref(a), plan, n, null),
+        "kd_attn_bwd_noalloc": lambda n: lib.kd_attn_bwd_noalloc(ctypes.byref(a), plan, n, null),
+        "kd_tile_masks": lambda n: lib.kd_tile_masks(plan, n, B, T, D, rows, rows, null),
+        "kd_mask_dense": lambda n: lib.kd_mask_dense(plan, n, B, H, T, D, rows, st, null),
+    }
+    for name, call in calls.items():
+        for n in (0, need - 1):
+            assert call(n) == _lib.KD_ERR_INVALID, name
+            msg = lib.kd_last_error_string().decode()
+            assert f"plan is {n} bytes" in msg and f"needs {need}" in msg, (name, msg)
+        if name.startswith("kd_attn"):
+            # with the full size the plan passes, and the call stops at the next
+            # argument check, still on the host: q is NULL
+            assert call(need) == _lib.KD_ERR_INVALID, name
+            msg = lib.kd_last_error_string().decode()
+            assert "plan is" not in msg and "q is NULL" in msg, (name, msg)
+    # kd_attn_bwd checks both halves before it launches either
+    assert calls["kd_attn_bwd"](need - 1) == _lib.KD_ERR_INVALID
 
 
 def test_c_caller_is_built_against_the_library():

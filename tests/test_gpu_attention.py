@@ -569,10 +569,10 @@ def test_split_backward_entry_points_match_fused(dev):
         a.delta = delta.data_ptr()
         if split:
             _lib.check(lib.kd_attn_bwd_delta(ctypes.byref(a), stream), "delta")
-            _lib.check(lib.kd_attn_bwd_dq(ctypes.byref(a), _ptr(plan), stream), "dq")
-            _lib.check(lib.kd_attn_bwd_dkdv(ctypes.byref(a), _ptr(plan), stream), "dkdv")
+            _lib.check(lib.kd_attn_bwd_dq(ctypes.byref(a), *_lib.plan_ref(plan), stream), "dq")
+            _lib.check(lib.kd_attn_bwd_dkdv(ctypes.byref(a), *_lib.plan_ref(plan), stream), "dkdv")
         else:
-            _lib.check(lib.kd_attn_bwd(ctypes.byref(a), _ptr(plan), stream), "bwd")
+            _lib.check(lib.kd_attn_bwd(ctypes.byref(a), *_lib.plan_ref(plan), stream), "bwd")
         torch.cuda.synchronize()
         outs.append((dq, dk, dv, delta))
     # the two Delta sums differ in order only: gradients agree to within a bf16 ulp

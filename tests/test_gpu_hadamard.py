@@ -114,7 +114,7 @@ def test_backward_epilogue_rotation_matches_separate_pass(dev):
             a.dq_strides, a.dk_strides, a.dv_strides = _strides3(dq), _strides3(dk), _strides3(dv)
             a.delta = delta.data_ptr()
             a.dqk_signs = signs.data_ptr() if fused else None
-            _lib.check(lib.kd_attn_bwd(ctypes.byref(a), _ptr(plan), stream), "bwd")
+            _lib.check(lib.kd_attn_bwd(ctypes.byref(a), *_lib.plan_ref(plan), stream), "bwd")
             if not fused:
                 dq, dk = hadamard_transform(dq, signs, inverse=True), hadamard_transform(dk, signs, inverse=True)
             torch.cuda.synchronize()

@@ -34,11 +34,11 @@ def _backward_both(dev, B, H, T, D, seed):
         a.dq_strides, a.dk_strides, a.dv_strides = _strides3(dq), _strides3(dk), _strides3(dv)
         if noalloc:
             a.delta = None  # ignored: the library's own workspace is used
-            _lib.check(lib.kd_attn_bwd_noalloc(ctypes.byref(a), _ptr(plan), stream), "kd_attn_bwd_noalloc")
+            _lib.check(lib.kd_attn_bwd_noalloc(ctypes.byref(a), *_lib.plan_ref(plan), stream), "kd_attn_bwd_noalloc")
         else:
             delta = torch.empty((2, B, H, T), dtype=torch.float32, device=dev)
             a.delta = delta.data_ptr()
-            _lib.check(lib.kd_attn_bwd(ctypes.byref(a), _ptr(plan), stream), "kd_attn_bwd")
+            _lib.check(lib.kd_attn_bwd(ctypes.byref(a), *_lib.plan_ref(plan), stream), "kd_attn_bwd")
         torch.cuda.synchronize()
         outs.append((dq, dk, dv))
     return outs
