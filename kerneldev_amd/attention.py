@@ -22,6 +22,7 @@ from __future__ import annotations
 import ctypes
 import math
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -410,9 +411,12 @@ def _bwd_x3_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tenso
     # -Delta with Delta = rowsum(dO O) in fp32, then -LSE / c (-inf where LSE is)
     ws = torch.empty((2, B, H, T), dtype=torch.float32, device=q.device)
     torch.sum(do.to(torch.float32) * o.to(torch.float32), dim=-1, out=ws[0]).neg_()
-    c = torch.tensor(sm_scale, dtype=torch.float32) * torch.tensor(LOG2E, dtype=torch.float32)
+    # -1/c as the kernels form it, in fp32 on the host: a Python float (exactly that
+    # fp32 value) enters the product as a scalar, with no host-to-device copy, so the
+    # op stays capturable in a HIP graph
+    neg_inv_c = -float(np.float32(1.0) / (np.float32(sm_scale) * np.float32(LOG2E)))
     ninf = torch.full_like(lse, -math.inf)
-    torch.where(lse == -math.inf, ninf, lse * (-(1.0 / c)).to(q.device), out=ws[1])
+    torch.where(lse == -math.inf, ninf, lse * neg_inv_c, out=ws[1])
     outs = [torch.empty((B, H, T, Dp), dtype=torch.bfloat16, device=q.device) for _ in range(6)]
     dqx, dkx, dvx, dq_lo, dk_lo, dv_lo = outs
     a = _attn_args(qx, kx, vx, sm_scale, _lib.KD_PREC_SPLIT)

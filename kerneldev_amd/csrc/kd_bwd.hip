@@ -28,24 +28,12 @@
 // swizzled layout of kd_tile.h (double buffered; dK/dV's Q triple buffered).
 #include "kd_tile.h"
 
-#ifndef DKDV_PF
-#define DKDV_PF 3
-#endif
-// 1: dK/dV at D = 64 on k_dkdv_wide (each wave all four products, two waves
-// per SIMD); 0: on the wave-pair kernel
-#ifndef DKDV64_FUSED
-#define DKDV64_FUSED 1
-#endif
-// 1: dK/dV at D = 128 (16-bit scores) on k_dkdv_wide, one wave per SIMD doing
-// all four products of its 32 keys; 0: on the wave-pair kernel
-#ifndef DKDV128_WIDE
-#define DKDV128_WIDE 0
-#endif
-#ifndef DQ_PF
-#define DQ_PF 3
-#endif
-
 namespace kd {
+
+// LDS operand reads run this many MFMA steps ahead of their use in the dQ and
+// dK/dV products
+constexpr int DQ_PF = 3;
+constexpr int DKDV_PF = 3;
 
 // The workspace holds -Delta per row (dK/dV starts its dP accumulators from
 // it), then -LSE / c with c the score scale
@@ -1164,13 +1152,8 @@ template <class E, int D, bool Q8, bool SP>
 static void launch_dkdv_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dkdv_blocks;
-  if constexpr (D == 64 && DKDV64_FUSED) {  // one launch, all four products per wave
+  if constexpr (D == 64) {  // one launch, all four products per wave
     hipLaunchKernelGGL((k_dkdv_wide<E, D, SP, 64, 0>), dim3(grid), dim3(256), 0, st, a,
-                       reinterpret_cast<const uint32_t*>(plan + L.codes),
-                       reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
-                       reinterpret_cast<const int32_t*>(plan + L.dkdv_count), L.nT, L.n_dkdv_blocks);
-  } else if constexpr (D == 128 && !Q8 && DKDV128_WIDE) {  // one launch, one wave per SIMD
-    hipLaunchKernelGGL((k_dkdv_wide<E, D, SP, 128, 0>), dim3(grid), dim3(256), 0, st, a,
                        reinterpret_cast<const uint32_t*>(plan + L.codes),
                        reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
                        reinterpret_cast<const int32_t*>(plan + L.dkdv_count), L.nT, L.n_dkdv_blocks);

@@ -45,22 +45,16 @@ template <class E> constexpr float rescale_log2();
 template <> constexpr float rescale_log2<BF16>() { return 16.f; }
 template <> constexpr float rescale_log2<F16>() { return 15.f; }
 
-#ifndef FWD_QB
-#define FWD_QB 1
-#endif
-#ifndef FWD_PF
-#define FWD_PF 4
-#endif
-#ifndef FWD_PFV
-#define FWD_PFV 4
-#endif
+// LDS operand reads run this many MFMA steps ahead of their use: the K rows
+// of the score product and the V^T blocks of P V
+constexpr int FWD_PF = 4;
 
-template <class E, int D, bool Q8, int QB, bool SP>
-__global__ __launch_bounds__(256 / QB, (QB == 1 && D <= 128) ? 2 : 1) void k_fwd(AttnArgs a, const uint32_t* __restrict__ codes,
-                                                                const uint32_t* __restrict__ list,
-                                                                const int32_t* __restrict__ count,
-                                                                const uint32_t* __restrict__ order, int nT, int nQB) {
-  constexpr int NW = 4 / QB;        // waves per 128-row q-block; each owns 32 QB rows
+template <class E, int D, bool Q8, bool SP>
+__global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_fwd(AttnArgs a, const uint32_t* __restrict__ codes,
+                                                             const uint32_t* __restrict__ list,
+                                                             const int32_t* __restrict__ count,
+                                                             const uint32_t* __restrict__ order, int nT, int nQB) {
+  constexpr int NW = 4;             // waves per 128-row q-block; each owns 32 rows
   using TL = Tile<D, NW>;           // V tiles (and K tiles on the 16-bit path)
   using SO = ScoreOp<E, D, Q8>;     // S^T = K Q^T, 16-bit or fp8
   using TK = Tile<Q8 ? D / 2 : D, NW>;  // K tiles (fp8: D bytes a row); same layout as SO::TL
@@ -98,27 +92,19 @@ __global__ __launch_bounds__(256 / QB, (QB == 1 && D <= 128) ? 2 : 1) void k_fwd
   const u32x4 rs_k = rsrc_words(ks_base, uint32_t(T) * krb);
   const u32x4 rs_v = rsrc_words(vg, uint32_t(T) * vrb);
 
-  // ---- this lane's query rows, one per 32-row block qb (B operands of S^T,
-  // kept in registers): i_lo[qb] + c ----
+  // ---- this lane's query row (the B operand of S^T, kept in registers) ----
   const int srow = sigma(c);
-  int qrow[QB];
-  bool qvalid[QB];
-  SO so[QB];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    qrow[qb] = qblock * 128 + (wave * QB + qb) * 32 + c;
-    qvalid[qb] = qrow[qb] < T;
-    so[qb].load_b(rs_q, uint32_t(qrow[qb]) * qrb, hf);
-    so[qb].init(srow, hf);
-  }
+  const int qrow = qblock * 128 + wave * 32 + c;
+  const bool qvalid = qrow < T;
+  SO so;
+  so.load_b(rs_q, uint32_t(qrow) * qrb, hf);
+  so.init(srow, hf);
   // this wave's rows lie in q-tile 2 qblock + member of the block (group of 2)
-  const int member = (wave * QB) >> 1;
+  const int member = wave >> 1;
   // token codes of batch row b (reads past T return 0: allow nothing); the
   // row mask of a PARTIAL tile is built from them (query_row_mask)
   const u32x4 rs_codes = rsrc_words(codes + int64_t(b) * T, uint32_t(T) * 4u);
-  uint32_t qcode[QB];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) qcode[qb] = qvalid[qb] ? codes[int64_t(b) * T + qrow[qb]] : 0u;
+  uint32_t qcode = qvalid ? codes[int64_t(b) * T + qrow] : 0u;
 
   const int lbase = item;  // b nQB + qblock
   const int n = count[lbase];
@@ -161,23 +147,21 @@ __global__ __launch_bounds__(256 / QB, (QB == 1 && D <= 128) ? 2 : 1) void k_fwd
         vaddr[db][half] = TL::at(r, chunk) + 8 * (i & 1);
       }
   }
-  // S^T = K Q^T for one tile: two 32-key halves x QB query blocks, each K
-  // operand read from LDS once for the QB independent chains
-  // The K operand of k-step i is read FWD_PF steps before its MFMA; the
-  // sched_barriers keep LDS reads and MFMAs in this order (VALU, SALU and
-  // transcendental work may move across them, to fill the MFMA shadow).
-  auto scores = [&](const uint8_t* kt, f32x16 (&s)[2][QB]) {
+  // S^T = K Q^T for one tile: two 32-key halves.  The K operand of k-step i
+  // is read FWD_PF steps before its MFMA; the sched_barriers keep LDS reads
+  // and MFMAs in this order (VALU, SALU and transcendental work may move
+  // across them, to fill the MFMA shadow).
+  auto scores = [&](const uint8_t* kt, f32x16 (&s)[2]) {
     constexpr int NS = 2 * SO::NK, PF = FWD_PF < NS ? FWD_PF : NS;  // steps: kb = i & 1, st = i >> 1
     typename SO::A av[PF];
 #pragma unroll
-    for (int i = 0; i < PF; ++i) av[i] = so[0].read_a(kt, i & 1, i >> 1);
+    for (int i = 0; i < PF; ++i) av[i] = so.read_a(kt, i & 1, i >> 1);
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int kb = i & 1, st = i >> 1;
       __builtin_amdgcn_sched_barrier(0x406);
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) s[kb][qb] = so[qb].mma_a(av[i % PF], st, st == 0 ? f32x16{} : s[kb][qb]);
-      if (i + PF < NS) av[i % PF] = so[0].read_a(kt, (i + PF) & 1, (i + PF) >> 1);
+      s[kb] = so.mma_a(av[i % PF], st, st == 0 ? f32x16{} : s[kb]);
+      if (i + PF < NS) av[i % PF] = so.read_a(kt, (i + PF) & 1, (i + PF) >> 1);
     }
     __builtin_amdgcn_sched_barrier(0x406);
   };
@@ -185,28 +169,20 @@ __global__ __launch_bounds__(256 / QB, (QB == 1 && D <= 128) ? 2 : 1) void k_fwd
   // the fp8 product carries the dequantisation scales of Q and K
   const float sl2 = a.sm_scale * 1.4426950408889634f * (Q8 ? a.q_scale[bh] * a.k_scale[bh] : 1.f);
   const float NEG_INF = -__builtin_inff();
-  float m_ref[QB], l0[QB], l1[QB];
-  f32x16 o[QB][DB];
+  float m_ref = NEG_INF, l0 = 0.f, l1 = 0.f;
+  f32x16 o[DB];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    m_ref[qb] = NEG_INF;
-    l0[qb] = l1[qb] = 0.f;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) o[qb][db] = f32x16{};
-  }
+  for (int db = 0; db < DB; ++db) o[db] = f32x16{};
 
-  f32x16 s[2][QB];
+  f32x16 s[2];
   if (n > 0) {
     load_k(0, 0);
     load_v(0, 0);
     if (n > 1) load_k(1, 1);
     load_codes(0, 0);
     wait_vmem();
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      so[qb].settle();  // the compiler's wait for the Q rows (and query codes) falls here
-      settle(qcode[qb]);
-    }
+    so.settle();  // the compiler's wait for the Q rows (and query codes) falls here
+    settle(qcode);
     __syncthreads();
     scores(s_k[0], s);
   }
@@ -228,79 +204,72 @@ __global__ __launch_bounds__(256 / QB, (QB == 1 && D <= 128) ? 2 : 1) void k_fwd
     if (e + 2 < n) load_k(e + 2, buf);
 
     const uint32_t mcls = entry_class(cur, member);
-    if (mcls != TILE_FULL) {  // wave-uniform.  Register r of s[kb][qb] holds key 32 kb + 16 (r / 8) + 8 hf + r % 8
+    if (mcls != TILE_FULL) {  // wave-uniform.  Register r of s[kb] holds key 32 kb + 16 (r / 8) + 8 hf + r % 8
       // of the tile: bit 16 (r / 8) + r % 8 of word kb of the row mask shifted by 8 hf
+      const uint64_t rowbits = mcls == TILE_PARTIAL  // EMPTY: nothing allowed
+                                   ? query_row_mask(qcode, qrow, s_kc[buf][lane], int(entry_tile(cur)) * 64)
+                                   : 0u;
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        const uint64_t rowbits = mcls == TILE_PARTIAL  // EMPTY: nothing allowed
-                                     ? query_row_mask(qcode[qb], qrow[qb], s_kc[buf][lane], int(entry_tile(cur)) * 64)
-                                     : 0u;
+      for (int kb = 0; kb < 2; ++kb) {
+        const uint32_t w = uint32_t(rowbits >> (32 * kb)) >> (8 * hf);
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const uint32_t w = uint32_t(rowbits >> (32 * kb)) >> (8 * hf);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) s[kb][qb][r] = mask_bit(s[kb][qb][r], w, 16 * (r >> 3) + (r & 7));
-        }
+        for (int r = 0; r < 16; ++r) s[kb][r] = mask_bit(s[kb][r], w, 16 * (r >> 3) + (r & 7));
       }
     }
-    // running max of this lane's rows; rescale only when it grows by > rescale_log2 (P bound)
-    float ms[QB];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
+    // running max of this lane's row; rescale only when it grows by > rescale_log2 (P bound)
+    float ms;
+    {
       float mx = NEG_INF;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][qb][r]);
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
       mx = xhalf_max(mx);
-      const float m_new = fmaxf(m_ref[qb], mx);
-      if ((m_new - m_ref[qb]) * sl2 > rescale_log2<E>()) {  // false for -inf - -inf (NaN); per lane
-        const float alpha = (m_ref[qb] == NEG_INF) ? 0.f : fast_exp2((m_ref[qb] - m_new) * sl2);
-        m_ref[qb] = m_new;
-        l0[qb] *= alpha;
-        l1[qb] *= alpha;
+      const float m_new = fmaxf(m_ref, mx);
+      if ((m_new - m_ref) * sl2 > rescale_log2<E>()) {  // false for -inf - -inf (NaN); per lane
+        const float alpha = (m_ref == NEG_INF) ? 0.f : fast_exp2((m_ref - m_new) * sl2);
+        m_ref = m_new;
+        l0 *= alpha;
+        l1 *= alpha;
 #pragma unroll
-        for (int db = 0; db < DB; ++db) o[qb][db] *= alpha;
+        for (int db = 0; db < DB; ++db) o[db] *= alpha;
       }
-      ms[qb] = (m_ref[qb] == NEG_INF) ? 0.f : m_ref[qb] * sl2;
+      ms = (m_ref == NEG_INF) ? 0.f : m_ref * sl2;
     }
 
     // softmax of tile e (VALU) alongside S of tile e+1 (MFMA; computed from
     // the other K buffer even past the last tile, where it is simply unused)
     // P packed for the MFMA (pk) and, with SP, its rounding residual (pl):
     // P V is then formed as pk V + pl V, P carried to ~16 significant bits
-    u32x4 pk[QB][2][2];
-    u32x4 pl[SP ? QB : 1][2][2];
+    u32x4 pk[2][2];
+    u32x4 pl[2][2];
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
+    for (int kb = 0; kb < 2; ++kb) {
+      float p[16];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        float p[16];
+      for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(s[kb][r], sl2, -ms));
 #pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(s[kb][qb][r], sl2, -ms[qb]));
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          pk[qb][kb][t] = pack8<E>(p + 8 * t);
-          l0[qb] = acc_pair<E>(pk[qb][kb][t][0], l0[qb]);
-          l1[qb] = acc_pair<E>(pk[qb][kb][t][1], l1[qb]);
-          l0[qb] = acc_pair<E>(pk[qb][kb][t][2], l0[qb]);
-          l1[qb] = acc_pair<E>(pk[qb][kb][t][3], l1[qb]);
-          if constexpr (SP) {
-            pl[qb][kb][t] = pack8_residual<E>(p + 8 * t, pk[qb][kb][t]);
-            l0[qb] = acc_pair<E>(pl[qb][kb][t][0], l0[qb]);
-            l1[qb] = acc_pair<E>(pl[qb][kb][t][1], l1[qb]);
-            l0[qb] = acc_pair<E>(pl[qb][kb][t][2], l0[qb]);
-            l1[qb] = acc_pair<E>(pl[qb][kb][t][3], l1[qb]);
-          }
+      for (int t = 0; t < 2; ++t) {
+        pk[kb][t] = pack8<E>(p + 8 * t);
+        l0 = acc_pair<E>(pk[kb][t][0], l0);
+        l1 = acc_pair<E>(pk[kb][t][1], l1);
+        l0 = acc_pair<E>(pk[kb][t][2], l0);
+        l1 = acc_pair<E>(pk[kb][t][3], l1);
+        if constexpr (SP) {
+          pl[kb][t] = pack8_residual<E>(p + 8 * t, pk[kb][t]);
+          l0 = acc_pair<E>(pl[kb][t][0], l0);
+          l1 = acc_pair<E>(pl[kb][t][1], l1);
+          l0 = acc_pair<E>(pl[kb][t][2], l0);
+          l1 = acc_pair<E>(pl[kb][t][3], l1);
         }
       }
     }
     scores(s_k[buf ^ 1], s);
-    // O^T += V^T P^T for tile e, each V^T operand read once for the QB blocks
-    // and FWD_PFV steps ahead of its MFMA (steps: t4 = i / DB, db = i % DB)
+    // O^T += V^T P^T for tile e, each V^T operand read FWD_PF steps ahead of
+    // its MFMA (steps: t4 = i / DB, db = i % DB)
     const uint8_t* vt = s_v[buf];
     {
-      constexpr int NV = 4 * DB, PFV = FWD_PFV < NV ? FWD_PFV : NV;
+      constexpr int NV = 4 * DB, PFV = FWD_PF < NV ? FWD_PF : NV;
       auto read_v = [&](int i) {
         const int t4 = i / DB, db = i % DB;
         const u32x2 lo = ds_read_tr16(vt + vaddr[db][0] + t4 * 16 * TL::ROWB);
@@ -314,11 +283,8 @@ __global__ __launch_bounds__(256 / QB, (QB == 1 && D <= 128) ? 2 : 1) void k_fwd
       for (int i = 0; i < NV; ++i) {
         const int t4 = i / DB, db = i % DB;
         __builtin_amdgcn_sched_barrier(0x406);
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          o[qb][db] = mfma32x32x16<E>(vv[i % PFV], pk[qb][t4 >> 1][t4 & 1], o[qb][db]);
-          if constexpr (SP) o[qb][db] = mfma32x32x16<E>(vv[i % PFV], pl[qb][t4 >> 1][t4 & 1], o[qb][db]);
-        }
+        o[db] = mfma32x32x16<E>(vv[i % PFV], pk[t4 >> 1][t4 & 1], o[db]);
+        if constexpr (SP) o[db] = mfma32x32x16<E>(vv[i % PFV], pl[t4 >> 1][t4 & 1], o[db]);
         if (i + PFV < NV) vv[i % PFV] = read_v(i + PFV);
       }
       __builtin_amdgcn_sched_barrier(0x406);
@@ -333,12 +299,11 @@ __global__ __launch_bounds__(256 / QB, (QB == 1 && D <= 128) ? 2 : 1) void k_fwd
   // O and LSE use the row sum of the ROUNDED P that entered P V (summed two
   // at a time by v_dot2c): O's weights then sum to exactly 1, and the sum
   // costs half an instruction per score instead of one fp32 add
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const float l_tot = xhalf_sum(l0[qb] + l1[qb]);
+  {
+    const float l_tot = xhalf_sum(l0 + l1);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    if (qvalid[qb]) {
-      const int row = qrow[qb];
+    if (qvalid) {
+      const int row = qrow;
       uint16_t* og = static_cast<uint16_t*>(a.o) + b * a.o_strides[0] + h * a.o_strides[1] + row * a.o_strides[2];
       // optional rounding residual O - bf16(O), so the backward's Delta can be
       // formed from O to ~16 significant bits (contiguous [B, H, T, D])
@@ -351,7 +316,7 @@ __global__ __launch_bounds__(256 / QB, (QB == 1 && D <= 128) ? 2 : 1) void k_fwd
           const int d0 = 32 * db + 8 * g + 4 * hf;
           float f[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) f[i] = o[qb][db][4 * g + i] * inv;
+          for (int i = 0; i < 4; ++i) f[i] = o[db][4 * g + i] * inv;
           const u32x2 w = {pack2<E>(f[0], f[1]), pack2<E>(f[2], f[3])};
           *reinterpret_cast<u32x2*>(og + d0) = w;
           if (lg != nullptr) {
@@ -361,18 +326,17 @@ __global__ __launch_bounds__(256 / QB, (QB == 1 && D <= 128) ? 2 : 1) void k_fwd
         }
       }
       if (a.lse != nullptr && hf == 0)
-        a.lse[int64_t(bh) * T + row] = l_tot > 0.f ? m_ref[qb] * sl2 + fast_log2(l_tot) : NEG_INF;
+        a.lse[int64_t(bh) * T + row] = l_tot > 0.f ? m_ref * sl2 + fast_log2(l_tot) : NEG_INF;
     }
   }
 }
 
 template <class E, int D, bool Q8, bool SP>
 static void launch_fwd_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
-  constexpr int QB = FWD_QB;
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const int nQB = L.n_fwd_blocks;
   const unsigned grid = unsigned(a.B) * a.H * nQB;
-  hipLaunchKernelGGL((k_fwd<E, D, Q8, QB, SP>), dim3(grid), dim3(256 / QB), 0, st, a,
+  hipLaunchKernelGGL((k_fwd<E, D, Q8, SP>), dim3(grid), dim3(256), 0, st, a,
                      reinterpret_cast<const uint32_t*>(plan + L.codes),
                      reinterpret_cast<const uint32_t*>(plan + L.fwd_list),
                      reinterpret_cast<const int32_t*>(plan + L.fwd_count),

@@ -95,19 +95,23 @@ def test_timing_module_runs(dev):
         assert s > 0 and nnz == 2 * 200 * 201 // 2
 
 
-def test_hip_graph_capture_and_replay(dev):
+@pytest.mark.parametrize("case", ["bf16_d64", "fp32_d32_tf32"])
+def test_hip_graph_capture_and_replay(dev, case):
     """flash_attention forward + backward captured in one HIP graph (torch.cuda.CUDAGraph) and
     replayed three times, with eager work on other inputs between the replays: every replay
     gives the eager result bit for bit (no host synchronisation or allocation outside the
-    graph's pool inside the ops)."""
+    graph's pool inside the ops).  fp32 inputs at precision "tf32" and head dim 32 take the
+    bf16x3 ops, whose backward forms its workspace with torch operations."""
     q, k, v, do, meta = _inputs(dev)
+    if case == "fp32_d32_tf32":
+        q, k, v, do = (x[..., :32].float().contiguous() for x in (q, k, v, do))
     qs, ks, vs = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
     dos = do.clone()
 
     def step():
         for t in (qs, ks, vs):
             t.grad = None
-        o = flash_attention(qs, ks, vs, in_span=meta[0], span_id=meta[1], is_prefix=meta[2])
+        o = flash_attention(qs, ks, vs, in_span=meta[0], span_id=meta[1], is_prefix=meta[2], precision="tf32")
         o.backward(dos)
         return o
 

@@ -12,7 +12,7 @@ import random
 import pytest
 import torch
 
-from helpers import assert_close, oracle_fwd_bwd, oracle_mask
+from helpers import assert_close, oracle_fwd_bwd, oracle_mask, single_key_rows
 from kerneldev_amd import flash_attention, generate_hadamard_signs
 from kerneldev_amd.synth import CONFIG3_LAYOUT, cocktail_batch, qkvdo
 from oracle import hadamard as ref_h
@@ -94,7 +94,7 @@ def _run_case(dev, case, c):
     out_dtype = c["dtype"]
     for name, got in (("o", o), ("dq", qd.grad), ("dk", kd.grad), ("dv", vd.grad)):
         assert got.dtype == c["dtype"]
-        assert_close(name, got, ref[name], out_dtype=out_dtype)
+        assert_close(name, got, ref[name], out_dtype=out_dtype, zero_ref_ok=name == "dq" and single_key_rows(mask))
     g, r = lse.double().cpu(), ref["lse"].double()
     assert torch.equal(torch.isinf(g), torch.isinf(r)), "LSE -inf pattern differs"
     fin = torch.isfinite(r)

@@ -1,7 +1,7 @@
 """CPU: the parity metric in tests/helpers.py (what the GPU tests assert with)."""
 import torch
 
-from helpers import REF_ZERO, assert_close, errors
+from helpers import REF_ZERO, assert_close, errors, single_key_rows
 
 
 def test_relative_error_and_ulp_excess():
@@ -18,16 +18,28 @@ def test_relative_error_and_ulp_excess():
 
 def test_zero_reference_has_no_relative_scale():
     """A reference that is 0 to fp64 rounding (dQ with one allowed key per row) is checked by
-    the absolute bar only; a real error there still fails it."""
+    the absolute bar only, when the caller says the exact result is zero; a real error there
+    still fails it, and without that flag a tiny reference keeps the relative bar."""
     ref = torch.full((4, 8), 3e-16, dtype=torch.float64)
     assert ref.pow(2).mean().sqrt().item() <= REF_ZERO
     x = ref + 2e-7
-    ma, rr, _ = errors(x, ref, out_dtype=torch.float32)
+    ma, rr, _ = errors(x, ref, out_dtype=torch.float32, zero_ref_ok=True)
     assert rr == 0.0 and ma < 3e-7
-    assert_close("dq", x, ref, out_dtype=torch.float32)
-    try:
-        assert_close("dq", ref + 0.5, ref, out_dtype=torch.float32)
-    except AssertionError:
-        pass
-    else:
-        raise AssertionError("an absolute error of 0.5 passed")
+    assert_close("dq", x, ref, out_dtype=torch.float32, zero_ref_ok=True)
+    for bad, flag in ((ref + 0.5, True), (x, False)):
+        try:
+            assert_close("dq", bad, ref, out_dtype=torch.float32, zero_ref_ok=flag)
+        except AssertionError:
+            pass
+        else:
+            raise AssertionError(f"error {float((bad - ref).abs().max()):.1e} passed (zero_ref_ok={flag})")
+    # a tiny but genuine reference (inputs scaled by 1e-14) is held to the relative bar
+    small = torch.linspace(-1, 1, 32, dtype=torch.float64) * 1e-14
+    _, rr, _ = errors(small * 1.1, small, out_dtype=torch.float32)
+    assert abs(rr - 0.1) < 1e-9
+
+
+def test_single_key_rows():
+    eye = torch.eye(5, dtype=torch.bool)[None]
+    assert single_key_rows(eye) and single_key_rows(torch.zeros(1, 3, 3, dtype=torch.bool))
+    assert not single_key_rows(torch.ones(1, 2, 2, dtype=torch.bool).tril())
