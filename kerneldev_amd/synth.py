@@ -5,9 +5,12 @@ Cocktail-party sequences follow the layout the reference's collate builds
 
     prefix bytes + [CLS] | context (one [MASK] inside) | ([SPAN] bytes [ES]) x n | [MASKQ] | [PAD]...
 
-with metadata per ``data_builder.py:603-643``: ``is_prefix`` through [CLS],
-``in_span``/``span_id`` over ``[SPAN]..[ES]`` inclusive with ids 1..n, and
-``span_id = -1`` at [MASKQ].  Byte tokens are ``6 + byte`` (ids 6..261,
+with the metadata the collate writes while it assembles the row
+(``data_builder.py:603-643``): ``is_prefix`` over the prefix bytes and [CLS],
+``in_span`` / ``span_id`` over each ``[SPAN]..[ES]`` inclusive with ids 1..n in
+the order the spans are placed, and ``span_id = -1`` at [MASKQ].  The
+metadata comes from the construction itself (where each piece was put), not
+from re-reading the tokens.  Byte tokens are ``6 + byte`` (ids 6..261,
 ``data_builder.py:141``).  A layout that does not fit in ``L`` is redrawn
 (the survey notes the maximal layouts of configs 3 and 4 overflow L).
 
@@ -44,7 +47,14 @@ def _randint(g, lo, hi):
 
 
 def cocktail_sequence(g: torch.Generator, L: int, layout: CocktailLayout, max_tries: int = 1000):
-    """One token row of length L (redrawn until the layout fits)."""
+    """One token row of length L (redrawn until the layout fits) and its metadata.
+
+    Returns ``(tokens, in_span, span_id, is_prefix)`` as lists of length L.  The
+    metadata is marked as the pieces are placed, as data_builder.py:606-643
+    does: the prefix and its [CLS] (:609-611), each span from its [SPAN] through
+    its [ES] with id 1 + its index in placement order (:620-634), and -1 at the
+    [MASKQ] (:637-643).
+    """
     for _ in range(max_tries):
         npre = _randint(g, *layout.prefix_bytes)
         nctx = _randint(g, *layout.context)
@@ -58,23 +68,37 @@ def cocktail_sequence(g: torch.Generator, L: int, layout: CocktailLayout, max_tr
     def byte_tokens(n):
         return (torch.randint(0, 256, (n,), generator=g) + NUM_SPECIAL).tolist()
     toks = byte_tokens(npre) + [CLS]
+    is_prefix = [True] * len(toks)
     ctx = byte_tokens(nctx)
     ctx[_randint(g, 0, nctx - 1)] = MASK
     toks += ctx
-    for n in lens:
-        toks += [SPAN] + byte_tokens(n) + [ES]
+    in_span = [False] * len(toks)
+    span_id = [0] * len(toks)
+    for sid, n in enumerate(lens, start=1):
+        piece = [SPAN] + byte_tokens(n) + [ES]
+        toks += piece
+        in_span += [True] * len(piece)
+        span_id += [sid] * len(piece)
     toks += [MASKQ]
-    toks += [PAD] * (L - len(toks))
-    return toks
+    in_span.append(False)
+    span_id.append(-1)
+    pad = L - len(toks)
+    toks += [PAD] * pad
+    in_span += [False] * pad
+    span_id += [0] * pad
+    is_prefix += [False] * (L - len(is_prefix))
+    return toks, in_span, span_id, is_prefix
 
 
 def cocktail_batch(B: int, L: int, layout: CocktailLayout, seed: int):
-    """Tokens ``[B, L]`` int64 plus collate metadata (in_span, span_id, is_prefix)."""
-    from .metadata import derive_metadata
-
+    """Tokens ``[B, L]`` int64 plus the construction-time collate metadata
+    (in_span bool, span_id int64, is_prefix bool), as cocktail_sequence marks it."""
     g = torch.Generator("cpu").manual_seed(seed)
-    tokens = torch.tensor([cocktail_sequence(g, L, layout) for _ in range(B)], dtype=torch.int64)
-    in_span, span_id, is_prefix = derive_metadata(tokens, rule="collate")
+    rows = [cocktail_sequence(g, L, layout) for _ in range(B)]
+    tokens = torch.tensor([r[0] for r in rows], dtype=torch.int64)
+    in_span = torch.tensor([r[1] for r in rows], dtype=torch.bool)
+    span_id = torch.tensor([r[2] for r in rows], dtype=torch.int64)
+    is_prefix = torch.tensor([r[3] for r in rows], dtype=torch.bool)
     return tokens, in_span, span_id, is_prefix
 
 

@@ -129,20 +129,25 @@ def test_broadcast_equals_bruteforce(case):
 
 
 def test_cocktail_layout_invariants():
-    from kerneldev_amd.synth import CONFIG3_LAYOUT, cocktail_batch
-    tokens, in_span, span_id, is_prefix = cocktail_batch(4, 1024, CONFIG3_LAYOUT, seed=3)
-    m = dense_mask(1024, in_span=in_span.numpy(), span_id=span_id.numpy(), is_prefix=is_prefix.numpy())
-    for b in range(4):
-        toks = tokens[b].numpy()
+    """On generator rows with their construction-time metadata
+    (tests/golden/cocktail_rows.npz, config-3 layout)."""
+    import os
+    fx = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "cocktail_rows.npz"))
+    tokens, in_span = fx["c3_tokens"].astype(np.int64), fx["c3_in_span"]
+    span_id, is_prefix = fx["c3_span_id"].astype(np.int64), fx["c3_is_prefix"]
+    B, T = tokens.shape
+    m = dense_mask(T, B=B, in_span=in_span, span_id=span_id, is_prefix=is_prefix)
+    for b in range(B):
+        toks = tokens[b]
         mq = int(np.nonzero(toks == MASKQ)[0][0])
         assert not m[b, :, mq].any()  # MASKQ column empty
         assert m[b].any(axis=1).all()  # every row sees something (prefix exists)
-        sid = span_id[b].numpy()
+        sid = span_id[b]
         spans = [s for s in np.unique(sid) if s > 0]
         for s1 in spans:
             for s2 in spans:
                 if s1 != s2:
                     assert not m[b][np.ix_(sid == s1, sid == s2)].any()  # span isolation
-        pre = is_prefix[b].numpy()
+        pre = is_prefix[b]
         assert m[b][np.ix_(pre, pre)].all()
         assert not m[b][np.ix_(pre, ~pre)].any()

@@ -8,6 +8,7 @@ check is chosen so that a plausible slip (a dropped term, a swapped sign or
 index, a transposed operand) fails it.
 """
 import math
+import os
 
 import numpy as np
 import pytest
@@ -102,23 +103,29 @@ def test_quantize_per_head_scale_and_error_bound():
 
 
 # ------------------------------------------------------------------ metadata
-def test_collate_metadata_vs_product_derivation_on_cocktail_batches():
-    from kerneldev_amd.metadata import derive_metadata
-    from kerneldev_amd.synth import CONFIG3_LAYOUT, cocktail_batch
+def _cocktail_rows():
+    """Generator rows with the metadata marked while each piece was placed
+    (tests/golden/cocktail_rows.npz, written by make_cocktail_rows.py)."""
+    fx = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "cocktail_rows.npz"))
+    for name in ("c3", "c4"):
+        yield (fx[f"{name}_tokens"].astype(np.int64), fx[f"{name}_in_span"], fx[f"{name}_span_id"].astype(np.int64),
+               fx[f"{name}_is_prefix"])
 
-    tokens, in_span, span_id, is_prefix = cocktail_batch(6, 1024, CONFIG3_LAYOUT, seed=5)
-    o_in, o_sid, o_pre = metadata.collate_metadata(tokens.numpy())
-    np.testing.assert_array_equal(in_span.numpy(), o_in)
-    np.testing.assert_array_equal(span_id.numpy(), o_sid)
-    np.testing.assert_array_equal(is_prefix.numpy(), o_pre)
-    f_in, f_sid, f_pre = metadata.fallback_metadata(tokens.numpy())
-    d_in, d_sid, d_pre = derive_metadata(tokens, rule="fallback")
-    np.testing.assert_array_equal(d_in.numpy(), f_in)
-    np.testing.assert_array_equal(d_sid.numpy(), f_sid)
-    np.testing.assert_array_equal(d_pre.numpy(), f_pre)
-    # the two rules differ exactly at the [ES] tokens (F7)
-    es = tokens.numpy() == ES
-    np.testing.assert_array_equal(o_in & ~f_in, es)
+
+def test_collate_metadata_equals_construction_metadata():
+    """The collate rule read off the tokens gives back exactly what the rows were
+    built with: prefix through [CLS], spans [SPAN]..[ES] inclusive numbered
+    1..n in placement order, -1 at [MASKQ] (data_builder.py:606-643)."""
+    for tokens, in_span, span_id, is_prefix in _cocktail_rows():
+        o_in, o_sid, o_pre = metadata.collate_metadata(tokens)
+        np.testing.assert_array_equal(o_in, in_span)
+        np.testing.assert_array_equal(o_sid, span_id)
+        np.testing.assert_array_equal(o_pre, is_prefix)
+        # the fallback rule differs from it exactly at the [ES] tokens (F7)
+        f_in, _, f_pre = metadata.fallback_metadata(tokens)
+        np.testing.assert_array_equal(o_in & ~f_in, tokens == ES)
+        np.testing.assert_array_equal(f_pre, is_prefix)
+        assert span_id.max() >= 4  # several spans per row
 
 
 def test_metadata_edge_cases():
@@ -131,6 +138,27 @@ def test_metadata_edge_cases():
     assert s1[2].tolist() == [0, 0, -1, 0]
     _, s2, _ = metadata.fallback_metadata(toks)
     assert s2[2].tolist() == [0, 0, -1, -1]
+
+
+def test_collate_numbers_several_spans_in_order():
+    """Two and three spans, hand-evaluated: ids 1, 2, 3 in order, each from its
+    [SPAN] through its [ES]; context and bytes between spans get 0; [MASKQ] -1."""
+    #        0  1    2  3     4  5   6     7   8   9     10  11   12
+    two = [[6, CLS, 7, SPAN, 8, ES, SPAN, 9, 10, ES, MASKQ, PAD, PAD]]
+    i2, s2, p2 = metadata.collate_metadata(np.array(two))
+    assert p2[0].tolist() == [1, 1] + [0] * 11
+    assert i2[0].tolist() == [0, 0, 0, 1, 1, 1, 1, 1, 1, 1, 0, 0, 0]
+    assert s2[0].tolist() == [0, 0, 0, 1, 1, 1, 2, 2, 2, 2, -1, 0, 0]
+    #          0    1  2     3   4     5     6   7   8     9  10  11     12
+    three = [[CLS, 7, SPAN, ES, SPAN, 11, ES, 12, SPAN, 13, 14, ES, MASKQ]]
+    i3, s3, p3 = metadata.collate_metadata(np.array(three))
+    assert p3[0].tolist() == [1] + [0] * 12
+    assert i3[0].tolist() == [0, 0, 1, 1, 1, 1, 1, 0, 1, 1, 1, 1, 0]
+    assert s3[0].tolist() == [0, 0, 1, 1, 2, 2, 2, 0, 3, 3, 3, 3, -1]
+    # the fallback rule: same ids, [ES] outside its span
+    fi, fs, _ = metadata.fallback_metadata(np.array(three))
+    assert fi[0].tolist() == [0, 0, 1, 0, 1, 1, 0, 0, 1, 1, 1, 0, 0]
+    assert fs[0].tolist() == [0, 0, 1, 0, 2, 2, 0, 0, 3, 3, 3, 0, -1]
 
 
 def _malformed_rows(seed, B=4, T=300):

@@ -58,5 +58,5 @@ def test_noalloc_rejects_oversized_workspace():
     a = _lib.AttnArgs()
     a.B, a.H, a.T, a.D = 64, 64, 8192, 128  # 2 B H T floats > KD_NOALLOC_WORKSPACE_FLOATS
     assert 2 * a.B * a.H * a.T > _lib.KD_NOALLOC_WORKSPACE_FLOATS
-    assert lib.kd_attn_bwd_noalloc(ctypes.byref(a), None, None) == _lib.KD_ERR_UNSUPPORTED
+    assert lib.kd_attn_bwd_noalloc(ctypes.byref(a), None, 0, None) == _lib.KD_ERR_UNSUPPORTED
     assert "exceeds the workspace" in lib.kd_last_error_string().decode()
