@@ -271,7 +271,9 @@ int kd_attn_bwd(const kd_attn_args *a, const void *plan, int64_t plan_bytes, voi
  * capture, serving loops, harnesses that forbid hipMalloc).  B*H*T above
  * KD_NOALLOC_WORKSPACE_FLOATS / 2 returns KD_ERR_UNSUPPORTED.  Every call on one
  * GPU uses that GPU's one array, so calls that overlap on one GPU (other
- * streams or threads) race and must be ordered by the caller. */
+ * streams or threads) race and must be ordered by the caller.  The first call
+ * on a device resolves the array's address; that call may itself be made
+ * inside a HIP graph capture (no warm-up call is needed). */
 #define KD_NOALLOC_WORKSPACE_FLOATS (1 << 22)
 int kd_attn_bwd_noalloc(const kd_attn_args *a, const void *plan, int64_t plan_bytes, void *stream);
 

@@ -28,9 +28,9 @@ def ulp(ref: torch.Tensor, dtype) -> torch.Tensor:
 def errors(x: torch.Tensor, ref: torch.Tensor, out_dtype=None, zero_ref_ok: bool = False):
     """(max_abs, rel_rms, max_excess): excess = |x - ref| beyond one ulp of the output dtype.
 
-    zero_ref_ok: the caller knows the exact result is zero, as for dQ when no
-    query row has more than one allowed key (dS = P (dP - Delta) cancels
-    exactly).  The fp64 oracle then gives ~1e-16 and an fp32 kernel dP's
+    zero_ref_ok: the caller knows the exact result is zero, as for dQ and dK
+    when no query row has more than one allowed key (dS = P (dP - Delta)
+    cancels exactly, so dQ = dS K and dK = dS^T Q vanish).  The fp64 oracle then gives ~1e-16 and an fp32 kernel dP's
     rounding level (~1e-7); such a reference (RMS <= REF_ZERO) has no scale for
     a relative error, and only the per-element absolute bar applies (rel_rms
     reported as 0).  Without the flag a tiny reference is held to the relative
@@ -95,7 +95,8 @@ def oracle_mask(inp, T, lens=None, attention_mask_given=False):
 
 def single_key_rows(mask) -> bool:
     """True when no query row of the mask [.., T, T] sees more than one key:
-    then dQ is exactly zero (the only case errors' zero_ref_ok is meant for)."""
+    then dS, and with it dQ and dK, is exactly zero (the only case errors'
+    zero_ref_ok is meant for)."""
     m = torch.as_tensor(mask)
     return bool((m.sum(-1) <= 1).all())
 

@@ -1,12 +1,12 @@
 """CPU emulation of the attention kernels' roundings of P and dS.
 
 Test infrastructure.  The kernels compute S, dP and every product in fp32 on
-the MFMA; the only roundings that matter on outlier data are those of the
-16-bit B operands P (into P V and dV = P^T dO) and dS (into dQ = dS K and
-dK = dS^T Q), and of the outputs.  This module restates those steps in numpy
-for one (b, h) head and measures, per product, the worst error beyond one
-output ulp (the per-element part of the parity bar, ``helpers.assert_close``)
-against an fp64 evaluation of the same inputs, for three forms of P and dS:
+the MFMA; the roundings that matter on outlier data are those of the 16-bit B
+operands P (into P V and dV = P^T dO) and dS (into dQ = dS K and dK = dS^T Q),
+and of the outputs.  This module restates those steps in numpy for one (b, h)
+head and measures, per product, the worst error beyond one output ulp (the
+per-element part of the parity bar, ``helpers.assert_close``) against an fp64
+evaluation of the same inputs, for three forms of P and dS:
 
 * ``"bf16"``: one rounding to bf16 (8 significant bits; the reference rounds P
   to V's dtype, original_kernel.py:566-571, and this is ``precision="bf16"``);
@@ -18,28 +18,39 @@ against an fp64 evaluation of the same inputs, for three forms of P and dS:
 
 The kernel steps restated (kd_fwd.hip, kd_bwd.hip):
 
-* forward: p = exp2(fma(S, c, -m c)) in fp32 with m the row max (the lazy
-  rescale only changes m by a power of two, which no form's relative rounding
-  sees), O = sum_j form(p_j) V_j / sum_j form(p_j), stored as bf16;
-* backward: P = exp2(fma(S, c, -LSE)) in fp32, dP = dO V^T accumulated in fp32,
-  Delta = rowsum(dO O) (O carried to ~16 bits by O + O_lo), dS = P (dP - Delta)
-  in fp32; dV = form(P)^T dO, dQ = sm_scale form(dS) K, dK = sm_scale
-  form(dS)^T Q, each stored as bf16; with Hadamard, dQ and dK are taken back
-  through R^T before the rounding, as the kernels' epilogues do.
+* forward: p = exp2(S c - m c) in fp32 with m the row max (the lazy rescale
+  only changes m by a power of two, which no form's relative rounding sees),
+  O = sum_j form(p_j) V_j / sum_j form(p_j), stored as bf16, and
+  LSE = m c + log2(sum_j form(p_j));
+* backward: P = exp2(S c - LSE) in fp32, dP = dO V^T accumulated in fp32,
+  Delta = rowsum(dO O) with the forward's O (carried to ~16 bits by O + O_lo),
+  dS = P (dP - Delta) in fp32; dV = form(P)^T dO, dQ = sm_scale form(dS) K,
+  dK = sm_scale form(dS)^T Q, each stored as bf16; with Hadamard, dQ and dK go
+  back through R^T before the rounding, as the kernels' epilogues do.
+
+The backward is evaluated twice: with the forward's O and LSE from the split
+forward (what the kernels run), which isolates each backward product's own
+rounding, and with the O and LSE of a forward whose P V took P rounded once to
+fp16 ("coupled"), which shows what that cheaper forward would do to the
+gradients through Delta = rowsum(dO O) and the dP - Delta cancellation.
 
 The products' own fp32 accumulation is evaluated in fp64 here: its error
 (~2^-24 relative per term) is three orders below every form's rounding.
+
+``python tests/rounding_emulation.py [b,h ...]`` prints the table for the
+listed config-4 heads (default: every head).
 """
 from __future__ import annotations
 
 import math
+import os
+import sys
 
 import numpy as np
 
 LOG2E = math.log2(math.e)
 FORMS = ("bf16", "fp16", "bf16x2")
 PRODUCTS = ("O", "dV", "dQ", "dK")  # P V, P^T dO, dS K, dS^T Q
-FP16_MAX = 65504.0
 
 
 def bf16_round(x: np.ndarray) -> np.ndarray:
@@ -91,8 +102,10 @@ def emulate_head(q, k, v, do, mask, sm_scale, rot=None, block=1024):
     q, k, v, do: float32 arrays [T, d] holding the bf16 inputs (q and k already
     rotated and rounded when ``rot`` is given); mask: bool [T, T]; rot: the
     fp64 rotation R (dQ, dK are reported for the unrotated inputs, times R^T).
-    Returns ``{"excess": {(product, form): float}, "max_abs_ds": float,
-    "ref_max": {product: float}}``.
+    Returns ``{"excess": {(product, form): float}, "coupled": {product: float},
+    "max_abs_ds": float, "ref_max": {product: float}}``: "coupled" holds dV,
+    dQ, dK in the split form with Delta and LSE from a forward whose P V took P
+    rounded once to fp16.
     """
     T, d = q.shape
     c32 = np.float32(sm_scale * LOG2E)
@@ -100,13 +113,16 @@ def emulate_head(q, k, v, do, mask, sm_scale, rot=None, block=1024):
     k64, v64, q64, do64 = (x.astype(np.float64) for x in (k, v, q, do))
     row_any = mask.any(axis=1)
 
-    # forward, query blocks: O per form, and the exact O and LSE for the backward
+    # forward, query blocks: O per form; O and LSE of the exact, split and fp16 forwards
     ex = {(p, f): 0.0 for p in PRODUCTS for f in FORMS}
     o_ref = np.zeros((T, d))
+    o_fwd = {"bf16x2": np.zeros((T, d)), "fp16": np.zeros((T, d))}
     lse = np.full(T, -np.inf)
+    lse_fwd = {f: np.full(T, -np.inf) for f in o_fwd}
     for r0 in range(0, T, block):
         rows = slice(r0, min(T, r0 + block))
         mb = mask[rows]
+        ok = row_any[rows]
         s64 = q64[rows] @ k64.T
         s32 = s64.astype(np.float32)
         m = np.where(mb, s32, -np.inf).max(axis=1)
@@ -114,7 +130,6 @@ def emulate_head(q, k, v, do, mask, sm_scale, rot=None, block=1024):
         p32 = np.exp2(np.where(mb, s32 * c32 - (m * c32)[:, None], -np.inf)).astype(np.float32)
         p64 = np.where(mb, np.exp2(s64 * c64 - (m.astype(np.float64) * c64)[:, None]), 0.0)
         l64 = p64.sum(axis=1)
-        ok = row_any[rows]
         ref = np.where(ok[:, None], (p64 @ v64) / np.where(ok, l64, 1.0)[:, None], 0.0)
         o_ref[rows] = ref
         lse[rows] = np.where(ok, m.astype(np.float64) * c64 + np.log2(np.where(ok, l64, 1.0)), -np.inf)
@@ -123,52 +138,65 @@ def emulate_head(q, k, v, do, mask, sm_scale, rot=None, block=1024):
             lf = pf.sum(axis=1)
             got = np.where(ok[:, None], (pf @ operand(v, f)) / np.where(lf > 0, lf, 1.0)[:, None], 0.0)
             ex[("O", f)] = max(ex[("O", f)], excess(got, ref))
+            if f in o_fwd:
+                o_fwd[f][rows] = got
+                lse_fwd[f][rows] = np.where(ok, m.astype(np.float64) * c64 + np.log2(np.where(lf > 0, lf, 1.0)),
+                                            -np.inf)
 
-    # backward: dQ per query block, dV and dK accumulated over the blocks
-    lse32 = lse.astype(np.float32)
-    delta64 = (do64 * o_ref).sum(axis=1)  # Delta from O to ~16 bits (O + O_lo)
-    delta32 = delta64.astype(np.float32)
-    dv_ref = np.zeros((T, d))
-    dk_ref = np.zeros((T, d))
-    dv = {f: np.zeros((T, d)) for f in FORMS}
-    dk = {f: np.zeros((T, d)) for f in FORMS}
+    # backward: dQ per query block, dV and dK accumulated over the blocks; the
+    # exact gradients use the exact O and LSE, the emulated ones the forward's
+    delta64 = (do64 * o_ref).sum(axis=1)
+    fwd_delta = {f: (do64 * o_fwd[f]).sum(axis=1).astype(np.float32) for f in o_fwd}
+    fwd_lse = {f: lse_fwd[f].astype(np.float32) for f in o_fwd}
+    runs = [("bf16x2", f) for f in FORMS] + [("fp16", "bf16x2")]  # (forward form, backward form)
+    acc = {r: {"dv": np.zeros((T, d)), "dk": np.zeros((T, d)), "dq": []} for r in runs}
+    dv_ref, dk_ref, dq_ref = np.zeros((T, d)), np.zeros((T, d)), []
     max_ds = 0.0
-    dq_parts = {f: [] for f in FORMS}
-    dq_ref_parts = []
     for r0 in range(0, T, block):
         rows = slice(r0, min(T, r0 + block))
         mb = mask[rows]
         s64 = q64[rows] @ k64.T
         s32 = s64.astype(np.float32)
-        l32 = np.where(np.isfinite(lse32[rows]), lse32[rows], np.float32(np.inf))
-        P32 = np.where(mb, np.exp2(s32 * c32 - l32[:, None]), 0.0).astype(np.float32)
         l64 = np.where(np.isfinite(lse[rows]), lse[rows], np.inf)
         P64 = np.where(mb, np.exp2(s64 * c64 - l64[:, None]), 0.0)
         dp64 = do64[rows] @ v64.T
-        dS32 = (P32 * (dp64.astype(np.float32) - delta32[rows][:, None])).astype(np.float32)
+        dp32 = dp64.astype(np.float32)
         dS64 = P64 * (dp64 - delta64[rows][:, None])
-        max_ds = max(max_ds, float(np.abs(dS32).max(initial=0.0)))
         dv_ref += P64.T @ do64[rows]
         dk_ref += dS64.T @ q64[rows]
-        dq_ref_parts.append(dS64 @ k64)
-        for f in FORMS:
-            Pf, dSf = as_form(P32, f), as_form(dS32, f)
-            dv[f] += Pf.T @ operand(do[rows], f)
-            dk[f] += dSf.T @ operand(q[rows], f)
-            dq_parts[f].append(dSf @ operand(k, f))
+        dq_ref.append(dS64 @ k64)
+        for ff in o_fwd:
+            l32 = np.where(np.isfinite(fwd_lse[ff][rows]), fwd_lse[ff][rows], np.float32(np.inf))
+            P32 = np.where(mb, np.exp2(s32 * c32 - l32[:, None]), 0.0).astype(np.float32)
+            dS32 = (P32 * (dp32 - fwd_delta[ff][rows][:, None])).astype(np.float32)
+            if ff == "bf16x2":
+                max_ds = max(max_ds, float(np.abs(dS32).max(initial=0.0)))
+            for fwd, f in runs:
+                if fwd != ff:
+                    continue
+                Pf, dSf = as_form(P32, f), as_form(dS32, f)
+                a = acc[(fwd, f)]
+                a["dv"] += Pf.T @ operand(do[rows], f)
+                a["dk"] += dSf.T @ operand(q[rows], f)
+                a["dq"].append(dSf @ operand(k, f))
 
     def finish(x):  # scale, and back through R^T for the rotated inputs
         x = x * sm_scale
         return x @ rot.T if rot is not None else x
 
-    dq_ref = finish(np.concatenate(dq_ref_parts))
+    dq_ref = finish(np.concatenate(dq_ref))
     dk_ref = finish(dk_ref)
     refs = {"O": o_ref, "dV": dv_ref, "dQ": dq_ref, "dK": dk_ref}
+
+    def grads(a):
+        return {"dV": excess(a["dv"], dv_ref), "dQ": excess(finish(np.concatenate(a["dq"])), dq_ref),
+                "dK": excess(finish(a["dk"]), dk_ref)}
+
     for f in FORMS:
-        ex[("dV", f)] = excess(dv[f], dv_ref)
-        ex[("dQ", f)] = excess(finish(np.concatenate(dq_parts[f])), dq_ref)
-        ex[("dK", f)] = excess(finish(dk[f]), dk_ref)
-    return {"excess": ex, "max_abs_ds": max_ds, "ref_max": {p: float(np.abs(r).max()) for p, r in refs.items()}}
+        for p, e in grads(acc[("bf16x2", f)]).items():
+            ex[(p, f)] = e
+    return {"excess": ex, "coupled": grads(acc[("fp16", "bf16x2")]), "max_abs_ds": max_ds,
+            "ref_max": {p: float(np.abs(r).max()) for p, r in refs.items()}}
 
 
 def config4_head(b: int, h: int, hadamard: bool, seed: int = 0):
@@ -191,3 +219,18 @@ def config4_head(b: int, h: int, hadamard: bool, seed: int = 0):
         q, k = (bf16_round(rotate_fp32(x, signs)) for x in (q, k))
         rot = rotation_matrix(signs)
     return q, k, v, do, mask, D ** -0.5, rot
+
+
+def main(argv):
+    heads = [tuple(int(x) for x in a.split(",")) for a in argv] or [(b, h) for b in range(2) for h in range(32)]
+    print("head       product  " + "  ".join(f"{f:>8}" for f in FORMS) + "  coupled")
+    for b, h in heads:
+        r = emulate_head(*config4_head(b, h, hadamard=True))
+        for p in PRODUCTS:
+            row = "  ".join(f"{r['excess'][(p, f)]:8.2e}" for f in FORMS)
+            print(f"({b:d},{h:2d})  {p:>6}  {row}  {r['coupled'].get(p, float('nan')):8.2e}", flush=True)
+
+
+if __name__ == "__main__":
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    main(sys.argv[1:])

@@ -36,7 +36,7 @@ def compare(got, ref, heads=None):
     for key in ("o", "dq", "dk", "dv"):
         g = got[key] if heads is None else select_heads(got[key], heads)
         try:
-            res[key] = assert_close(key, g, ref[key], zero_ref_ok=key == "dq" and ref.get("single_key", False))
+            res[key] = assert_close(key, g, ref[key], zero_ref_ok=key in ("dq", "dk") and ref.get("single_key", False))
         except AssertionError as exc:
             failures.append(str(exc))
     g = got["lse"] if heads is None else torch.cat([got["lse"][b:b + 1, h:h + 1] for b, h in heads], 0)
