@@ -19,11 +19,12 @@
  *     (b, h, t) strides multiples of 8 elements, the t stride >= D and
  *     T * t_stride * element size < 2^31 bytes.
  *   - Head dims 16, 32, 64, 128, 256 (original_kernel.py:1720).  bf16 / fp16
- *     at D = 64, 128, 256 run on the MFMA kernels (dqk_signs at 64, 128 only);
- *     fp32 inputs at D = 32, 64, 128 on the fp32 MFMA kernels; fp32 at D = 16,
- *     256 and 16-bit inputs at D = 16, 32 on fp32 vector-ALU kernels.  fp32
- *     inputs get no fp8 scores and no dqk_signs, and precision is always full
- *     fp32 for them.  (The Python layer runs fp32 inputs at precision "tf32"
+ *     run on the MFMA kernels at every head dim (16 and 32 on the D = 64
+ *     kernels, which read the columns past D as zeros and store only the D
+ *     real ones; dqk_signs at 64, 128 only; fp8 scores at 128); fp32 inputs at
+ *     D = 32, 64, 128 on the fp32 MFMA kernels, at D = 16, 256 on fp32
+ *     vector-ALU kernels.  fp32 inputs get no fp8 scores and no dqk_signs,
+ *     and precision is always full fp32 for them.  (The Python layer runs fp32 inputs at precision "tf32"
  *     and D = 16, 32 as bf16 operands of three times the head dim on the
  *     16-bit MFMA kernels instead, with dq_lo / dk_lo / dv_lo below.)
  *   - LSE is stored in log2 units (LSE2 = log2 sum_j exp2(S_ij * sm_scale *

@@ -31,19 +31,15 @@ from ._lib import AttnArgs, MetaArgs
 REFERENCE_HEAD_DIMS = (16, 32, 64, 128, 256)  # original_kernel.py:1720
 SUPPORTED_HEAD_DIMS = REFERENCE_HEAD_DIMS
 # bf16 / fp16 at these head dims run on the MFMA kernels with the fused
-# Hadamard epilogues (fp8 scores at 128); 256 runs there without them.  fp32
+# Hadamard epilogues (fp8 scores at 128); 16, 32 and 256 run there without
+# them (16 and 32 on the d = 64 kernels, which read the missing columns as
+# zeros).  fp32
 # inputs run on the fp32 MFMA kernels (kd_f32mma.hip: head dims 32, 64, 128,
 # and 16 zero-padded to 32, FP32_PADDED_HEAD_DIMS), except at precision "tf32"
 # and head dims 16, 32 (X3_ROUTED_HEAD_DIMS: bf16x3, faster there), and on the
 # fp32 vector-ALU kernels (kd_simt.hip) at 256
 MFMA_HEAD_DIMS = (64, 128)
 FP32_PADDED_HEAD_DIMS = {16: 32}
-# 16-bit inputs with these head dims run on the d = 64 MFMA kernels, zero-
-# padded: zero columns change no score (S = Q K^T), O's extra columns are
-# P 0 = 0 and the gradients' extra columns are dropped by the pad's autograd.
-# Twice the matrix work of a native kernel, an order of magnitude ahead of
-# the fp32 vector-ALU kernels that the C ABI runs them on.
-PADDED_HEAD_DIMS = {16: 64, 32: 64}
 
 # precision -> arithmetic of P and dS in the kernels.  The reference rounds P
 # to V's dtype for P V (original_kernel.py:566-571) and keeps P and dS in fp32
@@ -455,11 +451,13 @@ _fwd_x3_op.register_autograd(_backward_x3, setup_context=_setup_context_x3)
 
 def head_dim_route(dtype: torch.dtype, D: int, precision: str) -> tuple[bool, int]:
     """Which kernels flash_attention runs for inputs of this dtype and head dim:
-    (bf16x3 ops?, zero-padded head dim or 0).  16-bit d = 16, 32 pad to the d = 64
-    MFMA kernels; fp32 takes bf16x3 at "tf32" and d = 16, 32, else the C ABI's
-    fp32 kernels with d = 16 padded to 32 (the fp32 MFMA's smallest)."""
+    (bf16x3 ops?, zero-padded head dim or 0).  16-bit inputs go to the C ABI's
+    MFMA kernels at every head dim as they are (d = 16, 32 on the d = 64
+    kernels, which read the missing columns as zeros); fp32 takes bf16x3 at
+    "tf32" and d = 16, 32, else the C ABI's fp32 kernels with d = 16 padded to
+    32 (the fp32 MFMA's smallest)."""
     if dtype != torch.float32:
-        return False, PADDED_HEAD_DIMS.get(D, 0)
+        return False, 0
     if precision == "tf32" and D in X3_ROUTED_HEAD_DIMS:
         return True, 0
     return False, FP32_PADDED_HEAD_DIMS.get(D, 0)

@@ -90,13 +90,17 @@ __global__ __launch_bounds__(256) void k_delta(AttnArgs a) {
 // also each value's rounding residual at the same offsets of glo (the
 // caller's contiguous residual row), so that g + glo carries the fp32 value to
 // about twice the type's significant bits
+// dlim: columns from there on are not stored (head dims 16 and 32 on the
+// D = 64 kernels)
 template <class E, int D>
-KD_DEV void store_rows_T(uint16_t* g, const f32x16 (&acc)[D / 32], float scale, int hf, uint16_t* glo = nullptr) {
+KD_DEV void store_rows_T(uint16_t* g, const f32x16 (&acc)[D / 32], float scale, int hf, uint16_t* glo = nullptr,
+                         int dlim = D) {
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
     for (int gg = 0; gg < 4; ++gg) {
       const int d0 = 32 * db + 8 * gg + 4 * hf;
+      if (d0 >= dlim) continue;
       const float f[4] = {acc[db][4 * gg] * scale, acc[db][4 * gg + 1] * scale, acc[db][4 * gg + 2] * scale,
                           acc[db][4 * gg + 3] * scale};
       const u32x2 w = {pack2<E>(f[0], f[1]), pack2<E>(f[2], f[3])};
@@ -213,11 +217,17 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
   const int qrow = qblock * 128 + wave * 32 + c;
   const bool qvalid = qrow < T;
   SO so;  // B operand: this lane's query row (Q, or its fp8 copy)
+  // bytes of a row of the 16-bit inputs: 2 D, or fewer for head dims 16 and
+  // 32 on the D = 64 kernel, whose other columns are read as zeros
+  const uint32_t dbytes = uint32_t(a.D) * 2u;
   if constexpr (Q8) so.load_b(make_rsrc(a.q8 + int64_t(bh) * T * D, uint32_t(T) * D), uint32_t(qrow) * D, hf);
-  else so.load_b(rs_q, uint32_t(qrow) * qrb, hf);
+  else so.load_b(rs_q, uint32_t(qrow) * qrb, hf, dbytes);
   u32x4 dof[DS];
 #pragma unroll
-  for (int st = 0; st < DS; ++st) dof[st] = buf_load16(rs_do, uint32_t(qrow) * dorb + (16 * st + 8 * hf) * 2);
+  for (int st = 0; st < DS; ++st) {
+    const uint32_t col = (16 * st + 8 * hf) * 2;
+    dof[st] = buf_load16(rs_do, col_masked(uint32_t(qrow) * dorb + col, col, dbytes));
+  }
   const float INF = __builtin_inff();
   float lse, delta;
   if (fuse_delta) {  // uniform: compute this row's Delta and LSE copy here, for the dK/dV kernel too
@@ -225,15 +235,15 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
     const uint16_t* og = static_cast<const uint16_t*>(a.o) + b * a.o_strides[0] + h * a.o_strides[1];
     const uint32_t orb = uint32_t(a.o_strides[2]) * 2u;
     const auto rs_o = make_rsrc(og, uint32_t(T) * orb);
-    // o_lo is contiguous [B, H, T, D]; without it the empty resource reads zeros
-    const uint16_t* lg = a.o_lo == nullptr ? nullptr : static_cast<const uint16_t*>(a.o_lo) + int64_t(bh) * T * D;
-    const auto rs_lo = make_rsrc(lg, lg == nullptr ? 0u : uint32_t(T) * D * 2u);
+    // o_lo is contiguous [B, H, T, a.D]; without it the empty resource reads zeros
+    const uint16_t* lg = a.o_lo == nullptr ? nullptr : static_cast<const uint16_t*>(a.o_lo) + int64_t(bh) * T * a.D;
+    const auto rs_lo = make_rsrc(lg, lg == nullptr ? 0u : uint32_t(T) * dbytes);
     float sum = 0.f;
 #pragma unroll
     for (int st = 0; st < DS; ++st) {
       const uint32_t col = (16 * st + 8 * hf) * 2;
-      const u32x4 ov = buf_load16(rs_o, uint32_t(qrow) * orb + col);
-      const u32x4 lv = buf_load16(rs_lo, uint32_t(qrow) * D * 2u + col);
+      const u32x4 ov = buf_load16(rs_o, col_masked(uint32_t(qrow) * orb + col, col, dbytes));
+      const u32x4 lv = buf_load16(rs_lo, col_masked(uint32_t(qrow) * dbytes + col, col, dbytes));
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const float o0 = to_f32<E>(uint16_t(ov[w] & 0xFFFFu)) + to_f32<E>(uint16_t(lv[w] & 0xFFFFu));
@@ -271,8 +281,8 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
   const uint32_t* ent = list + int64_t(lbase) * nT;
 
   uint32_t koff[NL], voff[NL], k8off[NL8];
-  TL::load_offsets(wave, lane, krb, koff);
-  TL::load_offsets(wave, lane, vrb, voff);
+  TL::load_offsets(wave, lane, krb, koff, dbytes);
+  TL::load_offsets(wave, lane, vrb, voff, dbytes);
   TK8::load_offsets(wave, lane, uint32_t(D), k8off);
   const u32x4 rs_k8 = rsrc_words(Q8 ? a.k8 + int64_t(bh) * T * D : nullptr, Q8 ? uint32_t(T) * D : 0u);
   // inline-asm copies (dma_b128): the compiler places no wait for them
@@ -454,10 +464,10 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
   if (qvalid) {
     uint16_t* g = static_cast<uint16_t*>(a.dq) + b * a.dq_strides[0] + h * a.dq_strides[1] + qrow * a.dq_strides[2];
     uint16_t* glo = a.dq_lo == nullptr ? nullptr
-                                       : static_cast<uint16_t*>(a.dq_lo) + ((int64_t(b) * a.H + h) * a.T + qrow) * D;
+                                       : static_cast<uint16_t*>(a.dq_lo) + ((int64_t(b) * a.H + h) * a.T + qrow) * a.D;
     if constexpr (DH == D) {
       if (a.dqk_signs != nullptr) store_rows_T_unrot<E, D>(g, acc, a.sm_scale, hf, a.dqk_signs);
-      else store_rows_T<E, D>(g, acc, a.sm_scale, hf, glo);
+      else store_rows_T<E, D>(g, acc, a.sm_scale, hf, glo, a.D);
     } else {  // (no dqk_signs at split widths)
       store_rows_T<E, DH>(g + D0, acc, a.sm_scale, hf, glo == nullptr ? nullptr : glo + D0);
     }
@@ -939,13 +949,17 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
 
   const int krow = kblock * 128 + wave * 32 + c;
   const bool kvalid = krow < T;
+  // bytes of a row of the 16-bit inputs: 2 D, or fewer for head dims 16 and
+  // 32 on the D = 64 kernel, whose other columns are read as zeros
+  const uint32_t dbytes = uint32_t(a.D) * 2u;
   u32x4 bk[DS], bv[DS];  // this lane's K and V rows (B operands of S^T, dP^T)
   {
     const auto rk = make_rsrc(kg, uint32_t(T) * krb), rv = make_rsrc(vg, uint32_t(T) * vrb);
 #pragma unroll
     for (int st = 0; st < DS; ++st) {
-      bk[st] = buf_load16(rk, uint32_t(krow) * krb + (16 * st + 8 * hf) * 2);
-      bv[st] = buf_load16(rv, uint32_t(krow) * vrb + (16 * st + 8 * hf) * 2);
+      const uint32_t col = (16 * st + 8 * hf) * 2;
+      bk[st] = buf_load16(rk, col_masked(uint32_t(krow) * krb + col, col, dbytes));
+      bv[st] = buf_load16(rv, col_masked(uint32_t(krow) * vrb + col, col, dbytes));
     }
   }
   const int member = wave >> 1;
@@ -956,8 +970,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
   const uint32_t* ent = list + int64_t(lbase) * nT;
 
   uint32_t qoff[NL], dooff[NL];
-  TL::load_offsets(wave, lane, qrb, qoff);
-  TL::load_offsets(wave, lane, dorb, dooff);
+  TL::load_offsets(wave, lane, qrb, qoff, dbytes);
+  TL::load_offsets(wave, lane, dorb, dooff, dbytes);
   auto load_tile = [&](uint32_t en, int slot) {
     const uint32_t q0 = entry_tile(en) * 64u;
     TL::load_async(rs_q, q0 * qrb, qoff, lds_addr(s_q[slot]), wave);
@@ -1105,13 +1119,14 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
   if (kvalid) {
     uint16_t* gv = static_cast<uint16_t*>(a.dv) + b * a.dv_strides[0] + h * a.dv_strides[1] + krow * a.dv_strides[2];
     uint16_t* gk = static_cast<uint16_t*>(a.dk) + b * a.dk_strides[0] + h * a.dk_strides[1] + krow * a.dk_strides[2];
-    const int64_t lo_row = ((int64_t(b) * a.H + h) * a.T + krow) * D + D0;
+    const int64_t lo_row = ((int64_t(b) * a.H + h) * a.T + krow) * a.D + D0;
     uint16_t* gv_lo = a.dv_lo == nullptr ? nullptr : static_cast<uint16_t*>(a.dv_lo) + lo_row;
     uint16_t* gk_lo = a.dk_lo == nullptr ? nullptr : static_cast<uint16_t*>(a.dk_lo) + lo_row;
-    store_rows_T<E, DH>(gv + D0, acc_v, 1.f, hf, gv_lo);
+    // (a.D < D only for the head dims 16 and 32 on the D = 64 launch, DH == D)
+    store_rows_T<E, DH>(gv + D0, acc_v, 1.f, hf, gv_lo, DH == D ? a.D : DH);
     if constexpr (DH == D) {  // all columns here: dK can be rotated back (dqk_signs)
       if (a.dqk_signs != nullptr) store_rows_T_unrot<E, D>(gk, acc_k, a.sm_scale, hf, a.dqk_signs);
-      else store_rows_T<E, D>(gk, acc_k, a.sm_scale, hf, gk_lo);
+      else store_rows_T<E, D>(gk, acc_k, a.sm_scale, hf, gk_lo, a.D);
     } else {
       store_rows_T<E, DH>(gk + D0, acc_k, a.sm_scale, hf, gk_lo);  // (no dqk_signs at split widths)
     }
@@ -1179,22 +1194,35 @@ static void launch_dkdv_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st
   else launch_dkdv_s<E, D, Q8, true>(a, plan, st);
 }
 
+// head dims 16 and 32 run on the D = 64 kernels (their rows read as zeros past a.D)
 #define KD_DISPATCH(FN, ...)                                         \
   do {                                                               \
     if (a.dtype == KD_BF16) {                                        \
-      if (a.D == 64) FN<BF16, 64>(__VA_ARGS__);                      \
+      if (a.D <= 64) FN<BF16, 64>(__VA_ARGS__);                      \
       else if (a.D == 128) FN<BF16, 128>(__VA_ARGS__);               \
       else FN<BF16, 256>(__VA_ARGS__);                               \
     } else {                                                         \
-      if (a.D == 64) FN<F16, 64>(__VA_ARGS__);                       \
+      if (a.D <= 64) FN<F16, 64>(__VA_ARGS__);                       \
       else if (a.D == 128) FN<F16, 128>(__VA_ARGS__);                \
       else FN<F16, 256>(__VA_ARGS__);                                \
     }                                                                \
   } while (0)
 
+template <class E>
+static void launch_delta_e(const AttnArgs& a, hipStream_t st) {
+  switch (a.D) {  // k_delta reads whole rows of a.D elements
+    case 16: launch_delta_t<E, 16>(a, st); break;
+    case 32: launch_delta_t<E, 32>(a, st); break;
+    case 64: launch_delta_t<E, 64>(a, st); break;
+    case 128: launch_delta_t<E, 128>(a, st); break;
+    default: launch_delta_t<E, 256>(a, st); break;
+  }
+}
+
 int launch_delta(const AttnArgs& a, hipStream_t st) {
   if (use_simt(a)) return launch_simt_kernel(1, a, nullptr, st);
-  KD_DISPATCH(launch_delta_t, a, st);
+  if (a.dtype == KD_BF16) launch_delta_e<BF16>(a, st);
+  else launch_delta_e<F16>(a, st);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 int launch_dq(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_delta) {

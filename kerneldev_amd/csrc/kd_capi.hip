@@ -62,7 +62,7 @@ int check_common(const kd_attn_args* a) {
     return fail(KD_ERR_UNSUPPORTED, "head dim must be 16, 32, 64, 128 or 256");
   if (a->dtype != KD_BF16 && a->dtype != KD_F16 && a->dtype != KD_F32)
     return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16, fp16 or fp32");
-  if (a->dqk_signs != nullptr && (kd::use_simt(*a) || a->D == 256))
+  if (a->dqk_signs != nullptr && (kd::use_simt(*a) || (a->D != 64 && a->D != 128)))
     return fail(KD_ERR_UNSUPPORTED, "dqk_signs is built for bf16 / fp16 at head dim 64 or 128");
   if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale))
     return fail(KD_ERR_INVALID, "sm_scale must be finite and > 0");
@@ -286,8 +286,7 @@ static int check_bwd(const kd_attn_args* a, const void* plan, int64_t plan_bytes
     return fail(KD_ERR_INVALID, "lse and delta are required");
   if (a->dq_lo != nullptr || a->dk_lo != nullptr || a->dv_lo != nullptr) {
     if (kd::use_simt(*a) || a->dqk_signs != nullptr)
-      return fail(KD_ERR_UNSUPPORTED, "dq_lo / dk_lo / dv_lo are built for bf16 / fp16 at head dim 64, 128 or 256, "
-                                      "without dqk_signs");
+      return fail(KD_ERR_UNSUPPORTED, "dq_lo / dk_lo / dv_lo are built for bf16 / fp16 inputs, without dqk_signs");
     for (const void* p : {a->dq_lo, a->dk_lo, a->dv_lo})
       if (p != nullptr && !aligned16(p)) return fail(KD_ERR_INVALID, "dq_lo, dk_lo and dv_lo must be 16-byte aligned");
   }

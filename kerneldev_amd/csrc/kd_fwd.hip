@@ -91,13 +91,16 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_fwd(AttnArgs a, const
   const auto rs_q = make_rsrc(qs_base, uint32_t(T) * qrb);
   const u32x4 rs_k = rsrc_words(ks_base, uint32_t(T) * krb);
   const u32x4 rs_v = rsrc_words(vg, uint32_t(T) * vrb);
+  // bytes of a row of the 16-bit inputs: 2 D, or fewer for head dims 16 and
+  // 32 on the D = 64 kernel, whose other columns are read as zeros
+  const uint32_t dbytes = uint32_t(a.D) * 2u;
 
   // ---- this lane's query row (the B operand of S^T, kept in registers) ----
   const int srow = sigma(c);
   const int qrow = qblock * 128 + wave * 32 + c;
   const bool qvalid = qrow < T;
   SO so;
-  so.load_b(rs_q, uint32_t(qrow) * qrb, hf);
+  so.load_b(rs_q, uint32_t(qrow) * qrb, hf, dbytes);
   so.init(srow, hf);
   // this wave's rows lie in q-tile 2 qblock + member of the block (group of 2)
   const int member = wave >> 1;
@@ -111,8 +114,8 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_fwd(AttnArgs a, const
   const uint32_t* ent = list + int64_t(lbase) * nT;
 
   uint32_t koff[NLK], voff[NL];
-  TK::load_offsets(wave, lane, krb, koff);
-  TL::load_offsets(wave, lane, vrb, voff);
+  TK::load_offsets(wave, lane, krb, koff, Q8 ? uint32_t(TK::ROWB) : dbytes);
+  TL::load_offsets(wave, lane, vrb, voff, dbytes);
   // K tiles run one step ahead of V tiles (S of tile e+1 is computed while
   // tile e is softmaxed), so they are loaded separately.
   // slot = e & 1 (passed as a constant by the unrolled loop)
@@ -306,14 +309,15 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_fwd(AttnArgs a, const
       const int row = qrow;
       uint16_t* og = static_cast<uint16_t*>(a.o) + b * a.o_strides[0] + h * a.o_strides[1] + row * a.o_strides[2];
       // optional rounding residual O - bf16(O), so the backward's Delta can be
-      // formed from O to ~16 significant bits (contiguous [B, H, T, D])
+      // formed from O to ~16 significant bits (contiguous [B, H, T, a.D])
       uint16_t* lg = a.o_lo == nullptr ? nullptr
-                                       : static_cast<uint16_t*>(a.o_lo) + (int64_t(bh) * T + row) * D;
+                                       : static_cast<uint16_t*>(a.o_lo) + (int64_t(bh) * T + row) * a.D;
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d0 = 32 * db + 8 * g + 4 * hf;
+          if (D == 64 && d0 >= a.D) continue;  // head dims 16, 32: only the real columns
           float f[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) f[i] = o[db][4 * g + i] * inv;
@@ -353,12 +357,12 @@ int launch_fwd(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   if (use_simt(a)) return launch_simt_kernel(0, a, plan, st);
   if (a.q8 != nullptr) {  // fp8 QK^T: bf16, head dim 128 (checked by the C ABI)
     launch_fwd_p<BF16, 128, true>(a, plan, st);
-  } else if (a.dtype == KD_BF16) {
-    if (a.D == 64) launch_fwd_p<BF16, 64>(a, plan, st);
+  } else if (a.dtype == KD_BF16) {  // head dims 16 and 32 on the D = 64 kernel
+    if (a.D <= 64) launch_fwd_p<BF16, 64>(a, plan, st);
     else if (a.D == 128) launch_fwd_p<BF16, 128>(a, plan, st);
     else launch_fwd_p<BF16, 256>(a, plan, st);
   } else {
-    if (a.D == 64) launch_fwd_p<F16, 64>(a, plan, st);
+    if (a.D <= 64) launch_fwd_p<F16, 64>(a, plan, st);
     else if (a.D == 128) launch_fwd_p<F16, 128>(a, plan, st);
     else launch_fwd_p<F16, 256>(a, plan, st);
   }

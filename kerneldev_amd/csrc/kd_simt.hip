@@ -1,11 +1,11 @@
-// Attention in fp32 arithmetic on the vector ALUs, for the cases the MFMA
+// Attention in fp32 arithmetic on the vector ALUs, for the case the MFMA
 // kernels are not built for: fp32 inputs at head dim 16 or 256 (the
 // reference's precision="ieee" / "tf32" dots, original_kernel.py:452, :569,
 // :1239, :1331-1333, :1425, :1517-1523, here in full fp32; kd_f32mma.hip takes
-// fp32 at 32, 64, 128), and bf16 / fp16 inputs with head dim 16 or 32 (the
-// other sizes original_kernel.py:1720 accepts), plus Delta for fp32 inputs.  Same algebra, plan and masks as the MFMA kernels:
+// fp32 at 32, 64, 128), plus Delta for fp32 inputs at every head dim.  Same
+// algebra, plan and masks as the MFMA kernels:
 //   forward   O = softmax2(S c) V, LSE2 = m + log2 l      (:279-626)
-//   Delta     rowsum(O * dO), from O + O_lo for 16-bit O  (:649-710)
+//   Delta     rowsum(O * dO)                              (:649-710)
 //   dQ        P = exp2(S c - LSE), dS = P (dP - Delta), dQ = sm_scale dS K  (:1173-1336)
 //   dK / dV   dV = P^T dO, dK = sm_scale dS^T Q            (:1339-1525)
 // c = sm_scale log2(e) in fp32.  Only non-empty 64 x 64 tiles are visited;
@@ -23,29 +23,14 @@
 namespace kd {
 
 template <class E> struct Elem;
-template <> struct Elem<BF16> { typedef uint16_t T; };
-template <> struct Elem<F16> { typedef uint16_t T; };
 template <> struct Elem<F32> { typedef float T; };
 
 template <class E> KD_DEV float ld(const void* p, int64_t i);
-template <> KD_DEV float ld<BF16>(const void* p, int64_t i) { return to_f32<BF16>(static_cast<const uint16_t*>(p)[i]); }
-template <> KD_DEV float ld<F16>(const void* p, int64_t i) { return to_f32<F16>(static_cast<const uint16_t*>(p)[i]); }
 template <> KD_DEV float ld<F32>(const void* p, int64_t i) { return static_cast<const float*>(p)[i]; }
 
-// store x at element i of p; for 16-bit types with lo given, also the
-// rounding residual x - round(x) at element li of lo
+// store x at element i of p (the residual arguments are for 16-bit element types)
 template <class E> KD_DEV void st(void* p, int64_t i, float x, void* lo = nullptr, int64_t li = 0);
 template <> KD_DEV void st<F32>(void* p, int64_t i, float x, void*, int64_t) { static_cast<float*>(p)[i] = x; }
-template <> KD_DEV void st<BF16>(void* p, int64_t i, float x, void* lo, int64_t li) {
-  const uint32_t w = pack2<BF16>(x, 0.f);
-  static_cast<uint16_t*>(p)[i] = uint16_t(w & 0xFFFFu);
-  if (lo != nullptr) static_cast<uint16_t*>(lo)[li] = uint16_t(pack2_residual<BF16>(x, 0.f, w) & 0xFFFFu);
-}
-template <> KD_DEV void st<F16>(void* p, int64_t i, float x, void* lo, int64_t li) {
-  const uint32_t w = pack2<F16>(x, 0.f);
-  static_cast<uint16_t*>(p)[i] = uint16_t(w & 0xFFFFu);
-  if (lo != nullptr) static_cast<uint16_t*>(lo)[li] = uint16_t(pack2_residual<F16>(x, 0.f, w) & 0xFFFFu);
-}
 
 template <int G> KD_DEV float group_sum(float x) {
 #pragma unroll
@@ -355,14 +340,13 @@ static void launch_simt_d(int which, const AttnArgs& a, const uint8_t* plan, hip
   }
 }
 
-bool use_simt(const AttnArgs& a) { return a.dtype == KD_F32 || (a.D != 64 && a.D != 128 && a.D != 256); }
+// fp32 inputs (16-bit inputs run on the MFMA kernels at every head dim)
+bool use_simt(const AttnArgs& a) { return a.dtype == KD_F32; }
 
 // which: 0 forward, 1 Delta, 2 dQ, 3 dK/dV
 int launch_simt_kernel(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   if (which != 1 && use_f32mma(a)) return launch_f32mma(which, a, plan, st);
-  if (a.dtype == KD_F32) launch_simt_d<F32>(which, a, plan, st);
-  else if (a.dtype == KD_BF16) launch_simt_d<BF16>(which, a, plan, st);
-  else launch_simt_d<F16>(which, a, plan, st);
+  launch_simt_d<F32>(which, a, plan, st);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 

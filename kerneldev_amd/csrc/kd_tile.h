@@ -35,6 +35,17 @@ KD_DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+// A byte offset that no buffer resource here reaches (they all end below
+// 2^31 bytes, which the C ABI checks), also after a tile offset < 2^31 is
+// added: a load from it returns zeros, a DMA writes zeros to LDS.
+constexpr uint32_t OFF_OUTSIDE = 0x80000000u;
+
+// Head dims 16 and 32 run on the D = 64 kernels: each row holds dbytes =
+// 2 D_real bytes and the columns from there to 64 are read as zeros, by
+// sending the loads of those 16-byte chunks outside the buffer.  col: the
+// chunk's byte offset within the row.
+KD_DEV uint32_t col_masked(uint32_t off, uint32_t col, uint32_t dbytes) { return col < dbytes ? off : OFF_OUTSIDE; }
+
 // make_rsrc's four descriptor words, for the inline-asm loads below
 KD_DEV u32x4 rsrc_words(const void* base, uint32_t bytes) {
   const uint64_t a = reinterpret_cast<uint64_t>(base);
@@ -79,13 +90,15 @@ struct Tile {
 
   // Per-lane global byte offsets (relative to the tile's first row) of the
   // chunks this lane moves in each of its LOADS_PER_WAVE wave-wide loads.
-  KD_DEV static void load_offsets(int wave, int lane, uint32_t row_bytes, uint32_t (&off)[LOADS_PER_WAVE]) {
+  // Columns from dbytes on (rows narrower than the tile) read as zeros.
+  KD_DEV static void load_offsets(int wave, int lane, uint32_t row_bytes, uint32_t (&off)[LOADS_PER_WAVE],
+                                  uint32_t dbytes = ROWB) {
 #pragma unroll
     for (int j = 0; j < LOADS_PER_WAVE; ++j) {
       const int u = (wave * LOADS_PER_WAVE + j) * 64 + lane;  // LDS chunk index, row-major
       const int r = u / CPR, pos = u % CPR;
       const int chunk = pos ^ swz(r);
-      off[j] = uint32_t(r) * row_bytes + uint32_t(chunk) * 16u;
+      off[j] = col_masked(uint32_t(r) * row_bytes + uint32_t(chunk) * 16u, uint32_t(chunk) * 16u, dbytes);
     }
   }
   // This wave's share of the tile load through dma_b128 (invisible to the
@@ -228,9 +241,13 @@ struct ScoreOp<E, D, false> {
     return *reinterpret_cast<const u32x4*>(tile + addr[st] + kb * 32 * TL::ROWB);
   }
   KD_DEV f32x16 mma_a(const A& a, int st, const f32x16& c) const { return mfma32x32x16<E>(a, b[st], c); }
-  KD_DEV void load_b(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, int hf) {
+  // dbytes: the row's bytes (2 D_real); columns from there on read as zeros
+  KD_DEV void load_b(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, int hf, uint32_t dbytes = ROW_BYTES) {
 #pragma unroll
-    for (int st = 0; st < NK; ++st) b[st] = buf_load16(rs, row_off + (16 * st + 8 * hf) * 2);
+    for (int st = 0; st < NK; ++st) {
+      const uint32_t col = (16 * st + 8 * hf) * 2;
+      b[st] = buf_load16(rs, col_masked(row_off + col, col, dbytes));
+    }
   }
   KD_DEV void init(int srow, int hf) {
 #pragma unroll
@@ -262,7 +279,7 @@ struct ScoreOp<E, D, true> {
   KD_DEV f32x16 mma_a(const A& a, int st, const f32x16& c) const {
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b[st], c, 0, 0, 0, 127, 0, 127);
   }
-  KD_DEV void load_b(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, int hf) {
+  KD_DEV void load_b(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, int hf, uint32_t /*dbytes*/ = ROW_BYTES) {
 #pragma unroll
     for (int st = 0; st < NK; ++st) {
       const u32x4 lo = buf_load16(rs, row_off + 64 * st + 32 * hf);

@@ -132,27 +132,44 @@ def _other_dims_case(D, causal_only, seed):
 @pytest.mark.parametrize("causal_only", [True, False])
 def test_other_head_dims(dev, D, causal_only):
     """The head dims original_kernel.py:1720 accepts beyond 64 / 128: 16 and 32
-    zero-padded onto the d = 64 MFMA kernels, 256 on its own MFMA kernels."""
+    on the d = 64 MFMA kernels (columns past d read as zeros), 256 on its own
+    MFMA kernels."""
     _case(_other_dims_case(D, causal_only, seed=40 + D), dev)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("D", [16, 32])
-def test_small_head_dims_on_the_vector_alu_kernels(dev, D):
-    """flash_attention runs 16-bit d = 16, 32 zero-padded on the d = 64 MFMA
-    kernels; the C ABI itself runs them on the fp32 vector-ALU kernels, called
-    here directly through the ops with the unpadded operands."""
+@pytest.mark.parametrize("garbage_pad", [False, True])
+def test_small_head_dims_on_the_mfma_kernels(dev, D, dtype, garbage_pad):
+    """16-bit d = 16, 32 through the C ABI (the ops, unpadded operands) on the
+    d = 64 MFMA kernels: each row's missing columns are read as zeros and only
+    the d real ones stored.  With garbage_pad every row of q, k, v, dO is
+    followed by 8 NaNs in memory (t-stride d + 8): a read past the row would
+    turn the results into NaN.  The same with causal and cocktail masks."""
     from kerneldev_amd.attention import _bwd_op, _fwd_op
     from kerneldev_amd import _lib
 
-    inp = _other_dims_case(D, False, seed=70 + D)
-    print(f"vector-ALU kernels, bf16 D={D}", flush=True)
-    q, k, v, do = (inp[x].to(dev) for x in ("q", "k", "v", "do"))
-    meta = [inp[n].to(dev) for n in ("in_span", "span_id", "is_prefix")]
-    sc = D ** -0.5
-    o, lse, plan, o_lo, *_ = _fwd_op(q, k, v, None, *meta, sc, _lib.KD_MODE_FORMULA, True)
-    dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, sc, o_lo)
-    torch.cuda.synchronize()
-    compare({"o": o, "lse": lse, "dq": dq, "dk": dk, "dv": dv}, _reference(inp))
+    for causal_only in (True, False):
+        inp = _other_dims_case(D, causal_only, seed=70 + D + int(causal_only))
+        inp = {n: (t.to(dtype) if torch.is_tensor(t) and t.is_floating_point() else t) for n, t in inp.items()}
+        print(f"MFMA kernels, {dtype} D={D} garbage_pad={garbage_pad} {inp['name']}", flush=True)
+        xs = []
+        for n in ("q", "k", "v", "do"):
+            x = inp[n].to(dev)
+            if garbage_pad:
+                buf = torch.full(x.shape[:3] + (D + 8,), float("nan"), dtype=dtype, device=dev)
+                buf[..., :D] = x
+                x = buf[..., :D]
+                assert x.stride(2) == D + 8
+            xs.append(x)
+        q, k, v, do = xs
+        meta = [inp[n].to(dev) if inp.get(n) is not None else None for n in ("in_span", "span_id", "is_prefix")]
+        mode = _lib.KD_MODE_CAUSAL if causal_only else _lib.KD_MODE_FORMULA
+        sc = D ** -0.5
+        o, lse, plan, o_lo, *_ = _fwd_op(q, k, v, None, *meta, sc, mode, True)
+        dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, sc, o_lo)
+        torch.cuda.synchronize()
+        compare({"o": o, "lse": lse, "dq": dq, "dk": dk, "dv": dv}, _reference(inp))
 
 
 @pytest.mark.parametrize("D", [32, 256])
@@ -316,7 +333,7 @@ def test_fp16(dev):
 
 @pytest.mark.parametrize("D", [32, 128, 256])
 def test_fp16_head_dims(dev, D):
-    """fp16 on the d = 128 and 256 kernels and, zero-padded, the d = 64 ones (d = 32)."""
+    """fp16 on the d = 128 and 256 kernels, and at d = 32 on the d = 64 ones."""
     tokens, in_span, span_id, is_prefix = cocktail_batch(2, 512, CONFIG3_LAYOUT, seed=8 + D)
     q, k, v, do = qkvdo(2, 2, 384, D, seed=9 + D, dtype=torch.float16)
     _case(dict(name=f"fp16 D{D}", q=q, k=k, v=v, do=do, in_span=in_span[:, :384], span_id=span_id[:, :384],
@@ -520,8 +537,8 @@ def test_fp8_error_against_unquantised_oracle(dev):
 @pytest.mark.parametrize("D", [64, 32, 256])
 def test_out_layout_bthd(dev, D):
     """O written into [B, T, H, d] memory (model.py:95's layout), against the oracle,
-    with model-layout strided q/k/v views in (model.py:76-78); at d = 32 through
-    the zero-padded path, at d = 256 through the wide kernels."""
+    with model-layout strided q/k/v views in (model.py:76-78); at d = 32 on the
+    d = 64 kernels, at d = 256 through the wide kernels."""
     tokens, in_span, span_id, is_prefix = cocktail_batch(2, 512, CONFIG3_LAYOUT, seed=23)
     B, H, T = 2, 3, 512
     g = torch.Generator("cpu").manual_seed(24)
@@ -531,8 +548,7 @@ def test_out_layout_bthd(dev, D):
     print(f"out_layout bthd case D={D}", flush=True)
     o = flash_attention(q, k, v, out_layout="bthd", **meta)
     assert o.shape == (B, H, T, D)
-    if D >= 64:  # (padded head dims return a view of the padded output)
-        assert o.transpose(1, 2).is_contiguous()
+    assert o.transpose(1, 2).is_contiguous()
     o.backward(base[3].to(dev).transpose(1, 2))
     torch.cuda.synchronize()
     cpu = [x.transpose(1, 2) for x in base]

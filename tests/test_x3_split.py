@@ -57,7 +57,8 @@ def test_head_dim_route():
     from kerneldev_amd.attention import head_dim_route
 
     bf, f32 = torch.bfloat16, torch.float32
-    assert head_dim_route(bf, 16, "tf32") == (False, 64) and head_dim_route(bf, 32, "bf16") == (False, 64)
+    # 16-bit inputs go to the MFMA kernels unpadded at every head dim
+    assert all(head_dim_route(bf, d, p) == (False, 0) for d in (16, 32, 64, 128, 256) for p in ("tf32", "ieee", "bf16"))
     assert head_dim_route(torch.float16, 128, "ieee") == (False, 0)
     assert head_dim_route(f32, 16, "tf32") == (True, 0) and head_dim_route(f32, 32, "tf32") == (True, 0)
     assert head_dim_route(f32, 64, "tf32") == (False, 0) and head_dim_route(f32, 128, "tf32") == (False, 0)
