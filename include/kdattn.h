@@ -56,6 +56,11 @@ extern "C" {
                             hi + lo, ~16 significant bits (default) */
 #define KD_PREC_SINGLE 1 /* P and dS rounded once to the input type (8 significant bits for
                             bf16, as the reference's forward rounds P to V's dtype) */
+#define KD_PREC_SPLIT3 2 /* P and dS enter their products as a 16-bit triple hi + mid + lo, ~24
+                            significant bits (bf16), as the reference's fp32 backward dots take
+                            them at precision "ieee"; the residual outputs o_lo, dq_lo, dk_lo and
+                            dv_lo are then fp32, so that o + o_lo (etc.) carry fp32 precision and
+                            the backward's Delta sees O to it.  Not with fp8 scores. */
 /* span_id index dtypes */
 #define KD_I64 0
 #define KD_I32 1
@@ -112,9 +117,9 @@ typedef struct kd_attn_args {
                                    then -LSE / c [B, H, T] with c the score scale (sm_scale log2 e, times
                                    q_scale k_scale with fp8 scores; -inf for fully masked rows) */
   void *o_lo;                   /* optional contiguous [B, H, T, D], dtype of o (bf16 /
-                                   fp16 only; NULL with fp32 inputs): the forward writes
-                                   O_fp32 - O there, the backward's Delta reads it; NULL
-                                   to skip */
+                                   fp16 only; NULL with fp32 inputs), fp32 at precision
+                                   KD_PREC_SPLIT3: the forward writes O_fp32 - O there, the
+                                   backward's Delta reads it; NULL to skip */
   const uint8_t *q8, *k8;       /* optional fp8 e4m3 copies of q and k, contiguous
                                    [B, H, T, D] (kd_quant_fp8): when both are given, S = Q K^T
                                    is computed from them on fp8 MFMA, times q_scale * k_scale */
@@ -123,14 +128,15 @@ typedef struct kd_attn_args {
                                    Q R, K R with R = diag(signs) H_D / sqrt(D) (kd_hadamard), and
                                    dQ, dK are returned for the unrotated Q, K, i.e. times R^T,
                                    applied in the kernels' epilogues; NULL: dQ, dK as computed */
-  void *dq_lo, *dk_lo, *dv_lo;  /* optional contiguous [B, H, T, D] of the 16-bit dtype (bwd): the
+  void *dq_lo, *dk_lo, *dv_lo;  /* optional contiguous [B, H, T, D] of the 16-bit dtype (fp32 at
+                                   precision KD_PREC_SPLIT3) (bwd): the
                                    rounding residuals dQ_fp32 - dQ (etc.), so that dq + dq_lo carries
                                    the gradient to ~16 significant bits (as o_lo does for O); NULL to
                                    skip; not with dqk_signs or fp32 inputs */
   int32_t B, H, T, D;
   int32_t dtype;                /* KD_BF16 / KD_F16 / KD_F32 */
   float sm_scale;
-  int32_t precision;            /* KD_PREC_SPLIT (0, default) / KD_PREC_SINGLE */
+  int32_t precision;            /* KD_PREC_SPLIT (0, default) / KD_PREC_SINGLE / KD_PREC_SPLIT3 */
   int32_t pad_;
 } kd_attn_args;
 

@@ -20,7 +20,7 @@ KD_OK, KD_ERR_INVALID, KD_ERR_UNSUPPORTED, KD_ERR_LAUNCH = 0, -1, -2, -3
 KD_BF16, KD_F16, KD_F32 = 0, 1, 2
 KD_I64, KD_I32 = 0, 1
 KD_MODE_FORMULA, KD_MODE_CAUSAL, KD_MODE_ALL = 0, 1, 2
-KD_PREC_SPLIT, KD_PREC_SINGLE = 0, 1
+KD_PREC_SPLIT, KD_PREC_SINGLE, KD_PREC_SPLIT3 = 0, 1, 2
 KD_NOALLOC_WORKSPACE_FLOATS = 1 << 22
 
 I64x2 = c_int64 * 2

@@ -43,11 +43,19 @@ FP32_PADDED_HEAD_DIMS = {16: 32}
 
 # precision -> arithmetic of P and dS in the kernels.  The reference rounds P
 # to V's dtype for P V (original_kernel.py:566-571) and keeps P and dS in fp32
-# for its backward dots, taken as tf32 or ieee (:1331-1333, :1517-1523); the
-# split kernels carry P and dS as a 16-bit hi + lo pair (~16 significant
-# bits) in all four products, at or above the reference on each.  "bf16" (an
-# extension) rounds P and dS once to the input type: faster, 8 significant bits.
-PRECISIONS = {"ieee": _lib.KD_PREC_SPLIT, "tf32": _lib.KD_PREC_SPLIT, "bf16": _lib.KD_PREC_SINGLE}
+# for its backward dots, taken as tf32 or ieee (:1331-1333, :1517-1523).
+# "tf32" (the default): P and dS as a 16-bit hi + lo pair (~16 significant
+# bits, above tf32's 11) in all four products.  "ieee": as a hi + mid + lo
+# triple (~24 significant bits, the fp32 the reference's ieee dots take), with
+# O's rounding residual kept in fp32 so that the backward's Delta sees the fp32
+# O.  "bf16" (an extension) rounds P and dS once to the input type: faster, 8
+# significant bits.  fp32 inputs get fp32 arithmetic at "ieee" and "tf32" alike.
+PRECISIONS = {"ieee": _lib.KD_PREC_SPLIT3, "tf32": _lib.KD_PREC_SPLIT, "bf16": _lib.KD_PREC_SINGLE}
+
+
+def _lo_dtype(dtype: torch.dtype, prec: int) -> torch.dtype:
+    """dtype of the residual buffers (o_lo, dq_lo, ...): fp32 at KD_PREC_SPLIT3."""
+    return torch.float32 if prec == _lib.KD_PREC_SPLIT3 else dtype
 
 
 def _stream(device) -> ctypes.c_void_p:
@@ -230,7 +238,7 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
     o = _new_out(B, H, T, D, q, bthd)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
     # rounding residual of O, kept for the backward's Delta (see kd_bwd.hip)
-    o_lo = torch.empty((B, H, T, D) if need_lo else (0,), dtype=q.dtype, device=q.device)
+    o_lo = torch.empty((B, H, T, D) if need_lo else (0,), dtype=_lo_dtype(q.dtype, prec), device=q.device)
     a = _attn_args(q, k, v, sm_scale, prec)
     _set_fp8(a, _fp8_tuple(q8, k8, q_scale, k_scale))
     a.o, a.o_strides = o.data_ptr(), _strides3(o)
@@ -250,7 +258,7 @@ def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_l
     return (_new_out(B, H, T, D, q, bthd),
             torch.empty((B, H, T), dtype=torch.float32, device=q.device),
             torch.empty(_lib.plan_nbytes(B, T, D) if plan_in is None else 0, dtype=torch.uint8, device=q.device),
-            torch.empty((B, H, T, D) if need_lo else (0,), dtype=q.dtype, device=q.device),
+            torch.empty((B, H, T, D) if need_lo else (0,), dtype=_lo_dtype(q.dtype, prec), device=q.device),
             torch.empty(rot_shape, dtype=q.dtype, device=q.device),
             torch.empty(rot_shape, dtype=k.dtype, device=k.device),
             torch.empty(q8_shape, dtype=torch.uint8, device=q.device),
@@ -504,11 +512,14 @@ def flash_attention(
     Args mirror ``original_kernel.py:2096-2112``.  ``autotune`` and
     ``prescale_qk`` are accepted and ignored (tile shapes are compile-time
     constants here and the scale is always applied in fp32).  ``precision``
-    is ``"ieee"`` or ``"tf32"`` as in the reference; both run the kernels that
-    carry P and dS as 16-bit hi + lo pairs (about 16 significant bits in P V,
-    dV, dQ and dK, at or above the reference's bf16 P V and tf32 / ieee
-    backward dots).  The extension ``"bf16"`` rounds P and dS once to the
-    input type instead (faster; 8 significant bits with bf16 inputs).  fp32
+    is ``"ieee"`` or ``"tf32"`` as in the reference.  ``"tf32"`` runs the
+    kernels that carry P and dS as 16-bit hi + lo pairs (about 16 significant
+    bits in P V, dV, dQ and dK, at or above the reference's bf16 P V and tf32
+    backward dots); ``"ieee"`` carries them as hi + mid + lo triples (about 24
+    bits, the fp32 of the reference's ieee dots), with O's residual kept in
+    fp32 for the backward's Delta.  The extension ``"bf16"`` rounds P and dS
+    once to the input type instead (faster; 8 significant bits with bf16
+    inputs).  fp32
     inputs get fp32 arithmetic at both "ieee" and "tf32": the fp32 MFMA
     kernels at head dims 32, 64, 128 (16 zero-padded to 32) and the fp32
     vector-ALU kernels at 256, except "tf32" at 16 and 32, which runs as bf16x3
@@ -555,6 +566,8 @@ def flash_attention(
         raise ValueError(f"out_layout must be 'bhtd' or 'bthd', got {out_layout!r}")
     if qk_dtype not in ("bf16", "fp8_e4m3"):
         raise ValueError(f"qk_dtype must be 'bf16' or 'fp8_e4m3', got {qk_dtype!r}")
+    if qk_dtype == "fp8_e4m3" and precision == "ieee":
+        raise ValueError("the fp8 QK^T path runs at precision 'tf32' or 'bf16' (its scores carry 4 significant bits)")
     if not q.is_cuda:
         raise ValueError("flash_attention runs on the GPU only (no CPU fallback)")
     if k.device != q.device or v.device != q.device:

@@ -68,12 +68,24 @@ __global__ __launch_bounds__(256) void k_delta(AttnArgs a) {
                          t * a.do_strides[2] + seg * 8;
     const u32x4 ov = *reinterpret_cast<const u32x4*>(op);
     const u32x4 dv = *reinterpret_cast<const u32x4*>(dp);
-    u32x4 lv = {0, 0, 0, 0};
-    if (a.o_lo != nullptr) lv = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.o_lo) + row * D + seg * 8);
+    // O's residual: 16-bit, or fp32 at precision KD_PREC_SPLIT3
+    float lo[8] = {};
+    if (a.o_lo != nullptr) {
+      if (a.precision == KD_PREC_SPLIT3) {
+        const float* l32 = static_cast<const float*>(a.o_lo) + row * D + seg * 8;
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(l32), x1 = *reinterpret_cast<const f32x4*>(l32 + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lo[i] = x0[i], lo[4 + i] = x1[i];
+      } else {
+        const u32x4 lv = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.o_lo) + row * D + seg * 8);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) lo[2 * w] = to_f32<E>(uint16_t(lv[w] & 0xFFFFu)), lo[2 * w + 1] = to_f32<E>(uint16_t(lv[w] >> 16));
+      }
+    }
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float o0 = to_f32<E>(uint16_t(ov[w] & 0xFFFFu)) + to_f32<E>(uint16_t(lv[w] & 0xFFFFu));
-      const float o1 = to_f32<E>(uint16_t(ov[w] >> 16)) + to_f32<E>(uint16_t(lv[w] >> 16));
+      const float o0 = to_f32<E>(uint16_t(ov[w] & 0xFFFFu)) + lo[2 * w];
+      const float o1 = to_f32<E>(uint16_t(ov[w] >> 16)) + lo[2 * w + 1];
       sum += o0 * to_f32<E>(uint16_t(dv[w] & 0xFFFFu));
       sum += o1 * to_f32<E>(uint16_t(dv[w] >> 16));
     }
@@ -91,10 +103,11 @@ __global__ __launch_bounds__(256) void k_delta(AttnArgs a) {
 // caller's contiguous residual row), so that g + glo carries the fp32 value to
 // about twice the type's significant bits
 // dlim: columns from there on are not stored (head dims 16 and 32 on the
-// D = 64 kernels)
+// D = 64 kernels).  lo32: glo holds fp32 residuals (precision KD_PREC_SPLIT3),
+// so that g + glo is the fp32 value.
 template <class E, int D>
-KD_DEV void store_rows_T(uint16_t* g, const f32x16 (&acc)[D / 32], float scale, int hf, uint16_t* glo = nullptr,
-                         int dlim = D) {
+KD_DEV void store_rows_T(uint16_t* g, const f32x16 (&acc)[D / 32], float scale, int hf, void* glo = nullptr,
+                         int dlim = D, bool lo32 = false) {
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
@@ -105,11 +118,23 @@ KD_DEV void store_rows_T(uint16_t* g, const f32x16 (&acc)[D / 32], float scale, 
                           acc[db][4 * gg + 3] * scale};
       const u32x2 w = {pack2<E>(f[0], f[1]), pack2<E>(f[2], f[3])};
       *reinterpret_cast<u32x2*>(g + d0) = w;
-      if (glo != nullptr)
-        *reinterpret_cast<u32x2*>(glo + d0) = u32x2{pack2_residual<E>(f[0], f[1], w[0]),
-                                                    pack2_residual<E>(f[2], f[3], w[1])};
+      if (glo != nullptr && lo32)
+        *reinterpret_cast<f32x4*>(static_cast<float*>(glo) + d0) =
+            f32x4{f[0] - to_f32<E>(uint16_t(w[0] & 0xFFFFu)), f[1] - to_f32<E>(uint16_t(w[0] >> 16)),
+                  f[2] - to_f32<E>(uint16_t(w[1] & 0xFFFFu)), f[3] - to_f32<E>(uint16_t(w[1] >> 16))};
+      else if (glo != nullptr)
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(glo) + d0) =
+            u32x2{pack2_residual<E>(f[0], f[1], w[0]), pack2_residual<E>(f[2], f[3], w[1])};
     }
   }
+}
+
+// The contiguous residual row [.., a.D] of element row `row` of a residual
+// buffer (16-bit, or fp32 at precision KD_PREC_SPLIT3); NULL stays NULL
+KD_DEV void* lo_row(void* base, int64_t row, int dim, bool lo32) {
+  if (base == nullptr) return nullptr;
+  return lo32 ? static_cast<void*>(static_cast<float*>(base) + row * dim)
+              : static_cast<void*>(static_cast<uint16_t*>(base) + row * dim);
 }
 
 // The rows of a transposed accumulator times R^T, R = diag(s) H_D / sqrt(D)
@@ -171,12 +196,14 @@ KD_DEV void tr_addrs(int lane, int (&addr)[D / 32][2]) {
 // DH, D0: this launch accumulates dQ's columns [D0, D0 + DH) (D = 256 runs
 // two launches of 128 columns, each recomputing S and dP, so that the dQ
 // accumulators fit next to the operands of the full head dim)
-template <class E, int D, bool Q8, bool SP, int DH = D, int D0 = 0>
+// NSP: the parts dS enters dQ in (1, 2 or 3: parts_of the precision)
+template <class E, int D, bool Q8, int NSP, int DH = D, int D0 = 0>
 __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const uint32_t* __restrict__ codes,
                                                const uint32_t* __restrict__ list,
                                                const int32_t* __restrict__ count,
                                                const uint32_t* __restrict__ order, int nT, int nQB,
                                                bool fuse_delta) {
+  constexpr bool SP = NSP >= 2, S3 = NSP == 3;
   using TL = Tile<D>;
   using SO = ScoreOp<E, D, Q8>;  // S^T = K Q^T (16-bit, or fp8 from the K8 tile)
   using TK8 = typename ScoreOp<E, D, true>::TL;
@@ -235,19 +262,34 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
     const uint16_t* og = static_cast<const uint16_t*>(a.o) + b * a.o_strides[0] + h * a.o_strides[1];
     const uint32_t orb = uint32_t(a.o_strides[2]) * 2u;
     const auto rs_o = make_rsrc(og, uint32_t(T) * orb);
-    // o_lo is contiguous [B, H, T, a.D]; without it the empty resource reads zeros
-    const uint16_t* lg = a.o_lo == nullptr ? nullptr : static_cast<const uint16_t*>(a.o_lo) + int64_t(bh) * T * a.D;
-    const auto rs_lo = make_rsrc(lg, lg == nullptr ? 0u : uint32_t(T) * dbytes);
+    // o_lo is contiguous [B, H, T, a.D] (fp32 with S3); without it the empty
+    // resource reads zeros
+    const uint32_t lsz = S3 ? 4u : 2u;  // bytes per residual element
+    const uint8_t* lg = a.o_lo == nullptr ? nullptr
+                                          : static_cast<const uint8_t*>(a.o_lo) + int64_t(bh) * T * a.D * lsz;
+    const auto rs_lo = make_rsrc(lg, lg == nullptr ? 0u : uint32_t(T) * uint32_t(a.D) * lsz);
     float sum = 0.f;
 #pragma unroll
     for (int st = 0; st < DS; ++st) {
       const uint32_t col = (16 * st + 8 * hf) * 2;
       const u32x4 ov = buf_load16(rs_o, col_masked(uint32_t(qrow) * orb + col, col, dbytes));
-      const u32x4 lv = buf_load16(rs_lo, col_masked(uint32_t(qrow) * dbytes + col, col, dbytes));
+      float lo[8];
+      if constexpr (S3) {
+        const uint32_t l0 = uint32_t(qrow) * dbytes * 2u + col * 2u;
+        const u32x4 x0 = buf_load16(rs_lo, col_masked(l0, col, dbytes));
+        const u32x4 x1 = buf_load16(rs_lo, col_masked(l0 + 16u, col, dbytes));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lo[i] = __uint_as_float(x0[i]), lo[4 + i] = __uint_as_float(x1[i]);
+      } else {
+        const u32x4 lv = buf_load16(rs_lo, col_masked(uint32_t(qrow) * dbytes + col, col, dbytes));
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+          lo[2 * w] = to_f32<E>(uint16_t(lv[w] & 0xFFFFu)), lo[2 * w + 1] = to_f32<E>(uint16_t(lv[w] >> 16));
+      }
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const float o0 = to_f32<E>(uint16_t(ov[w] & 0xFFFFu)) + to_f32<E>(uint16_t(lv[w] & 0xFFFFu));
-        const float o1 = to_f32<E>(uint16_t(ov[w] >> 16)) + to_f32<E>(uint16_t(lv[w] >> 16));
+        const float o0 = to_f32<E>(uint16_t(ov[w] & 0xFFFFu)) + lo[2 * w];
+        const float o1 = to_f32<E>(uint16_t(ov[w] >> 16)) + lo[2 * w + 1];
         sum += o0 * to_f32<E>(uint16_t(dof[st][w] & 0xFFFFu));
         sum += o1 * to_f32<E>(uint16_t(dof[st][w] >> 16));
       }
@@ -418,9 +460,10 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
       __builtin_amdgcn_sched_barrier(0x4);
     }
     // dS packed for the MFMA and, with SP, its rounding residual: dQ takes
-    // dS to ~16 significant bits as two products
+    // dS to ~16 significant bits as two products (with S3, ~24 as three)
     u32x4 dsb[2][2];
     u32x4 dsl[SP ? 2 : 1][2];
+    u32x4 dsm[S3 ? 2 : 1][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       float ds[16];
@@ -430,6 +473,7 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
       for (int t = 0; t < 2; ++t) {
         dsb[kb][t] = pack8<E>(ds + 8 * t);
         if constexpr (SP) dsl[kb][t] = pack8_residual<E>(ds + 8 * t, dsb[kb][t]);
+        if constexpr (S3) dsm[kb][t] = pack8_residual2<E>(ds + 8 * t, dsb[kb][t], dsl[kb][t]);
       }
     }
     // dQ^T += K^T dS^T, K^T read transposed DQ_PF steps ahead (steps: t4 = i / DB, db = i % DB)
@@ -450,6 +494,7 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
         __builtin_amdgcn_sched_barrier(0x406);
         acc[db] = mfma32x32x16<E>(av[i % PF], dsb[t4 >> 1][t4 & 1], acc[db]);
         if constexpr (SP) acc[db] = mfma32x32x16<E>(av[i % PF], dsl[t4 >> 1][t4 & 1], acc[db]);
+        if constexpr (S3) acc[db] = mfma32x32x16<E>(av[i % PF], dsm[S3 ? t4 >> 1 : 0][t4 & 1], acc[db]);
         if (i + PF < NS) av[i % PF] = read(i + PF);
       }
       __builtin_amdgcn_sched_barrier(0x406);
@@ -463,13 +508,13 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
 
   if (qvalid) {
     uint16_t* g = static_cast<uint16_t*>(a.dq) + b * a.dq_strides[0] + h * a.dq_strides[1] + qrow * a.dq_strides[2];
-    uint16_t* glo = a.dq_lo == nullptr ? nullptr
-                                       : static_cast<uint16_t*>(a.dq_lo) + ((int64_t(b) * a.H + h) * a.T + qrow) * a.D;
+    void* glo = lo_row(a.dq_lo, (int64_t(b) * a.H + h) * a.T + qrow, a.D, S3);
     if constexpr (DH == D) {
       if (a.dqk_signs != nullptr) store_rows_T_unrot<E, D>(g, acc, a.sm_scale, hf, a.dqk_signs);
-      else store_rows_T<E, D>(g, acc, a.sm_scale, hf, glo, a.D);
+      else store_rows_T<E, D>(g, acc, a.sm_scale, hf, glo, a.D, S3);
     } else {  // (no dqk_signs at split widths)
-      store_rows_T<E, DH>(g + D0, acc, a.sm_scale, hf, glo == nullptr ? nullptr : glo + D0);
+      void* glo_h = glo == nullptr ? nullptr : static_cast<void*>(static_cast<uint8_t*>(glo) + D0 * (S3 ? 4 : 2));
+      store_rows_T<E, DH>(g + D0, acc, a.sm_scale, hf, glo_h, DH, S3);
     }
   }
 }
@@ -489,10 +534,12 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
 // e - 1 with the P written in step e - 1.  So one barrier per step orders
 // everything (tile e landed, P(e-1) written, P(e-2) and tile e-2 released),
 // at the price of a third Q buffer (dK reads Q of tile e - 1).
-template <class E, int D, bool Q8, bool SP>
+// NSP: the parts P and dS enter dV and dK in (1, 2 or 3: parts_of the precision)
+template <class E, int D, bool Q8, int NSP>
 __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __restrict__ codes,
                                                  const uint32_t* __restrict__ list,
                                                  const int32_t* __restrict__ count, int nT, int nKB) {
+  constexpr bool SP = NSP >= 2, S3 = NSP == 3;
   constexpr int NW = 8;
   using TL = Tile<D, NW>;
   using TQ8 = Tile<Q8 ? D / 2 : D, NW>;  // fp8 Q tiles (D bytes a row); only used at D = 128
@@ -654,8 +701,9 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   // acc^T += A^T bop over the 64 queries of a tile (k-steps k4 = 2 qb + t),
   // A^T read transposed from tile `at`; steps i = 4 k4 ... ordered (k4, db)
   // With SP, bopl holds the residual of bop and enters the same accumulator
-  // through a second MFMA on the same A operand.
-  auto accumulate = [&](const uint8_t* at_g, const u32x4 (&bop)[2][2], const u32x4 (&bopl)[2][2]) {
+  // through a second MFMA on the same A operand; with S3 bopm a third part.
+  auto accumulate = [&](const uint8_t* at_g, const u32x4 (&bop)[2][2], const u32x4 (&bopl)[2][2],
+                        const u32x4 (&bopm)[2][2]) {
     lds_u8* at = to_lds(at_g);
     constexpr int NS = 4 * DB;
     lds_u8* pa[DB][2];  // one address per (db, half); the k-step offsets are immediates
@@ -679,6 +727,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
       __builtin_amdgcn_sched_barrier(0x406);
       acc[db] = mfma32x32x16<E>(av[i % PF], bop[k4 >> 1][k4 & 1], acc[db]);
       if constexpr (SP) acc[db] = mfma32x32x16<E>(av[i % PF], bopl[k4 >> 1][k4 & 1], acc[db]);
+      if constexpr (S3) acc[db] = mfma32x32x16<E>(av[i % PF], bopm[k4 >> 1][k4 & 1], acc[db]);
       if (i + PF < NS) av[i % PF] = read(i + PF);
     }
     __builtin_amdgcn_sched_barrier(0x406);
@@ -797,6 +846,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
         if constexpr (Q8) load_q16(en, sl);
         u32x4 bop[2][2];                // packed P: B operand of k-step 2 qb + t
         u32x4 bopl[2][2];               // SP: its rounding residual (unused otherwise)
+        u32x4 bopm[2][2];               // S3: its third part (unused otherwise)
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
@@ -807,6 +857,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
             bop[qb][t] = pack8<E>(p);
             if constexpr (SP) {
               bopl[qb][t] = pack8_residual<E>(p, bop[qb][t]);
+              if constexpr (S3) bopm[qb][t] = pack8_residual2<E>(p, bop[qb][t], bopl[qb][t]);
               // the fp32 P for the dS wave, stored as it is formed (holding
               // it across the dV MFMAs would take 32 more registers)
               s_p[pb][pair][2 * (2 * qb + t)][lane] = u32x4{__float_as_uint(p[0]), __float_as_uint(p[1]),
@@ -815,7 +866,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
                                                                 __float_as_uint(p[6]), __float_as_uint(p[7])};
             }
           }
-        accumulate(s_do[sl.d], bop, bopl);  // dV^T += dO^T P
+        accumulate(s_do[sl.d], bop, bopl, bopm);  // dV^T += dO^T P
         // 16-bit P for the dS wave (read after the next barrier).  Written
         // after the MFMAs: LDS stores may not cross the product's scheduling
         // fences, so stores placed before it would hold all of P's VALU work
@@ -832,6 +883,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
         const int qprev = wrap(sl.q + NQ - 1, NQ);
         u32x4 dsb[2][2];
         u32x4 dsl[2][2];  // SP: dS's rounding residual (unused otherwise)
+        u32x4 dsm[2][2];  // S3: its third part (unused otherwise)
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
@@ -856,8 +908,9 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
             }
             dsb[qb][t] = pack8<E>(ds);
             if constexpr (SP) dsl[qb][t] = pack8_residual<E>(ds, dsb[qb][t]);
+            if constexpr (S3) dsm[qb][t] = pack8_residual2<E>(ds, dsb[qb][t], dsl[qb][t]);
           }
-        accumulate(s_q[qprev], dsb, dsl);  // dK^T += Q^T dS
+        accumulate(s_q[qprev], dsb, dsl, dsm);  // dK^T += Q^T dS
       }
       if (e < n) {  // dP of tile e, started from -Delta of its query (register layout as for S)
 #pragma unroll
@@ -889,12 +942,11 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
     uint16_t* g = role == 0
         ? static_cast<uint16_t*>(a.dv) + b * a.dv_strides[0] + h * a.dv_strides[1] + krow * a.dv_strides[2]
         : static_cast<uint16_t*>(a.dk) + b * a.dk_strides[0] + h * a.dk_strides[1] + krow * a.dk_strides[2];
-    void* lo = role == 0 ? a.dv_lo : a.dk_lo;
-    uint16_t* glo = lo == nullptr ? nullptr : static_cast<uint16_t*>(lo) + ((int64_t(b) * H + h) * T + krow) * D;
+    void* glo = lo_row(role == 0 ? a.dv_lo : a.dk_lo, (int64_t(b) * H + h) * T + krow, D, S3);
     if (__builtin_amdgcn_readfirstlane(role) == 1 && a.dqk_signs != nullptr)  // dK, rotated back
       store_rows_T_unrot<E, D>(g, acc, a.sm_scale, hf, a.dqk_signs);
     else
-      store_rows_T<E, D>(g, acc, role == 0 ? 1.f : a.sm_scale, hf, glo);
+      store_rows_T<E, D>(g, acc, role == 0 ? 1.f : a.sm_scale, hf, glo, D, S3);
   }
 }
 
@@ -912,10 +964,11 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
 // blocks, read transposed).  Two launches (D0 = 0, 128) give the whole
 // gradient, each recomputing S and dP.  Tiles are copied one step ahead into
 // two slots (2 x 2 x 32 KiB).
-template <class E, int D, bool SP, int DH, int D0>
+template <class E, int D, int NSP, int DH, int D0>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, const uint32_t* __restrict__ codes,
                                                       const uint32_t* __restrict__ list,
                                                       const int32_t* __restrict__ count, int nT, int nKB) {
+  constexpr bool SP = NSP >= 2, S3 = NSP == 3;
   using TL = Tile<D, 4>;
   constexpr int DS = D / 16, NL = TL::LOADS_PER_WAVE;
   constexpr int HB = DH / 32, HB0 = D0 / 32;  // column blocks of this launch
@@ -1019,7 +1072,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
     __builtin_amdgcn_sched_barrier(0x406);
   };
   auto accumulate = [&](const uint8_t* at_g, f32x16 (&acc)[HB], const u32x4 (&bop)[2][2],
-                        const u32x4 (&bopl)[2][2]) {
+                        const u32x4 (&bopl)[2][2], const u32x4 (&bopm)[2][2]) {
     lds_u8* at = to_lds(at_g);
     constexpr int NS = 4 * HB;
     auto read = [&](int i) {
@@ -1037,6 +1090,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
       __builtin_amdgcn_sched_barrier(0x406);
       acc[db] = mfma32x32x16<E>(av[i % PF], bop[k4 >> 1][k4 & 1], acc[db]);
       if constexpr (SP) acc[db] = mfma32x32x16<E>(av[i % PF], bopl[k4 >> 1][k4 & 1], acc[db]);
+      if constexpr (S3) acc[db] = mfma32x32x16<E>(av[i % PF], bopm[k4 >> 1][k4 & 1], acc[db]);
       if (i + PF < NS) av[i % PF] = read(i + PF);
     }
     __builtin_amdgcn_sched_barrier(0x406);
@@ -1093,7 +1147,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
         for (int r = 0; r < 16; ++r) x[qb][r] = mask_bit(x[qb][r], w, 16 * (r >> 3) + (r & 7));
       }
     }
-    u32x4 pb[2][2], pl[2][2], sb[2][2], sl_[2][2];
+    u32x4 pb[2][2], pl[2][2], pm[2][2], sb[2][2], sl_[2][2], sm[2][2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
@@ -1110,25 +1164,33 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
           pl[qb][t] = pack8_residual<E>(p, pb[qb][t]);
           sl_[qb][t] = pack8_residual<E>(ds, sb[qb][t]);
         }
+        if constexpr (S3) {
+          pm[qb][t] = pack8_residual2<E>(p, pb[qb][t], pl[qb][t]);
+          sm[qb][t] = pack8_residual2<E>(ds, sb[qb][t], sl_[qb][t]);
+        }
       }
-    accumulate(s_do[slot], acc_v, pb, pl);  // dV^T += dO^T P
-    accumulate(s_q[slot], acc_k, sb, sl_);  // dK^T += Q^T dS
+    accumulate(s_do[slot], acc_v, pb, pl, pm);  // dV^T += dO^T P
+    accumulate(s_q[slot], acc_k, sb, sl_, sm);  // dK^T += Q^T dS
     slot ^= 1;
   }
 
   if (kvalid) {
     uint16_t* gv = static_cast<uint16_t*>(a.dv) + b * a.dv_strides[0] + h * a.dv_strides[1] + krow * a.dv_strides[2];
     uint16_t* gk = static_cast<uint16_t*>(a.dk) + b * a.dk_strides[0] + h * a.dk_strides[1] + krow * a.dk_strides[2];
-    const int64_t lo_row = ((int64_t(b) * a.H + h) * a.T + krow) * a.D + D0;
-    uint16_t* gv_lo = a.dv_lo == nullptr ? nullptr : static_cast<uint16_t*>(a.dv_lo) + lo_row;
-    uint16_t* gk_lo = a.dk_lo == nullptr ? nullptr : static_cast<uint16_t*>(a.dk_lo) + lo_row;
+    const int64_t row = (int64_t(b) * a.H + h) * a.T + krow;
+    auto lo_at = [&](void* base) {  // this launch's first column of the residual row
+      void* r = lo_row(base, row, a.D, S3);
+      return r == nullptr ? nullptr : static_cast<void*>(static_cast<uint8_t*>(r) + D0 * (S3 ? 4 : 2));
+    };
+    void* gv_lo = lo_at(a.dv_lo);
+    void* gk_lo = lo_at(a.dk_lo);
     // (a.D < D only for the head dims 16 and 32 on the D = 64 launch, DH == D)
-    store_rows_T<E, DH>(gv + D0, acc_v, 1.f, hf, gv_lo, DH == D ? a.D : DH);
+    store_rows_T<E, DH>(gv + D0, acc_v, 1.f, hf, gv_lo, DH == D ? a.D : DH, S3);
     if constexpr (DH == D) {  // all columns here: dK can be rotated back (dqk_signs)
       if (a.dqk_signs != nullptr) store_rows_T_unrot<E, D>(gk, acc_k, a.sm_scale, hf, a.dqk_signs);
-      else store_rows_T<E, D>(gk, acc_k, a.sm_scale, hf, gk_lo, a.D);
+      else store_rows_T<E, D>(gk, acc_k, a.sm_scale, hf, gk_lo, a.D, S3);
     } else {
-      store_rows_T<E, DH>(gk + D0, acc_k, a.sm_scale, hf, gk_lo);  // (no dqk_signs at split widths)
+      store_rows_T<E, DH>(gk + D0, acc_k, a.sm_scale, hf, gk_lo, DH, S3);  // (no dqk_signs at split widths)
     }
   }
 }
@@ -1140,7 +1202,7 @@ static void launch_delta_t(const AttnArgs& a, hipStream_t st) {
   const int64_t rows = int64_t(a.B) * a.H * a.T;
   hipLaunchKernelGGL((k_delta<E, D>), dim3(unsigned((rows + RPB - 1) / RPB)), dim3(256), 0, st, a);
 }
-template <class E, int D, bool Q8, bool SP>
+template <class E, int D, bool Q8, int NSP>
 static void launch_dq_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_delta) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dq_blocks;
@@ -1149,26 +1211,31 @@ static void launch_dq_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st, 
   auto* cnt = reinterpret_cast<const int32_t*>(plan + L.dq_count);
   auto* order = reinterpret_cast<const uint32_t*>(plan + L.dq_order);
   if constexpr (D == 256) {  // two launches, the column halves of dQ; the first forms Delta
-    hipLaunchKernelGGL((k_dq<E, D, Q8, SP, 128, 0>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, order, L.nT,
+    hipLaunchKernelGGL((k_dq<E, D, Q8, NSP, 128, 0>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, order, L.nT,
                        L.n_dq_blocks, fuse_delta);
-    hipLaunchKernelGGL((k_dq<E, D, Q8, SP, 128, 128>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, order, L.nT,
+    hipLaunchKernelGGL((k_dq<E, D, Q8, NSP, 128, 128>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, order, L.nT,
                        L.n_dq_blocks, false);
   } else {
-    hipLaunchKernelGGL((k_dq<E, D, Q8, SP>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, order, L.nT,
+    hipLaunchKernelGGL((k_dq<E, D, Q8, NSP>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, order, L.nT,
                        L.n_dq_blocks, fuse_delta);
   }
 }
 template <class E, int D, bool Q8 = false>
 static void launch_dq_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_delta) {
-  if (a.precision == KD_PREC_SINGLE) launch_dq_s<E, D, Q8, false>(a, plan, st, fuse_delta);
-  else launch_dq_s<E, D, Q8, true>(a, plan, st, fuse_delta);
+  switch (parts_of(a.precision)) {
+    case 1: launch_dq_s<E, D, Q8, 1>(a, plan, st, fuse_delta); break;
+    case 2: launch_dq_s<E, D, Q8, 2>(a, plan, st, fuse_delta); break;
+    default:
+      if constexpr (!Q8) launch_dq_s<E, D, Q8, 3>(a, plan, st, fuse_delta);  // (refused with fp8 by the C ABI)
+      break;
+  }
 }
-template <class E, int D, bool Q8, bool SP>
+template <class E, int D, bool Q8, int NSP>
 static void launch_dkdv_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dkdv_blocks;
   if constexpr (D == 64) {  // one launch, all four products per wave
-    hipLaunchKernelGGL((k_dkdv_wide<E, D, SP, 64, 0>), dim3(grid), dim3(256), 0, st, a,
+    hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 64, 0>), dim3(grid), dim3(256), 0, st, a,
                        reinterpret_cast<const uint32_t*>(plan + L.codes),
                        reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
                        reinterpret_cast<const int32_t*>(plan + L.dkdv_count), L.nT, L.n_dkdv_blocks);
@@ -1176,12 +1243,12 @@ static void launch_dkdv_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st
     auto* codes = reinterpret_cast<const uint32_t*>(plan + L.codes);
     auto* list = reinterpret_cast<const uint32_t*>(plan + L.dkdv_list);
     auto* cnt = reinterpret_cast<const int32_t*>(plan + L.dkdv_count);
-    hipLaunchKernelGGL((k_dkdv_wide<E, D, SP, 128, 0>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, L.nT,
+    hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 128, 0>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, L.nT,
                        L.n_dkdv_blocks);
-    hipLaunchKernelGGL((k_dkdv_wide<E, D, SP, 128, 128>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, L.nT,
+    hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 128, 128>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, L.nT,
                        L.n_dkdv_blocks);
   } else {
-    hipLaunchKernelGGL((k_dkdv<E, D, Q8, SP>), dim3(grid), dim3(512), 0, st, a,
+    hipLaunchKernelGGL((k_dkdv<E, D, Q8, NSP>), dim3(grid), dim3(512), 0, st, a,
                        reinterpret_cast<const uint32_t*>(plan + L.codes),
                        reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
                        reinterpret_cast<const int32_t*>(plan + L.dkdv_count), L.nT, L.n_dkdv_blocks);
@@ -1190,8 +1257,13 @@ static void launch_dkdv_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st
 
 template <class E, int D, bool Q8 = false>
 static void launch_dkdv_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
-  if (a.precision == KD_PREC_SINGLE) launch_dkdv_s<E, D, Q8, false>(a, plan, st);
-  else launch_dkdv_s<E, D, Q8, true>(a, plan, st);
+  switch (parts_of(a.precision)) {
+    case 1: launch_dkdv_s<E, D, Q8, 1>(a, plan, st); break;
+    case 2: launch_dkdv_s<E, D, Q8, 2>(a, plan, st); break;
+    default:
+      if constexpr (!Q8) launch_dkdv_s<E, D, Q8, 3>(a, plan, st);  // (refused with fp8 by the C ABI)
+      break;
+  }
 }
 
 // head dims 16 and 32 run on the D = 64 kernels (their rows read as zeros past a.D)

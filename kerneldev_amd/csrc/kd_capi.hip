@@ -66,8 +66,8 @@ int check_common(const kd_attn_args* a) {
     return fail(KD_ERR_UNSUPPORTED, "dqk_signs is built for bf16 / fp16 at head dim 64 or 128");
   if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale))
     return fail(KD_ERR_INVALID, "sm_scale must be finite and > 0");
-  if (a->precision != KD_PREC_SPLIT && a->precision != KD_PREC_SINGLE)
-    return fail(KD_ERR_INVALID, "precision must be KD_PREC_SPLIT or KD_PREC_SINGLE");
+  if (a->precision != KD_PREC_SPLIT && a->precision != KD_PREC_SINGLE && a->precision != KD_PREC_SPLIT3)
+    return fail(KD_ERR_INVALID, "precision must be KD_PREC_SPLIT, KD_PREC_SINGLE or KD_PREC_SPLIT3");
   return KD_OK;
 }
 
@@ -245,6 +245,8 @@ int kd_plan_build(const kd_meta_args* m, void* plan, int64_t plan_bytes, void* s
 static int check_fp8(const kd_attn_args* a) {
   if ((a->q8 == nullptr) != (a->k8 == nullptr)) return fail(KD_ERR_INVALID, "q8 and k8 go together");
   if (a->q8 == nullptr) return KD_OK;
+  if (a->precision == KD_PREC_SPLIT3)
+    return fail(KD_ERR_UNSUPPORTED, "KD_PREC_SPLIT3 is not built with fp8 scores");
   if (a->D != 128) return fail(KD_ERR_UNSUPPORTED, "the fp8 QK^T path is built for head dim 128");
   if (a->dtype != KD_BF16) return fail(KD_ERR_UNSUPPORTED, "the fp8 QK^T path is built for bf16");
   if (!aligned16(a->q8) || !aligned16(a->k8)) return fail(KD_ERR_INVALID, "q8 and k8 must be 16-byte aligned");

@@ -144,6 +144,14 @@ template <> KD_DEV float to_f32<F16>(uint16_t bits) {
 template <class E> KD_DEV uint32_t pack2_residual(float lo, float hi, uint32_t w) {
   return pack2<E>(lo - to_f32<E>(uint16_t(w & 0xFFFFu)), hi - to_f32<E>(uint16_t(w >> 16)));
 }
+// The third part of a three-way split: with w = pack2<E>(lo, hi) and r =
+// pack2_residual<E>(lo, hi, w), the 16-bit rounding of what w + r leave
+// over (both subtractions are exact in fp32), so that w + r + the result
+// carry lo and hi to about three times the type's significant bits.
+template <class E> KD_DEV uint32_t pack2_residual2(float lo, float hi, uint32_t w, uint32_t r) {
+  return pack2<E>(lo - to_f32<E>(uint16_t(w & 0xFFFFu)) - to_f32<E>(uint16_t(r & 0xFFFFu)),
+                  hi - to_f32<E>(uint16_t(w >> 16)) - to_f32<E>(uint16_t(r >> 16)));
+}
 // Eight fp32 values as a 16-bit MFMA operand (u32x4), and their residual
 template <class E> KD_DEV u32x4 pack8(const float* p) {
   return u32x4{pack2<E>(p[0], p[1]), pack2<E>(p[2], p[3]), pack2<E>(p[4], p[5]), pack2<E>(p[6], p[7])};
@@ -151,6 +159,10 @@ template <class E> KD_DEV u32x4 pack8(const float* p) {
 template <class E> KD_DEV u32x4 pack8_residual(const float* p, const u32x4& w) {
   return u32x4{pack2_residual<E>(p[0], p[1], w[0]), pack2_residual<E>(p[2], p[3], w[1]),
                pack2_residual<E>(p[4], p[5], w[2]), pack2_residual<E>(p[6], p[7], w[3])};
+}
+template <class E> KD_DEV u32x4 pack8_residual2(const float* p, const u32x4& w, const u32x4& r) {
+  return u32x4{pack2_residual2<E>(p[0], p[1], w[0], r[0]), pack2_residual2<E>(p[2], p[3], w[1], r[1]),
+               pack2_residual2<E>(p[4], p[5], w[2], r[2]), pack2_residual2<E>(p[6], p[7], w[3], r[3])};
 }
 
 // Row permutation used for the A operand of 32x32 MFMAs whose output feeds the

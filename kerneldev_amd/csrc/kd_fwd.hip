@@ -49,11 +49,13 @@ template <> constexpr float rescale_log2<F16>() { return 15.f; }
 // of the score product and the V^T blocks of P V
 constexpr int FWD_PF = 4;
 
-template <class E, int D, bool Q8, bool SP>
+// NSP: the parts P enters P V in (1, 2 or 3: parts_of the precision)
+template <class E, int D, bool Q8, int NSP>
 __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_fwd(AttnArgs a, const uint32_t* __restrict__ codes,
                                                              const uint32_t* __restrict__ list,
                                                              const int32_t* __restrict__ count,
                                                              const uint32_t* __restrict__ order, int nT, int nQB) {
+  constexpr bool SP = NSP >= 2, S3 = NSP == 3;
   constexpr int NW = 4;             // waves per 128-row q-block; each owns 32 rows
   using TL = Tile<D, NW>;           // V tiles (and K tiles on the 16-bit path)
   using SO = ScoreOp<E, D, Q8>;     // S^T = K Q^T, 16-bit or fp8
@@ -243,9 +245,11 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_fwd(AttnArgs a, const
     // softmax of tile e (VALU) alongside S of tile e+1 (MFMA; computed from
     // the other K buffer even past the last tile, where it is simply unused)
     // P packed for the MFMA (pk) and, with SP, its rounding residual (pl):
-    // P V is then formed as pk V + pl V, P carried to ~16 significant bits
+    // P V is then formed as pk V + pl V, P carried to ~16 significant bits;
+    // with S3 a third part pm carries it to ~24
     u32x4 pk[2][2];
     u32x4 pl[2][2];
+    u32x4 pm[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       float p[16];
@@ -264,6 +268,13 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_fwd(AttnArgs a, const
           l1 = acc_pair<E>(pl[kb][t][1], l1);
           l0 = acc_pair<E>(pl[kb][t][2], l0);
           l1 = acc_pair<E>(pl[kb][t][3], l1);
+        }
+        if constexpr (S3) {
+          pm[kb][t] = pack8_residual2<E>(p + 8 * t, pk[kb][t], pl[kb][t]);
+          l0 = acc_pair<E>(pm[kb][t][0], l0);
+          l1 = acc_pair<E>(pm[kb][t][1], l1);
+          l0 = acc_pair<E>(pm[kb][t][2], l0);
+          l1 = acc_pair<E>(pm[kb][t][3], l1);
         }
       }
     }
@@ -288,6 +299,7 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_fwd(AttnArgs a, const
         __builtin_amdgcn_sched_barrier(0x406);
         o[db] = mfma32x32x16<E>(vv[i % PFV], pk[t4 >> 1][t4 & 1], o[db]);
         if constexpr (SP) o[db] = mfma32x32x16<E>(vv[i % PFV], pl[t4 >> 1][t4 & 1], o[db]);
+        if constexpr (S3) o[db] = mfma32x32x16<E>(vv[i % PFV], pm[t4 >> 1][t4 & 1], o[db]);
         if (i + PFV < NV) vv[i % PFV] = read_v(i + PFV);
       }
       __builtin_amdgcn_sched_barrier(0x406);
@@ -309,9 +321,12 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_fwd(AttnArgs a, const
       const int row = qrow;
       uint16_t* og = static_cast<uint16_t*>(a.o) + b * a.o_strides[0] + h * a.o_strides[1] + row * a.o_strides[2];
       // optional rounding residual O - bf16(O), so the backward's Delta can be
-      // formed from O to ~16 significant bits (contiguous [B, H, T, a.D])
-      uint16_t* lg = a.o_lo == nullptr ? nullptr
-                                       : static_cast<uint16_t*>(a.o_lo) + (int64_t(bh) * T + row) * a.D;
+      // formed from O to ~16 significant bits (contiguous [B, H, T, a.D]); in
+      // fp32 with S3, so that O + O_lo is the fp32 O
+      uint16_t* lg = a.o_lo == nullptr || S3 ? nullptr
+                                             : static_cast<uint16_t*>(a.o_lo) + (int64_t(bh) * T + row) * a.D;
+      float* lg32 = a.o_lo == nullptr || !S3 ? nullptr
+                                             : static_cast<float*>(a.o_lo) + (int64_t(bh) * T + row) * a.D;
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
 #pragma unroll
@@ -327,6 +342,10 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_fwd(AttnArgs a, const
             const u32x2 r = {pack2_residual<E>(f[0], f[1], w[0]), pack2_residual<E>(f[2], f[3], w[1])};
             *reinterpret_cast<u32x2*>(lg + d0) = r;
           }
+          if (lg32 != nullptr)
+            *reinterpret_cast<f32x4*>(lg32 + d0) =
+                f32x4{f[0] - to_f32<E>(uint16_t(w[0] & 0xFFFFu)), f[1] - to_f32<E>(uint16_t(w[0] >> 16)),
+                      f[2] - to_f32<E>(uint16_t(w[1] & 0xFFFFu)), f[3] - to_f32<E>(uint16_t(w[1] >> 16))};
         }
       }
       if (a.lse != nullptr && hf == 0)
@@ -335,12 +354,12 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_fwd(AttnArgs a, const
   }
 }
 
-template <class E, int D, bool Q8, bool SP>
+template <class E, int D, bool Q8, int NSP>
 static void launch_fwd_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const int nQB = L.n_fwd_blocks;
   const unsigned grid = unsigned(a.B) * a.H * nQB;
-  hipLaunchKernelGGL((k_fwd<E, D, Q8, SP>), dim3(grid), dim3(256), 0, st, a,
+  hipLaunchKernelGGL((k_fwd<E, D, Q8, NSP>), dim3(grid), dim3(256), 0, st, a,
                      reinterpret_cast<const uint32_t*>(plan + L.codes),
                      reinterpret_cast<const uint32_t*>(plan + L.fwd_list),
                      reinterpret_cast<const int32_t*>(plan + L.fwd_count),
@@ -349,8 +368,13 @@ static void launch_fwd_t(const AttnArgs& a, const uint8_t* plan, hipStream_t st)
 
 template <class E, int D, bool Q8 = false>
 static void launch_fwd_p(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
-  if (a.precision == KD_PREC_SINGLE) launch_fwd_t<E, D, Q8, false>(a, plan, st);
-  else launch_fwd_t<E, D, Q8, true>(a, plan, st);
+  switch (parts_of(a.precision)) {
+    case 1: launch_fwd_t<E, D, Q8, 1>(a, plan, st); break;
+    case 2: launch_fwd_t<E, D, Q8, 2>(a, plan, st); break;
+    default:
+      if constexpr (!Q8) launch_fwd_t<E, D, Q8, 3>(a, plan, st);  // (the C ABI refuses it with fp8 scores)
+      break;
+  }
 }
 
 int launch_fwd(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {

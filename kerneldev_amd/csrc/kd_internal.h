@@ -12,6 +12,12 @@ typedef kd_attn_args AttnArgs;
 
 enum : uint8_t { TILE_EMPTY = 0, TILE_PARTIAL = 1, TILE_FULL = 2 };
 
+// The parts P and dS enter their products in (kd_attn_args.precision):
+// KD_PREC_SINGLE 1, KD_PREC_SPLIT 2 (hi + lo), KD_PREC_SPLIT3 3 (hi + mid + lo)
+inline int parts_of(int precision) {
+  return precision == KD_PREC_SINGLE ? 1 : precision == KD_PREC_SPLIT3 ? 3 : 2;
+}
+
 // Block shapes of the attention kernels (rows per workgroup).  The plan's
 // work lists group the 64x64 class map by these.
 inline int fwd_rows_per_block(int /*D*/) { return 128; }

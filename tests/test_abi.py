@@ -73,7 +73,12 @@ def test_bad_arguments_return_status_without_gpu():
     a.sm_scale = float("nan")
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID
     a.sm_scale = 0.125
+    a.precision = 3  # KD_PREC_SPLIT (0), KD_PREC_SINGLE (1), KD_PREC_SPLIT3 (2) only
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID
+    assert "precision" in lib.kd_last_error_string().decode()
+    a.precision = _lib.KD_PREC_SPLIT3
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID  # q is NULL
+    a.precision = _lib.KD_PREC_SPLIT
     a.q = a.k = a.v = a.o = 32
     a.q_strides[:] = [1024, 1024, 8]  # t stride < head dim: rows overlap
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID
@@ -86,6 +91,10 @@ def test_bad_arguments_return_status_without_gpu():
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_UNSUPPORTED
     a.D = 128
     a.q_strides[:] = [1024, 1024, 128]
+    a.precision = _lib.KD_PREC_SPLIT3  # the three-part split is not built with fp8 scores
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_UNSUPPORTED
+    assert "SPLIT3" in lib.kd_last_error_string().decode()
+    a.precision = _lib.KD_PREC_SPLIT
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID  # no scales
     assert "scale" in lib.kd_last_error_string().decode()
     b = _lib.AttnArgs()  # the backward's rounding-residual outputs: 16-bit MFMA paths only, aligned
@@ -156,6 +165,9 @@ def test_python_boundary_validation():
         flash_attention(q, q, q, lens=torch.zeros(1, dtype=torch.int64))
     with pytest.raises(ValueError, match="qk_dtype"):
         flash_attention(q, q, q, qk_dtype="int8")
+    with pytest.raises(ValueError, match="fp8"):
+        z = torch.zeros(1, 2, 16, 128)
+        flash_attention(z, z, z, qk_dtype="fp8_e4m3", precision="ieee")
     assert 32 in REFERENCE_HEAD_DIMS and 256 in REFERENCE_HEAD_DIMS
 
 

@@ -460,6 +460,60 @@ def test_split_precision_is_what_config4_needs(dev):
         assert worst["tf32"][k] < worst["bf16"][k], k
 
 
+def test_ieee_carries_p_and_ds_to_fp32(dev):
+    """precision="ieee" (KD_PREC_SPLIT3) against "tf32" (KD_PREC_SPLIT) on config
+    4's head (1, 17), through the C ABI with the residual outputs: o + o_lo,
+    dq + dq_lo, dk + dk_lo and dv + dv_lo are the kernels' fp32 results (fp32
+    residuals under SPLIT3, 16-bit ones under SPLIT), compared with the fp64
+    oracle by rel-RMS.  The triple carries P and dS to ~24 bits and keeps O's
+    residual in fp32 for Delta; the pair carries them to ~16 bits.  What is
+    left under "ieee" is fp32 arithmetic itself, the floor of the reference's
+    fp32 dots too: S = Q K^T accumulated in fp32 from -LSE / c, whose partial
+    sums near |S c| ~ 30 round at 2^-24, gives P a relative error of a few
+    1e-6.  Measured on this head: dQ 2.6e-5 -> 6.2e-6, dK 1.4e-5 -> 1.1e-5,
+    dV and O at that floor (1.7e-5, ~2e-6) in both."""
+    import ctypes
+
+    from kerneldev_amd import _lib
+    from kerneldev_amd.attention import _attn_args, _fwd_op, _strides3
+
+    inp = config_inputs(4, seed=0)
+    b, h = 1, 17
+    ref = _reference(inp, [(b, h)])
+    q, k, v, do = (inp[n][b:b + 1, h:h + 1].to(dev) for n in ("q", "k", "v", "do"))
+    meta = [inp[n][b:b + 1].to(dev) for n in ("in_span", "span_id", "is_prefix")]
+    sc = q.shape[-1] ** -0.5
+    lib = _lib.load()
+    rel = {}
+    for name, prec in (("tf32", _lib.KD_PREC_SPLIT), ("ieee", _lib.KD_PREC_SPLIT3)):
+        print(f"config 4 head ({b}, {h}) {name} with residual outputs", flush=True)
+        lo_dt = torch.float32 if prec == _lib.KD_PREC_SPLIT3 else q.dtype
+        o, lse, plan, o_lo, *_ = _fwd_op(q, k, v, None, *meta, sc, _lib.KD_MODE_FORMULA, True, prec=prec)
+        assert o_lo.dtype == lo_dt
+        grads = [torch.empty_like(q) for _ in range(3)]
+        los = [torch.empty(q.shape, dtype=lo_dt, device=dev) for _ in range(3)]
+        delta = torch.empty((2, 1, 1, q.shape[2]), dtype=torch.float32, device=dev)
+        a = _attn_args(q, k, v, sc, prec)
+        a.o, a.o_strides, a.lse, a.o_lo = o.data_ptr(), _strides3(o), lse.data_ptr(), o_lo.data_ptr()
+        a.dout, a.do_strides = do.data_ptr(), _strides3(do)
+        a.dq, a.dk, a.dv = (g.data_ptr() for g in grads)
+        a.dq_strides, a.dk_strides, a.dv_strides = (_strides3(g) for g in grads)
+        a.dq_lo, a.dk_lo, a.dv_lo = (x.data_ptr() for x in los)
+        a.delta = delta.data_ptr()
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(lib.kd_attn_bwd(ctypes.byref(a), *_lib.plan_ref(plan), st), "kd_attn_bwd")
+        torch.cuda.synchronize()
+        full = {"o": o.double() + o_lo.double()}
+        for key, g, lo in zip(("dq", "dk", "dv"), grads, los):
+            full[key] = g.double() + lo.double()
+        rel[name] = {key: _rel_rms(full[key].cpu(), ref[key]) for key in full}
+        print("  rel-RMS of the fp32 results: " + " ".join(f"{k_} {v_:.2e}" for k_, v_ in rel[name].items()))
+    for key in ("o", "dq", "dk", "dv"):
+        assert rel["ieee"][key] <= 3e-5, key
+        assert rel["ieee"][key] <= rel["tf32"][key] * 1.05, key
+    assert rel["ieee"]["dq"] <= rel["tf32"]["dq"] / 3
+
+
 @pytest.mark.parametrize("hadamard", [False, True])
 def test_fp8_cocktail_small(dev, hadamard):
     """fp8 e4m3 Q K^T against the oracle fed the same e4m3 operands.
