@@ -187,7 +187,7 @@ class Step:
         import torch
 
         from kerneldev_amd import _lib, generate_hadamard_signs
-        from kerneldev_amd.attention import PRECISIONS, _attn_args, _dtype_code, _strides3, mask_mode
+        from kerneldev_amd.attention import PRECISIONS, _attn_args, _dtype_code, _lo_dtype, _strides3, mask_mode
 
         self.torch, self.lib, self.dev = torch, _lib.load(), dev
         self._check = _lib.check
@@ -211,7 +211,8 @@ class Step:
         self.o = torch.empty_like(q)
         self.lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
         self.delta = torch.empty((2, B, H, T), dtype=torch.float32, device=dev)
-        self.o_lo = torch.empty_like(q)  # O's rounding residual, kept for Delta (training step)
+        # O's rounding residual, kept for Delta (training step); fp32 at "ieee"
+        self.o_lo = torch.empty(q.shape, dtype=_lo_dtype(q.dtype, PRECISIONS[precision]), device=dev)
         self.dq, self.dk, self.dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
         self.inputs = (q, k, v, do)
         a = _attn_args(q, k, v, D ** -0.5, PRECISIONS[precision])

@@ -23,7 +23,9 @@ namespace kd {
 // (S_j & sid_j > 0).  That minimum is always the start of a run of equal
 // eligible ids, so one pass lists each row's run starts (and their ids) in
 // ascending order, and each eligible token takes the first listed run with
-// its id: O(T * runs) instead of O(T^2), exact for any int64 span ids.
+// its id.  When the ids increase strictly from run to run (checked per row)
+// that is the token's own run; otherwise a linear search of the list finds
+// it: O(T * runs) at worst instead of O(T^2), exact for any int64 span ids.
 
 KD_DEV int64_t load_sid(const MetaArgs& m, int b, int t) {
   if (m.span_id == nullptr) return 0;
@@ -39,44 +41,9 @@ KD_DEV bool eligible(const MetaArgs& m, int b, int t, int64_t* sid) {
   return m.span_id != nullptr && load_flag(m.in_span, m.in_span_strides, b, t) && *sid > 0;
 }
 
-// One 1024-thread workgroup per batch row; thread i takes a contiguous
-// segment, counts its run starts, and a block scan gives each segment its
-// first output slot, so the list comes out in ascending order.
-__global__ __launch_bounds__(1024) void k_runs(MetaArgs m, uint32_t* runs, int64_t* run_sid, int32_t* run_count) {
-  __shared__ int s_warp[16];
-  const int b = blockIdx.x, tid = threadIdx.x, T = m.T;
-  const int seg = (T + 1023) / 1024, t0 = min(T, tid * seg), t1 = min(T, t0 + seg);
-  uint32_t* out = runs + int64_t(b) * T;
-  int64_t* out_sid = run_sid + int64_t(b) * T;
-  // a run starts at an eligible token whose predecessor is not eligible with the same id
-  auto scan = [&](auto&& emit) {
-    int64_t prev = 0;
-    bool prev_el = t0 > 0 && t0 < T && eligible(m, b, t0 - 1, &prev);
-    for (int t = t0; t < t1; ++t) {
-      int64_t sid;
-      const bool el = eligible(m, b, t, &sid);
-      if (el && !(prev_el && prev == sid)) emit(t, sid);
-      prev_el = el;
-      prev = sid;
-    }
-  };
-  int cnt = 0;
-  scan([&](int, int64_t) { ++cnt; });
-  const int incl = block_scan(cnt, s_warp);
-  int pos = incl - cnt;
-  scan([&](int t, int64_t sid) {
-    out[pos] = uint32_t(t);
-    out_sid[pos] = sid;
-    ++pos;
-  });
-  if (tid == int(blockDim.x) - 1) run_count[b] = incl;
-}
-
 // The representative of eligible token t of row b: the first listed run
 // with its id (always found: t's own run is listed).
-KD_DEV uint32_t run_rep(const MetaArgs& m, const uint32_t* runs, const int64_t* run_sid, const int32_t* run_count,
-                        int b, int64_t sid) {
-  const int n = run_count[b];
+KD_DEV uint32_t run_rep(const MetaArgs& m, const uint32_t* runs, const int64_t* run_sid, int n, int b, int64_t sid) {
   const int64_t* rs = run_sid + int64_t(b) * m.T;
   int i = 0;
   while (i < n - 1 && rs[i] != sid) ++i;
@@ -151,77 +118,280 @@ __global__ __launch_bounds__(256) void k_token_meta(kd_token_args a, uint8_t* in
   }
 }
 
-// ---- token codes -------------------------------------------------------
-// runs / run_sid / run_count: the run-start lists of k_runs (formula mode
-// with span ids); rep receives each eligible token's representative.
-__global__ void k_codes(MetaArgs m, const uint32_t* runs, const int64_t* run_sid, const int32_t* run_count,
-                        uint32_t* rep, uint32_t* codes) {
-  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (idx >= int64_t(m.B) * m.T) return;
-  const int b = int(idx / m.T), t = int(idx % m.T);
-  int seq_len = m.T;
-  if (m.lens != nullptr) seq_len = min(m.lens[int64_t(b) * m.lens_stride], m.T);
-  uint32_t code = 0;
-  if (t < seq_len) {
-    if (m.mode == KD_MODE_CAUSAL) {
-      code = FLAG_C;  // every token context: C & C & i >= j  (:512-513)
-    } else if (m.mode == KD_MODE_ALL) {
-      code = FLAG_P | (FLAG_P << 4);  // P sees P: every pair (:514-515)
-    } else {
-      const bool P = load_flag(m.is_prefix, m.is_prefix_strides, b, t);
-      const bool S = load_flag(m.in_span, m.in_span_strides, b, t);
-      const int64_t sid = load_sid(m, b, t);
-      const bool M = m.span_id != nullptr && sid == -1;
-      const bool C = !S && !P && !M;
-      uint32_t acc = 0;
-      if (P || C) acc |= FLAG_P;          // prefix_to_prefix, context_to_prefix
-      if (S) acc |= FLAG_C;               // span_to_context
-      if (M) acc |= FLAG_S | FLAG_P;      // maskq_to_spans, maskq_to_cls
-      code = (P ? FLAG_P : 0u) | (S ? FLAG_S : 0u) | (M ? FLAG_M : 0u) | (C ? FLAG_C : 0u) | (acc << 4);
-      if (m.span_id != nullptr && S && sid > 0) {  // same_span: eligible, so k_runs listed its run
-        const uint32_t r = run_rep(m, runs, run_sid, run_count, b, sid);
-        rep[idx] = r;
-        code |= (r + 1u) << 8;
-      }
-    }
-  }
-  codes[idx] = code;
+// ---- token codes (first of the plan's three launches) --------------------
+// The code of a token (layout in kd_common.h) from its prefix / span / [MASKQ]
+// flags, with representative r when has_rep (an eligible token in formula
+// mode with span ids).
+KD_DEV uint32_t token_code(int mode, bool P, bool S, bool M, bool has_rep, uint32_t r) {
+  if (mode == KD_MODE_CAUSAL) return FLAG_C;               // every token context: C & C & i >= j  (:512-513)
+  if (mode == KD_MODE_ALL) return FLAG_P | (FLAG_P << 4);  // P sees P: every pair (:514-515)
+  const bool C = !S && !P && !M;
+  uint32_t acc = 0;
+  if (P || C) acc |= FLAG_P;      // prefix_to_prefix, context_to_prefix
+  if (S) acc |= FLAG_C;           // span_to_context
+  if (M) acc |= FLAG_S | FLAG_P;  // maskq_to_spans, maskq_to_cls
+  uint32_t code = (P ? FLAG_P : 0u) | (S ? FLAG_S : 0u) | (M ? FLAG_M : 0u) | (C ? FLAG_C : 0u) | (acc << 4);
+  if (has_rep) code |= (r + 1u) << 8;  // same_span
+  return code;
 }
 
-// ---- 64x64 tile classifier ---------------------------------------------
-// One wave per tile.  The row mask of query lane i over the tile's 64 keys is
-// built from wave-wide ballots instead of 64 per-key tests: with F_j the key
-// flags and A_i the query's allowed flags, A_i & F_j != 0 selects the ballot
-// of keys carrying each flag of A_i; context queries add context keys at
-// j <= i (all of them below the diagonal, none above); and for the same-span
-// term the wave walks the distinct span representatives among the tile's keys
-// (usually one to three), one ballot each: query_row_mask, the function the
-// forward and dQ kernels use for PARTIAL tiles.  That is the rule of allow(),
-// term for term.
-__global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, int nT, uint8_t* cls,
-                                                 int32_t* nnz) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int qt = blockIdx.y, b = blockIdx.z;
-  const int kt0 = blockIdx.x * 4;
-  __shared__ uint32_t s_k[256];
+constexpr int CODE_SEG = 8;  // most tokens per thread and round (span ids)
+
+// Grid (chunks, B) of 1024 threads.  Without span ids each workgroup codes a
+// chunk of row b.  With span ids (formula mode) one workgroup takes the row
+// whole, in rounds of 1024 seg tokens (seg = T / 1024 rounded up, at most
+// CODE_SEG): thread i loads the metadata of its seg consecutive tokens (and
+// of the token before) at once, marks the
+// run starts (eligible tokens whose predecessor is not eligible with the same
+// id), and a block scan gives its first slot in the row's ascending list of
+// run starts (runs, run_sid).  It then codes its tokens, taking as each
+// eligible token's representative its own run's start -- the start of the run
+// before its first slot for a run that began earlier.  That is the first run
+// with the token's id whenever the ids increase strictly from run to run
+// (each id has one run), the layout of the token-derived metadata and of the
+// collate builders; the workgroup checks that over the finished list and
+// otherwise recodes the eligible tokens with the first listed run with their
+// id (run_rep).  The workgroups also zero the forward list lengths, which the
+// tile classifier accumulates.
+__global__ __launch_bounds__(1024) void k_codes_rows(MetaArgs m, uint32_t* runs, int64_t* run_sid, int32_t* run_count,
+                                                     uint32_t* rep, uint32_t* codes, int32_t* fwd_n, int n_fwd) {
+  __shared__ int s_warp[16];
+  __shared__ int s_n, s_dup;
+  const int b = blockIdx.y, tid = threadIdx.x, T = m.T;
+  const bool spans = m.mode == KD_MODE_FORMULA && m.span_id != nullptr && m.in_span != nullptr;
   {
-    const int j = kt0 * 64 + threadIdx.x;
-    s_k[threadIdx.x] = (j < T) ? codes[int64_t(b) * T + j] : 0u;
+    const int gid = (blockIdx.y * gridDim.x + blockIdx.x) * 1024 + tid, nth = gridDim.x * gridDim.y * 1024;
+    for (int i = gid; i < n_fwd; i += nth) fwd_n[i] = 0;
   }
+  int seq_len = T;
+  if (m.lens != nullptr) seq_len = min(m.lens[int64_t(b) * m.lens_stride], T);
+  if (!spans) {
+    const int per = (T + gridDim.x - 1) / gridDim.x;
+    const int c0 = blockIdx.x * per, c1 = min(T, c0 + per);
+    for (int t = c0 + tid; t < c1; t += 1024) {
+      uint32_t code = 0;
+      if (t < seq_len) {
+        const bool P = load_flag(m.is_prefix, m.is_prefix_strides, b, t);
+        const bool S = load_flag(m.in_span, m.in_span_strides, b, t);
+        const bool M = m.span_id != nullptr && load_sid(m, b, t) == -1;
+        code = token_code(m.mode, P, S, M, false, 0u);
+      }
+      codes[int64_t(b) * T + t] = code;
+    }
+    return;
+  }
+  // (gridDim.x == 1 in this mode)
+  if (tid == 0) s_dup = 0;
+  uint32_t* out = runs + int64_t(b) * T;
+  int64_t* out_sid = run_sid + int64_t(b) * T;
+  int n_before = 0;  // runs listed in earlier rounds
+  const int seg = min(CODE_SEG, (T + 1023) / 1024);
+  for (int base = 0; base < T; base += 1024 * seg) {
+    const int t0 = base + tid * seg;
+    int64_t prev = 0;
+    const bool prev_el = t0 > 0 && t0 < T && eligible(m, b, t0 - 1, &prev);
+    bool P[CODE_SEG], S[CODE_SEG], el[CODE_SEG], st[CODE_SEG];
+    int64_t sid[CODE_SEG];
+#pragma unroll
+    for (int k = 0; k < CODE_SEG; ++k) {
+      const int t = t0 + k;
+      const bool in = k < seg && t < T;
+      sid[k] = in ? load_sid(m, b, t) : 0;
+      S[k] = in && load_flag(m.in_span, m.in_span_strides, b, t);
+      P[k] = in && load_flag(m.is_prefix, m.is_prefix_strides, b, t);
+      el[k] = S[k] && sid[k] > 0;
+    }
+    int cnt = 0;
+    {
+      bool pe = prev_el;
+      int64_t ps = prev;
+#pragma unroll
+      for (int k = 0; k < CODE_SEG; ++k) {
+        st[k] = el[k] && !(pe && ps == sid[k]);
+        cnt += st[k];
+        pe = el[k];
+        ps = sid[k];
+      }
+    }
+    const int incl = block_scan(cnt, s_warp);
+    const int first = n_before + incl - cnt;
+    int pos = first;
+#pragma unroll
+    for (int k = 0; k < CODE_SEG; ++k)
+      if (st[k]) {
+        out[pos] = uint32_t(t0 + k);
+        out_sid[pos] = sid[k];
+        ++pos;
+      }
+    if (tid == 1023) s_n = n_before + incl;
+    __syncthreads();
+    // the run token t0 - 1 belongs to (if eligible): the last one listed before this thread's first slot
+    uint32_t start = (prev_el && first > 0) ? out[first - 1] : 0u;
+#pragma unroll
+    for (int k = 0; k < CODE_SEG; ++k) {
+      const int t = t0 + k;
+      if (k >= seg || t >= T) break;
+      if (st[k]) start = uint32_t(t);
+      const int64_t idx = int64_t(b) * T + t;
+      uint32_t code = 0;
+      if (t < seq_len) {
+        if (el[k]) rep[idx] = start;
+        code = token_code(m.mode, P[k], S[k], sid[k] == -1, el[k], start);
+      }
+      codes[idx] = code;
+    }
+    n_before = s_n;  // (s_n is next written after the next round's block scan barriers)
+  }
+  if (tid == 0) run_count[b] = n_before;
+  for (int i = tid; i + 1 < n_before; i += 1024)
+    if (out_sid[i] >= out_sid[i + 1]) s_dup = 1;
   __syncthreads();
-  const int kt = kt0 + wave;
-  if (kt >= nT) return;
+  if (s_dup == 0) return;  // workgroup-uniform
+  for (int t = tid; t < seq_len; t += 1024) {
+    int64_t sid;
+    if (!eligible(m, b, t, &sid)) continue;
+    const int64_t idx = int64_t(b) * T + t;
+    const uint32_t r = run_rep(m, runs, run_sid, n_before, b, sid);
+    rep[idx] = r;
+    codes[idx] = (codes[idx] & 0xFFu) | ((r + 1u) << 8);
+  }
+}
+
+// ---- 64x64 tile classifier (second launch) ------------------------------
+// Four waves per workgroup, on the two q-tiles of row block blockIdx.y and
+// 2 kpw consecutive k-tiles: wave w takes q-tile 2 rb + (w & 1) against the
+// kpw k-tiles of half (w >> 1), one after another (kpw > 1 on large plans,
+// where the grid fills the chip anyway and each wave's loads and barrier then
+// serve more tiles).  The row mask of query lane i
+// over a tile's 64 keys is built from wave-wide ballots instead of 64
+// per-key tests: with F_j the key flags and A_i the query's allowed flags,
+// A_i & F_j != 0 selects the ballot of keys carrying each flag of A_i;
+// context queries add context keys at j <= i (all of them below the diagonal,
+// none above); and for the same-span term the wave walks the distinct span
+// representatives among the tile's keys (usually one to three), one ballot
+// each: query_row_mask, the function the forward and dQ kernels use for
+// PARTIAL tiles.  That is the rule of allow(), term for term.  The workgroup
+// then adds its k-tiles with a non-empty tile in the row block to that row
+// block's forward list length (zeroed by the first launch).
+constexpr int TM_KPW = 4;  // most k-tiles per wave
+
+__global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, int nT, int kpw, uint8_t* cls,
+                                                 int32_t* nnz, int32_t* fwd_n) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int rb = blockIdx.y, b = blockIdx.z, nqb = int(gridDim.y);
+  const int qt = rb * 2 + (wave & 1), half = wave >> 1;
+  const int kt0 = blockIdx.x * 2 * kpw;
+  __shared__ uint32_t s_k[2 * TM_KPW * 64];
+  __shared__ uint32_t s_ne[2];  // bit i: k-tile kt0 + i has a non-empty tile, per q-tile
+  for (int x = threadIdx.x; x < 2 * kpw * 64; x += 256) {
+    const int j = kt0 * 64 + x;
+    s_k[x] = (j < T) ? codes[int64_t(b) * T + j] : 0u;
+  }
+  if (threadIdx.x < 2) s_ne[threadIdx.x] = 0u;
+  __syncthreads();
   const int i = qt * 64 + lane;
-  const uint32_t qc = (i < T) ? codes[int64_t(b) * T + i] : 0u;
-  const uint32_t kc = s_k[wave * 64 + lane];  // key j = 64 kt + lane (code 0 past T: allows nothing)
-  const uint64_t row = query_row_mask(qc, i, kc, kt * 64);
-  int cnt = __builtin_popcountll(row);
-  for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off);
-  const int64_t o = (int64_t(b) * nT + qt) * nT + kt;
-  const uint8_t k = cnt == 0 ? TILE_EMPTY : (cnt == 64 * 64 ? TILE_FULL : TILE_PARTIAL);
-  if (lane == 0) {
-    cls[o] = k;
-    if (nnz != nullptr) nnz[o] = cnt;
+  const uint32_t qc = (qt < nT && i < T) ? codes[int64_t(b) * T + i] : 0u;
+  uint32_t ne = 0;
+  if (qt < nT) {  // wave-uniform
+    for (int x = half * kpw; x < (half + 1) * kpw; ++x) {
+      const int kt = kt0 + x;
+      if (kt >= nT) break;
+      const uint32_t kc = s_k[x * 64 + lane];  // key j = 64 kt + lane (code 0 past T: allows nothing)
+      const uint64_t row = query_row_mask(qc, i, kc, kt * 64);
+      int cnt = __builtin_popcountll(row);
+      for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off);
+      const int64_t o = (int64_t(b) * nT + qt) * nT + kt;
+      if (lane == 0) {
+        cls[o] = cnt == 0 ? TILE_EMPTY : (cnt == 64 * 64 ? TILE_FULL : TILE_PARTIAL);
+        if (nnz != nullptr) nnz[o] = cnt;
+      }
+      if (cnt != 0) ne |= 1u << x;
+    }
+  }
+  if (lane == 0 && ne != 0u) atomicOr(&s_ne[wave & 1], ne);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int add = __builtin_popcount(s_ne[0] | s_ne[1]);
+    if (add != 0) atomicAdd(fwd_n + int64_t(b) * nqb + rb, add);
+  }
+}
+
+// ---- work lists and work order (third launch) -----------------------------
+// One workgroup per list: the B nqb row blocks of the forward / dQ lists (two
+// q-tiles against every k-tile; the two lists are the same), then the B nkb
+// key blocks of the dK/dV list (two k-tiles against every q-tile).  Wave 0
+// compacts the block's non-empty entries in ascending order with a ballot and
+// a prefix popcount, and zero-fills the tail.  The forward / dQ work order
+// ranks the B nqb items b nqb + block by descending list length, equal lengths
+// in ascending item order (item i goes to position #{j : c_j > c_i or
+// (c_j == c_i and j < i)}); the attention kernels take each head's blocks in
+// this order, so the longest start first and the short ones fill the end of
+// every XCD's range (longest-first list scheduling).  The forward list
+// lengths arrive complete from the classifier, so each row-block workgroup
+// ranks its own item and no workgroup waits for another.
+struct ListOut {
+  uint32_t *fwd, *dq, *dkdv;       // entries, [B nb nT]
+  int32_t *fwd_n, *dq_n, *dkdv_n;  // counts, [B nb]
+  uint32_t *fwd_order, *dq_order;  // [B nb]
+  int nqb, nkb;                    // row blocks (forward and dQ), key blocks (dK/dV)
+};
+
+// entry class bits of block rb (tiles 2 rb, 2 rb + 1) against tile c of the
+// other axis (by_key: the block's tiles are key tiles, a column of the map)
+KD_DEV uint32_t block_classes(const uint8_t* cls_b, int nT, int rb, int c, bool by_key) {
+  uint32_t classes = 0;
+  for (int r = 0; r < 2; ++r) {
+    const int t = rb * 2 + r;
+    if (t < nT) classes |= uint32_t(by_key ? cls_b[int64_t(c) * nT + t] : cls_b[int64_t(t) * nT + c]) << (2 * r);
+  }
+  return classes;
+}
+
+__global__ __launch_bounds__(256) void k_lists(const uint8_t* __restrict__ cls, int nT, ListOut lo) {
+  __shared__ int s_cnt[4];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int B = int(gridDim.y), b = blockIdx.y;
+  const bool rows = int(blockIdx.x) < lo.nqb;  // a row block of the forward / dQ lists, else a key block
+  const int blk = rows ? int(blockIdx.x) : int(blockIdx.x) - lo.nqb;
+  const int item = b * (rows ? lo.nqb : lo.nkb) + blk;
+  if (wave == 0) {
+    const uint8_t* cls_b = cls + int64_t(b) * nT * nT;
+    uint32_t* out = (rows ? lo.fwd : lo.dkdv) + int64_t(item) * nT;
+    uint32_t* out2 = rows ? lo.dq + int64_t(item) * nT : nullptr;
+    int n = 0;
+    for (int c0 = 0; c0 < nT; c0 += 64) {
+      const int c = c0 + lane;
+      const uint32_t classes = c < nT ? block_classes(cls_b, nT, blk, c, !rows) : 0u;
+      const bool any_ne = classes != 0u;
+      const uint64_t msk = __builtin_amdgcn_ballot_w64(any_ne);
+      const int pos = n + __builtin_popcountll(msk & ((uint64_t(1) << lane) - 1));
+      if (any_ne) {
+        out[pos] = (uint32_t(c) << 8) | classes;
+        if (rows) out2[pos] = (uint32_t(c) << 8) | classes;
+      }
+      n += __builtin_popcountll(msk);
+    }
+    for (int c = n + lane; c < nT; c += 64) {
+      out[c] = 0;
+      if (rows) out2[c] = 0;
+    }
+    if (lane == 0) (rows ? lo.dq_n : lo.dkdv_n)[item] = n;  // (fwd_n: the classifier's sums, the same n)
+  }
+  if (!rows) return;  // workgroup-uniform
+  // this item's rank: the items before it in the order
+  const int ci = lo.fwd_n[item], n_items = B * lo.nqb;
+  int before = 0;
+  for (int j = tid; j < n_items; j += 256) {
+    const int cj = lo.fwd_n[j];
+    before += (cj > ci || (cj == ci && j < item)) ? 1 : 0;
+  }
+  for (int off = 32; off > 0; off >>= 1) before += __shfl_xor(before, off);
+  if (lane == 0) s_cnt[wave] = before;
+  __syncthreads();
+  if (tid == 0) {
+    const int rank = s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
+    lo.fwd_order[rank] = uint32_t(item);
+    lo.dq_order[rank] = uint32_t(item);
   }
 }
 
@@ -240,78 +410,6 @@ __global__ __launch_bounds__(256) void k_tile_masks(const uint32_t* codes, int T
   const int64_t o = ((int64_t(b) * nT + qt) * nT + kt) * 64 + lane;
   rows[o] = query_row_mask(qc, i, kc, kt * 64);
   cols[o] = key_col_mask(kc, j, qc, qt * 64);
-}
-
-// ---- per-row-block work lists ------------------------------------------
-// One wave per row block: lanes test 64 columns at a time and compact the
-// non-empty ones in ascending order with a ballot + prefix popcount; the
-// tail of the list is zero-filled.  All three lists build in one launch
-// (blockIdx.y picks the list).
-struct ListSpec {
-  uint32_t* entries;
-  int32_t* counts;
-  int group, by_key, nrb;
-};
-struct ListSpecs {
-  ListSpec l[3];
-};
-
-__global__ __launch_bounds__(64) void k_lists(const uint8_t* __restrict__ cls, int B, int nT, ListSpecs specs) {
-  const ListSpec sp = specs.l[blockIdx.y];
-  const int idx = blockIdx.x;  // b * nrb + rb
-  if (idx >= B * sp.nrb) return;
-  const int b = idx / sp.nrb, rb = idx % sp.nrb, lane = threadIdx.x;
-  const uint8_t* base = cls + int64_t(b) * nT * nT;
-  uint32_t* out = sp.entries + int64_t(idx) * nT;
-  int n = 0;
-  for (int c0 = 0; c0 < nT; c0 += 64) {
-    const int c = c0 + lane;
-    bool any_ne = false;
-    uint32_t classes = 0;
-    if (c < nT) {
-      for (int r = 0; r < sp.group; ++r) {
-        const int row = rb * sp.group + r;
-        uint8_t k = TILE_EMPTY;
-        if (row < nT) k = sp.by_key ? base[int64_t(c) * nT + row] : base[int64_t(row) * nT + c];
-        any_ne |= (k != TILE_EMPTY);
-        classes |= uint32_t(k) << (2 * r);
-      }
-    }
-    const uint64_t m = __builtin_amdgcn_ballot_w64(any_ne);
-    const int pos = n + __builtin_popcountll(m & ((uint64_t(1) << lane) - 1));
-    if (any_ne) out[pos] = (uint32_t(c) << 8) | classes;
-    n += __builtin_popcountll(m);
-  }
-  for (int c = n + lane; c < nT; c += 64) out[c] = 0;
-  if (lane == 0) sp.counts[idx] = n;
-}
-
-// ---- work order ----------------------------------------------------------
-// Forward and dQ lists: the B n items (b, block) = b n + block sorted by descending list
-// length, equal lengths in ascending item order: item i goes to position
-// #{j : c_j > c_i or (c_j == c_i and j < i)}.  The attention kernels take
-// each head's blocks in this order, so the longest ones start first and the
-// short ones fill the end of every XCD's range (longest-first list
-// scheduling), instead of a fixed block order whose longest blocks may come
-// last.
-struct OrderSpecs {
-  const int32_t* counts[2];
-  uint32_t* order[2];
-  int n[2];
-};
-
-__global__ __launch_bounds__(256) void k_order(OrderSpecs specs) {
-  const int y = blockIdx.y, n = specs.n[y];
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const int32_t* c = specs.counts[y];
-  const int ci = c[i];
-  int rank = 0;
-  for (int j = 0; j < n; ++j) {
-    const int cj = c[j];
-    rank += (cj > ci || (cj == ci && j < i)) ? 1 : 0;
-  }
-  specs.order[y][rank] = uint32_t(i);
 }
 
 // ---- dense mask output (return_attention_mask) -------------------------
@@ -378,34 +476,33 @@ int launch_plan(const MetaArgs& m, uint8_t* plan, hipStream_t st) {
   uint32_t* rep = reinterpret_cast<uint32_t*>(plan + L.rep);
   uint8_t* cls = plan + L.cls;
   int32_t* nnz = reinterpret_cast<int32_t*>(plan + L.nnz);
-  const int64_t BT = int64_t(m.B) * m.T;
   uint32_t* runs = reinterpret_cast<uint32_t*>(plan + L.runs);
   int64_t* run_sid = reinterpret_cast<int64_t*>(plan + L.run_sid);
   int32_t* run_count = reinterpret_cast<int32_t*>(plan + L.run_count);
-  // (k_codes reads the run lists only for eligible tokens, which exist only in this mode)
-  if (m.mode == KD_MODE_FORMULA && m.span_id != nullptr && m.in_span != nullptr)
-    hipLaunchKernelGGL(k_runs, dim3(unsigned(m.B)), dim3(1024), 0, st, m, runs, run_sid, run_count);
-  hipLaunchKernelGGL(k_codes, dim3(unsigned((BT + 255) / 256)), dim3(256), 0, st, m, runs, run_sid, run_count, rep,
-                     codes);
-  hipLaunchKernelGGL(k_tilemap, dim3((L.nT + 3) / 4, L.nT, m.B), dim3(256), 0, st, codes, m.T, L.nT, cls, nnz);
-  ListSpecs specs;
-  specs.l[0] = {reinterpret_cast<uint32_t*>(plan + L.fwd_list), reinterpret_cast<int32_t*>(plan + L.fwd_count),
-                L.fwd_group, 0, L.n_fwd_blocks};
-  specs.l[1] = {reinterpret_cast<uint32_t*>(plan + L.dq_list), reinterpret_cast<int32_t*>(plan + L.dq_count),
-                L.dq_group, 0, L.n_dq_blocks};
-  specs.l[2] = {reinterpret_cast<uint32_t*>(plan + L.dkdv_list), reinterpret_cast<int32_t*>(plan + L.dkdv_count),
-                L.dkdv_group, 1, L.n_dkdv_blocks};
-  const int max_rb = std::max(L.n_fwd_blocks, std::max(L.n_dq_blocks, L.n_dkdv_blocks));
-  hipLaunchKernelGGL(k_lists, dim3(unsigned(m.B * max_rb), 3), dim3(64), 0, st, cls, m.B, L.nT, specs);
-  OrderSpecs os;
-  uint32_t* const ords[2] = {reinterpret_cast<uint32_t*>(plan + L.fwd_order), reinterpret_cast<uint32_t*>(plan + L.dq_order)};
-  for (int y = 0; y < 2; ++y) {
-    os.counts[y] = specs.l[y].counts;
-    os.order[y] = ords[y];
-    os.n[y] = m.B * specs.l[y].nrb;
-  }
-  hipLaunchKernelGGL(k_order, dim3(unsigned((m.B * std::max(L.n_fwd_blocks, L.n_dq_blocks) + 255) / 256), 2), dim3(256),
-                     0, st, os);
+  // k_tilemap and k_lists build lists of blocks of two 64-row tiles
+  if (L.fwd_group != 2 || L.dq_group != 2 || L.dkdv_group != 2) return KD_ERR_UNSUPPORTED;
+  // formula mode with span ids: one workgroup per row (it lists the row's
+  // runs before coding its tokens); otherwise chunks of 8 tokens a thread
+  const bool spans = m.mode == KD_MODE_FORMULA && m.span_id != nullptr && m.in_span != nullptr;
+  const unsigned chunks = spans ? 1u : unsigned(std::max(1, (m.T + 8191) / 8192));
+  ListOut lo;
+  lo.fwd = reinterpret_cast<uint32_t*>(plan + L.fwd_list);
+  lo.dq = reinterpret_cast<uint32_t*>(plan + L.dq_list);
+  lo.dkdv = reinterpret_cast<uint32_t*>(plan + L.dkdv_list);
+  lo.fwd_n = reinterpret_cast<int32_t*>(plan + L.fwd_count);
+  lo.dq_n = reinterpret_cast<int32_t*>(plan + L.dq_count);
+  lo.dkdv_n = reinterpret_cast<int32_t*>(plan + L.dkdv_count);
+  lo.fwd_order = reinterpret_cast<uint32_t*>(plan + L.fwd_order);
+  lo.dq_order = reinterpret_cast<uint32_t*>(plan + L.dq_order);
+  lo.nqb = L.n_fwd_blocks;  // (the forward and dQ lists share the grouping of two q-tiles)
+  lo.nkb = L.n_dkdv_blocks;
+  hipLaunchKernelGGL(k_codes_rows, dim3(chunks, unsigned(m.B)), dim3(1024), 0, st, m, runs, run_sid, run_count, rep,
+                     codes, lo.fwd_n, m.B * lo.nqb);
+  // k-tiles per wave: TM_KPW once the grid holds 2048 workgroups at that, else 1
+  const int kpw = int64_t(m.B) * lo.nqb * ((L.nT + 2 * TM_KPW - 1) / (2 * TM_KPW)) >= 2048 ? TM_KPW : 1;
+  hipLaunchKernelGGL(k_tilemap, dim3(unsigned((L.nT + 2 * kpw - 1) / (2 * kpw)), unsigned(lo.nqb), unsigned(m.B)),
+                     dim3(256), 0, st, codes, m.T, L.nT, kpw, cls, nnz, lo.fwd_n);
+  hipLaunchKernelGGL(k_lists, dim3(unsigned(lo.nqb + lo.nkb), unsigned(m.B)), dim3(256), 0, st, cls, L.nT, lo);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 

@@ -114,6 +114,34 @@ def test_plan_fuzzed_metadata(dev, seed):
     _check_plan(p, m)
 
 
+def test_plan_spans_across_rounds(dev):
+    """Rows longer than the codes kernel's 8192-token round, with a span running across the
+    boundary: row 0's ids increase from span to span (each token's own run is its group's
+    first), row 1 reuses a few ids in separate spans (the first run with the id is earlier)."""
+    T, B = 8192 + 333, 2
+    rng = np.random.default_rng(5)
+    in_span = np.zeros((B, T), bool)
+    span_id = np.zeros((B, T), np.int64)
+    is_prefix = np.zeros((B, T), bool)
+    is_prefix[:, :40] = True
+    for b in range(B):
+        t, sid = 40, 0
+        while t < T:
+            t += int(rng.integers(1, 30))
+            n = int(rng.integers(1, 120))
+            sid = sid + 1 if b == 0 else int(rng.integers(1, 6))
+            in_span[b, t:t + n] = True
+            span_id[b, t:t + n] = sid
+            t += n
+        in_span[b, 8192 - 5:8192 + 5] = True
+        span_id[b, 8192 - 5:8192 + 5] = span_id[b, 8192 - 5] if span_id[b, 8192 - 5] > 0 else 3
+    kw = dict(in_span=torch.from_numpy(in_span), span_id=torch.from_numpy(span_id),
+              is_prefix=torch.from_numpy(is_prefix))
+    print(f"plan spans across rounds T={T}", flush=True)
+    p = _device_plan(dev, B, T, 64, **kw)
+    _check_plan(p, dense_mask(T, in_span=in_span, span_id=span_id, is_prefix=is_prefix))
+
+
 def test_plan_strided_metadata(dev):
     rng = np.random.default_rng(11)
     T = 333
