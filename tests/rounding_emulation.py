@@ -103,9 +103,10 @@ def emulate_head(q, k, v, do, mask, sm_scale, rot=None, block=1024):
     rotated and rounded when ``rot`` is given); mask: bool [T, T]; rot: the
     fp64 rotation R (dQ, dK are reported for the unrotated inputs, times R^T).
     Returns ``{"excess": {(product, form): float}, "coupled": {product: float},
-    "max_abs_ds": float, "ref_max": {product: float}}``: "coupled" holds dV,
-    dQ, dK in the split form with Delta and LSE from a forward whose P V took P
-    rounded once to fp16.
+    "max_abs_ds": float, "ref_max": {product: float}, "refs": {product: array}}``:
+    "coupled" holds dV, dQ, dK in the split form with Delta and LSE from a
+    forward whose P V took P rounded once to fp16; "refs" the fp64 results the
+    excesses are measured against.
     """
     T, d = q.shape
     c32 = np.float32(sm_scale * LOG2E)
@@ -196,7 +197,7 @@ def emulate_head(q, k, v, do, mask, sm_scale, rot=None, block=1024):
         for p, e in grads(acc[("bf16x2", f)]).items():
             ex[(p, f)] = e
     return {"excess": ex, "coupled": grads(acc[("fp16", "bf16x2")]), "max_abs_ds": max_ds,
-            "ref_max": {p: float(np.abs(r).max()) for p, r in refs.items()}}
+            "ref_max": {p: float(np.abs(r).max()) for p, r in refs.items()}, "refs": refs}
 
 
 def config4_head(b: int, h: int, hadamard: bool, seed: int = 0):
