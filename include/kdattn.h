@@ -195,7 +195,9 @@ typedef struct kd_span_args {
   int64_t dh_strides[2];    /* (b, t) in elements, unit d stride */
 } kd_span_args;
 
-/* Library version (major*10000 + minor*100 + patch). */
+/* Library version (major*10000 + minor*100 + patch).  3.0.0: the plan's size
+ * beside its pointer in every entry point that takes a plan.  3.1.0:
+ * kd_plan_layout writes 20 offsets (the dK/dV work order added). */
 int kd_version(void);
 
 /* Message for the last non-zero status returned on this thread. */
@@ -215,13 +217,14 @@ void kd_struct_sizes3(size_t *tokens);
  * Workspace ("plan") bytes for B sequences of length T at head dim D, and
  * the byte offsets of its sections (token codes, class map, per-tile allowed
  * counts, the forward / dQ / dK-dV work lists, the work orders).  offsets[]
- * receives 19 int64: codes, rep, cls, nnz, fwd_list, fwd_count, dq_list,
+ * receives 20 int64: codes, rep, cls, nnz, fwd_list, fwd_count, dq_list,
  * dq_count, dkdv_list, dkdv_count, nT, fwd_group, dq_group, dkdv_group,
- * n_fwd_blocks, n_dq_blocks, n_dkdv_blocks, fwd_order, dq_order.  A list
- * entry is (tile << 8) | the class of group member r in bits 2r..2r+1.  A
- * work order (u32 [B n]) lists the items b n + block of the forward or dQ
- * list by descending list length (equal lengths in ascending item order);
- * those kernels take each head's blocks in that order.  The plan holds no
+ * n_fwd_blocks, n_dq_blocks, n_dkdv_blocks, fwd_order, dq_order, dkdv_order.
+ * A list entry is (tile << 8) | the class of group member r in bits 2r..2r+1.
+ * A work order (u32 [B n]) lists the items b n + block of the forward, dQ or
+ * dK/dV list by descending list length (equal lengths in ascending item
+ * order); the forward and dQ kernels, and the dK/dV kernel at head dims 16,
+ * 32, 64 and 256, take each head's blocks in that order.  The plan holds no
  * per-element masks (the kernels build PARTIAL tiles' masks from the codes),
  * so it takes O(B T + B nT^2) bytes.  Replaces the per-tile mask evaluation of
  * original_kernel.py:457-517 (the reference has no tile map). */

@@ -211,12 +211,12 @@ def plan_nbytes(B, T, D):
     return (r(BT * 4) + r(BT * 4) + r(BT * 4) + r(BT * 8) + r(B * 4) + r(BT) + r(BT * 8) + r(BT)
             + r(BTT) + r(BTT * 4)
             + 3 * (r(B * nb * nT * 4) + r(B * nb * 4))
-            + 2 * r(B * nb * 4))
+            + 3 * r(B * nb * 4))
 
 
 PLAN_FIELDS = ("codes", "rep", "cls", "nnz", "fwd_list", "fwd_count", "dq_list", "dq_count",
                "dkdv_list", "dkdv_count", "nT", "fwd_group", "dq_group", "dkdv_group",
-               "n_fwd_blocks", "n_dq_blocks", "n_dkdv_blocks", "fwd_order", "dq_order")
+               "n_fwd_blocks", "n_dq_blocks", "n_dkdv_blocks", "fwd_order", "dq_order", "dkdv_order")
 
 
 def plan_layout(B: int, T: int, D: int) -> dict:

@@ -672,6 +672,7 @@ def plan_views(plan: torch.Tensor, B: int, T: int, D: int) -> dict:
         # work orders: items b n + block by descending list length
         "fwd_order": view(L["fwd_order"], B * nf, torch.int32),
         "dq_order": view(L["dq_order"], B * nq, torch.int32),
+        "dkdv_order": view(L["dkdv_order"], B * nk, torch.int32),
         "layout": L,
     }
 

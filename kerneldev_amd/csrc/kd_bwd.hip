@@ -967,7 +967,8 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
 template <class E, int D, int NSP, int DH, int D0>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, const uint32_t* __restrict__ codes,
                                                       const uint32_t* __restrict__ list,
-                                                      const int32_t* __restrict__ count, int nT, int nKB) {
+                                                      const int32_t* __restrict__ count,
+                                                      const uint32_t* __restrict__ order, int nT, int nKB) {
   constexpr bool SP = NSP >= 2, S3 = NSP == 3;
   using TL = Tile<D, 4>;
   constexpr int DS = D / 16, NL = TL::LOADS_PER_WAVE;
@@ -983,9 +984,9 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
             c = lane & 31;
   const int T = a.T, H = a.H;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
-  const int hb = work / nKB;
-  const int kblock = work % nKB;
-  const int b = hb % a.B, h = hb / a.B, bh = b * H + h;
+  const int h = work / (a.B * nKB);  // head-major, then the plan's longest-first dK/dV order
+  const int item = int(order[work - h * (a.B * nKB)]);
+  const int b = item / nKB, kblock = item - b * nKB, bh = b * H + h;
 
   const uint16_t* qg = static_cast<const uint16_t*>(a.q) + b * a.q_strides[0] + h * a.q_strides[1];
   const uint16_t* dog = static_cast<const uint16_t*>(a.dout) + b * a.do_strides[0] + h * a.do_strides[1];
@@ -1238,15 +1239,17 @@ static void launch_dkdv_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st
     hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 64, 0>), dim3(grid), dim3(256), 0, st, a,
                        reinterpret_cast<const uint32_t*>(plan + L.codes),
                        reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
-                       reinterpret_cast<const int32_t*>(plan + L.dkdv_count), L.nT, L.n_dkdv_blocks);
+                       reinterpret_cast<const int32_t*>(plan + L.dkdv_count),
+                       reinterpret_cast<const uint32_t*>(plan + L.dkdv_order), L.nT, L.n_dkdv_blocks);
   } else if constexpr (D == 256) {  // two launches, the column halves of dK and dV
     auto* codes = reinterpret_cast<const uint32_t*>(plan + L.codes);
     auto* list = reinterpret_cast<const uint32_t*>(plan + L.dkdv_list);
     auto* cnt = reinterpret_cast<const int32_t*>(plan + L.dkdv_count);
-    hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 128, 0>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, L.nT,
-                       L.n_dkdv_blocks);
-    hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 128, 128>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, L.nT,
-                       L.n_dkdv_blocks);
+    auto* order = reinterpret_cast<const uint32_t*>(plan + L.dkdv_order);
+    hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 128, 0>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, order,
+                       L.nT, L.n_dkdv_blocks);
+    hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 128, 128>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, order,
+                       L.nT, L.n_dkdv_blocks);
   } else {
     hipLaunchKernelGGL((k_dkdv<E, D, Q8, NSP>), dim3(grid), dim3(512), 0, st, a,
                        reinterpret_cast<const uint32_t*>(plan + L.codes),

@@ -118,7 +118,7 @@ int check_plan(const void* plan, int64_t plan_bytes, int B, int T, int D) {
 
 extern "C" {
 
-int kd_version(void) { return 30000; }
+int kd_version(void) { return 30100; }
 
 const char* kd_last_error_string(void) { return g_err.c_str(); }
 
@@ -218,12 +218,12 @@ int64_t kd_plan_bytes(int32_t B, int32_t T, int32_t D) {
 int kd_plan_layout(int32_t B, int32_t T, int32_t D, int64_t* off) {
   if (off == nullptr || B < 1 || T < 1) return fail(KD_ERR_INVALID, "bad plan_layout arguments");
   const kd::PlanLayout L = kd::plan_layout(B, T, D);
-  const int64_t v[19] = {int64_t(L.codes),     int64_t(L.rep),        int64_t(L.cls),     int64_t(L.nnz),
+  const int64_t v[20] = {int64_t(L.codes),     int64_t(L.rep),        int64_t(L.cls),     int64_t(L.nnz),
                          int64_t(L.fwd_list),  int64_t(L.fwd_count),  int64_t(L.dq_list), int64_t(L.dq_count),
                          int64_t(L.dkdv_list), int64_t(L.dkdv_count), L.nT,               L.fwd_group,
                          L.dq_group,           L.dkdv_group,          L.n_fwd_blocks,     L.n_dq_blocks,
-                         L.n_dkdv_blocks,      int64_t(L.fwd_order),  int64_t(L.dq_order)};
-  for (int i = 0; i < 19; ++i) off[i] = v[i];
+                         L.n_dkdv_blocks,      int64_t(L.fwd_order),  int64_t(L.dq_order), int64_t(L.dkdv_order)};
+  for (int i = 0; i < 20; ++i) off[i] = v[i];
   return KD_OK;
 }
 

@@ -35,7 +35,7 @@ KD_DEV inline bool entry_full(uint32_t e, int group) {
 
 struct PlanLayout {
   size_t codes, rep, runs, run_sid, run_count, tok_in_span, tok_span_id, tok_prefix, cls, nnz, fwd_list, fwd_count, dq_list, dq_count, dkdv_list, dkdv_count,
-      fwd_order, dq_order, total;
+      fwd_order, dq_order, dkdv_order, total;
   int nT, fwd_group, dq_group, dkdv_group, n_fwd_blocks, n_dq_blocks, n_dkdv_blocks;
 };
 

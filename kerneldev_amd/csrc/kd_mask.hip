@@ -151,10 +151,11 @@ constexpr int CODE_SEG = 8;  // most tokens per thread and round (span ids)
 // (each id has one run), the layout of the token-derived metadata and of the
 // collate builders; the workgroup checks that over the finished list and
 // otherwise recodes the eligible tokens with the first listed run with their
-// id (run_rep).  The workgroups also zero the forward list lengths, which the
-// tile classifier accumulates.
+// id (run_rep).  The workgroups also zero the forward and dK/dV list lengths,
+// which the tile classifier accumulates.
 __global__ __launch_bounds__(1024) void k_codes_rows(MetaArgs m, uint32_t* runs, int64_t* run_sid, int32_t* run_count,
-                                                     uint32_t* rep, uint32_t* codes, int32_t* fwd_n, int n_fwd) {
+                                                     uint32_t* rep, uint32_t* codes, int32_t* fwd_n, int n_fwd,
+                                                     int32_t* dkdv_n, int n_dkdv) {
   __shared__ int s_warp[16];
   __shared__ int s_n, s_dup;
   const int b = blockIdx.y, tid = threadIdx.x, T = m.T;
@@ -162,6 +163,7 @@ __global__ __launch_bounds__(1024) void k_codes_rows(MetaArgs m, uint32_t* runs,
   {
     const int gid = (blockIdx.y * gridDim.x + blockIdx.x) * 1024 + tid, nth = gridDim.x * gridDim.y * 1024;
     for (int i = gid; i < n_fwd; i += nth) fwd_n[i] = 0;
+    for (int i = gid; i < n_dkdv; i += nth) dkdv_n[i] = 0;
   }
   int seq_len = T;
   if (m.lens != nullptr) seq_len = min(m.lens[int64_t(b) * m.lens_stride], T);
@@ -272,11 +274,13 @@ __global__ __launch_bounds__(1024) void k_codes_rows(MetaArgs m, uint32_t* runs,
 // each: query_row_mask, the function the forward and dQ kernels use for
 // PARTIAL tiles.  That is the rule of allow(), term for term.  The workgroup
 // then adds its k-tiles with a non-empty tile in the row block to that row
-// block's forward list length (zeroed by the first launch).
+// block's forward list length, and for each of its key blocks (k-tiles
+// 2 kb, 2 kb + 1) its q-tiles with a non-empty tile there to that key block's
+// dK/dV list length (both zeroed by the first launch).
 constexpr int TM_KPW = 4;  // most k-tiles per wave
 
 __global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, int nT, int kpw, uint8_t* cls,
-                                                 int32_t* nnz, int32_t* fwd_n) {
+                                                 int32_t* nnz, int32_t* fwd_n, int32_t* dkdv_n, int nkb) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int rb = blockIdx.y, b = blockIdx.z, nqb = int(gridDim.y);
   const int qt = rb * 2 + (wave & 1), half = wave >> 1;
@@ -313,26 +317,31 @@ __global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, i
   if (threadIdx.x == 0) {
     const int add = __builtin_popcount(s_ne[0] | s_ne[1]);
     if (add != 0) atomicAdd(fwd_n + int64_t(b) * nqb + rb, add);
+  } else if (int(threadIdx.x) <= kpw) {  // key block j = threadIdx.x - 1 of this workgroup
+    const int j = int(threadIdx.x) - 1, kb = int(blockIdx.x) * kpw + j;
+    const int add = int(((s_ne[0] >> (2 * j)) & 3u) != 0u) + int(((s_ne[1] >> (2 * j)) & 3u) != 0u);
+    if (kb < nkb && add != 0) atomicAdd(dkdv_n + int64_t(b) * nkb + kb, add);
   }
 }
 
-// ---- work lists and work order (third launch) -----------------------------
+// ---- work lists and work orders (third launch) ----------------------------
 // One workgroup per list: the B nqb row blocks of the forward / dQ lists (two
 // q-tiles against every k-tile; the two lists are the same), then the B nkb
 // key blocks of the dK/dV list (two k-tiles against every q-tile).  Wave 0
 // compacts the block's non-empty entries in ascending order with a ballot and
-// a prefix popcount, and zero-fills the tail.  The forward / dQ work order
-// ranks the B nqb items b nqb + block by descending list length, equal lengths
-// in ascending item order (item i goes to position #{j : c_j > c_i or
-// (c_j == c_i and j < i)}); the attention kernels take each head's blocks in
-// this order, so the longest start first and the short ones fill the end of
-// every XCD's range (longest-first list scheduling).  The forward list
-// lengths arrive complete from the classifier, so each row-block workgroup
-// ranks its own item and no workgroup waits for another.
+// a prefix popcount, and zero-fills the tail.  A work order ranks a list's
+// B n items b n + block by descending list length, equal lengths in ascending
+// item order (item i goes to position #{j : c_j > c_i or (c_j == c_i and
+// j < i)}); the kernels that use one take each head's blocks in this order,
+// so the longest start first and the short ones fill the end of every XCD's
+// range (longest-first list scheduling).  The list lengths arrive complete
+// from the classifier, so each workgroup ranks its own item and no workgroup
+// waits for another.
 struct ListOut {
   uint32_t *fwd, *dq, *dkdv;       // entries, [B nb nT]
   int32_t *fwd_n, *dq_n, *dkdv_n;  // counts, [B nb]
-  uint32_t *fwd_order, *dq_order;  // [B nb]
+  uint32_t *fwd_order, *dq_order;  // [B nqb]
+  uint32_t* dkdv_order;            // [B nkb]
   int nqb, nkb;                    // row blocks (forward and dQ), key blocks (dK/dV)
 };
 
@@ -375,14 +384,14 @@ __global__ __launch_bounds__(256) void k_lists(const uint8_t* __restrict__ cls, 
       out[c] = 0;
       if (rows) out2[c] = 0;
     }
-    if (lane == 0) (rows ? lo.dq_n : lo.dkdv_n)[item] = n;  // (fwd_n: the classifier's sums, the same n)
+    if (lane == 0 && rows) lo.dq_n[item] = n;  // (fwd_n, dkdv_n: the classifier's sums, the same n)
   }
-  if (!rows) return;  // workgroup-uniform
   // this item's rank: the items before it in the order
-  const int ci = lo.fwd_n[item], n_items = B * lo.nqb;
+  const int32_t* len = rows ? lo.fwd_n : lo.dkdv_n;
+  const int ci = len[item], n_items = B * (rows ? lo.nqb : lo.nkb);
   int before = 0;
   for (int j = tid; j < n_items; j += 256) {
-    const int cj = lo.fwd_n[j];
+    const int cj = len[j];
     before += (cj > ci || (cj == ci && j < item)) ? 1 : 0;
   }
   for (int off = 32; off > 0; off >>= 1) before += __shfl_xor(before, off);
@@ -390,8 +399,12 @@ __global__ __launch_bounds__(256) void k_lists(const uint8_t* __restrict__ cls, 
   __syncthreads();
   if (tid == 0) {
     const int rank = s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
-    lo.fwd_order[rank] = uint32_t(item);
-    lo.dq_order[rank] = uint32_t(item);
+    if (rows) {
+      lo.fwd_order[rank] = uint32_t(item);
+      lo.dq_order[rank] = uint32_t(item);
+    } else {
+      lo.dkdv_order[rank] = uint32_t(item);
+    }
   }
 }
 
@@ -466,6 +479,7 @@ PlanLayout plan_layout(int B, int T, int D) {
   L.dkdv_count = take(size_t(B) * nk * 4);
   L.fwd_order = take(size_t(B) * nf * 4);
   L.dq_order = take(size_t(B) * nq * 4);
+  L.dkdv_order = take(size_t(B) * nk * 4);
   L.total = off;
   return L;
 }
@@ -494,14 +508,15 @@ int launch_plan(const MetaArgs& m, uint8_t* plan, hipStream_t st) {
   lo.dkdv_n = reinterpret_cast<int32_t*>(plan + L.dkdv_count);
   lo.fwd_order = reinterpret_cast<uint32_t*>(plan + L.fwd_order);
   lo.dq_order = reinterpret_cast<uint32_t*>(plan + L.dq_order);
+  lo.dkdv_order = reinterpret_cast<uint32_t*>(plan + L.dkdv_order);
   lo.nqb = L.n_fwd_blocks;  // (the forward and dQ lists share the grouping of two q-tiles)
   lo.nkb = L.n_dkdv_blocks;
   hipLaunchKernelGGL(k_codes_rows, dim3(chunks, unsigned(m.B)), dim3(1024), 0, st, m, runs, run_sid, run_count, rep,
-                     codes, lo.fwd_n, m.B * lo.nqb);
+                     codes, lo.fwd_n, m.B * lo.nqb, lo.dkdv_n, m.B * lo.nkb);
   // k-tiles per wave: TM_KPW once the grid holds 2048 workgroups at that, else 1
   const int kpw = int64_t(m.B) * lo.nqb * ((L.nT + 2 * TM_KPW - 1) / (2 * TM_KPW)) >= 2048 ? TM_KPW : 1;
   hipLaunchKernelGGL(k_tilemap, dim3(unsigned((L.nT + 2 * kpw - 1) / (2 * kpw)), unsigned(lo.nqb), unsigned(m.B)),
-                     dim3(256), 0, st, codes, m.T, L.nT, kpw, cls, nnz, lo.fwd_n);
+                     dim3(256), 0, st, codes, m.T, L.nT, kpw, cls, nnz, lo.fwd_n, lo.dkdv_n, lo.nkb);
   hipLaunchKernelGGL(k_lists, dim3(unsigned(lo.nqb + lo.nkb), unsigned(m.B)), dim3(256), 0, st, cls, L.nT, lo);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }

@@ -38,7 +38,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_struct_layouts_and_version():
     lib = _lib.load()  # load() itself checks the three struct sizes
-    assert lib.kd_version() >= 30000  # 3.0: plan sizes at the boundary
+    assert lib.kd_version() >= 30100  # 3.0: plan sizes at the boundary; 3.1: the dK/dV work order
     assert ctypes.sizeof(_lib.AttnArgs) % 8 == 0
 
 
@@ -50,9 +50,9 @@ def test_plan_sizes_and_layout_offsets():
     offs = [L[k] for k in _lib.PLAN_FIELDS[:10]]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
     assert _lib.plan_bytes(2, 8192, 128) > L["dkdv_count"]
-    tail = [L[k] for k in ("dkdv_count", "fwd_order", "dq_order")]
+    tail = [L[k] for k in ("dkdv_count", "fwd_order", "dq_order", "dkdv_order")]
     assert tail == sorted(tail) and all(o % 256 == 0 for o in tail)
-    assert _lib.plan_bytes(2, 8192, 128) >= L["dq_order"] + 4 * 2 * L["n_dq_blocks"]
+    assert _lib.plan_bytes(2, 8192, 128) >= L["dkdv_order"] + 4 * 2 * L["n_dkdv_blocks"]
 
 
 def test_bad_arguments_return_status_without_gpu():

@@ -51,9 +51,9 @@ def _check_plan(p, mask):
         ent, counts = fn(cls, group)
         np.testing.assert_array_equal(p[f"{name}_count"], counts, err_msg=name)
         np.testing.assert_array_equal(p[f"{name}_list"].view(np.uint32), ent, err_msg=name)
-        if name != "dkdv":  # work order: descending count, ties by ascending item (a stable sort of -count)
-            flat = np.asarray(counts).reshape(-1)
-            np.testing.assert_array_equal(p[f"{name}_order"], np.argsort(-flat, kind="stable"), err_msg=name)
+        # work order: descending count, ties by ascending item (a stable sort of -count)
+        flat = np.asarray(counts).reshape(-1)
+        np.testing.assert_array_equal(p[f"{name}_order"], np.argsort(-flat, kind="stable"), err_msg=name)
     # row / column bit masks as the kernels build them from the codes (kd_tile_masks),
     # bit-exact on every tile (the kernels use them on PARTIAL tiles)
     qbits, kbits = tilemap.tile_bits(mask, 64)
