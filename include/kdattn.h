@@ -292,7 +292,8 @@ int kd_attn_bwd_noalloc(const kd_attn_args *a, const void *plan, int64_t plan_by
  * (bit j of entry r: query 64 qt + r may see key 64 kt + j) and cols
  * [B, nT, nT, 64] (bit r of entry j: query 64 qt + r may see key 64 kt + j).
  * An inspection aid (the kernels never store them); no reference counterpart,
- * the reference evaluates original_kernel.py:478-517 per element. */
+ * the reference evaluates original_kernel.py:478-517 per element.  T is at
+ * most 65535 * 64 here (KD_ERR_UNSUPPORTED beyond). */
 int kd_tile_masks(const void *plan, int64_t plan_bytes, int32_t B, int32_t T, int32_t D, uint64_t *rows,
                   uint64_t *cols, void *stream);
 

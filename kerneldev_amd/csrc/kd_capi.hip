@@ -165,6 +165,7 @@ int kd_plan_build_tokens(const kd_token_args* t, void* plan, int64_t plan_bytes,
   if (t == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
   if (t->B < 1 || t->T < 1) return fail(KD_ERR_INVALID, "B and T must be >= 1");
   if (t->T > (1 << 24) - 2) return fail(KD_ERR_UNSUPPORTED, "T must be < 2^24 - 1");
+  if (t->B > 65535) return fail(KD_ERR_UNSUPPORTED, "B must be <= 65535");
   if (int r = check_plan(plan, plan_bytes, t->B, t->T, t->D)) return r;
   if (t->tokens == nullptr) return fail(KD_ERR_INVALID, "tokens is NULL");
   if (t->tokens_dtype != KD_I64 && t->tokens_dtype != KD_I32)
@@ -231,6 +232,7 @@ int kd_plan_build(const kd_meta_args* m, void* plan, int64_t plan_bytes, void* s
   if (m == nullptr) return fail(KD_ERR_INVALID, "meta is NULL");
   if (m->B < 1 || m->T < 1) return fail(KD_ERR_INVALID, "B and T must be >= 1");
   if (m->T > (1 << 24) - 2) return fail(KD_ERR_UNSUPPORTED, "T must be < 2^24 - 1");
+  if (m->B > 65535) return fail(KD_ERR_UNSUPPORTED, "B must be <= 65535");
   if (int r = check_plan(plan, plan_bytes, m->B, m->T, m->D)) return r;
   if (m->mode != KD_MODE_FORMULA && m->mode != KD_MODE_CAUSAL && m->mode != KD_MODE_ALL)
     return fail(KD_ERR_INVALID, "unknown mask mode");
@@ -365,7 +367,9 @@ int kd_tile_masks(const void* plan, int64_t plan_bytes, int32_t B, int32_t T, in
                   uint64_t* cols, void* stream) {
   if (rows == nullptr || cols == nullptr) return fail(KD_ERR_INVALID, "NULL argument");
   if (B < 1 || T < 1) return fail(KD_ERR_INVALID, "B and T must be >= 1");
-  if (T > (1 << 24) - 2) return fail(KD_ERR_UNSUPPORTED, "T must be < 2^24 - 1");
+  // (one workgroup row per q-tile: the grid's y extent holds at most 65535)
+  if (T > 65535 * 64) return fail(KD_ERR_UNSUPPORTED, "kd_tile_masks takes T <= 65535 * 64");
+  if (B > 65535) return fail(KD_ERR_UNSUPPORTED, "B must be <= 65535");
   if (int r = check_plan(plan, plan_bytes, B, T, D)) return r;
   const int r = kd::launch_tile_masks(static_cast<const uint8_t*>(plan), B, T, D, rows, cols, as_stream(stream));
   return r ? fail(r, "kernel launch failed (tile masks)") : KD_OK;

@@ -279,11 +279,10 @@ __global__ __launch_bounds__(1024) void k_codes_rows(MetaArgs m, uint32_t* runs,
 // dK/dV list length (both zeroed by the first launch).
 constexpr int TM_KPW = 4;  // most k-tiles per wave
 
-__global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, int nT, int kpw, uint8_t* cls,
+__global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, int nT, int kpw, int nqb, uint8_t* cls,
                                                  int32_t* nnz, int32_t* fwd_n, int32_t* dkdv_n, int nkb) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int rb = blockIdx.y, b = blockIdx.z, nqb = int(gridDim.y);
-  const int qt = rb * 2 + (wave & 1), half = wave >> 1;
+  const int b = blockIdx.z, half = wave >> 1;
   const int kt0 = blockIdx.x * 2 * kpw;
   __shared__ uint32_t s_k[2 * TM_KPW * 64];
   __shared__ uint32_t s_ne[2];  // bit i: k-tile kt0 + i has a non-empty tile, per q-tile
@@ -291,36 +290,41 @@ __global__ __launch_bounds__(256) void k_tilemap(const uint32_t* codes, int T, i
     const int j = kt0 * 64 + x;
     s_k[x] = (j < T) ? codes[int64_t(b) * T + j] : 0u;
   }
-  if (threadIdx.x < 2) s_ne[threadIdx.x] = 0u;
-  __syncthreads();
-  const int i = qt * 64 + lane;
-  const uint32_t qc = (qt < nT && i < T) ? codes[int64_t(b) * T + i] : 0u;
-  uint32_t ne = 0;
-  if (qt < nT) {  // wave-uniform
-    for (int x = half * kpw; x < (half + 1) * kpw; ++x) {
-      const int kt = kt0 + x;
-      if (kt >= nT) break;
-      const uint32_t kc = s_k[x * 64 + lane];  // key j = 64 kt + lane (code 0 past T: allows nothing)
-      const uint64_t row = query_row_mask(qc, i, kc, kt * 64);
-      int cnt = __builtin_popcountll(row);
-      for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off);
-      const int64_t o = (int64_t(b) * nT + qt) * nT + kt;
-      if (lane == 0) {
-        cls[o] = cnt == 0 ? TILE_EMPTY : (cnt == 64 * 64 ? TILE_FULL : TILE_PARTIAL);
-        if (nnz != nullptr) nnz[o] = cnt;
+  // row blocks blockIdx.y, + gridDim.y, ... (the grid's y extent is capped at 65535)
+  for (int rb = blockIdx.y; rb < nqb; rb += gridDim.y) {
+    if (threadIdx.x < 2) s_ne[threadIdx.x] = 0u;
+    __syncthreads();  // s_k landed (first pass), s_ne cleared
+    const int qt = rb * 2 + (wave & 1);
+    const int i = qt * 64 + lane;
+    const uint32_t qc = (qt < nT && i < T) ? codes[int64_t(b) * T + i] : 0u;
+    uint32_t ne = 0;
+    if (qt < nT) {  // wave-uniform
+      for (int x = half * kpw; x < (half + 1) * kpw; ++x) {
+        const int kt = kt0 + x;
+        if (kt >= nT) break;
+        const uint32_t kc = s_k[x * 64 + lane];  // key j = 64 kt + lane (code 0 past T: allows nothing)
+        const uint64_t row = query_row_mask(qc, i, kc, kt * 64);
+        int cnt = __builtin_popcountll(row);
+        for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off);
+        const int64_t o = (int64_t(b) * nT + qt) * nT + kt;
+        if (lane == 0) {
+          cls[o] = cnt == 0 ? TILE_EMPTY : (cnt == 64 * 64 ? TILE_FULL : TILE_PARTIAL);
+          if (nnz != nullptr) nnz[o] = cnt;
+        }
+        if (cnt != 0) ne |= 1u << x;
       }
-      if (cnt != 0) ne |= 1u << x;
     }
-  }
-  if (lane == 0 && ne != 0u) atomicOr(&s_ne[wave & 1], ne);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int add = __builtin_popcount(s_ne[0] | s_ne[1]);
-    if (add != 0) atomicAdd(fwd_n + int64_t(b) * nqb + rb, add);
-  } else if (int(threadIdx.x) <= kpw) {  // key block j = threadIdx.x - 1 of this workgroup
-    const int j = int(threadIdx.x) - 1, kb = int(blockIdx.x) * kpw + j;
-    const int add = int(((s_ne[0] >> (2 * j)) & 3u) != 0u) + int(((s_ne[1] >> (2 * j)) & 3u) != 0u);
-    if (kb < nkb && add != 0) atomicAdd(dkdv_n + int64_t(b) * nkb + kb, add);
+    if (lane == 0 && ne != 0u) atomicOr(&s_ne[wave & 1], ne);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int add = __builtin_popcount(s_ne[0] | s_ne[1]);
+      if (add != 0) atomicAdd(fwd_n + int64_t(b) * nqb + rb, add);
+    } else if (int(threadIdx.x) <= kpw) {  // key block j = threadIdx.x - 1 of this workgroup
+      const int j = int(threadIdx.x) - 1, kb = int(blockIdx.x) * kpw + j;
+      const int add = int(((s_ne[0] >> (2 * j)) & 3u) != 0u) + int(((s_ne[1] >> (2 * j)) & 3u) != 0u);
+      if (kb < nkb && add != 0) atomicAdd(dkdv_n + int64_t(b) * nkb + kb, add);
+    }
+    __syncthreads();  // every read of s_ne done before the next pass clears it
   }
 }
 
@@ -515,8 +519,10 @@ int launch_plan(const MetaArgs& m, uint8_t* plan, hipStream_t st) {
                      codes, lo.fwd_n, m.B * lo.nqb, lo.dkdv_n, m.B * lo.nkb);
   // k-tiles per wave: TM_KPW once the grid holds 2048 workgroups at that, else 1
   const int kpw = int64_t(m.B) * lo.nqb * ((L.nT + 2 * TM_KPW - 1) / (2 * TM_KPW)) >= 2048 ? TM_KPW : 1;
-  hipLaunchKernelGGL(k_tilemap, dim3(unsigned((L.nT + 2 * kpw - 1) / (2 * kpw)), unsigned(lo.nqb), unsigned(m.B)),
-                     dim3(256), 0, st, codes, m.T, L.nT, kpw, cls, nnz, lo.fwd_n, lo.dkdv_n, lo.nkb);
+  hipLaunchKernelGGL(k_tilemap,
+                     dim3(unsigned((L.nT + 2 * kpw - 1) / (2 * kpw)), unsigned(std::min(lo.nqb, 65535)),
+                     unsigned(m.B)),
+                     dim3(256), 0, st, codes, m.T, L.nT, kpw, lo.nqb, cls, nnz, lo.fwd_n, lo.dkdv_n, lo.nkb);
   hipLaunchKernelGGL(k_lists, dim3(unsigned(lo.nqb + lo.nkb), unsigned(m.B)), dim3(256), 0, st, cls, L.nT, lo);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }

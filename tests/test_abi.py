@@ -242,3 +242,23 @@ def test_c_caller_is_built_against_the_library():
     if shutil.which("ldd"):
         out = subprocess.run(["ldd", C_ABI_BIN], capture_output=True, text=True).stdout
         assert "libkdattn.so =>" in out and "not found" not in out.split("libkdattn.so")[1].split("\n")[0]
+
+
+def test_grid_limits_are_refused_before_any_launch():
+    """Shapes whose plan launches would exceed a grid dimension (65535 workgroups
+    on y and z) get KD_ERR_UNSUPPORTED from the host checks: B > 65535 for the
+    plan builds, and kd_tile_masks (one workgroup row per q-tile) past
+    T = 65535 * 64."""
+    lib = _lib.load()
+    null = ctypes.c_void_p(0)
+    plan = ctypes.c_void_p(1 << 20)
+    m = _lib.MetaArgs()
+    m.B, m.T, m.D, m.mode = 65536, 64, 64, _lib.KD_MODE_CAUSAL
+    assert lib.kd_plan_build(ctypes.byref(m), plan, BIG, null) == _lib.KD_ERR_UNSUPPORTED
+    assert "B must be" in lib.kd_last_error_string().decode()
+    t = _lib.TokenArgs()
+    t.B, t.T, t.D, t.tokens = 65536, 64, 64, 256
+    assert lib.kd_plan_build_tokens(ctypes.byref(t), plan, BIG, null) == _lib.KD_ERR_UNSUPPORTED
+    rows = ctypes.c_void_p(256)
+    assert lib.kd_tile_masks(plan, BIG, 1, 65535 * 64 + 1, 64, rows, rows, null) == _lib.KD_ERR_UNSUPPORTED
+    assert "kd_tile_masks" in lib.kd_last_error_string().decode()
