@@ -223,8 +223,8 @@ void kd_struct_sizes3(size_t *tokens);
  * A list entry is (tile << 8) | the class of group member r in bits 2r..2r+1.
  * A work order (u32 [B n]) lists the items b n + block of the forward, dQ or
  * dK/dV list by descending list length (equal lengths in ascending item
- * order); the forward and dQ kernels, and the dK/dV kernel at head dims 16,
- * 32, 64 and 256, take each head's blocks in that order.  The plan holds no
+ * order); the forward, dQ and dK/dV kernels take each head's blocks in that
+ * order.  The plan holds no
  * per-element masks (the kernels build PARTIAL tiles' masks from the codes),
  * so it takes O(B T + B nT^2) bytes.  Replaces the per-tile mask evaluation of
  * original_kernel.py:457-517 (the reference has no tile map). */

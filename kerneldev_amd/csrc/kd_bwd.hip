@@ -538,7 +538,8 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
 template <class E, int D, bool Q8, int NSP>
 __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __restrict__ codes,
                                                  const uint32_t* __restrict__ list,
-                                                 const int32_t* __restrict__ count, int nT, int nKB) {
+                                                 const int32_t* __restrict__ count,
+                                                 const uint32_t* __restrict__ order, int nT, int nKB) {
   constexpr bool SP = NSP >= 2, S3 = NSP == 3;
   constexpr int NW = 8;
   using TL = Tile<D, NW>;
@@ -571,12 +572,9 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   const int pair = wave & 3, role = wave >> 2;
   const int T = a.T, H = a.H;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
-  // head-major, then batch row, then ascending key block: the longest-first
-  // order of the forward and dQ measured no better here (one workgroup per CU
-  // already balances well, and mixing batch rows spreads the Q / dO reads)
-  const int hb = work / nKB;
-  const int kblock = work % nKB;
-  const int b = hb % a.B, h = hb / a.B, bh = b * H + h;
+  const int h = work / (a.B * nKB);  // head-major, then the plan's longest-first dK/dV order
+  const int item = int(order[work - h * (a.B * nKB)]);
+  const int b = item / nKB, kblock = item - b * nKB, bh = b * H + h;
 
   const uint16_t* qg = static_cast<const uint16_t*>(a.q) + b * a.q_strides[0] + h * a.q_strides[1];
   const uint16_t* dog = static_cast<const uint16_t*>(a.dout) + b * a.do_strides[0] + h * a.do_strides[1];
@@ -1254,7 +1252,8 @@ static void launch_dkdv_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st
     hipLaunchKernelGGL((k_dkdv<E, D, Q8, NSP>), dim3(grid), dim3(512), 0, st, a,
                        reinterpret_cast<const uint32_t*>(plan + L.codes),
                        reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
-                       reinterpret_cast<const int32_t*>(plan + L.dkdv_count), L.nT, L.n_dkdv_blocks);
+                       reinterpret_cast<const int32_t*>(plan + L.dkdv_count),
+                       reinterpret_cast<const uint32_t*>(plan + L.dkdv_order), L.nT, L.n_dkdv_blocks);
   }
 }
 

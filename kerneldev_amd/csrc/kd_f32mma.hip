@@ -357,7 +357,7 @@ template <int D>
 __global__ __launch_bounds__(256, D <= 32 ? 2 : 1) void k_dkdv_f32m(AttnArgs a, const uint32_t* __restrict__ codes,
                                                                     const uint32_t* __restrict__ list,
                                                                     const int32_t* __restrict__ count, int nT,
-                                                                    int nblk) {
+                                                                    int nblk, const uint32_t* __restrict__ order) {
   using FT = F32Tile<D>;
   constexpr int DB = D / 32;
   __shared__ __attribute__((aligned(1024))) uint8_t s_q[2][FT::BYTES];
@@ -367,9 +367,10 @@ __global__ __launch_bounds__(256, D <= 32 ? 2 : 1) void k_dkdv_f32m(AttnArgs a, 
   __shared__ __attribute__((aligned(256))) uint32_t s_qc[2][64];
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), member = wave >> 1;
-  // head-major, then batch row, then ascending key block
+  // head-major, then the plan's longest-first dK/dV order
   const int work = xcd_remap(blockIdx.x, gridDim.x), T = a.T;
-  const int hb = work / nblk, blk = work - hb * nblk, b = hb % a.B, hh = hb / a.B, bh = b * a.H + hh;
+  const int hh = work / (a.B * nblk), item = int(order[work - hh * (a.B * nblk)]);
+  const int b = item / nblk, blk = item - b * nblk, bh = b * a.H + hh;
   const int k = blk * 128 + wave * 32 + c;  // this lane's key
   const bool kvalid = k < T;
   const float cs = a.sm_scale * 1.4426950408889634f;
@@ -480,7 +481,7 @@ void launch_f32m_d(int which, const AttnArgs& a, const uint8_t* plan, hipStream_
                        lst(L.dq_list), cnt(L.dq_count), L.nT, L.n_dq_blocks, lst(L.dq_order));
   else
     hipLaunchKernelGGL((k_dkdv_f32m<D>), dim3(bh * unsigned(L.n_dkdv_blocks)), dim3(256), 0, st, a, codes,
-                       lst(L.dkdv_list), cnt(L.dkdv_count), L.nT, L.n_dkdv_blocks);
+                       lst(L.dkdv_list), cnt(L.dkdv_count), L.nT, L.n_dkdv_blocks, lst(L.dkdv_order));
 }
 
 }  // namespace

@@ -70,9 +70,8 @@ int noalloc_workspace(float** out, const char** err);
 // Linear workgroup id -> work index so that each XCD (workgroups are dealt
 // round-robin over the 8 XCDs) receives one contiguous range of work items,
 // i.e. the blocks of the same head share that XCD's L2.  The kernels order
-// work head-major (so every XCD gets the same mix of batch rows): the forward
-// and dQ take each head's (b, block) items in the plan's longest-first work
-// order, the dK/dV kernel by batch row, then block.
+// work head-major (so every XCD gets the same mix of batch rows) and take
+// each head's (b, block) items in the plan's longest-first work order.
 KD_DEV int xcd_remap(int wg, int n) {
   constexpr int NX = 8;
   const int per = n / NX;
