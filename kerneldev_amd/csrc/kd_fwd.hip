@@ -73,9 +73,9 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_fwd(AttnArgs a, const
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, hf = lane >> 5,
             c = lane & 31;
   const int T = a.T, H = a.H;
-  const int work = xcd_remap(blockIdx.x, gridDim.x);
-  const int h = work / (a.B * nQB);  // head-major, then the plan's longest-first order
-  const int item = int(order[work - h * (a.B * nQB)]);
+  int h, rank;  // (fwd_work: per XCD, the plan's longest-first order)
+  fwd_work(blockIdx.x, gridDim.x, a.B * nQB, &h, &rank);
+  const int item = int(order[rank]);
   const int b = item / nQB, qblock = item - b * nQB, bh = b * H + h;
 
   // Q and K as the score product sees them: the 16-bit inputs, or their
