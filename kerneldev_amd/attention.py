@@ -31,7 +31,7 @@ from ._lib import AttnArgs, MetaArgs
 REFERENCE_HEAD_DIMS = (16, 32, 64, 128, 256)  # original_kernel.py:1720
 SUPPORTED_HEAD_DIMS = REFERENCE_HEAD_DIMS
 # bf16 / fp16 at these head dims run on the MFMA kernels with the fused
-# Hadamard epilogues (fp8 scores at 128); 16, 32 and 256 run there without
+# Hadamard epilogues and fp8 scores; 16, 32 and 256 run there without
 # them (16 and 32 on the d = 64 kernels, which read the missing columns as
 # zeros).  fp32
 # inputs run on the fp32 MFMA kernels (kd_f32mma.hip: head dims 32, 64, 128,
@@ -39,6 +39,7 @@ SUPPORTED_HEAD_DIMS = REFERENCE_HEAD_DIMS
 # and head dims 16, 32 (X3_ROUTED_HEAD_DIMS: bf16x3, faster there), and on the
 # fp32 vector-ALU kernels (kd_simt.hip) at 256
 MFMA_HEAD_DIMS = (64, 128)
+FP8_HEAD_DIMS = (64, 128)  # fp8 e4m3 Q K^T (bf16 inputs; fp32 ones are narrowed to bf16 first)
 FP32_PADDED_HEAD_DIMS = {16: 32}
 
 # precision -> arithmetic of P and dS in the kernels.  The reference rounds P
@@ -572,8 +573,8 @@ def flash_attention(
         raise ValueError("flash_attention runs on the GPU only (no CPU fallback)")
     if k.device != q.device or v.device != q.device:
         raise ValueError("q, k and v must be on the same device")
-    if qk_dtype == "fp8_e4m3" and (D != 128 or q.dtype not in (torch.bfloat16, torch.float32)):
-        raise ValueError("the fp8 QK^T path is built for head_dim 128 with bf16 (or fp32) inputs")
+    if qk_dtype == "fp8_e4m3" and (D not in FP8_HEAD_DIMS or q.dtype not in (torch.bfloat16, torch.float32)):
+        raise ValueError(f"the fp8 QK^T path is built for head_dim in {FP8_HEAD_DIMS} with bf16 (or fp32) inputs")
 
     if sm_scale is None:
         sm_scale = D ** -0.5  # original_kernel.py:2145-2147

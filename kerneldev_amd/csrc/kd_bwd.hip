@@ -543,7 +543,7 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
   constexpr bool SP = NSP >= 2, S3 = NSP == 3;
   constexpr int NW = 8;
   using TL = Tile<D, NW>;
-  using TQ8 = Tile<Q8 ? D / 2 : D, NW>;  // fp8 Q tiles (D bytes a row); only used at D = 128
+  using TQ8 = Tile<Q8 ? D / 2 : D, 4>;  // fp8 Q tiles (D bytes a row): their layout (TC8 copies them)
   constexpr int DS = D / 16, DB = D / 32;
   // Tiles are loaded PD steps ahead: 2, or 1 where the fp8 variant's Q8
   // tiles or SP's fp32 P exchange take the LDS.  Slot counts follow from who
@@ -1233,7 +1233,7 @@ template <class E, int D, bool Q8, int NSP>
 static void launch_dkdv_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dkdv_blocks;
-  if constexpr (D == 64) {  // one launch, all four products per wave
+  if constexpr (D == 64 && !Q8) {  // one launch, all four products per wave (fp8 scores: the wave pairs below)
     hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 64, 0>), dim3(grid), dim3(256), 0, st, a,
                        reinterpret_cast<const uint32_t*>(plan + L.codes),
                        reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
@@ -1304,13 +1304,19 @@ int launch_dq(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_
     const int r = fuse_delta ? launch_simt_kernel(1, a, plan, st) : KD_OK;
     return r ? r : launch_simt_kernel(2, a, plan, st);
   }
-  if (a.q8 != nullptr) launch_dq_t<BF16, 128, true>(a, plan, st, fuse_delta);  // fp8 QK^T (checked by the C ABI)
+  if (a.q8 != nullptr) {  // fp8 QK^T: bf16 at head dim 64 or 128 (checked by the C ABI)
+    if (a.D == 64) launch_dq_t<BF16, 64, true>(a, plan, st, fuse_delta);
+    else launch_dq_t<BF16, 128, true>(a, plan, st, fuse_delta);
+  }
   else KD_DISPATCH(launch_dq_t, a, plan, st, fuse_delta);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 int launch_dkdv(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   if (use_simt(a)) return launch_simt_kernel(3, a, plan, st);
-  if (a.q8 != nullptr) launch_dkdv_t<BF16, 128, true>(a, plan, st);  // fp8 QK^T (checked by the C ABI)
+  if (a.q8 != nullptr) {  // fp8 QK^T: bf16 at head dim 64 or 128 (checked by the C ABI)
+    if (a.D == 64) launch_dkdv_t<BF16, 64, true>(a, plan, st);
+    else launch_dkdv_t<BF16, 128, true>(a, plan, st);
+  }
   else KD_DISPATCH(launch_dkdv_t, a, plan, st);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }

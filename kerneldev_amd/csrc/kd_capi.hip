@@ -249,7 +249,7 @@ static int check_fp8(const kd_attn_args* a) {
   if (a->q8 == nullptr) return KD_OK;
   if (a->precision == KD_PREC_SPLIT3)
     return fail(KD_ERR_UNSUPPORTED, "KD_PREC_SPLIT3 is not built with fp8 scores");
-  if (a->D != 128) return fail(KD_ERR_UNSUPPORTED, "the fp8 QK^T path is built for head dim 128");
+  if (a->D != 64 && a->D != 128) return fail(KD_ERR_UNSUPPORTED, "the fp8 QK^T path is built for head dims 64 and 128");
   if (a->dtype != KD_BF16) return fail(KD_ERR_UNSUPPORTED, "the fp8 QK^T path is built for bf16");
   if (!aligned16(a->q8) || !aligned16(a->k8)) return fail(KD_ERR_INVALID, "q8 and k8 must be 16-byte aligned");
   if (a->q_scale == nullptr || a->k_scale == nullptr) return fail(KD_ERR_INVALID, "q_scale and k_scale are required");

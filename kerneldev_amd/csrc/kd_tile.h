@@ -81,8 +81,12 @@ struct Tile {
 
   KD_DEV static int swz(int r) {
     // D = 256: 512-byte rows meet the banks as 256-byte rows do, so the
-    // D = 128 swizzle (low four chunk bits) serves them too
+    // D = 128 swizzle (low four chunk bits) serves them too.  D = 32 (64-byte
+    // rows: the fp8 tiles at head dim 64): the 16 rows a half-wave reads fill
+    // the 256 bytes of banks 4 times over, rows r and r + 4 k sharing their
+    // bank offset, so their chunks are told apart by row bits 2 and 3
     if constexpr (D >= 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+    else if constexpr (D == 32) return (r >> 2) & 3;
     else return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
   }
   // byte offset of (row, 16-byte chunk) inside the tile

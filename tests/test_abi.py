@@ -84,11 +84,14 @@ def test_bad_arguments_return_status_without_gpu():
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID
     assert "overlap" in lib.kd_last_error_string().decode()
     a.q_strides[:] = [1024, 1024, 64]
-    a.q8 = 64  # fp8 operands: q8 without k8, then head dim 64
+    a.q8 = 64  # fp8 operands: q8 without k8, then fp16 inputs (fp8 scores are built for bf16 at 64 / 128)
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID
     assert "q8 and k8" in lib.kd_last_error_string().decode()
     a.k8 = 64
+    a.dtype = _lib.KD_F16
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_UNSUPPORTED
+    assert "bf16" in lib.kd_last_error_string().decode()
+    a.dtype = _lib.KD_BF16
     a.D = 128
     a.q_strides[:] = [1024, 1024, 128]
     a.precision = _lib.KD_PREC_SPLIT3  # the three-part split is not built with fp8 scores

@@ -710,6 +710,30 @@ def test_fp8_random_cases(dev, case):
 
 
 @pytest.mark.parametrize("case", range(8))
+def test_fp8_head_dim_64_cases(dev, case):
+    """fp8 e4m3 scores at head dim 64 (config 5's model: the forward and dQ kernels at
+    D = 64, dK/dV on the wave-pair kernel): seeded B, H, ragged T, causal or
+    cocktail-party metadata, lens, Hadamard on or off, split or single rounding;
+    against the oracle fed the same e4m3 operands."""
+    import random
+
+    rng = random.Random(300 + case)
+    B, H, T = rng.choice([1, 2]), rng.choice([1, 2, 3]), rng.choice([1, 64, 130, 513, 1024, 2048])
+    seed = rng.randrange(1 << 20)
+    q, k, v, do = qkvdo(B, H, T, 64, seed=seed, dtype=torch.bfloat16)
+    inp = dict(name=f"fp8 d64 {case} B{B} H{H} T{T}", q=q, k=k, v=v, do=do, causal=rng.random() < 0.6)
+    if rng.random() < 0.6:
+        _, in_span, span_id, is_prefix = cocktail_batch(B, max(T, 1170), CONFIG3_LAYOUT, seed=seed)
+        inp.update(in_span=in_span[:, :T].contiguous(), span_id=span_id[:, :T].contiguous(),
+                   is_prefix=is_prefix[:, :T].contiguous())
+    kw = {}
+    if rng.random() < 0.3:
+        kw["lens"] = torch.tensor([rng.randint(0, T) for _ in range(B)], dtype=torch.int32)
+    _case(inp, dev, qk_dtype="fp8_e4m3", hadamard=rng.random() < 0.5, hadamard_seed=case % 5,
+          precision=rng.choice(["tf32", "bf16"]), **kw)
+
+
+@pytest.mark.parametrize("case", range(8))
 def test_strided_layouts_random(dev, case):
     """q, k, v and dO as views of larger buffers: rows padded (t-stride d + 0 / 8 / 24) and
     [B, T, H, d] or [B, H, T, d] memory, chosen per tensor; seeded B, H, ragged T, head dim and
