@@ -385,6 +385,20 @@ def test_lens_and_fully_masked_rows(dev, D):
     assert (got["dq"][2] == 0).all() and (got["dk"][2] == 0).all() and (got["dv"][2] == 0).all()
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_wide_batch_small_rows(dev, D):
+    """Many batch rows of short cocktail-party sequences with ragged lens: B = 200
+    on the plan's batch grid dimension and in every work order (B nb items per
+    head), each head checked against the oracle."""
+    B, H, T = 200, 2, 70
+    _, in_span, span_id, is_prefix = cocktail_batch(B, 1170, CONFIG3_LAYOUT, seed=21)
+    q, k, v, do = qkvdo(B, H, T, D, seed=22)
+    g = torch.Generator().manual_seed(23)
+    lens = torch.randint(0, T + 1, (B,), generator=g, dtype=torch.int32)
+    _case(dict(name=f"wide batch D{D}", q=q, k=k, v=v, do=do, in_span=in_span[:, :T].contiguous(),
+               span_id=span_id[:, :T].contiguous(), is_prefix=is_prefix[:, :T].contiguous()), dev, lens=lens)
+
+
 def test_attention_mask_without_metadata_is_causal(dev):
     q, k, v, do = qkvdo(1, 2, 192, 64, seed=9)
     am = torch.ones(1, 192, 192, dtype=torch.bool, device=dev)
