@@ -142,6 +142,26 @@ def test_plan_spans_across_rounds(dev):
     _check_plan(p, dense_mask(T, in_span=in_span, span_id=span_id, is_prefix=is_prefix))
 
 
+@pytest.mark.parametrize("rule", ["collate", "fallback"])
+def test_plan_from_tokens_long_row(dev, rule):
+    """Token rows longer than the codes kernel's 8192-token round: a well-formed
+    cocktail-party row (config 4's layout, collate rule) and a random row over the
+    special ids (fallback rule), against the oracle's metadata, mask and tiles."""
+    T = 8192 + 500
+    if rule == "collate":
+        tokens, _, _, _ = cocktail_batch(1, T, CONFIG4_LAYOUT, seed=41)
+    else:
+        rng = np.random.default_rng(42)
+        tokens = torch.from_numpy(rng.choice(np.array([0, 1, 2, 3, 4, 5, 40, 41, 42]), size=(1, T),
+                                             p=[.1, .01, .01, .03, .03, .01, .35, .38, .08]))
+    print(f"plan from tokens, long row, rule={rule} T={T}", flush=True)
+    got = build_plan_from_tokens(tokens.to(dev), 64, rule=rule)
+    torch.cuda.synchronize()
+    in_span, span_id, is_prefix = ORACLE_RULES[rule](tokens.numpy())
+    _check_plan(_views(got.tensor, 1, T, 64),
+                dense_mask(T, B=1, in_span=in_span, span_id=span_id, is_prefix=is_prefix))
+
+
 def test_plan_strided_metadata(dev):
     rng = np.random.default_rng(11)
     T = 333
