@@ -285,10 +285,10 @@ class Step:
             out.append(("rot_qk", rot))
         if self.fp8:
             def quant():
-                if not self.hadamard:  # the per-(b, h) absmax (exact: the max of 16-bit magnitudes)
-                    q, k = self.inputs[:2]
-                    self.amax[0].copy_(self.torch.amax(q.abs(), dim=(2, 3)))
-                    self.amax[1].copy_(self.torch.amax(k.abs(), dim=(2, 3)))
+                if not self.hadamard:  # the per-(b, h) absmax; with Hadamard the rotation pass gives it
+                    for i, qa in enumerate(self.quant):
+                        ck(L.kd_absmax(ctypes.byref(qa), ctypes.c_void_p(self.amax[i].data_ptr()), self.sptr),
+                           "absmax")
                 for qa in self.quant:
                     ck(L.kd_quant_fp8(ctypes.byref(qa), self.sptr), "quant")
             out.append(("quant", quant))

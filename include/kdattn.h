@@ -314,6 +314,13 @@ int kd_hadamard(const kd_rot_args *a, void *stream);
  * which has no fp8 path; the operation is specified by the build. */
 int kd_quant_fp8(const kd_quant_args *a, void *stream);
 
+/* amax[b H + h] = max |x| over (t, d) of the bf16 / fp16 [B, H, T, D] tensor
+ * a->x (a->x_strides; the other fields of a are not read), exact in fp32, for
+ * kd_quant_fp8 when no rotation pass (kd_hadamard with amax) produced it.
+ * Every element of amax is written; nothing needs to be zeroed first.  No
+ * counterpart in the reference, which has no fp8 path. */
+int kd_absmax(const kd_quant_args *a, float *amax, void *stream);
+
 /* Cocktail-party head forward: span_lo/hi, mask_pos, h_ctx, h_spans and
  * scores.  Replaces the Python double loop and einsum of GPTModel.forward
  * (model.py:263-298). */

@@ -121,6 +121,7 @@ SIGNATURES = {
     "kd_plan_build_tokens": (c_int, [POINTER(TokenArgs), c_void_p, c_int64, c_void_p]),
     "kd_hadamard": (c_int, [POINTER(RotArgs), c_void_p]),
     "kd_quant_fp8": (c_int, [POINTER(QuantArgs), c_void_p]),
+    "kd_absmax": (c_int, [POINTER(QuantArgs), c_void_p, c_void_p]),
     "kd_plan_bytes": (c_int64, [c_int32, c_int32, c_int32]),
     "kd_plan_layout": (c_int, [c_int32, c_int32, c_int32, POINTER(c_int64)]),
     "kd_plan_build": (c_int, [POINTER(MetaArgs), c_void_p, c_int64, c_void_p]),

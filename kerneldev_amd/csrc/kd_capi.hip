@@ -192,6 +192,19 @@ int kd_quant_fp8(const kd_quant_args* a, void* stream) {
   return r ? fail(r, "kernel launch failed (quant)") : KD_OK;
 }
 
+int kd_absmax(const kd_quant_args* a, float* amax, void* stream) {
+  if (a == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
+  if (a->B < 1 || a->H < 1 || a->T < 1) return fail(KD_ERR_INVALID, "B, H and T must be >= 1");
+  if (a->D != 16 && a->D != 32 && a->D != 64 && a->D != 128 && a->D != 256)
+    return fail(KD_ERR_UNSUPPORTED, "head dim must be 16, 32, 64, 128 or 256");
+  if (a->dtype != KD_BF16 && a->dtype != KD_F16) return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16 or fp16");
+  if (amax == nullptr) return fail(KD_ERR_INVALID, "amax is required");
+  int r;
+  if ((r = check_tensor(a->x, a->x_strides, "x", a->T, a->D))) return r;
+  r = kd::launch_absmax(*a, amax, as_stream(stream));
+  return r ? fail(r, "kernel launch failed (absmax)") : KD_OK;
+}
+
 int kd_hadamard(const kd_rot_args* a, void* stream) {
   if (a == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
   if (a->B < 1 || a->H < 1 || a->T < 1) return fail(KD_ERR_INVALID, "B, H and T must be >= 1");

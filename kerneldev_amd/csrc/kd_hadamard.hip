@@ -208,6 +208,57 @@ __global__ __launch_bounds__(256) void k_quant8(kd_quant_args a) {
   *reinterpret_cast<u32x2*>(yp) = u32x2{w[0], w[1]};
 }
 
+// ---- per-(b, h) max |x| -----------------------------------------------------
+// One 1024-thread workgroup per (b, h) reads its T x D slice in 16-byte
+// chunks (8 elements), four chunks in flight per thread.  The magnitudes of
+// non-negative bf16 / fp16 values order as their bit patterns do, so the
+// reduction runs on 15-bit integers (the sign bit cleared) and the maximum is
+// converted to fp32 once: exact, and independent of the order of the fold.
+// Written straight to amax[b H + h] (no zeroing, no atomics).
+template <class E>
+__global__ __launch_bounds__(1024) void k_absmax(kd_quant_args a, float* __restrict__ amax) {
+  const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H, tid = threadIdx.x;
+  const int cpr = a.D / 8;  // 16-byte chunks per row
+  const int64_t n = int64_t(a.T) * cpr;
+  const uint16_t* base = static_cast<const uint16_t*>(a.x) + b * a.x_strides[0] + h * a.x_strides[1];
+  uint32_t m = 0;
+  auto fold = [&](const u32x4& v) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = max(m, max(v[j] & 0x7FFFu, (v[j] >> 16) & 0x7FFFu));
+  };
+  auto chunk = [&](int64_t i) {
+    const int64_t t = i / cpr;
+    const int c = int(i - t * cpr);
+    return *reinterpret_cast<const u32x4*>(base + t * a.x_strides[2] + c * 8);
+  };
+  int64_t i = tid;
+  for (; i + 3 * 1024 < n; i += 4 * 1024) {
+    const u32x4 v0 = chunk(i), v1 = chunk(i + 1024), v2 = chunk(i + 2048), v3 = chunk(i + 3072);
+    fold(v0);
+    fold(v1);
+    fold(v2);
+    fold(v3);
+  }
+  for (; i < n; i += 1024) fold(chunk(i));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = max(m, uint32_t(__shfl_xor(int(m), off, 64)));
+  __shared__ uint32_t s_m[16];
+  if ((tid & 63) == 0) s_m[tid >> 6] = m;
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t r = 0;
+    for (int w = 0; w < 16; ++w) r = max(r, s_m[w]);
+    amax[bh] = to_f32<E>(uint16_t(r));
+  }
+}
+
+int launch_absmax(const kd_quant_args& a, float* amax, hipStream_t st) {
+  const dim3 grid(unsigned(int64_t(a.B) * a.H)), block(1024);
+  if (a.dtype == KD_BF16) hipLaunchKernelGGL(k_absmax<BF16>, grid, block, 0, st, a, amax);
+  else hipLaunchKernelGGL(k_absmax<F16>, grid, block, 0, st, a, amax);
+  return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
+}
+
 template <class E, int D>
 static void launch_quant_t(const kd_quant_args& a, hipStream_t st) {
   constexpr int RPB = 256 / (D / 8);

@@ -53,6 +53,7 @@ int launch_dq(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_
 int launch_dkdv(const AttnArgs& a, const uint8_t* plan, hipStream_t st);
 int launch_hadamard(const kd_rot_args& a, hipStream_t st);
 int launch_quant(const kd_quant_args& a, hipStream_t st);
+int launch_absmax(const kd_quant_args& a, float* amax, hipStream_t st);
 int launch_span(const kd_span_args& a, hipStream_t st);
 int launch_span_bwd(const kd_span_args& a, hipStream_t st);
 // fp32 vector-ALU attention (kd_simt.hip) for fp32 inputs and head dims the

@@ -129,6 +129,28 @@ def _quant_fake(x, amax):
             torch.empty(x.shape[:2], dtype=torch.float32, device=x.device))
 
 
+@torch.library.custom_op("kdattn::absmax", mutates_args=(), device_types=("cuda",))
+def _absmax_op(x: torch.Tensor) -> torch.Tensor:
+    """max |x| per (b, h) of a bf16 / fp16 [B, H, T, d] tensor (kd_absmax), exact in fp32."""
+    from .attention import _dtype_code, _kernel_ready
+
+    x = _kernel_ready(x)
+    B, H, T, D = x.shape
+    amax = torch.empty((B, H), dtype=torch.float32, device=x.device)
+    a = QuantArgs()
+    a.x, a.x_strides = x.data_ptr(), _strides3(x)
+    a.B, a.H, a.T, a.D = B, H, T, D
+    a.dtype = _dtype_code(x.dtype)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+    _lib.check(_lib.load().kd_absmax(ctypes.byref(a), ctypes.c_void_p(amax.data_ptr()), stream), "kd_absmax")
+    return amax
+
+
+@_absmax_op.register_fake
+def _absmax_fake(x):
+    return torch.empty(x.shape[:2], dtype=torch.float32, device=x.device)
+
+
 def _check(x: torch.Tensor, signs: torch.Tensor):
     if x.dim() != 4:
         raise ValueError("x must be [batch, heads, time, head_dim]")
@@ -160,7 +182,7 @@ def quantize_fp8(x: torch.Tensor, amax: torch.Tensor | None = None):
 
     ``x8 = e4m3(clamp(x * fp32(448 / amax), -448, 448))`` with round to nearest
     even, ``scale = amax / 448`` (``amax == 0``: both factors are 1), so that
-    ``x ~= scale * x8``.  ``amax`` defaults to ``max |x|`` per (b, h).  Returns
+    ``x ~= scale * x8``.  ``amax`` defaults to ``max |x|`` per (b, h) (kd_absmax).  Returns
     ``(x8 as uint8 bytes [B, H, T, d], scale fp32 [B, H])``; not differentiable.
     """
     if x.dim() != 4 or x.dtype not in (torch.bfloat16, torch.float16) or not x.is_cuda:
@@ -168,7 +190,7 @@ def quantize_fp8(x: torch.Tensor, amax: torch.Tensor | None = None):
     if x.shape[-1] not in (64, 128):
         raise ValueError(f"head_dim must be 64 or 128, got {x.shape[-1]}")
     if amax is None:
-        amax = x.detach().abs().amax(dim=(2, 3)).float()
+        amax = _absmax_op(x.detach())
     if amax.shape != x.shape[:2] or amax.dtype != torch.float32 or amax.device != x.device:
         raise ValueError("amax must be float32 [batch, heads] on x's device")
     return _quant_op(x.detach(), amax.detach())

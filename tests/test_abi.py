@@ -127,6 +127,13 @@ def test_bad_arguments_return_status_without_gpu():
     assert lib.kd_quant_fp8(ctypes.byref(qa), null) == _lib.KD_ERR_INVALID  # amax / scale / y missing
     qa.D = 96
     assert lib.kd_quant_fp8(ctypes.byref(qa), null) == _lib.KD_ERR_UNSUPPORTED
+    buf = ctypes.c_void_p(256)  # never dereferenced on the host
+    assert lib.kd_absmax(ctypes.byref(qa), buf, null) == _lib.KD_ERR_UNSUPPORTED  # head dim 96
+    qa.D, qa.dtype = 64, _lib.KD_F32
+    assert lib.kd_absmax(ctypes.byref(qa), buf, null) == _lib.KD_ERR_UNSUPPORTED  # 16-bit inputs only
+    qa.dtype = _lib.KD_BF16
+    assert lib.kd_absmax(ctypes.byref(qa), null, null) == _lib.KD_ERR_INVALID  # amax missing
+    assert lib.kd_absmax(ctypes.byref(qa), buf, null) == _lib.KD_ERR_INVALID  # x missing
     m = _lib.MetaArgs()
     m.B, m.T, m.mode = 1, 8, 7
     assert lib.kd_plan_build(ctypes.byref(m), ctypes.c_void_p(256), BIG, null) == _lib.KD_ERR_INVALID

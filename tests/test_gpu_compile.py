@@ -14,7 +14,7 @@ import torch
 
 from kerneldev_amd import flash_attention, generate_hadamard_signs
 from kerneldev_amd.attention import _bwd_op, _bwd_x3_op, _fwd_op, _fwd_x3_op, _lib
-from kerneldev_amd.hadamard import _quant_op, _rot_op
+from kerneldev_amd.hadamard import _absmax_op, _quant_op, _rot_op
 from kerneldev_amd.synth import CONFIG3_LAYOUT, cocktail_batch, qkvdo
 
 pytestmark = pytest.mark.gpu
@@ -58,6 +58,8 @@ def test_opcheck_rotation_and_quantiser_ops(dev):
     amax = q.float().abs().amax(dim=(2, 3)).contiguous()
     print("opcheck kdattn::quant", flush=True)
     torch.library.opcheck(_quant_op, (q, amax))
+    print("opcheck kdattn::absmax", flush=True)
+    torch.library.opcheck(_absmax_op, (q,))
 
 
 def _fwd_bwd(fn, q, k, v, do, meta):

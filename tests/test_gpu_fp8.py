@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from kerneldev_amd import generate_hadamard_signs
-from kerneldev_amd.hadamard import hadamard_absmax, quantize_fp8
+from kerneldev_amd.hadamard import _absmax_op, hadamard_absmax, quantize_fp8
 from kerneldev_amd.synth import config_inputs
 from oracle import fp8 as ref_fp8
 from oracle import hadamard as ref_h
@@ -31,6 +31,26 @@ def _check(x_cpu, got8, got_scale, amax=None):
     bad = int((g8 != want8).sum())
     assert bad == 0, f"{bad} of {g8.size} e4m3 bytes differ"
     assert np.array_equal(got_scale.cpu().numpy(), want_scale)
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_absmax_exact(dev, D, dtype):
+    """kd_absmax (quantize_fp8's default amax) equals torch's max |x| per (b, h) exactly,
+    on ragged T, an all-zero head, a negative outlier, and a strided [B, T, H, d] view."""
+    print(f"absmax D={D} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(D + 7)
+    x = torch.randn(3, 4, 1037, D, generator=g).to(dtype)
+    x[0, 1] = 0
+    x[2, 3, 1000, D - 1] = -300.0
+    got = _absmax_op(x.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), x.float().abs().amax(dim=(2, 3)))
+    base = torch.randn(2, 333, 3, D, generator=g).to(dtype)
+    view = base.to(dev).transpose(1, 2)
+    got = _absmax_op(view)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), base.transpose(1, 2).float().abs().amax(dim=(2, 3)))
 
 
 @pytest.mark.parametrize("D", [64, 128])
