@@ -22,7 +22,7 @@
  *     run on the MFMA kernels at every head dim (16 and 32 on the D = 64
  *     kernels, which read the columns past D as zeros and store only the D
  *     real ones; dqk_signs at 64, 128 only; fp8 scores at 64, 128 for bf16); fp32 inputs at
- *     D = 32, 64, 128 on the fp32 MFMA kernels, at D = 16, 256 on fp32
+ *     D = 32, 64, 128, 256 on the fp32 MFMA kernels, at D = 16 on fp32
  *     vector-ALU kernels.  fp32 inputs get no fp8 scores and no dqk_signs,
  *     and precision is always full fp32 for them.  (The Python layer runs fp32 inputs at precision "tf32"
  *     and D = 16, 32 as bf16 operands of three times the head dim on the

@@ -12,8 +12,8 @@ shim over the C ABI of ``libkdattn.so``:
 * ``kdattn::fwd_x3`` / ``kdattn::bwd_x3`` -> the 16-bit kernels for fp32
   inputs at precision "tf32" and head dims 16 and 32, as three bf16 products
   per product (see X3_HEAD_DIMS).  Other fp32 inputs go through ``kdattn::fwd``
-  / ``::bwd`` to the fp32 MFMA kernels (head dims 32, 64, 128; 16 zero-padded
-  to 32) or the fp32 vector-ALU kernels (256).
+  / ``::bwd`` to the fp32 MFMA kernels (head dims 32, 64, 128, 256; 16
+  zero-padded to 32).
 
 There is no CPU or PyTorch fallback: a missing library raises.
 """
@@ -35,9 +35,9 @@ SUPPORTED_HEAD_DIMS = REFERENCE_HEAD_DIMS
 # them (16 and 32 on the d = 64 kernels, which read the missing columns as
 # zeros).  fp32
 # inputs run on the fp32 MFMA kernels (kd_f32mma.hip: head dims 32, 64, 128,
-# and 16 zero-padded to 32, FP32_PADDED_HEAD_DIMS), except at precision "tf32"
-# and head dims 16, 32 (X3_ROUTED_HEAD_DIMS: bf16x3, faster there), and on the
-# fp32 vector-ALU kernels (kd_simt.hip) at 256
+# and 16 zero-padded to 32, FP32_PADDED_HEAD_DIMS; kd_f32w.hip: 256), except
+# at precision "tf32" and head dims 16, 32 (X3_ROUTED_HEAD_DIMS: bf16x3,
+# faster there)
 MFMA_HEAD_DIMS = (64, 128)
 FP8_HEAD_DIMS = (64, 128)  # fp8 e4m3 Q K^T (bf16 inputs; fp32 ones are narrowed to bf16 first)
 FP32_PADDED_HEAD_DIMS = {16: 32}
@@ -522,8 +522,8 @@ def flash_attention(
     once to the input type instead (faster; 8 significant bits with bf16
     inputs).  fp32
     inputs get fp32 arithmetic at both "ieee" and "tf32": the fp32 MFMA
-    kernels at head dims 32, 64, 128 (16 zero-padded to 32) and the fp32
-    vector-ALU kernels at 256, except "tf32" at 16 and 32, which runs as bf16x3
+    kernels at head dims 32, 64, 128, 256 (16 zero-padded to 32), except
+    "tf32" at 16 and 32, which runs as bf16x3
     on the 16-bit kernels (see head_dim_route).  O and the gradients stay fp32.
     ``attention_mask``'s contents are not
     read, exactly as in the reference: when it is given without metadata the

@@ -486,9 +486,12 @@ void launch_f32m_d(int which, const AttnArgs& a, const uint8_t* plan, hipStream_
 
 }  // namespace
 
-bool use_f32mma(const AttnArgs& a) { return a.dtype == KD_F32 && (a.D == 32 || a.D == 64 || a.D == 128); }
+bool use_f32mma(const AttnArgs& a) {
+  return a.dtype == KD_F32 && (a.D == 32 || a.D == 64 || a.D == 128 || a.D == 256);
+}
 
 int launch_f32mma(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
+  if (a.D == 256) return launch_f32w(which, a, plan, st);  // the 16 x 16 form (kd_f32w.hip)
   switch (a.D) {
     case 32: launch_f32m_d<32>(which, a, plan, st); break;
     case 64: launch_f32m_d<64>(which, a, plan, st); break;

@@ -265,11 +265,11 @@ def test_fp32_tf32_ops_directly(dev, D):
         assert torch.equal(run_gpu(inp, dev)["lse"], lse)
 
 
-@pytest.mark.parametrize("D", [16, 32, 64, 128])
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 def test_fp32_on_the_fp32_mfma_kernels(dev, D):
-    """fp32 inputs at precision "ieee" run on the fp32 MFMA kernels (kd_f32mma.hip)
-    at head dims 32, 64, 128 (16 zero-padded to 32), and so does "tf32" at 64 and
-    128: ragged T with lens (an
+    """fp32 inputs at precision "ieee" run on the fp32 MFMA kernels (kd_f32mma.hip
+    at head dims 32, 64, 128, 16 zero-padded to 32; kd_f32w.hip at 256), and so
+    does "tf32" at 64, 128 and 256: ragged T with lens (an
     empty batch row, a partial one), [B, T, H, D] memory viewed [B, H, T, D]
     (model.py:76-78) with cocktail-party metadata; rel-RMS <= 1e-5 against the
     fp64 oracle, exact zeros where nothing is allowed."""
@@ -303,10 +303,10 @@ def test_fp32_on_the_fp32_mfma_kernels(dev, D):
                     f"strided D={D} {precision}")
 
 
-@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("D", [32, 64, 256])
 def test_fp32_tf32_lens_hadamard_and_bthd(dev, D):
     """fp32 at precision "tf32" on the bf16x3 path (d = 32) and on the fp32 MFMA
-    kernels (d = 64) with lens (fully masked rows: O = 0, LSE = -inf, zero
+    kernels (d = 64, 256) with lens (fully masked rows: O = 0, LSE = -inf, zero
     gradients), with the Hadamard rotation, and with out_layout="bthd"."""
     q, k, v, do = qkvdo(3, 2, 300, D, seed=12, dtype=torch.float32)
     lens = torch.tensor([300, 129, 0], dtype=torch.int32)
