@@ -49,7 +49,7 @@ extern "C" {
 /* element dtypes */
 #define KD_BF16 0
 #define KD_F16 1
-#define KD_F32 2 /* attention only: computed in fp32 (fp32 MFMA at D = 32, 64, 128) */
+#define KD_F32 2 /* attention only: computed in fp32 (fp32 MFMA at D = 32, 64, 128, 256) */
 /* arithmetic of the softmax weights P and the score gradients dS inside the
  * attention kernels (kd_attn_args.precision) */
 #define KD_PREC_SPLIT 0  /* P and dS enter their products (P V, dV, dQ, dK) as a 16-bit pair

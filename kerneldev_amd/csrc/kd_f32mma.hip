@@ -1,7 +1,9 @@
 // Attention for fp32 inputs on the fp32 matrix cores (v_mfma_f32_32x32x2_f32):
 // the reference's fp32 dots (original_kernel.py:452, :569, :1239, :1331-1333,
-// :1425, :1517-1523) with fp32 operands and fp32 accumulation, at head dims
-// 32, 64 and 128.  Same algebra, plan, lists and masks as the 16-bit kernels:
+// :1425, :1517-1523) with fp32 operands and fp32 accumulation, at head dim 32
+// (and 16, zero-padded to 32 by the Python layer; head dims 64, 128 and 256
+// run on the 16 x 16 form of kd_f32w.hip).  The kernels are templates over the
+// head dim and were built for 64 and 128 too.  Same algebra, plan, lists and masks as the 16-bit kernels:
 //   forward   O = softmax2(S c) V, LSE2 = m + log2 l      (:279-626)
 //   dQ        P = exp2(S c - LSE), dS = P (dP - Delta), dQ = sm_scale dS K  (:1173-1336)
 //   dK / dV   dV = P^T dO, dK = sm_scale dS^T Q            (:1339-1525)
@@ -490,13 +492,11 @@ bool use_f32mma(const AttnArgs& a) {
   return a.dtype == KD_F32 && (a.D == 32 || a.D == 64 || a.D == 128 || a.D == 256);
 }
 
+// Head dim 32 here; 64, 128 and 256 on the 16 x 16 form (kd_f32w.hip), which
+// runs them 5-16% faster (d = 64, 128) and fits 256 at all.
 int launch_f32mma(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
-  if (a.D == 256) return launch_f32w(which, a, plan, st);  // the 16 x 16 form (kd_f32w.hip)
-  switch (a.D) {
-    case 32: launch_f32m_d<32>(which, a, plan, st); break;
-    case 64: launch_f32m_d<64>(which, a, plan, st); break;
-    default: launch_f32m_d<128>(which, a, plan, st); break;
-  }
+  if (a.D != 32) return launch_f32w(which, a, plan, st);
+  launch_f32m_d<32>(which, a, plan, st);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 

@@ -1,22 +1,23 @@
-// Attention for fp32 inputs at head dim 256 on the fp32 matrix cores
-// (v_mfma_f32_16x16x4f32): the reference's fp32 dots (original_kernel.py:452,
-// :569, :1239, :1331-1333, :1425, :1517-1523) at HEAD_DIM 256 (:1720), fp32
-// operands and fp32 accumulation.  Same algebra, plan, lists and masks as the
-// head-dim 32-128 kernels of kd_f32mma.hip:
+// Attention for fp32 inputs on the fp32 matrix cores in their 16 x 16 x 4
+// form (v_mfma_f32_16x16x4f32), for head dims WD = 64, 128 and 256: the
+// reference's fp32 dots (original_kernel.py:452, :569, :1239, :1331-1333,
+// :1425, :1517-1523) for HEAD_DIM in {64, 128, 256} (:1720), fp32 operands and
+// fp32 accumulation.  Same algebra, plan, lists and masks as the 32 x 32 x 2
+// kernels of kd_f32mma.hip:
 //   forward   O = softmax2(S c) V, LSE2 = m + log2 l      (:279-626)
 //   dQ        P = exp2(S c - LSE), dS = P (dP - Delta), dQ = sm_scale dS K  (:1173-1336)
 //   dK / dV   dV = P^T dO, dK = sm_scale dS^T Q            (:1339-1525)
 // with c = sm_scale log2(e) folded into the register-resident Q (forward, dQ)
 // or K (dK/dV).  Delta comes from k_delta_simt (kd_simt.hip).
 //
-// Why a 16 x 16 product.  With 32 tokens per wave (the 32 x 32 x 2 form of
-// the smaller head dims) a lane holds 128 floats of each register row and 128
-// accumulators at d = 256, more than one wave's registers once the compiler's
-// copies are counted.  With 16 tokens per wave a register row is 64 floats a
-// lane and a [256 x 16] accumulator 64, so the forward holds ~150 values, dQ
-// ~240 and dK/dV ~310, within one wave per SIMD (512 registers).  The 16 x 16
-// x 4 form runs at the same rate as the 32 x 32 x 2 one (2048 FLOP in 8
-// passes against 4096 in 16).
+// Why a 16 x 16 product.  With 32 tokens per wave (the 32 x 32 x 2 form) a
+// lane holds WD / 2 floats of each register row and WD / 2 accumulators per
+// output; at WD = 256 that is more than one wave's registers once the
+// compiler's copies are counted.  With 16 tokens per wave a register row is
+// WD / 4 floats a lane and a [WD x 16] accumulator WD / 4, so at WD = 256 the
+// forward holds ~150 values, dQ ~240 and dK/dV ~310, within one wave per SIMD
+// (512 registers).  The 16 x 16 x 4 form runs at the same rate as the 32 x 32
+// x 2 one (2048 FLOP in 8 passes against 4096 in 16).
 //
 // The MFMA.  D[16 x 16] += A[16 x 4] B[4 x 16]: lane l (i = l % 16, g = l / 16)
 // supplies A[i][g] and B[g][i], and register r of the result holds D[4 g + r][i].
@@ -34,56 +35,73 @@
 //   * over the chunk's tokens, k-step (kb, r) contracts token 16 kb + 4 g + r
 //     on lane group g, which is where register r of score block kb already
 //     holds it: the scores are the B operand as they stand;
-//   * output block db (of 16) row 4 g + r is head-dim column 16 (4 g + r) + db,
-//     so a lane's A reads for the 16 blocks of one k-step are 16 consecutive
-//     floats of one row (four 16-byte reads).
+//   * output block db (of NDB = WD / 16) row 4 g + r is head-dim column
+//     NDB (4 g + r) + db, so a lane's A reads for the NDB blocks of one k-step
+//     are NDB consecutive floats of one row (NDB / 4 16-byte reads).
 //
 // Workgroup: 4 waves x 16 tokens = one 64-token member of a 128-token plan
 // block (workgroups 2 w and 2 w + 1 take the two members of block w), blocks
 // head-major (xcd_remap) and in the plan's longest-first order.  A member
 // whose class is EMPTY for a list entry skips it altogether (no copy, no
-// product).  The entry's 64 tokens are streamed as two 32-row chunks (32 KiB
-// of fp32 rows each), copied global -> LDS by buffer_load ... lds one chunk
-// ahead into two slots: 128 KiB for the two streamed operands.
+// product).  The entry's 64 tokens are streamed as two 32-row chunks (32 WD
+// fp32 values each: 32 KiB at WD = 256), copied global -> LDS by
+// buffer_load ... lds one chunk ahead into two slots.
 //
-// LDS layout of a chunk row (1 KiB = 64 chunks of 16 bytes): logical chunk c
-// of row r sits at c ^ (r & 15) ^ ((c >> 4) & 3).  Both read patterns are
-// bank-conflict free: (a) 16 lanes read one chunk of 16 different rows (the
-// r & 15 term spreads them over all 64 banks), (b) 16 lanes read chunks 4 i + j
-// (i = 0..15, fixed j) of one row (the (c >> 4) & 3 term does).
+// LDS layout of a chunk row (CPR = WD / 4 chunks of 16 bytes): logical chunk
+// c of row r sits at c ^ (r & 15) ^ ((c >> 4) & (CPR / 16 - 1)).  Both read
+// patterns are bank-conflict free: (a) 16 lanes read one chunk of 16
+// different rows (the r & 15 term spreads them over all 64 banks), (b) 16
+// lanes read chunks (NDB / 4) i + j (i = 0..15, fixed j) of one row (the
+// (c >> 4) term does, where those chunks span more than 256 bytes).
 #include "kd_tile.h"
 
 namespace kd {
 namespace {
 
-constexpr int WD = 256;             // head dim
-constexpr int CH = 32;              // rows per streamed chunk
-constexpr int CROWB = WD * 4;       // bytes per chunk row
-constexpr int CBYTES = CH * CROWB;  // 32 KiB
-constexpr int NDB = WD / 16;        // 16 output blocks of 16 columns
-constexpr int NR = WD / 4;          // 64 floats of a register row per lane
+constexpr int CH = 32;  // rows per streamed chunk
+
+template <int WD>
+struct Geo {
+  static constexpr int CROWB = WD * 4;        // bytes per chunk row
+  static constexpr int CBYTES = CH * CROWB;   // bytes per chunk
+  static constexpr int CPR = WD / 4;          // 16-byte chunks per row
+  static constexpr int NDB = WD / 16;         // output blocks of 16 rows
+  static constexpr int NR = WD / 4;           // floats of a register row per lane
+  static constexpr int RPL = 1024 / CROWB;    // rows per wave-wide 1 KiB load
+  static constexpr int LPW = CH / RPL / 4;    // such loads per wave and chunk
+  static constexpr int HMASK = CPR / 16 - 1;  // chunk bits above the low four, folded in
+  // workgroups per CU the kernels are built for (1: up to 512 registers a
+  // wave; the LDS of two chunk slots of two operands, 4 CBYTES, allows 1, 2, 4)
+  static constexpr int WAVES = WD == 256 ? 1 : WD == 128 ? 2 : 3;
+  static_assert(WD == 64 || WD == 128 || WD == 256, "head dims 64, 128, 256");
+  // byte offset of logical 16-byte chunk c of chunk row r
+  KD_DEV static int cat(int r, int c) { return r * CROWB + ((c ^ (r & 15) ^ ((c >> 4) & HMASK)) << 4); }
+};
 
 KD_DEV f32x4 mma16(float a, float b, const f32x4& c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 
-// byte offset of logical 16-byte chunk c of chunk row r
-KD_DEV int cat(int r, int c) { return r * CROWB + ((c ^ (r & 15) ^ ((c >> 4) & 3)) << 4); }
-
-// This wave's share (8 of the 32 rows) of the copy of rows r0 .. r0 + 31 of
-// an fp32 [T, row_bytes] slice into an LDS chunk: one wave-wide 16-byte-per-
-// lane load per row, lane l filling chunk position l of the row, i.e. the
-// logical chunk whose position is l.  Rows at or past T read as zeros.
+// This wave's share of the copy of rows r0 .. r0 + 31 of an fp32
+// [T, row_bytes] slice into an LDS chunk: wave-wide 16-byte-per-lane loads of
+// 1 KiB (RPL rows each), lane l filling chunk position l % CPR of row
+// l / CPR of its load, i.e. the logical chunk whose position that is.  Rows
+// at or past T read as zeros.
+template <int WD>
 KD_DEV void copy_chunk(const u32x4& rs, uint32_t r0, uint32_t row_bytes, uint32_t lds_chunk, int wave, int lane) {
+  using G = Geo<WD>;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int rr = 8 * wave + j;
-    const int c = (lane & 48) | ((lane & 15) ^ (rr & 15) ^ ((lane >> 4) & 3));
-    const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_chunk + uint32_t(rr) * CROWB)));
+  for (int j = 0; j < G::LPW; ++j) {
+    const int ld = G::LPW * wave + j;                   // load index within the chunk
+    const int rr = ld * G::RPL + lane / G::CPR, p = lane % G::CPR;  // row, position
+    const int c = (p & ~15) | ((p & 15) ^ (rr & 15) ^ ((p >> 4) & G::HMASK));
+    const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_chunk + uint32_t(ld) * 1024u)));
     dma_b128(rs, (r0 + uint32_t(rr)) * row_bytes + uint32_t(c) * 16u, m);
   }
 }
 
 // this lane's row x[row][.] in k-step order: out[4u + t] = x[row][16u + 4g + t] * scale
-KD_DEV void load_row16(const float* base, int64_t row_stride, int row, bool valid, int g, float scale, float (&out)[NR]) {
+template <int WD>
+KD_DEV void load_row16(const float* base, int64_t row_stride, int row, bool valid, int g, float scale,
+                       float (&out)[Geo<WD>::NR]) {
   const float* p = base + int64_t(valid ? row : 0) * row_stride + 4 * g;  // row 0 stands in past T
   const float sc = valid ? scale : 0.f;
 #pragma unroll
@@ -98,10 +116,10 @@ KD_DEV void load_row16(const float* base, int64_t row_stride, int row, bool vali
 // register r of the result = sum_d chunk[16 kb + 4 g + r][d] reg-row[d].  Both
 // blocks at once (two independent chains); each 16-byte read is issued one
 // group of four k-steps ahead of its MFMAs.
-KD_DEV void score_pair(const uint8_t* chunk, int i, int g, const float (&reg)[NR], f32x4 (&s)[2]) {
+template <int WD>
+KD_DEV void score_pair(const uint8_t* chunk, int i, int g, const float (&reg)[Geo<WD>::NR], f32x4 (&s)[2]) {
   s[0] = s[1] = f32x4{};
-  const uint8_t* row0 = chunk + 0;
-  auto rd = [&](int kb, int u) { return *reinterpret_cast<const f32x4*>(row0 + cat(16 * kb + i, 4 * u + g)); };
+  auto rd = [&](int kb, int u) { return *reinterpret_cast<const f32x4*>(chunk + Geo<WD>::cat(16 * kb + i, 4 * u + g)); };
   f32x4 a0 = rd(0, 0), a1 = rd(1, 0);
 #pragma unroll
   for (int u = 0; u < WD / 16; ++u) {
@@ -121,43 +139,48 @@ KD_DEV void score_pair(const uint8_t* chunk, int i, int g, const float (&reg)[NR
   }
 }
 
-// acc[db] (the [d][token] product, 16 blocks) += chunk^T B over the chunk's 32
-// rows, B = the score-shaped registers s (row 16 kb + 4 g + r in register r of
-// s[kb]).  For k-step (kb, r) lane (i, g) reads columns 16 i .. 16 i + 15 of
-// chunk row 16 kb + 4 g + r, one float per output block.
-KD_DEV void accumulate16(const uint8_t* chunk, int i, int g, const f32x4 (&s)[2], f32x4 (&acc)[NDB]) {
-  auto rd = [&](int step, f32x4 (&a)[4]) {
+// acc[db] (the [d][token] product, NDB blocks) += chunk^T B over the chunk's
+// 32 rows, B = the score-shaped registers s (row 16 kb + 4 g + r in register r
+// of s[kb]).  For k-step (kb, r) lane (i, g) reads columns NDB i .. NDB i +
+// NDB - 1 of chunk row 16 kb + 4 g + r, one float per output block.
+template <int WD>
+KD_DEV void accumulate16(const uint8_t* chunk, int i, int g, const f32x4 (&s)[2], f32x4 (&acc)[Geo<WD>::NDB]) {
+  using G = Geo<WD>;
+  constexpr int NC = G::NDB / 4;  // 16-byte reads per k-step
+  auto rd = [&](int step, f32x4 (&a)[NC]) {
     const int row = 16 * (step >> 2) + 4 * g + (step & 3);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) a[j] = *reinterpret_cast<const f32x4*>(chunk + cat(row, 4 * i + j));
+    for (int j = 0; j < NC; ++j) a[j] = *reinterpret_cast<const f32x4*>(chunk + G::cat(row, NC * i + j));
   };
-  f32x4 a[4];
+  f32x4 a[NC];
   rd(0, a);
 #pragma unroll
   for (int step = 0; step < 8; ++step) {
-    f32x4 nx[4];
+    f32x4 nx[NC];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) nx[j] = a[j];
+    for (int j = 0; j < NC; ++j) nx[j] = a[j];
     if (step + 1 < 8) rd(step + 1, nx);
     const float b = s[step >> 2][step & 3];
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) acc[db] = mma16(a[db >> 2][db & 3], b, acc[db]);
+    for (int db = 0; db < G::NDB; ++db) acc[db] = mma16(a[db >> 2][db & 3], b, acc[db]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) a[j] = nx[j];
+    for (int j = 0; j < NC; ++j) a[j] = nx[j];
   }
 }
 
-// store the [d][token] accumulators of this lane's token to row `out` (256
-// floats), times scale: register r of block db is column 64 g + 16 r + db
-KD_DEV void store16(float* out, const f32x4 (&acc)[NDB], int g, float scale) {
+// store the [d][token] accumulators of this lane's token to row `out` (WD
+// floats), times scale: register r of block db is column NDB (4 g + r) + db
+template <int WD>
+KD_DEV void store16(float* out, const f32x4 (&acc)[Geo<WD>::NDB], int g, float scale) {
+  constexpr int NDB = Geo<WD>::NDB;
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NDB / 4; ++j) {
       const f32x4 x = {acc[4 * j][r] * scale, acc[4 * j + 1][r] * scale, acc[4 * j + 2][r] * scale,
                        acc[4 * j + 3][r] * scale};
-      *reinterpret_cast<f32x4*>(out + 64 * g + 16 * r + 4 * j) = x;
+      *reinterpret_cast<f32x4*>(out + NDB * (4 * g + r) + 4 * j) = x;
     }
 }
 
@@ -192,12 +215,15 @@ KD_DEV int next_live(const uint32_t* ent, int e, int n, int member) {
 }
 
 // ------------------------------------------------------------------ forward
-__global__ __launch_bounds__(256, 1) void k_fwd_f32w(AttnArgs a, const uint32_t* __restrict__ codes,
+template <int WD>
+__global__ __launch_bounds__(256, Geo<WD>::WAVES) void k_fwd_f32w(AttnArgs a, const uint32_t* __restrict__ codes,
                                                      const uint32_t* __restrict__ list,
                                                      const int32_t* __restrict__ count, int nT, int nblk,
                                                      const uint32_t* __restrict__ order) {
-  __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][CBYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][CBYTES];
+  using G = Geo<WD>;
+  constexpr int NR = G::NR, NDB = G::NDB;
+  __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][G::CBYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][G::CBYTES];
   __shared__ __attribute__((aligned(256))) uint32_t s_kc[2][64];
   const int tid = threadIdx.x, lane = tid & 63, i = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -216,7 +242,7 @@ __global__ __launch_bounds__(256, 1) void k_fwd_f32w(AttnArgs a, const uint32_t*
   uint32_t qcode = qvalid ? codes[int64_t(it.b) * T + q] : 0u;
 
   float qr[NR];
-  load_row16(qg, a.q_strides[2], q, qvalid, g, cs, qr);
+  load_row16<WD>(qg, a.q_strides[2], q, qvalid, g, cs, qr);
 
   const int lb = it.b * nblk + it.blk;
   const int n = count[lb];
@@ -224,8 +250,8 @@ __global__ __launch_bounds__(256, 1) void k_fwd_f32w(AttnArgs a, const uint32_t*
   // chunk (entry e, half hf): keys 64 tile + 32 hf .. + 31
   auto copy = [&](int e, int hf, int slot) {
     const uint32_t r0 = entry_tile(ent[e]) * 64u + uint32_t(32 * hf);
-    copy_chunk(rs_k, r0, krb, lds_addr(s_k[slot]), wave, lane);
-    copy_chunk(rs_v, r0, vrb, lds_addr(s_v[slot]), wave, lane);
+    copy_chunk<WD>(rs_k, r0, krb, lds_addr(s_k[slot]), wave, lane);
+    copy_chunk<WD>(rs_v, r0, vrb, lds_addr(s_v[slot]), wave, lane);
     if (wave == 0)
       dma_b32(rs_c, (r0 + uint32_t(lane)) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(s_kc[slot])))));
   };
@@ -251,7 +277,7 @@ __global__ __launch_bounds__(256, 1) void k_fwd_f32w(AttnArgs a, const uint32_t*
     }
     if (ne < n) copy(ne, nh, slot ^ 1);
     f32x4 s[2];
-    score_pair(s_k[slot], i, g, qr, s);
+    score_pair<WD>(s_k[slot], i, g, qr, s);
     if (entry_class(en, it.member) == TILE_PARTIAL) {
       const int k0 = int(entry_tile(en)) * 64 + 32 * hf;
 #pragma unroll
@@ -279,25 +305,28 @@ __global__ __launch_bounds__(256, 1) void k_fwd_f32w(AttnArgs a, const uint32_t*
     l = l * alpha + group_sum(ls);
 #pragma unroll
     for (int db = 0; db < NDB; ++db) o[db] *= alpha;
-    accumulate16(s_v[slot], i, g, s, o);
+    accumulate16<WD>(s_v[slot], i, g, s, o);
     e = ne;
     hf = nh;
     slot ^= 1;
   }
   if (!qvalid) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  store16(static_cast<float*>(a.o) + it.b * a.o_strides[0] + it.hh * a.o_strides[1] + int64_t(q) * a.o_strides[2], o,
+  store16<WD>(static_cast<float*>(a.o) + it.b * a.o_strides[0] + it.hh * a.o_strides[1] + int64_t(q) * a.o_strides[2], o,
           g, inv);
   if (g == 0 && a.lse != nullptr) a.lse[int64_t(bh) * T + q] = l > 0.f ? m + fast_log2(l) : -__builtin_inff();
 }
 
 // ----------------------------------------------------------------------- dQ
-__global__ __launch_bounds__(256, 1) void k_dq_f32w(AttnArgs a, const uint32_t* __restrict__ codes,
+template <int WD>
+__global__ __launch_bounds__(256, Geo<WD>::WAVES) void k_dq_f32w(AttnArgs a, const uint32_t* __restrict__ codes,
                                                     const uint32_t* __restrict__ list,
                                                     const int32_t* __restrict__ count, int nT, int nblk,
                                                     const uint32_t* __restrict__ order) {
-  __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][CBYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][CBYTES];
+  using G = Geo<WD>;
+  constexpr int NR = G::NR, NDB = G::NDB;
+  __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][G::CBYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][G::CBYTES];
   __shared__ __attribute__((aligned(256))) uint32_t s_kc[2][64];
   const int tid = threadIdx.x, lane = tid & 63, i = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -321,16 +350,16 @@ __global__ __launch_bounds__(256, 1) void k_dq_f32w(AttnArgs a, const uint32_t* 
   float ndelta = qvalid ? a.delta[int64_t(bh) * T + q] : 0.f;  // the workspace holds -Delta
 
   float qr[NR], dr[NR];
-  load_row16(qg, a.q_strides[2], q, qvalid, g, cs, qr);
-  load_row16(dog, a.do_strides[2], q, qvalid, g, 1.f, dr);
+  load_row16<WD>(qg, a.q_strides[2], q, qvalid, g, cs, qr);
+  load_row16<WD>(dog, a.do_strides[2], q, qvalid, g, 1.f, dr);
 
   const int lb = it.b * nblk + it.blk;
   const int n = count[lb];
   const uint32_t* ent = list + int64_t(lb) * nT;
   auto copy = [&](int e, int hf, int slot) {
     const uint32_t r0 = entry_tile(ent[e]) * 64u + uint32_t(32 * hf);
-    copy_chunk(rs_k, r0, krb, lds_addr(s_k[slot]), wave, lane);
-    copy_chunk(rs_v, r0, vrb, lds_addr(s_v[slot]), wave, lane);
+    copy_chunk<WD>(rs_k, r0, krb, lds_addr(s_k[slot]), wave, lane);
+    copy_chunk<WD>(rs_v, r0, vrb, lds_addr(s_v[slot]), wave, lane);
     if (wave == 0)
       dma_b32(rs_c, (r0 + uint32_t(lane)) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(s_kc[slot])))));
   };
@@ -360,8 +389,8 @@ __global__ __launch_bounds__(256, 1) void k_dq_f32w(AttnArgs a, const uint32_t* 
     }
     if (ne < n) copy(ne, nh, slot ^ 1);
     f32x4 s[2], dp[2];
-    score_pair(s_k[slot], i, g, qr, s);
-    score_pair(s_v[slot], i, g, dr, dp);
+    score_pair<WD>(s_k[slot], i, g, qr, s);
+    score_pair<WD>(s_v[slot], i, g, dr, dp);
     if (entry_class(en, it.member) == TILE_PARTIAL) {
       const int k0 = int(entry_tile(en)) * 64 + 32 * hf;
 #pragma unroll
@@ -377,23 +406,26 @@ __global__ __launch_bounds__(256, 1) void k_dq_f32w(AttnArgs a, const uint32_t* 
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) s[kb][r] = fast_exp2(s[kb][r] - lse) * (dp[kb][r] + ndelta);
-    accumulate16(s_k[slot], i, g, s, dq);
+    accumulate16<WD>(s_k[slot], i, g, s, dq);
     e = ne;
     hf = nh;
     slot ^= 1;
   }
   if (!qvalid) return;
-  store16(static_cast<float*>(a.dq) + it.b * a.dq_strides[0] + it.hh * a.dq_strides[1] + int64_t(q) * a.dq_strides[2],
+  store16<WD>(static_cast<float*>(a.dq) + it.b * a.dq_strides[0] + it.hh * a.dq_strides[1] + int64_t(q) * a.dq_strides[2],
           dq, g, a.sm_scale);
 }
 
 // -------------------------------------------------------------------- dK/dV
-__global__ __launch_bounds__(256, 1) void k_dkdv_f32w(AttnArgs a, const uint32_t* __restrict__ codes,
+template <int WD>
+__global__ __launch_bounds__(256, Geo<WD>::WAVES) void k_dkdv_f32w(AttnArgs a, const uint32_t* __restrict__ codes,
                                                       const uint32_t* __restrict__ list,
                                                       const int32_t* __restrict__ count, int nT, int nblk,
                                                       const uint32_t* __restrict__ order) {
-  __shared__ __attribute__((aligned(1024))) uint8_t s_q[2][CBYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t s_do[2][CBYTES];
+  using G = Geo<WD>;
+  constexpr int NR = G::NR, NDB = G::NDB;
+  __shared__ __attribute__((aligned(1024))) uint8_t s_q[2][G::CBYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_do[2][G::CBYTES];
   __shared__ __attribute__((aligned(256))) float s_lse[2][64];
   __shared__ __attribute__((aligned(256))) float s_dl[2][64];
   __shared__ __attribute__((aligned(256))) uint32_t s_qc[2][64];
@@ -417,8 +449,8 @@ __global__ __launch_bounds__(256, 1) void k_dkdv_f32w(AttnArgs a, const uint32_t
   uint32_t kcode = kvalid ? codes[int64_t(it.b) * T + k] : 0u;
 
   float kr[NR], vr[NR];
-  load_row16(kg, a.k_strides[2], k, kvalid, g, cs, kr);
-  load_row16(vg, a.v_strides[2], k, kvalid, g, 1.f, vr);
+  load_row16<WD>(kg, a.k_strides[2], k, kvalid, g, cs, kr);
+  load_row16<WD>(vg, a.v_strides[2], k, kvalid, g, 1.f, vr);
 
   const int lb = it.b * nblk + it.blk;
   const int n = count[lb];
@@ -427,8 +459,8 @@ __global__ __launch_bounds__(256, 1) void k_dkdv_f32w(AttnArgs a, const uint32_t
   // codes, LSE and -Delta (64 values copied, the first 32 used)
   auto copy = [&](int e, int hf, int slot) {
     const uint32_t r0 = entry_tile(ent[e]) * 64u + uint32_t(32 * hf);
-    copy_chunk(rs_q, r0, qrb, lds_addr(s_q[slot]), wave, lane);
-    copy_chunk(rs_do, r0, dorb, lds_addr(s_do[slot]), wave, lane);
+    copy_chunk<WD>(rs_q, r0, qrb, lds_addr(s_q[slot]), wave, lane);
+    copy_chunk<WD>(rs_do, r0, dorb, lds_addr(s_do[slot]), wave, lane);
     const uint32_t off = (r0 + uint32_t(lane)) * 4u;
     if (wave == 0) dma_b32(rs_c, off, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(s_qc[slot])))));
     if (wave == 1) dma_b32(rs_l, off, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(s_lse[slot])))));
@@ -460,8 +492,8 @@ __global__ __launch_bounds__(256, 1) void k_dkdv_f32w(AttnArgs a, const uint32_t
     const int q0 = int(entry_tile(en)) * 64 + 32 * hf;
     const bool full = entry_class(en, it.member) == TILE_FULL;
     f32x4 s[2], dp[2];
-    score_pair(s_q[slot], i, g, kr, s);
-    score_pair(s_do[slot], i, g, vr, dp);
+    score_pair<WD>(s_q[slot], i, g, kr, s);
+    score_pair<WD>(s_do[slot], i, g, vr, dp);
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       const int row = 16 * qb + 4 * g;  // rows row .. row + 3 of the chunk are registers 0 .. 3
@@ -484,36 +516,45 @@ __global__ __launch_bounds__(256, 1) void k_dkdv_f32w(AttnArgs a, const uint32_t
         dp[qb][r] = p * (dp[qb][r] + dv4[r]);  // dS
       }
     }
-    accumulate16(s_do[slot], i, g, s, dv);
-    accumulate16(s_q[slot], i, g, dp, dk);
+    accumulate16<WD>(s_do[slot], i, g, s, dv);
+    accumulate16<WD>(s_q[slot], i, g, dp, dk);
     e = ne;
     hf = nh;
     slot ^= 1;
   }
   if (!kvalid) return;
-  store16(static_cast<float*>(a.dk) + it.b * a.dk_strides[0] + it.hh * a.dk_strides[1] + int64_t(k) * a.dk_strides[2],
+  store16<WD>(static_cast<float*>(a.dk) + it.b * a.dk_strides[0] + it.hh * a.dk_strides[1] + int64_t(k) * a.dk_strides[2],
           dk, g, a.sm_scale);
-  store16(static_cast<float*>(a.dv) + it.b * a.dv_strides[0] + it.hh * a.dv_strides[1] + int64_t(k) * a.dv_strides[2],
+  store16<WD>(static_cast<float*>(a.dv) + it.b * a.dv_strides[0] + it.hh * a.dv_strides[1] + int64_t(k) * a.dv_strides[2],
           dv, g, 1.f);
 }
 
-}  // namespace
-
-int launch_f32w(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
+template <int WD>
+void launch_f32w_d(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const uint32_t* codes = reinterpret_cast<const uint32_t*>(plan + L.codes);
   auto lst = [&](size_t off) { return reinterpret_cast<const uint32_t*>(plan + off); };
   auto cnt = [&](size_t off) { return reinterpret_cast<const int32_t*>(plan + off); };
   const unsigned bh2 = 2u * unsigned(a.B) * unsigned(a.H);  // two member workgroups per block
   if (which == 0)
-    hipLaunchKernelGGL(k_fwd_f32w, dim3(bh2 * unsigned(L.n_fwd_blocks)), dim3(256), 0, st, a, codes, lst(L.fwd_list),
-                       cnt(L.fwd_count), L.nT, L.n_fwd_blocks, lst(L.fwd_order));
+    hipLaunchKernelGGL(k_fwd_f32w<WD>, dim3(bh2 * unsigned(L.n_fwd_blocks)), dim3(256), 0, st, a, codes,
+                       lst(L.fwd_list), cnt(L.fwd_count), L.nT, L.n_fwd_blocks, lst(L.fwd_order));
   else if (which == 2)
-    hipLaunchKernelGGL(k_dq_f32w, dim3(bh2 * unsigned(L.n_dq_blocks)), dim3(256), 0, st, a, codes, lst(L.dq_list),
-                       cnt(L.dq_count), L.nT, L.n_dq_blocks, lst(L.dq_order));
+    hipLaunchKernelGGL(k_dq_f32w<WD>, dim3(bh2 * unsigned(L.n_dq_blocks)), dim3(256), 0, st, a, codes,
+                       lst(L.dq_list), cnt(L.dq_count), L.nT, L.n_dq_blocks, lst(L.dq_order));
   else
-    hipLaunchKernelGGL(k_dkdv_f32w, dim3(bh2 * unsigned(L.n_dkdv_blocks)), dim3(256), 0, st, a, codes,
+    hipLaunchKernelGGL(k_dkdv_f32w<WD>, dim3(bh2 * unsigned(L.n_dkdv_blocks)), dim3(256), 0, st, a, codes,
                        lst(L.dkdv_list), cnt(L.dkdv_count), L.nT, L.n_dkdv_blocks, lst(L.dkdv_order));
+}
+
+}  // namespace
+
+int launch_f32w(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
+  switch (a.D) {
+    case 64: launch_f32w_d<64>(which, a, plan, st); break;
+    case 128: launch_f32w_d<128>(which, a, plan, st); break;
+    default: launch_f32w_d<256>(which, a, plan, st); break;
+  }
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 
