@@ -96,9 +96,11 @@ def excess(got_f64: np.ndarray, ref: np.ndarray) -> float:
     return float(np.max(np.maximum(np.abs(out - ref) - ulp_bf16(ref), 0.0), initial=0.0))
 
 
-def emulate_head(q, k, v, do, mask, sm_scale, rot=None, block=1024):
+def emulate_head(q, k, v, do, mask, sm_scale, rot=None, block=256):
     """Worst error beyond one bf16 ulp per (product, form) for one head.
 
+    block: query rows per pass (256: [256, T] temporaries of 16 MB in fp64;
+    the fp64 sums over passes change with it in the last bits only).
     q, k, v, do: float32 arrays [T, d] holding the bf16 inputs (q and k already
     rotated and rounded when ``rot`` is given); mask: bool [T, T]; rot: the
     fp64 rotation R (dQ, dK are reported for the unrotated inputs, times R^T).
@@ -200,20 +202,51 @@ def emulate_head(q, k, v, do, mask, sm_scale, rot=None, block=1024):
             "ref_max": {p: float(np.abs(r).max()) for p, r in refs.items()}, "refs": refs}
 
 
+def head_qkvdo(b, h, B, H, L, d, seed, outlier_frac=0.0, outlier_mult=20.0):
+    """Head (b, h) of ``kerneldev_amd.synth.qkvdo(B, H, L, d, seed, ...)``'s
+    Q, K, V, dO (bf16), drawn without the other heads: the same generator
+    calls in the same order, one [L, d] slice at a time.  torch's CPU normal
+    fill draws its uniforms in order and transforms them in independent blocks
+    of 16, so slices of L d values (a multiple of 16) reproduce the whole
+    tensor's draw (tests/test_rounding_budget.py pins this against qkvdo).
+    Config 4's full inputs are ~1 GB each in fp32; one head is 4 MB."""
+    import math
+
+    import torch
+
+    g = torch.Generator("cpu").manual_seed(seed)
+    out = []
+    for idx in range(4):
+        x = None
+        for bh in range(B * H):
+            c = torch.randn(L, d, generator=g, dtype=torch.float32)
+            if bh == b * H + h:
+                x = c
+        if outlier_frac > 0 and idx < 3:
+            n_out = math.ceil(outlier_frac * d)
+            for hh in range(H):
+                ch = torch.randperm(d, generator=g)[:n_out]
+                if hh == h:
+                    x[:, ch] *= outlier_mult
+        out.append(x.to(torch.bfloat16))
+    return tuple(out)
+
+
 def config4_head(b: int, h: int, hadamard: bool, seed: int = 0):
-    """Inputs of one config-4 head as emulate_head takes them, plus its mask."""
+    """Inputs of one config-4 head (``kerneldev_amd.synth.config_inputs(4,
+    seed)[.][b, h]``) as emulate_head takes them, plus its mask."""
     import torch
 
     from kerneldev_amd.hadamard import generate_hadamard_signs
-    from kerneldev_amd.synth import config_inputs
+    from kerneldev_amd.synth import CONFIG4_LAYOUT, cocktail_batch
     from oracle.hadamard import rotate_fp32, rotation_matrix
     from oracle.mask import dense_mask
 
-    inp = config_inputs(4, seed=seed)
-    T, D = inp["q"].shape[2], inp["q"].shape[3]
-    mask = dense_mask(T, B=inp["q"].shape[0], in_span=inp["in_span"].numpy(), span_id=inp["span_id"].numpy(),
-                      is_prefix=inp["is_prefix"].numpy())[b]
-    q, k, v, do = (inp[n][b, h].to(torch.float32).numpy() for n in ("q", "k", "v", "do"))
+    B, H, T, D = 2, 32, 8192, 128
+    _, in_span, span_id, is_prefix = cocktail_batch(B, T, CONFIG4_LAYOUT, seed)
+    mask = dense_mask(T, B=1, in_span=in_span[b:b + 1].numpy(), span_id=span_id[b:b + 1].numpy(),
+                      is_prefix=is_prefix[b:b + 1].numpy())[0]
+    q, k, v, do = (x.to(torch.float32).numpy() for x in head_qkvdo(b, h, B, H, T, D, seed + 1, outlier_frac=0.01))
     rot = None
     if hadamard:
         signs = generate_hadamard_signs(D, 0).numpy()

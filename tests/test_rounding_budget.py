@@ -19,7 +19,7 @@ import pytest
 import torch
 
 from oracle import attention as oracle_attention
-from rounding_emulation import FORMS, LOG2E, PRODUCTS, as_form, bf16_round, config4_head, emulate_head
+from rounding_emulation import FORMS, LOG2E, PRODUCTS, as_form, bf16_round, config4_head, emulate_head, head_qkvdo
 
 BAR, MARGIN = 2e-2, 2.0
 HEADS = [(1, 17), (0, 1)]
@@ -99,3 +99,14 @@ def test_emulation_reference_is_the_oracle():
     dq, dk, dv, _ = oracle_attention.backward(t[0], t[1], t[2], o, t[3], m, sm_scale)
     for name, want in (("O", o), ("dQ", dq), ("dK", dk), ("dV", dv)):
         np.testing.assert_allclose(refs[name], want[0, 0].numpy(), rtol=1e-9, atol=1e-12, err_msg=name)
+
+
+def test_head_generator_is_the_config_generator():
+    """head_qkvdo (config4_head's inputs, one head at a time) equals the head
+    of synth.qkvdo, outlier channels included, here on a small shape."""
+    from kerneldev_amd.synth import qkvdo
+
+    full = qkvdo(2, 3, 96, 64, seed=5, outlier_frac=0.05)
+    for b, h in ((0, 0), (1, 2), (0, 1)):
+        for x, y in zip(full, head_qkvdo(b, h, 2, 3, 96, 64, seed=5, outlier_frac=0.05)):
+            assert torch.equal(x[b, h], y)
