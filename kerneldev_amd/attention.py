@@ -34,8 +34,8 @@ SUPPORTED_HEAD_DIMS = REFERENCE_HEAD_DIMS
 # Hadamard epilogues and fp8 scores; 16, 32 and 256 run there without
 # them (16 and 32 on the d = 64 kernels, which read the missing columns as
 # zeros).  fp32
-# inputs run on the fp32 MFMA kernels (kd_f32mma.hip: head dim 32, and 16
-# zero-padded to 32, FP32_PADDED_HEAD_DIMS; kd_f32w.hip: 64, 128, 256), except
+# inputs run on the fp32 MFMA kernels (kd_f32w.hip: head dims 32, 64, 128,
+# 256, and 16 zero-padded to 32, FP32_PADDED_HEAD_DIMS), except
 # at precision "tf32" and head dims 16, 32 (X3_ROUTED_HEAD_DIMS: bf16x3,
 # faster there)
 MFMA_HEAD_DIMS = (64, 128)

@@ -1,19 +1,20 @@
 // Attention for fp32 inputs on the fp32 matrix cores in their 16 x 16 x 4
-// form (v_mfma_f32_16x16x4f32), for head dims WD = 64, 128 and 256: the
-// reference's fp32 dots (original_kernel.py:452, :569, :1239, :1331-1333,
-// :1425, :1517-1523) for HEAD_DIM in {64, 128, 256} (:1720), fp32 operands and
-// fp32 accumulation.  Same algebra, plan, lists and masks as the 32 x 32 x 2
-// kernels of kd_f32mma.hip:
+// form (v_mfma_f32_16x16x4f32), for head dims WD = 32, 64, 128 and 256 (16
+// is zero-padded to 32 by the Python layer): the reference's fp32 dots
+// (original_kernel.py:452, :569, :1239, :1331-1333, :1425, :1517-1523) for
+// HEAD_DIM in {32, 64, 128, 256} (:1720), fp32 operands and fp32
+// accumulation.  Same algebra, plan, lists and masks as the 16-bit kernels:
 //   forward   O = softmax2(S c) V, LSE2 = m + log2 l      (:279-626)
 //   dQ        P = exp2(S c - LSE), dS = P (dP - Delta), dQ = sm_scale dS K  (:1173-1336)
 //   dK / dV   dV = P^T dO, dK = sm_scale dS^T Q            (:1339-1525)
 // with c = sm_scale log2(e) folded into the register-resident Q (forward, dQ)
 // or K (dK/dV).  Delta comes from k_delta_simt (kd_simt.hip).
 //
-// Why a 16 x 16 product.  With 32 tokens per wave (the 32 x 32 x 2 form) a
-// lane holds WD / 2 floats of each register row and WD / 2 accumulators per
-// output; at WD = 256 that is more than one wave's registers once the
-// compiler's copies are counted.  With 16 tokens per wave a register row is
+// Why a 16 x 16 product.  With 32 tokens per wave (the 32 x 32 x 2 form,
+// which these kernels replaced) a lane holds WD / 2 floats of each register
+// row and WD / 2 accumulators per output; at WD = 256 that is more than one
+// wave's registers once the compiler's copies are counted, and at WD = 32-128
+// its 64-row tiles took twice the LDS of 32-row chunks for no gain.  With 16 tokens per wave a register row is
 // WD / 4 floats a lane and a [WD x 16] accumulator WD / 4, so at WD = 256 the
 // forward holds ~150 values, dQ ~240 and dK/dV ~310, within one wave per SIMD
 // (512 registers).  The 16 x 16 x 4 form runs at the same rate as the 32 x 32
@@ -69,13 +70,22 @@ struct Geo {
   static constexpr int NR = WD / 4;           // floats of a register row per lane
   static constexpr int RPL = 1024 / CROWB;    // rows per wave-wide 1 KiB load
   static constexpr int LPW = CH / RPL / 4;    // such loads per wave and chunk
-  static constexpr int HMASK = CPR / 16 - 1;  // chunk bits above the low four, folded in
+  static constexpr int HMASK = CPR >= 16 ? CPR / 16 - 1 : 0;  // chunk bits above the low four, folded in
   // workgroups per CU the kernels are built for (1: up to 512 registers a
-  // wave; the LDS of two chunk slots of two operands, 4 CBYTES, allows 1, 2, 4)
-  static constexpr int WAVES = WD == 256 ? 1 : WD == 128 ? 2 : 3;
-  static_assert(WD == 64 || WD == 128 || WD == 256, "head dims 64, 128, 256");
+  // wave; the LDS of two chunk slots of two operands, 4 CBYTES, allows 1, 2,
+  // 4, 9 at WD = 256, 128, 64, 32)
+  static constexpr int WAVES = WD == 256 ? 1 : WD == 128 ? 2 : WD == 64 ? 3 : 4;
+  static_assert(WD == 32 || WD == 64 || WD == 128 || WD == 256, "head dims 32, 64, 128, 256");
+  // position of logical 16-byte chunk c in chunk row r (an involution for a
+  // fixed r): at WD = 32 a row is 128 bytes, two rows a bank sweep, and 16
+  // rows read at one chunk fill the 64 banks once with the row pair's half
+  // (r & 1) and the chunk XOR (r >> 1) & 7
+  KD_DEV static int pos(int r, int c) {
+    if constexpr (WD == 32) return c ^ ((r >> 1) & 7);
+    else return c ^ (r & 15) ^ ((c >> 4) & HMASK);
+  }
   // byte offset of logical 16-byte chunk c of chunk row r
-  KD_DEV static int cat(int r, int c) { return r * CROWB + ((c ^ (r & 15) ^ ((c >> 4) & HMASK)) << 4); }
+  KD_DEV static int cat(int r, int c) { return r * CROWB + (pos(r, c) << 4); }
 };
 
 KD_DEV f32x4 mma16(float a, float b, const f32x4& c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
@@ -92,7 +102,7 @@ KD_DEV void copy_chunk(const u32x4& rs, uint32_t r0, uint32_t row_bytes, uint32_
   for (int j = 0; j < G::LPW; ++j) {
     const int ld = G::LPW * wave + j;                   // load index within the chunk
     const int rr = ld * G::RPL + lane / G::CPR, p = lane % G::CPR;  // row, position
-    const int c = (p & ~15) | ((p & 15) ^ (rr & 15) ^ ((p >> 4) & G::HMASK));
+    const int c = G::pos(rr, p);  // (pos is its own inverse for a fixed row)
     const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_chunk + uint32_t(ld) * 1024u)));
     dma_b128(rs, (r0 + uint32_t(rr)) * row_bytes + uint32_t(c) * 16u, m);
   }
@@ -146,7 +156,24 @@ KD_DEV void score_pair(const uint8_t* chunk, int i, int g, const float (&reg)[Ge
 template <int WD>
 KD_DEV void accumulate16(const uint8_t* chunk, int i, int g, const f32x4 (&s)[2], f32x4 (&acc)[Geo<WD>::NDB]) {
   using G = Geo<WD>;
-  constexpr int NC = G::NDB / 4;  // 16-byte reads per k-step
+  if constexpr (G::NDB == 2) {  // WD = 32: two floats (8 bytes) a lane and k-step
+    auto rd = [&](int step) {
+      const int row = 16 * (step >> 2) + 4 * g + (step & 3);
+      return *reinterpret_cast<const f32x2*>(chunk + G::cat(row, i >> 1) + 8 * (i & 1));
+    };
+    f32x2 a = rd(0);
+#pragma unroll
+    for (int step = 0; step < 8; ++step) {
+      const f32x2 nx = step + 1 < 8 ? rd(step + 1) : a;
+      const float b = s[step >> 2][step & 3];
+      acc[0] = mma16(a[0], b, acc[0]);
+      acc[1] = mma16(a[1], b, acc[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      a = nx;
+    }
+    return;
+  }
+  constexpr int NC = G::NDB >= 4 ? G::NDB / 4 : 1;  // 16-byte reads per k-step
   auto rd = [&](int step, f32x4 (&a)[NC]) {
     const int row = 16 * (step >> 2) + 4 * g + (step & 3);
 #pragma unroll
@@ -174,6 +201,12 @@ KD_DEV void accumulate16(const uint8_t* chunk, int i, int g, const f32x4 (&s)[2]
 template <int WD>
 KD_DEV void store16(float* out, const f32x4 (&acc)[Geo<WD>::NDB], int g, float scale) {
   constexpr int NDB = Geo<WD>::NDB;
+  if constexpr (NDB == 2) {  // WD = 32
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      *reinterpret_cast<f32x2*>(out + 2 * (4 * g + r)) = f32x2{acc[0][r] * scale, acc[1][r] * scale};
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -549,8 +582,13 @@ void launch_f32w_d(int which, const AttnArgs& a, const uint8_t* plan, hipStream_
 
 }  // namespace
 
-int launch_f32w(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
+bool use_f32mma(const AttnArgs& a) {
+  return a.dtype == KD_F32 && (a.D == 32 || a.D == 64 || a.D == 128 || a.D == 256);
+}
+
+int launch_f32mma(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   switch (a.D) {
+    case 32: launch_f32w_d<32>(which, a, plan, st); break;
     case 64: launch_f32w_d<64>(which, a, plan, st); break;
     case 128: launch_f32w_d<128>(which, a, plan, st); break;
     default: launch_f32w_d<256>(which, a, plan, st); break;

@@ -60,11 +60,10 @@ int launch_span_bwd(const kd_span_args& a, hipStream_t st);
 // MFMA kernels are not built for; which: 0 forward, 1 Delta, 2 dQ, 3 dK/dV
 bool use_simt(const AttnArgs& a);
 int launch_simt_kernel(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st);
-// fp32 inputs at head dim 32 (kd_f32mma.hip) and 64, 128, 256 (kd_f32w.hip)
-// on the fp32 MFMA; which: 0 forward, 2 dQ, 3 dK/dV (Delta stays on k_delta_simt)
+// fp32 inputs at head dims 32, 64, 128, 256 on the fp32 MFMA (kd_f32w.hip);
+// which: 0 forward, 2 dQ, 3 dK/dV (Delta stays on k_delta_simt)
 bool use_f32mma(const AttnArgs& a);
 int launch_f32mma(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st);
-int launch_f32w(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st);
 // Device address of the no-allocation workspace on the current device
 // (kd_noalloc.hip); KD_OK, or a status with *err set.
 int noalloc_workspace(float** out, const char** err);

@@ -1,8 +1,8 @@
 // Attention in fp32 arithmetic on the vector ALUs, for the case the MFMA
-// kernels are not built for: fp32 inputs at head dim 16 or 256 (the
-// reference's precision="ieee" / "tf32" dots, original_kernel.py:452, :569,
-// :1239, :1331-1333, :1425, :1517-1523, here in full fp32; kd_f32mma.hip takes
-// fp32 at 32, 64, 128), plus Delta for fp32 inputs at every head dim.  Same
+// kernels are not built for: fp32 inputs at head dim 16 through the C ABI
+// (the reference's precision="ieee" / "tf32" dots, original_kernel.py:452,
+// :569, :1239, :1331-1333, :1425, :1517-1523, here in full fp32; kd_f32w.hip
+// takes fp32 at 32, 64, 128, 256), plus Delta for fp32 inputs at every head dim.  Same
 // algebra, plan and masks as the MFMA kernels:
 //   forward   O = softmax2(S c) V, LSE2 = m + log2 l      (:279-626)
 //   Delta     rowsum(O * dO)                              (:649-710)
