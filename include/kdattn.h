@@ -21,9 +21,9 @@
  *   - Head dims 16, 32, 64, 128, 256 (original_kernel.py:1720).  bf16 / fp16
  *     run on the MFMA kernels at every head dim (16 and 32 on the D = 64
  *     kernels, which read the columns past D as zeros and store only the D
- *     real ones; dqk_signs at 64, 128 only; fp8 scores at 64, 128 for bf16); fp32 inputs at
- *     D = 32, 64, 128, 256 on the fp32 MFMA kernels, at D = 16 on fp32
- *     vector-ALU kernels.  fp32 inputs get no fp8 scores and no dqk_signs,
+ *     real ones; dqk_signs at 64, 128 only; fp8 scores at 64, 128 for bf16); fp32 inputs
+ *     on the fp32 MFMA kernels at every head dim (16 on the D = 32 kernels,
+ *     the same way).  fp32 inputs get no fp8 scores and no dqk_signs,
  *     and precision is always full fp32 for them.  (The Python layer runs fp32 inputs at precision "tf32"
  *     and D = 16, 32 as bf16 operands of three times the head dim on the
  *     16-bit MFMA kernels instead, with dq_lo / dk_lo / dv_lo below.)
@@ -49,7 +49,7 @@ extern "C" {
 /* element dtypes */
 #define KD_BF16 0
 #define KD_F16 1
-#define KD_F32 2 /* attention only: computed in fp32 (fp32 MFMA at D = 32, 64, 128, 256) */
+#define KD_F32 2 /* attention only: computed in fp32 (fp32 MFMA at every head dim) */
 /* arithmetic of the softmax weights P and the score gradients dS inside the
  * attention kernels (kd_attn_args.precision) */
 #define KD_PREC_SPLIT 0  /* P and dS enter their products (P V, dV, dQ, dK) as a 16-bit pair

@@ -12,8 +12,7 @@ shim over the C ABI of ``libkdattn.so``:
 * ``kdattn::fwd_x3`` / ``kdattn::bwd_x3`` -> the 16-bit kernels for fp32
   inputs at precision "tf32" and head dims 16 and 32, as three bf16 products
   per product (see X3_HEAD_DIMS).  Other fp32 inputs go through ``kdattn::fwd``
-  / ``::bwd`` to the fp32 MFMA kernels (head dims 32, 64, 128, 256; 16
-  zero-padded to 32).
+  / ``::bwd`` to the fp32 MFMA kernels (every head dim).
 
 There is no CPU or PyTorch fallback: a missing library raises.
 """
@@ -34,13 +33,12 @@ SUPPORTED_HEAD_DIMS = REFERENCE_HEAD_DIMS
 # Hadamard epilogues and fp8 scores; 16, 32 and 256 run there without
 # them (16 and 32 on the d = 64 kernels, which read the missing columns as
 # zeros).  fp32
-# inputs run on the fp32 MFMA kernels (kd_f32w.hip: head dims 32, 64, 128,
-# 256, and 16 zero-padded to 32, FP32_PADDED_HEAD_DIMS), except
-# at precision "tf32" and head dims 16, 32 (X3_ROUTED_HEAD_DIMS: bf16x3,
-# faster there)
+# inputs run on the fp32 MFMA kernels at every head dim (kd_f32w.hip; 16 on
+# the d = 32 kernels, which read the missing columns as zeros), except at
+# precision "tf32" and head dims 16, 32 (X3_ROUTED_HEAD_DIMS: bf16x3, faster
+# there)
 MFMA_HEAD_DIMS = (64, 128)
 FP8_HEAD_DIMS = (64, 128)  # fp8 e4m3 Q K^T (bf16 inputs; fp32 ones are narrowed to bf16 first)
-FP32_PADDED_HEAD_DIMS = {16: 32}
 
 # precision -> arithmetic of P and dS in the kernels.  The reference rounds P
 # to V's dtype for P V (original_kernel.py:566-571) and keeps P and dS in fp32
@@ -458,18 +456,14 @@ def _backward_x3(ctx, do, dlse, dplan):
 _fwd_x3_op.register_autograd(_backward_x3, setup_context=_setup_context_x3)
 
 
-def head_dim_route(dtype: torch.dtype, D: int, precision: str) -> tuple[bool, int]:
-    """Which kernels flash_attention runs for inputs of this dtype and head dim:
-    (bf16x3 ops?, zero-padded head dim or 0).  16-bit inputs go to the C ABI's
-    MFMA kernels at every head dim as they are (d = 16, 32 on the d = 64
-    kernels, which read the missing columns as zeros); fp32 takes bf16x3 at
-    "tf32" and d = 16, 32, else the C ABI's fp32 kernels with d = 16 padded to
-    32 (the fp32 MFMA's smallest)."""
-    if dtype != torch.float32:
-        return False, 0
-    if precision == "tf32" and D in X3_ROUTED_HEAD_DIMS:
-        return True, 0
-    return False, FP32_PADDED_HEAD_DIMS.get(D, 0)
+def head_dim_route(dtype: torch.dtype, D: int, precision: str) -> bool:
+    """Whether flash_attention runs inputs of this dtype, head dim and precision
+    on the bf16x3 ops (fp32 at "tf32" and d = 16, 32); everything else goes to
+    the C ABI's kernels as it is, with no padding: 16-bit inputs on the MFMA
+    kernels at every head dim (d = 16, 32 on the d = 64 kernels, which read the
+    missing columns as zeros), fp32 on the fp32 MFMA kernels (d = 16 on the
+    d = 32 ones, the same way)."""
+    return dtype == torch.float32 and precision == "tf32" and D in X3_ROUTED_HEAD_DIMS
 
 
 # -------------------------------------------------------------- public entry
@@ -522,7 +516,7 @@ def flash_attention(
     once to the input type instead (faster; 8 significant bits with bf16
     inputs).  fp32
     inputs get fp32 arithmetic at both "ieee" and "tf32": the fp32 MFMA
-    kernels at head dims 32, 64, 128, 256 (16 zero-padded to 32), except
+    kernels at every head dim, except
     "tf32" at 16 and 32, which runs as bf16x3
     on the 16-bit kernels (see head_dim_route).  O and the gradients stay fp32.
     ``attention_mask``'s contents are not
@@ -608,9 +602,7 @@ def flash_attention(
             fused_signs = signs
         else:
             q, k = _rot_op(q, signs, False), _rot_op(k, signs, False)
-    x3, pad_to = head_dim_route(q.dtype, D, precision)
-    if pad_to:  # after the rotation, which acts on the caller's head dim
-        q, k, v = (torch.nn.functional.pad(x, (0, pad_to - D)) for x in (q, k, v))
+    x3 = head_dim_route(q.dtype, D, precision)
     fp8 = ()
     if qk_dtype == "fp8_e4m3" and not hadamard:  # with Hadamard the op quantises Q R, K R itself
         (q8, q_scale), (k8, k_scale) = quantize_fp8(q), quantize_fp8(k)
@@ -630,8 +622,6 @@ def flash_attention(
                                      quant_fp8=hadamard and qk_dtype == "fp8_e4m3", prec=PRECISIONS[precision])
     if plan is not None:
         plan_t = plan.tensor
-    if pad_to:
-        o = o[..., :D]
     if in_dtype == torch.float32:
         o = o.to(torch.float32)
 

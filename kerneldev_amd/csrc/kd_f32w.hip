@@ -94,9 +94,11 @@ KD_DEV f32x4 mma16(float a, float b, const f32x4& c) { return __builtin_amdgcn_m
 // [T, row_bytes] slice into an LDS chunk: wave-wide 16-byte-per-lane loads of
 // 1 KiB (RPL rows each), lane l filling chunk position l % CPR of row
 // l / CPR of its load, i.e. the logical chunk whose position that is.  Rows
-// at or past T read as zeros.
+// at or past T read as zeros, and so do the columns from dbytes on (head dim
+// 16 on the WD = 32 kernels: their offsets go outside the buffer resource).
 template <int WD>
-KD_DEV void copy_chunk(const u32x4& rs, uint32_t r0, uint32_t row_bytes, uint32_t lds_chunk, int wave, int lane) {
+KD_DEV void copy_chunk(const u32x4& rs, uint32_t r0, uint32_t row_bytes, uint32_t lds_chunk, int wave, int lane,
+                       uint32_t dbytes) {
   using G = Geo<WD>;
 #pragma unroll
   for (int j = 0; j < G::LPW; ++j) {
@@ -104,19 +106,20 @@ KD_DEV void copy_chunk(const u32x4& rs, uint32_t r0, uint32_t row_bytes, uint32_
     const int rr = ld * G::RPL + lane / G::CPR, p = lane % G::CPR;  // row, position
     const int c = G::pos(rr, p);  // (pos is its own inverse for a fixed row)
     const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(int(lds_chunk + uint32_t(ld) * 1024u)));
-    dma_b128(rs, (r0 + uint32_t(rr)) * row_bytes + uint32_t(c) * 16u, m);
+    dma_b128(rs, col_masked((r0 + uint32_t(rr)) * row_bytes + uint32_t(c) * 16u, uint32_t(c) * 16u, dbytes), m);
   }
 }
 
-// this lane's row x[row][.] in k-step order: out[4u + t] = x[row][16u + 4g + t] * scale
+// this lane's row x[row][.] in k-step order: out[4u + t] = x[row][16u + 4g + t] * scale,
+// zero from column dreal on (a row of dreal < WD floats, not read past its end)
 template <int WD>
 KD_DEV void load_row16(const float* base, int64_t row_stride, int row, bool valid, int g, float scale,
-                       float (&out)[Geo<WD>::NR]) {
+                       float (&out)[Geo<WD>::NR], int dreal) {
   const float* p = base + int64_t(valid ? row : 0) * row_stride + 4 * g;  // row 0 stands in past T
   const float sc = valid ? scale : 0.f;
 #pragma unroll
   for (int u = 0; u < WD / 16; ++u) {
-    const f32x4 x = *reinterpret_cast<const f32x4*>(p + 16 * u);
+    const f32x4 x = 16 * u + 4 * g < dreal ? *reinterpret_cast<const f32x4*>(p + 16 * u) : f32x4{};
 #pragma unroll
     for (int t = 0; t < 4; ++t) out[4 * u + t] = x[t] * sc;
   }
@@ -196,15 +199,17 @@ KD_DEV void accumulate16(const uint8_t* chunk, int i, int g, const f32x4 (&s)[2]
   }
 }
 
-// store the [d][token] accumulators of this lane's token to row `out` (WD
-// floats), times scale: register r of block db is column NDB (4 g + r) + db
+// store the [d][token] accumulators of this lane's token to row `out`, times
+// scale: register r of block db is column NDB (4 g + r) + db; only the
+// columns below dreal (a multiple of NDB) are stored
 template <int WD>
-KD_DEV void store16(float* out, const f32x4 (&acc)[Geo<WD>::NDB], int g, float scale) {
+KD_DEV void store16(float* out, const f32x4 (&acc)[Geo<WD>::NDB], int g, float scale, int dreal) {
   constexpr int NDB = Geo<WD>::NDB;
   if constexpr (NDB == 2) {  // WD = 32
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      *reinterpret_cast<f32x2*>(out + 2 * (4 * g + r)) = f32x2{acc[0][r] * scale, acc[1][r] * scale};
+      if (2 * (4 * g + r) < dreal)
+        *reinterpret_cast<f32x2*>(out + 2 * (4 * g + r)) = f32x2{acc[0][r] * scale, acc[1][r] * scale};
     return;
   }
 #pragma unroll
@@ -255,6 +260,7 @@ __global__ __launch_bounds__(256, Geo<WD>::WAVES) void k_fwd_f32w(AttnArgs a, co
                                                      const uint32_t* __restrict__ order) {
   using G = Geo<WD>;
   constexpr int NR = G::NR, NDB = G::NDB;
+  const uint32_t dbytes = uint32_t(a.D) * 4u;  // a row of a.D <= WD floats (16 on the WD = 32 kernels)
   __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][G::CBYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][G::CBYTES];
   __shared__ __attribute__((aligned(256))) uint32_t s_kc[2][64];
@@ -275,7 +281,7 @@ __global__ __launch_bounds__(256, Geo<WD>::WAVES) void k_fwd_f32w(AttnArgs a, co
   uint32_t qcode = qvalid ? codes[int64_t(it.b) * T + q] : 0u;
 
   float qr[NR];
-  load_row16<WD>(qg, a.q_strides[2], q, qvalid, g, cs, qr);
+  load_row16<WD>(qg, a.q_strides[2], q, qvalid, g, cs, qr, a.D);
 
   const int lb = it.b * nblk + it.blk;
   const int n = count[lb];
@@ -283,8 +289,8 @@ __global__ __launch_bounds__(256, Geo<WD>::WAVES) void k_fwd_f32w(AttnArgs a, co
   // chunk (entry e, half hf): keys 64 tile + 32 hf .. + 31
   auto copy = [&](int e, int hf, int slot) {
     const uint32_t r0 = entry_tile(ent[e]) * 64u + uint32_t(32 * hf);
-    copy_chunk<WD>(rs_k, r0, krb, lds_addr(s_k[slot]), wave, lane);
-    copy_chunk<WD>(rs_v, r0, vrb, lds_addr(s_v[slot]), wave, lane);
+    copy_chunk<WD>(rs_k, r0, krb, lds_addr(s_k[slot]), wave, lane, dbytes);
+    copy_chunk<WD>(rs_v, r0, vrb, lds_addr(s_v[slot]), wave, lane, dbytes);
     if (wave == 0)
       dma_b32(rs_c, (r0 + uint32_t(lane)) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(s_kc[slot])))));
   };
@@ -346,7 +352,7 @@ __global__ __launch_bounds__(256, Geo<WD>::WAVES) void k_fwd_f32w(AttnArgs a, co
   if (!qvalid) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
   store16<WD>(static_cast<float*>(a.o) + it.b * a.o_strides[0] + it.hh * a.o_strides[1] + int64_t(q) * a.o_strides[2], o,
-          g, inv);
+          g, inv, a.D);
   if (g == 0 && a.lse != nullptr) a.lse[int64_t(bh) * T + q] = l > 0.f ? m + fast_log2(l) : -__builtin_inff();
 }
 
@@ -358,6 +364,7 @@ __global__ __launch_bounds__(256, Geo<WD>::WAVES) void k_dq_f32w(AttnArgs a, con
                                                     const uint32_t* __restrict__ order) {
   using G = Geo<WD>;
   constexpr int NR = G::NR, NDB = G::NDB;
+  const uint32_t dbytes = uint32_t(a.D) * 4u;  // a row of a.D <= WD floats (16 on the WD = 32 kernels)
   __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][G::CBYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][G::CBYTES];
   __shared__ __attribute__((aligned(256))) uint32_t s_kc[2][64];
@@ -383,16 +390,16 @@ __global__ __launch_bounds__(256, Geo<WD>::WAVES) void k_dq_f32w(AttnArgs a, con
   float ndelta = qvalid ? a.delta[int64_t(bh) * T + q] : 0.f;  // the workspace holds -Delta
 
   float qr[NR], dr[NR];
-  load_row16<WD>(qg, a.q_strides[2], q, qvalid, g, cs, qr);
-  load_row16<WD>(dog, a.do_strides[2], q, qvalid, g, 1.f, dr);
+  load_row16<WD>(qg, a.q_strides[2], q, qvalid, g, cs, qr, a.D);
+  load_row16<WD>(dog, a.do_strides[2], q, qvalid, g, 1.f, dr, a.D);
 
   const int lb = it.b * nblk + it.blk;
   const int n = count[lb];
   const uint32_t* ent = list + int64_t(lb) * nT;
   auto copy = [&](int e, int hf, int slot) {
     const uint32_t r0 = entry_tile(ent[e]) * 64u + uint32_t(32 * hf);
-    copy_chunk<WD>(rs_k, r0, krb, lds_addr(s_k[slot]), wave, lane);
-    copy_chunk<WD>(rs_v, r0, vrb, lds_addr(s_v[slot]), wave, lane);
+    copy_chunk<WD>(rs_k, r0, krb, lds_addr(s_k[slot]), wave, lane, dbytes);
+    copy_chunk<WD>(rs_v, r0, vrb, lds_addr(s_v[slot]), wave, lane, dbytes);
     if (wave == 0)
       dma_b32(rs_c, (r0 + uint32_t(lane)) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(s_kc[slot])))));
   };
@@ -446,7 +453,7 @@ __global__ __launch_bounds__(256, Geo<WD>::WAVES) void k_dq_f32w(AttnArgs a, con
   }
   if (!qvalid) return;
   store16<WD>(static_cast<float*>(a.dq) + it.b * a.dq_strides[0] + it.hh * a.dq_strides[1] + int64_t(q) * a.dq_strides[2],
-          dq, g, a.sm_scale);
+          dq, g, a.sm_scale, a.D);
 }
 
 // -------------------------------------------------------------------- dK/dV
@@ -457,6 +464,7 @@ __global__ __launch_bounds__(256, Geo<WD>::WAVES) void k_dkdv_f32w(AttnArgs a, c
                                                       const uint32_t* __restrict__ order) {
   using G = Geo<WD>;
   constexpr int NR = G::NR, NDB = G::NDB;
+  const uint32_t dbytes = uint32_t(a.D) * 4u;  // a row of a.D <= WD floats (16 on the WD = 32 kernels)
   __shared__ __attribute__((aligned(1024))) uint8_t s_q[2][G::CBYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_do[2][G::CBYTES];
   __shared__ __attribute__((aligned(256))) float s_lse[2][64];
@@ -482,8 +490,8 @@ __global__ __launch_bounds__(256, Geo<WD>::WAVES) void k_dkdv_f32w(AttnArgs a, c
   uint32_t kcode = kvalid ? codes[int64_t(it.b) * T + k] : 0u;
 
   float kr[NR], vr[NR];
-  load_row16<WD>(kg, a.k_strides[2], k, kvalid, g, cs, kr);
-  load_row16<WD>(vg, a.v_strides[2], k, kvalid, g, 1.f, vr);
+  load_row16<WD>(kg, a.k_strides[2], k, kvalid, g, cs, kr, a.D);
+  load_row16<WD>(vg, a.v_strides[2], k, kvalid, g, 1.f, vr, a.D);
 
   const int lb = it.b * nblk + it.blk;
   const int n = count[lb];
@@ -492,8 +500,8 @@ __global__ __launch_bounds__(256, Geo<WD>::WAVES) void k_dkdv_f32w(AttnArgs a, c
   // codes, LSE and -Delta (64 values copied, the first 32 used)
   auto copy = [&](int e, int hf, int slot) {
     const uint32_t r0 = entry_tile(ent[e]) * 64u + uint32_t(32 * hf);
-    copy_chunk<WD>(rs_q, r0, qrb, lds_addr(s_q[slot]), wave, lane);
-    copy_chunk<WD>(rs_do, r0, dorb, lds_addr(s_do[slot]), wave, lane);
+    copy_chunk<WD>(rs_q, r0, qrb, lds_addr(s_q[slot]), wave, lane, dbytes);
+    copy_chunk<WD>(rs_do, r0, dorb, lds_addr(s_do[slot]), wave, lane, dbytes);
     const uint32_t off = (r0 + uint32_t(lane)) * 4u;
     if (wave == 0) dma_b32(rs_c, off, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(s_qc[slot])))));
     if (wave == 1) dma_b32(rs_l, off, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(s_lse[slot])))));
@@ -557,9 +565,9 @@ __global__ __launch_bounds__(256, Geo<WD>::WAVES) void k_dkdv_f32w(AttnArgs a, c
   }
   if (!kvalid) return;
   store16<WD>(static_cast<float*>(a.dk) + it.b * a.dk_strides[0] + it.hh * a.dk_strides[1] + int64_t(k) * a.dk_strides[2],
-          dk, g, a.sm_scale);
+          dk, g, a.sm_scale, a.D);
   store16<WD>(static_cast<float*>(a.dv) + it.b * a.dv_strides[0] + it.hh * a.dv_strides[1] + int64_t(k) * a.dv_strides[2],
-          dv, g, 1.f);
+          dv, g, 1.f, a.D);
 }
 
 template <int WD>
@@ -582,12 +590,9 @@ void launch_f32w_d(int which, const AttnArgs& a, const uint8_t* plan, hipStream_
 
 }  // namespace
 
-bool use_f32mma(const AttnArgs& a) {
-  return a.dtype == KD_F32 && (a.D == 32 || a.D == 64 || a.D == 128 || a.D == 256);
-}
-
 int launch_f32mma(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   switch (a.D) {
+    case 16:  // on the WD = 32 kernels: columns 16-31 read as zeros, not stored
     case 32: launch_f32w_d<32>(which, a, plan, st); break;
     case 64: launch_f32w_d<64>(which, a, plan, st); break;
     case 128: launch_f32w_d<128>(which, a, plan, st); break;

@@ -56,13 +56,12 @@ int launch_quant(const kd_quant_args& a, hipStream_t st);
 int launch_absmax(const kd_quant_args& a, float* amax, hipStream_t st);
 int launch_span(const kd_span_args& a, hipStream_t st);
 int launch_span_bwd(const kd_span_args& a, hipStream_t st);
-// fp32 vector-ALU attention (kd_simt.hip) for fp32 inputs and head dims the
-// MFMA kernels are not built for; which: 0 forward, 1 Delta, 2 dQ, 3 dK/dV
+// fp32 inputs (kd_simt.hip): Delta on the vector ALUs and the fp32 MFMA
+// kernels; which: 0 forward, 1 Delta, 2 dQ, 3 dK/dV
 bool use_simt(const AttnArgs& a);
 int launch_simt_kernel(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st);
-// fp32 inputs at head dims 32, 64, 128, 256 on the fp32 MFMA (kd_f32w.hip);
-// which: 0 forward, 2 dQ, 3 dK/dV (Delta stays on k_delta_simt)
-bool use_f32mma(const AttnArgs& a);
+// fp32 attention at head dims 16 (on the 32 kernels), 32, 64, 128, 256 on the
+// fp32 MFMA (kd_f32w.hip); which: 0 forward, 2 dQ, 3 dK/dV
 int launch_f32mma(int which, const AttnArgs& a, const uint8_t* plan, hipStream_t st);
 // Device address of the no-allocation workspace on the current device
 // (kd_noalloc.hip); KD_OK, or a status with *err set.

@@ -268,7 +268,7 @@ def test_fp32_tf32_ops_directly(dev, D):
 @pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 def test_fp32_on_the_fp32_mfma_kernels(dev, D):
     """fp32 inputs at precision "ieee" run on the fp32 MFMA kernels (kd_f32w.hip
-    at head dims 32, 64, 128, 256, 16 zero-padded to 32), and so
+    at every head dim, 16 on the d = 32 kernels with no padding), and so
     does "tf32" at 64, 128 and 256: ragged T with lens (an
     empty batch row, a partial one), [B, T, H, D] memory viewed [B, H, T, D]
     (model.py:76-78) with cocktail-party metadata; rel-RMS <= 1e-5 against the

@@ -58,9 +58,9 @@ def test_head_dim_route():
 
     bf, f32 = torch.bfloat16, torch.float32
     # 16-bit inputs go to the MFMA kernels unpadded at every head dim
-    assert all(head_dim_route(bf, d, p) == (False, 0) for d in (16, 32, 64, 128, 256) for p in ("tf32", "ieee", "bf16"))
-    assert head_dim_route(torch.float16, 128, "ieee") == (False, 0)
-    assert head_dim_route(f32, 16, "tf32") == (True, 0) and head_dim_route(f32, 32, "tf32") == (True, 0)
-    assert head_dim_route(f32, 64, "tf32") == (False, 0) and head_dim_route(f32, 128, "tf32") == (False, 0)
-    assert head_dim_route(f32, 16, "ieee") == (False, 32) and head_dim_route(f32, 32, "ieee") == (False, 0)
-    assert head_dim_route(f32, 256, "ieee") == (False, 0)
+    assert not any(head_dim_route(bf, d, p) for d in (16, 32, 64, 128, 256) for p in ("tf32", "ieee", "bf16"))
+    assert not head_dim_route(torch.float16, 128, "ieee")
+    # fp32: bf16x3 at "tf32" and d = 16, 32; the fp32 MFMA kernels, unpadded, otherwise
+    assert head_dim_route(f32, 16, "tf32") and head_dim_route(f32, 32, "tf32")
+    assert not head_dim_route(f32, 64, "tf32") and not head_dim_route(f32, 128, "tf32")
+    assert not any(head_dim_route(f32, d, "ieee") for d in (16, 32, 64, 128, 256))
