@@ -6,9 +6,6 @@
 
 namespace kd {
 
-template <class E> KD_DEV float ld(const void* p, int64_t i);
-template <> KD_DEV float ld<F32>(const void* p, int64_t i) { return static_cast<const float*>(p)[i]; }
-
 template <int G> KD_DEV float group_sum(float x) {
 #pragma unroll
   for (int o = 1; o < G; o <<= 1) x += __shfl_xor(x, o, 64);
@@ -37,11 +34,17 @@ __global__ __launch_bounds__(256) void k_delta_simt(AttnArgs a) {
     const int t = int(r % a.T), bh = int(r / a.T), b = bh / a.H, h = bh % a.H;
     const int64_t ob = b * a.o_strides[0] + h * a.o_strides[1] + int64_t(t) * a.o_strides[2] + g * S::EL;
     const int64_t db = b * a.do_strides[0] + h * a.do_strides[1] + int64_t(t) * a.do_strides[2] + g * S::EL;
+    // 16-byte reads: rows and the lane's EL (a multiple of 4) elements are
+    // 16-byte aligned (the C ABI's stride and base checks); fp32 inputs carry
+    // no O residual (the C ABI refuses o_lo for them)
+    const float* op = static_cast<const float*>(a.o) + ob;
+    const float* dp = static_cast<const float*>(a.dout) + db;
 #pragma unroll
-    for (int d = 0; d < S::EL; ++d) {
-      float o = ld<E>(a.o, ob + d);
-      if (a.o_lo != nullptr) o += ld<E>(a.o_lo, r * D + g * S::EL + d);  // 16-bit O only (the C ABI refuses it for fp32)
-      sum = __builtin_fmaf(o, ld<E>(a.dout, db + d), sum);
+    for (int d = 0; d < S::EL; d += 4) {
+      const f32x4 o = *reinterpret_cast<const f32x4*>(op + d);
+      const f32x4 x = *reinterpret_cast<const f32x4*>(dp + d);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sum = __builtin_fmaf(o[j], x[j], sum);
     }
   }
   sum = group_sum<S::G>(sum);
