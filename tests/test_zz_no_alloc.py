@@ -25,19 +25,21 @@ pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def _backward_both(dev, B, H, T, D, seed):
+def _backward_both(dev, B, H, T, D, seed, dtype=torch.bfloat16):
     tokens, in_span, span_id, is_prefix = cocktail_batch(B, 1024, CONFIG3_LAYOUT, seed=seed)
     meta = [x[:, :T].to(dev) for x in (in_span, span_id, is_prefix)]
-    q, k, v, do = (x.to(dev) for x in qkvdo(B, H, T, D, seed=seed + 1))
+    q, k, v, do = (x.to(dev) for x in qkvdo(B, H, T, D, seed=seed + 1, dtype=dtype))
     sc = D ** -0.5
-    o, lse, plan, o_lo, *_ = _fwd_op(q, k, v, None, *meta, sc, 0, True)
+    fp32 = dtype == torch.float32  # (fp32 O carries no residual)
+    o, lse, plan, o_lo, *_ = _fwd_op(q, k, v, None, *meta, sc, 0, not fp32)
     lib = _lib.load()
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     outs = []
     for noalloc in (False, True):
         dq, dk, dv = torch.full_like(q, float("nan")), torch.full_like(k, float("nan")), torch.full_like(v, float("nan"))
         a = _attn_args(q, k, v, sc)
-        a.o, a.o_strides, a.lse, a.o_lo = o.data_ptr(), _strides3(o), lse.data_ptr(), o_lo.data_ptr()
+        a.o, a.o_strides, a.lse = o.data_ptr(), _strides3(o), lse.data_ptr()
+        a.o_lo = None if fp32 else o_lo.data_ptr()
         a.dout, a.do_strides = do.data_ptr(), _strides3(do)
         a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
         a.dq_strides, a.dk_strides, a.dv_strides = _strides3(dq), _strides3(dk), _strides3(dv)
@@ -54,9 +56,11 @@ def _backward_both(dev, B, H, T, D, seed):
 
 
 def test_noalloc_backward_matches_allocating_entry_point(dev):
-    for B, H, T, D, seed in ((2, 4, 1024, 128, 80), (1, 2, 300, 64, 82)):
-        print(f"noalloc backward B={B} H={H} T={T} D={D}", flush=True)
-        ref, got = _backward_both(dev, B, H, T, D, seed)
+    cases = ((2, 4, 1024, 128, 80, torch.bfloat16), (1, 2, 300, 64, 82, torch.bfloat16),
+             (1, 3, 700, 256, 84, torch.float32), (1, 2, 200, 16, 86, torch.float32))
+    for B, H, T, D, seed, dtype in cases:
+        print(f"noalloc backward B={B} H={H} T={T} D={D} {dtype}", flush=True)
+        ref, got = _backward_both(dev, B, H, T, D, seed, dtype)
         for name, x, y in zip(("dq", "dk", "dv"), ref, got):
             assert torch.isfinite(y).all(), name
             assert torch.equal(x, y), f"{name} differs (B={B} T={T} D={D})"
