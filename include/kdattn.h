@@ -21,7 +21,7 @@
  *   - Head dims 16, 32, 64, 128, 256 (original_kernel.py:1720).  bf16 / fp16
  *     run on the MFMA kernels at every head dim (16 and 32 on the D = 64
  *     kernels, which read the columns past D as zeros and store only the D
- *     real ones; dqk_signs at 64, 128 only; fp8 scores at 64, 128 for bf16); fp32 inputs
+ *     real ones; dqk_signs at 64, 128 only; fp8 scores at 64, 128, 256 for bf16); fp32 inputs
  *     on the fp32 MFMA kernels at every head dim (16 on the D = 32 kernels,
  *     the same way).  fp32 inputs get no fp8 scores and no dqk_signs,
  *     and precision is always full fp32 for them.  (The Python layer runs fp32 inputs at precision "tf32"

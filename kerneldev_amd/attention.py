@@ -30,15 +30,15 @@ from ._lib import AttnArgs, MetaArgs
 REFERENCE_HEAD_DIMS = (16, 32, 64, 128, 256)  # original_kernel.py:1720
 SUPPORTED_HEAD_DIMS = REFERENCE_HEAD_DIMS
 # bf16 / fp16 at these head dims run on the MFMA kernels with the fused
-# Hadamard epilogues and fp8 scores; 16, 32 and 256 run there without
-# them (16 and 32 on the d = 64 kernels, which read the missing columns as
-# zeros).  fp32
+# Hadamard epilogues; 16, 32 and 256 run there without them (16 and 32 on
+# the d = 64 kernels, which read the missing columns as zeros).  fp8 scores
+# are built at 64, 128 and 256.  fp32
 # inputs run on the fp32 MFMA kernels at every head dim (kd_f32w.hip; 16 on
 # the d = 32 kernels, which read the missing columns as zeros), except at
 # precision "tf32" and head dims 16, 32 (X3_ROUTED_HEAD_DIMS: bf16x3, faster
 # there)
 MFMA_HEAD_DIMS = (64, 128)
-FP8_HEAD_DIMS = (64, 128)  # fp8 e4m3 Q K^T (bf16 inputs; fp32 ones are narrowed to bf16 first)
+FP8_HEAD_DIMS = (64, 128, 256)  # fp8 e4m3 Q K^T (bf16 inputs; fp32 ones are narrowed to bf16 first)
 
 # precision -> arithmetic of P and dS in the kernels.  The reference rounds P
 # to V's dtype for P V (original_kernel.py:566-571) and keeps P and dS in fp32
@@ -587,25 +587,29 @@ def flash_attention(
         # fp8 scores come from bf16 operands: fp32 inputs are rounded to bf16
         # for this path and O cast back
         q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
-    from .hadamard import _rot_op, generate_hadamard_signs, quantize_fp8
+    from .hadamard import _rot_amax_op, _rot_op, generate_hadamard_signs, quantize_fp8
 
     fused_signs = None
+    amax = (None, None)
     if hadamard:
         # (Q R)(K R)^T = Q K^T with R = diag(s) H_d / sqrt(d).  On the MFMA
         # kernels the attention op rotates Q and K itself (fp8: the rotation
         # pass also yields the per-(b, h) absmax that scales the e4m3 copies),
         # and its backward kernels return dQ' R^T, dK' R^T directly.  Elsewhere
         # (fp32, other head dims) Q and K go through the differentiable
-        # rotation op first.
+        # rotation op first (fp8: the form whose pass also yields the absmax).
         signs = generate_hadamard_signs(D, hadamard_seed, device=device)
         if q.dtype != torch.float32 and D in MFMA_HEAD_DIMS:
             fused_signs = signs
+        elif qk_dtype == "fp8_e4m3":
+            (q, q_amax), (k, k_amax) = _rot_amax_op(q, signs), _rot_amax_op(k, signs)
+            amax = (q_amax, k_amax)
         else:
             q, k = _rot_op(q, signs, False), _rot_op(k, signs, False)
     x3 = head_dim_route(q.dtype, D, precision)
     fp8 = ()
-    if qk_dtype == "fp8_e4m3" and not hadamard:  # with Hadamard the op quantises Q R, K R itself
-        (q8, q_scale), (k8, k_scale) = quantize_fp8(q), quantize_fp8(k)
+    if qk_dtype == "fp8_e4m3" and fused_signs is None:  # fused: the op quantises Q R, K R itself
+        (q8, q_scale), (k8, k_scale) = quantize_fp8(q, amax[0]), quantize_fp8(k, amax[1])
         fp8 = (q8, k8, q_scale, k_scale)
 
     if x3:
@@ -619,7 +623,8 @@ def flash_attention(
         o, lse, plan_t, *_ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode),
                                      need_lo, *(fp8 or (None, None, None, None)), bthd=out_layout == "bthd",
                                      plan_in=None if plan is None else plan.tensor, signs=fused_signs,
-                                     quant_fp8=hadamard and qk_dtype == "fp8_e4m3", prec=PRECISIONS[precision])
+                                     quant_fp8=fused_signs is not None and qk_dtype == "fp8_e4m3",
+                                     prec=PRECISIONS[precision])
     if plan is not None:
         plan_t = plan.tensor
     if in_dtype == torch.float32:

@@ -207,8 +207,15 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
   using TL = Tile<D>;
   using SO = ScoreOp<E, D, Q8>;  // S^T = K Q^T (16-bit, or fp8 from the K8 tile)
   using TK8 = typename ScoreOp<E, D, true>::TL;
-  constexpr int DS = D / 16, DB = DH / 32, NL = TL::LOADS_PER_WAVE, NL8 = TK8::LOADS_PER_WAVE;
-  __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][TL::BYTES];
+  // fp8 scores (Q8) take S from the K8 tile, so the 16-bit K tile feeds only
+  // dQ^T += K^T dS^T, i.e. only this launch's columns [D0, D0 + DH): it is
+  // loaded DH wide (KHALF), which keeps the d = 256 launch's two slots of K,
+  // V and K8 within the LDS
+  constexpr bool KHALF = Q8 && DH < D;
+  using TLK = Tile<KHALF ? DH : D>;  // 16-bit K tiles
+  constexpr int DS = D / 16, DB = DH / 32, NL = TL::LOADS_PER_WAVE, NLK = TLK::LOADS_PER_WAVE,
+                NL8 = TK8::LOADS_PER_WAVE;
+  __shared__ __attribute__((aligned(1024))) uint8_t s_k[2][TLK::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_v[2][TL::BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t s_k8[Q8 ? 2 : 1][Q8 ? TK8::BYTES : 16];
   // the 64 key codes of each step's tile (lane = key), from which PARTIAL
@@ -322,8 +329,8 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
   const int n = count[lbase];
   const uint32_t* ent = list + int64_t(lbase) * nT;
 
-  uint32_t koff[NL], voff[NL], k8off[NL8];
-  TL::load_offsets(wave, lane, krb, koff, dbytes);
+  uint32_t koff[NLK], voff[NL], k8off[NL8];
+  TLK::load_offsets(wave, lane, krb, koff, KHALF ? uint32_t(DH) * 2u : dbytes);
   TL::load_offsets(wave, lane, vrb, voff, dbytes);
   TK8::load_offsets(wave, lane, uint32_t(D), k8off);
   const u32x4 rs_k8 = rsrc_words(Q8 ? a.k8 + int64_t(bh) * T * D : nullptr, Q8 ? uint32_t(T) * D : 0u);
@@ -331,7 +338,8 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
   // before this step's LDS reads, so tile e+1 loads during all of step e
   auto load_tile = [&](int kt, int buf) {
     const uint32_t k0 = uint32_t(kt) * 64u;
-    TL::load_async(rs_k, k0 * krb, koff, lds_addr(s_k[buf]), wave);
+    // (KHALF: the tile's columns start at D0 of the row)
+    TLK::load_async(rs_k, k0 * krb + (KHALF ? uint32_t(D0) * 2u : 0u), koff, lds_addr(s_k[buf]), wave);
     TL::load_async(rs_v, k0 * vrb, voff, lds_addr(s_v[buf]), wave);
     if constexpr (Q8) TK8::load_async(rs_k8, k0 * uint32_t(D), k8off, lds_addr(s_k8[buf]), wave);
   };
@@ -355,11 +363,15 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
   for (int st = 0; st < DS; ++st) raddr[st] = TL::at(srow, 2 * st + hf);
   int taddr_all[D / 32][2];
   tr_addrs<D>(lane, taddr_all);
-  int taddr[DB][2];  // the column blocks of this launch
+  int taddr[DB][2];  // the column blocks of this launch (KHALF: the DH-wide tile's own)
+  if constexpr (KHALF) {
+    tr_addrs<DH>(lane, taddr);
+  } else {
 #pragma unroll
-  for (int db = 0; db < DB; ++db) {
-    taddr[db][0] = taddr_all[D0 / 32 + db][0];
-    taddr[db][1] = taddr_all[D0 / 32 + db][1];
+    for (int db = 0; db < DB; ++db) {
+      taddr[db][0] = taddr_all[D0 / 32 + db][0];
+      taddr[db][1] = taddr_all[D0 / 32 + db][1];
+    }
   }
 
   // the fp8 product carries the dequantisation scales of Q and K
@@ -481,8 +493,8 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void k_dq(AttnArgs a, const 
       constexpr int NS = 4 * DB, PF = DQ_PF;
       auto read = [&](int i) {
         const int t4 = i / DB, db = i % DB;
-        const u32x2 lo = ds_read_tr16(kt + taddr[db][0] + t4 * 16 * TL::ROWB);
-        const u32x2 hi = ds_read_tr16(kt + taddr[db][1] + t4 * 16 * TL::ROWB);
+        const u32x2 lo = ds_read_tr16(kt + taddr[db][0] + t4 * 16 * TLK::ROWB);
+        const u32x2 hi = ds_read_tr16(kt + taddr[db][1] + t4 * 16 * TLK::ROWB);
         return u32x4{lo[0], lo[1], hi[0], hi[1]};
       };
       u32x4 av[PF];
@@ -962,17 +974,25 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
 // blocks, read transposed).  Two launches (D0 = 0, 128) give the whole
 // gradient, each recomputing S and dP.  Tiles are copied one step ahead into
 // two slots (2 x 2 x 32 KiB).
-template <class E, int D, int NSP, int DH, int D0>
+template <class E, int D, int NSP, int DH, int D0, bool Q8 = false>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, const uint32_t* __restrict__ codes,
                                                       const uint32_t* __restrict__ list,
                                                       const int32_t* __restrict__ count,
                                                       const uint32_t* __restrict__ order, int nT, int nKB) {
   constexpr bool SP = NSP >= 2, S3 = NSP == 3;
   using TL = Tile<D, 4>;
-  constexpr int DS = D / 16, NL = TL::LOADS_PER_WAVE;
+  // fp8 scores (Q8): S^T comes from the e4m3 Q8 tile and this lane's K8 row,
+  // so the 16-bit Q tile feeds only dK^T += Q^T dS, i.e. only this launch's
+  // columns [D0, D0 + DH): it is loaded DH wide (QHALF), which keeps the d = 256
+  // launch's two slots of Q, Q8 and dO within the LDS
+  constexpr bool QHALF = Q8 && DH < D;
+  using TLQ = Tile<QHALF ? DH : D, 4>;    // 16-bit Q tiles
+  using TQ8 = Tile<Q8 ? D / 2 : D, 4>;    // e4m3 Q tiles (D bytes a row), with Q8
+  constexpr int DS = D / 16, NL = TL::LOADS_PER_WAVE, NLQ = TLQ::LOADS_PER_WAVE, NL8 = TQ8::LOADS_PER_WAVE;
   constexpr int HB = DH / 32, HB0 = D0 / 32;  // column blocks of this launch
   constexpr int NSL = 2;                      // slots per stream (copies one step ahead)
-  __shared__ __attribute__((aligned(1024))) uint8_t s_q[NSL][TL::BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_q[NSL][TLQ::BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_q8[Q8 ? NSL : 1][Q8 ? TQ8::BYTES : 16];
   __shared__ __attribute__((aligned(1024))) uint8_t s_do[NSL][TL::BYTES];
   __shared__ __attribute__((aligned(256))) float s_lse[NSL][64];
   __shared__ __attribute__((aligned(256))) float s_delta[NSL][64];
@@ -1004,14 +1024,24 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
   // bytes of a row of the 16-bit inputs: 2 D, or fewer for head dims 16 and
   // 32 on the D = 64 kernel, whose other columns are read as zeros
   const uint32_t dbytes = uint32_t(a.D) * 2u;
-  u32x4 bk[DS], bv[DS];  // this lane's K and V rows (B operands of S^T, dP^T)
+  u32x4 bk[Q8 ? 1 : DS], bv[DS];  // this lane's K and V rows (B operands of S^T, dP^T)
+  i32x8 bk8[Q8 ? D / 64 : 1];      // fp8: its K8 row instead, k-step st = bytes 64 st + 32 hf .. + 31
   {
     const auto rk = make_rsrc(kg, uint32_t(T) * krb), rv = make_rsrc(vg, uint32_t(T) * vrb);
 #pragma unroll
     for (int st = 0; st < DS; ++st) {
       const uint32_t col = (16 * st + 8 * hf) * 2;
-      bk[st] = buf_load16(rk, col_masked(uint32_t(krow) * krb + col, col, dbytes));
+      if constexpr (!Q8) bk[st] = buf_load16(rk, col_masked(uint32_t(krow) * krb + col, col, dbytes));
       bv[st] = buf_load16(rv, col_masked(uint32_t(krow) * vrb + col, col, dbytes));
+    }
+    if constexpr (Q8) {
+      const auto rs8 = make_rsrc(a.k8 + int64_t(bh) * T * D, uint32_t(T) * D);
+#pragma unroll
+      for (int st = 0; st < D / 64; ++st) {
+        const u32x4 lo = buf_load16(rs8, uint32_t(krow) * D + 64 * st + 32 * hf);
+        const u32x4 hi = buf_load16(rs8, uint32_t(krow) * D + 64 * st + 32 * hf + 16);
+        bk8[st] = i32x8{int(lo[0]), int(lo[1]), int(lo[2]), int(lo[3]), int(hi[0]), int(hi[1]), int(hi[2]), int(hi[3])};
+      }
     }
   }
   const int member = wave >> 1;
@@ -1021,13 +1051,17 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
   const int n = count[lbase];
   const uint32_t* ent = list + int64_t(lbase) * nT;
 
-  uint32_t qoff[NL], dooff[NL];
-  TL::load_offsets(wave, lane, qrb, qoff, dbytes);
+  uint32_t qoff[NLQ], dooff[NL], q8off[NL8];
+  TLQ::load_offsets(wave, lane, qrb, qoff, QHALF ? uint32_t(DH) * 2u : dbytes);
   TL::load_offsets(wave, lane, dorb, dooff, dbytes);
+  if constexpr (Q8) TQ8::load_offsets(wave, lane, uint32_t(D), q8off);
+  const u32x4 rs_q8 = rsrc_words(Q8 ? a.q8 + int64_t(bh) * T * D : nullptr, Q8 ? uint32_t(T) * D : 0u);
   auto load_tile = [&](uint32_t en, int slot) {
     const uint32_t q0 = entry_tile(en) * 64u;
-    TL::load_async(rs_q, q0 * qrb, qoff, lds_addr(s_q[slot]), wave);
+    // (QHALF: the tile's columns start at D0 of the row)
+    TLQ::load_async(rs_q, q0 * qrb + (QHALF ? uint32_t(D0) * 2u : 0u), qoff, lds_addr(s_q[slot]), wave);
     TL::load_async(rs_do, q0 * dorb, dooff, lds_addr(s_do[slot]), wave);
+    if constexpr (Q8) TQ8::load_async(rs_q8, q0 * uint32_t(D), q8off, lds_addr(s_q8[Q8 ? slot : 0]), wave);
     if (wave == 1)
       dma_b32(rs_lse, (q0 + lane) * 4u, uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(&s_lse[slot][0])))));
     else if (wave == 2)
@@ -1048,8 +1082,17 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
     taddr[db][0] = taddr_all[HB0 + db][0];
     taddr[db][1] = taddr_all[HB0 + db][1];
   }
+  // the transposed reads of the Q tile: as for dO, or the DH-wide tile's own blocks (QHALF)
+  int taddr_q[HB][2];
+  if constexpr (QHALF) {
+    tr_addrs<DH>(lane, taddr_q);
+  } else {
+#pragma unroll
+    for (int db = 0; db < HB; ++db) taddr_q[db][0] = taddr[db][0], taddr_q[db][1] = taddr[db][1];
+  }
 
-  const float sl2 = a.sm_scale * 1.4426950408889634f;
+  // the fp8 product carries the dequantisation scales of Q and K
+  const float sl2 = a.sm_scale * 1.4426950408889634f * (Q8 ? a.q_scale[bh] * a.k_scale[bh] : 1.f);
   f32x16 acc_v[HB], acc_k[HB];  // dV^T, dK^T for this launch's columns
 #pragma unroll
   for (int db = 0; db < HB; ++db) acc_v[db] = acc_k[db] = f32x16{};
@@ -1070,14 +1113,18 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
     }
     __builtin_amdgcn_sched_barrier(0x406);
   };
+  // q_c: a std::integral_constant, true for the Q tile (TLQ's layout), false for dO
   auto accumulate = [&](const uint8_t* at_g, f32x16 (&acc)[HB], const u32x4 (&bop)[2][2],
-                        const u32x4 (&bopl)[2][2], const u32x4 (&bopm)[2][2]) {
+                        const u32x4 (&bopl)[2][2], const u32x4 (&bopm)[2][2], auto q_c) {
+    constexpr bool IS_Q = decltype(q_c)::value;
+    constexpr int ROWB = IS_Q ? TLQ::ROWB : TL::ROWB;
+    const int (&ta)[HB][2] = IS_Q ? taddr_q : taddr;
     lds_u8* at = to_lds(at_g);
     constexpr int NS = 4 * HB;
     auto read = [&](int i) {
-      const int k4 = i / HB, db = i % HB, off = k4 * 16 * TL::ROWB;
-      const u32x2 lo = ds_read_tr16(at + taddr[db][0] + off);
-      const u32x2 hi = ds_read_tr16(at + taddr[db][1] + off);
+      const int k4 = i / HB, db = i % HB, off = k4 * 16 * ROWB;
+      const u32x2 lo = ds_read_tr16(at + ta[db][0] + off);
+      const u32x2 hi = ds_read_tr16(at + ta[db][1] + off);
       return u32x4{lo[0], lo[1], hi[0], hi[1]};
     };
     u32x4 av[PF];
@@ -1114,8 +1161,12 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
   wait_vmem();
 #pragma unroll
   for (int st = 0; st < DS; ++st) {
-    settle(bk[st]);
+    if constexpr (!Q8) settle(bk[st]);
     settle(bv[st]);
+  }
+  if constexpr (Q8) {
+#pragma unroll
+    for (int st = 0; st < D / 64; ++st) settle(bk8[st]);
   }
   settle(kcode);
   uint32_t en_cur = n > 0 ? ent[0] : 0u, en_next = n > 1 ? ent[1] : 0u;  // entries of tiles e, e + 1
@@ -1136,7 +1187,22 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
     f32x16 x[2], y[2];  // S^T - LSE / c and dP^T - Delta
     splat_rows(s_lse[slot], x);
     splat_rows(s_delta[slot], y);
-    rows_times_b(s_q[slot], bk, x);
+    if constexpr (Q8) {  // S^T = Q8 K8^T on the fp8 MFMA; A = Q8 rows, 32 bytes per lane and k-step
+      const uint8_t* t8 = s_q8[Q8 ? slot : 0];
+#pragma unroll
+      for (int st = 0; st < D / 64; ++st) {
+        const int a0 = TQ8::at(srow, 4 * st + 2 * hf), a1 = TQ8::at(srow, 4 * st + 2 * hf + 1);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          const u32x4 lo = *reinterpret_cast<const u32x4*>(t8 + a0 + qb * 32 * TQ8::ROWB);
+          const u32x4 hi = *reinterpret_cast<const u32x4*>(t8 + a1 + qb * 32 * TQ8::ROWB);
+          const i32x8 av = {int(lo[0]), int(lo[1]), int(lo[2]), int(lo[3]), int(hi[0]), int(hi[1]), int(hi[2]), int(hi[3])};
+          x[qb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bk8[st], x[qb], 0, 0, 0, 127, 0, 127);
+        }
+      }
+    } else {
+      rows_times_b(s_q[slot], bk, x);
+    }
     rows_times_b(s_do[slot], bv, y);
     const uint32_t mcls = entry_class(en, member);
     if (mcls != TILE_FULL) {  // wave-uniform
@@ -1172,8 +1238,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, 
           sm[qb][t] = pack8_residual2<E>(ds, sb[qb][t], sl_[qb][t]);
         }
       }
-    accumulate(s_do[slot], acc_v, pb, pl, pm);  // dV^T += dO^T P
-    accumulate(s_q[slot], acc_k, sb, sl_, sm);  // dK^T += Q^T dS
+    accumulate(s_do[slot], acc_v, pb, pl, pm, std::false_type{});  // dV^T += dO^T P
+    accumulate(s_q[slot], acc_k, sb, sl_, sm, std::true_type{});    // dK^T += Q^T dS
   };
   if constexpr (D <= 64) {
     for (int e = 0; e < n; e += 2) {
@@ -1248,21 +1314,21 @@ template <class E, int D, bool Q8, int NSP>
 static void launch_dkdv_s(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   const PlanLayout L = plan_layout(a.B, a.T, a.D);
   const unsigned grid = unsigned(a.B) * a.H * L.n_dkdv_blocks;
-  if constexpr (D == 64 && !Q8) {  // one launch, all four products per wave (fp8 scores: the wave pairs below)
-    hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 64, 0>), dim3(grid), dim3(256), 0, st, a,
+  if constexpr (D == 64) {  // one launch, all four products per wave (fp8 scores too)
+    hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 64, 0, Q8>), dim3(grid), dim3(256), 0, st, a,
                        reinterpret_cast<const uint32_t*>(plan + L.codes),
                        reinterpret_cast<const uint32_t*>(plan + L.dkdv_list),
                        reinterpret_cast<const int32_t*>(plan + L.dkdv_count),
                        reinterpret_cast<const uint32_t*>(plan + L.dkdv_order), L.nT, L.n_dkdv_blocks);
-  } else if constexpr (D == 256) {  // two launches, the column halves of dK and dV
+  } else if constexpr (D == 256) {  // two launches, the column halves of dK and dV (fp8 scores too)
     auto* codes = reinterpret_cast<const uint32_t*>(plan + L.codes);
     auto* list = reinterpret_cast<const uint32_t*>(plan + L.dkdv_list);
     auto* cnt = reinterpret_cast<const int32_t*>(plan + L.dkdv_count);
     auto* order = reinterpret_cast<const uint32_t*>(plan + L.dkdv_order);
-    hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 128, 0>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, order,
+    hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 128, 0, Q8>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, order,
                        L.nT, L.n_dkdv_blocks);
-    hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 128, 128>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt, order,
-                       L.nT, L.n_dkdv_blocks);
+    hipLaunchKernelGGL((k_dkdv_wide<E, D, NSP, 128, 128, Q8>), dim3(grid), dim3(256), 0, st, a, codes, list, cnt,
+                       order, L.nT, L.n_dkdv_blocks);
   } else {
     hipLaunchKernelGGL((k_dkdv<E, D, Q8, NSP>), dim3(grid), dim3(512), 0, st, a,
                        reinterpret_cast<const uint32_t*>(plan + L.codes),
@@ -1319,18 +1385,20 @@ int launch_dq(const AttnArgs& a, const uint8_t* plan, hipStream_t st, bool fuse_
     const int r = fuse_delta ? launch_simt_kernel(1, a, plan, st) : KD_OK;
     return r ? r : launch_simt_kernel(2, a, plan, st);
   }
-  if (a.q8 != nullptr) {  // fp8 QK^T: bf16 at head dim 64 or 128 (checked by the C ABI)
+  if (a.q8 != nullptr) {  // fp8 QK^T: bf16 at head dim 64, 128 or 256 (checked by the C ABI)
     if (a.D == 64) launch_dq_t<BF16, 64, true>(a, plan, st, fuse_delta);
-    else launch_dq_t<BF16, 128, true>(a, plan, st, fuse_delta);
+    else if (a.D == 128) launch_dq_t<BF16, 128, true>(a, plan, st, fuse_delta);
+    else launch_dq_t<BF16, 256, true>(a, plan, st, fuse_delta);
   }
   else KD_DISPATCH(launch_dq_t, a, plan, st, fuse_delta);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 int launch_dkdv(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   if (use_simt(a)) return launch_simt_kernel(3, a, plan, st);
-  if (a.q8 != nullptr) {  // fp8 QK^T: bf16 at head dim 64 or 128 (checked by the C ABI)
+  if (a.q8 != nullptr) {  // fp8 QK^T: bf16 at head dim 64, 128 or 256 (checked by the C ABI)
     if (a.D == 64) launch_dkdv_t<BF16, 64, true>(a, plan, st);
-    else launch_dkdv_t<BF16, 128, true>(a, plan, st);
+    else if (a.D == 128) launch_dkdv_t<BF16, 128, true>(a, plan, st);
+    else launch_dkdv_t<BF16, 256, true>(a, plan, st);
   }
   else KD_DISPATCH(launch_dkdv_t, a, plan, st);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;

@@ -181,7 +181,8 @@ int kd_plan_build_tokens(const kd_token_args* t, void* plan, int64_t plan_bytes,
 int kd_quant_fp8(const kd_quant_args* a, void* stream) {
   if (a == nullptr) return fail(KD_ERR_INVALID, "args is NULL");
   if (a->B < 1 || a->H < 1 || a->T < 1) return fail(KD_ERR_INVALID, "B, H and T must be >= 1");
-  if (a->D != 64 && a->D != 128) return fail(KD_ERR_UNSUPPORTED, "head dim must be 64 or 128");
+  if (a->D != 64 && a->D != 128 && a->D != 256)
+    return fail(KD_ERR_UNSUPPORTED, "head dim must be 64, 128 or 256");
   if (a->dtype != KD_BF16 && a->dtype != KD_F16) return fail(KD_ERR_UNSUPPORTED, "dtype must be bf16 or fp16");
   if (a->amax == nullptr || a->scale == nullptr || a->y == nullptr)
     return fail(KD_ERR_INVALID, "amax, scale and y are required");
@@ -262,7 +263,8 @@ static int check_fp8(const kd_attn_args* a) {
   if (a->q8 == nullptr) return KD_OK;
   if (a->precision == KD_PREC_SPLIT3)
     return fail(KD_ERR_UNSUPPORTED, "KD_PREC_SPLIT3 is not built with fp8 scores");
-  if (a->D != 64 && a->D != 128) return fail(KD_ERR_UNSUPPORTED, "the fp8 QK^T path is built for head dims 64 and 128");
+  if (a->D != 64 && a->D != 128 && a->D != 256)
+    return fail(KD_ERR_UNSUPPORTED, "the fp8 QK^T path is built for head dims 64, 128 and 256");
   if (a->dtype != KD_BF16) return fail(KD_ERR_UNSUPPORTED, "the fp8 QK^T path is built for bf16");
   if (!aligned16(a->q8) || !aligned16(a->k8)) return fail(KD_ERR_INVALID, "q8 and k8 must be 16-byte aligned");
   if (a->q_scale == nullptr || a->k_scale == nullptr) return fail(KD_ERR_INVALID, "q_scale and k_scale are required");

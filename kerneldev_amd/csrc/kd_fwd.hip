@@ -379,9 +379,10 @@ static void launch_fwd_p(const AttnArgs& a, const uint8_t* plan, hipStream_t st)
 
 int launch_fwd(const AttnArgs& a, const uint8_t* plan, hipStream_t st) {
   if (use_simt(a)) return launch_simt_kernel(0, a, plan, st);
-  if (a.q8 != nullptr) {  // fp8 QK^T: bf16 at head dim 64 or 128 (checked by the C ABI)
+  if (a.q8 != nullptr) {  // fp8 QK^T: bf16 at head dim 64, 128 or 256 (checked by the C ABI)
     if (a.D == 64) launch_fwd_p<BF16, 64, true>(a, plan, st);
-    else launch_fwd_p<BF16, 128, true>(a, plan, st);
+    else if (a.D == 128) launch_fwd_p<BF16, 128, true>(a, plan, st);
+    else launch_fwd_p<BF16, 256, true>(a, plan, st);
   } else if (a.dtype == KD_BF16) {  // head dims 16 and 32 on the D = 64 kernel
     if (a.D <= 64) launch_fwd_p<BF16, 64>(a, plan, st);
     else if (a.D == 128) launch_fwd_p<BF16, 128>(a, plan, st);

@@ -209,17 +209,30 @@ __global__ __launch_bounds__(256) void k_quant8(kd_quant_args a) {
 }
 
 // ---- per-(b, h) max |x| -----------------------------------------------------
-// One 1024-thread workgroup per (b, h) reads its T x D slice in 16-byte
-// chunks (8 elements), four chunks in flight per thread.  The magnitudes of
-// non-negative bf16 / fp16 values order as their bit patterns do, so the
-// reduction runs on 15-bit integers (the sign bit cleared) and the maximum is
-// converted to fp32 once: exact, and independent of the order of the fold.
-// Written straight to amax[b H + h] (no zeroing, no atomics).
+// S B H workgroups, S a (b, h): the S 1024-thread workgroups stride over its
+// T x D slice in 16-byte chunks (8 elements), four chunks in flight per
+// thread; S is chosen so that about 256 workgroups (one a CU, 16 waves each)
+// fill the chip whatever B H is, with few atomics meeting at one address.  The magnitudes of non-negative bf16 / fp16 values order as their
+// bit patterns do, so the reduction runs on 15-bit integers (the sign bit
+// cleared); a workgroup converts its maximum to fp32 once and folds it into
+// amax[b H + h] with an integer atomic max on the float's bits, which
+// non-negative floats order by too: exact, and independent of the order of
+// the fold.  k_zero_f32 clears amax first, on the same stream.  A workgroup
+// first reads amax[b H + h] and skips the atomic when the value there is
+// already at least its own: amax only grows, so a stale read can only cost an
+// atomic, never lose one.  (Device-scope atomics from the eight XCDs onto the
+// few cache lines of amax serialise: 16 times the workgroups, four thousand
+// atomics onto 64 heads, took several times as long as the reads.)
+__global__ __launch_bounds__(256) void k_zero_f32(float* __restrict__ p, int n) {
+  const int i = int(blockIdx.x) * 256 + int(threadIdx.x);
+  if (i < n) p[i] = 0.f;
+}
+
 template <class E>
-__global__ __launch_bounds__(1024) void k_absmax(kd_quant_args a, float* __restrict__ amax) {
-  const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H, tid = threadIdx.x;
-  const int cpr = a.D / 8;  // 16-byte chunks per row
-  const int64_t n = int64_t(a.T) * cpr;
+__global__ __launch_bounds__(1024) void k_absmax(kd_quant_args a, float* __restrict__ amax, int cpr_log2, int S) {
+  const int bh = int(blockIdx.x) / S, part = int(blockIdx.x) % S, b = bh / a.H, h = bh % a.H, tid = threadIdx.x;
+  const int64_t n = int64_t(a.T) << cpr_log2;  // chunks in the slice (D / 8 a row, a power of two)
+  const int cmask = (1 << cpr_log2) - 1;
   const uint16_t* base = static_cast<const uint16_t*>(a.x) + b * a.x_strides[0] + h * a.x_strides[1];
   uint32_t m = 0;
   auto fold = [&](const u32x4& v) {
@@ -227,19 +240,18 @@ __global__ __launch_bounds__(1024) void k_absmax(kd_quant_args a, float* __restr
     for (int j = 0; j < 4; ++j) m = max(m, max(v[j] & 0x7FFFu, (v[j] >> 16) & 0x7FFFu));
   };
   auto chunk = [&](int64_t i) {
-    const int64_t t = i / cpr;
-    const int c = int(i - t * cpr);
-    return *reinterpret_cast<const u32x4*>(base + t * a.x_strides[2] + c * 8);
+    return *reinterpret_cast<const u32x4*>(base + (i >> cpr_log2) * a.x_strides[2] + (int(i) & cmask) * 8);
   };
-  int64_t i = tid;
-  for (; i + 3 * 1024 < n; i += 4 * 1024) {
-    const u32x4 v0 = chunk(i), v1 = chunk(i + 1024), v2 = chunk(i + 2048), v3 = chunk(i + 3072);
+  const int64_t step = int64_t(S) * 1024;
+  int64_t i = int64_t(part) * 1024 + tid;
+  for (; i + 3 * step < n; i += 4 * step) {
+    const u32x4 v0 = chunk(i), v1 = chunk(i + step), v2 = chunk(i + 2 * step), v3 = chunk(i + 3 * step);
     fold(v0);
     fold(v1);
     fold(v2);
     fold(v3);
   }
-  for (; i < n; i += 1024) fold(chunk(i));
+  for (; i < n; i += step) fold(chunk(i));
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) m = max(m, uint32_t(__shfl_xor(int(m), off, 64)));
   __shared__ uint32_t s_m[16];
@@ -247,15 +259,25 @@ __global__ __launch_bounds__(1024) void k_absmax(kd_quant_args a, float* __restr
   __syncthreads();
   if (tid == 0) {
     uint32_t r = 0;
+#pragma unroll
     for (int w = 0; w < 16; ++w) r = max(r, s_m[w]);
-    amax[bh] = to_f32<E>(uint16_t(r));
+    unsigned int* dst = reinterpret_cast<unsigned int*>(amax) + bh;
+    const unsigned int bits = __float_as_uint(to_f32<E>(uint16_t(r)));
+    if (r != 0u && __hip_atomic_load(dst, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < bits) atomicMax(dst, bits);
   }
 }
 
 int launch_absmax(const kd_quant_args& a, float* amax, hipStream_t st) {
-  const dim3 grid(unsigned(int64_t(a.B) * a.H)), block(1024);
-  if (a.dtype == KD_BF16) hipLaunchKernelGGL(k_absmax<BF16>, grid, block, 0, st, a, amax);
-  else hipLaunchKernelGGL(k_absmax<F16>, grid, block, 0, st, a, amax);
+  const int bh = a.B * a.H;
+  const int cpr_log2 = __builtin_ctz(unsigned(a.D / 8));
+  const int64_t chunks = int64_t(a.T) << cpr_log2;
+  const int64_t per_bh = (chunks + 4095) / 4096;  // workgroups that each take four chunks a thread
+  const int want = bh >= 256 ? 1 : 256 / bh;
+  const int S = int(per_bh < want ? per_bh : want);
+  hipLaunchKernelGGL(k_zero_f32, dim3(unsigned((bh + 255) / 256)), dim3(256), 0, st, amax, bh);
+  const dim3 grid(unsigned(int64_t(S) * bh)), block(1024);
+  if (a.dtype == KD_BF16) hipLaunchKernelGGL(k_absmax<BF16>, grid, block, 0, st, a, amax, cpr_log2, S);
+  else hipLaunchKernelGGL(k_absmax<F16>, grid, block, 0, st, a, amax, cpr_log2, S);
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }
 
@@ -269,10 +291,12 @@ static void launch_quant_t(const kd_quant_args& a, hipStream_t st) {
 int launch_quant(const kd_quant_args& a, hipStream_t st) {
   if (a.dtype == KD_BF16) {
     if (a.D == 64) launch_quant_t<BF16, 64>(a, st);
-    else launch_quant_t<BF16, 128>(a, st);
+    else if (a.D == 128) launch_quant_t<BF16, 128>(a, st);
+    else launch_quant_t<BF16, 256>(a, st);
   } else {
     if (a.D == 64) launch_quant_t<F16, 64>(a, st);
-    else launch_quant_t<F16, 128>(a, st);
+    else if (a.D == 128) launch_quant_t<F16, 128>(a, st);
+    else launch_quant_t<F16, 256>(a, st);
   }
   return hipGetLastError() == hipSuccess ? KD_OK : KD_ERR_LAUNCH;
 }

@@ -187,8 +187,8 @@ def quantize_fp8(x: torch.Tensor, amax: torch.Tensor | None = None):
     """
     if x.dim() != 4 or x.dtype not in (torch.bfloat16, torch.float16) or not x.is_cuda:
         raise ValueError("x must be a bf16 / fp16 [batch, heads, time, head_dim] GPU tensor")
-    if x.shape[-1] not in (64, 128):
-        raise ValueError(f"head_dim must be 64 or 128, got {x.shape[-1]}")
+    if x.shape[-1] not in (64, 128, 256):
+        raise ValueError(f"head_dim must be 64, 128 or 256, got {x.shape[-1]}")
     if amax is None:
         amax = _absmax_op(x.detach())
     if amax.shape != x.shape[:2] or amax.dtype != torch.float32 or amax.device != x.device:

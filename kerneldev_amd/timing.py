@@ -1,6 +1,7 @@
 """Time ``flash_attention`` forward + backward at a given shape and dtype.
 
 ``python -m kerneldev_amd.timing --dtype fp32 --B 2 --H 8 --T 4096 --D 128``
+(``--qk-dtype fp8_e4m3`` and ``--hadamard`` as ``flash_attention`` takes them)
 
 Causal attention (``--no-causal``: all keys) on seeded N(0, 1) inputs, through
 the public API exactly as a model calls it (plan, forward, backward).  It runs
@@ -25,14 +26,15 @@ from .synth import qkvdo
 DTYPES = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}
 
 
-def time_step(B, H, T, D, dtype, precision="tf32", causal=True, steps=10, warmup=3, seed=1):
+def time_step(B, H, T, D, dtype, precision="tf32", causal=True, steps=10, warmup=3, seed=1, qk_dtype="bf16",
+              hadamard=False):
     """Seconds per fwd+bwd step and the step's allowed score entries."""
     dev = torch.device("cuda:0")
     q, k, v, do = (x.to(dev) for x in qkvdo(B, H, T, D, seed=seed, dtype=dtype))
     q, k, v = (x.requires_grad_(True) for x in (q, k, v))
 
     def step():
-        o = flash_attention(q, k, v, causal=causal, precision=precision)
+        o = flash_attention(q, k, v, causal=causal, precision=precision, qk_dtype=qk_dtype, hadamard=hadamard)
         o.backward(do)
 
     for _ in range(warmup):
@@ -118,6 +120,8 @@ def main():
     ap.add_argument("--T", type=int, default=4096)
     ap.add_argument("--D", type=int, nargs="+", default=[128])
     ap.add_argument("--no-causal", action="store_true")
+    ap.add_argument("--qk-dtype", default="bf16", choices=("bf16", "fp8_e4m3"))
+    ap.add_argument("--hadamard", action="store_true")
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     args = ap.parse_args()
@@ -130,8 +134,8 @@ def main():
         return
     for D in args.D:
         s, nnz = time_step(args.B, args.H, args.T, D, DTYPES[args.dtype], args.precision, not args.no_causal,
-                           args.steps, args.warmup)
-        print(f"{args.dtype} {args.precision} B={args.B} H={args.H} T={args.T} D={D} "
+                           args.steps, args.warmup, qk_dtype=args.qk_dtype, hadamard=args.hadamard)
+        print(f"{args.dtype} {args.precision} qk {args.qk_dtype}{' hadamard' if args.hadamard else ''} B={args.B} H={args.H} T={args.T} D={D} "
               f"{'all keys' if args.no_causal else 'causal'}: {s * 1e3:.3f} ms fwd+bwd, "
               f"{14 * D * nnz / s / 1e12:.1f} TFLOP/s useful", flush=True)
 

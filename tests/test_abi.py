@@ -84,7 +84,7 @@ def test_bad_arguments_return_status_without_gpu():
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID
     assert "overlap" in lib.kd_last_error_string().decode()
     a.q_strides[:] = [1024, 1024, 64]
-    a.q8 = 64  # fp8 operands: q8 without k8, then fp16 inputs (fp8 scores are built for bf16 at 64 / 128)
+    a.q8 = 64  # fp8 operands: q8 without k8, then fp16 inputs (fp8 scores are built for bf16 at 64 / 128 / 256)
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID
     assert "q8 and k8" in lib.kd_last_error_string().decode()
     a.k8 = 64
@@ -99,6 +99,10 @@ def test_bad_arguments_return_status_without_gpu():
     assert "SPLIT3" in lib.kd_last_error_string().decode()
     a.precision = _lib.KD_PREC_SPLIT
     assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID  # no scales
+    assert "scale" in lib.kd_last_error_string().decode()
+    a.D = 256  # head dim 256 passes the fp8 checks as far as the scales too
+    a.q_strides[:] = [4096, 4096, 256]
+    assert lib.kd_attn_fwd(ctypes.byref(a), ctypes.c_void_p(16), BIG, null) == _lib.KD_ERR_INVALID
     assert "scale" in lib.kd_last_error_string().decode()
     b = _lib.AttnArgs()  # the backward's rounding-residual outputs: 16-bit MFMA paths only, aligned
     b.B, b.H, b.T, b.D, b.dtype, b.sm_scale = 1, 1, 16, 64, _lib.KD_F32, 0.125
@@ -125,6 +129,8 @@ def test_bad_arguments_return_status_without_gpu():
     qa = _lib.QuantArgs()
     qa.B, qa.H, qa.T, qa.D, qa.dtype = 1, 1, 4, 128, _lib.KD_BF16
     assert lib.kd_quant_fp8(ctypes.byref(qa), null) == _lib.KD_ERR_INVALID  # amax / scale / y missing
+    qa.D = 256
+    assert lib.kd_quant_fp8(ctypes.byref(qa), null) == _lib.KD_ERR_INVALID  # 256 is built; buffers still missing
     qa.D = 96
     assert lib.kd_quant_fp8(ctypes.byref(qa), null) == _lib.KD_ERR_UNSUPPORTED
     buf = ctypes.c_void_p(256)  # never dereferenced on the host

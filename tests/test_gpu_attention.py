@@ -772,6 +772,51 @@ def test_fp8_head_dim_64_cases(dev, case):
           precision=rng.choice(["tf32", "bf16"]), **kw)
 
 
+@pytest.mark.parametrize("case", range(6))
+def test_fp8_head_dim_256_cases(dev, case):
+    """fp8 e4m3 scores at head dim 256 (the forward, dQ and dK/dV kernels at D = 256, whose
+    16-bit operand tiles are loaded 128 columns wide beside the full-width fp8 ones; the
+    Hadamard rotation as its own pass, which also yields the absmax): seeded B, H, ragged T,
+    causal or cocktail-party metadata, lens, Hadamard on or off, split or single rounding;
+    against the oracle fed the same e4m3 operands."""
+    import random
+
+    rng = random.Random(400 + case)
+    B, H, T = rng.choice([1, 2]), rng.choice([1, 2]), rng.choice([1, 64, 130, 513, 1024])
+    seed = rng.randrange(1 << 20)
+    q, k, v, do = qkvdo(B, H, T, 256, seed=seed, dtype=torch.bfloat16)
+    inp = dict(name=f"fp8 d256 {case} B{B} H{H} T{T}", q=q, k=k, v=v, do=do, causal=rng.random() < 0.6)
+    if rng.random() < 0.6:
+        _, in_span, span_id, is_prefix = cocktail_batch(B, max(T, 1170), CONFIG3_LAYOUT, seed=seed)
+        inp.update(in_span=in_span[:, :T].contiguous(), span_id=span_id[:, :T].contiguous(),
+                   is_prefix=is_prefix[:, :T].contiguous())
+    kw = {}
+    if rng.random() < 0.3:
+        kw["lens"] = torch.tensor([rng.randint(0, T) for _ in range(B)], dtype=torch.int32)
+    _case(inp, dev, qk_dtype="fp8_e4m3", hadamard=case in (1, 3) or rng.random() < 0.3, hadamard_seed=case % 5,
+          precision=rng.choice(["tf32", "bf16"]), **kw)
+
+
+@pytest.mark.parametrize("D", [128, 256])
+@pytest.mark.parametrize("hadamard", [False, True])
+def test_fp8_fp32_inputs_are_the_bf16_run(dev, D, hadamard):
+    """fp8 scores come from bf16 operands: fp32 inputs are rounded to bf16 on the
+    way in (and dO on the way back), so fp32 inputs that hold bf16 values give
+    the bf16 run's O and gradients, bit for bit, in fp32."""
+    q, k, v, do = qkvdo(2, 2, 300, D, seed=70 + D, dtype=torch.bfloat16)
+    outs = {}
+    for dt in (torch.bfloat16, torch.float32):
+        print(f"fp8 D={D} hadamard={hadamard} {dt} inputs", flush=True)
+        x = [t.to(dev).to(dt).requires_grad_() for t in (q, k, v)]
+        o = flash_attention(*x, causal=True, qk_dtype="fp8_e4m3", hadamard=hadamard, hadamard_seed=2)
+        o.backward(do.to(dev).to(dt))
+        torch.cuda.synchronize()
+        assert o.dtype == dt and all(t.grad.dtype == dt for t in x)
+        outs[dt] = [o.detach()] + [t.grad for t in x]
+    for name, a, b in zip(("o", "dq", "dk", "dv"), outs[torch.bfloat16], outs[torch.float32]):
+        assert torch.equal(a.float(), b), name
+
+
 @pytest.mark.parametrize("case", range(8))
 def test_strided_layouts_random(dev, case):
     """q, k, v and dO as views of larger buffers: rows padded (t-stride d + 0 / 8 / 24) and

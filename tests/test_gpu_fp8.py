@@ -53,7 +53,28 @@ def test_absmax_exact(dev, D, dtype):
     assert torch.equal(got.cpu(), base.transpose(1, 2).float().abs().amax(dim=(2, 3)))
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("B,H,T,D", [(32, 64, 64, 128), (8, 100, 300, 256), (1, 3, 70000, 32), (2, 8, 4096, 256)])
+def test_absmax_split_over_workgroups(dev, B, H, T, D):
+    """kd_absmax splits each (b, h) over up to 256 / (B H) workgroups that stride over
+    it and fold their maxima atomically: many heads (one workgroup each, several strides),
+    a long head (69 workgroups) and 16 heads of 16 workgroups, two strides each.  Outliers sit in the last chunk,
+    on stride boundaries and in every head's last row; one head is all zeros."""
+    print(f"absmax split B={B} H={H} T={T} D={D}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(B * H + T)
+    x = torch.randn(B, H, T, D, generator=g, device=dev).to(torch.bfloat16)
+    x[-1, -1, -1, -1] = -4096.0
+    flat = x.view(B * H, -1)
+    for j, pos in enumerate((256 * 8 - 1, 512 * 8, 1024 * 8 + 3)):
+        if pos < flat.shape[1]:
+            flat[j % (B * H), pos] = 77.0 + j
+    x[:, :, -1, 0] = 50.0
+    x[0, 0] = 0
+    got = _absmax_op(x)
+    torch.cuda.synchronize()
+    assert torch.equal(got, x.float().abs().amax(dim=(2, 3)))
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_quantize_bit_exact(dev, D, dtype):
     print(f"fp8 quantiser D={D} {dtype}", flush=True)
