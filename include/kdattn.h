@@ -198,7 +198,8 @@ typedef struct kd_span_args {
 /* Library version (major*10000 + minor*100 + patch).  3.0.0: the plan's size
  * beside its pointer in every entry point that takes a plan.  3.1.0:
  * kd_plan_layout writes 20 offsets (the dK/dV work order added).  3.2.0:
- * kd_absmax added. */
+ * kd_absmax added.  3.3.0: fp8 scores (q8 / k8) and kd_quant_fp8 at head
+ * dim 256. */
 int kd_version(void);
 
 /* Message for the last non-zero status returned on this thread. */

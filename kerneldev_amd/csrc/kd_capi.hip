@@ -118,7 +118,7 @@ int check_plan(const void* plan, int64_t plan_bytes, int B, int T, int D) {
 
 extern "C" {
 
-int kd_version(void) { return 30200; }
+int kd_version(void) { return 30300; }
 
 const char* kd_last_error_string(void) { return g_err.c_str(); }
 

@@ -38,7 +38,8 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_struct_layouts_and_version():
     lib = _lib.load()  # load() itself checks the three struct sizes
-    assert lib.kd_version() >= 30200  # 3.0: plan sizes at the boundary; 3.1: the dK/dV work order; 3.2: kd_absmax
+    # 3.0: plan sizes at the boundary; 3.1: the dK/dV work order; 3.2: kd_absmax; 3.3: fp8 scores at d = 256
+    assert lib.kd_version() >= 30300
     assert ctypes.sizeof(_lib.AttnArgs) % 8 == 0
 
 
