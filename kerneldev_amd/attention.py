@@ -220,20 +220,26 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
     # a caller's plan is used as is (and not returned: outputs may not alias inputs)
     plan = plan_in if plan_in is not None else build_plan(B, T, D, q.device, mode, in_span, span_id, is_prefix, lens)
     # signs: attention of Q R and K R, returned for the backward (which hands
-    # back dQ, dK for q, k themselves); with quant_fp8 the scores come from
-    # e4m3 copies of Q R and K R, scaled by the rotation pass's absmax, also
-    # returned.  Every unused output is its own empty tensor (outputs may not alias).
+    # back dQ, dK for q, k themselves).  quant_fp8: the scores come from e4m3
+    # copies of the (rotated) Q and K, made here and returned, scaled by the
+    # rotation pass's absmax or, without one, by kd_absmax's.  Every unused
+    # output is its own empty tensor (outputs may not alias).
     q_r, k_r = q.new_empty(0), k.new_empty(0)
     q8_o, k8_o = q.new_empty(0, dtype=torch.uint8), k.new_empty(0, dtype=torch.uint8)
     qs_o, ks_o = q.new_empty(0, dtype=torch.float32), k.new_empty(0, dtype=torch.float32)
+    from .hadamard import _absmax_launch, _launch, _quant_launch
     if signs is not None:
-        from .hadamard import _launch, _quant_op
+        # (the rotation folds its absmax into amax with atomics: zeroed first)
         amax = torch.zeros((2, B, H), dtype=torch.float32, device=q.device) if quant_fp8 else None
         q = q_r = _launch(q, signs, False, None if amax is None else amax[0])
         k = k_r = _launch(k, signs, False, None if amax is None else amax[1])
-        if quant_fp8:
-            (q8_o, qs_o), (k8_o, ks_o) = _quant_op(q_r, amax[0]), _quant_op(k_r, amax[1])
-            q8, k8, q_scale, k_scale = q8_o, k8_o, qs_o, ks_o
+    elif quant_fp8:
+        amax = torch.empty((2, B, H), dtype=torch.float32, device=q.device)
+        _absmax_launch(q, amax[0])
+        _absmax_launch(k, amax[1])
+    if quant_fp8:
+        (q8_o, qs_o), (k8_o, ks_o) = _quant_launch(q, amax[0]), _quant_launch(k, amax[1])
+        q8, k8, q_scale, k_scale = q8_o, k8_o, qs_o, ks_o
     o = _new_out(B, H, T, D, q, bthd)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
     # rounding residual of O, kept for the backward's Delta (see kd_bwd.hip)
@@ -252,8 +258,8 @@ def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_l
               q_scale=None, k_scale=None, bthd=False, plan_in=None, signs=None, quant_fp8=False, prec=0):
     B, H, T, D = q.shape
     rot_shape = (B, H, T, D) if signs is not None else (0,)
-    q8_shape = (B, H, T, D) if signs is not None and quant_fp8 else (0,)
-    sc_shape = (B, H) if signs is not None and quant_fp8 else (0,)
+    q8_shape = (B, H, T, D) if quant_fp8 else (0,)
+    sc_shape = (B, H) if quant_fp8 else (0,)
     return (_new_out(B, H, T, D, q, bthd),
             torch.empty((B, H, T), dtype=torch.float32, device=q.device),
             torch.empty(_lib.plan_nbytes(B, T, D) if plan_in is None else 0, dtype=torch.uint8, device=q.device),
@@ -306,7 +312,7 @@ def _setup_context(ctx, inputs, output):
     if plan_in is not None:
         plan = plan_in
     ctx.mark_non_differentiable(q_r, k_r, q8_o, k8_o, qs_o, ks_o)
-    if signs is not None and quant_fp8:
+    if quant_fp8:
         q8, k8, q_scale, k_scale = q8_o, k8_o, qs_o, ks_o
     ctx.fp8 = q8 is not None
     ctx.rot = signs is not None
@@ -587,30 +593,23 @@ def flash_attention(
         # fp8 scores come from bf16 operands: fp32 inputs are rounded to bf16
         # for this path and O cast back
         q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
-    from .hadamard import _rot_amax_op, _rot_op, generate_hadamard_signs, quantize_fp8
+    from .hadamard import _rot_op, generate_hadamard_signs
 
     fused_signs = None
-    amax = (None, None)
     if hadamard:
         # (Q R)(K R)^T = Q K^T with R = diag(s) H_d / sqrt(d).  On the MFMA
         # kernels the attention op rotates Q and K itself (fp8: the rotation
         # pass also yields the per-(b, h) absmax that scales the e4m3 copies),
         # and its backward kernels return dQ' R^T, dK' R^T directly.  Elsewhere
         # (fp32, other head dims) Q and K go through the differentiable
-        # rotation op first (fp8: the form whose pass also yields the absmax).
+        # rotation op first.  With fp8 scores the attention op quantises the
+        # Q and K it attends with (after the rotation) itself.
         signs = generate_hadamard_signs(D, hadamard_seed, device=device)
         if q.dtype != torch.float32 and D in MFMA_HEAD_DIMS:
             fused_signs = signs
-        elif qk_dtype == "fp8_e4m3":
-            (q, q_amax), (k, k_amax) = _rot_amax_op(q, signs), _rot_amax_op(k, signs)
-            amax = (q_amax, k_amax)
         else:
             q, k = _rot_op(q, signs, False), _rot_op(k, signs, False)
     x3 = head_dim_route(q.dtype, D, precision)
-    fp8 = ()
-    if qk_dtype == "fp8_e4m3" and fused_signs is None:  # fused: the op quantises Q R, K R itself
-        (q8, q_scale), (k8, k_scale) = quantize_fp8(q, amax[0]), quantize_fp8(k, amax[1])
-        fp8 = (q8, k8, q_scale, k_scale)
 
     if x3:
         # fp32 at the reference's default precision: bf16x3 on the MFMA kernels
@@ -621,10 +620,9 @@ def flash_attention(
         need_lo = (q.dtype != torch.float32 and torch.is_grad_enabled()
                    and any(x.requires_grad for x in (q, k, v)))
         o, lse, plan_t, *_ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode),
-                                     need_lo, *(fp8 or (None, None, None, None)), bthd=out_layout == "bthd",
+                                     need_lo, None, None, None, None, bthd=out_layout == "bthd",
                                      plan_in=None if plan is None else plan.tensor, signs=fused_signs,
-                                     quant_fp8=fused_signs is not None and qk_dtype == "fp8_e4m3",
-                                     prec=PRECISIONS[precision])
+                                     quant_fp8=qk_dtype == "fp8_e4m3", prec=PRECISIONS[precision])
     if plan is not None:
         plan_t = plan.tensor
     if in_dtype == torch.float32:

@@ -104,11 +104,10 @@ def _rot_amax_backward(ctx, gy, gamax):
 _rot_amax_op.register_autograd(_rot_amax_backward, setup_context=_rot_amax_setup)
 
 
-@torch.library.custom_op("kdattn::quant", mutates_args=(), device_types=("cuda",))
-def _quant_op(x: torch.Tensor, amax: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    from .attention import _dtype_code, _kernel_ready
+def _quant_launch(x: torch.Tensor, amax: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """kd_quant_fp8 of a kernel-ready bf16 / fp16 [B, H, T, d] tensor with its fp32 [B, H] amax."""
+    from .attention import _dtype_code
 
-    x = _kernel_ready(x)
     B, H, T, D = x.shape
     y = torch.empty((B, H, T, D), dtype=torch.uint8, device=x.device)
     scale = torch.empty((B, H), dtype=torch.float32, device=x.device)
@@ -123,20 +122,24 @@ def _quant_op(x: torch.Tensor, amax: torch.Tensor) -> tuple[torch.Tensor, torch.
     return y, scale
 
 
+@torch.library.custom_op("kdattn::quant", mutates_args=(), device_types=("cuda",))
+def _quant_op(x: torch.Tensor, amax: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    from .attention import _kernel_ready
+
+    return _quant_launch(_kernel_ready(x), amax)
+
+
 @_quant_op.register_fake
 def _quant_fake(x, amax):
     return (torch.empty(x.shape, dtype=torch.uint8, device=x.device),
             torch.empty(x.shape[:2], dtype=torch.float32, device=x.device))
 
 
-@torch.library.custom_op("kdattn::absmax", mutates_args=(), device_types=("cuda",))
-def _absmax_op(x: torch.Tensor) -> torch.Tensor:
-    """max |x| per (b, h) of a bf16 / fp16 [B, H, T, d] tensor (kd_absmax), exact in fp32."""
-    from .attention import _dtype_code, _kernel_ready
+def _absmax_launch(x: torch.Tensor, amax: torch.Tensor) -> torch.Tensor:
+    """kd_absmax of a kernel-ready bf16 / fp16 [B, H, T, d] tensor into the contiguous fp32 [B, H] amax."""
+    from .attention import _dtype_code
 
-    x = _kernel_ready(x)
     B, H, T, D = x.shape
-    amax = torch.empty((B, H), dtype=torch.float32, device=x.device)
     a = QuantArgs()
     a.x, a.x_strides = x.data_ptr(), _strides3(x)
     a.B, a.H, a.T, a.D = B, H, T, D
@@ -144,6 +147,15 @@ def _absmax_op(x: torch.Tensor) -> torch.Tensor:
     stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
     _lib.check(_lib.load().kd_absmax(ctypes.byref(a), ctypes.c_void_p(amax.data_ptr()), stream), "kd_absmax")
     return amax
+
+
+@torch.library.custom_op("kdattn::absmax", mutates_args=(), device_types=("cuda",))
+def _absmax_op(x: torch.Tensor) -> torch.Tensor:
+    """max |x| per (b, h) of a bf16 / fp16 [B, H, T, d] tensor (kd_absmax), exact in fp32."""
+    from .attention import _kernel_ready
+
+    x = _kernel_ready(x)
+    return _absmax_launch(x, torch.empty(x.shape[:2], dtype=torch.float32, device=x.device))
 
 
 @_absmax_op.register_fake

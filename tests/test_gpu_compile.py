@@ -2,8 +2,8 @@
 runs its op inside torch.compile(fullgraph=True, dynamic=True), with fake
 implementations at :1781-1803 and :1901-1923).
 
-* torch.library.opcheck on kdattn::fwd, kdattn::bwd, kdattn::fwd_x3, kdattn::bwd_x3,
-  kdattn::rot and kdattn::quant:
+* torch.library.opcheck on kdattn::fwd (also quantising Q and K for fp8 scores),
+  kdattn::bwd, kdattn::fwd_x3, kdattn::bwd_x3, kdattn::rot and kdattn::quant:
   schema, autograd registration, fake kernels against the real outputs, and
   AOT dispatch with dynamic shapes.
 * flash_attention under torch.compile(fullgraph=True), static and dynamic
@@ -36,6 +36,19 @@ def test_opcheck_forward_and_backward_ops(dev):
     o, lse, plan, o_lo, *_ = _fwd_op(q, k, v, None, *meta, sc, _lib.KD_MODE_FORMULA, True)
     print("opcheck kdattn::bwd", flush=True)
     torch.library.opcheck(_bwd_op, (q, k, v, o, lse, do, plan, sc, o_lo))
+
+
+@pytest.mark.parametrize("D,rotate", [(128, True), (128, False), (256, False)])
+def test_opcheck_forward_op_with_fp8_scores(dev, D, rotate):
+    """kdattn::fwd quantising Q and K itself (quant_fp8): the e4m3 copies and scales it returns
+    come after its fused rotation's absmax, or from kd_absmax without one."""
+    q, k, v, do, meta = _inputs(dev, D=D)
+    sc = D ** -0.5
+    signs = generate_hadamard_signs(D, 1, device=dev) if rotate else None
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
+    print(f"opcheck kdattn::fwd with fp8 scores, D={D} rotate={rotate}", flush=True)
+    torch.library.opcheck(_fwd_op, (qg, kg, vg, None, *meta, sc, _lib.KD_MODE_FORMULA, True),
+                          {"signs": signs, "quant_fp8": True})
 
 
 def test_opcheck_fp32_bf16x3_ops(dev):
