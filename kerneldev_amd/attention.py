@@ -207,8 +207,6 @@ def _fp8_tuple(q8, k8, q_scale, k_scale):
 def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tensor | None,
             in_span: torch.Tensor | None, span_id: torch.Tensor | None,
             is_prefix: torch.Tensor | None, sm_scale: float, mode: int, need_lo: bool,
-            q8: torch.Tensor | None = None, k8: torch.Tensor | None = None,
-            q_scale: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
             bthd: bool = False, plan_in: torch.Tensor | None = None, signs: torch.Tensor | None = None,
             quant_fp8: bool = False, prec: int = 0,
             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
@@ -223,7 +221,9 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
     # back dQ, dK for q, k themselves).  quant_fp8: the scores come from e4m3
     # copies of the (rotated) Q and K, made here and returned, scaled by the
     # rotation pass's absmax or, without one, by kd_absmax's.  Every unused
-    # output is its own empty tensor (outputs may not alias).
+    # output is its own empty tensor (outputs may not alias).  (The autograd
+    # wrapper's per-call cost grows with the square of the argument count, so
+    # the op takes no fp8 tensors of a caller's: it makes them itself.)
     q_r, k_r = q.new_empty(0), k.new_empty(0)
     q8_o, k8_o = q.new_empty(0, dtype=torch.uint8), k.new_empty(0, dtype=torch.uint8)
     qs_o, ks_o = q.new_empty(0, dtype=torch.float32), k.new_empty(0, dtype=torch.float32)
@@ -239,13 +239,12 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
         _absmax_launch(k, amax[1])
     if quant_fp8:
         (q8_o, qs_o), (k8_o, ks_o) = _quant_launch(q, amax[0]), _quant_launch(k, amax[1])
-        q8, k8, q_scale, k_scale = q8_o, k8_o, qs_o, ks_o
     o = _new_out(B, H, T, D, q, bthd)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
     # rounding residual of O, kept for the backward's Delta (see kd_bwd.hip)
     o_lo = torch.empty((B, H, T, D) if need_lo else (0,), dtype=_lo_dtype(q.dtype, prec), device=q.device)
     a = _attn_args(q, k, v, sm_scale, prec)
-    _set_fp8(a, _fp8_tuple(q8, k8, q_scale, k_scale))
+    _set_fp8(a, (q8_o, k8_o, qs_o, ks_o) if quant_fp8 else None)
     a.o, a.o_strides = o.data_ptr(), _strides3(o)
     a.lse = lse.data_ptr()
     a.o_lo = o_lo.data_ptr() if need_lo else None
@@ -254,8 +253,8 @@ def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tenso
 
 
 @_fwd_op.register_fake
-def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8=None, k8=None,
-              q_scale=None, k_scale=None, bthd=False, plan_in=None, signs=None, quant_fp8=False, prec=0):
+def _fwd_fake(q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, bthd=False, plan_in=None,
+              signs=None, quant_fp8=False, prec=0):
     B, H, T, D = q.shape
     rot_shape = (B, H, T, D) if signs is not None else (0,)
     q8_shape = (B, H, T, D) if quant_fp8 else (0,)
@@ -306,19 +305,17 @@ def _bwd_fake(q, k, v, o, lse, do, plan, sm_scale, o_lo, q8=None, k8=None, q_sca
 
 
 def _setup_context(ctx, inputs, output):
-    (q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, q8, k8, q_scale, k_scale, bthd, plan_in,
-     signs, quant_fp8, prec) = inputs
+    (q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, need_lo, bthd, plan_in, signs, quant_fp8,
+     prec) = inputs
     o, lse, plan, o_lo, q_r, k_r, q8_o, k8_o, qs_o, ks_o = output
     if plan_in is not None:
         plan = plan_in
     ctx.mark_non_differentiable(q_r, k_r, q8_o, k8_o, qs_o, ks_o)
-    if quant_fp8:
-        q8, k8, q_scale, k_scale = q8_o, k8_o, qs_o, ks_o
-    ctx.fp8 = q8 is not None
+    ctx.fp8 = quant_fp8
     ctx.rot = signs is not None
     if ctx.rot:  # the backward recomputes from the rotated operands and rotates dQ, dK back
         q, k = q_r, k_r
-    extra = (q8, k8, q_scale, k_scale) if ctx.fp8 else ()
+    extra = (q8_o, k8_o, qs_o, ks_o) if ctx.fp8 else ()
     ctx.save_for_backward(q, k, v, o, lse, plan, o_lo, *((signs,) if ctx.rot else ()), *extra)
     ctx.sm_scale = sm_scale
     ctx.prec = prec
@@ -332,7 +329,7 @@ def _backward(ctx, do, dlse, dplan, do_lo, *_unused):
     signs = rest.pop(0) if ctx.rot else None
     fp8 = tuple(rest) if ctx.fp8 else (None, None, None, None)
     dq, dk, dv = _bwd_op(q, k, v, o, lse, do, plan, ctx.sm_scale, o_lo, *fp8, dqk_signs=signs, prec=ctx.prec)
-    return (dq, dk, dv) + (None,) * 16
+    return (dq, dk, dv) + (None,) * 12
 
 
 _fwd_op.register_autograd(_backward, setup_context=_setup_context)
@@ -620,7 +617,7 @@ def flash_attention(
         need_lo = (q.dtype != torch.float32 and torch.is_grad_enabled()
                    and any(x.requires_grad for x in (q, k, v)))
         o, lse, plan_t, *_ = _fwd_op(q, k, v, lens, in_span, span_id, is_prefix, float(sm_scale), int(mode),
-                                     need_lo, None, None, None, None, bthd=out_layout == "bthd",
+                                     need_lo, bthd=out_layout == "bthd",
                                      plan_in=None if plan is None else plan.tensor, signs=fused_signs,
                                      quant_fp8=qk_dtype == "fp8_e4m3", prec=PRECISIONS[precision])
     if plan is not None:
