@@ -310,7 +310,12 @@ def _setup_context(ctx, inputs, output):
     o, lse, plan, o_lo, q_r, k_r, q8_o, k8_o, qs_o, ks_o = output
     if plan_in is not None:
         plan = plan_in
-    ctx.mark_non_differentiable(q_r, k_r, q8_o, k8_o, qs_o, ks_o)
+    # O's residual and the fp8 / rotated copies are internal; LSE stays
+    # differentiable but its gradient is ignored, so the gradients of unused
+    # outputs are left as None rather than filled with zeros (o_lo's fill alone
+    # would write B H T d 16-bit zeros every backward)
+    ctx.mark_non_differentiable(q_r, k_r, q8_o, k8_o, qs_o, ks_o, o_lo)
+    ctx.set_materialize_grads(False)
     ctx.fp8 = quant_fp8
     ctx.rot = signs is not None
     if ctx.rot:  # the backward recomputes from the rotated operands and rotates dQ, dK back
@@ -325,6 +330,8 @@ def _backward(ctx, do, dlse, dplan, do_lo, *_unused):
     # dlse is ignored, as in original_kernel.py:1965-1992.  With fp8 scores the
     # backward recomputes P from the same fp8 Q8 K8^T and forms dQ = dS K,
     # dK = dS^T Q from the 16-bit operands: the straight-through estimator.
+    if do is None:  # O did not reach the loss (only LSE did, whose gradient is ignored)
+        return (None,) * 15
     q, k, v, o, lse, plan, o_lo, *rest = ctx.saved_tensors
     signs = rest.pop(0) if ctx.rot else None
     fp8 = tuple(rest) if ctx.fp8 else (None, None, None, None)
@@ -447,10 +454,13 @@ def _setup_context_x3(ctx, inputs, output):
     q, k, v, lens, in_span, span_id, is_prefix, sm_scale, mode, bthd, plan_in = inputs
     o, lse, plan = output
     ctx.save_for_backward(q, k, v, o, lse, plan_in if plan_in is not None else plan)
+    ctx.set_materialize_grads(False)  # (LSE's gradient is ignored: no zeros made for it)
     ctx.sm_scale = sm_scale
 
 
 def _backward_x3(ctx, do, dlse, dplan):
+    if do is None:  # only LSE reached the loss
+        return (None,) * 11
     q, k, v, o, lse, plan = ctx.saved_tensors
     dq, dk, dv = _bwd_x3_op(q, k, v, o, lse, do, plan, ctx.sm_scale)
     return (dq, dk, dv) + (None,) * 8

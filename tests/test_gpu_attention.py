@@ -797,6 +797,32 @@ def test_fp8_head_dim_256_cases(dev, case):
           precision=rng.choice(["tf32", "bf16"]), **kw)
 
 
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.float32, 32)])
+def test_lse_gradient_is_ignored(dev, dtype, D):
+    """The gradient reaching LSE is ignored, as original_kernel.py:1965-1992 ignores dlse:
+    a loss on O and LSE gives the gradients of the loss on O alone, bit for bit, and a
+    loss on LSE alone leaves q, k, v without a gradient (the ops hand unused outputs'
+    gradients on as None instead of zero tensors).  bf16 at d = 64 runs kdattn::fwd,
+    fp32 at d = 32 the bf16x3 op kdattn::fwd_x3."""
+    q, k, v, do = qkvdo(2, 2, 200, D, seed=80 + D, dtype=dtype)
+    grads = []
+    for with_lse in (False, True):
+        print(f"LSE gradient {dtype} D={D} loss on O{' and LSE' if with_lse else ''}", flush=True)
+        x = [t.to(dev).requires_grad_() for t in (q, k, v)]
+        o, lse = flash_attention(*x, causal=True, return_lse=True)
+        loss = (o.float() * do.to(dev).float()).sum() + (3 * lse.sum() if with_lse else 0)
+        loss.backward()
+        torch.cuda.synchronize()
+        grads.append([t.grad for t in x])
+    for name, a, b in zip(("dq", "dk", "dv"), *grads):
+        assert torch.equal(a, b), name
+    x = [t.to(dev).requires_grad_() for t in (q, k, v)]
+    _, lse = flash_attention(*x, causal=True, return_lse=True)
+    lse.sum().backward()
+    torch.cuda.synchronize()
+    assert all(t.grad is None for t in x)
+
+
 @pytest.mark.parametrize("D", [128, 256])
 @pytest.mark.parametrize("hadamard", [False, True])
 def test_fp8_fp32_inputs_are_the_bf16_run(dev, D, hadamard):
