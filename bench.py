@@ -63,8 +63,8 @@ KERNEL_MFMA_PER_ENTRY = {
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs scaled by a 1 GiB copy's counts
 # (profiles/attn_config4_{bf16,fp8_e4m3}_hbm_traffic.md); re-measured whenever the kernels change.
 CONFIG4_TRAFFIC_BYTES = {
-    "bf16": {"fwd": 1145.3e6, "dq": 1485.6e6, "dkdv": 1389.5e6},
-    "fp8_e4m3": {"fwd": 830.0e6, "dq": 1609.9e6, "dkdv": 1551.7e6},
+    "bf16": {"fwd": 1133.7e6, "dq": 1486.6e6, "dkdv": 1389.4e6},
+    "fp8_e4m3": {"fwd": 832.2e6, "dq": 1611.4e6, "dkdv": 1552.3e6},
 }
 
 
