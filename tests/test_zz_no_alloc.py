@@ -1,8 +1,9 @@
 """GPU: kd_attn_bwd_noalloc (workspace in the library's device array) against
 kd_attn_bwd (caller's workspace), through the C ABI, on two calls in a row --
 the second smaller -- so the array's contents from the first call must not
-leak into the second.  Both run the same kernels on the same inputs, so dQ,
-dK and dV must agree bit for bit.  And captured in a HIP graph on its first
+leak into the second (bf16 and fp32 inputs, and fp8 scores at d = 64 and
+256).  Both run the same kernels on the same inputs, so dQ, dK and dV must
+agree bit for bit.  And captured in a HIP graph on its first
 call in a process (the call that resolves the array's device address, in a
 child process so that no earlier test has made it), replayed three times,
 each replay bit-equal to the eager kd_attn_bwd.
@@ -17,7 +18,7 @@ import pytest
 import torch
 
 from kerneldev_amd import _lib
-from kerneldev_amd.attention import _attn_args, _fwd_op, _ptr, _strides3
+from kerneldev_amd.attention import _attn_args, _fwd_op, _ptr, _set_fp8, _strides3
 from kerneldev_amd.synth import CONFIG3_LAYOUT, cocktail_batch, qkvdo
 
 pytestmark = pytest.mark.gpu
@@ -25,13 +26,14 @@ pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def _backward_both(dev, B, H, T, D, seed, dtype=torch.bfloat16):
+def _backward_both(dev, B, H, T, D, seed, dtype=torch.bfloat16, fp8=False):
     tokens, in_span, span_id, is_prefix = cocktail_batch(B, 1024, CONFIG3_LAYOUT, seed=seed)
     meta = [x[:, :T].to(dev) for x in (in_span, span_id, is_prefix)]
     q, k, v, do = (x.to(dev) for x in qkvdo(B, H, T, D, seed=seed + 1, dtype=dtype))
     sc = D ** -0.5
     fp32 = dtype == torch.float32  # (fp32 O carries no residual)
-    o, lse, plan, o_lo, *_ = _fwd_op(q, k, v, None, *meta, sc, 0, not fp32)
+    # fp8: the forward op's e4m3 copies of Q and K and their scales feed both backward calls
+    o, lse, plan, o_lo, _, _, *q8k8 = _fwd_op(q, k, v, None, *meta, sc, 0, not fp32, quant_fp8=fp8)
     lib = _lib.load()
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     outs = []
@@ -43,6 +45,7 @@ def _backward_both(dev, B, H, T, D, seed, dtype=torch.bfloat16):
         a.dout, a.do_strides = do.data_ptr(), _strides3(do)
         a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
         a.dq_strides, a.dk_strides, a.dv_strides = _strides3(dq), _strides3(dk), _strides3(dv)
+        _set_fp8(a, tuple(q8k8) if fp8 else None)
         if noalloc:
             a.delta = None  # ignored: the library's own workspace is used
             _lib.check(lib.kd_attn_bwd_noalloc(ctypes.byref(a), *_lib.plan_ref(plan), stream), "kd_attn_bwd_noalloc")
@@ -56,11 +59,12 @@ def _backward_both(dev, B, H, T, D, seed, dtype=torch.bfloat16):
 
 
 def test_noalloc_backward_matches_allocating_entry_point(dev):
-    cases = ((2, 4, 1024, 128, 80, torch.bfloat16), (1, 2, 300, 64, 82, torch.bfloat16),
-             (1, 3, 700, 256, 84, torch.float32), (1, 2, 200, 16, 86, torch.float32))
-    for B, H, T, D, seed, dtype in cases:
-        print(f"noalloc backward B={B} H={H} T={T} D={D} {dtype}", flush=True)
-        ref, got = _backward_both(dev, B, H, T, D, seed, dtype)
+    cases = ((2, 4, 1024, 128, 80, torch.bfloat16, False), (1, 2, 300, 64, 82, torch.bfloat16, False),
+             (1, 3, 700, 256, 84, torch.float32, False), (1, 2, 200, 16, 86, torch.float32, False),
+             (1, 2, 600, 256, 88, torch.bfloat16, True), (2, 1, 300, 64, 90, torch.bfloat16, True))
+    for B, H, T, D, seed, dtype, fp8 in cases:
+        print(f"noalloc backward B={B} H={H} T={T} D={D} {dtype} fp8={fp8}", flush=True)
+        ref, got = _backward_both(dev, B, H, T, D, seed, dtype, fp8)
         for name, x, y in zip(("dq", "dk", "dv"), ref, got):
             assert torch.isfinite(y).all(), name
             assert torch.equal(x, y), f"{name} differs (B={B} T={T} D={D})"
