@@ -2,8 +2,9 @@
 runs its op inside torch.compile(fullgraph=True, dynamic=True), with fake
 implementations at :1781-1803 and :1901-1923).
 
-* torch.library.opcheck on kdattn::fwd (also quantising Q and K for fp8 scores),
-  kdattn::bwd, kdattn::fwd_x3, kdattn::bwd_x3, kdattn::rot and kdattn::quant:
+* torch.library.opcheck on every kdattn op: kdattn::fwd (also quantising Q and K
+  for fp8 scores), kdattn::bwd, kdattn::fwd_x3, kdattn::bwd_x3, kdattn::rot,
+  kdattn::rot_amax, kdattn::quant, kdattn::absmax, kdattn::span_fwd and kdattn::span_bwd:
   schema, autograd registration, fake kernels against the real outputs, and
   AOT dispatch with dynamic shapes.
 * flash_attention under torch.compile(fullgraph=True), static and dynamic
@@ -14,7 +15,8 @@ import torch
 
 from kerneldev_amd import flash_attention, generate_hadamard_signs
 from kerneldev_amd.attention import _bwd_op, _bwd_x3_op, _fwd_op, _fwd_x3_op, _lib
-from kerneldev_amd.hadamard import _absmax_op, _quant_op, _rot_op
+from kerneldev_amd.hadamard import _absmax_op, _quant_op, _rot_amax_op, _rot_op
+from kerneldev_amd.span_head import _span_bwd_op, _span_fwd_op, max_spans
 from kerneldev_amd.synth import CONFIG3_LAYOUT, cocktail_batch, qkvdo
 
 pytestmark = pytest.mark.gpu
@@ -73,6 +75,20 @@ def test_opcheck_rotation_and_quantiser_ops(dev):
     torch.library.opcheck(_quant_op, (q, amax))
     print("opcheck kdattn::absmax", flush=True)
     torch.library.opcheck(_absmax_op, (q,))
+    print("opcheck kdattn::rot_amax", flush=True)
+    torch.library.opcheck(_rot_amax_op, (q.clone().requires_grad_(True), signs))
+
+
+def test_opcheck_span_head_ops(dev):
+    tokens, *_ = cocktail_batch(2, 1024, CONFIG3_LAYOUT, seed=91)
+    tokens = tokens.to(dev)
+    h = torch.randn(2, 1024, 64, generator=torch.Generator().manual_seed(92)).to(torch.bfloat16).to(dev)
+    n = max_spans(tokens)
+    print("opcheck kdattn::span_fwd", flush=True)
+    torch.library.opcheck(_span_fwd_op, (tokens, h.clone().requires_grad_(True), n))
+    scores, h_ctx, h_spans, lo, hi, mpos = _span_fwd_op(tokens, h, n)
+    print("opcheck kdattn::span_bwd", flush=True)
+    torch.library.opcheck(_span_bwd_op, (tokens, h, torch.randn_like(scores), h_ctx, h_spans, lo, hi, mpos))
 
 
 def _fwd_bwd(fn, q, k, v, do, meta):
