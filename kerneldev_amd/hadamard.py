@@ -93,10 +93,14 @@ def _rot_amax_fake(x, signs):
 def _rot_amax_setup(ctx, inputs, output):
     ctx.save_for_backward(inputs[1])
     ctx.inverse = False
+    # amax only feeds the fp8 scales, which are not differentiated
+    ctx.mark_non_differentiable(output[1])
+    ctx.set_materialize_grads(False)
 
 
 def _rot_amax_backward(ctx, gy, gamax):
-    # amax only feeds the fp8 scales, which are not differentiated
+    if gy is None:  # x R did not reach the loss
+        return None, None
     (signs,) = ctx.saved_tensors
     return _rot_op(gy.contiguous(), signs, True), None
 

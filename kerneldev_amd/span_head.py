@@ -117,9 +117,12 @@ def _span_setup(ctx, inputs, output):
     _, h_ctx, h_spans, lo, hi, mpos = output
     ctx.save_for_backward(tokens, h, h_ctx, h_spans, lo, hi, mpos)
     ctx.mark_non_differentiable(h_ctx, h_spans, lo, hi, mpos)
+    ctx.set_materialize_grads(False)  # (no zero tensors for the gradients of those outputs)
 
 
 def _span_backward(ctx, dscores, *_):
+    if dscores is None:  # the scores did not reach the loss
+        return None, None, None
     tokens, h, h_ctx, h_spans, lo, hi, mpos = ctx.saved_tensors
     return None, _span_bwd_op(tokens, h, dscores, h_ctx, h_spans, lo, hi, mpos), None
 

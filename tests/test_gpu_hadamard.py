@@ -60,6 +60,13 @@ def test_rotation_roundtrip_and_gradient(dev):
     back = hadamard_transform(y.detach(), signs, inverse=True)
     assert (back.float() - x.detach().float()).abs().max().item() < 3e-2
     assert torch.equal(x.grad, hadamard_transform(gy, signs, inverse=True))
+    # the form that also returns the absmax: the same gradient, none through amax
+    x2 = x.detach().clone().requires_grad_(True)
+    y2, amax = hadamard_absmax(x2, signs)
+    assert torch.equal(y2, y.detach()) and not amax.requires_grad
+    y2.backward(gy)
+    torch.cuda.synchronize()
+    assert torch.equal(x2.grad, x.grad)
 
 
 def test_attention_with_hadamard_matches_unrotated_reference(dev):
