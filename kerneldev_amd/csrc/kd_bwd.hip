@@ -973,7 +973,8 @@ __global__ __launch_bounds__(512, 1) void k_dkdv(AttnArgs a, const uint32_t* __r
 // registers and dV^T, dK^T for DH columns (A operands: dO^T and Q^T column
 // blocks, read transposed).  Two launches (D0 = 0, 128) give the whole
 // gradient, each recomputing S and dP.  Tiles are copied one step ahead into
-// two slots (2 x 2 x 32 KiB).
+// two slots (2 x 2 x 32 KiB).  With fp8 scores (Q8, at D = 64 and 256) S^T
+// comes from an e4m3 Q8 tile and the lane's K8 row instead (QHALF below).
 template <class E, int D, int NSP, int DH, int D0, bool Q8 = false>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void k_dkdv_wide(AttnArgs a, const uint32_t* __restrict__ codes,
                                                       const uint32_t* __restrict__ list,
